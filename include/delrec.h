@@ -1,0 +1,210 @@
+/*
+ * delrec.h — C ABI of the MI355X delayed-LIF recurrent layer (forward + BPTT backward).
+ *
+ * One shared library, libdelrec_hip.so, built for gfx950. Every entry point takes raw
+ * device pointers, sizes and a hipStream_t (passed as void*), launches asynchronously on
+ * that stream, allocates nothing, and returns a delrec_status (0 = ok). Scratch memory is
+ * passed in by the caller, sized by delrec_query_workspace().
+ *
+ * Layouts (all row-major, contiguous):
+ *   x, y, u, dx, gy      (T, B, N) float32, time-major
+ *   W                    (N, N): W[i*N + j] is the weight from source j to receiver i;
+ *                        float32, or bfloat16 when the args' w_bf16 flag is set
+ *   d (axonal)           (N,)  float32 delay per source
+ *   d (synaptic)         (N, N) float32 delay per connection, d[i*N + j]
+ *   base, offsets        hybrid delays d[i*N+j] = base[j] + offsets[i*N+j]; offsets int8
+ *   spike bits           (B, ceil(T/32), N) uint32: bit (t % 32) of word [b][t/32][i]
+ *                        is the spike of neuron i at step t
+ *
+ * Reference interfaces replaced (paths relative to the DelRec repository):
+ *   delrec_axonal_fwd   recdel_triton_forward + recdel_fwd_kernel
+ *                       (src/delrec/triton_kernels/recdel_base.py:136-182, :34-129)
+ *   delrec_axonal_bwd   recdel_triton_backward + recdel_bwd_kernel + the dW / dmask host
+ *                       reductions + autograd through build_mask
+ *                       (recdel_base.py:288-342, :189-285, :402-439)
+ *   delrec_syn_fwd      _ed_scatter_compact_kernel as launched by EventDrivenSyn.forward
+ *                       and HybridSynDelay.forward (synaptic_eventdriven.py:106-164,
+ *                       :385-416; synaptic_hybrid.py:139-172)
+ *   delrec_syn_bwd      _ed_bwd_kernel + the Cstack GEMMs + dW + dd/dp
+ *                       (synaptic_eventdriven.py:323-364, :419-471;
+ *                        synaptic_hybrid.py:174-211)
+ *   delrec_delay_grad   _delay_grad / _hybrid_dd_kernel (synaptic_hybrid.py:83-126)
+ *   delrec_lif_fwd/bwd  the plain multi-step LIF layer the SNN_* stacks build around the
+ *                       recurrent layer (spikingjelly LIFNode, networks.py:82-100)
+ */
+#ifndef DELREC_H
+#define DELREC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    DELREC_OK = 0,
+    DELREC_ERR_ARG = 1,          /* bad size, null pointer or inconsistent flags       */
+    DELREC_ERR_UNSUPPORTED = 2,  /* regime this build does not implement               */
+    DELREC_ERR_WORKSPACE = 3,    /* workspace missing or smaller than queried          */
+    DELREC_ERR_LAUNCH = 4,       /* a kernel launch failed (hipGetLastError)           */
+    DELREC_ERR_WINDOW = 5,       /* window length L out of range for the on-chip ring  */
+    DELREC_ERR_DEVICE = 6        /* device query failed / not a gfx950 device          */
+} delrec_status;
+
+/* Neuron constants (spikingjelly LIFNode semantics; reference lif.py:25-56). */
+typedef struct {
+    float tau;           /* membrane time constant                                      */
+    float decay;         /* float(1 - 1/tau) evaluated in double by the caller          */
+    float v_threshold;
+    float v_reset;       /* ignored when soft_reset                                     */
+    int32_t soft_reset;  /* 1: v_reset is None (v -= spike * v_threshold)              */
+    int32_t decay_input; /* 1: h = v + (x - (v - v_reset)) / tau                       */
+    int32_t detach_reset;
+    int32_t surrogate;   /* 0 = triangle(gamma), 1 = atan(alpha): the reference's ids   */
+    float gamma;
+    float alpha;
+} delrec_lif;
+
+/* Forward tap modes of the axonal layer (reference FWD constexpr, recdel_base.py:59-61). */
+enum { DELREC_TAPS_SOFT = 0, DELREC_TAPS_ROUND = 1, DELREC_TAPS_INTERP = 2 };
+
+typedef struct {
+    int32_t T, B, N, L;          /* L: window length, ceil(1 + max d + max s) + 1       */
+    const float* x;              /* (T,B,N)                                             */
+    const void* W;               /* (N,N) fp32 or bf16                                  */
+    int32_t w_bf16;
+    const float* bias;           /* (N) or NULL                                         */
+    const float* d;              /* (N) delays (already STE-rounded when requested)      */
+    const float* s;              /* (N) per-source half-width, or NULL -> s_uniform     */
+    float s_uniform;             /* 1 + sigma                                           */
+    const float* drop;           /* (B,N) fixed recurrent-dropout multiplier or NULL    */
+    int32_t taps;                /* DELREC_TAPS_*                                       */
+    const int32_t* lag;          /* (N) hard lag for ROUND / INTERP, else NULL          */
+    const float* frac;           /* (N) INTERP weight of lag+1, else NULL               */
+    delrec_lif lif;
+    float* y;                    /* out (T,B,N) spikes                                  */
+    float* u;                    /* out (T,B,N) pre-reset membrane                      */
+    float* rec;                  /* out (T,B,N) recurrent input incl. bias, or NULL     */
+    float* z;                    /* out (T,B,N) delayed source trace (for dW)           */
+    uint32_t* bits;              /* out (B, ceil(T/32), N) spike bitmask                */
+    void* workspace;             /* N > 256: transposed W                               */
+    size_t workspace_bytes;
+} delrec_axonal_fwd_args;
+
+/* Backward gfut modes (reference APPROX constexpr, recdel_base.py:216-233). */
+enum { DELREC_BWD_SOFT = 0, DELREC_BWD_STRAIGHT = 1 };
+
+typedef struct {
+    int32_t T, B, N, L;
+    const float* gy;             /* (T,B,N) upstream gradient                            */
+    const float* u;              /* (T,B,N) saved membrane                               */
+    const uint32_t* bits;        /* saved spike bitmask                                  */
+    const float* z;              /* saved delayed trace                                  */
+    const void* W;
+    int32_t w_bf16;
+    const float* d;
+    const float* s;
+    float s_uniform;
+    const float* drop;
+    int32_t mode;                /* DELREC_BWD_SOFT or DELREC_BWD_STRAIGHT               */
+    const int32_t* lag;          /* (N) for STRAIGHT                                     */
+    delrec_lif lif;
+    float* dx;                   /* out (T,B,N)                                          */
+    float* dW;                   /* out (N,N) float32, or NULL                           */
+    float* db;                   /* out (N), or NULL                                     */
+    float* dd;                   /* out (N), or NULL                                     */
+    float* ds;                   /* out (N) gradient w.r.t. the half-width s, or NULL    */
+    void* workspace;
+    size_t workspace_bytes;
+} delrec_axonal_bwd_args;
+
+typedef struct {
+    int32_t T, B, N, L;
+    const float* x;
+    const void* W;               /* (N,N) W[i*N+j], fp32 or bf16                         */
+    int32_t w_bf16;
+    const float* bias;
+    const float* d;              /* (N,N) per-connection delays, or NULL when hybrid      */
+    const float* base;           /* (N) hybrid base delay per source                     */
+    const int8_t* offsets;       /* (N,N) hybrid integer offsets, offsets[i*N+j]         */
+    const float* s;              /* (N) per-source half-width or NULL                    */
+    float s_uniform;
+    const float* drop;           /* (B,N) or NULL                                        */
+    delrec_lif lif;
+    float* y;
+    float* u;
+    uint32_t* bits;
+    void* workspace;
+    size_t workspace_bytes;
+} delrec_syn_fwd_args;
+
+typedef struct {
+    int32_t T, B, N, L;
+    const float* gy;
+    const float* u;
+    const float* y;              /* (T,B,N) saved spikes                                 */
+    const uint32_t* bits;
+    const void* W;
+    int32_t w_bf16;
+    const float* d;
+    const float* base;
+    const int8_t* offsets;
+    const float* s;
+    float s_uniform;
+    const float* drop;
+    delrec_lif lif;
+    float* dx;                   /* out (T,B,N)                                          */
+    float* dW;                   /* out (N,N) or NULL                                    */
+    float* dd;                   /* out (N,N) per-connection delay gradient, or NULL     */
+    float* ds;                   /* out (N) half-width gradient, or NULL                 */
+    float* db;                   /* out (N) or NULL                                      */
+    void* workspace;
+    size_t workspace_bytes;
+} delrec_syn_bwd_args;
+
+/* Plain multi-step LIF layer (no recurrence). */
+typedef struct {
+    int32_t T, B, N;
+    const float* x;
+    delrec_lif lif;
+    float* y;
+    float* u;
+} delrec_lif_fwd_args;
+
+typedef struct {
+    int32_t T, B, N;
+    const float* gy;
+    const float* u;
+    const float* y;
+    delrec_lif lif;
+    float* dx;
+} delrec_lif_bwd_args;
+
+/* Workspace kinds for delrec_query_workspace; flags bit 0: weights are bf16. */
+enum { DELREC_WS_AXONAL_FWD = 1, DELREC_WS_AXONAL_BWD = 2, DELREC_WS_SYN_FWD = 3,
+       DELREC_WS_SYN_BWD = 4 };
+
+int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream);
+int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream);
+int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream);
+int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream);
+int delrec_lif_fwd(const delrec_lif_fwd_args* a, void* stream);
+int delrec_lif_bwd(const delrec_lif_bwd_args* a, void* stream);
+
+/* dd[i*N+j] = W[i*N+j] * sum_{l=1}^{Lm-1} C[(i*N+j)*Lm + l] * sign(l-1-d)[|l-1-d| <= s]/s^2
+ * with s = 1 + sigma: the reference's closed-form delay gradient test hook. */
+int delrec_delay_grad(const float* C, const float* W, const float* d, float sigma,
+                      int32_t N, int32_t Lm, float* dd, void* stream);
+
+/* Bytes of scratch the given entry point needs for these sizes and flags. */
+int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_t L,
+                           int32_t flags, size_t* bytes);
+
+const char* delrec_strerror(int status);
+const char* delrec_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DELREC_H */

@@ -1,0 +1,426 @@
+// extern "C" entry points of libdelrec_hip.so (declared in include/delrec.h).
+//
+// Host side only: argument validation, workspace carving, launch-shape selection and
+// kernel launches on the caller's stream. Nothing here allocates device memory or
+// synchronises the stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+
+#include "kernels.h"
+
+using namespace delrec;
+
+namespace {
+
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct Carver {
+    char* base;
+    size_t cap, used = 0;
+    Carver(void* p, size_t c) : base(static_cast<char*>(p)), cap(c) {}
+    template <class T>
+    T* take(size_t count) {
+        const size_t bytes = align_up(count * sizeof(T));
+        if (!base || used + bytes > cap) return nullptr;
+        T* out = reinterpret_cast<T*>(base + used);
+        used += bytes;
+        return out;
+    }
+};
+
+// Sizes only (no pointers): mirrors Carver so query_workspace and the entry points agree.
+struct Counter {
+    size_t used = 0;
+    template <class T>
+    void take(size_t count) { used += align_up(count * sizeof(T)); }
+};
+
+int max_lds_bytes() {
+    static int cached = -1;
+    if (cached < 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+            v = 65536;
+        cached = v;
+    }
+    return cached;
+}
+
+int num_cus() {
+    static int cached = -1;
+    if (cached < 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            v = 256;
+        cached = v;
+    }
+    return cached;
+}
+
+int finish_launch() {
+    return hipGetLastError() == hipSuccess ? DELREC_OK : DELREC_ERR_LAUNCH;
+}
+
+bool lif_ok(const delrec_lif& l) {
+    if (!(l.tau > 0.0f)) return false;
+    if (l.surrogate != 0 && l.surrogate != 1) return false;
+    if (l.surrogate == 0 && !(l.gamma > 0.0f)) return false;
+    return true;
+}
+
+// ------------------------------------------------------------------ axonal layout ------
+struct AxLayout {
+    bool res;
+    int G, CH, CHS, NZ, block, hw;
+};
+
+bool axonal_layout(int N, int L, AxLayout& o) {
+    const int lags = std::max(L - 1, 1);
+    if (lags <= 64) o.hw = 1;
+    else if (lags <= 128) o.hw = 2;
+    else if (lags <= 256) o.hw = 4;
+    else return false;
+    if (N <= 256) {
+        o.res = true;
+        // lanes per neuron: as many as fit 1024 threads, keeping >= 4 weights per lane
+        int G = 16;
+        while (G > 1) {
+            const int rpw = 64 / G;
+            const int npad = (N + rpw - 1) / rpw * rpw;
+            const int ch = ((N + G - 1) / G + 3) / 4 * 4;
+            if (npad * G <= 1024 && ch >= 4 && ch <= 64) break;
+            G >>= 1;
+        }
+        const int rpw = 64 / G;
+        const int npad = (N + rpw - 1) / rpw * rpw;
+        int ch = ((N + G - 1) / G + 3) / 4 * 4;
+        int chp = 4;
+        while (chp < ch) chp <<= 1;   // kernels are instantiated for 4..64
+        if (chp > 64 || npad * G > 1024) return false;
+        o.G = G;
+        o.CH = chp;
+        o.CHS = chp;
+        o.NZ = G * chp;
+        o.block = npad * G;
+    } else {
+        o.res = false;
+        int G = 1;
+        while (G < 16) {
+            const int rpw = 64 / (G * 2);
+            const int npad = (N + rpw - 1) / rpw * rpw;
+            if (npad * G * 2 > 1024) break;
+            G <<= 1;
+        }
+        const int rpw = 64 / G;
+        const int npad = (N + rpw - 1) / rpw * rpw;
+        if (npad * G > 1024) {
+            // more receivers than threads: not supported by the one-row-per-workgroup scan
+            return false;
+        }
+        o.G = G;
+        o.CH = 1;
+        o.CHS = (N + G - 1) / G;
+        o.NZ = (G * o.CHS + 3) / 4 * 4;
+        o.block = npad * G;
+    }
+    return true;
+}
+
+template <class C>
+void axonal_bwd_ws(C& c, int T, int B, int N, const AxLayout& lay) {
+    c.template take<float>((size_t)3 * B * N);          // per-row partials
+    c.template take<float>((size_t)T * B * N);          // gr (dropout / decay_input)
+    const int tiles = (N + 127) / 128;
+    const int ks = std::max(1, std::min((2 * num_cus() + tiles * tiles - 1) / (tiles * tiles),
+                                        std::max(1, T * B / 256)));
+    c.template take<float>((size_t)ks * N * N);         // dW split-K partials
+    (void)lay;
+}
+
+int dw_splits(int T, int B, int N) {
+    const int tiles = (N + 127) / 128;
+    return std::max(1, std::min((2 * num_cus() + tiles * tiles - 1) / (tiles * tiles),
+                                std::max(1, T * B / 256)));
+}
+
+// ------------------------------------------------------------------ synaptic layout ----
+struct SynLayout {
+    int block, R, NP, NF;
+    bool lds_ring;
+    size_t lds;
+};
+
+SynLayout syn_layout(int N, int L, bool fwd) {
+    SynLayout o;
+    o.block = std::min(1024, (N + 63) / 64 * 64);
+    o.R = std::max(L, 2);
+    o.NP = N;
+    o.NF = N;
+    const int npt = (N + o.block - 1) / o.block;
+    const size_t extra = fwd ? (size_t)(o.NF + npt * (o.block / 64) + 4) * sizeof(int) : 0;
+    const size_t ring = (size_t)o.R * o.NP * sizeof(float);
+    o.lds_ring = ring + extra <= (size_t)max_lds_bytes();
+    o.lds = (o.lds_ring ? ring : 0) + extra;
+    return o;
+}
+
+int lag_splits(int T, int N) {
+    const int tiles = (N + 63) / 64;
+    return std::max(1, std::min((2 * num_cus() + tiles * tiles - 1) / (tiles * tiles), T));
+}
+
+template <class C>
+void syn_fwd_ws(C& c, int B, int N, int L, bool hybrid, bool bf16) {
+    const SynLayout lay = syn_layout(N, L, true);
+    if (bf16) c.template take<uint16_t>((size_t)N * N); else c.template take<float>((size_t)N * N);
+    if (hybrid) c.template take<int8_t>((size_t)N * N); else c.template take<float>((size_t)N * N);
+    if (!lay.lds_ring) c.template take<float>((size_t)B * lay.R * N);
+}
+
+template <class C>
+void syn_bwd_ws(C& c, int T, int B, int N, int L) {
+    const SynLayout lay = syn_layout(N, L, false);
+    const int ks = lag_splits(T, N);
+    c.template take<float>((size_t)T * B * N);          // gr
+    c.template take<float>((size_t)B * N);              // db partials
+    c.template take<float>((size_t)3 * ks * N * N);     // lag-GEMM partials
+    if (!lay.lds_ring) c.template take<float>((size_t)B * lay.R * N);
+}
+
+// out[c*rows + r] = in[r*cols + c] for elements of `esize` bytes
+template <class E>
+__global__ void transpose_kernel(const E* __restrict__ in, E* __restrict__ out, int n) {
+    __shared__ E tile[32][33];
+    const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
+    for (int k = threadIdx.y; k < 32; k += 8) {
+        const int r = by + k, c = bx + threadIdx.x;
+        if (r < n && c < n) tile[k][threadIdx.x] = in[(size_t)r * n + c];
+    }
+    __syncthreads();
+    for (int k = threadIdx.y; k < 32; k += 8) {
+        const int r = bx + k, c = by + threadIdx.x;
+        if (r < n && c < n) out[(size_t)r * n + c] = tile[threadIdx.x][k];
+    }
+}
+
+template <class E>
+void transpose(const void* in, void* out, int n, hipStream_t s) {
+    dim3 grid((n + 31) / 32, (n + 31) / 32);
+    hipLaunchKernelGGL(transpose_kernel<E>, grid, dim3(32, 8), 0, s, static_cast<const E*>(in),
+                       static_cast<E*>(out), n);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* delrec_version(void) { return "delrec-mi355x 0.1.0 (gfx950)"; }
+
+const char* delrec_strerror(int status) {
+    switch (status) {
+        case DELREC_OK: return "ok";
+        case DELREC_ERR_ARG: return "invalid argument";
+        case DELREC_ERR_UNSUPPORTED: return "unsupported regime";
+        case DELREC_ERR_WORKSPACE: return "workspace missing or too small";
+        case DELREC_ERR_LAUNCH: return "kernel launch failed";
+        case DELREC_ERR_WINDOW: return "delay window too long for this layer size";
+        case DELREC_ERR_DEVICE: return "device query failed";
+        default: return "unknown status";
+    }
+}
+
+int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_t L,
+                           int32_t flags, size_t* bytes) {
+    if (!bytes || T <= 0 || B <= 0 || N <= 0 || L < 1) return DELREC_ERR_ARG;
+    Counter c;
+    const bool bf16 = flags & 1;
+    switch (kind) {
+        case DELREC_WS_AXONAL_FWD: {
+            AxLayout lay;
+            if (!axonal_layout(N, L, lay)) return DELREC_ERR_UNSUPPORTED;
+            if (!lay.res) c.take<float>((size_t)N * N);
+            break;
+        }
+        case DELREC_WS_AXONAL_BWD: {
+            AxLayout lay;
+            if (!axonal_layout(N, L, lay)) return DELREC_ERR_UNSUPPORTED;
+            axonal_bwd_ws(c, T, B, N, lay);
+            break;
+        }
+        case DELREC_WS_SYN_FWD: syn_fwd_ws(c, B, N, L, (flags & 2) != 0, bf16); break;
+        case DELREC_WS_SYN_BWD: syn_bwd_ws(c, T, B, N, L); break;
+        default: return DELREC_ERR_ARG;
+    }
+    *bytes = c.used;
+    return DELREC_OK;
+}
+
+int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
+    if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
+    if (!a->x || !a->W || !a->d || !a->y || !a->u || !a->bits || !lif_ok(a->lif)) return DELREC_ERR_ARG;
+    if (a->taps < 0 || a->taps > 2) return DELREC_ERR_ARG;
+    if (a->taps != DELREC_TAPS_SOFT && !a->lag) return DELREC_ERR_ARG;
+    if (a->taps == DELREC_TAPS_INTERP && !a->frac) return DELREC_ERR_ARG;
+    AxLayout lay;
+    if (!axonal_layout(a->N, a->L, lay)) return DELREC_ERR_WINDOW;
+    const size_t lds = (size_t)2 * lay.NZ * sizeof(float);
+    if (lds > (size_t)max_lds_bytes()) return DELREC_ERR_WINDOW;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    AxFwd p{};
+    p.T = a->T; p.B = a->B; p.N = a->N; p.L = a->L;
+    p.G = lay.G; p.NZ = lay.NZ; p.CHS = lay.CHS;
+    p.x = a->x; p.W = a->W; p.Wt = nullptr; p.w_bf16 = a->w_bf16;
+    p.bias = a->bias; p.d = a->d; p.s = a->s; p.s_uniform = a->s_uniform; p.drop = a->drop;
+    p.taps = a->taps; p.lag = a->lag; p.frac = a->frac; p.lif = make_lif(a->lif);
+    p.y = a->y; p.u = a->u; p.rec = a->rec; p.z = a->z; p.bits = a->bits;
+    if (!lay.res) {
+        Carver cv(a->workspace, a->workspace_bytes);
+        void* wt = a->w_bf16 ? (void*)cv.take<uint16_t>((size_t)a->N * a->N)
+                             : (void*)cv.take<float>((size_t)a->N * a->N);
+        if (!wt) return DELREC_ERR_WORKSPACE;
+        if (a->w_bf16) transpose<uint16_t>(a->W, wt, a->N, s); else transpose<float>(a->W, wt, a->N, s);
+        p.Wt = wt;
+    }
+    if (!launch_axonal(true, &p, nullptr, lay.CH, lay.res, lay.hw, a->B, lay.block, lds, s))
+        return DELREC_ERR_UNSUPPORTED;
+    return finish_launch();
+}
+
+int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
+    if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
+    if (!a->gy || !a->u || !a->bits || !a->W || !a->d || !a->dx || !lif_ok(a->lif)) return DELREC_ERR_ARG;
+    if (a->mode != DELREC_BWD_SOFT && a->mode != DELREC_BWD_STRAIGHT) return DELREC_ERR_ARG;
+    if (a->mode == DELREC_BWD_STRAIGHT && !a->lag) return DELREC_ERR_ARG;
+    if (a->dW && !a->z) return DELREC_ERR_ARG;
+    AxLayout lay;
+    if (!axonal_layout(a->N, a->L, lay)) return DELREC_ERR_WINDOW;
+    const int R = std::max(a->L, 2);
+    const size_t lds = ((size_t)2 * lay.NZ + (size_t)R * a->N) * sizeof(float);
+    if (lds > (size_t)max_lds_bytes()) return DELREC_ERR_WINDOW;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int T = a->T, B = a->B, N = a->N;
+    Carver cv(a->workspace, a->workspace_bytes);
+    float* part = cv.take<float>((size_t)3 * B * N);
+    float* grbuf = cv.take<float>((size_t)T * B * N);
+    const int ks = dw_splits(T, B, N);
+    float* gemm_part = cv.take<float>((size_t)ks * N * N);
+    if (!part || !grbuf || !gemm_part) return DELREC_ERR_WORKSPACE;
+    const bool need_gr = a->drop != nullptr || a->lif.decay_input;
+
+    AxBwd p{};
+    p.T = T; p.B = B; p.N = N; p.L = a->L;
+    p.G = lay.G; p.NZ = lay.NZ; p.CHS = lay.CHS; p.R = R; p.NP = N;
+    p.gy = a->gy; p.u = a->u; p.bits = a->bits; p.W = a->W; p.w_bf16 = a->w_bf16;
+    p.d = a->d; p.s = a->s; p.s_uniform = a->s_uniform; p.drop = a->drop;
+    p.mode = a->mode; p.lag = a->lag; p.lif = make_lif(a->lif);
+    p.dx = a->dx; p.gr = need_gr ? grbuf : nullptr; p.part = part;
+    if (!launch_axonal(false, nullptr, &p, lay.CH, lay.res, lay.hw, B, lay.block, lds, s))
+        return DELREC_ERR_UNSUPPORTED;
+    int st = finish_launch();
+    if (st) return st;
+    launch_reduce_rows(part, B, N, a->db, a->dd, a->ds, s);
+    if (a->dW) {
+        launch_dw_gemm(need_gr ? grbuf : a->dx, a->z, T * B, N, ks, gemm_part, s);
+        launch_sum_partials(gemm_part, ks, (size_t)N * N, a->dW, s);
+    }
+    return finish_launch();
+}
+
+int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
+    if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
+    if (!a->x || !a->W || !a->y || !a->u || !a->bits || !lif_ok(a->lif)) return DELREC_ERR_ARG;
+    const bool hybrid = a->d == nullptr;
+    if (hybrid && (!a->base || !a->offsets)) return DELREC_ERR_ARG;
+    if (a->N > 4096) return DELREC_ERR_UNSUPPORTED;
+    const SynLayout lay = syn_layout(a->N, a->L, true);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int N = a->N;
+    Carver cv(a->workspace, a->workspace_bytes);
+    void* wt = a->w_bf16 ? (void*)cv.take<uint16_t>((size_t)N * N) : (void*)cv.take<float>((size_t)N * N);
+    void* dt = hybrid ? (void*)cv.take<int8_t>((size_t)N * N) : (void*)cv.take<float>((size_t)N * N);
+    float* gring = lay.lds_ring ? nullptr : cv.take<float>((size_t)a->B * lay.R * N);
+    if (!wt || !dt || (!lay.lds_ring && !gring)) return DELREC_ERR_WORKSPACE;
+    if (a->w_bf16) transpose<uint16_t>(a->W, wt, N, s); else transpose<float>(a->W, wt, N, s);
+    if (hybrid) transpose<int8_t>(a->offsets, dt, N, s); else transpose<float>(a->d, dt, N, s);
+
+    SynFwd p{};
+    p.T = a->T; p.B = a->B; p.N = N; p.L = a->L; p.R = lay.R; p.NP = lay.NP; p.NF = lay.NF;
+    p.x = a->x; p.Wt = wt; p.w_bf16 = a->w_bf16; p.bias = a->bias;
+    p.dt = hybrid ? nullptr : static_cast<const float*>(dt);
+    p.base = a->base; p.offt = hybrid ? static_cast<const int8_t*>(dt) : nullptr;
+    p.s = a->s; p.s_uniform = a->s_uniform; p.drop = a->drop; p.lif = make_lif(a->lif);
+    p.y = a->y; p.u = a->u; p.bits = a->bits; p.gring = gring;
+    launch_syn_fwd(p, lay.block, lay.lds, s);
+    return finish_launch();
+}
+
+int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
+    if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
+    if (!a->gy || !a->u || !a->y || !a->W || !a->dx || !lif_ok(a->lif)) return DELREC_ERR_ARG;
+    const bool hybrid = a->d == nullptr;
+    if (hybrid && (!a->base || !a->offsets)) return DELREC_ERR_ARG;
+    if (a->N > 4096) return DELREC_ERR_UNSUPPORTED;
+    const SynLayout lay = syn_layout(a->N, a->L, false);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int T = a->T, B = a->B, N = a->N;
+    const int ks = lag_splits(T, N);
+    Carver cv(a->workspace, a->workspace_bytes);
+    float* gr = cv.take<float>((size_t)T * B * N);
+    float* part = cv.take<float>((size_t)B * N);
+    float* lagp = cv.take<float>((size_t)3 * ks * N * N);
+    float* gring = lay.lds_ring ? nullptr : cv.take<float>((size_t)B * lay.R * N);
+    if (!gr || !part || !lagp || (!lay.lds_ring && !gring)) return DELREC_ERR_WORKSPACE;
+
+    SynBwd p{};
+    p.T = T; p.B = B; p.N = N; p.L = a->L; p.R = lay.R; p.NP = lay.NP;
+    p.gy = a->gy; p.u = a->u; p.W = a->W; p.w_bf16 = a->w_bf16;
+    p.d = a->d; p.base = a->base; p.off = a->offsets; p.s = a->s; p.s_uniform = a->s_uniform;
+    p.drop = a->drop; p.lif = make_lif(a->lif);
+    p.dx = a->dx; p.gr = gr; p.part = part; p.gring = gring;
+    launch_syn_bwd(p, lay.block, lay.lds, s);
+    int st = finish_launch();
+    if (st) return st;
+    launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
+    if (a->dW || a->dd || a->ds) {
+        LagGemm g{};
+        g.T = T; g.B = B; g.N = N; g.L = a->L; g.KS = ks;
+        g.gr = gr; g.y = a->y; g.W = a->W; g.w_bf16 = a->w_bf16;
+        g.d = a->d; g.base = a->base; g.off = a->offsets; g.s = a->s; g.s_uniform = a->s_uniform;
+        const size_t NN = (size_t)N * N;
+        g.pw = lagp;
+        g.pd = lagp + (size_t)ks * NN;
+        g.ps = a->ds ? lagp + (size_t)2 * ks * NN : nullptr;
+        launch_lag_gemm(g, s);
+        launch_lag_finish(g, a->dW, a->dd, a->ds, s);
+    }
+    return finish_launch();
+}
+
+int delrec_lif_fwd(const delrec_lif_fwd_args* a, void* stream) {
+    if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || !a->x || !a->y || !a->u || !lif_ok(a->lif))
+        return DELREC_ERR_ARG;
+    launch_lif(true, a, nullptr, make_lif(a->lif), static_cast<hipStream_t>(stream));
+    return finish_launch();
+}
+
+int delrec_lif_bwd(const delrec_lif_bwd_args* a, void* stream) {
+    if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || !a->gy || !a->u || !a->dx || !lif_ok(a->lif))
+        return DELREC_ERR_ARG;
+    launch_lif(false, nullptr, a, make_lif(a->lif), static_cast<hipStream_t>(stream));
+    return finish_launch();
+}
+
+int delrec_delay_grad(const float* C, const float* W, const float* d, float sigma, int32_t N,
+                      int32_t Lm, float* dd, void* stream) {
+    if (!C || !W || !d || !dd || N <= 0 || Lm < 1 || !(sigma >= 0.0f)) return DELREC_ERR_ARG;
+    launch_delay_grad(C, W, d, sigma, N, Lm, dd, static_cast<hipStream_t>(stream));
+    return finish_launch();
+}
+
+}  // extern "C"

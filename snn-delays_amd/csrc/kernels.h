@@ -1,0 +1,127 @@
+// Kernel parameter blocks and launchers shared by the HIP sources and the C ABI layer.
+#pragma once
+
+#include "common.h"
+
+namespace delrec {
+
+struct AxFwd {
+    int T, B, N, L;
+    int G, NZ, CHS;            // lanes per receiver, padded z length, streamed chunk
+    const float* x;
+    const void* W;             // row-major (resident form)
+    const void* Wt;            // transposed copy (streamed form)
+    int w_bf16;
+    const float* bias;
+    const float* d;
+    const float* s;
+    float s_uniform;
+    const float* drop;
+    int taps;
+    const int* lag;
+    const float* frac;
+    Lif lif;
+    float* y;
+    float* u;
+    float* rec;
+    float* z;
+    uint32_t* bits;
+};
+
+struct AxBwd {
+    int T, B, N, L;
+    int G, NZ, CHS, R, NP;     // lanes per source, padded gr length, streamed chunk, ring slots, ring pitch
+    const float* gy;
+    const float* u;
+    const uint32_t* bits;
+    const void* W;
+    int w_bf16;
+    const float* d;
+    const float* s;
+    float s_uniform;
+    const float* drop;
+    int mode;
+    const int* lag;
+    Lif lif;
+    float* dx;
+    float* gr;                 // (T,B,N) dL/drec, written when it differs from dx, else NULL
+    float* part;               // [3][B][N] per-row partials of db, dd, ds
+};
+
+struct SynFwd {
+    int T, B, N, L, R, NP, NF;  // ring slots / pitch, fired-list capacity
+    const float* x;
+    const void* Wt;             // transposed: Wt[o*N + i] = W[i, o]
+    int w_bf16;
+    const float* bias;
+    const float* dt;            // transposed delays dt[o*N + i], or NULL (hybrid)
+    const float* base;
+    const int8_t* offt;         // transposed hybrid offsets offt[o*N + i]
+    const float* s;
+    float s_uniform;
+    const float* drop;
+    Lif lif;
+    float* y;
+    float* u;
+    uint32_t* bits;
+    float* gring;               // global ring [B][R][N] when the ring does not fit LDS, else NULL
+};
+
+struct SynBwd {
+    int T, B, N, L, R, NP;
+    const float* gy;
+    const float* u;
+    const void* W;              // row-major W[i*N + j]
+    int w_bf16;
+    const float* d;             // row-major d[i*N + j], or NULL (hybrid)
+    const float* base;
+    const int8_t* off;          // row-major offsets
+    const float* s;
+    float s_uniform;
+    const float* drop;
+    Lif lif;
+    float* dx;
+    float* gr;                  // (T,B,N) dL/drec (always written: the dW / dd GEMM reads it)
+    float* part;                // [B][N] db partials
+    float* gring;               // global ring [B][R][N] when the ring does not fit LDS, else NULL
+};
+
+struct LagGemm {
+    int T, B, N, L, KS;
+    const float* gr;            // (T,B,N)
+    const float* y;             // (T,B,N)
+    const void* W;
+    int w_bf16;
+    const float* d;             // row-major, or NULL (hybrid)
+    const float* base;
+    const int8_t* off;
+    const float* s;
+    float s_uniform;
+    float* pw;                  // [KS][N][N] partial sum_l h * C_l
+    float* pd;                  // [KS][N][N] partial sum_l sign * C_l, or NULL
+    float* ps;                  // [KS][N][N] partial sum_l dh/ds * C_l, or NULL
+};
+
+bool launch_axonal(bool fwd, const AxFwd* fa, const AxBwd* ba, int ch, bool res, int hw,
+                   int grid, int block, size_t lds, hipStream_t stream);
+void launch_reduce_rows(const float* part, int B, int N, float* o0, float* o1, float* o2,
+                        hipStream_t stream);
+
+// dW[i,j] = sum_k A[k,i] * Bm[k,j] over K rows (split K into ks chunks of partials).
+void launch_dw_gemm(const float* A, const float* Bm, int K, int N, int ks, float* partial,
+                    hipStream_t stream);
+// out[idx] = sum_k partial[k][idx] for idx < count
+void launch_sum_partials(const float* partial, int ks, size_t count, float* out, hipStream_t stream);
+
+void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream);
+void launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);
+void launch_lag_gemm(const LagGemm& a, hipStream_t stream);
+// dW = sum_k pw; dd = W/s^2 * sum_k pd; ds[j] = sum_i W[i,j] * sum_k ps[i,j]
+void launch_lag_finish(const LagGemm& a, float* dW, float* dd, float* ds, hipStream_t stream);
+
+void launch_lif(bool fwd, const delrec_lif_fwd_args* fa, const delrec_lif_bwd_args* ba,
+                const Lif& k, hipStream_t stream);
+void launch_delay_grad(const float* C, const float* W, const float* d, float sigma, int N,
+                       int Lm, float* dd, hipStream_t stream);
+
+}  // namespace delrec

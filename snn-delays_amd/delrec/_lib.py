@@ -1,0 +1,160 @@
+"""ctypes binding of ``libdelrec_hip.so`` (the C ABI declared in ``include/delrec.h``).
+
+The library is loaded once, after ``torch`` (so both share torch's HIP runtime). There is
+no fallback: if the shared object is missing or a call returns a non-zero status, a
+``DelrecError`` is raised. Tensors are passed as raw device pointers on torch's current
+stream; scratch memory comes from torch's caching allocator, sized by
+``delrec_query_workspace``.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get('DELREC_HIP_LIB', _HERE / 'libdelrec_hip.so'))
+
+c_f32 = ctypes.c_float
+c_i32 = ctypes.c_int32
+c_vp = ctypes.c_void_p
+c_size = ctypes.c_size_t
+
+DELREC_TAPS_SOFT, DELREC_TAPS_ROUND, DELREC_TAPS_INTERP = 0, 1, 2
+DELREC_BWD_SOFT, DELREC_BWD_STRAIGHT = 0, 1
+WS_AXONAL_FWD, WS_AXONAL_BWD, WS_SYN_FWD, WS_SYN_BWD = 1, 2, 3, 4
+
+# Every symbol include/delrec.h declares (checked by the CPU test suite).
+EXPORTS = ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_syn_fwd', 'delrec_syn_bwd',
+           'delrec_lif_fwd', 'delrec_lif_bwd', 'delrec_delay_grad', 'delrec_query_workspace',
+           'delrec_strerror', 'delrec_version')
+
+
+class DelrecError(RuntimeError):
+    """A non-zero ``delrec_status`` from the HIP library."""
+
+    def __init__(self, fn, status, message):
+        super().__init__(f'{fn} failed: status {status} ({message})')
+        self.status = status
+
+
+class Lif(ctypes.Structure):
+    _fields_ = [('tau', c_f32), ('decay', c_f32), ('v_threshold', c_f32), ('v_reset', c_f32),
+                ('soft_reset', c_i32), ('decay_input', c_i32), ('detach_reset', c_i32),
+                ('surrogate', c_i32), ('gamma', c_f32), ('alpha', c_f32)]
+
+
+class AxonalFwdArgs(ctypes.Structure):
+    _fields_ = [('T', c_i32), ('B', c_i32), ('N', c_i32), ('L', c_i32),
+                ('x', c_vp), ('W', c_vp), ('w_bf16', c_i32), ('bias', c_vp), ('d', c_vp),
+                ('s', c_vp), ('s_uniform', c_f32), ('drop', c_vp), ('taps', c_i32),
+                ('lag', c_vp), ('frac', c_vp), ('lif', Lif),
+                ('y', c_vp), ('u', c_vp), ('rec', c_vp), ('z', c_vp), ('bits', c_vp),
+                ('workspace', c_vp), ('workspace_bytes', c_size)]
+
+
+class AxonalBwdArgs(ctypes.Structure):
+    _fields_ = [('T', c_i32), ('B', c_i32), ('N', c_i32), ('L', c_i32),
+                ('gy', c_vp), ('u', c_vp), ('bits', c_vp), ('z', c_vp), ('W', c_vp),
+                ('w_bf16', c_i32), ('d', c_vp), ('s', c_vp), ('s_uniform', c_f32), ('drop', c_vp),
+                ('mode', c_i32), ('lag', c_vp), ('lif', Lif),
+                ('dx', c_vp), ('dW', c_vp), ('db', c_vp), ('dd', c_vp), ('ds', c_vp),
+                ('workspace', c_vp), ('workspace_bytes', c_size)]
+
+
+class SynFwdArgs(ctypes.Structure):
+    _fields_ = [('T', c_i32), ('B', c_i32), ('N', c_i32), ('L', c_i32),
+                ('x', c_vp), ('W', c_vp), ('w_bf16', c_i32), ('bias', c_vp), ('d', c_vp),
+                ('base', c_vp), ('offsets', c_vp), ('s', c_vp), ('s_uniform', c_f32),
+                ('drop', c_vp), ('lif', Lif), ('y', c_vp), ('u', c_vp), ('bits', c_vp),
+                ('workspace', c_vp), ('workspace_bytes', c_size)]
+
+
+class SynBwdArgs(ctypes.Structure):
+    _fields_ = [('T', c_i32), ('B', c_i32), ('N', c_i32), ('L', c_i32),
+                ('gy', c_vp), ('u', c_vp), ('y', c_vp), ('bits', c_vp), ('W', c_vp),
+                ('w_bf16', c_i32), ('d', c_vp), ('base', c_vp), ('offsets', c_vp), ('s', c_vp),
+                ('s_uniform', c_f32), ('drop', c_vp), ('lif', Lif),
+                ('dx', c_vp), ('dW', c_vp), ('dd', c_vp), ('ds', c_vp), ('db', c_vp),
+                ('workspace', c_vp), ('workspace_bytes', c_size)]
+
+
+class LifFwdArgs(ctypes.Structure):
+    _fields_ = [('T', c_i32), ('B', c_i32), ('N', c_i32), ('x', c_vp), ('lif', Lif),
+                ('y', c_vp), ('u', c_vp)]
+
+
+class LifBwdArgs(ctypes.Structure):
+    _fields_ = [('T', c_i32), ('B', c_i32), ('N', c_i32), ('gy', c_vp), ('u', c_vp), ('y', c_vp),
+                ('lif', Lif), ('dx', c_vp)]
+
+
+_lib = None
+
+
+def load():
+    """Load the HIP library (once). Raises ImportError with the build hint if missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(f'{LIB_PATH} is not built: run `python -c "import __graft_entry__ as g; '
+                          f'g.build()"` from the repository root')
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name in ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_syn_fwd', 'delrec_syn_bwd',
+                 'delrec_lif_fwd', 'delrec_lif_bwd'):
+        getattr(lib, name).restype = c_i32
+        getattr(lib, name).argtypes = [c_vp, c_vp]
+    lib.delrec_delay_grad.restype = c_i32
+    lib.delrec_delay_grad.argtypes = [c_vp, c_vp, c_vp, c_f32, c_i32, c_i32, c_vp, c_vp]
+    lib.delrec_query_workspace.restype = c_i32
+    lib.delrec_query_workspace.argtypes = [c_i32] * 6 + [ctypes.POINTER(c_size)]
+    lib.delrec_strerror.restype = ctypes.c_char_p
+    lib.delrec_strerror.argtypes = [c_i32]
+    lib.delrec_version.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def _check(fn, status):
+    if status != 0:
+        raise DelrecError(fn, status, load().delrec_strerror(status).decode())
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def make_lif(tau, v_threshold, v_reset, decay_input, detach_reset, surr_id, gamma, alpha):
+    """``delrec_lif`` from the neuron constants; ``v_reset=None`` means soft reset."""
+    tau = float(tau)
+    return Lif(tau=tau, decay=float(1.0 - 1.0 / tau), v_threshold=float(v_threshold),
+               v_reset=0.0 if v_reset is None else float(v_reset),
+               soft_reset=1 if v_reset is None else 0, decay_input=int(bool(decay_input)),
+               detach_reset=int(bool(detach_reset)), surrogate=int(surr_id),
+               gamma=float(gamma), alpha=float(alpha))
+
+
+def workspace(kind, T, B, N, L, flags, device):
+    size = c_size(0)
+    _check('delrec_query_workspace', load().delrec_query_workspace(kind, T, B, N, L, flags,
+                                                                   ctypes.byref(size)))
+    return torch.empty(max(int(size.value), 1), dtype=torch.uint8, device=device)
+
+
+def call(name, args, stream):
+    _check(name, getattr(load(), name)(ctypes.byref(args), stream))
+
+
+def delay_grad(C, W, d, sigma, N, Lm, out, stream):
+    _check('delrec_delay_grad', load().delrec_delay_grad(ptr(C), ptr(W), ptr(d), float(sigma), N,
+                                                         Lm, ptr(out), stream))
+
+
+def version():
+    return load().delrec_version().decode()

@@ -1,0 +1,72 @@
+"""Layer-side glue between the delay-layer modules and the HIP autograd Functions.
+
+Counterpart of the reference's ``delrec/delay_layers_triton.py`` mixins
+(``AxonalTritonScans.multi_step_forward_triton`` :21-79,
+``SynapticTritonScans.multi_step_forward_eventdriven`` :85-96,
+``SynapticHybridScans.multi_step_forward_hybrid_triton`` :108-112): it reads the layer's
+configuration (surrogate id and width, recurrent dropout mask fixed over time, optional
+bias and learned spread, STE-rounded delays) and calls the Function. The method names
+are the reference's, so code that calls them directly keeps working.
+"""
+
+import torch
+
+from .kernels import AxonalRecdelHip, eventdriven_trainable_forward, hybrid_trainable_forward
+from .kernels._common import require_device
+from .kernels.surrogate import surrogate_id
+
+
+class AxonalHipScans:
+    """Fused scans for per-neuron (axonal) delays."""
+
+    def multi_step_forward_triton(self, x_seq, approx=False, ste_mode=0):
+        require_device(x_seq)
+        T, B, N = x_seq.shape
+        gamma_cfg = getattr(self.config, 'surrogate_gamma', None)
+        sid, gamma, alpha = surrogate_id(self.config.surrogate_function, gamma_cfg)
+        if self.training and self.config.recurrent_dropout_rate > 0:
+            drop = self.dropout(torch.ones(B, N, device=x_seq.device, dtype=x_seq.dtype))
+        else:
+            drop = None
+        p_spread = (self.p_spread if self.use_sig_p
+                    else torch.zeros(N, device=x_seq.device, dtype=x_seq.dtype))
+        bias = self.recurrent_bias if self.use_rec_bias else None
+        if ste_mode:
+            ste_mode = 1 if getattr(self.config, 'ste_round_forward', True) else 2
+        d_in = self.recurrent_delays
+        if d_in.numel() == 1 and N > 1:       # common_recdel: one delay shared by the layer
+            d_in = d_in.expand(N)
+        if self.round_delays:
+            d_in = d_in + (d_in.round() - d_in).detach()
+        nm = self.neuron_module
+        y = AxonalRecdelHip.apply(
+            x_seq, self.recurrent_weights, bias, d_in, p_spread, drop,
+            float(self.sigma), nm.tau, nm.v_threshold, nm.v_reset, self.use_sig_p,
+            self.config.detach_reset, sid, gamma, approx, ste_mode, alpha,
+            getattr(nm, 'decay_input', False))
+        self.x_seq = x_seq
+        self.rec_now_seq = None
+        if self.store_v_seq:
+            self.v_seq = None
+        return y
+
+
+class SynapticHipScans:
+    """Spike-sparse scan for per-connection (synaptic) delays."""
+
+    def multi_step_forward_eventdriven(self, x_seq):
+        require_device(x_seq)
+        y = eventdriven_trainable_forward(self, x_seq)
+        self.x_seq = x_seq
+        self.rec_now_seq = None
+        if self.store_v_seq:
+            self.v_seq = None
+        return y
+
+
+class SynapticHybridScans:
+    """Scan for hybrid recurrent delays (learned per-source base + frozen integer offsets)."""
+
+    def multi_step_forward_hybrid_triton(self, x_seq):
+        require_device(x_seq)
+        return hybrid_trainable_forward(self, x_seq)

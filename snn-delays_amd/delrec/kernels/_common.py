@@ -1,0 +1,70 @@
+"""Host helpers shared by the autograd Functions: device checks, neuron constants,
+surrogate ids, window length, dropout-mask normalisation."""
+
+import math
+
+import torch
+
+from .. import _lib
+from .surrogate import surrogate_id
+
+
+def require_device(x, what='input'):
+    """The layer runs only on the GPU: a CPU tensor is an error, never a fallback."""
+    if not x.is_cuda:
+        raise RuntimeError(f'delrec-mi355x runs the delayed-LIF scan with HIP kernels on the GPU; '
+                           f'{what} is on {x.device}. The pure-PyTorch scans of the reference are '
+                           f'not part of this build.')
+
+
+def lif_struct(neuron, surrogate_function, gamma=None):
+    """``delrec_lif`` of a LIFNode-like object plus the config's surrogate."""
+    sid, g, alpha = surrogate_id(surrogate_function, gamma)
+    return _lib.make_lif(neuron.tau, neuron.v_threshold, neuron.v_reset,
+                         getattr(neuron, 'decay_input', False), getattr(neuron, 'detach_reset', False),
+                         sid, g, alpha)
+
+
+def window_length_f32(d_max, s_max):
+    """``L = ceil(1 + max d + max s) + 1`` in fp32 (``delays.build_mask``, reference
+    ``triton_kernels/delays.py:26``)."""
+    v = (torch.tensor(1.0, dtype=torch.float32) + torch.tensor(float(d_max), dtype=torch.float32)
+         + torch.tensor(float(s_max), dtype=torch.float32))
+    return int(torch.ceil(v).item()) + 1
+
+
+def window_length_f64(d_max, s_max):
+    """The same in double precision, as ``EventDrivenSyn`` / ``HybridSynDelay`` compute it
+    (``synaptic_eventdriven.py:391``, ``synaptic_hybrid.py:148``)."""
+    return int(math.ceil(1.0 + float(d_max) + float(s_max))) + 1
+
+
+def drop_bn(drop, T, B, N):
+    """Normalise a recurrent-dropout multiplier to a contiguous ``(B, N)`` fp32 tensor, or
+    ``None`` when absent. A ``(T, B, N)`` argument must hold the same mask at every step
+    (the fixed-mask semantics of the reference, ``delay_layers_triton.py:37-48``)."""
+    if drop is None:
+        return None
+    drop = drop.detach()
+    if drop.dim() == 3:
+        if drop.shape != (T, B, N):
+            raise ValueError(f'drop has shape {tuple(drop.shape)}, expected {(T, B, N)}')
+        first = drop[0]
+        if drop.stride(0) != 0 and T > 1 and not torch.equal(drop, first.unsqueeze(0).expand_as(drop)):
+            raise ValueError('drop must be the same (B, N) mask at every time step')
+        drop = first
+    if drop.shape != (B, N):
+        raise ValueError(f'drop has shape {tuple(drop.shape)}, expected {(B, N)}')
+    return drop.to(torch.float32).contiguous()
+
+
+def weights(W):
+    """Contiguous device weights and the bf16 flag (fp32 and bf16 are native)."""
+    W = W.detach()
+    if W.dtype == torch.bfloat16:
+        return W.contiguous(), 1
+    return W.to(torch.float32).contiguous(), 0
+
+
+def bits_shape(T, B, N):
+    return (B, (T + 31) // 32, N)

@@ -1,0 +1,115 @@
+"""Axonal delayed-LIF layer: the autograd Function over ``delrec_axonal_fwd/bwd``.
+
+Drop-in for ``AxonalRecdelTriton`` (reference ``triton_kernels/recdel_base.py:349-439``):
+same argument order and meaning, ``(x, W, bias, d, p_spread, drop, sigma, tau, v_th,
+v_reset, use_sig_p, detach_reset, surr_id, gamma, approx, ste_mode, alpha)``, plus an
+optional trailing ``decay_input`` (the reference routes ``decay_input=True`` to its
+PyTorch scan; the HIP kernel implements that charge form). The backward returns the
+gradients of ``x, W, bias, d, p_spread`` and ``None`` for the rest.
+
+Modes (reference ``recdel_base.py:361-383``):
+  exact      soft triangle taps forward and backward, ``dd`` / ``dp`` from the
+             closed-form kernel derivative accumulated in the scan;
+  approx     one rounded tap forward, the single-tap backward and the straight-through
+             ``dd = sum gz * (y[t-lag-1] - y[t-lag])``;
+  ste_mode   1: rounded tap forward, 2: two-tap interpolated forward; soft backward.
+"""
+
+import torch
+
+from .. import _lib
+from ._common import bits_shape, drop_bn, require_device, weights, window_length_f32
+from .delays import build_lag, build_lag_interp
+
+
+class AxonalRecdelHip(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, W, bias, d, p_spread, drop, sigma, tau, v_th, v_reset, use_sig_p,
+                detach_reset, surr_id, gamma=1.0, approx=False, ste_mode=0, alpha=2.0,
+                decay_input=False):
+        require_device(x)
+        T, B, N = x.shape
+        dev = x.device
+        xc = x.detach().to(torch.float32).contiguous()
+        Wc, w_bf16 = weights(W)
+        dc = d.detach().to(torch.float32).contiguous()
+        sigma = float(sigma)
+        if use_sig_p:
+            s_vec = (1.0 + 2.0 * sigma * torch.sigmoid(p_spread.detach().to(torch.float32))).contiguous()
+            s_max = float(s_vec.max())
+        else:
+            s_vec = None
+            s_max = float(torch.tensor(1.0 + sigma, dtype=torch.float32))
+        d_max = float(dc.max())
+        lag = frac = None
+        if ste_mode:
+            L = window_length_f32(d_max, s_max)
+            if ste_mode == 1:
+                lag, taps = build_lag(dc, L), _lib.DELREC_TAPS_ROUND
+            else:
+                (lag, frac), taps = build_lag_interp(dc, L), _lib.DELREC_TAPS_INTERP
+            approx = False
+            mode = _lib.DELREC_BWD_SOFT
+        elif approx:
+            L = int(torch.round(dc).max().item()) + 2
+            lag, taps, mode = build_lag(dc, L), _lib.DELREC_TAPS_ROUND, _lib.DELREC_BWD_STRAIGHT
+        else:
+            L = window_length_f32(d_max, s_max)
+            taps, mode = _lib.DELREC_TAPS_SOFT, _lib.DELREC_BWD_SOFT
+        L = max(L, 2)
+        m = drop_bn(drop, T, B, N)
+        bc = None if bias is None else bias.detach().to(torch.float32).contiguous()
+        lif = _lib.make_lif(tau, v_th, v_reset, decay_input, detach_reset, surr_id, gamma, alpha)
+
+        y = torch.empty(T, B, N, device=dev, dtype=torch.float32)
+        u = torch.empty_like(y)
+        z = torch.empty_like(y)
+        bits = torch.empty(bits_shape(T, B, N), device=dev, dtype=torch.int32)
+        ws = _lib.workspace(_lib.WS_AXONAL_FWD, T, B, N, L, w_bf16, dev)
+        args = _lib.AxonalFwdArgs(
+            T=T, B=B, N=N, L=L, x=_lib.ptr(xc), W=_lib.ptr(Wc), w_bf16=w_bf16, bias=_lib.ptr(bc),
+            d=_lib.ptr(dc), s=_lib.ptr(s_vec), s_uniform=1.0 + sigma, drop=_lib.ptr(m), taps=taps,
+            lag=_lib.ptr(lag), frac=_lib.ptr(frac), lif=lif, y=_lib.ptr(y), u=_lib.ptr(u), rec=None,
+            z=_lib.ptr(z), bits=_lib.ptr(bits), workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
+        _lib.call('delrec_axonal_fwd', args, _lib.stream_of(xc))
+
+        ctx.save_for_backward(u, z, bits, Wc, dc, s_vec, m, lag, p_spread)
+        ctx.meta = (T, B, N, L, w_bf16, sigma, bool(use_sig_p), mode, W.dtype)
+        ctx.lif = lif
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        u, z, bits, Wc, dc, s_vec, m, lag, p_spread = ctx.saved_tensors
+        T, B, N, L, w_bf16, sigma, use_sig_p, mode, w_dtype = ctx.meta
+        dev = u.device
+        gy = gy.to(torch.float32).contiguous()
+        need_W, need_b, need_d = ctx.needs_input_grad[1], ctx.needs_input_grad[2], ctx.needs_input_grad[3]
+        need_p = use_sig_p and ctx.needs_input_grad[4] and mode == _lib.DELREC_BWD_SOFT
+        dx = torch.empty_like(gy)
+        dW = torch.empty(N, N, device=dev, dtype=torch.float32) if need_W else None
+        db = torch.empty(N, device=dev, dtype=torch.float32) if need_b else None
+        dd = torch.empty(N, device=dev, dtype=torch.float32) if need_d else None
+        ds = torch.empty(N, device=dev, dtype=torch.float32) if need_p else None
+        ws = _lib.workspace(_lib.WS_AXONAL_BWD, T, B, N, L, w_bf16, dev)
+        args = _lib.AxonalBwdArgs(
+            T=T, B=B, N=N, L=L, gy=_lib.ptr(gy), u=_lib.ptr(u), bits=_lib.ptr(bits), z=_lib.ptr(z),
+            W=_lib.ptr(Wc), w_bf16=w_bf16, d=_lib.ptr(dc), s=_lib.ptr(s_vec), s_uniform=1.0 + sigma,
+            drop=_lib.ptr(m), mode=mode, lag=_lib.ptr(lag), lif=ctx.lif, dx=_lib.ptr(dx),
+            dW=_lib.ptr(dW), db=_lib.ptr(db), dd=_lib.ptr(dd), ds=_lib.ptr(ds),
+            workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
+        _lib.call('delrec_axonal_bwd', args, _lib.stream_of(gy))
+        dp = None
+        if need_p:
+            with torch.enable_grad():
+                p_ = p_spread.detach().to(torch.float32).requires_grad_(True)
+                s_ = 1.0 + 2.0 * sigma * torch.sigmoid(p_)
+                (dp,) = torch.autograd.grad(s_, p_, ds)
+            dp = dp.to(p_spread.dtype)
+        if dW is not None and w_dtype != torch.float32:
+            dW = dW.to(w_dtype)
+        return (dx, dW, db, dd, dp) + (None,) * 13
+
+
+# The reference's name for this Function (``delrec.triton_kernels.AxonalRecdelTriton``).
+AxonalRecdelTriton = AxonalRecdelHip

@@ -1,0 +1,135 @@
+"""Synaptic (per-connection) delayed-LIF layer over ``delrec_syn_fwd/bwd``.
+
+Drop-in for ``EventDrivenSyn`` / ``eventdriven_trainable_forward`` (reference
+``triton_kernels/synaptic_eventdriven.py:379-488``): ``EventDrivenSyn.apply(x, W, d,
+p_spread, bias, drop, layer) -> y`` with backward ``(dx, dW, dd, dp, dbias, None, None)``.
+The forward is the spike-sparse scatter scan; the backward is the dense reverse BPTT scan
+followed by the lag-correlation GEMM, which folds ``dW = sum_l h * C_l`` and
+``dd = W * sum_l dh/dd * C_l`` (and ``ds``) into its epilogue instead of materialising the
+``(N, N, L)`` lag stack.
+"""
+
+import torch
+
+from .. import _lib
+from ._common import bits_shape, drop_bn, lif_struct, require_device, weights, window_length_f64
+
+
+def _spread(layer, device):
+    """Per-source half-width (``use_sig_p``) or the uniform ``1 + sigma``."""
+    if layer.use_sig_p:
+        s = (1.0 + 2.0 * float(layer.sigma) * torch.sigmoid(
+            layer.p_spread.detach().to(device=device, dtype=torch.float32))).contiguous()
+        return s, float(s.max())
+    return None, 1.0 + float(layer.sigma)
+
+
+def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, s_max, d_max, bias, drop, lif):
+    """Launch ``delrec_syn_fwd`` with per-connection delays ``d_eff`` (N, N), or with the
+    hybrid ``base`` (N) + int8 ``offsets`` (N, N) when ``d_eff`` is None; ``d_max`` is the
+    largest effective delay. Returns ``(y, u, bits, L, Wc, w_bf16)``."""
+    require_device(x)
+    T, B, N = x.shape
+    dev = x.device
+    xc = x.detach().to(torch.float32).contiguous()
+    Wc, w_bf16 = weights(W)
+    L = max(window_length_f64(d_max, s_max), 2)
+    y = torch.empty(T, B, N, device=dev, dtype=torch.float32)
+    u = torch.empty_like(y)
+    bits = torch.empty(bits_shape(T, B, N), device=dev, dtype=torch.int32)
+    flags = w_bf16 | (2 if d_eff is None else 0)
+    ws = _lib.workspace(_lib.WS_SYN_FWD, T, B, N, L, flags, dev)
+    args = _lib.SynFwdArgs(
+        T=T, B=B, N=N, L=L, x=_lib.ptr(xc), W=_lib.ptr(Wc), w_bf16=w_bf16, bias=_lib.ptr(bias),
+        d=_lib.ptr(d_eff), base=_lib.ptr(base), offsets=_lib.ptr(offsets), s=_lib.ptr(s_vec),
+        s_uniform=float(s_uniform), drop=_lib.ptr(drop), lif=lif, y=_lib.ptr(y), u=_lib.ptr(u),
+        bits=_lib.ptr(bits), workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
+    _lib.call('delrec_syn_fwd', args, _lib.stream_of(xc))
+    return y, u, bits, L, Wc, w_bf16
+
+
+def syn_backward(gy, u, y, bits, Wc, w_bf16, d_eff, base, offsets, s_vec, s_uniform, drop, lif, L,
+                 need_W, need_d, need_s, need_b):
+    """Launch ``delrec_syn_bwd``. Returns ``(dx, dW, dd, ds, db)`` (``None`` where not
+    requested)."""
+    T, B, N = u.shape
+    dev = u.device
+    gy = gy.to(torch.float32).contiguous()
+    dx = torch.empty_like(gy)
+    dW = torch.empty(N, N, device=dev, dtype=torch.float32) if need_W else None
+    dd = torch.empty(N, N, device=dev, dtype=torch.float32) if need_d else None
+    ds = torch.empty(N, device=dev, dtype=torch.float32) if need_s else None
+    db = torch.empty(N, device=dev, dtype=torch.float32) if need_b else None
+    ws = _lib.workspace(_lib.WS_SYN_BWD, T, B, N, L, w_bf16, dev)
+    args = _lib.SynBwdArgs(
+        T=T, B=B, N=N, L=L, gy=_lib.ptr(gy), u=_lib.ptr(u), y=_lib.ptr(y), bits=_lib.ptr(bits),
+        W=_lib.ptr(Wc), w_bf16=w_bf16, d=_lib.ptr(d_eff), base=_lib.ptr(base),
+        offsets=_lib.ptr(offsets), s=_lib.ptr(s_vec), s_uniform=float(s_uniform), drop=_lib.ptr(drop),
+        lif=lif, dx=_lib.ptr(dx), dW=_lib.ptr(dW), dd=_lib.ptr(dd), ds=_lib.ptr(ds), db=_lib.ptr(db),
+        workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
+    _lib.call('delrec_syn_bwd', args, _lib.stream_of(gy))
+    return dx, dW, dd, ds, db
+
+
+def layer_lif(layer):
+    cfg = layer.config
+    return lif_struct(layer.neuron_module, cfg.surrogate_function, getattr(cfg, 'surrogate_gamma', None))
+
+
+class EventDrivenSyn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, W, d, p_spread, bias, drop, layer):
+        T, B, N = x.shape
+        dev = x.device
+        d_eff = (d.detach().round() if layer.round_delays else d.detach()).to(torch.float32).contiguous()
+        s_vec, s_max = _spread(layer, dev)
+        s_uniform = 1.0 + float(layer.sigma)
+        m = drop_bn(drop, T, B, N)
+        bc = None if bias is None else bias.detach().to(torch.float32).contiguous()
+        lif = layer_lif(layer)
+        y, u, bits, L, Wc, w_bf16 = syn_forward(x, W, d_eff, None, None, s_vec, s_uniform, s_max,
+                                                float(d_eff.max()), bc, m, lif)
+        ctx.save_for_backward(u, y, bits, Wc, d_eff, s_vec, m, p_spread)
+        ctx.meta = (L, w_bf16, s_uniform, float(layer.sigma), bool(layer.use_sig_p), bias is not None,
+                    W.dtype)
+        ctx.lif = lif
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        u, y, bits, Wc, d_eff, s_vec, m, p_spread = ctx.saved_tensors
+        L, w_bf16, s_uniform, sigma, use_sig_p, use_bias, w_dtype = ctx.meta
+        need_p = use_sig_p and ctx.needs_input_grad[3]
+        dx, dW, dd, ds, db = syn_backward(
+            gy, u, y, bits, Wc, w_bf16, d_eff, None, None, s_vec, s_uniform, m, ctx.lif, L,
+            ctx.needs_input_grad[1], ctx.needs_input_grad[2], need_p,
+            use_bias and ctx.needs_input_grad[4])
+        dp = None
+        if need_p:
+            with torch.enable_grad():
+                p_ = p_spread.detach().to(torch.float32).requires_grad_(True)
+                (dp,) = torch.autograd.grad(1.0 + 2.0 * sigma * torch.sigmoid(p_), p_, ds)
+        if dW is not None and w_dtype != torch.float32:
+            dW = dW.to(w_dtype)
+        return dx, dW, dd, dp, db, None, None
+
+
+def recurrent_drop(layer, x_seq):
+    """The layer's fixed recurrent-dropout mask ``(B, N)``, or ``None`` when inactive
+    (reference ``synaptic_eventdriven.py:479-483``)."""
+    T, B, N = x_seq.shape
+    if layer.training and getattr(layer.config, 'recurrent_dropout_rate', 0.0) > 0:
+        return layer.dropout(torch.ones(B, N, device=x_seq.device, dtype=x_seq.dtype))
+    return None
+
+
+def eventdriven_trainable_forward(layer, x_seq):
+    """Autograd-enabled synaptic forward; gradients reach ``recurrent_weights``,
+    ``recurrent_delays``, ``recurrent_bias``, ``p_spread`` and ``x``."""
+    T, B, N = x_seq.shape
+    drop = recurrent_drop(layer, x_seq)
+    bias = layer.recurrent_bias if layer.use_rec_bias else None
+    p_spread = (layer.p_spread if layer.use_sig_p
+                else torch.zeros(N, device=x_seq.device, dtype=x_seq.dtype))
+    return EventDrivenSyn.apply(x_seq, layer.recurrent_weights, layer.recurrent_delays,
+                                p_spread, bias, drop, layer)

@@ -1,0 +1,117 @@
+"""GPU parity of the axonal layer (HIP kernels through the C ABI) against the CPU oracle.
+
+Spikes must match exactly except at units whose oracle membrane is within 1e-5 of the
+threshold; membranes and every gradient within fp32 rtol 1e-4 / atol 1e-5 (relative to
+the scale of each tensor), as the acceptance bar states.
+"""
+
+import pytest
+import torch
+
+from helpers import assert_close, first_flip, gen, lif_params, oracle_axonal
+
+RTOL, ATOL = 1e-4, 1e-5
+
+CASES = [
+    # T,  B,  N,  dmax, sigma, extra
+    (24, 4, 32, 8.0, 0.0, {}),
+    (24, 4, 32, 8.0, 0.5, {}),
+    (20, 3, 64, 16.0, 1.0, {}),
+    (16, 2, 256, 32.0, 1.0, {}),
+    (16, 3, 48, 6.0, 1.3, {'bias': True}),
+    (16, 3, 40, 6.0, 0.7, {'soft': True}),
+    (16, 3, 40, 6.0, 0.7, {'decay_input': True}),
+    (16, 3, 40, 6.0, 0.7, {'triangle': True}),
+    (16, 3, 40, 6.0, 0.7, {'detach': True}),
+    (16, 3, 40, 6.0, 0.7, {'sig_p': True}),
+    (16, 3, 40, 6.0, 0.7, {'v_reset': -0.2}),
+    (16, 2, 300, 10.0, 0.5, {}),                 # streamed-weight layout (N > 256)
+    (12, 2, 24, 70.0, 0.0, {}),                  # window > 64 lags: two history words
+]
+
+
+def _run(dev, T, B, N, dmax, sigma, extra, seed=0):
+    from delrec.kernels import AxonalRecdelHip
+    g = gen(seed)
+    x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
+    W = torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)
+    d = torch.rand(N, generator=g) * dmax
+    gy = torch.randn(T, B, N, generator=g)
+    bias = torch.randn(N, generator=g) * 0.1 if extra.get('bias') else None
+    p = torch.randn(N, generator=g) if extra.get('sig_p') else None
+    v_reset = None if extra.get('soft') else extra.get('v_reset', 0.0)
+    surr = ('triangle', 1.0) if extra.get('triangle') else ('atan', 2.0)
+    lif = lif_params(tau=2.0, v_reset=v_reset, decay_input=extra.get('decay_input', False),
+                     detach_reset=extra.get('detach', False), surrogate=surr)
+    y_ref, u_ref, gref = oracle_axonal(x, W, d, lif, sigma, gy, bias=bias, p=p,
+                                       use_sig_p=p is not None)
+
+    leaves = [t.to(dev).requires_grad_(True) for t in (x, W, d)]
+    bg = bias.to(dev).requires_grad_(True) if bias is not None else None
+    pg = p.to(dev).requires_grad_(True) if p is not None else torch.zeros(N, device=dev)
+    y = AxonalRecdelHip.apply(leaves[0], leaves[1], bg, leaves[2], pg, None, sigma, lif.tau,
+                              lif.v_threshold, lif.v_reset, p is not None, lif.detach_reset,
+                              0 if surr[0] == 'triangle' else 1, 1.0, False, 0, 2.0,
+                              lif.decay_input)
+    (y * gy.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    return y.detach().cpu(), y_ref, u_ref, gref, leaves, bg, pg, lif
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}d{c[3]}s{c[4]}{"".join(c[5])}'
+                                            for c in CASES])
+def test_axonal_fwd_bwd_matches_oracle(dev, case):
+    T, B, N, dmax, sigma, extra = case
+    print(f'case {case}', flush=True)
+    y, y_ref, u_ref, gref, leaves, bg, pg, lif = _run(dev, T, B, N, dmax, sigma, extra)
+    flip = first_flip(y, y_ref, u_ref, lif.v_threshold)
+    assert flip is None, f'near-threshold flip at t={flip}; pick another seed'
+    print(f'  spikes identical ({int(y.sum())} spikes of {y.numel()})')
+    scale = lambda r: ATOL * max(1.0, float(r.abs().max()))
+    assert_close(leaves[0].grad, gref['x'], RTOL, scale(gref['x']), 'dx')
+    assert_close(leaves[1].grad, gref['W'], RTOL, scale(gref['W']), 'dW')
+    assert_close(leaves[2].grad, gref['d'], RTOL, scale(gref['d']), 'dd')
+    if bg is not None:
+        assert_close(bg.grad, gref['bias'], RTOL, scale(gref['bias']), 'db')
+    if 'p' in gref:
+        assert_close(pg.grad, gref['p'], RTOL, scale(gref['p']), 'dp')
+
+
+@pytest.mark.gpu
+def test_axonal_forward_membrane_and_trace_via_abi(dev):
+    """Membrane u and the saved delayed trace z, read straight from the C ABI outputs."""
+    from delrec import _lib
+    from delrec.kernels._common import bits_shape
+    from oracle import scans
+    T, B, N, sigma = 20, 3, 64, 1.0
+    g = gen(3)
+    x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
+    W = torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)
+    d = torch.rand(N, generator=g) * 10.0
+    lif = lif_params()
+    y_ref, ext = scans.axonal_v2(x, W, d, lif, sigma=sigma)
+    L = ext['L']
+    xs, Ws, ds = x.to(dev), W.to(dev), d.to(dev)
+    y = torch.empty(T, B, N, device=dev)
+    u = torch.empty_like(y)
+    z = torch.empty_like(y)
+    rec = torch.empty_like(y)
+    bits = torch.zeros(bits_shape(T, B, N), device=dev, dtype=torch.int32)
+    ws = _lib.workspace(_lib.WS_AXONAL_FWD, T, B, N, L, 0, dev)
+    args = _lib.AxonalFwdArgs(T=T, B=B, N=N, L=L, x=_lib.ptr(xs), W=_lib.ptr(Ws), w_bf16=0,
+                              bias=None, d=_lib.ptr(ds), s=None, s_uniform=1.0 + sigma, drop=None,
+                              taps=0, lag=None, frac=None,
+                              lif=_lib.make_lif(2.0, 1.0, 0.0, False, False, 1, 1.0, 2.0),
+                              y=_lib.ptr(y), u=_lib.ptr(u), rec=_lib.ptr(rec), z=_lib.ptr(z),
+                              bits=_lib.ptr(bits), workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
+    _lib.call('delrec_axonal_fwd', args, _lib.stream_of(xs))
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), y_ref)
+    assert_close(u, ext['u'], RTOL, ATOL, 'u')
+    assert_close(rec, ext['rec'], RTOL, ATOL, 'rec')
+    # the bitmask holds the same spikes
+    b = bits.cpu().to(torch.int64) & 0xFFFFFFFF
+    t = torch.arange(T)
+    unpacked = (b[:, t // 32, :] >> (t % 32).view(1, T, 1)) & 1         # (B, T, N)
+    assert torch.equal(unpacked.permute(1, 0, 2).float(), y_ref)

@@ -1,0 +1,183 @@
+"""GPU parity of the synaptic and hybrid layers against the CPU oracle."""
+
+import pytest
+import torch
+
+from helpers import assert_close, first_flip, gen, lif_params, oracle_synaptic
+
+RTOL, ATOL = 1e-4, 1e-5
+
+SYN_CASES = [
+    # T,  B,  N,  dmax, sigma, extra
+    (20, 3, 32, 6.0, 0.0, {}),
+    (20, 3, 32, 6.0, 0.5, {}),
+    (16, 2, 64, 10.0, 1.0, {'bias': True}),
+    (16, 2, 48, 6.0, 0.8, {'sig_p': True}),
+    (16, 2, 48, 6.0, 0.8, {'soft': True, 'triangle': True}),
+    (16, 2, 48, 6.0, 0.8, {'decay_input': True}),
+    (12, 2, 96, 4.0, 4.0, {}),                  # wide triangle
+]
+
+
+def _syn_inputs(T, B, N, dmax, extra, seed):
+    g = gen(seed)
+    x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
+    W = torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)
+    d = torch.rand(N, N, generator=g) * dmax
+    gy = torch.randn(T, B, N, generator=g)
+    bias = torch.randn(N, generator=g) * 0.1 if extra.get('bias') else None
+    p = torch.randn(N, generator=g) if extra.get('sig_p') else None
+    return x, W, d, gy, bias, p
+
+
+class _Layer:
+    """Minimal stand-in carrying what EventDrivenSyn / HybridSynDelay read from a layer."""
+
+    def __init__(self, sigma, lif, use_sig_p=False, p=None, round_delays=False):
+        from delrec.neuron import LIFNode, ATan
+        from delrec.utils import Triangle
+
+        class Cfg:
+            pass
+
+        cfg = Cfg()
+        kind, width = lif.surrogate
+        cfg.surrogate_function = ATan(width) if kind == 'atan' else Triangle.apply
+        cfg.surrogate_gamma = width if kind == 'triangle' else 1.0
+        cfg.detach_reset = lif.detach_reset
+        cfg.recurrent_dropout_rate = 0.0
+        self.config = cfg
+        self.neuron_module = LIFNode(tau=lif.tau, decay_input=lif.decay_input,
+                                     v_threshold=lif.v_threshold, v_reset=lif.v_reset,
+                                     detach_reset=lif.detach_reset)
+        self.sigma = sigma
+        self.use_sig_p = use_sig_p
+        self.p_spread = p
+        self.round_delays = round_delays
+        self.training = False
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', SYN_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}d{c[3]}s{c[4]}{"".join(c[5])}'
+                                                for c in SYN_CASES])
+def test_synaptic_fwd_bwd_matches_oracle(dev, case):
+    from delrec.kernels import EventDrivenSyn
+    T, B, N, dmax, sigma, extra = case
+    print(f'case {case}', flush=True)
+    x, W, d, gy, bias, p = _syn_inputs(T, B, N, dmax, extra, seed=1)
+    v_reset = None if extra.get('soft') else 0.0
+    surr = ('triangle', 1.0) if extra.get('triangle') else ('atan', 2.0)
+    lif = lif_params(v_reset=v_reset, decay_input=extra.get('decay_input', False), surrogate=surr)
+    y_ref, u_ref, gref = oracle_synaptic(x, W, d, lif, sigma, gy, bias=bias, p=p, use_sig_p=p is not None)
+
+    xg, Wg, dg = (t.to(dev).requires_grad_(True) for t in (x, W, d))
+    bg = bias.to(dev).requires_grad_(True) if bias is not None else None
+    pg = p.to(dev).requires_grad_(True) if p is not None else torch.zeros(N, device=dev)
+    layer = _Layer(sigma, lif, use_sig_p=p is not None, p=pg if p is not None else None)
+    y = EventDrivenSyn.apply(xg, Wg, dg, pg, bg, None, layer)
+    (y * gy.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    flip = first_flip(y.detach().cpu(), y_ref, u_ref, lif.v_threshold)
+    assert flip is None, f'near-threshold flip at t={flip}'
+    print(f'  spikes identical ({int(y_ref.sum())} spikes of {y_ref.numel()})')
+    scale = lambda r: ATOL * max(1.0, float(r.abs().max()))
+    assert_close(xg.grad, gref['x'], RTOL, scale(gref['x']), 'dx')
+    assert_close(Wg.grad, gref['W'], RTOL, scale(gref['W']), 'dW')
+    assert_close(dg.grad, gref['d'], RTOL, scale(gref['d']), 'dd')
+    if bg is not None:
+        assert_close(bg.grad, gref['bias'], RTOL, scale(gref['bias']), 'db')
+    if p is not None:
+        assert_close(pg.grad, gref['p'], RTOL, scale(gref['p']), 'dp')
+
+
+HYB_CASES = [
+    # T, B, N, base range (lo, hi), max offset, bf16 weights
+    (20, 3, 32, (0.0, 8.0), 4, False),
+    (20, 3, 64, (-2.0, 6.0), 4, False),          # centred base: negative effective delays
+    (16, 2, 48, (0.0, 10.0), 8, True),           # bf16 W_rec, fp32 state
+]
+
+
+def mem_config(**kw):
+    from configs.perf_MEM import Config
+    cfg = Config()
+    for k, v in kw.items():
+        setattr(cfg, k, v)
+    return cfg
+
+
+def hybrid_layer(N, W, base, offsets, dev, bf16=False, **cfg_kw):
+    """A product ``synaptic_recdel`` carrying the hybrid parametrisation with the given
+    weights, base and offsets."""
+    from delrec.delay_layers import synaptic_recdel
+    from delrec.networks import _reparametrize_recurrent_delay
+    cfg = mem_config(hybrid_base_centering='normal', **cfg_kw)
+    layer = synaptic_recdel(cfg, N)
+    _reparametrize_recurrent_delay(layer, int(offsets.max().item()) or 1, gen(5), cfg)
+    with torch.no_grad():
+        layer.parametrizations.recurrent_delays.original.copy_(base)
+        layer.parametrizations.recurrent_delays[0].offsets.copy_(offsets)
+    layer.recurrent_weights = torch.nn.Parameter(W.bfloat16() if bf16 else W.clone())
+    return layer.to(dev)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', HYB_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}{"bf16" if c[5] else ""}'
+                                                for c in HYB_CASES])
+def test_hybrid_fwd_bwd_matches_oracle(dev, case):
+    """Hybrid delays through the base + int8-offset kernel path of a parametrised layer."""
+    import delrec.kernels.synaptic_hybrid as sh
+    T, B, N, (lo, hi), K, bf16 = case
+    print(f'case {case}', flush=True)
+    g = gen(2)
+    x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
+    W = torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)
+    if bf16:
+        W = W.bfloat16().float()
+    base = lo + torch.rand(N, generator=g) * (hi - lo)
+    offsets = torch.randint(K + 1, (N, N), generator=g).float()
+    gy = torch.randn(T, B, N, generator=g)
+    lif = lif_params()
+    y_ref, u_ref, gref = oracle_synaptic(x, W, None, lif, 0.0, gy, base=base, offsets=offsets)
+
+    layer = hybrid_layer(N, W, base, offsets, dev, bf16=bf16)
+    base8, _ = sh._int8_offsets(layer)
+    assert base8 is not None, 'the base + int8 offsets path was not taken'
+    xg = x.to(dev).requires_grad_(True)
+    y = layer.multi_step_forward_hybrid_triton(xg)
+    (y * gy.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    flip = first_flip(y.detach().cpu(), y_ref, u_ref, lif.v_threshold)
+    assert flip is None, f'near-threshold flip at t={flip}'
+    print(f'  spikes identical ({int(y_ref.sum())} spikes of {y_ref.numel()})')
+    rtol = 2e-2 if bf16 else RTOL
+    scale = lambda r: ATOL * max(1.0, float(r.abs().max()))
+    assert_close(xg.grad, gref['x'], rtol, scale(gref['x']), 'dx')
+    assert_close(layer.recurrent_weights.grad.float(), gref['W'], rtol, scale(gref['W']), 'dW')
+    assert_close(layer.parametrizations.recurrent_delays.original.grad, gref['base'], rtol,
+                 scale(gref['base']), 'dbase')
+
+
+@pytest.mark.gpu
+def test_delay_grad_known_answer(dev):
+    """The reference's known-answer inputs (tests/check_hybrid_kernel.py:143-152) with the
+    expected values worked out by hand: for s = 1 the closed form picks the two or three
+    lags around 1 + d with signs -1 / 0 / +1, and C[..., l] = l^2."""
+    from delrec.kernels import _delay_grad
+    from delrec.kernels.delays import build_syn_mask
+    values = torch.tensor([0.0, 1.0, 2.0, 0.25, 1.5])
+    d = values.repeat(5, 1)
+    W = torch.arange(1, 26).float().reshape(5, 5) / 25
+    # sigma = 0: d=0 -> C2-C0 = 4; d=1 -> C3-C1 = 8; d=2 -> C4-C2 = 12; d=.25 -> C2-C1 = 3; d=1.5 -> C3-C2 = 5
+    expected = W * torch.tensor([4.0, 8.0, 12.0, 3.0, 5.0])
+    for sigma in (0.0, 0.5, 1.0):
+        mask, L = build_syn_mask(d.clone().requires_grad_(True), sigma, None, False)
+        C = torch.arange(L).float().square().expand(5, 5, L).contiguous()
+        dr = d.clone().requires_grad_(True)
+        m2, _ = build_syn_mask(dr, sigma, None, False)
+        ref, = torch.autograd.grad((m2 * W.unsqueeze(-1) * C).sum(), dr)
+        actual = _delay_grad(C.to(dev), W.to(dev), d.to(dev), sigma, L).cpu()
+        torch.testing.assert_close(actual, ref, atol=2e-5, rtol=2e-5)
+        assert ref[:, :3].abs().max() > 0
+        if sigma == 0.0:
+            torch.testing.assert_close(actual, expected, atol=1e-6, rtol=1e-6)
