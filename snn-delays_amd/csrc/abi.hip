@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 
 #include "kernels.h"
@@ -76,8 +77,8 @@ bool lif_ok(const delrec_lif& l) {
 
 // ------------------------------------------------------------------ axonal layout ------
 struct AxLayout {
-    bool res;
-    int G, CH, CHS, NZ, block, hw;
+    bool res;       // N <= 256: tiled kernels with W resident in VGPRs
+    int G, CH, CHS, NZ, block, hw, ri;
 };
 
 bool axonal_layout(int N, int L, AxLayout& o) {
@@ -87,29 +88,33 @@ bool axonal_layout(int N, int L, AxLayout& o) {
     else if (lags <= 256) o.hw = 4;
     else return false;
     if (N <= 256) {
-        o.res = true;
-        // lanes per neuron: as many as fit 1024 threads, keeping >= 4 weights per lane
-        int G = 16;
-        while (G > 1) {
-            const int rpw = 64 / G;
-            const int npad = (N + rpw - 1) / rpw * rpw;
-            const int ch = ((N + G - 1) / G + 3) / 4 * 4;
-            if (npad * G <= 1024 && ch >= 4 && ch <= 64) break;
-            G >>= 1;
+        // NJ chunk lanes of 16 sources per receiver group (a power of two <= 16), RI
+        // receivers per lane: the smallest RI that fits the lanes in 1024 threads.
+        constexpr int kCJ = 16, kCJP = 20;
+        int nj = 1;
+        while (nj * kCJ < N) nj <<= 1;
+        // RI = 8 runs 512 threads (2 waves per SIMD, 256 VGPRs per wave)
+        int ri = 1;
+        while (ri < 8 && ((N + ri - 1) / ri) * nj > (ri >= 8 ? 512 : 1024)) ri <<= 1;
+        if (ri == 4 && nj == 16) ri = 8;
+        if (const char* e = getenv("DELREC_AXONAL_RI")) {
+            const int want = atoi(e);
+            if (nj == 16 && (want == 2 || want == 4 || want == 8) &&
+                ((N + want - 1) / want) * nj <= (want >= 8 ? 512 : 1024))
+                ri = want;
         }
-        const int rpw = 64 / G;
-        const int npad = (N + rpw - 1) / rpw * rpw;
-        int ch = ((N + G - 1) / G + 3) / 4 * 4;
-        int chp = 4;
-        while (chp < ch) chp <<= 1;   // kernels are instantiated for 4..64
-        if (chp > 64 || npad * G > 1024) return false;
-        o.G = G;
-        o.CH = chp;
-        o.CHS = chp;
-        o.NZ = G * chp;
-        o.block = npad * G;
+        const int lanes = ((N + ri - 1) / ri) * nj;
+        if (lanes > (ri >= 8 ? 512 : 1024)) return false;
+        o.res = true;
+        o.G = nj;
+        o.ri = ri;
+        o.CH = kCJ;
+        o.CHS = kCJ;
+        o.NZ = nj * kCJP;
+        o.block = std::max((N + 63) / 64 * 64, (lanes + 63) / 64 * 64);
     } else {
         o.res = false;
+        o.ri = 0;
         int G = 1;
         while (G < 16) {
             const int rpw = 64 / (G * 2);
@@ -119,10 +124,7 @@ bool axonal_layout(int N, int L, AxLayout& o) {
         }
         const int rpw = 64 / G;
         const int npad = (N + rpw - 1) / rpw * rpw;
-        if (npad * G > 1024) {
-            // more receivers than threads: not supported by the one-row-per-workgroup scan
-            return false;
-        }
+        if (npad * G > 1024) return false;   // more receivers than threads of one workgroup
         o.G = G;
         o.CH = 1;
         o.CHS = (N + G - 1) / G;
@@ -132,21 +134,19 @@ bool axonal_layout(int N, int L, AxLayout& o) {
     return true;
 }
 
+// split-K count of the dW GEMM: about one 64x64-tile workgroup per CU, chunks >= 256 rows
+int dw_splits(int T, int B, int N) {
+    const int tiles = (N + 63) / 64;
+    return std::max(1, std::min((num_cus() + tiles * tiles - 1) / (tiles * tiles),
+                                std::max(1, T * B / 256)));
+}
+
 template <class C>
 void axonal_bwd_ws(C& c, int T, int B, int N, const AxLayout& lay) {
     c.template take<float>((size_t)3 * B * N);          // per-row partials
     c.template take<float>((size_t)T * B * N);          // gr (dropout / decay_input)
-    const int tiles = (N + 127) / 128;
-    const int ks = std::max(1, std::min((2 * num_cus() + tiles * tiles - 1) / (tiles * tiles),
-                                        std::max(1, T * B / 256)));
-    c.template take<float>((size_t)ks * N * N);         // dW split-K partials
+    c.template take<float>((size_t)dw_splits(T, B, N) * N * N);   // dW split-K partials
     (void)lay;
-}
-
-int dw_splits(int T, int B, int N) {
-    const int tiles = (N + 127) / 128;
-    return std::max(1, std::min((2 * num_cus() + tiles * tiles - 1) / (tiles * tiles),
-                                std::max(1, T * B / 256)));
 }
 
 // ------------------------------------------------------------------ synaptic layout ----
@@ -269,7 +269,7 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
     if (a->taps == DELREC_TAPS_INTERP && !a->frac) return DELREC_ERR_ARG;
     AxLayout lay;
     if (!axonal_layout(a->N, a->L, lay)) return DELREC_ERR_WINDOW;
-    const size_t lds = (size_t)2 * lay.NZ * sizeof(float);
+    const size_t lds = ((size_t)2 * lay.NZ + (lay.res ? (size_t)a->N : 0)) * sizeof(float);
     if (lds > (size_t)max_lds_bytes()) return DELREC_ERR_WINDOW;
     hipStream_t s = static_cast<hipStream_t>(stream);
     AxFwd p{};
@@ -287,8 +287,9 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
         if (a->w_bf16) transpose<uint16_t>(a->W, wt, a->N, s); else transpose<float>(a->W, wt, a->N, s);
         p.Wt = wt;
     }
-    if (!launch_axonal(true, &p, nullptr, lay.CH, lay.res, lay.hw, a->B, lay.block, lds, s))
-        return DELREC_ERR_UNSUPPORTED;
+    const bool ok = lay.res ? launch_axonal_tiled(true, &p, nullptr, lay.ri, lay.G, lay.hw, a->B, lay.block, lds, s)
+                            : launch_axonal(true, &p, nullptr, lay.CH, lay.res, lay.hw, a->B, lay.block, lds, s);
+    if (!ok) return DELREC_ERR_UNSUPPORTED;
     return finish_launch();
 }
 
@@ -301,7 +302,7 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     AxLayout lay;
     if (!axonal_layout(a->N, a->L, lay)) return DELREC_ERR_WINDOW;
     const int R = std::max(a->L, 2);
-    const size_t lds = ((size_t)2 * lay.NZ + (size_t)R * a->N) * sizeof(float);
+    const size_t lds = ((size_t)2 * lay.NZ + (size_t)(R + kMaxTaps) * a->N) * sizeof(float);
     if (lds > (size_t)max_lds_bytes()) return DELREC_ERR_WINDOW;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int T = a->T, B = a->B, N = a->N;
@@ -320,8 +321,9 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     p.d = a->d; p.s = a->s; p.s_uniform = a->s_uniform; p.drop = a->drop;
     p.mode = a->mode; p.lag = a->lag; p.lif = make_lif(a->lif);
     p.dx = a->dx; p.gr = need_gr ? grbuf : nullptr; p.part = part;
-    if (!launch_axonal(false, nullptr, &p, lay.CH, lay.res, lay.hw, B, lay.block, lds, s))
-        return DELREC_ERR_UNSUPPORTED;
+    const bool ok = lay.res ? launch_axonal_tiled(false, nullptr, &p, lay.ri, lay.G, lay.hw, B, lay.block, lds, s)
+                            : launch_axonal(false, nullptr, &p, lay.CH, lay.res, lay.hw, B, lay.block, lds, s);
+    if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();
     if (st) return st;
     launch_reduce_rows(part, B, N, a->db, a->dd, a->ds, s);

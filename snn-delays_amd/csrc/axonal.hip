@@ -48,6 +48,31 @@ __device__ __forceinline__ uint32_t spike_bit(const uint32_t* bits, int TW, int 
     return (bits[((size_t)b * TW + (tau >> 5)) * N + j] >> (tau & 31)) & 1u;
 }
 
+// Spike bits of one neuron read backwards in time, one 32-step word at a time, with the
+// next older word loaded a word ahead so the stream never waits on memory.
+struct SpikeStream {
+    const uint32_t* col;   // &bits[b][0][j]; word w at col[w * N]
+    int N, widx;
+    uint32_t cur, pre;
+    __device__ void init(const uint32_t* bits, int TW, int Nn, int b, int j, int tau) {
+        N = Nn;
+        col = bits + (size_t)b * TW * Nn + j;
+        widx = tau >> 5;   // arithmetic shift: -1 for tau in [-32, -1]
+        cur = widx >= 0 ? col[(size_t)widx * N] : 0u;
+        pre = widx >= 1 ? col[(size_t)(widx - 1) * N] : 0u;
+    }
+    // bit of time tau; successive calls must go down by one
+    __device__ uint32_t bit(int tau) {
+        if (tau < 0) return 0u;
+        if ((tau >> 5) != widx) {
+            widx = tau >> 5;
+            cur = pre;
+            pre = widx >= 1 ? col[(size_t)(widx - 1) * N] : 0u;
+        }
+        return (cur >> (tau & 31)) & 1u;
+    }
+};
+
 // Delayed trace of one neuron from its history (forward tap modes).
 template <int HW>
 __device__ __forceinline__ float axonal_trace(const History<HW>& h, int taps, float c, float s,
@@ -66,6 +91,9 @@ __device__ __forceinline__ float axonal_trace(const History<HW>& h, int taps, fl
 
 // ---------------------------------------------------------------------------------------
 // Forward.
+constexpr int kPrefetch = 4;      // steps of x loaded ahead of use (forward)
+constexpr int kPrefetchBwd = 3;   // steps of gy / u loaded ahead of use (backward)
+
 template <int CH, bool RES, int HW>
 __global__ void __launch_bounds__(1024) axonal_fwd_kernel(AxFwd p) {
     extern __shared__ float smem[];
@@ -90,13 +118,17 @@ __global__ void __launch_bounds__(1024) axonal_fwd_kernel(AxFwd p) {
     }
     const int jbeg = g * p.CHS, jend = min(N, jbeg + p.CHS);   // streaming chunk
 
-    // this neuron as a source of the delayed trace
-    const float dval = p.d[ic];
-    const float c = 1.0f + dval;
+    // this neuron as a source of the delayed trace: its tap weights, computed once
+    const float c = 1.0f + p.d[ic];
     const float s = p.s ? p.s[ic] : p.s_uniform;
     const float s2 = s * s;
     int lo, hi;
     tap_range(c, s, p.L, lo, hi);
+    const int nt = hi - lo + 1;
+    const bool fast = p.taps == DELREC_TAPS_SOFT && nt <= kMaxTaps && HW == 1;
+    float wq[kMaxTaps];
+#pragma unroll
+    for (int q = 0; q < kMaxTaps; ++q) wq[q] = (q < nt) ? tri_weight((float)(lo + q), c, s, s2) : 0.0f;
     const int lag = p.lag ? p.lag[ic] : 1;
     const float frac = p.frac ? p.frac[ic] : 0.0f;
     const float m = p.drop ? p.drop[(size_t)b * N + ic] : 1.0f;
@@ -111,8 +143,9 @@ __global__ void __launch_bounds__(1024) axonal_fwd_kernel(AxFwd p) {
     uint32_t word = 0;
     const size_t BN = (size_t)B * N;
     const size_t row = (size_t)b * N + ic;
-    float xq0 = act ? p.x[row] : 0.0f;
-    float xq1 = (act && T > 1) ? p.x[BN + row] : 0.0f;
+    float xq[kPrefetch];
+#pragma unroll
+    for (int q = 0; q < kPrefetch; ++q) xq[q] = (act && q < T) ? p.x[(size_t)q * BN + row] : 0.0f;
     if (act && g == 0 && p.z) p.z[row] = 0.0f;
 
     for (int t = 0; t < T; ++t) {
@@ -132,11 +165,12 @@ __global__ void __launch_bounds__(1024) axonal_fwd_kernel(AxFwd p) {
             for (int j = jbeg; j < jend; ++j)
                 acc = fmaf(act ? load_w(p.Wt, p.w_bf16, (size_t)j * N + i) : 0.0f, zc[j], acc);
         }
-        for (int msk = G >> 1; msk > 0; msk >>= 1) acc += wave_xor(acc, msk);
+        acc = group_sum(acc, G);
 
-        const float xv = xq0;
-        xq0 = xq1;
-        if (act && t + 2 < T) xq1 = p.x[(size_t)(t + 2) * BN + row];
+        const float xv = xq[0];
+#pragma unroll
+        for (int q = 0; q < kPrefetch - 1; ++q) xq[q] = xq[q + 1];
+        xq[kPrefetch - 1] = (act && t + kPrefetch < T) ? p.x[(size_t)(t + kPrefetch) * BN + row] : 0.0f;
 
         const float r = acc + bias;
         const float a = xv + r * m;
@@ -155,13 +189,21 @@ __global__ void __launch_bounds__(1024) axonal_fwd_kernel(AxFwd p) {
         }
         if ((t & 31) == 31) word = 0;
         if (t + 1 < T) {
-            const float zn = act ? axonal_trace<HW>(hist, p.taps, c, s, s2, lo, hi, lag, frac) : 0.0f;
+            float zn;
+            if (fast) {
+                const uint64_t hs = hist.w[0] >> (lo - 1);
+                zn = 0.0f;
+#pragma unroll
+                for (int q = 0; q < kMaxTaps; ++q) zn += wq[q] * (float)((hs >> q) & 1ull);
+            } else {
+                zn = axonal_trace<HW>(hist, p.taps, c, s, s2, lo, hi, lag, frac);
+            }
             if (act && g == 0) {
                 zbuf[((t + 1) & 1) * NZ + i] = zn;
                 if (p.z) p.z[(size_t)(t + 1) * BN + row] = zn;
             }
         }
-        __syncthreads();
+        barrier_lds();
     }
 }
 
@@ -173,6 +215,7 @@ __global__ void __launch_bounds__(1024) axonal_bwd_kernel(AxBwd p) {
     const int N = p.N, T = p.T, B = p.B, G = p.G, NZ = p.NZ, R = p.R, NP = p.NP;
     float* grbuf = smem;                 // [2][NZ]
     float* ring = smem + 2 * NZ;         // [R][NP] future gz
+    float* htab = ring + R * NP;         // [kMaxTaps][NP] tap weights of each source
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
     const int j = tid / G, g = tid - (tid / G) * G;
@@ -191,16 +234,25 @@ __global__ void __launch_bounds__(1024) axonal_bwd_kernel(AxBwd p) {
     }
     const int ibeg = g * p.CHS, iend = min(N, ibeg + p.CHS);
 
-    const float dval = p.d[jc];
-    const float c = 1.0f + dval;
+    const float c = 1.0f + p.d[jc];
     const float s = p.s ? p.s[jc] : p.s_uniform;
     const float s2 = s * s;
     int lo, hi;
     tap_range(c, s, p.L, lo, hi);
+    const int nt = hi - lo + 1;
+    const bool soft = p.mode == DELREC_BWD_SOFT;
+    const bool fast = soft && nt <= kMaxTaps && HW == 1;
+    const bool need_ds = p.s != nullptr;
+
     const int lag = p.lag ? p.lag[jc] : 1;
     const float m = p.drop ? p.drop[(size_t)b * N + jc] : 1.0f;
 
     for (int q = tid; q < 2 * NZ + R * NP; q += blockDim.x) smem[q] = 0.0f;
+    if (act && g == 0) {
+#pragma unroll
+        for (int q = 0; q < kMaxTaps; ++q)
+            htab[q * NP + j] = (q < nt) ? tri_weight((float)(lo + q), c, s, s2) : 0.0f;
+    }
     __syncthreads();
 
     // past spikes of j relative to step t: bit(l) = y[t-l]; start at t = T-1
@@ -210,13 +262,30 @@ __global__ void __launch_bounds__(1024) axonal_bwd_kernel(AxBwd p) {
 
     const size_t BN = (size_t)B * N;
     const size_t rowj = (size_t)b * N + jc;
+    float gq[kPrefetchBwd], uq[kPrefetchBwd];
+#pragma unroll
+    for (int q = 0; q < kPrefetchBwd; ++q) {
+        const int tt = T - 1 - q;
+        gq[q] = (act && tt >= 0) ? p.gy[(size_t)tt * BN + rowj] : 0.0f;
+        uq[q] = (act && tt >= 0) ? p.u[(size_t)tt * BN + rowj] : 0.0f;
+    }
     float lam = 0.0f, db_acc = 0.0f, dd_acc = 0.0f, ds_acc = 0.0f;
     int tmod = (T - 1) % R;
 
     for (int t = T - 1; t >= 0; --t) {
         // future gradient through the delayed trace
         float gfut = 0.0f;
-        if (p.mode == DELREC_BWD_SOFT) {
+        if (fast) {
+#pragma unroll
+            for (int q = 0; q < kMaxTaps; ++q) {
+                const int l = lo + q;
+                if (q < nt && t + l < T) {
+                    int slot = tmod + l;
+                    if (slot >= R) slot -= R;
+                    gfut += htab[q * NP + jc] * ring[slot * NP + jc];
+                }
+            }
+        } else if (soft) {
             for (int l = lo; l <= hi && t + l < T; ++l) {
                 int slot = tmod + l;
                 if (slot >= R) slot -= R;
@@ -227,21 +296,29 @@ __global__ void __launch_bounds__(1024) axonal_bwd_kernel(AxBwd p) {
             if (slot >= R) slot -= R;
             gfut = ring[slot * NP + jc];
         }
-        const size_t o = (size_t)t * BN + rowj;
-        const float gy = act ? p.gy[o] : 0.0f;
-        const float u = act ? p.u[o] : 0.0f;
+        const float gy = gq[0], u = uq[0];
+#pragma unroll
+        for (int q = 0; q < kPrefetchBwd - 1; ++q) {
+            gq[q] = gq[q + 1];
+            uq[q] = uq[q + 1];
+        }
+        const int tn = t - kPrefetchBwd;
+        gq[kPrefetchBwd - 1] = (act && tn >= 0) ? p.gy[(size_t)tn * BN + rowj] : 0.0f;
+        uq[kPrefetchBwd - 1] = (act && tn >= 0) ? p.u[(size_t)tn * BN + rowj] : 0.0f;
+
         const float y = lif_fire(k, u);
         const float du = lif_backward(k, gy + gfut, u, y, lam);
         lam = k.decay * du;
         const float da = lif_dx(k, du);       // dL/d(input of the charge)
         const float gr = da * m;
         if (act && g == 0) {
+            const size_t o = (size_t)t * BN + rowj;
             p.dx[o] = da;
             if (p.gr) p.gr[o] = gr;
             grbuf[(t & 1) * NZ + j] = gr;
         }
         db_acc += gr;
-        __syncthreads();
+        barrier_lds();
 
         // gz_j = sum_i gr_i W[i, j]
         const float* gb = grbuf + (t & 1) * NZ;
@@ -260,17 +337,23 @@ __global__ void __launch_bounds__(1024) axonal_bwd_kernel(AxBwd p) {
             for (int i = ibeg; i < iend; ++i)
                 acc = fmaf(act ? load_w(p.W, p.w_bf16, (size_t)i * N + j) : 0.0f, gb[i], acc);
         }
-        for (int msk = G >> 1; msk > 0; msk >>= 1) acc += wave_xor(acc, msk);
-        const float gz = acc;
+        const float gz = group_sum(acc, G);
         if (act) ring[tmod * NP + j] = gz;
 
         // delay / half-width gradients: dL/dh[j,l] = gz_t * y[t-l]
-        if (p.mode == DELREC_BWD_SOFT) {
+        if (fast && !need_ds) {
+            const uint64_t ps = past.w[0] >> (lo - 1);
+            float sd = 0.0f;
+#pragma unroll
+            for (int q = 0; q < kMaxTaps; ++q)
+                if (q < nt && ((ps >> q) & 1ull)) sd += tri_dsign((float)(lo + q), c, s);
+            dd_acc += gz * sd;
+        } else if (soft) {
             float sd = 0.0f, sds = 0.0f;
             for (int l = lo; l <= hi; ++l) {
                 const float yv = past.bit(l);
                 sd += tri_dsign((float)l, c, s) * yv;
-                sds += tri_ds((float)l, c, s, s2) * yv;
+                if (need_ds) sds += tri_ds((float)l, c, s, s2) * yv;
             }
             dd_acc += gz * sd;
             ds_acc += gz * sds;
@@ -284,22 +367,346 @@ __global__ void __launch_bounds__(1024) axonal_bwd_kernel(AxBwd p) {
     }
     if (act && g == 0) {
         p.part[(size_t)0 * B * N + rowj] = db_acc;
-        p.part[(size_t)1 * B * N + rowj] = (p.mode == DELREC_BWD_SOFT) ? dd_acc / s2 : dd_acc;
+        p.part[(size_t)1 * B * N + rowj] = soft ? dd_acc / s2 : dd_acc;
         p.part[(size_t)2 * B * N + rowj] = ds_acc;
     }
 }
 
-// Sum the per-row partials over the batch: out_k[j] = sum_b part[k][b][j].
-__global__ void reduce_rows_kernel(const float* part, int B, int N, float* o0, float* o1, float* o2) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+// ---------------------------------------------------------------------------------------
+// Tiled forms for N <= 256 (the fast path). The GEMV lanes hold an RI x CJ tile of W in
+// VGPRs: lane (grp, jcg) owns receivers grp*RI .. +RI and sources jcg*CJ .. +CJ; the NJ
+// chunk lanes of a group sit in one 16-lane DPP row and reduce there. Per-neuron work
+// (LIF, trace, stores) runs on lanes tid < N only. z / gr are broadcast through LDS with
+// a chunk pitch of CJ + 4 floats so the NJ chunk reads of a row hit distinct banks.
+constexpr int kCJ = 16;
+constexpr int kCJP = kCJ + 4;
+
+__device__ __forceinline__ int zpos(int j) { return (j / kCJ) * kCJP + (j % kCJ); }
+
+template <int RI> struct TiledThreads { static constexpr int value = RI >= 8 ? 512 : 1024; };
+
+template <int RI, int NJ, int HW>
+__global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_fwd_tiled(AxFwd p) {
+    extern __shared__ float smem[];
+    const int N = p.N, T = p.T, B = p.B, NZ = p.NZ;
+    float* zbuf = smem;                 // [2][NZ], NZ = NJ * kCJP
+    float* rbuf = smem + 2 * NZ;        // [N] recurrent input of this step
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int grp = tid / NJ, jcg = tid - (tid / NJ) * NJ;
+    const Lif k = p.lif;
+    const int TW = (T + 31) >> 5;
+
+    float w[RI][kCJ];
+#pragma unroll
+    for (int a = 0; a < RI; ++a)
+#pragma unroll
+        for (int c = 0; c < kCJ; ++c) {
+            const int i = grp * RI + a, j = jcg * kCJ + c;
+            w[a][c] = (i < N && j < N) ? load_w(p.W, p.w_bf16, (size_t)i * N + j) : 0.0f;
+        }
+
+    // per-neuron lanes
+    const bool nl = tid < N;
+    const int i = nl ? tid : 0;
+    const float c = 1.0f + p.d[i];
+    const float s = p.s ? p.s[i] : p.s_uniform;
+    const float s2 = s * s;
+    int lo, hi;
+    tap_range(c, s, p.L, lo, hi);
+    const int nt = hi - lo + 1;
+    const bool fast = p.taps == DELREC_TAPS_SOFT && nt <= kMaxTaps && HW == 1;
+    float wq[kMaxTaps];
+#pragma unroll
+    for (int q = 0; q < kMaxTaps; ++q) wq[q] = (q < nt) ? tri_weight((float)(lo + q), c, s, s2) : 0.0f;
+    const int lag = p.lag ? p.lag[i] : 1;
+    const float frac = p.frac ? p.frac[i] : 0.0f;
+    const float m = p.drop ? p.drop[(size_t)b * N + i] : 1.0f;
+    const float bias = p.bias ? p.bias[i] : 0.0f;
+
+    for (int q = tid; q < 2 * NZ; q += blockDim.x) zbuf[q] = 0.0f;
+    __syncthreads();
+
+    History<HW> hist;
+    hist.clear();
+    float v = k.v0;
+    uint32_t word = 0;
+    const size_t BN = (size_t)B * N;
+    const size_t row = (size_t)b * N + i;
+    float xq[kPrefetch];
+#pragma unroll
+    for (int q = 0; q < kPrefetch; ++q) xq[q] = (nl && q < T) ? p.x[(size_t)q * BN + row] : 0.0f;
+    if (nl && p.z) p.z[row] = 0.0f;
+
+    // one time step; `xs` is this step's prefetch slot, refilled with x[t + kPrefetch]
+    auto step = [&](const int t, float& xs) {
+        // GEMV: r_i = sum_j W[i, j] z_j over this lane's tile, reduced across the row
+        const float4* z4 = reinterpret_cast<const float4*>(zbuf + (t & 1) * NZ + jcg * kCJP);
+        float acc[RI];
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc[a] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kCJ / 4; ++q) {
+            const float4 zz = z4[q];
+#pragma unroll
+            for (int a = 0; a < RI; ++a) {
+                acc[a] = fmaf(w[a][4 * q + 0], zz.x, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 1], zz.y, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 2], zz.z, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 3], zz.w, acc[a]);
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc[a] = group_sum_t<NJ>(acc[a]);
+        if (jcg == 0) {
+#pragma unroll
+            for (int a = 0; a < RI; ++a)
+                if (grp * RI + a < N) rbuf[grp * RI + a] = acc[a];
+        }
+        barrier_lds();
+
+        if (nl) {
+            const float xv = xs;
+            xs = (t + kPrefetch < T) ? p.x[(size_t)(t + kPrefetch) * BN + row] : 0.0f;
+            const float r = rbuf[i] + bias;
+            const float a = xv + r * m;
+            const float u = lif_charge(k, v, a);
+            const float y = lif_fire(k, u);
+            v = lif_reset(k, u, y);
+            const uint32_t yb = y != 0.0f ? 1u : 0u;
+            hist.push(yb);
+            word |= yb << (t & 31);
+            const size_t o = (size_t)t * BN + row;
+            p.y[o] = y;
+            p.u[o] = u;
+            if (p.rec) p.rec[o] = r;
+            if ((t & 31) == 31 || t == T - 1) {
+                p.bits[((size_t)b * TW + (t >> 5)) * N + i] = word;
+                word = 0;
+            }
+            if (t + 1 < T) {
+                float zn;
+                if (fast) {
+                    const uint64_t hs = hist.w[0] >> (lo - 1);
+                    zn = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < kMaxTaps; ++q) zn += wq[q] * (float)((hs >> q) & 1ull);
+                } else {
+                    zn = axonal_trace<HW>(hist, p.taps, c, s, s2, lo, hi, lag, frac);
+                }
+                zbuf[((t + 1) & 1) * NZ + zpos(i)] = zn;
+                if (p.z) p.z[(size_t)(t + 1) * BN + row] = zn;
+            }
+        }
+        barrier_lds();
+    };
+
+    for (int t0 = 0; t0 < T; t0 += kPrefetch) {
+#pragma unroll
+        for (int q = 0; q < kPrefetch; ++q)
+            if (t0 + q < T) step(t0 + q, xq[q]);
+    }
+}
+
+template <int RI, int NJ, int HW>
+__global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBwd p) {
+    extern __shared__ float smem[];
+    const int N = p.N, T = p.T, B = p.B, NZ = p.NZ, R = p.R, NP = p.NP;
+    float* grbuf = smem;                 // [2][NZ]
+    float* ring = smem + 2 * NZ;         // [R][NP] gz of the future steps
+    float* htab = ring + R * NP;         // [kMaxTaps][NP] tap weights of each source
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int grp = tid / NJ, jcg = tid - (tid / NJ) * NJ;
+    const Lif k = p.lif;
+    const int TW = (T + 31) >> 5;
+
+    // tile of W^T: sources grp*RI + a (rows of the GEMV), receivers jcg*CJ + c (columns)
+    float w[RI][kCJ];
+#pragma unroll
+    for (int a = 0; a < RI; ++a)
+#pragma unroll
+        for (int cc = 0; cc < kCJ; ++cc) {
+            const int j = grp * RI + a, i = jcg * kCJ + cc;
+            w[a][cc] = (i < N && j < N) ? load_w(p.W, p.w_bf16, (size_t)i * N + j) : 0.0f;
+        }
+
+    const bool nl = tid < N;
+    const int j = nl ? tid : 0;
+    const float c = 1.0f + p.d[j];
+    const float s = p.s ? p.s[j] : p.s_uniform;
+    const float s2 = s * s;
+    int lo, hi;
+    tap_range(c, s, p.L, lo, hi);
+    const int nt = hi - lo + 1;
+    const bool soft = p.mode == DELREC_BWD_SOFT;
+    const bool fast = soft && nt <= kMaxTaps && HW == 1;
+    const bool need_ds = p.s != nullptr;
+    const int lag = p.lag ? p.lag[j] : 1;
+    const float m = p.drop ? p.drop[(size_t)b * N + j] : 1.0f;
+
+    for (int q = tid; q < 2 * NZ + R * NP; q += blockDim.x) smem[q] = 0.0f;
+    if (nl) {
+#pragma unroll
+        for (int q = 0; q < kMaxTaps; ++q)
+            htab[q * NP + j] = (q < nt) ? tri_weight((float)(lo + q), c, s, s2) : 0.0f;
+    }
+    __syncthreads();
+
+    History<HW> past;   // bit(l) = y[tw - l] for the window time tw
+    past.clear();
+    if (nl)
+        for (int l = 64 * HW; l >= 1; --l) past.push(spike_bit(p.bits, TW, N, b, T - 1 - l, j));
+    SpikeStream oldest;  // the bit that enters the window at lag 64*HW
+    oldest.init(p.bits, TW, N, b, j, T - 2 - 64 * HW);
+
+    const size_t BN = (size_t)B * N;
+    const size_t rowj = (size_t)b * N + j;
+    float gq[kPrefetchBwd], uq[kPrefetchBwd];
+#pragma unroll
+    for (int q = 0; q < kPrefetchBwd; ++q) {
+        const int tt = T - 1 - q;
+        gq[q] = (nl && tt >= 0) ? p.gy[(size_t)tt * BN + rowj] : 0.0f;
+        uq[q] = (nl && tt >= 0) ? p.u[(size_t)tt * BN + rowj] : 0.0f;
+    }
+    float lam = 0.0f, db_acc = 0.0f, dd_acc = 0.0f, ds_acc = 0.0f;
+
+    // dd / ds contribution of gz at the window time: dL/dh[j,l] = gz * y[tw-l]
+    auto delay_grad = [&](float gz) {
+        if (fast && !need_ds) {
+            const uint64_t ps = past.w[0] >> (lo - 1);
+            float sd = 0.0f;
+#pragma unroll
+            for (int q = 0; q < kMaxTaps; ++q)
+                if (q < nt && ((ps >> q) & 1ull)) sd += tri_dsign((float)(lo + q), c, s);
+            dd_acc += gz * sd;
+        } else if (soft) {
+            float sd = 0.0f, sds = 0.0f;
+            for (int l = lo; l <= hi; ++l) {
+                const float yv = past.bit(l);
+                sd += tri_dsign((float)l, c, s) * yv;
+                if (need_ds) sds += tri_ds((float)l, c, s, s2) * yv;
+            }
+            dd_acc += gz * sd;
+            ds_acc += gz * sds;
+        } else {
+            dd_acc += gz * (past.bit(lag + 1) - past.bit(lag));
+        }
+    };
+
+    int tmod = (T - 1) % R;
+    // one reverse step; `gs`, `us` are this step's prefetch slots, refilled with step t - P
+    auto step = [&](const int t, float& gs, float& us) {
+        if (nl) {
+            if (t < T - 1) {
+                int s1 = tmod + 1;
+                if (s1 >= R) s1 -= R;
+                delay_grad(ring[s1 * NP + j]);                 // gz_{t+1} with the window of t+1
+                past.pull(oldest.bit(t - 64 * HW));
+            }
+            float gfut = 0.0f;
+            if (fast) {
+#pragma unroll
+                for (int q = 0; q < kMaxTaps; ++q) {
+                    const int l = lo + q;
+                    if (q < nt && t + l < T) {
+                        int slot = tmod + l;
+                        if (slot >= R) slot -= R;
+                        gfut += htab[q * NP + j] * ring[slot * NP + j];
+                    }
+                }
+            } else if (soft) {
+                for (int l = lo; l <= hi && t + l < T; ++l) {
+                    int slot = tmod + l;
+                    if (slot >= R) slot -= R;
+                    gfut += tri_weight((float)l, c, s, s2) * ring[slot * NP + j];
+                }
+            } else if (t + lag < T) {
+                int slot = tmod + lag;
+                if (slot >= R) slot -= R;
+                gfut = ring[slot * NP + j];
+            }
+            const float gy = gs, u = us;
+            const int tn = t - kPrefetchBwd;
+            gs = tn >= 0 ? p.gy[(size_t)tn * BN + rowj] : 0.0f;
+            us = tn >= 0 ? p.u[(size_t)tn * BN + rowj] : 0.0f;
+
+            const float y = lif_fire(k, u);
+            const float du = lif_backward(k, gy + gfut, u, y, lam);
+            lam = k.decay * du;
+            const float da = lif_dx(k, du);
+            const float gr = da * m;
+            const size_t o = (size_t)t * BN + rowj;
+            p.dx[o] = da;
+            if (p.gr) p.gr[o] = gr;
+            grbuf[(t & 1) * NZ + zpos(j)] = gr;
+            db_acc += gr;
+        }
+        barrier_lds();
+
+        // gz_j = sum_i gr_i W[i, j]
+        const float4* g4 = reinterpret_cast<const float4*>(grbuf + (t & 1) * NZ + jcg * kCJP);
+        float acc[RI];
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc[a] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kCJ / 4; ++q) {
+            const float4 gg = g4[q];
+#pragma unroll
+            for (int a = 0; a < RI; ++a) {
+                acc[a] = fmaf(w[a][4 * q + 0], gg.x, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 1], gg.y, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 2], gg.z, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 3], gg.w, acc[a]);
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc[a] = group_sum_t<NJ>(acc[a]);
+        if (jcg == 0) {
+#pragma unroll
+            for (int a = 0; a < RI; ++a)
+                if (grp * RI + a < N) ring[tmod * NP + grp * RI + a] = acc[a];
+        }
+        barrier_lds();
+        tmod = tmod == 0 ? R - 1 : tmod - 1;
+    };
+
+    // steps T-1, T-2, ... in groups of kPrefetchBwd; slot q holds step T-1-(n*P+q)
+    for (int t0 = T - 1; t0 >= 0; t0 -= kPrefetchBwd) {
+#pragma unroll
+        for (int q = 0; q < kPrefetchBwd; ++q)
+            if (t0 - q >= 0) step(t0 - q, gq[q], uq[q]);
+    }
+    if (nl) {
+        int s0 = tmod + 1;
+        if (s0 >= R) s0 -= R;
+        delay_grad(ring[s0 * NP + j]);                          // gz_0 with the window of 0
+        p.part[(size_t)0 * B * N + rowj] = db_acc;
+        p.part[(size_t)1 * B * N + rowj] = soft ? dd_acc / s2 : dd_acc;
+        p.part[(size_t)2 * B * N + rowj] = ds_acc;
+    }
+}
+
+// Sum the per-row partials over the batch: out_k[j] = sum_b part[k][b][j]. Block (64, 16):
+// 64 consecutive neurons x 16 batch stripes, reduced through LDS.
+__global__ void __launch_bounds__(1024) reduce_rows_kernel(const float* part, int B, int N,
+                                                           float* o0, float* o1, float* o2) {
+    __shared__ float red[16][65];
     const int kk = blockIdx.y;
-    if (j >= N) return;
     float* out = kk == 0 ? o0 : (kk == 1 ? o1 : o2);
     if (!out) return;
+    const int j = blockIdx.x * 64 + threadIdx.x;
     const float* src = part + (size_t)kk * B * N;
     float acc = 0.0f;
-    for (int b = 0; b < B; ++b) acc += src[(size_t)b * N + j];
-    out[j] = acc;
+    if (j < N)
+        for (int b = threadIdx.y; b < B; b += 16) acc += src[(size_t)b * N + j];
+    red[threadIdx.y][threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.y == 0 && j < N) {
+        float t = 0.0f;
+        for (int r = 0; r < 16; ++r) t += red[r][threadIdx.x];
+        out[j] = t;
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -325,19 +732,40 @@ __global__ void reduce_rows_kernel(const float* part, int B, int N, float* o0, f
 
 bool launch_axonal(bool fwd, const AxFwd* fa, const AxBwd* ba, int ch, bool res, int hw,
                    int grid, int block, size_t lds, hipStream_t stream) {
-    DELREC_AX_HW(4, true)
-    DELREC_AX_HW(8, true)
-    DELREC_AX_HW(16, true)
-    DELREC_AX_HW(32, true)
-    DELREC_AX_HW(64, true)
     DELREC_AX_HW(1, false)
+    return false;
+}
+
+#define DELREC_AXT_CASE(RIV, NJV, HWV)                                                      \
+    if (ri == RIV && nj == NJV && hw == HWV) {                                              \
+        if (fwd) {                                                                          \
+            (void)hipFuncSetAttribute((const void*)axonal_fwd_tiled<RIV, NJV, HWV>,         \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+            hipLaunchKernelGGL((axonal_fwd_tiled<RIV, NJV, HWV>), dim3(grid), dim3(block),   \
+                               lds, stream, *fa);                                           \
+        } else {                                                                            \
+            (void)hipFuncSetAttribute((const void*)axonal_bwd_tiled<RIV, NJV, HWV>,         \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+            hipLaunchKernelGGL((axonal_bwd_tiled<RIV, NJV, HWV>), dim3(grid), dim3(block),   \
+                               lds, stream, *ba);                                           \
+        }                                                                                   \
+        return true;                                                                        \
+    }
+#define DELREC_AXT_HW(RIV, NJV) \
+    DELREC_AXT_CASE(RIV, NJV, 1) DELREC_AXT_CASE(RIV, NJV, 2) DELREC_AXT_CASE(RIV, NJV, 4)
+
+// (RI, NJ) pairs chosen by the host layout for N <= 256
+bool launch_axonal_tiled(bool fwd, const AxFwd* fa, const AxBwd* ba, int ri, int nj, int hw,
+                         int grid, int block, size_t lds, hipStream_t stream) {
+    DELREC_AXT_HW(1, 1) DELREC_AXT_HW(1, 2) DELREC_AXT_HW(1, 4) DELREC_AXT_HW(1, 8)
+    DELREC_AXT_HW(2, 16) DELREC_AXT_HW(4, 16) DELREC_AXT_HW(8, 16)
     return false;
 }
 
 void launch_reduce_rows(const float* part, int B, int N, float* o0, float* o1, float* o2,
                         hipStream_t stream) {
-    dim3 grid((N + 255) / 256, 3);
-    hipLaunchKernelGGL(reduce_rows_kernel, grid, dim3(256), 0, stream, part, B, N, o0, o1, o2);
+    dim3 grid((N + 63) / 64, 3);
+    hipLaunchKernelGGL(reduce_rows_kernel, grid, dim3(64, 16), 0, stream, part, B, N, o0, o1, o2);
 }
 
 }  // namespace delrec

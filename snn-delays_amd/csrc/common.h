@@ -110,11 +110,16 @@ __device__ __forceinline__ float tri_ds(float l, float c, float s, float s2) {
     return 1.0f / s2 - (inner / (s2 * s2)) * (s + s);
 }
 
-// First and last integer lag >= 1 whose closed-support derivative may be non-zero:
-// |l - c| <= s  ->  l in [ceil(c - s), floor(c + s)].
+// First and last integer lag in [1, L-1] on the closed support |l - c| <= s (the lags
+// whose weight or derivative may be non-zero), decided with the same fp32 test the
+// weight functions use.
 __device__ __forceinline__ void tap_range(float c, float s, int L, int& lo, int& hi) {
     lo = (int)ceilf(c - s);
+    if (fabsf((float)(lo - 1) - c) <= s) lo -= 1;
+    if (fabsf((float)lo - c) > s) lo += 1;
     hi = (int)floorf(c + s);
+    if (fabsf((float)(hi + 1) - c) <= s) hi += 1;
+    if (fabsf((float)hi - c) > s) hi -= 1;
     if (lo < 1) lo = 1;
     if (hi > L - 1) hi = L - 1;
 }
@@ -134,5 +139,43 @@ __device__ __forceinline__ float load_w(const void* W, int bf16, size_t idx) {
 __device__ __forceinline__ float wave_xor(float v, int mask) {
     return __shfl_xor(v, mask, kWave);
 }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of G consecutive lanes (G a power of two); every lane of the
+// group receives the total. DPP quad permutes / row mirrors for G <= 16.
+__device__ __forceinline__ float group_sum(float v, int G) {
+    if (G >= 2) v += dpp<0xB1>(v);    // quad_perm [1,0,3,2]: lane ^ 1
+    if (G >= 4) v += dpp<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
+    if (G >= 8) v += dpp<0x141>(v);   // row_half_mirror: other quad of the 8-lane half row
+    if (G >= 16) v += dpp<0x140>(v);  // row_mirror: other half of the 16-lane row
+    if (G >= 32) v += wave_xor(v, 16);
+    if (G >= 64) v += wave_xor(v, 32);
+    return v;
+}
+
+// Workgroup barrier that orders LDS only: outstanding global loads (prefetches) and
+// stores stay in flight across it. Every LDS access that must be visible to other
+// waves is complete (lgkmcnt 0) before the barrier.
+__device__ __forceinline__ void barrier_lds() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Compile-time group width: no runtime branches in the reduction.
+template <int G>
+__device__ __forceinline__ float group_sum_t(float v) {
+    if constexpr (G >= 2) v += dpp<0xB1>(v);
+    if constexpr (G >= 4) v += dpp<0x4E>(v);
+    if constexpr (G >= 8) v += dpp<0x141>(v);
+    if constexpr (G >= 16) v += dpp<0x140>(v);
+    if constexpr (G >= 32) v += wave_xor(v, 16);
+    if constexpr (G >= 64) v += wave_xor(v, 32);
+    return v;
+}
+
+constexpr int kMaxTaps = 8;   // register-resident tap weights per neuron (fast path)
 
 }  // namespace delrec

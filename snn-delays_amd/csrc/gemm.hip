@@ -16,59 +16,99 @@ namespace delrec {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kDwTile = 128;
-constexpr int kDwKt = 16;
+constexpr int kDwTile = 64;
+constexpr int kDwKt = 32;
+constexpr int kDwPitch = kDwTile + 4;
 
+// 64x64 output tile per workgroup (4 waves of 32x32, 2x2 MFMA blocks each); the K range
+// of the split is staged through two LDS buffers 32 rows at a time, the next stage's
+// global loads (float4) held in registers while the current stage is multiplied.
 __global__ void __launch_bounds__(256) dw_gemm_kernel(const float* __restrict__ A,
                                                       const float* __restrict__ Bm, int K, int N,
                                                       int kchunk, float* __restrict__ partial) {
-    __shared__ float sA[kDwKt][kDwTile + 4];
-    __shared__ float sB[kDwKt][kDwTile + 4];
+    __shared__ float sA[2][kDwKt][kDwPitch];
+    __shared__ float sB[2][kDwKt][kDwPitch];
     const int i0 = blockIdx.x * kDwTile, j0 = blockIdx.y * kDwTile, ks = blockIdx.z;
     const int kb = ks * kchunk, ke = min(K, kb + kchunk);
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wi = w >> 1, wj = w & 1;
     const int lr = lane >> 4, lc = lane & 15;
-    floatx4 acc[4][4];
+    const bool vec = (N & 3) == 0;
+    // staging assignment: 32 rows x 16 float4 per matrix = 512 float4, 2 per thread
+    const int r0 = threadIdx.x >> 4, c4 = (threadIdx.x & 15) * 4;
+    floatx4 acc[2][2];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[a][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < 2; ++c) acc[a][c] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    for (int k0 = kb; k0 < ke; k0 += kDwKt) {
-        for (int q = threadIdx.x; q < kDwKt * kDwTile; q += 256) {
-            const int r = q / kDwTile, c = q - r * kDwTile;
-            const int k = k0 + r;
+    float4 ra[2], rb[2];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = k0 + r0 + 16 * h;
             const bool kin = k < ke;
-            sA[r][c] = (kin && i0 + c < N) ? A[(size_t)k * N + i0 + c] : 0.0f;
-            sB[r][c] = (kin && j0 + c < N) ? Bm[(size_t)k * N + j0 + c] : 0.0f;
+            if (vec) {
+                ra[h] = (kin && i0 + c4 < N) ? *reinterpret_cast<const float4*>(A + (size_t)k * N + i0 + c4)
+                                             : float4{0.f, 0.f, 0.f, 0.f};
+                rb[h] = (kin && j0 + c4 < N) ? *reinterpret_cast<const float4*>(Bm + (size_t)k * N + j0 + c4)
+                                             : float4{0.f, 0.f, 0.f, 0.f};
+            } else {
+                float a4[4], b4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    a4[e] = (kin && i0 + c4 + e < N) ? A[(size_t)k * N + i0 + c4 + e] : 0.0f;
+                    b4[e] = (kin && j0 + c4 + e < N) ? Bm[(size_t)k * N + j0 + c4 + e] : 0.0f;
+                }
+                ra[h] = float4{a4[0], a4[1], a4[2], a4[3]};
+                rb[h] = float4{b4[0], b4[1], b4[2], b4[3]};
+            }
         }
-        __syncthreads();
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            *reinterpret_cast<float4*>(&sA[buf][r0 + 16 * h][c4]) = ra[h];
+            *reinterpret_cast<float4*>(&sB[buf][r0 + 16 * h][c4]) = rb[h];
+        }
+    };
+
+    int buf = 0;
+    if (kb < ke) {
+        fetch(kb);
+        stash(0);
+    }
+    __syncthreads();
+    for (int k0 = kb; k0 < ke; k0 += kDwKt) {
+        const bool more = k0 + kDwKt < ke;
+        if (more) fetch(k0 + kDwKt);
 #pragma unroll
         for (int kk = 0; kk < kDwKt; kk += 4) {
-            float av[4], bv[4];
+            float av[2], bv[2];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                av[q] = sA[kk + lr][wi * 64 + q * 16 + lc];
-                bv[q] = sB[kk + lr][wj * 64 + q * 16 + lc];
+            for (int q = 0; q < 2; ++q) {
+                av[q] = sA[buf][kk + lr][wi * 32 + q * 16 + lc];
+                bv[q] = sB[buf][kk + lr][wj * 32 + q * 16 + lc];
             }
 #pragma unroll
-            for (int a = 0; a < 4; ++a)
+            for (int a = 0; a < 2; ++a)
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
+                for (int c = 0; c < 2; ++c)
                     acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[c], acc[a][c], 0, 0, 0);
         }
+        if (more) stash(buf ^ 1);
         __syncthreads();
+        buf ^= 1;
     }
     float* P = partial + (size_t)ks * N * N;
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int i = i0 + wi * 64 + a * 16 + 4 * lr + r;
-                const int j = j0 + wj * 64 + c * 16 + lc;
+                const int i = i0 + wi * 32 + a * 16 + 4 * lr + r;
+                const int j = j0 + wj * 32 + c * 16 + lc;
                 if (i < N && j < N) P[(size_t)i * N + j] = acc[a][c][r];
             }
 }

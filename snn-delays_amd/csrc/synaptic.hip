@@ -29,16 +29,6 @@ __device__ __forceinline__ float syn_delay(const SynBwd& p, int i, int j) {
     return p.base[j] + 0.0f + 1.0f * (float)p.off[(size_t)i * p.N + j];
 }
 
-// closed support |l - c| <= s, as integer lags within [1, L-1]
-__device__ __forceinline__ void closed_taps(float c, float s, int L, int& lo, int& hi) {
-    lo = (int)ceilf(c - s);
-    if (fabsf((float)(lo - 1) - c) <= s) lo -= 1;
-    hi = (int)floorf(c + s);
-    if (fabsf((float)(hi + 1) - c) <= s) hi += 1;
-    if (lo < 1) lo = 1;
-    if (hi > L - 1) hi = L - 1;
-}
-
 template <int NPT>
 __global__ void __launch_bounds__(1024) syn_fwd_kernel(SynFwd p) {
     extern __shared__ float smem[];
@@ -132,7 +122,7 @@ __global__ void __launch_bounds__(1024) syn_fwd_kernel(SynFwd p) {
                 const float w = load_w(p.Wt, p.w_bf16, (size_t)o * N + i);
                 const float c = 1.0f + syn_delay_t(p, o, i);
                 int lo, hi;
-                closed_taps(c, so, p.L, lo, hi);
+                tap_range(c, so, p.L, lo, hi);
                 for (int l = lo; l <= hi; ++l) {
                     const float h = tri_weight((float)l, c, so, s2);
                     if (h == 0.0f) continue;
@@ -189,7 +179,7 @@ __global__ void __launch_bounds__(1024) syn_bwd_kernel(SynBwd p) {
                 const float c = 1.0f + syn_delay(p, i, j);
                 const float sv = s[q], s2 = sv * sv;
                 int lo, hi;
-                closed_taps(c, sv, p.L, lo, hi);
+                tap_range(c, sv, p.L, lo, hi);
                 float acc = 0.0f;
                 for (int l = lo; l <= hi && t + l < T; ++l) {
                     int slot = tmod + l;

@@ -147,7 +147,35 @@ def workspace(kind, T, B, N, L, flags, device):
     return torch.empty(max(int(size.value), 1), dtype=torch.uint8, device=device)
 
 
+class _Timing:
+    """Optional HIP-event brackets around every library call (used by the benchmark):
+    events are recorded on the same stream the kernels are launched on."""
+
+    active = None   # list of (entry point, start event, end event) while timing
+
+    def __enter__(self):
+        _Timing.active = []
+        return _Timing.active
+
+    def __exit__(self, *exc):
+        _Timing.active = None
+        return False
+
+
+def timing():
+    return _Timing()
+
+
 def call(name, args, stream):
+    rec = _Timing.active
+    if rec is not None:
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        _check(name, getattr(load(), name)(ctypes.byref(args), stream))
+        e.record()
+        rec.append((name, s, e))
+        return
     _check(name, getattr(load(), name)(ctypes.byref(args), stream))
 
 

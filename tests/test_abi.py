@@ -1,0 +1,83 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol, and its
+argument structs have the same layout in C (as the compiler lays out include/delrec.h) and
+in the ctypes binding. No kernel is launched."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, 'include', 'delrec.h')
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r'^\s*(?:int|const char\*)\s+(delrec_\w+)\s*\(', text, re.M)))
+
+
+def test_header_declares_the_binding_exports():
+    from delrec import _lib
+    assert _declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_loads_and_exports_every_symbol():
+    from delrec import _lib
+    lib = _lib.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert _lib.version().startswith('delrec-mi355x')
+    assert lib.delrec_strerror(0) == b'ok'
+    assert b'workspace' in lib.delrec_strerror(3)
+
+
+def test_query_workspace_and_argument_errors_without_gpu():
+    from delrec import _lib
+    lib = _lib.load()
+    size = ctypes.c_size_t(0)
+    assert lib.delrec_query_workspace(_lib.WS_AXONAL_BWD, 128, 128, 256, 36, 0, ctypes.byref(size)) == 0
+    assert size.value >= 128 * 128 * 256 * 4
+    assert lib.delrec_query_workspace(99, 1, 1, 1, 2, 0, ctypes.byref(size)) == 1       # bad kind
+    assert lib.delrec_query_workspace(_lib.WS_SYN_FWD, 0, 1, 1, 2, 0, ctypes.byref(size)) == 1
+    # null / inconsistent arguments are rejected before anything touches the device
+    assert lib.delrec_axonal_fwd(None, None) == 1
+    args = _lib.AxonalFwdArgs(T=4, B=1, N=8, L=3)
+    assert lib.delrec_axonal_fwd(ctypes.byref(args), None) == 1          # null tensors
+    assert lib.delrec_syn_bwd(None, None) == 1
+    assert lib.delrec_delay_grad(None, None, None, 0.0, 4, 3, None, None) == 1
+
+
+_STRUCTS = ['delrec_lif', 'delrec_axonal_fwd_args', 'delrec_axonal_bwd_args', 'delrec_syn_fwd_args',
+            'delrec_syn_bwd_args', 'delrec_lif_fwd_args', 'delrec_lif_bwd_args']
+
+
+def _c_layout():
+    """sizeof / offsetof of every field, as gcc lays out the header."""
+    from delrec import _lib
+    classes = {'delrec_lif': _lib.Lif, 'delrec_axonal_fwd_args': _lib.AxonalFwdArgs,
+               'delrec_axonal_bwd_args': _lib.AxonalBwdArgs, 'delrec_syn_fwd_args': _lib.SynFwdArgs,
+               'delrec_syn_bwd_args': _lib.SynBwdArgs, 'delrec_lif_fwd_args': _lib.LifFwdArgs,
+               'delrec_lif_bwd_args': _lib.LifBwdArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
+    for st in _STRUCTS:
+        lines.append(f'  printf("{st} size %zu\\n", sizeof({st}));')
+        for fname, _ in classes[st]._fields_:
+            lines.append(f'  printf("{st} {fname} %zu\\n", offsetof({st}, {fname}));')
+    lines += ['  return 0;', '}']
+    with tempfile.TemporaryDirectory() as tmp:
+        src, exe = os.path.join(tmp, 'probe.c'), os.path.join(tmp, 'probe')
+        open(src, 'w').write('\n'.join(lines))
+        subprocess.run(['gcc', '-std=c11', src, '-o', exe], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout
+    return classes, dict((' '.join(l.split()[:2]), int(l.split()[2])) for l in out.splitlines())
+
+
+def test_struct_layout_matches_ctypes():
+    classes, c = _c_layout()
+    for st, cls in classes.items():
+        assert c[f'{st} size'] == ctypes.sizeof(cls), st
+        for fname, _ in cls._fields_:
+            assert c[f'{st} {fname}'] == getattr(cls, fname).offset, f'{st}.{fname}'

@@ -1,0 +1,208 @@
+"""CPU tests of the module / model API (no kernel launch).
+
+Mirrors the CPU part of the reference's tests/test_hybrid_delay_invariance.py for the
+recurrent classes (its feedforward half needs DCLS and is out of scope): state_dict and
+initial values of the hybrid at ``hybrid_offset_scale == 0`` equal the axonal model's,
+offsets are frozen integer buffers, invalid knobs raise; the forward comparisons run
+through the oracle. Also the dispatch and error conventions of this build.
+"""
+
+import pytest
+import torch
+
+from oracle.model import reference_forward
+
+T, B = 10, 4
+
+
+def base_config(maximum):
+    from configs.perf_MEM import Config
+    cfg = Config()
+    cfg.input_size = 8
+    cfg.output_size = 3
+    cfg.hidden_layers = [16]
+    cfg.time_window = T
+    cfg.batch_size = B
+    cfg.use_batch_norm = False
+    cfg.feedforward_dropout_rate = 0.0
+    cfg.recurrent_dropout_rate = 0.0
+    cfg.no_recurrence_in_last_layer = False
+    cfg.kernel_count = 1
+    cfg.hybrid_offset_scale = maximum
+    cfg.hybrid_delay_seed = 123
+    return cfg
+
+
+def _probe(cfg):
+    return torch.randn(cfg.time_window, B, cfg.input_size, generator=torch.Generator().manual_seed(7))
+
+
+def test_maximum_zero_is_the_axonal_model():
+    from delrec import networks
+    cfg = base_config(0)
+    torch.manual_seed(0)
+    hybrid = networks.SNN_recurrent_hybrid_delays(cfg)
+    torch.manual_seed(0)
+    axonal = networks.SNN_axonal_recurrent_delays(cfg)
+    hs, as_ = hybrid.state_dict(), axonal.state_dict()
+    assert set(hs) == set(as_)
+    for key in as_:
+        assert torch.equal(hs[key], as_[key]), key
+    x = _probe(cfg)
+    hybrid.eval()
+    axonal.eval()
+    torch.testing.assert_close(reference_forward(hybrid, x), reference_forward(axonal, x), atol=1e-6, rtol=0)
+
+
+def test_maximum_positive_keeps_axonal_delay_budget():
+    from delrec import networks
+    from delrec.delay_layers import axonal_recdel
+    from delrec.networks import learned_delay_parameter
+    cfg = base_config(4)
+    torch.manual_seed(0)
+    hybrid = networks.SNN_recurrent_hybrid_delays(cfg)
+    torch.manual_seed(0)
+    axonal = networks.SNN_axonal_recurrent_delays(base_config(0))
+    h = [learned_delay_parameter(m, 'recurrent_delays') for m in hybrid.layers if isinstance(m, axonal_recdel)]
+    a = [learned_delay_parameter(m, 'recurrent_delays') for m in axonal.layers if isinstance(m, axonal_recdel)]
+    assert len(h) == len(a) == 1
+    assert h[0].requires_grad and h[0].numel() == a[0].numel()
+    offsets = [b for n, b in hybrid.named_buffers() if n.endswith('.offsets')]
+    assert offsets and all(not b.requires_grad for b in offsets)
+    assert all(int(b.max()) <= 4 and int(b.min()) >= 0 for b in offsets)
+    hybrid.eval()
+    out = reference_forward(hybrid, _probe(cfg))
+    assert out.shape == (T, B, cfg.output_size) and torch.isfinite(out).all()
+
+
+def test_hybrid_base_is_row_zero_of_the_initial_delays_centred():
+    from delrec import networks
+    cfg = base_config(4)
+    cfg.hybrid_base_centering = 'centered'
+    torch.manual_seed(0)
+    syn = networks.SNN_synaptic_recurrent_delays(cfg)
+    torch.manual_seed(0)
+    hyb = networks.SNN_recurrent_hybrid_delays(cfg)
+    d0 = syn.layers[2].recurrent_delays[0].detach()
+    base = hyb.layers[2].parametrizations.recurrent_delays.original.detach()
+    torch.testing.assert_close(base, d0 - 2.0)
+    d = hyb.layers[2].recurrent_delays
+    off = hyb.layers[2].parametrizations.recurrent_delays[0].offsets
+    assert torch.equal(d, base[None, :] + off)
+
+
+@pytest.mark.parametrize('bad', [-1, 1.5])
+def test_maximum_must_be_nonnegative_integer(bad):
+    from delrec import networks
+    with pytest.raises(ValueError):
+        networks.SNN_recurrent_hybrid_delays(base_config(bad))
+
+
+def test_kernel_count_must_be_one():
+    from delrec import networks
+    cfg = base_config(4)
+    cfg.kernel_count = 2
+    with pytest.raises(ValueError):
+        networks.SNN_recurrent_hybrid_delays(cfg)
+
+
+def test_offset_distributions():
+    from delrec.networks import _draw_offsets
+    g = torch.Generator().manual_seed(0)
+    for dist, sig in (('uniform', None), ('gaussian', 2.0), ('triangular', None)):
+        o = _draw_offsets((50, 50), 6, g, dist, sig)
+        assert o.min() >= 0 and o.max() <= 6 and torch.equal(o, o.round())
+    with pytest.raises(ValueError):
+        _draw_offsets((2, 2), 3, g, 'cauchy')
+
+
+def test_forward_dispatch_and_errors():
+    from delrec.delay_layers import axonal_recdel, synaptic_recdel
+    cfg = base_config(0)
+    ax = axonal_recdel(cfg, 8)
+    x = torch.zeros(4, 2, 8)
+    with pytest.raises(RuntimeError, match='GPU'):
+        ax(x)                                      # CPU input: no fallback, a loud error
+    ax.forward_version = 'v2'
+    with pytest.raises(NotImplementedError):
+        ax(x)
+    ax.forward_version = 'eventdriven'
+    with pytest.raises(ValueError):
+        ax(x)
+    syn = synaptic_recdel(cfg, 8)
+    syn.forward_version = 'eventdriven_torch'
+    with pytest.raises(ValueError):
+        syn(x)
+    syn.forward_version = 'nonsense'
+    with pytest.raises(ValueError):
+        syn(x)
+
+
+def test_surrogate_ids():
+    from delrec.kernels.surrogate import surrogate_id
+    from delrec.neuron import ATan
+    from delrec.utils import Triangle
+    assert surrogate_id(ATan(3.0)) == (1, 1.0, 3.0)
+    assert surrogate_id(Triangle.apply, 0.7) == (0, 0.7, 2.0)
+    with pytest.raises(ValueError):
+        surrogate_id(torch.sigmoid)
+
+
+def test_drop_mask_normalisation():
+    from delrec.kernels._common import drop_bn
+    m = torch.rand(3, 5)
+    assert torch.equal(drop_bn(m, 4, 3, 5), m)
+    assert torch.equal(drop_bn(m.unsqueeze(0).expand(4, 3, 5), 4, 3, 5), m)
+    assert drop_bn(None, 4, 3, 5) is None
+    varying = torch.rand(4, 3, 5)
+    with pytest.raises(ValueError):
+        drop_bn(varying, 4, 3, 5)
+
+
+def test_hard_lag_builders():
+    from delrec.kernels.delays import build_lag, build_lag_interp
+    d = torch.tensor([0.0, 0.4, 0.6, 2.5, 9.7])
+    assert build_lag(d, 6).tolist() == [1, 1, 2, 3, 5]          # round half to even, clamp to L-1
+    lag, frac = build_lag_interp(d, 12)
+    assert lag.tolist() == [1, 1, 1, 3, 10]
+    torch.testing.assert_close(frac, torch.tensor([0.0, 0.4, 0.6, 0.5, 0.7]))
+
+
+def test_sigma_schedule_clamp_and_round():
+    from delrec import networks
+    from delrec.delay_layers import axonal_recdel
+    cfg = base_config(0)
+    cfg.sigma_init, cfg.sigma_decay, cfg.epochs = 2.0, 0.95, 50
+    torch.manual_seed(0)
+    model = networks.SNN_axonal_recurrent_delays(cfg)
+    layer = [m for m in model.layers if isinstance(m, axonal_recdel)][0]
+    layer.update_sigma(10)
+    assert layer.sigma == pytest.approx(2.0 * (0.95 ** (100 / 50)) ** 10)
+    assert 'sigma' not in ''.join(model.state_dict())
+    with torch.no_grad():
+        layer.recurrent_delays[:3] = torch.tensor([-1.0, 2.4, 2.6])
+    model.round_pos()
+    assert layer.recurrent_delays[:3].tolist() == [0.0, 2.0, 3.0]
+
+
+def test_common_recdel_has_one_shared_delay():
+    from delrec import networks
+    cfg = base_config(0)
+    torch.manual_seed(0)
+    model = networks.SNN_common_recurrent_delays(cfg)
+    layer = model.layers[2]
+    assert layer.recurrent_delays.shape == (1,) and layer.forward_version is None
+
+
+def test_fixed_models_freeze_delays():
+    from delrec import networks
+    cfg = base_config(4)
+    torch.manual_seed(0)
+    for cls in (networks.SNN_fixed_recurrent_delays, networks.SNN_fixed_synaptic_recurrent_delays,
+                networks.SNN_fixed_hybrid_recurrent_delays, networks.SNN_vanilla_recurrent):
+        model = cls(base_config(4))
+        layer = model.layers[2]
+        from delrec.networks import learned_delay_parameter
+        leaf = learned_delay_parameter(layer, 'recurrent_delays')
+        assert not leaf.requires_grad and layer.sigma == 0.0
+        assert torch.equal(leaf, leaf.round())
