@@ -79,6 +79,7 @@ bool lif_ok(const delrec_lif& l) {
 struct AxLayout {
     bool res;       // N <= 256: tiled kernels with W resident in VGPRs
     int G, CH, CHS, NZ, block, hw, ri;
+    int np;         // padded neuron count of the tiled kernels' per-neuron LDS rows
 };
 
 bool axonal_layout(int N, int L, AxLayout& o) {
@@ -112,6 +113,7 @@ bool axonal_layout(int N, int L, AxLayout& o) {
         o.CHS = kCJ;
         o.NZ = nj * kCJP;
         o.block = std::max((N + 63) / 64 * 64, (lanes + 63) / 64 * 64);
+        o.np = std::max(N, (o.block / nj) * ri);   // every lane group's RI rows are in bounds
     } else {
         o.res = false;
         o.ri = 0;
@@ -130,6 +132,7 @@ bool axonal_layout(int N, int L, AxLayout& o) {
         o.CHS = (N + G - 1) / G;
         o.NZ = (G * o.CHS + 3) / 4 * 4;
         o.block = npad * G;
+        o.np = N;
     }
     return true;
 }
@@ -269,7 +272,7 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
     if (a->taps == DELREC_TAPS_INTERP && !a->frac) return DELREC_ERR_ARG;
     AxLayout lay;
     if (!axonal_layout(a->N, a->L, lay)) return DELREC_ERR_WINDOW;
-    const size_t lds = ((size_t)2 * lay.NZ + (lay.res ? (size_t)a->N : 0)) * sizeof(float);
+    const size_t lds = ((size_t)2 * lay.NZ + (lay.res ? (size_t)lay.np : 0)) * sizeof(float);
     if (lds > (size_t)max_lds_bytes()) return DELREC_ERR_WINDOW;
     hipStream_t s = static_cast<hipStream_t>(stream);
     AxFwd p{};
@@ -301,8 +304,10 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     if (a->dW && !a->z) return DELREC_ERR_ARG;
     AxLayout lay;
     if (!axonal_layout(a->N, a->L, lay)) return DELREC_ERR_WINDOW;
-    const int R = std::max(a->L, 2);
-    const size_t lds = ((size_t)2 * lay.NZ + (size_t)(R + kMaxTaps) * a->N) * sizeof(float);
+    // the tiled backward reads kMaxTaps consecutive ring slots from the first tap lag on
+    const int R = std::max(a->L, 2) + (lay.res ? kMaxTaps : 0);
+    const int NP = lay.res ? lay.np : a->N;
+    const size_t lds = ((size_t)2 * lay.NZ + (size_t)(R + kMaxTaps) * NP) * sizeof(float);
     if (lds > (size_t)max_lds_bytes()) return DELREC_ERR_WINDOW;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int T = a->T, B = a->B, N = a->N;
@@ -316,7 +321,7 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
 
     AxBwd p{};
     p.T = T; p.B = B; p.N = N; p.L = a->L;
-    p.G = lay.G; p.NZ = lay.NZ; p.CHS = lay.CHS; p.R = R; p.NP = N;
+    p.G = lay.G; p.NZ = lay.NZ; p.CHS = lay.CHS; p.R = R; p.NP = NP;
     p.gy = a->gy; p.u = a->u; p.bits = a->bits; p.W = a->W; p.w_bf16 = a->w_bf16;
     p.d = a->d; p.s = a->s; p.s_uniform = a->s_uniform; p.drop = a->drop;
     p.mode = a->mode; p.lag = a->lag; p.lif = make_lif(a->lif);

@@ -342,11 +342,11 @@ __global__ void __launch_bounds__(1024) axonal_bwd_kernel(AxBwd p) {
 
         // delay / half-width gradients: dL/dh[j,l] = gz_t * y[t-l]
         if (fast && !need_ds) {
-            const uint64_t ps = past.w[0] >> (lo - 1);
+            const uint32_t ps = (uint32_t)(past.w[0] >> (lo - 1));
             float sd = 0.0f;
 #pragma unroll
             for (int q = 0; q < kMaxTaps; ++q)
-                if (q < nt && ((ps >> q) & 1ull)) sd += tri_dsign((float)(lo + q), c, s);
+                sd += (q < nt && ((ps >> q) & 1u)) ? tri_dsign((float)(lo + q), c, s) : 0.0f;
             dd_acc += gz * sd;
         } else if (soft) {
             float sd = 0.0f, sds = 0.0f;
@@ -460,8 +460,7 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_fwd_tiled(AxFw
         for (int a = 0; a < RI; ++a) acc[a] = group_sum_t<NJ>(acc[a]);
         if (jcg == 0) {
 #pragma unroll
-            for (int a = 0; a < RI; ++a)
-                if (grp * RI + a < N) rbuf[grp * RI + a] = acc[a];
+            for (int a = 0; a < RI; ++a) rbuf[grp * RI + a] = acc[a];   // rbuf padded to the lane groups
         }
         barrier_lds();
 
@@ -487,10 +486,10 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_fwd_tiled(AxFw
             if (t + 1 < T) {
                 float zn;
                 if (fast) {
-                    const uint64_t hs = hist.w[0] >> (lo - 1);
+                    const uint32_t hs = (uint32_t)(hist.w[0] >> (lo - 1));
                     zn = 0.0f;
 #pragma unroll
-                    for (int q = 0; q < kMaxTaps; ++q) zn += wq[q] * (float)((hs >> q) & 1ull);
+                    for (int q = 0; q < kMaxTaps; ++q) zn += ((hs >> q) & 1u) ? wq[q] : 0.0f;
                 } else {
                     zn = axonal_trace<HW>(hist, p.taps, c, s, s2, lo, hi, lag, frac);
                 }
@@ -513,7 +512,7 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
     extern __shared__ float smem[];
     const int N = p.N, T = p.T, B = p.B, NZ = p.NZ, R = p.R, NP = p.NP;
     float* grbuf = smem;                 // [2][NZ]
-    float* ring = smem + 2 * NZ;         // [R][NP] gz of the future steps
+    float* ring = smem + 2 * NZ;         // [R][NP] gz of the future steps (R >= L + kMaxTaps)
     float* htab = ring + R * NP;         // [kMaxTaps][NP] tap weights of each source
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
@@ -531,8 +530,12 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
             w[a][cc] = (i < N && j < N) ? load_w(p.W, p.w_bf16, (size_t)i * N + j) : 0.0f;
         }
 
-    const bool nl = tid < N;
-    const int j = nl ? tid : 0;
+    // Lanes [0, N) run the LIF chain of source j = tid; lanes [N, 2N) (when the block has
+    // them) accumulate the delay / half-width gradient of source j = tid - N concurrently.
+    const bool split = (int)blockDim.x >= 2 * N;
+    const bool nl = tid < N;                                  // LIF lanes
+    const bool dl = split ? (tid >= N && tid < 2 * N) : nl;   // delay-gradient lanes
+    const int j = nl ? tid : (dl ? tid - N : 0);
     const float c = 1.0f + p.d[j];
     const float s = p.s ? p.s[j] : p.s_uniform;
     const float s2 = s * s;
@@ -542,6 +545,9 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
     const bool soft = p.mode == DELREC_BWD_SOFT;
     const bool fast = soft && nt <= kMaxTaps && HW == 1;
     const bool need_ds = p.s != nullptr;
+    float dsg[kMaxTaps];
+#pragma unroll
+    for (int q = 0; q < kMaxTaps; ++q) dsg[q] = (q < nt) ? tri_dsign((float)(lo + q), c, s) : 0.0f;
     const int lag = p.lag ? p.lag[j] : 1;
     const float m = p.drop ? p.drop[(size_t)b * N + j] : 1.0f;
 
@@ -553,12 +559,13 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
     }
     __syncthreads();
 
-    History<HW> past;   // bit(l) = y[tw - l] for the window time tw
+    History<HW> past;   // delay lanes: bit(l) = y[tw - l] for the window time tw
     past.clear();
-    if (nl)
+    SpikeStream oldest; // the bit that enters the window at lag 64*HW
+    if (dl) {
         for (int l = 64 * HW; l >= 1; --l) past.push(spike_bit(p.bits, TW, N, b, T - 1 - l, j));
-    SpikeStream oldest;  // the bit that enters the window at lag 64*HW
-    oldest.init(p.bits, TW, N, b, j, T - 2 - 64 * HW);
+        oldest.init(p.bits, TW, N, b, j, T - 2 - 64 * HW);
+    }
 
     const size_t BN = (size_t)B * N;
     const size_t rowj = (size_t)b * N + j;
@@ -574,11 +581,10 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
     // dd / ds contribution of gz at the window time: dL/dh[j,l] = gz * y[tw-l]
     auto delay_grad = [&](float gz) {
         if (fast && !need_ds) {
-            const uint64_t ps = past.w[0] >> (lo - 1);
+            const uint32_t ps = (uint32_t)(past.w[0] >> (lo - 1));
             float sd = 0.0f;
 #pragma unroll
-            for (int q = 0; q < kMaxTaps; ++q)
-                if (q < nt && ((ps >> q) & 1ull)) sd += tri_dsign((float)(lo + q), c, s);
+            for (int q = 0; q < kMaxTaps; ++q) sd += ((ps >> q) & 1u) ? dsg[q] : 0.0f;
             dd_acc += gz * sd;
         } else if (soft) {
             float sd = 0.0f, sds = 0.0f;
@@ -597,23 +603,23 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
     int tmod = (T - 1) % R;
     // one reverse step; `gs`, `us` are this step's prefetch slots, refilled with step t - P
     auto step = [&](const int t, float& gs, float& us) {
+        if (dl && t < T - 1) {
+            int s1 = tmod + 1;
+            if (s1 >= R) s1 -= R;
+            delay_grad(ring[s1 * NP + j]);                     // gz_{t+1} with the window of t+1
+            past.pull(oldest.bit(t - 64 * HW));
+        }
         if (nl) {
-            if (t < T - 1) {
-                int s1 = tmod + 1;
-                if (s1 >= R) s1 -= R;
-                delay_grad(ring[s1 * NP + j]);                 // gz_{t+1} with the window of t+1
-                past.pull(oldest.bit(t - 64 * HW));
-            }
             float gfut = 0.0f;
             if (fast) {
+                // taps past the support weigh 0 and ring slots of times >= T still hold 0
+                int sb = tmod + lo;
+                if (sb >= R) sb -= R;
 #pragma unroll
                 for (int q = 0; q < kMaxTaps; ++q) {
-                    const int l = lo + q;
-                    if (q < nt && t + l < T) {
-                        int slot = tmod + l;
-                        if (slot >= R) slot -= R;
-                        gfut += htab[q * NP + j] * ring[slot * NP + j];
-                    }
+                    int slot = sb + q;
+                    if (slot >= R) slot -= R;
+                    gfut += htab[q * NP + j] * ring[slot * NP + j];
                 }
             } else if (soft) {
                 for (int l = lo; l <= hi && t + l < T; ++l) {
@@ -664,8 +670,7 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
         for (int a = 0; a < RI; ++a) acc[a] = group_sum_t<NJ>(acc[a]);
         if (jcg == 0) {
 #pragma unroll
-            for (int a = 0; a < RI; ++a)
-                if (grp * RI + a < N) ring[tmod * NP + grp * RI + a] = acc[a];
+            for (int a = 0; a < RI; ++a) ring[tmod * NP + grp * RI + a] = acc[a];   // NP >= groups * RI
         }
         barrier_lds();
         tmod = tmod == 0 ? R - 1 : tmod - 1;
@@ -677,14 +682,14 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
         for (int q = 0; q < kPrefetchBwd; ++q)
             if (t0 - q >= 0) step(t0 - q, gq[q], uq[q]);
     }
-    if (nl) {
+    if (dl) {
         int s0 = tmod + 1;
         if (s0 >= R) s0 -= R;
         delay_grad(ring[s0 * NP + j]);                          // gz_0 with the window of 0
-        p.part[(size_t)0 * B * N + rowj] = db_acc;
         p.part[(size_t)1 * B * N + rowj] = soft ? dd_acc / s2 : dd_acc;
         p.part[(size_t)2 * B * N + rowj] = ds_acc;
     }
+    if (nl) p.part[(size_t)0 * B * N + rowj] = db_acc;
 }
 
 // Sum the per-row partials over the batch: out_k[j] = sum_b part[k][b][j]. Block (64, 16):
