@@ -107,55 +107,65 @@ def upstream_gradient(layer, readout, x, labels):
 
 
 def algorithmic_work(w):
-    """Algorithmic bytes and flops per neuron-timestep of the whole fwd+BPTT and per kernel.
+    """Algorithmic bytes and flops per neuron-timestep, for the whole fwd+BPTT and for each
+    time-scan kernel.
 
-    Bytes: x read, y write, gy read, dx write in fp32 (16 B). Flops (useful MACs x2, no
-    sparsity credit; k = non-zero triangle taps = 2(1 + sigma)): axonal / hybrid
-    6N + 6k, synaptic 8kN. Forward scan kernel: the contraction and taps, 2N + 2k
-    (axonal; 2kN synaptic).
+    Bytes: x read, y write, gy read, dx write in fp32 (16 B). Flops are useful MACs x 2
+    with no sparsity credit; k = non-zero triangle taps = 2(1 + sigma). Axonal and hybrid
+    (the hybrid's integer offsets only shift which step of z_j a connection reads):
+    6N + 6k in total = forward scan 2N + 2k (contraction W z, taps of z) + backward scan
+    2N + 4k (W^T gr, taps of the future gradient, delay-gradient taps) + dW GEMM 2N.
+    Synaptic: 8kN in total = forward scan 2kN + backward scan 2kN + lag GEMM 4kN.
     """
     N, sigma = w['N'], w['sigma']
     k = 2.0 * (1.0 + sigma)
     if w['kind'] == 'synaptic':
-        return {'bytes': 16.0, 'flops': 8.0 * k * N, 'fwd_flops': 2.0 * k * N, 'fwd_bytes': 8.0}
-    return {'bytes': 16.0, 'flops': 6.0 * N + 6.0 * k, 'fwd_flops': 2.0 * N + 2.0 * k, 'fwd_bytes': 8.0}
+        return {'bytes': 16.0, 'flops': 8.0 * k * N,
+                'scan_flops': {'syn_fwd_scan': 2.0 * k * N, 'syn_bwd_scan': 2.0 * k * N}}
+    return {'bytes': 16.0, 'flops': 6.0 * N + 6.0 * k,
+            'scan_flops': {'axonal_fwd_scan': 2.0 * N + 2.0 * k, 'axonal_bwd_scan': 2.0 * N + 4.0 * k,
+                           'syn_fwd_scan': 2.0 * N + 2.0 * k, 'syn_bwd_scan': 2.0 * N + 4.0 * k}}
 
 
-def cpu_baseline(w, budget_s=25.0):
+# kernel symbol of each time-scan kind at the benchmark shapes (for the rocprof summaries)
+SCAN_SYMBOL = {'axonal_fwd_scan': 'axonal_fwd_tiled', 'axonal_bwd_scan': 'axonal_bwd_tiled',
+               'syn_fwd_scan': 'syn_fwd_kernel', 'syn_bwd_scan': 'syn_bwd_kernel'}
+
+
+def cpu_baseline(layer, x, w, budget_s=25.0):
     """The oracle (pure-PyTorch v2 scan, autograd BPTT, fp32) on the host cores, on a
-    bounded sample: full B and N, the first T' steps, scaled to neuron-timesteps/s."""
+    bounded sample of the same workload: the layer's own weights and delays and the first
+    T' steps of the same input at full B and N, scaled to neuron-timesteps/s."""
     from oracle import neuron as oneuron, scans
+    from oracle.delays import hybrid_delays
     cores = max(1, min(16, len(os.sched_getaffinity(0))))
     torch.set_num_threads(cores)
-    torch.manual_seed(0)
     T, B, N = w['T'], w['B'], w['N']
     lif = oneuron.LIFParams(tau=w['tau'])
-    g = torch.Generator().manual_seed(7)
-    W = (torch.rand(N, N, generator=g) * 2 - 1) / N ** 0.5
-    if w['w_bf16']:
-        W = W.bfloat16().float()
+    W = layer.recurrent_weights.detach().float().cpu()
     if w['kind'] == 'axonal':
-        d = torch.rand(N, generator=g) * w['dmax']
+        d = layer.recurrent_delays.detach().cpu()
         fn = scans.axonal_v2
     elif w['kind'] == 'hybrid':
-        d = (torch.rand(N, generator=g) * w['dmax'])[None, :] + torch.randint(
-            w['offset_max'] + 1, (N, N), generator=g).float()
+        par = layer.parametrizations.recurrent_delays
+        d = hybrid_delays(par.original.detach().cpu(), par[0].offsets.detach().float().cpu())
         fn = scans.synaptic_v2
     else:
-        d = torch.rand(N, N, generator=g) * w['dmax']
+        d = layer.recurrent_delays.detach().cpu()
         fn = scans.synaptic_v2
+    xc = x.detach().cpu()
 
     def one(Tp):
-        x = (torch.randn(Tp, B, N, generator=g) * 0.8).requires_grad_(True)
+        xs = xc[:Tp].clone().requires_grad_(True)
         Wl, dl = W.clone().requires_grad_(True), d.clone().requires_grad_(True)
         t0 = time.perf_counter()
-        y, _ = fn(x, Wl, dl, lif, sigma=w['sigma'])
+        y, _ = fn(xs, Wl, dl, lif, sigma=w['sigma'])
         y.sum().backward()
         return time.perf_counter() - t0
 
     Tp = min(T, 16)
     t_probe = one(Tp)
-    # grow the sample while it fits the budget (1 warmup already done + 3 timed runs)
+    # grow the sample while 3 timed runs stay within the budget (the probe is the warmup)
     while Tp < T and t_probe * 2 * 3 < budget_s:
         Tp = min(T, Tp * 2)
         t_probe = one(Tp)
@@ -163,9 +173,22 @@ def cpu_baseline(w, budget_s=25.0):
     t_med = times[1]
     nts = Tp * B * N / t_med
     return {'value': nts, 'unit': 'neuron-timesteps/s', 'cores': cores, 'kind': 'port',
-            'sample': f'oracle v2 scan + autograd BPTT, fp32, full B={B} N={N}, first {Tp} of '
-                      f'T={T} steps, median of 3 (after 1 warmup), scaled per neuron-timestep',
+            'sample': f'oracle v2 scan + autograd BPTT, fp32, same weights/delays/input, full B={B} '
+                      f'N={N}, first {Tp} of T={T} steps, median of 3 (after a warmup), scaled per '
+                      f'neuron-timestep',
             'seconds_per_sample': t_med}
+
+
+def calibrate_copy(mib):
+    """A plain device copy of `mib` MiB, five times: the known-size kernel whose FETCH_SIZE /
+    WRITE_SIZE readings scale the counters of the scan kernels to bytes."""
+    n = mib * (1 << 20) // 4
+    src = torch.rand(n, device='cuda:0')
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({'copy_bytes_read': n * 4, 'copy_bytes_written': n * 4, 'launches': 5}), flush=True)
 
 
 def load_traffic(kernel, config):
@@ -183,12 +206,17 @@ def main():
     ap.add_argument('--warmup', type=int, default=3)
     ap.add_argument('--config', default='C2', choices=sorted(WORKLOADS))
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
+    ap.add_argument('--calibrate-copy', type=int, metavar='MIB', default=0,
+                    help='only run a plain device copy of MIB MiB (counter calibration)')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU; --gpus {args.gpus} is not supported by this build '
               f'(the layer shards over batch rows with one dW/dd all-reduce per step, not run here)',
               file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
     w = WORKLOADS[args.config]
     dev = torch.device('cuda:0')
     from delrec import _lib
@@ -208,35 +236,33 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    with _lib.timing() as rec:
+    with _lib.timing() as rec, _lib.scan_timing(2 * args.steps + 8) as scans_t:
         t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / args.steps
-    per_entry = {}
+    per_entry, per_scan = {}, {}
     for name, s, e in rec:
         per_entry.setdefault(name, []).append(s.elapsed_time(e))
+    for kind, dt in scans_t.launches:
+        per_scan.setdefault(kind, []).append(dt)
     avg = {k: sum(v) / len(v) for k, v in per_entry.items()}
+    scan_avg = {k: sum(v) / len(v) for k, v in per_scan.items()}
     nt = T * B * N
     value = nt / (ms * 1e-3)
     work = algorithmic_work(w)
     peak_c = PEAK_BF16 if (w['w_bf16'] and w['kind'] != 'synaptic') else PEAK_FP32
     t_bound = max(work['bytes'] * nt / PEAK_HBM, work['flops'] * nt / peak_c)
 
-    fwd_entry = 'delrec_axonal_fwd' if w['kind'] == 'axonal' else 'delrec_syn_fwd'
-    bwd_entry = 'delrec_axonal_bwd' if w['kind'] == 'axonal' else 'delrec_syn_bwd'
-    dom = max(avg, key=avg.get) if avg else fwd_entry
-    kernel = {'delrec_axonal_fwd': 'axonal_fwd_kernel', 'delrec_axonal_bwd': 'axonal_bwd(+dW gemm)',
-              'delrec_syn_fwd': 'syn_fwd_kernel', 'delrec_syn_bwd': 'syn_bwd(+lag gemm)'}.get(dom, dom)
-    if dom == fwd_entry:
-        flops = work['fwd_flops'] * nt
-    else:
-        flops = (work['flops'] - work['fwd_flops']) * nt
-    dur = avg.get(dom, ms) * 1e-3
+    # the dominant kernel: the time-scan kernel with the longest average launch
+    dom = max(scan_avg, key=scan_avg.get)
+    dur = scan_avg[dom] * 1e-3
+    flops = work['scan_flops'][dom] * nt
     achieved = flops / dur
-    traffic = load_traffic(kernel.split('(')[0], args.config)
+    kernel = SCAN_SYMBOL[dom]
+    traffic = load_traffic(kernel, args.config)
     line = {
         'metric': 'neuron-timesteps/sec fwd+BPTT per recurrent layer',
         'value': value,
@@ -252,16 +278,17 @@ def main():
         'data': 'synthetic (seeded inputs of the stated shape, random-init weights)',
         'config': {'workload': f"{args.config}: {w['label']}", 'T': T, 'B': B, 'N': N,
                    'delay_kind': w['kind'], 'sigma': w['sigma'], 'firing_rate': firing},
-        'roofline': {'bound': 'mfma', 'achieved': achieved / 1e12, 'peak': PEAK_FP32 / 1e12
-                     if peak_c == PEAK_FP32 else peak_c / 1e12, 'unit': 'TFLOP/s',
-                     'frac': achieved / peak_c, 'traffic': traffic, 'kernel': kernel,
-                     'avg_launch_ms': avg.get(dom)},
+        'roofline': {'bound': 'mfma', 'achieved': achieved / 1e12, 'peak': PEAK_FP32 / 1e12,
+                     'unit': 'TFLOP/s', 'frac': achieved / PEAK_FP32, 'traffic': traffic,
+                     'kernel': kernel, 'avg_launch_ms': scan_avg[dom],
+                     'flops_per_launch': flops},
         'layer_roofline': {'t_bound_ms': t_bound * 1e3, 'frac': t_bound / (ms * 1e-3),
                            'bytes_per_nt': work['bytes'], 'flops_per_nt': work['flops']},
+        'scan_ms': scan_avg,
         'entry_ms': avg,
     }
     if not args.no_cpu:
-        line['cpu_baseline'] = cpu_baseline(w)
+        line['cpu_baseline'] = cpu_baseline(layer, x, w)
     print(json.dumps(line), flush=True)
 
 

@@ -201,6 +201,15 @@ int delrec_delay_grad(const float* C, const float* W, const float* d, float sigm
 int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_t L,
                            int32_t flags, size_t* bytes);
 
+/* Benchmark hook, with no counterpart in the reference (its profiler times whole layer
+ * calls): delrec_scan_timing(n) with n > 0 brackets the time-scan kernel of the next n
+ * axonal / synaptic forward and backward calls with HIP events recorded on the caller's
+ * stream; n == 0 switches it off. delrec_scan_timing_read waits for those events and
+ * writes each launch's duration in ms and its DELREC_WS_* kind (at most `capacity`); it
+ * returns the number of launches recorded, or a negative status. Single-threaded use. */
+int delrec_scan_timing(int32_t capacity);
+int delrec_scan_timing_read(float* ms, int32_t* kinds, int32_t capacity);
+
 const char* delrec_strerror(int status);
 const char* delrec_version(void);
 

@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <vector>
 
 #include "kernels.h"
 
@@ -219,6 +220,33 @@ void transpose(const void* in, void* out, int n, hipStream_t s) {
                        static_cast<E*>(out), n);
 }
 
+// HIP-event brackets around the time-scan kernels (benchmark hook)
+struct ScanTiming {
+    std::vector<hipEvent_t> ev;    // two per launch
+    std::vector<int32_t> kind;
+    int used = 0;
+};
+ScanTiming g_scan;
+
+bool scan_begin(int kind, hipStream_t s) {
+    const int cap = (int)g_scan.kind.size();
+    if (g_scan.used >= cap) return false;
+    g_scan.kind[g_scan.used] = kind;
+    return hipEventRecord(g_scan.ev[2 * g_scan.used], s) == hipSuccess;
+}
+
+void scan_end(bool on, hipStream_t s) {
+    if (!on) return;
+    if (hipEventRecord(g_scan.ev[2 * g_scan.used + 1], s) == hipSuccess) ++g_scan.used;
+}
+
+void scan_release() {
+    for (hipEvent_t e : g_scan.ev) (void)hipEventDestroy(e);
+    g_scan.ev.clear();
+    g_scan.kind.clear();
+    g_scan.used = 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -290,8 +318,10 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
         if (a->w_bf16) transpose<uint16_t>(a->W, wt, a->N, s); else transpose<float>(a->W, wt, a->N, s);
         p.Wt = wt;
     }
+    const bool timed = scan_begin(DELREC_WS_AXONAL_FWD, s);
     const bool ok = lay.res ? launch_axonal_tiled(true, &p, nullptr, lay.ri, lay.G, lay.hw, a->B, lay.block, lds, s)
                             : launch_axonal(true, &p, nullptr, lay.CH, lay.res, lay.hw, a->B, lay.block, lds, s);
+    scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     return finish_launch();
 }
@@ -326,8 +356,10 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     p.d = a->d; p.s = a->s; p.s_uniform = a->s_uniform; p.drop = a->drop;
     p.mode = a->mode; p.lag = a->lag; p.lif = make_lif(a->lif);
     p.dx = a->dx; p.gr = need_gr ? grbuf : nullptr; p.part = part;
+    const bool timed = scan_begin(DELREC_WS_AXONAL_BWD, s);
     const bool ok = lay.res ? launch_axonal_tiled(false, nullptr, &p, lay.ri, lay.G, lay.hw, B, lay.block, lds, s)
                             : launch_axonal(false, nullptr, &p, lay.CH, lay.res, lay.hw, B, lay.block, lds, s);
+    scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();
     if (st) return st;
@@ -363,7 +395,9 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     p.base = a->base; p.offt = hybrid ? static_cast<const int8_t*>(dt) : nullptr;
     p.s = a->s; p.s_uniform = a->s_uniform; p.drop = a->drop; p.lif = make_lif(a->lif);
     p.y = a->y; p.u = a->u; p.bits = a->bits; p.gring = gring;
+    const bool timed = scan_begin(DELREC_WS_SYN_FWD, s);
     launch_syn_fwd(p, lay.block, lay.lds, s);
+    scan_end(timed, s);
     return finish_launch();
 }
 
@@ -390,7 +424,9 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     p.d = a->d; p.base = a->base; p.off = a->offsets; p.s = a->s; p.s_uniform = a->s_uniform;
     p.drop = a->drop; p.lif = make_lif(a->lif);
     p.dx = a->dx; p.gr = gr; p.part = part; p.gring = gring;
+    const bool timed = scan_begin(DELREC_WS_SYN_BWD, s);
     launch_syn_bwd(p, lay.block, lay.lds, s);
+    scan_end(timed, s);
     int st = finish_launch();
     if (st) return st;
     launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
@@ -428,6 +464,34 @@ int delrec_delay_grad(const float* C, const float* W, const float* d, float sigm
     if (!C || !W || !d || !dd || N <= 0 || Lm < 1 || !(sigma >= 0.0f)) return DELREC_ERR_ARG;
     launch_delay_grad(C, W, d, sigma, N, Lm, dd, static_cast<hipStream_t>(stream));
     return finish_launch();
+}
+
+int delrec_scan_timing(int32_t capacity) {
+    if (capacity < 0) return DELREC_ERR_ARG;
+    scan_release();
+    if (capacity == 0) return DELREC_OK;
+    g_scan.ev.assign((size_t)2 * capacity, nullptr);
+    for (hipEvent_t& e : g_scan.ev) {
+        if (hipEventCreate(&e) != hipSuccess) {
+            e = nullptr;
+            scan_release();
+            return DELREC_ERR_DEVICE;
+        }
+    }
+    g_scan.kind.assign((size_t)capacity, 0);
+    return DELREC_OK;
+}
+
+int delrec_scan_timing_read(float* ms, int32_t* kinds, int32_t capacity) {
+    if (!ms || !kinds || capacity < 0) return -DELREC_ERR_ARG;
+    const int n = std::min(g_scan.used, (int)capacity);
+    for (int k = 0; k < n; ++k) {
+        if (hipEventSynchronize(g_scan.ev[2 * k + 1]) != hipSuccess) return -DELREC_ERR_DEVICE;
+        if (hipEventElapsedTime(&ms[k], g_scan.ev[2 * k], g_scan.ev[2 * k + 1]) != hipSuccess)
+            return -DELREC_ERR_DEVICE;
+        kinds[k] = g_scan.kind[k];
+    }
+    return n;
 }
 
 }  // extern "C"

@@ -28,7 +28,7 @@ WS_AXONAL_FWD, WS_AXONAL_BWD, WS_SYN_FWD, WS_SYN_BWD = 1, 2, 3, 4
 # Every symbol include/delrec.h declares (checked by the CPU test suite).
 EXPORTS = ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_syn_fwd', 'delrec_syn_bwd',
            'delrec_lif_fwd', 'delrec_lif_bwd', 'delrec_delay_grad', 'delrec_query_workspace',
-           'delrec_strerror', 'delrec_version')
+           'delrec_strerror', 'delrec_version', 'delrec_scan_timing', 'delrec_scan_timing_read')
 
 
 class DelrecError(RuntimeError):
@@ -113,6 +113,10 @@ def load():
     lib.delrec_strerror.restype = ctypes.c_char_p
     lib.delrec_strerror.argtypes = [c_i32]
     lib.delrec_version.restype = ctypes.c_char_p
+    lib.delrec_scan_timing.restype = c_i32
+    lib.delrec_scan_timing.argtypes = [c_i32]
+    lib.delrec_scan_timing_read.restype = c_i32
+    lib.delrec_scan_timing_read.argtypes = [ctypes.POINTER(c_f32), ctypes.POINTER(c_i32), c_i32]
     _lib = lib
     return lib
 
@@ -177,6 +181,34 @@ def call(name, args, stream):
         rec.append((name, s, e))
         return
     _check(name, getattr(load(), name)(ctypes.byref(args), stream))
+
+
+SCAN_KINDS = {1: 'axonal_fwd_scan', 2: 'axonal_bwd_scan', 3: 'syn_fwd_scan', 4: 'syn_bwd_scan'}
+
+
+class scan_timing:
+    """HIP-event durations of the time-scan kernels launched inside the block (at most
+    ``capacity`` launches): ``with scan_timing(n) as st: ...`` then ``st.launches`` is a
+    list of (kind name, ms)."""
+
+    def __init__(self, capacity):
+        self.capacity = int(capacity)
+        self.launches = []
+
+    def __enter__(self):
+        _check('delrec_scan_timing', load().delrec_scan_timing(self.capacity))
+        return self
+
+    def __exit__(self, *exc):
+        lib = load()
+        ms = (c_f32 * self.capacity)()
+        kinds = (c_i32 * self.capacity)()
+        n = lib.delrec_scan_timing_read(ms, kinds, self.capacity)
+        lib.delrec_scan_timing(0)
+        if n < 0:
+            _check('delrec_scan_timing_read', -n)
+        self.launches = [(SCAN_KINDS.get(kinds[k], str(kinds[k])), ms[k]) for k in range(n)]
+        return False
 
 
 def delay_grad(C, W, d, sigma, N, Lm, out, stream):

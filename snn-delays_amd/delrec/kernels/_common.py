@@ -3,6 +3,7 @@ surrogate ids, window length, dropout-mask normalisation."""
 
 import math
 
+import numpy as np
 import torch
 
 from .. import _lib
@@ -26,11 +27,16 @@ def lif_struct(neuron, surrogate_function, gamma=None):
 
 
 def window_length_f32(d_max, s_max):
-    """``L = ceil(1 + max d + max s) + 1`` in fp32 (``delays.build_mask``, reference
+    """``L = ceil(1 + max d + max s) + 1`` with the sum rounded to fp32 after each addition,
+    as the reference's fp32 tensors compute it (``delays.build_mask``, reference
     ``triton_kernels/delays.py:26``)."""
-    v = (torch.tensor(1.0, dtype=torch.float32) + torch.tensor(float(d_max), dtype=torch.float32)
-         + torch.tensor(float(s_max), dtype=torch.float32))
-    return int(torch.ceil(v).item()) + 1
+    v = np.float32(np.float32(1.0) + np.float32(d_max)) + np.float32(s_max)
+    return int(math.ceil(float(np.float32(v)))) + 1
+
+
+def round_half_even_f32(v):
+    """``torch.round`` of an fp32 value (half to even), as an int."""
+    return int(np.round(np.float32(v)))
 
 
 def window_length_f64(d_max, s_max):

@@ -18,7 +18,7 @@ Modes (reference ``recdel_base.py:361-383``):
 import torch
 
 from .. import _lib
-from ._common import bits_shape, drop_bn, require_device, weights, window_length_f32
+from ._common import bits_shape, drop_bn, require_device, round_half_even_f32, weights, window_length_f32
 from .delays import build_lag, build_lag_interp
 
 
@@ -34,13 +34,24 @@ class AxonalRecdelHip(torch.autograd.Function):
         Wc, w_bf16 = weights(W)
         dc = d.detach().to(torch.float32).contiguous()
         sigma = float(sigma)
+        s_vec = None
         if use_sig_p:
             s_vec = (1.0 + 2.0 * sigma * torch.sigmoid(p_spread.detach().to(torch.float32))).contiguous()
-            s_max = float(s_vec.max())
+        m = drop_bn(drop, T, B, N)
+        bc = None if bias is None else bias.detach().to(torch.float32).contiguous()
+        lif = _lib.make_lif(tau, v_th, v_reset, decay_input, detach_reset, surr_id, gamma, alpha)
+        y = torch.empty(T, B, N, device=dev, dtype=torch.float32)
+        u = torch.empty_like(y)
+        z = torch.empty_like(y)
+        bits = torch.empty(bits_shape(T, B, N), device=dev, dtype=torch.int32)
+        ws = _lib.workspace(_lib.WS_AXONAL_FWD, T, B, N, 2, w_bf16, dev)   # size does not depend on L
+
+        # The window length needs max d (and max s): the one device-to-host read of the call,
+        # taken after the host work above so that it overlaps the GPU work still queued.
+        if use_sig_p:
+            d_max, s_max = torch.stack([dc.max(), s_vec.max()]).tolist()
         else:
-            s_vec = None
-            s_max = float(torch.tensor(1.0 + sigma, dtype=torch.float32))
-        d_max = float(dc.max())
+            d_max, s_max = dc.max().item(), 1.0 + sigma
         lag = frac = None
         if ste_mode:
             L = window_length_f32(d_max, s_max)
@@ -51,21 +62,12 @@ class AxonalRecdelHip(torch.autograd.Function):
             approx = False
             mode = _lib.DELREC_BWD_SOFT
         elif approx:
-            L = int(torch.round(dc).max().item()) + 2
+            L = round_half_even_f32(d_max) + 2          # max(round(d)) = round(max(d))
             lag, taps, mode = build_lag(dc, L), _lib.DELREC_TAPS_ROUND, _lib.DELREC_BWD_STRAIGHT
         else:
             L = window_length_f32(d_max, s_max)
             taps, mode = _lib.DELREC_TAPS_SOFT, _lib.DELREC_BWD_SOFT
         L = max(L, 2)
-        m = drop_bn(drop, T, B, N)
-        bc = None if bias is None else bias.detach().to(torch.float32).contiguous()
-        lif = _lib.make_lif(tau, v_th, v_reset, decay_input, detach_reset, surr_id, gamma, alpha)
-
-        y = torch.empty(T, B, N, device=dev, dtype=torch.float32)
-        u = torch.empty_like(y)
-        z = torch.empty_like(y)
-        bits = torch.empty(bits_shape(T, B, N), device=dev, dtype=torch.int32)
-        ws = _lib.workspace(_lib.WS_AXONAL_FWD, T, B, N, L, w_bf16, dev)
         args = _lib.AxonalFwdArgs(
             T=T, B=B, N=N, L=L, x=_lib.ptr(xc), W=_lib.ptr(Wc), w_bf16=w_bf16, bias=_lib.ptr(bc),
             d=_lib.ptr(dc), s=_lib.ptr(s_vec), s_uniform=1.0 + sigma, drop=_lib.ptr(m), taps=taps,

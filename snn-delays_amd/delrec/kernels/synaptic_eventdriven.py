@@ -16,27 +16,33 @@ from ._common import bits_shape, drop_bn, lif_struct, require_device, weights, w
 
 
 def _spread(layer, device):
-    """Per-source half-width (``use_sig_p``) or the uniform ``1 + sigma``."""
+    """Per-source half-width (``use_sig_p``) or ``None`` for the uniform ``1 + sigma``."""
     if layer.use_sig_p:
-        s = (1.0 + 2.0 * float(layer.sigma) * torch.sigmoid(
+        return (1.0 + 2.0 * float(layer.sigma) * torch.sigmoid(
             layer.p_spread.detach().to(device=device, dtype=torch.float32))).contiguous()
-        return s, float(s.max())
-    return None, 1.0 + float(layer.sigma)
+    return None
 
 
-def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, s_max, d_max, bias, drop, lif):
+def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop, lif):
     """Launch ``delrec_syn_fwd`` with per-connection delays ``d_eff`` (N, N), or with the
-    hybrid ``base`` (N) + int8 ``offsets`` (N, N) when ``d_eff`` is None; ``d_max`` is the
-    largest effective delay. Returns ``(y, u, bits, L, Wc, w_bf16)``."""
+    hybrid ``base`` (N) + int8 ``offsets`` (N, N) when ``d_eff`` is None; ``d_all`` is a
+    device tensor holding every effective delay (for the window length). Returns
+    ``(y, u, bits, L, Wc, w_bf16)``."""
     require_device(x)
     T, B, N = x.shape
     dev = x.device
     xc = x.detach().to(torch.float32).contiguous()
     Wc, w_bf16 = weights(W)
-    L = max(window_length_f64(d_max, s_max), 2)
     y = torch.empty(T, B, N, device=dev, dtype=torch.float32)
     u = torch.empty_like(y)
     bits = torch.empty(bits_shape(T, B, N), device=dev, dtype=torch.int32)
+    # the window length needs max d (and max s): the one device-to-host read of the call,
+    # taken after the host work above so that it overlaps the GPU work still queued
+    if s_vec is not None:
+        d_max, s_max = torch.stack([d_all.max(), s_vec.max()]).tolist()
+    else:
+        d_max, s_max = d_all.max().item(), s_uniform
+    L = max(window_length_f64(d_max, s_max), 2)
     flags = w_bf16 | (2 if d_eff is None else 0)
     ws = _lib.workspace(_lib.WS_SYN_FWD, T, B, N, L, flags, dev)
     args = _lib.SynFwdArgs(
@@ -82,13 +88,13 @@ class EventDrivenSyn(torch.autograd.Function):
         T, B, N = x.shape
         dev = x.device
         d_eff = (d.detach().round() if layer.round_delays else d.detach()).to(torch.float32).contiguous()
-        s_vec, s_max = _spread(layer, dev)
+        s_vec = _spread(layer, dev)
         s_uniform = 1.0 + float(layer.sigma)
         m = drop_bn(drop, T, B, N)
         bc = None if bias is None else bias.detach().to(torch.float32).contiguous()
         lif = layer_lif(layer)
-        y, u, bits, L, Wc, w_bf16 = syn_forward(x, W, d_eff, None, None, s_vec, s_uniform, s_max,
-                                                float(d_eff.max()), bc, m, lif)
+        y, u, bits, L, Wc, w_bf16 = syn_forward(x, W, d_eff, None, None, s_vec, s_uniform, d_eff,
+                                                bc, m, lif)
         ctx.save_for_backward(u, y, bits, Wc, d_eff, s_vec, m, p_spread)
         ctx.meta = (L, w_bf16, s_uniform, float(layer.sigma), bool(layer.use_sig_p), bias is not None,
                     W.dtype)

@@ -72,8 +72,7 @@ class HybridSynDelay(torch.autograd.Function):
         bc = None if bias is None else bias.detach().to(torch.float32).contiguous()
         lif = layer_lif(layer)
         d_arg = None if base is not None else d_eff
-        y, u, bits, L, Wc, w_bf16 = syn_forward(x, W, d_arg, base, off8, None, s, s,
-                                                float(d_eff.max()), bc, m, lif)
+        y, u, bits, L, Wc, w_bf16 = syn_forward(x, W, d_arg, base, off8, None, s, d_eff, bc, m, lif)
         ctx.save_for_backward(u, y, bits, Wc, d_arg, base, off8, m)
         ctx.meta = (L, w_bf16, s, bias is not None, W.dtype)
         ctx.lif = lif
