@@ -174,9 +174,19 @@ SynLayout syn_layout(int N, int L, bool fwd) {
     return o;
 }
 
-int lag_splits(int T, int N) {
-    const int tiles = (N + 63) / 64;
-    return std::max(1, std::min((2 * num_cus() + tiles * tiles - 1) / (tiles * tiles), T));
+// the bf16 lag GEMM's packed operands: rows t * Bp + b (+ one stage of zero rows), columns
+// padded to the 128-wide output tile
+struct LagPack {
+    int Bp, Np, Kp, KS;
+};
+
+LagPack lag_pack(int T, int B, int N) {
+    LagPack q;
+    q.Bp = (B + 7) / 8 * 8;
+    q.Np = (N + 127) / 128 * 128;
+    q.Kp = T * q.Bp + 32;
+    q.KS = lag_bf16_splits(T, q.Bp, q.Np, num_cus());
+    return q;
 }
 
 template <class C>
@@ -190,10 +200,15 @@ void syn_fwd_ws(C& c, int B, int N, int L, bool hybrid, bool bf16) {
 template <class C>
 void syn_bwd_ws(C& c, int T, int B, int N, int L) {
     const SynLayout lay = syn_layout(N, L, false);
-    const int ks = lag_splits(T, N);
+    const LagPack q = lag_pack(T, B, N);
+    const size_t packed = (size_t)q.Kp / 8 * q.Np;       // uint4 per packed operand
     c.template take<float>((size_t)T * B * N);          // gr
     c.template take<float>((size_t)B * N);              // db partials
-    c.template take<float>((size_t)3 * ks * N * N);     // lag-GEMM partials
+    c.template take<float>((size_t)3 * q.KS * N * N);   // lag-GEMM partials
+    c.template take<uint4>(packed);                     // gr_hi
+    c.template take<uint4>(packed);                     // gr_lo
+    c.template take<uint4>(packed);                     // shifted spikes
+    c.template take<int>((size_t)N + 64);               // R and first lag per column
     if (!lay.lds_ring) c.template take<float>((size_t)B * lay.R * N);
 }
 
@@ -403,20 +418,27 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
 
 int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
-    if (!a->gy || !a->u || !a->y || !a->W || !a->dx || !lif_ok(a->lif)) return DELREC_ERR_ARG;
+    if (!a->gy || !a->u || !a->bits || !a->W || !a->dx || !lif_ok(a->lif)) return DELREC_ERR_ARG;
     const bool hybrid = a->d == nullptr;
     if (hybrid && (!a->base || !a->offsets)) return DELREC_ERR_ARG;
+    if (hybrid && a->s) return DELREC_ERR_UNSUPPORTED;     // the hybrid has one uniform half-width
     if (a->N > 4096) return DELREC_ERR_UNSUPPORTED;
     const SynLayout lay = syn_layout(a->N, a->L, false);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int T = a->T, B = a->B, N = a->N;
-    const int ks = lag_splits(T, N);
+    const LagPack q = lag_pack(T, B, N);
+    const size_t packed = (size_t)q.Kp / 8 * q.Np;
     Carver cv(a->workspace, a->workspace_bytes);
     float* gr = cv.take<float>((size_t)T * B * N);
     float* part = cv.take<float>((size_t)B * N);
-    float* lagp = cv.take<float>((size_t)3 * ks * N * N);
+    float* lagp = cv.take<float>((size_t)3 * q.KS * N * N);
+    uint4* ahi = cv.take<uint4>(packed);
+    uint4* alo = cv.take<uint4>(packed);
+    uint4* yb = cv.take<uint4>(packed);
+    int* meta = cv.take<int>((size_t)N + 64);
     float* gring = lay.lds_ring ? nullptr : cv.take<float>((size_t)B * lay.R * N);
-    if (!gr || !part || !lagp || (!lay.lds_ring && !gring)) return DELREC_ERR_WORKSPACE;
+    if (!gr || !part || !lagp || !ahi || !alo || !yb || !meta || (!lay.lds_ring && !gring))
+        return DELREC_ERR_WORKSPACE;
 
     SynBwd p{};
     p.T = T; p.B = B; p.N = N; p.L = a->L; p.R = lay.R; p.NP = lay.NP;
@@ -431,16 +453,22 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     if (st) return st;
     launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
     if (a->dW || a->dd || a->ds) {
-        LagGemm g{};
-        g.T = T; g.B = B; g.N = N; g.L = a->L; g.KS = ks;
-        g.gr = gr; g.y = a->y; g.W = a->W; g.w_bf16 = a->w_bf16;
-        g.d = a->d; g.base = a->base; g.off = a->offsets; g.s = a->s; g.s_uniform = a->s_uniform;
         const size_t NN = (size_t)N * N;
+        LagBf16 g{};
+        g.T = T; g.B = B; g.Bp = q.Bp; g.N = N; g.Np = q.Np; g.L = a->L; g.Kp = q.Kp; g.KS = q.KS;
+        g.R = std::max(a->L - 1, 1);
+        g.ahi = ahi; g.alo = alo; g.yb = yb;
+        g.meta = hybrid ? meta : nullptr;
+        g.lo = hybrid ? meta + 64 : nullptr;
+        g.d = a->d; g.base = a->base; g.off = a->offsets; g.s = a->s; g.s_uniform = a->s_uniform;
         g.pw = lagp;
-        g.pd = lagp + (size_t)ks * NN;
-        g.ps = a->ds ? lagp + (size_t)2 * ks * NN : nullptr;
-        launch_lag_gemm(g, s);
-        launch_lag_finish(g, a->dW, a->dd, a->ds, s);
+        g.pd = lagp + (size_t)q.KS * NN;
+        g.ps = a->ds ? lagp + (size_t)2 * q.KS * NN : nullptr;
+        launch_lag_bf16(g, gr, a->bits, s);
+        LagGemm f{};
+        f.N = N; f.KS = q.KS; f.W = a->W; f.w_bf16 = a->w_bf16; f.s = a->s; f.s_uniform = a->s_uniform;
+        f.pw = g.pw; f.pd = g.pd; f.ps = g.ps;
+        launch_lag_finish(f, a->dW, a->dd, a->ds, s);
     }
     return finish_launch();
 }

@@ -3,10 +3,7 @@
 //   dw_gemm     dW[i,j] = sum_{t,b} gr[t,b,i] * z[t,b,j]: the axonal weight gradient, the
 //               reference's host GEMM at recdel_base.py:327-330. 128x128 tiles, split-K
 //               into deterministic partials (no atomics), summed by sum_partials.
-//   lag_gemm    C_l[i,j] = sum_{t>=l,b} gr[t,b,i] * y[t-l,b,j] for every lag l, reduced in
-//               the epilogue straight into dW = sum_l h*C_l, sum_l sign*C_l and
-//               sum_l dh/ds*C_l, so the (N, N, L) Cstack of the reference
-//               (synaptic_eventdriven.py:441-468, synaptic_hybrid.py:196-208) never exists.
+//   lag_finish  dW, dd (and ds) from the split partials of the lag-correlation GEMM.
 //
 // MFMA 16x16x4 f32 operand layout (wave64): lane l supplies A[l%16][l/16] and
 // B[l/16][l%16]; accumulator register r of lane l holds D[4*(l/16) + r][l%16].
@@ -136,111 +133,7 @@ void launch_sum_partials(const float* partial, int ks, size_t count, float* out,
 }
 
 // ---------------------------------------------------------------------------------------
-// Lag-correlation GEMM with the triangle epilogue. 64x64 tile per workgroup (4 waves of
-// 32x32), split over source-time chunks (blockIdx.z).
-constexpr int kLgTile = 64;
-constexpr int kLgKt = 16;
-
-__device__ __forceinline__ float conn_delay(const LagGemm& p, int i, int j) {
-    if (p.d) return p.d[(size_t)i * p.N + j];
-    return p.base[j] + 0.0f + 1.0f * (float)p.off[(size_t)i * p.N + j];
-}
-
-__global__ void __launch_bounds__(256) lag_gemm_kernel(LagGemm p) {
-    __shared__ float sA[kLgKt][kLgTile + 4];
-    __shared__ float sB[kLgKt][kLgTile + 4];
-    const int N = p.N, T = p.T, B = p.B;
-    const int i0 = blockIdx.x * kLgTile, j0 = blockIdx.y * kLgTile, ks = blockIdx.z;
-    const int tchunk = (T + p.KS - 1) / p.KS;
-    const int tb = ks * tchunk, te = min(T, tb + tchunk);   // source-time range tau
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int wi = w >> 1, wj = w & 1;
-    const int lr = lane >> 4, lc = lane & 15;
-
-    // per-element delay centre and half-width for the 16 outputs of this lane
-    float cc[2][2][4], ss[2][2][4];
-    bool ok[2][2][4];
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = i0 + wi * 32 + a * 16 + 4 * lr + r;
-                const int j = j0 + wj * 32 + c * 16 + lc;
-                ok[a][c][r] = i < N && j < N;
-                const int ic = ok[a][c][r] ? i : 0, jc = ok[a][c][r] ? j : 0;
-                cc[a][c][r] = 1.0f + conn_delay(p, ic, jc);
-                ss[a][c][r] = p.s ? p.s[jc] : p.s_uniform;
-            }
-    float ow[2][2][4] = {}, od[2][2][4] = {}, os[2][2][4] = {};
-
-    for (int l = 1; l < p.L; ++l) {
-        const int tend = min(te, T - l);
-        if (tend <= tb) break;
-        floatx4 acc[2][2];
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int c = 0; c < 2; ++c) acc[a][c] = floatx4{0.f, 0.f, 0.f, 0.f};
-        const int kb = tb * B, ke = tend * B;   // rows of y (source time tau); gr row = k + l*B
-        const size_t shift = (size_t)l * B;
-        for (int k0 = kb; k0 < ke; k0 += kLgKt) {
-            for (int q = threadIdx.x; q < kLgKt * kLgTile; q += 256) {
-                const int r = q / kLgTile, c = q - r * kLgTile;
-                const int k = k0 + r;
-                const bool kin = k < ke;
-                sA[r][c] = (kin && i0 + c < N) ? p.gr[(k + shift) * N + i0 + c] : 0.0f;
-                sB[r][c] = (kin && j0 + c < N) ? p.y[(size_t)k * N + j0 + c] : 0.0f;
-            }
-            __syncthreads();
-#pragma unroll
-            for (int kk = 0; kk < kLgKt; kk += 4) {
-                float av[2], bv[2];
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    av[q] = sA[kk + lr][wi * 32 + q * 16 + lc];
-                    bv[q] = sB[kk + lr][wj * 32 + q * 16 + lc];
-                }
-#pragma unroll
-                for (int a = 0; a < 2; ++a)
-#pragma unroll
-                    for (int c = 0; c < 2; ++c)
-                        acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[c], acc[a][c], 0, 0, 0);
-            }
-            __syncthreads();
-        }
-        const float lf = (float)l;
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int c = 0; c < 2; ++c)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float C = acc[a][c][r];
-                    const float cv = cc[a][c][r], sv = ss[a][c][r], s2 = sv * sv;
-                    ow[a][c][r] += tri_weight(lf, cv, sv, s2) * C;
-                    od[a][c][r] += tri_dsign(lf, cv, sv) * C;
-                    os[a][c][r] += tri_ds(lf, cv, sv, s2) * C;
-                }
-    }
-    const size_t NN = (size_t)N * N;
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (!ok[a][c][r]) continue;
-                const int i = i0 + wi * 32 + a * 16 + 4 * lr + r;
-                const int j = j0 + wj * 32 + c * 16 + lc;
-                const size_t o = (size_t)ks * NN + (size_t)i * N + j;
-                p.pw[o] = ow[a][c][r];
-                if (p.pd) p.pd[o] = od[a][c][r];
-                if (p.ps) p.ps[o] = os[a][c][r];
-            }
-}
-
+// Sums of the lag-GEMM partials (lagmm.hip) into dW, dd and ds.
 __global__ void lag_finish_kernel(LagGemm p, float* dW, float* dd) {
     const size_t NN = (size_t)p.N * p.N;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -269,11 +162,6 @@ __global__ void lag_ds_kernel(LagGemm p, float* ds) {
         acc += load_w(p.W, p.w_bf16, (size_t)i * p.N + j) * c;
     }
     ds[j] = acc;
-}
-
-void launch_lag_gemm(const LagGemm& a, hipStream_t stream) {
-    const int tiles = (a.N + kLgTile - 1) / kLgTile;
-    hipLaunchKernelGGL(lag_gemm_kernel, dim3(tiles, tiles, a.KS), dim3(256), 0, stream, a);
 }
 
 void launch_lag_finish(const LagGemm& a, float* dW, float* dd, float* ds, hipStream_t stream) {

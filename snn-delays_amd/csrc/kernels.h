@@ -86,20 +86,34 @@ struct SynBwd {
     float* gring;               // global ring [B][R][N] when the ring does not fit LDS, else NULL
 };
 
+// the split partials of the lag GEMM and what dd / ds are formed from
 struct LagGemm {
-    int T, B, N, L, KS;
-    const float* gr;            // (T,B,N)
-    const float* y;             // (T,B,N)
+    int N, KS;
     const void* W;
     int w_bf16;
-    const float* d;             // row-major, or NULL (hybrid)
-    const float* base;
-    const int8_t* off;
     const float* s;
     float s_uniform;
     float* pw;                  // [KS][N][N] partial sum_l h * C_l
     float* pd;                  // [KS][N][N] partial sum_l sign * C_l, or NULL
     float* ps;                  // [KS][N][N] partial sum_l dh/ds * C_l, or NULL
+};
+
+// bf16-MFMA lag-correlation GEMM (lagmm.hip): operands packed in the k-blocked layout
+struct LagBf16 {
+    int T, B, Bp, N, Np, L, Kp, KS, R;   // R: relative lags when meta == NULL
+    const uint4* ahi;            // gr_hi (Kp, Np) k-blocked
+    const uint4* alo;            // gr_lo
+    const uint4* yb;             // shifted spikes Y' (Kp, Np) k-blocked
+    int* meta;                   // hybrid: meta[0] = R written by lag_range_kernel, else NULL
+    int* lo;                     // hybrid: first lag per column, else NULL (lo = 1)
+    const float* d;              // row-major, or NULL (hybrid)
+    const float* base;
+    const int8_t* off;
+    const float* s;
+    float s_uniform;
+    float* pw;                   // [KS][N][N] partial sum_l h * C_l
+    float* pd;                   // [KS][N][N] partial sum_l sign * C_l
+    float* ps;                   // [KS][N][N] partial sum_l dh/ds * C_l, or NULL
 };
 
 bool launch_axonal(bool fwd, const AxFwd* fa, const AxBwd* ba, int ch, bool res, int hw,
@@ -117,7 +131,9 @@ void launch_sum_partials(const float* partial, int ks, size_t count, float* out,
 
 void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream);
 void launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);
-void launch_lag_gemm(const LagGemm& a, hipStream_t stream);
+int lag_bf16_splits(int T, int Bp, int Np, int cus);
+// packs gr / spikes, then the lag GEMM into a.pw / a.pd / a.ps
+void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hipStream_t stream);
 // dW = sum_k pw; dd = W/s^2 * sum_k pd; ds[j] = sum_i W[i,j] * sum_k ps[i,j]
 void launch_lag_finish(const LagGemm& a, float* dW, float* dd, float* ds, hipStream_t stream);
 
