@@ -152,6 +152,7 @@ typedef struct {
     const int8_t* offsets;
     const float* s;
     float s_uniform;
+    float s_max;                 /* largest half-width: max of s[], or s_uniform           */
     const float* drop;
     delrec_lif lif;
     float* dx;                   /* out (T,B,N)                                          */

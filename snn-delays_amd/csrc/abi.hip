@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <initializer_list>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -174,6 +175,42 @@ SynLayout syn_layout(int N, int L, bool fwd) {
     return o;
 }
 
+constexpr int kSynMaxTaps = 64;   // half-widths up to s = 31
+
+// Backward ring of the synaptic / hybrid scan: source-major rows of R = L slots plus KT
+// mirror slots, KT = taps walked per connection (from the largest half-width).
+struct SynBwdLayout {
+    int block, R, RS, RP, KT, NT;
+    bool lds_ring;
+    size_t lds;
+};
+
+int syn_taps(float s_max, bool hybrid) {
+    // hybrid: taps of one column's triangle from its first closed-support lag (s == 1 needs 2);
+    // synaptic: lags from max(1, ceil(c - s)) up to floor(c + s)
+    const int need = hybrid ? (s_max == 1.0f ? 2 : (int)std::ceil(2.0f * s_max) + 1)
+                            : (int)std::floor(2.0f * s_max) + 2;
+    // compiled run lengths: 2 and 4 (hybrid), 4, 8 and 12 (synaptic); others run with a
+    // runtime tap count
+    for (int kt : hybrid ? std::initializer_list<int>{2, 4} : std::initializer_list<int>{4, 8, 12})
+        if (kt >= need) return kt;
+    return need <= kSynMaxTaps ? need : 0;
+}
+
+SynBwdLayout syn_bwd_layout(int N, int L, int KT) {
+    SynBwdLayout o;
+    o.block = std::min(1024, (N + 63) / 64 * 64);
+    o.R = std::max(L, 2);
+    o.KT = KT;
+    o.RS = o.R + KT;
+    o.RP = o.RS | 1;                         // odd pitch: a gather's lanes hit distinct banks
+    o.NT = (N + 15) / 16 * 16;
+    const size_t ring = (size_t)N * o.RP * sizeof(float);
+    o.lds_ring = ring <= (size_t)max_lds_bytes();
+    o.lds = o.lds_ring ? ring : 0;
+    return o;
+}
+
 // the bf16 lag GEMM's packed operands: rows t * Bp + b (+ one stage of zero rows), columns
 // padded to the 128-wide output tile
 struct LagPack {
@@ -199,7 +236,8 @@ void syn_fwd_ws(C& c, int B, int N, int L, bool hybrid, bool bf16) {
 
 template <class C>
 void syn_bwd_ws(C& c, int T, int B, int N, int L) {
-    const SynLayout lay = syn_layout(N, L, false);
+    // sized for the widest tap run, so the ring may always go to the workspace
+    const SynBwdLayout lay = syn_bwd_layout(N, L, kSynMaxTaps);
     const LagPack q = lag_pack(T, B, N);
     const size_t packed = (size_t)q.Kp / 8 * q.Np;       // uint4 per packed operand
     c.template take<float>((size_t)T * B * N);          // gr
@@ -209,30 +247,63 @@ void syn_bwd_ws(C& c, int T, int B, int N, int L) {
     c.template take<uint4>(packed);                     // gr_lo
     c.template take<uint4>(packed);                     // shifted spikes
     c.template take<int>((size_t)N + 64);               // R and first lag per column
-    if (!lay.lds_ring) c.template take<float>((size_t)B * lay.R * N);
+    c.template take<float>((size_t)N * lay.NT);         // W^T (fp32 or bf16)
+    c.template take<float>((size_t)N * lay.NT);         // d^T or the offsets^T
+    c.template take<float>((size_t)B * N * lay.RP);     // ring when it does not fit LDS
 }
 
-// out[c*rows + r] = in[r*cols + c] for elements of `esize` bytes
+// out[c * op + r] = in[r * n + c] for an (n, n) matrix; output columns r in [n, op) are 0
 template <class E>
-__global__ void transpose_kernel(const E* __restrict__ in, E* __restrict__ out, int n) {
+__global__ void transpose_kernel(const E* __restrict__ in, E* __restrict__ out, int n, int op) {
     __shared__ E tile[32][33];
     const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
     for (int k = threadIdx.y; k < 32; k += 8) {
         const int r = by + k, c = bx + threadIdx.x;
-        if (r < n && c < n) tile[k][threadIdx.x] = in[(size_t)r * n + c];
+        tile[k][threadIdx.x] = (r < n && c < n) ? in[(size_t)r * n + c] : E(0);
     }
     __syncthreads();
     for (int k = threadIdx.y; k < 32; k += 8) {
         const int r = bx + k, c = by + threadIdx.x;
-        if (r < n && c < n) out[(size_t)r * n + c] = tile[threadIdx.x][k];
+        if (r < n && c < op) out[(size_t)r * op + c] = tile[threadIdx.x][k];
+    }
+}
+
+// Blocked transpose for per-lane streaming: lane j reads 16 consecutive i of column j of
+// an (n, n) row-major matrix as one contiguous run of 16 elements, and a wave's lanes read
+// adjacent runs: out[((i / 16) * n + j) * 16 + i % 16] = in[i * n + j], zero for i >= n
+// (the chunks cover nc = ceil(n / 16) * 16 rows).
+template <class E>
+__global__ void block_transpose_kernel(const E* __restrict__ in, E* __restrict__ out, int n) {
+    const int nc = (n + 15) / 16;
+    const size_t total = (size_t)nc * n;
+    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total;
+         q += (size_t)gridDim.x * blockDim.x) {
+        const int c = (int)(q / n), j = (int)(q - (size_t)c * n);
+        E v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int i = c * 16 + e;
+            v[e] = i < n ? in[(size_t)i * n + j] : E(0);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) out[q * 16 + e] = v[e];
     }
 }
 
 template <class E>
-void transpose(const void* in, void* out, int n, hipStream_t s) {
-    dim3 grid((n + 31) / 32, (n + 31) / 32);
+void block_transpose(const void* in, void* out, int n, hipStream_t s) {
+    const size_t total = (size_t)((n + 15) / 16) * n;
+    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 65535);
+    hipLaunchKernelGGL(block_transpose_kernel<E>, dim3(blocks), dim3(256), 0, s,
+                       static_cast<const E*>(in), static_cast<E*>(out), n);
+}
+
+template <class E>
+void transpose(const void* in, void* out, int n, hipStream_t s, int op = 0) {
+    if (op < n) op = n;
+    const dim3 grid((n + 31) / 32, (op + 31) / 32);
     hipLaunchKernelGGL(transpose_kernel<E>, grid, dim3(32, 8), 0, s, static_cast<const E*>(in),
-                       static_cast<E*>(out), n);
+                       static_cast<E*>(out), n, op);
 }
 
 // HIP-event brackets around the time-scan kernels (benchmark hook)
@@ -419,11 +490,15 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
 int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
     if (!a->gy || !a->u || !a->bits || !a->W || !a->dx || !lif_ok(a->lif)) return DELREC_ERR_ARG;
+    if (!(a->s_max > 0.0f)) return DELREC_ERR_ARG;
     const bool hybrid = a->d == nullptr;
     if (hybrid && (!a->base || !a->offsets)) return DELREC_ERR_ARG;
     if (hybrid && a->s) return DELREC_ERR_UNSUPPORTED;     // the hybrid has one uniform half-width
     if (a->N > 4096) return DELREC_ERR_UNSUPPORTED;
-    const SynLayout lay = syn_layout(a->N, a->L, false);
+    const int KT = syn_taps(hybrid ? a->s_uniform : a->s_max, hybrid);
+    if (KT == 0) return DELREC_ERR_UNSUPPORTED;             // half-width beyond the widest tap run
+    const SynBwdLayout lay = syn_bwd_layout(a->N, a->L, KT);
+    const SynBwdLayout wlay = syn_bwd_layout(a->N, a->L, kSynMaxTaps);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int T = a->T, B = a->B, N = a->N;
     const LagPack q = lag_pack(T, B, N);
@@ -436,19 +511,37 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     uint4* alo = cv.take<uint4>(packed);
     uint4* yb = cv.take<uint4>(packed);
     int* meta = cv.take<int>((size_t)N + 64);
-    float* gring = lay.lds_ring ? nullptr : cv.take<float>((size_t)B * lay.R * N);
-    if (!gr || !part || !lagp || !ahi || !alo || !yb || !meta || (!lay.lds_ring && !gring))
+    void* wt = cv.take<float>((size_t)N * wlay.NT);
+    void* dt = cv.take<float>((size_t)N * wlay.NT);
+    float* gring = cv.take<float>((size_t)B * N * wlay.RP);
+    if (!gr || !part || !lagp || !ahi || !alo || !yb || !meta || !wt || !dt || !gring)
         return DELREC_ERR_WORKSPACE;
 
+    if (a->w_bf16) block_transpose<uint16_t>(a->W, wt, N, s); else block_transpose<float>(a->W, wt, N, s);
+    if (hybrid) {
+        block_transpose<int8_t>(a->offsets, dt, N, s);
+        // offset range (meta[0] = relative lags of the lag GEMM, meta[1] = smallest offset)
+        // and each column's first lag, read by the scan and the lag GEMM
+        launch_lag_range(a->offsets, a->base, N, a->L, a->s_uniform, meta, meta + 64, s);
+    } else {
+        block_transpose<float>(a->d, dt, N, s);
+    }
+
     SynBwd p{};
-    p.T = T; p.B = B; p.N = N; p.L = a->L; p.R = lay.R; p.NP = lay.NP;
-    p.gy = a->gy; p.u = a->u; p.W = a->W; p.w_bf16 = a->w_bf16;
-    p.d = a->d; p.base = a->base; p.off = a->offsets; p.s = a->s; p.s_uniform = a->s_uniform;
+    p.T = T; p.B = B; p.N = N; p.L = a->L;
+    p.R = lay.R; p.RS = lay.RS; p.RP = lay.RP; p.KT = lay.KT; p.NT = lay.NT;
+    p.gy = a->gy; p.u = a->u; p.Wt = wt; p.w_bf16 = a->w_bf16;
+    p.dt = hybrid ? nullptr : static_cast<const float*>(dt);
+    p.base = a->base;
+    p.offt = hybrid ? static_cast<const int8_t*>(dt) : nullptr;
+    p.meta = hybrid ? meta : nullptr;
+    p.s = a->s; p.s_uniform = a->s_uniform;
     p.drop = a->drop; p.lif = make_lif(a->lif);
-    p.dx = a->dx; p.gr = gr; p.part = part; p.gring = gring;
+    p.dx = a->dx; p.gr = gr; p.part = part; p.gring = lay.lds_ring ? nullptr : gring;
     const bool timed = scan_begin(DELREC_WS_SYN_BWD, s);
-    launch_syn_bwd(p, lay.block, lay.lds, s);
-    scan_end(timed, s);
+    const bool ok = launch_syn_bwd(p, lay.block, lay.lds, s);
+    scan_end(timed && ok, s);
+    if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();
     if (st) return st;
     launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);

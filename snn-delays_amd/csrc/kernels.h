@@ -68,14 +68,20 @@ struct SynFwd {
 };
 
 struct SynBwd {
-    int T, B, N, L, R, NP;
+    int T, B, N, L;
+    int R;                      // ring slots (time mod R), R >= L
+    int RS;                     // slots per ring row incl. the KT mirror slots
+    int RP;                     // ring row pitch (floats)
+    int KT;                     // taps walked per connection (2, 4, 8, 12, 16)
+    int NT;                     // rows of the blocked W^T / d^T / offsets^T (multiple of 16)
     const float* gy;
     const float* u;
-    const void* W;              // row-major W[i*N + j]
+    const void* Wt;             // blocked W^T: W[i][j] at ((i/16)*N + j)*16 + i%16, 0 for i >= N
     int w_bf16;
-    const float* d;             // row-major d[i*N + j], or NULL (hybrid)
-    const float* base;
-    const int8_t* off;          // row-major offsets
+    const float* dt;            // blocked d^T (synaptic), or NULL
+    const float* base;          // hybrid base (N)
+    const int8_t* offt;         // blocked hybrid offsets^T (int8), or NULL
+    const int* meta;            // hybrid: meta[1] = smallest offset
     const float* s;
     float s_uniform;
     const float* drop;
@@ -83,7 +89,7 @@ struct SynBwd {
     float* dx;
     float* gr;                  // (T,B,N) dL/drec (always written: the dW / dd GEMM reads it)
     float* part;                // [B][N] db partials
-    float* gring;               // global ring [B][R][N] when the ring does not fit LDS, else NULL
+    float* gring;               // global ring [B][N][RP] when it does not fit LDS, else NULL
 };
 
 // the split partials of the lag GEMM and what dd / ds are formed from
@@ -130,8 +136,11 @@ void launch_dw_gemm(const float* A, const float* Bm, int K, int N, int ks, float
 void launch_sum_partials(const float* partial, int ks, size_t count, float* out, hipStream_t stream);
 
 void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream);
-void launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);
+bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);
 int lag_bf16_splits(int T, int Bp, int Np, int cus);
+// hybrid: meta[0] = relative lags, meta[1] = smallest offset, lo[j] = first lag of column j
+void launch_lag_range(const int8_t* off, const float* base, int N, int L, float s, int* meta, int* lo,
+                      hipStream_t stream);
 // packs gr / spikes, then the lag GEMM into a.pw / a.pd / a.ps
 void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hipStream_t stream);
 // dW = sum_k pw; dd = W/s^2 * sum_k pd; ds[j] = sum_i W[i,j] * sum_k ps[i,j]

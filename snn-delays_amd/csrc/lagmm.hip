@@ -104,7 +104,8 @@ __global__ void pack_spikes_kernel(const uint32_t* __restrict__ bits, const int*
 }
 
 // Hybrid lag range: one workgroup reduces the offsets to their min / max, then writes the
-// number of relative lags R (meta[0]) and each column's first lag lo_j.
+// number of relative lags R (meta[0]), the smallest offset (meta[1]) and each column's
+// first lag lo_j.
 __global__ void __launch_bounds__(1024) lag_range_kernel(const int8_t* __restrict__ off,
                                                          const float* __restrict__ base, int N, int L,
                                                          float s, int* __restrict__ meta,
@@ -138,6 +139,7 @@ __global__ void __launch_bounds__(1024) lag_range_kernel(const int8_t* __restric
         const bool full = R >= L - 1;
         if (full) R = L - 1;
         meta[0] = max(R, 1);
+        meta[1] = a;
         s_omin = a;
         s_full = full ? 1 : 0;
     }
@@ -299,6 +301,11 @@ __global__ void __launch_bounds__(256) lag_bf16_kernel(LagBf16 p) {
             }
 }
 
+void launch_lag_range(const int8_t* off, const float* base, int N, int L, float s, int* meta, int* lo,
+                      hipStream_t stream) {
+    hipLaunchKernelGGL(lag_range_kernel, dim3(1), dim3(1024), 0, stream, off, base, N, L, s, meta, lo);
+}
+
 int lag_bf16_splits(int T, int Bp, int Np, int cus) {
     const int tiles = (Np / kLT) * (Np / kLT);
     const int steps = (T * Bp + kLK - 1) / kLK;
@@ -311,9 +318,6 @@ void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hi
     const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 65535u * 4);
     hipLaunchKernelGGL(pack_gr_kernel, dim3(blocks), dim3(256), 0, stream, gr, a.T, a.B, a.Bp, a.N,
                        a.Np, a.Kp, const_cast<uint4*>(a.ahi), const_cast<uint4*>(a.alo));
-    if (a.meta)
-        hipLaunchKernelGGL(lag_range_kernel, dim3(1), dim3(1024), 0, stream, a.off, a.base, a.N, a.L,
-                           a.s_uniform, const_cast<int*>(a.meta), const_cast<int*>(a.lo));
     hipLaunchKernelGGL(pack_spikes_kernel, dim3(blocks), dim3(256), 0, stream, bits, a.lo, a.T, a.B,
                        a.Bp, a.N, a.Np, a.Kp, const_cast<uint4*>(a.yb));
     const dim3 grid(a.Np / kLT, a.Np / kLT, a.KS);

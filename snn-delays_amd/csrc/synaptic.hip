@@ -10,11 +10,12 @@
 // compaction this replaces). Hybrid delays are read as base[o] + offsets[i,o] (int8)
 // instead of a materialised float (N, N) tensor.
 //
-// Backward (dense, reverse time): lane j owns sources; the future recurrent-input
-// gradients gr[t + l, :] live in an LDS ring, and gfut_j = sum_i W[i,j] sum_l h(l; d_ij)
-// gr[t+l, i] is gathered for every j (reference _ed_bwd_kernel,
-// synaptic_eventdriven.py:323-364). The weight / delay gradients are then formed by the
-// lag-correlation GEMM (gemm.hip).
+// Backward (dense, reverse time): lane j owns sources and gathers
+// gfut_j = sum_i W[i,j] sum_l h(l; d_ij) gr[t+l, i] from a source-major ring of future
+// recurrent-input gradients (reference _ed_bwd_kernel, synaptic_eventdriven.py:323-364).
+// The weight / delay gradients are then formed by the lag-correlation GEMM (lagmm.hip).
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace delrec {
@@ -22,11 +23,6 @@ namespace delrec {
 __device__ __forceinline__ float syn_delay_t(const SynFwd& p, int o, int i) {
     if (p.dt) return p.dt[(size_t)o * p.N + i];
     return p.base[o] + 0.0f + 1.0f * (float)p.offt[(size_t)o * p.N + i];
-}
-
-__device__ __forceinline__ float syn_delay(const SynBwd& p, int i, int j) {
-    if (p.d) return p.d[(size_t)i * p.N + j];
-    return p.base[j] + 0.0f + 1.0f * (float)p.off[(size_t)i * p.N + j];
 }
 
 template <int NPT>
@@ -137,20 +133,38 @@ __global__ void __launch_bounds__(1024) syn_fwd_kernel(SynFwd p) {
     }
 }
 
-template <int NPT>
-__global__ void __launch_bounds__(1024) syn_bwd_kernel(SynBwd p) {
+// Backward scan. Lane j owns source j (NPT sources per lane). The future gr of every
+// receiver i sits in a source-major ring row: ring[i * RP + slot], slot = time mod R, plus
+// KT mirror slots (slot s < KT is also written at R + s) so that a run of KT taps starting
+// at any slot never wraps. Each step every lane walks i = 0 .. N-1 over the same ring row
+// (all lanes gather inside one row), with W^T[j, i..] and d^T[j, i..] (or the int8
+// offsets) streamed in chunks of 16 receivers from blocked copies in which a wave's lanes
+// read adjacent 16-byte runs, one chunk ahead of the gather:
+//   general:  gfut_j = sum_i W_ij sum_{q<KT} max(0, s - |lo_ij + q - c_ij|) gr_i(t + lo_ij + q) / s^2
+//             with c_ij = 1 + d_ij and lo_ij = max(1, ceil(c_ij - s));
+//   hybrid:   the taps of column j are those of c_j = 1 + base_j shifted by the integer
+//             offset, so the KT weights are per-lane constants and a connection only adds
+//             its offset to the slot (int8 offsets, 2 bytes per connection with bf16 W).
+// The ring is in LDS when N * RP floats fit, else in the workspace (one row per receiver,
+// so a step's gathers of all lanes stay within one cache-line run per i).
+template <int NPT, int KT, bool HYB, int MAXT, bool GRING>
+__global__ void __launch_bounds__(MAXT) syn_bwd_kernel(SynBwd p) {
     extern __shared__ float smem[];
-    const int N = p.N, T = p.T, B = p.B, R = p.R, NP = p.NP;
+    constexpr int KA = (HYB && KT > 0) ? KT : 1;        // per-tap accumulators (hybrid, fixed KT)
+    const int N = p.N, T = p.T, B = p.B, R = p.R, RP = p.RP;
+    const int kt = KT > 0 ? KT : p.KT;                  // KT == 0: the tap count is a runtime value
     const int b = blockIdx.x, tid = threadIdx.x, BS = blockDim.x;
-    const bool lds_ring = p.gring == nullptr;
-    float* ring = lds_ring ? smem : p.gring + (size_t)b * R * N;
-    const int pitch = lds_ring ? NP : N;
+    float* ring = GRING ? p.gring + (size_t)b * N * RP : smem;
     const Lif k = p.lif;
     const size_t BN = (size_t)B * N;
+    const bool wbf = p.w_bf16 != 0;
 
     int idx[NPT];
     bool act[NPT];
-    float lam[NPT], m[NPT], s[NPT], dbacc[NPT];
+    float lam[NPT], m[NPT], dbacc[NPT], sv[NPT], is2[NPT], cj[NPT];
+    float hq[NPT][KA];
+    int lob[NPT];
+    bool chk[NPT];
 #pragma unroll
     for (int q = 0; q < NPT; ++q) {
         idx[q] = tid + q * BS;
@@ -159,51 +173,203 @@ __global__ void __launch_bounds__(1024) syn_bwd_kernel(SynBwd p) {
         lam[q] = 0.0f;
         dbacc[q] = 0.0f;
         m[q] = p.drop ? p.drop[(size_t)b * N + jc] : 1.0f;
-        s[q] = p.s ? p.s[jc] : p.s_uniform;
-        for (int r = 0; r < R; ++r)
-            if (act[q]) ring[(size_t)r * pitch + idx[q]] = 0.0f;
+        sv[q] = p.s ? p.s[jc] : p.s_uniform;
+        is2[q] = 1.0f / (sv[q] * sv[q]);
+        lob[q] = 1;
+        chk[q] = false;
+        cj[q] = 0.0f;
+        if (HYB) {
+            // unclamped first lag of the closed support of c_j (a connection adds its offset)
+            const float c = 1.0f + p.base[jc];
+            int lo = (int)ceilf(c - sv[q]);
+            if (fabsf((float)(lo - 1) - c) <= sv[q]) lo -= 1;
+            if (fabsf((float)lo - c) > sv[q]) lo += 1;
+            lob[q] = lo;
+            cj[q] = c;
+#pragma unroll
+            for (int e = 0; e < KA; ++e) hq[q][e] = fmaxf(sv[q] - fabsf((float)(lo + e) - c), 0.0f);
+            // some connection of j reaches a lag <= 0 (the zero offsets of the padded W^T
+            // columns i >= N count too)
+            chk[q] = lo + min(p.meta[1], 0) < 1;
+        }
+        for (int r = 0; r < p.RS; ++r)
+            if (act[q]) ring[(size_t)idx[q] * RP + r] = 0.0f;
     }
+    // lanes whose connections may reach lags <= 0 take the masked gather, wave by wave
+    bool any_chk = false;
+#pragma unroll
+    for (int q = 0; q < NPT; ++q) any_chk = any_chk || chk[q];
+    any_chk = __any(any_chk) != 0;
     __syncthreads();
+
+    float gq[NPT][2], uq[NPT][2];
+#pragma unroll
+    for (int q = 0; q < NPT; ++q)
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const int tt = T - 1 - f;
+            const size_t o = (size_t)(tt >= 0 ? tt : 0) * BN + (size_t)b * N + (act[q] ? idx[q] : 0);
+            gq[q][f] = (act[q] && tt >= 0) ? p.gy[o] : 0.0f;
+            uq[q][f] = (act[q] && tt >= 0) ? p.u[o] : 0.0f;
+        }
 
     int tmod = (T - 1) % R;
     for (int t = T - 1; t >= 0; --t) {
-        float gf[NPT];
+        float acc[NPT][KA];
 #pragma unroll
-        for (int q = 0; q < NPT; ++q) gf[q] = 0.0f;
-        for (int i = 0; i < N; ++i) {
+        for (int q = 0; q < NPT; ++q)
+#pragma unroll
+            for (int e = 0; e < KA; ++e) acc[q][e] = 0.0f;
+
+        // stream the chunks of 16 receivers: W^T (and d^T / offsets^T) of chunk c + 1 are
+        // loaded while chunk c is gathered
+        uint32_t wa[NPT][16], da[NPT][16], wb[NPT][16], db[NPT][16];
+        auto fetch = [&](int c, uint32_t (&cw)[NPT][16], uint32_t (&cd)[NPT][16]) {
 #pragma unroll
             for (int q = 0; q < NPT; ++q) {
-                if (!act[q]) continue;
-                const int j = idx[q];
-                const float w = load_w(p.W, p.w_bf16, (size_t)i * N + j);
-                const float c = 1.0f + syn_delay(p, i, j);
-                const float sv = s[q], s2 = sv * sv;
-                int lo, hi;
-                tap_range(c, sv, p.L, lo, hi);
-                float acc = 0.0f;
-                for (int l = lo; l <= hi && t + l < T; ++l) {
-                    int slot = tmod + l;
-                    if (slot >= R) slot -= R;
-                    acc += tri_weight((float)l, c, sv, s2) * ring[(size_t)slot * pitch + i];
+                const size_t blk = (size_t)c * N + (act[q] ? idx[q] : 0);
+                const int nw = wbf ? 2 : 4;
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    if (h < nw) {
+                        const uint4 v = static_cast<const uint4*>(p.Wt)[blk * nw + h];
+                        cw[q][4 * h] = v.x; cw[q][4 * h + 1] = v.y; cw[q][4 * h + 2] = v.z; cw[q][4 * h + 3] = v.w;
+                    }
                 }
-                gf[q] = fmaf(w, acc, gf[q]);
+                if (HYB) {
+                    const uint4 v = reinterpret_cast<const uint4*>(p.offt)[blk];
+                    cd[q][0] = v.x; cd[q][1] = v.y; cd[q][2] = v.z; cd[q][3] = v.w;
+                } else {
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) {
+                        const uint4 v = reinterpret_cast<const uint4*>(p.dt)[blk * 4 + h];
+                        cd[q][4 * h] = v.x; cd[q][4 * h + 1] = v.y; cd[q][4 * h + 2] = v.z; cd[q][4 * h + 3] = v.w;
+                    }
+                }
+            }
+        };
+        auto gather = [&](int c, const uint32_t (&w32)[NPT][16], const uint32_t (&d32)[NPT][16],
+                          auto checked) {
+            constexpr bool CHK = decltype(checked)::value;
+#pragma unroll
+            for (int q = 0; q < NPT; ++q) {
+                float wf[16];
+                if (wbf) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        wf[e] = __uint_as_float((e & 1) ? (w32[q][e >> 1] & 0xFFFF0000u) : (w32[q][e >> 1] << 16));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) wf[e] = __uint_as_float(w32[q][e]);
+                }
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int i = min(c * 16 + e, N - 1);  // W^T is zero past N
+                    const float* row = ring + (size_t)i * RP;
+                    const float w = wf[e];
+                    if (HYB) {
+                        const int off = ((int)(d32[q][e >> 2] << (24 - 8 * (e & 3)))) >> 24;
+                        const int lag0 = lob[q] + off;
+                        if (!CHK) {                        // every lag lag0 + f >= 1
+                            int slot = tmod + lag0;
+                            slot = slot >= R ? slot - R : slot;
+                            if (KT > 0) {
+#pragma unroll
+                                for (int f = 0; f < KA; ++f) acc[q][f] = fmaf(w, row[slot + f], acc[q][f]);
+                            } else {
+                                float a = 0.0f;
+                                for (int f = 0; f < kt; ++f)
+                                    a = fmaf(fmaxf(sv[q] - fabsf((float)(lob[q] + f) - cj[q]), 0.0f), row[slot + f], a);
+                                acc[q][0] = fmaf(w, a, acc[q][0]);
+                            }
+                        } else if (KT > 0) {
+                            // lags <= 0 do not exist: read a valid slot, weigh it 0
+#pragma unroll
+                            for (int f = 0; f < KA; ++f) {
+                                int slot = tmod + max(lag0 + f, 1);
+                                slot = slot >= R ? slot - R : slot;
+                                const float g = row[slot];
+                                acc[q][f] = fmaf(w, (lag0 + f >= 1) ? g : 0.0f, acc[q][f]);
+                            }
+                        } else {
+                            float a = 0.0f;
+                            for (int f = 0; f < kt; ++f) {
+                                int slot = tmod + max(lag0 + f, 1);
+                                slot = slot >= R ? slot - R : slot;
+                                const float g = row[slot];
+                                a = fmaf(fmaxf(sv[q] - fabsf((float)(lob[q] + f) - cj[q]), 0.0f),
+                                         (lag0 + f >= 1) ? g : 0.0f, a);
+                            }
+                            acc[q][0] = fmaf(w, a, acc[q][0]);
+                        }
+                    } else {
+                        const float c1 = 1.0f + __uint_as_float(d32[q][e]);
+                        const int lo = max(1, (int)ceilf(c1 - sv[q]));
+                        int slot = tmod + lo;
+                        slot = slot >= R ? slot - R : slot;
+                        const float x0 = (float)lo - c1;
+                        float a = 0.0f;
+                        if (KT > 0) {
+#pragma unroll
+                            for (int f = 0; f < (KT > 0 ? KT : 1); ++f)
+                                a = fmaf(fmaxf(sv[q] - fabsf(x0 + (float)f), 0.0f), row[slot + f], a);
+                        } else {
+                            for (int f = 0; f < kt; ++f)
+                                a = fmaf(fmaxf(sv[q] - fabsf(x0 + (float)f), 0.0f), row[slot + f], a);
+                        }
+                        acc[q][0] = fmaf(w, a, acc[q][0]);
+                    }
+                }
+            }
+        };
+        auto gather_any = [&](int c, const uint32_t (&w32)[NPT][16], const uint32_t (&d32)[NPT][16]) {
+            if (HYB && any_chk) gather(c, w32, d32, std::true_type{});
+            else gather(c, w32, d32, std::false_type{});
+        };
+        // chunks of 16 receivers, ping-ponged between two register buffers: chunk c + 1 is
+        // loaded while chunk c is gathered
+        const int NC = (N + 15) >> 4;
+        fetch(0, wa, da);
+        for (int c = 0; c < NC; c += 2) {
+            if (c + 1 < NC) fetch(c + 1, wb, db);
+            gather_any(c, wa, da);
+            if (c + 1 < NC) {
+                if (c + 2 < NC) fetch(c + 2, wa, da);
+                gather_any(c + 1, wb, db);
             }
         }
+
 #pragma unroll
         for (int q = 0; q < NPT; ++q) {
+            float gf = 0.0f;
+            if (HYB && KT > 0) {
+#pragma unroll
+                for (int f = 0; f < KA; ++f) gf = fmaf(hq[q][f], acc[q][f], gf);
+            } else {
+                gf = acc[q][0];
+            }
+            gf *= is2[q];
+            const float gyv = gq[q][0], u = uq[q][0];
+            gq[q][0] = gq[q][1];
+            uq[q][0] = uq[q][1];
+            const int tn = t - 2;
+            const size_t on = (size_t)(tn >= 0 ? tn : 0) * BN + (size_t)b * N + (act[q] ? idx[q] : 0);
+            gq[q][1] = (act[q] && tn >= 0) ? p.gy[on] : 0.0f;
+            uq[q][1] = (act[q] && tn >= 0) ? p.u[on] : 0.0f;
             if (!act[q]) continue;
             const int j = idx[q];
             const size_t o = (size_t)t * BN + (size_t)b * N + j;
-            const float u = p.u[o];
             const float y = lif_fire(k, u);
-            const float du = lif_backward(k, p.gy[o] + gf[q], u, y, lam[q]);
+            const float du = lif_backward(k, gyv + gf, u, y, lam[q]);
             lam[q] = k.decay * du;
             const float da = lif_dx(k, du);
             const float gr = da * m[q];
             p.dx[o] = da;
             p.gr[o] = gr;
             dbacc[q] += gr;
-            ring[(size_t)tmod * pitch + j] = gr;
+            float* row = ring + (size_t)j * RP;
+            row[tmod] = gr;
+            if (tmod < kt) row[tmod + R] = gr;
         }
         __syncthreads();
         tmod = tmod == 0 ? R - 1 : tmod - 1;
@@ -227,18 +393,45 @@ void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream) 
     }
 }
 
-void launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream) {
-    const int npt = (a.N + block - 1) / block;
-    if (npt == 1) {
-        (void)hipFuncSetAttribute((const void*)syn_bwd_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(syn_bwd_kernel<1>, dim3(a.B), dim3(block), lds, stream, a);
-    } else if (npt == 2) {
-        (void)hipFuncSetAttribute((const void*)syn_bwd_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(syn_bwd_kernel<2>, dim3(a.B), dim3(block), lds, stream, a);
+template <int NPT, int KT, bool HYB, int MAXT>
+void launch_syn_bwd_k(const SynBwd& a, int block, size_t lds, hipStream_t stream) {
+    if (a.gring) {
+        hipLaunchKernelGGL((syn_bwd_kernel<NPT, KT, HYB, MAXT, true>), dim3(a.B), dim3(block), 0, stream, a);
     } else {
-        (void)hipFuncSetAttribute((const void*)syn_bwd_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(syn_bwd_kernel<4>, dim3(a.B), dim3(block), lds, stream, a);
+        (void)hipFuncSetAttribute((const void*)syn_bwd_kernel<NPT, KT, HYB, MAXT, false>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipLaunchKernelGGL((syn_bwd_kernel<NPT, KT, HYB, MAXT, false>), dim3(a.B), dim3(block), lds, stream, a);
     }
+}
+
+// tap runs compiled for fixed lengths; other lengths take the runtime-count variant (KT = 0)
+template <int NPT, bool HYB, int MAXT>
+void launch_syn_bwd_kt(const SynBwd& a, int block, size_t lds, hipStream_t stream) {
+    if (HYB && a.KT == 2) launch_syn_bwd_k<NPT, 2, HYB, MAXT>(a, block, lds, stream);
+    else if (a.KT == 4) launch_syn_bwd_k<NPT, 4, HYB, MAXT>(a, block, lds, stream);
+    else if (!HYB && a.KT == 8) launch_syn_bwd_k<NPT, 8, HYB, MAXT>(a, block, lds, stream);
+    else if (!HYB && a.KT == 12) launch_syn_bwd_k<NPT, 12, HYB, MAXT>(a, block, lds, stream);
+    else launch_syn_bwd_k<NPT, 0, HYB, MAXT>(a, block, lds, stream);
+}
+
+// blocks of up to 512 threads get the 256-VGPR variants (two waves per SIMD)
+bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream) {
+    const int npt = (a.N + block - 1) / block;
+    const bool hyb = a.offt != nullptr;
+    if (npt == 1 && block <= 512) {
+        if (hyb) launch_syn_bwd_kt<1, true, 512>(a, block, lds, stream);
+        else launch_syn_bwd_kt<1, false, 512>(a, block, lds, stream);
+    } else if (npt == 1) {
+        if (hyb) launch_syn_bwd_kt<1, true, 1024>(a, block, lds, stream);
+        else launch_syn_bwd_kt<1, false, 1024>(a, block, lds, stream);
+    } else if (npt == 2) {
+        if (hyb) launch_syn_bwd_kt<2, true, 1024>(a, block, lds, stream);
+        else launch_syn_bwd_kt<2, false, 1024>(a, block, lds, stream);
+    } else {
+        if (hyb) launch_syn_bwd_kt<4, true, 1024>(a, block, lds, stream);
+        else launch_syn_bwd_kt<4, false, 1024>(a, block, lds, stream);
+    }
+    return true;
 }
 
 // ---------------------------------------------------------------------------------------

@@ -75,7 +75,7 @@ class SynBwdArgs(ctypes.Structure):
     _fields_ = [('T', c_i32), ('B', c_i32), ('N', c_i32), ('L', c_i32),
                 ('gy', c_vp), ('u', c_vp), ('y', c_vp), ('bits', c_vp), ('W', c_vp),
                 ('w_bf16', c_i32), ('d', c_vp), ('base', c_vp), ('offsets', c_vp), ('s', c_vp),
-                ('s_uniform', c_f32), ('drop', c_vp), ('lif', Lif),
+                ('s_uniform', c_f32), ('s_max', c_f32), ('drop', c_vp), ('lif', Lif),
                 ('dx', c_vp), ('dW', c_vp), ('dd', c_vp), ('ds', c_vp), ('db', c_vp),
                 ('workspace', c_vp), ('workspace_bytes', c_size)]
 

@@ -27,7 +27,7 @@ def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop,
     """Launch ``delrec_syn_fwd`` with per-connection delays ``d_eff`` (N, N), or with the
     hybrid ``base`` (N) + int8 ``offsets`` (N, N) when ``d_eff`` is None; ``d_all`` is a
     device tensor holding every effective delay (for the window length). Returns
-    ``(y, u, bits, L, Wc, w_bf16)``."""
+    ``(y, u, bits, L, Wc, w_bf16, s_max)``."""
     require_device(x)
     T, B, N = x.shape
     dev = x.device
@@ -51,11 +51,11 @@ def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop,
         s_uniform=float(s_uniform), drop=_lib.ptr(drop), lif=lif, y=_lib.ptr(y), u=_lib.ptr(u),
         bits=_lib.ptr(bits), workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
     _lib.call('delrec_syn_fwd', args, _lib.stream_of(xc))
-    return y, u, bits, L, Wc, w_bf16
+    return y, u, bits, L, Wc, w_bf16, float(s_max)
 
 
-def syn_backward(gy, u, y, bits, Wc, w_bf16, d_eff, base, offsets, s_vec, s_uniform, drop, lif, L,
-                 need_W, need_d, need_s, need_b):
+def syn_backward(gy, u, y, bits, Wc, w_bf16, d_eff, base, offsets, s_vec, s_uniform, s_max, drop, lif,
+                 L, need_W, need_d, need_s, need_b):
     """Launch ``delrec_syn_bwd``. Returns ``(dx, dW, dd, ds, db)`` (``None`` where not
     requested)."""
     T, B, N = u.shape
@@ -70,8 +70,8 @@ def syn_backward(gy, u, y, bits, Wc, w_bf16, d_eff, base, offsets, s_vec, s_unif
     args = _lib.SynBwdArgs(
         T=T, B=B, N=N, L=L, gy=_lib.ptr(gy), u=_lib.ptr(u), y=_lib.ptr(y), bits=_lib.ptr(bits),
         W=_lib.ptr(Wc), w_bf16=w_bf16, d=_lib.ptr(d_eff), base=_lib.ptr(base),
-        offsets=_lib.ptr(offsets), s=_lib.ptr(s_vec), s_uniform=float(s_uniform), drop=_lib.ptr(drop),
-        lif=lif, dx=_lib.ptr(dx), dW=_lib.ptr(dW), dd=_lib.ptr(dd), ds=_lib.ptr(ds), db=_lib.ptr(db),
+        offsets=_lib.ptr(offsets), s=_lib.ptr(s_vec), s_uniform=float(s_uniform), s_max=float(s_max),
+        drop=_lib.ptr(drop), lif=lif, dx=_lib.ptr(dx), dW=_lib.ptr(dW), dd=_lib.ptr(dd), ds=_lib.ptr(ds), db=_lib.ptr(db),
         workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
     _lib.call('delrec_syn_bwd', args, _lib.stream_of(gy))
     return dx, dW, dd, ds, db
@@ -93,21 +93,21 @@ class EventDrivenSyn(torch.autograd.Function):
         m = drop_bn(drop, T, B, N)
         bc = None if bias is None else bias.detach().to(torch.float32).contiguous()
         lif = layer_lif(layer)
-        y, u, bits, L, Wc, w_bf16 = syn_forward(x, W, d_eff, None, None, s_vec, s_uniform, d_eff,
-                                                bc, m, lif)
+        y, u, bits, L, Wc, w_bf16, s_max = syn_forward(x, W, d_eff, None, None, s_vec, s_uniform, d_eff,
+                                                       bc, m, lif)
         ctx.save_for_backward(u, y, bits, Wc, d_eff, s_vec, m, p_spread)
-        ctx.meta = (L, w_bf16, s_uniform, float(layer.sigma), bool(layer.use_sig_p), bias is not None,
-                    W.dtype)
+        ctx.meta = (L, w_bf16, s_uniform, s_max, float(layer.sigma), bool(layer.use_sig_p),
+                    bias is not None, W.dtype)
         ctx.lif = lif
         return y
 
     @staticmethod
     def backward(ctx, gy):
         u, y, bits, Wc, d_eff, s_vec, m, p_spread = ctx.saved_tensors
-        L, w_bf16, s_uniform, sigma, use_sig_p, use_bias, w_dtype = ctx.meta
+        L, w_bf16, s_uniform, s_max, sigma, use_sig_p, use_bias, w_dtype = ctx.meta
         need_p = use_sig_p and ctx.needs_input_grad[3]
         dx, dW, dd, ds, db = syn_backward(
-            gy, u, y, bits, Wc, w_bf16, d_eff, None, None, s_vec, s_uniform, m, ctx.lif, L,
+            gy, u, y, bits, Wc, w_bf16, d_eff, None, None, s_vec, s_uniform, s_max, m, ctx.lif, L,
             ctx.needs_input_grad[1], ctx.needs_input_grad[2], need_p,
             use_bias and ctx.needs_input_grad[4])
         dp = None

@@ -72,7 +72,7 @@ class HybridSynDelay(torch.autograd.Function):
         bc = None if bias is None else bias.detach().to(torch.float32).contiguous()
         lif = layer_lif(layer)
         d_arg = None if base is not None else d_eff
-        y, u, bits, L, Wc, w_bf16 = syn_forward(x, W, d_arg, base, off8, None, s, d_eff, bc, m, lif)
+        y, u, bits, L, Wc, w_bf16, _ = syn_forward(x, W, d_arg, base, off8, None, s, d_eff, bc, m, lif)
         ctx.save_for_backward(u, y, bits, Wc, d_arg, base, off8, m)
         ctx.meta = (L, w_bf16, s, bias is not None, W.dtype)
         ctx.lif = lif
@@ -83,7 +83,7 @@ class HybridSynDelay(torch.autograd.Function):
         u, y, bits, Wc, d_arg, base, off8, m = ctx.saved_tensors
         L, w_bf16, s, use_bias, w_dtype = ctx.meta
         dx, dW, dd, _, db = syn_backward(
-            gy, u, y, bits, Wc, w_bf16, d_arg, base, off8, None, s, m, ctx.lif, L,
+            gy, u, y, bits, Wc, w_bf16, d_arg, base, off8, None, s, s, m, ctx.lif, L,
             ctx.needs_input_grad[1], ctx.needs_input_grad[2], False,
             use_bias and ctx.needs_input_grad[3])
         if dW is not None and w_dtype != torch.float32:

@@ -16,6 +16,8 @@ SYN_CASES = [
     (16, 2, 48, 6.0, 0.8, {'soft': True, 'triangle': True}),
     (16, 2, 48, 6.0, 0.8, {'decay_input': True}),
     (12, 2, 96, 4.0, 4.0, {}),                  # wide triangle
+    (12, 2, 40, 6.0, 8.0, {}),                  # half-width 9: runtime tap count
+    (70, 2, 600, 60.0, 1.0, {}),                # backward ring too large for LDS: workspace ring
 ]
 
 
@@ -91,10 +93,12 @@ def test_synaptic_fwd_bwd_matches_oracle(dev, case):
 
 
 HYB_CASES = [
-    # T, B, N, base range (lo, hi), max offset, bf16 weights
-    (20, 3, 32, (0.0, 8.0), 4, False),
-    (20, 3, 64, (-2.0, 6.0), 4, False),          # centred base: negative effective delays
-    (16, 2, 48, (0.0, 10.0), 8, True),           # bf16 W_rec, fp32 state
+    # T, B, N, base range (lo, hi), max offset, bf16 weights, sigma
+    (20, 3, 32, (0.0, 8.0), 4, False, 0.0),
+    (20, 3, 64, (-2.0, 6.0), 4, False, 0.0),     # centred base: negative effective delays
+    (16, 2, 48, (0.0, 10.0), 8, True, 0.0),      # bf16 W_rec, fp32 state
+    (16, 2, 40, (-1.0, 7.0), 3, False, 0.7),     # mid-anneal triangle, four taps per column
+    (12, 2, 32, (0.0, 6.0), 3, False, 8.0),      # half-width 9: runtime tap count
 ]
 
 
@@ -122,12 +126,12 @@ def hybrid_layer(N, W, base, offsets, dev, bf16=False, **cfg_kw):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('case', HYB_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}{"bf16" if c[5] else ""}'
+@pytest.mark.parametrize('case', HYB_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}{"bf16" if c[5] else ""}s{c[6]}'
                                                 for c in HYB_CASES])
 def test_hybrid_fwd_bwd_matches_oracle(dev, case):
     """Hybrid delays through the base + int8-offset kernel path of a parametrised layer."""
     import delrec.kernels.synaptic_hybrid as sh
-    T, B, N, (lo, hi), K, bf16 = case
+    T, B, N, (lo, hi), K, bf16, sigma = case
     print(f'case {case}', flush=True)
     g = gen(2)
     x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
@@ -138,9 +142,10 @@ def test_hybrid_fwd_bwd_matches_oracle(dev, case):
     offsets = torch.randint(K + 1, (N, N), generator=g).float()
     gy = torch.randn(T, B, N, generator=g)
     lif = lif_params()
-    y_ref, u_ref, gref = oracle_synaptic(x, W, None, lif, 0.0, gy, base=base, offsets=offsets)
+    y_ref, u_ref, gref = oracle_synaptic(x, W, None, lif, sigma, gy, base=base, offsets=offsets)
 
-    layer = hybrid_layer(N, W, base, offsets, dev, bf16=bf16)
+    layer = hybrid_layer(N, W, base, offsets, dev, bf16=bf16, sigma_init=sigma)
+    assert layer.sigma == sigma
     base8, _ = sh._int8_offsets(layer)
     assert base8 is not None, 'the base + int8 offsets path was not taken'
     xg = x.to(dev).requires_grad_(True)
