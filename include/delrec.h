@@ -130,6 +130,7 @@ typedef struct {
     const int8_t* offsets;       /* (N,N) hybrid integer offsets, offsets[i*N+j]         */
     const float* s;              /* (N) per-source half-width or NULL                    */
     float s_uniform;
+    float s_max;                 /* largest half-width: max of s[], or s_uniform           */
     const float* drop;           /* (B,N) or NULL                                        */
     delrec_lif lif;
     float* y;

@@ -226,11 +226,16 @@ LagPack lag_pack(int T, int B, int N) {
     return q;
 }
 
+// the forward's gather form: history words of 64 lags and the window of one connection
+int syn_gather_words(int L) { return L - 1 <= 64 ? 1 : (L - 1 <= 128 ? 2 : 0); }
+int syn_gather_taps(float s_max) { return (int)std::floor(2.0f * s_max) + 2; }
+
 template <class C>
 void syn_fwd_ws(C& c, int B, int N, int L, bool hybrid, bool bf16) {
     const SynLayout lay = syn_layout(N, L, true);
-    if (bf16) c.template take<uint16_t>((size_t)N * N); else c.template take<float>((size_t)N * N);
-    if (hybrid) c.template take<int8_t>((size_t)N * N); else c.template take<float>((size_t)N * N);
+    const size_t nb = (size_t)((N + 15) / 16) * 16 * N;   // blocked copies
+    if (bf16) c.template take<uint16_t>(nb); else c.template take<float>(nb);
+    if (hybrid) c.template take<int8_t>(nb); else c.template take<float>(nb);
     if (!lay.lds_ring) c.template take<float>((size_t)B * lay.R * N);
 }
 
@@ -268,33 +273,35 @@ __global__ void transpose_kernel(const E* __restrict__ in, E* __restrict__ out, 
     }
 }
 
-// Blocked transpose for per-lane streaming: lane j reads 16 consecutive i of column j of
-// an (n, n) row-major matrix as one contiguous run of 16 elements, and a wave's lanes read
-// adjacent runs: out[((i / 16) * n + j) * 16 + i % 16] = in[i * n + j], zero for i >= n
-// (the chunks cover nc = ceil(n / 16) * 16 rows).
-template <class E>
-__global__ void block_transpose_kernel(const E* __restrict__ in, E* __restrict__ out, int n) {
+// Blocked copies for per-lane streaming of an (n, n) row-major matrix in runs of 16:
+//   columns (ROWS = false): lane j reads i = 16c .. 16c+15 of column j,
+//       out[((i / 16) * n + j) * 16 + i % 16] = in[i * n + j];
+//   rows (ROWS = true): lane i reads j = 16c .. 16c+15 of row i,
+//       out[((j / 16) * n + i) * 16 + j % 16] = in[i * n + j];
+// a wave's lanes read adjacent runs; entries past n are zero (ceil(n / 16) runs per lane).
+template <class E, bool ROWS>
+__global__ void block_copy_kernel(const E* __restrict__ in, E* __restrict__ out, int n) {
     const int nc = (n + 15) / 16;
     const size_t total = (size_t)nc * n;
     for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total;
          q += (size_t)gridDim.x * blockDim.x) {
-        const int c = (int)(q / n), j = (int)(q - (size_t)c * n);
+        const int c = (int)(q / n), lane = (int)(q - (size_t)c * n);
         E v[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const int i = c * 16 + e;
-            v[e] = i < n ? in[(size_t)i * n + j] : E(0);
+            const int k = c * 16 + e;
+            v[e] = k < n ? (ROWS ? in[(size_t)lane * n + k] : in[(size_t)k * n + lane]) : E(0);
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) out[q * 16 + e] = v[e];
     }
 }
 
-template <class E>
+template <class E, bool ROWS = false>
 void block_transpose(const void* in, void* out, int n, hipStream_t s) {
     const size_t total = (size_t)((n + 15) / 16) * n;
     const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 65535);
-    hipLaunchKernelGGL(block_transpose_kernel<E>, dim3(blocks), dim3(256), 0, s,
+    hipLaunchKernelGGL((block_copy_kernel<E, ROWS>), dim3(blocks), dim3(256), 0, s,
                        static_cast<const E*>(in), static_cast<E*>(out), n);
 }
 
@@ -466,23 +473,44 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     const SynLayout lay = syn_layout(a->N, a->L, true);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int N = a->N;
+    const size_t nb = (size_t)((N + 15) / 16) * 16 * N;
     Carver cv(a->workspace, a->workspace_bytes);
-    void* wt = a->w_bf16 ? (void*)cv.take<uint16_t>((size_t)N * N) : (void*)cv.take<float>((size_t)N * N);
-    void* dt = hybrid ? (void*)cv.take<int8_t>((size_t)N * N) : (void*)cv.take<float>((size_t)N * N);
+    void* wt = a->w_bf16 ? (void*)cv.take<uint16_t>(nb) : (void*)cv.take<float>(nb);
+    void* dt = hybrid ? (void*)cv.take<int8_t>(nb) : (void*)cv.take<float>(nb);
     float* gring = lay.lds_ring ? nullptr : cv.take<float>((size_t)a->B * lay.R * N);
     if (!wt || !dt || (!lay.lds_ring && !gring)) return DELREC_ERR_WORKSPACE;
-    if (a->w_bf16) transpose<uint16_t>(a->W, wt, N, s); else transpose<float>(a->W, wt, N, s);
-    if (hybrid) transpose<int8_t>(a->offsets, dt, N, s); else transpose<float>(a->d, dt, N, s);
 
     SynFwd p{};
     p.T = a->T; p.B = a->B; p.N = N; p.L = a->L; p.R = lay.R; p.NP = lay.NP; p.NF = lay.NF;
-    p.x = a->x; p.Wt = wt; p.w_bf16 = a->w_bf16; p.bias = a->bias;
-    p.dt = hybrid ? nullptr : static_cast<const float*>(dt);
-    p.base = a->base; p.offt = hybrid ? static_cast<const int8_t*>(dt) : nullptr;
+    p.x = a->x; p.w_bf16 = a->w_bf16; p.bias = a->bias;
+    p.base = a->base;
     p.s = a->s; p.s_uniform = a->s_uniform; p.drop = a->drop; p.lif = make_lif(a->lif);
-    p.y = a->y; p.u = a->u; p.bits = a->bits; p.gring = gring;
+    p.y = a->y; p.u = a->u; p.bits = a->bits;
+    // a ring that fits LDS takes the event-driven scatter; otherwise the gather form reads
+    // spike-history words (windows of up to 128 lags and 32 taps), else the workspace ring
+    const int hw = syn_gather_words(a->L);
+    const int kt = syn_gather_taps(a->s ? a->s_max : std::max(a->s_max, a->s_uniform));
+    const bool gather = !lay.lds_ring && hw > 0 && kt <= 32;
+    size_t lds = lay.lds;
+    if (gather) {
+        if (a->w_bf16) block_transpose<uint16_t, true>(a->W, wt, N, s); else block_transpose<float, true>(a->W, wt, N, s);
+        if (hybrid) block_transpose<int8_t, true>(a->offsets, dt, N, s); else block_transpose<float, true>(a->d, dt, N, s);
+        p.Wr = wt;
+        p.dr = hybrid ? nullptr : static_cast<const float*>(dt);
+        p.offr = hybrid ? static_cast<const int8_t*>(dt) : nullptr;
+        p.HW = hw;
+        p.KT = kt;
+        lds = (size_t)2 * hw * N * sizeof(uint64_t) + (size_t)2 * N * sizeof(float);
+    } else {
+        if (a->w_bf16) transpose<uint16_t>(a->W, wt, N, s); else transpose<float>(a->W, wt, N, s);
+        if (hybrid) transpose<int8_t>(a->offsets, dt, N, s); else transpose<float>(a->d, dt, N, s);
+        p.Wt = wt;
+        p.dt = hybrid ? nullptr : static_cast<const float*>(dt);
+        p.offt = hybrid ? static_cast<const int8_t*>(dt) : nullptr;
+        p.gring = gring;
+    }
     const bool timed = scan_begin(DELREC_WS_SYN_FWD, s);
-    launch_syn_fwd(p, lay.block, lay.lds, s);
+    launch_syn_fwd(p, lay.block, lds, s);
     scan_end(timed, s);
     return finish_launch();
 }
@@ -495,7 +523,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     if (hybrid && (!a->base || !a->offsets)) return DELREC_ERR_ARG;
     if (hybrid && a->s) return DELREC_ERR_UNSUPPORTED;     // the hybrid has one uniform half-width
     if (a->N > 4096) return DELREC_ERR_UNSUPPORTED;
-    const int KT = syn_taps(hybrid ? a->s_uniform : a->s_max, hybrid);
+    const int KT = syn_taps(hybrid ? a->s_uniform : (a->s ? a->s_max : std::max(a->s_max, a->s_uniform)), hybrid);
     if (KT == 0) return DELREC_ERR_UNSUPPORTED;             // half-width beyond the widest tap run
     const SynBwdLayout lay = syn_bwd_layout(a->N, a->L, KT);
     const SynBwdLayout wlay = syn_bwd_layout(a->N, a->L, kSynMaxTaps);

@@ -65,6 +65,12 @@ struct SynFwd {
     float* u;
     uint32_t* bits;
     float* gring;               // global ring [B][R][N] when the ring does not fit LDS, else NULL
+    // gather form (rings too large for LDS): W / d / offsets in row-blocked copies,
+    // W[i][j] at ((j/16)*N + i)*16 + j%16; HW history words, KT taps per window
+    int HW, KT;
+    const void* Wr;
+    const float* dr;
+    const int8_t* offr;
 };
 
 struct SynBwd {

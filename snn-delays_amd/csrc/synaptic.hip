@@ -25,16 +25,15 @@ __device__ __forceinline__ float syn_delay_t(const SynFwd& p, int o, int i) {
     return p.base[o] + 0.0f + 1.0f * (float)p.offt[(size_t)o * p.N + i];
 }
 
-template <int NPT>
+template <int NPT, bool GRING>
 __global__ void __launch_bounds__(1024) syn_fwd_kernel(SynFwd p) {
     extern __shared__ float smem[];
     const int N = p.N, T = p.T, B = p.B, R = p.R, NP = p.NP;
     const int b = blockIdx.x, tid = threadIdx.x, BS = blockDim.x;
     const int lane = tid & 63, wave = tid >> 6, nwaves = BS >> 6;
-    const bool lds_ring = p.gring == nullptr;
-    float* ring = lds_ring ? smem : p.gring + (size_t)b * R * N;
-    const int pitch = lds_ring ? NP : N;
-    int* fired = reinterpret_cast<int*>(smem + (lds_ring ? (size_t)R * NP : 0));
+    float* ring = GRING ? p.gring + (size_t)b * R * N : smem;
+    const int pitch = GRING ? N : NP;
+    int* fired = reinterpret_cast<int*>(smem + (GRING ? 0 : (size_t)R * NP));
     int* wcnt = fired + p.NF;
     const Lif k = p.lif;
     const int TW = (T + 31) >> 5;
@@ -60,6 +59,17 @@ __global__ void __launch_bounds__(1024) syn_fwd_kernel(SynFwd p) {
             if (act[q]) ring[(size_t)r * pitch + idx[q]] = 0.0f;
     }
     __syncthreads();
+
+    // the per-connection data of a fired source o for this lane's receivers
+    auto load_src = [&](int o, float (&w)[NPT], float (&dl)[NPT]) {
+#pragma unroll
+        for (int q = 0; q < NPT; ++q) {
+            const int i = act[q] ? idx[q] : 0;
+            w[q] = load_w(p.Wt, p.w_bf16, (size_t)o * N + i);
+            dl[q] = p.dt ? p.dt[(size_t)o * N + i]
+                         : p.base[o] + 0.0f + 1.0f * (float)p.offt[(size_t)o * N + i];
+        }
+    };
 
     int tmod = 0;
     for (int t = 0; t < T; ++t) {
@@ -106,30 +116,227 @@ __global__ void __launch_bounds__(1024) syn_fwd_kernel(SynFwd p) {
             }
         }
         __syncthreads();
-        // scatter the fired sources into the ring (lags >= 1: slot (t + l) mod R)
+        // scatter the fired sources into the ring (lags >= 1: slot (t + l) mod R); the next
+        // source's weights and delays load while this one is scattered, and the taps of a
+        // source are read and written four at a time
+        float wn[NPT], dn[NPT];
+        int on = 0;
+        if (nf > 0) {
+            on = fired[0];
+            load_src(on, wn, dn);
+        }
         for (int f = 0; f < nf; ++f) {
-            const int o = fired[f];
+            const int o = on;
+            float w[NPT], dl[NPT];
+#pragma unroll
+            for (int q = 0; q < NPT; ++q) {
+                w[q] = wn[q];
+                dl[q] = dn[q];
+            }
+            if (f + 1 < nf) {
+                on = fired[f + 1];
+                load_src(on, wn, dn);
+            }
             const float so = p.s ? p.s[o] : p.s_uniform;
-            const float s2 = so * so;
+            const float is2 = 1.0f / (so * so);
 #pragma unroll
             for (int q = 0; q < NPT; ++q) {
                 if (!act[q]) continue;
                 const int i = idx[q];
-                const float w = load_w(p.Wt, p.w_bf16, (size_t)o * N + i);
-                const float c = 1.0f + syn_delay_t(p, o, i);
+                const float c = 1.0f + dl[q];
                 int lo, hi;
                 tap_range(c, so, p.L, lo, hi);
-                for (int l = lo; l <= hi; ++l) {
-                    const float h = tri_weight((float)l, c, so, s2);
-                    if (h == 0.0f) continue;
-                    int slot = tmod + l;
-                    if (slot >= R) slot -= R;
-                    float* cell = ring + (size_t)slot * pitch + i;
-                    *cell = *cell + w * h;
+                const float wq = w[q] * is2;
+                for (int l0 = lo; l0 <= hi; l0 += 4) {
+                    float* cell[4];
+                    float old[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        int slot = tmod + min(l0 + e, hi);
+                        slot = slot >= R ? slot - R : slot;
+                        cell[e] = ring + (size_t)slot * pitch + i;
+                        old[e] = *cell[e];
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int l = l0 + e;
+                        if (l <= hi) *cell[e] = old[e] + wq * fmaxf(so - fabsf((float)l - c), 0.0f);
+                    }
                 }
             }
         }
         tmod = tmod + 1 == R ? 0 : tmod + 1;
+    }
+}
+
+// Forward in gather form, for rings too large for LDS: lane i owns receiver i and sums
+//   rec_i(t) = sum_j W_ij sum_l max(0, s_j - |l - c_ij|) / s_j^2 * y_j(t - l),  c_ij = 1 + d_ij,
+// over every source each step. The spike history of each source is a bit word in LDS
+// (bit l-1 = y_j(t - l), HW words of 64 lags, double-buffered so one barrier per step
+// suffices); a connection reads the KT bits from its first lag lo_ij = max(1, ceil(c_ij - s_j))
+// and adds the weight of each set bit. W and d (or the int8 offsets) stream in row-blocked
+// chunks of 16 sources, one chunk ahead; sources silent for the whole window are skipped by
+// the wave (the history word is wave-uniform).
+template <int HW>
+__device__ __forceinline__ uint32_t hist_window(const uint64_t (&h)[HW], int sh) {
+    if (HW == 1) return (uint32_t)(h[0] >> sh);
+    const uint64_t lo64 = sh < 64 ? (h[0] >> sh) | (sh ? h[HW - 1] << (64 - sh) : 0ull) : (h[HW - 1] >> (sh - 64));
+    return (uint32_t)lo64;
+}
+
+template <int NPT, bool HYB, int HW>
+__global__ void __launch_bounds__(1024) syn_fwd_gather_kernel(SynFwd p) {
+    extern __shared__ float smem[];
+    const int N = p.N, T = p.T, B = p.B;
+    const int b = blockIdx.x, tid = threadIdx.x, BS = blockDim.x;
+    uint64_t* hist = reinterpret_cast<uint64_t*>(smem);          // [2][HW][N]
+    float* s_l = reinterpret_cast<float*>(hist + (size_t)2 * HW * N);
+    float* base_l = s_l + N;
+    const Lif k = p.lif;
+    const int TW = (T + 31) >> 5;
+    const size_t BN = (size_t)B * N;
+    const uint32_t wmask = p.KT >= 32 ? 0xFFFFFFFFu : ((1u << p.KT) - 1u);
+    const bool wbf = p.w_bf16 != 0;
+
+    int idx[NPT];
+    bool act[NPT];
+    float v[NPT], m[NPT], bias[NPT], xq0[NPT], xq1[NPT];
+    uint32_t word[NPT];
+#pragma unroll
+    for (int q = 0; q < NPT; ++q) {
+        idx[q] = tid + q * BS;
+        act[q] = idx[q] < N;
+        const int ic = act[q] ? idx[q] : 0;
+        v[q] = k.v0;
+        m[q] = p.drop ? p.drop[(size_t)b * N + ic] : 1.0f;
+        bias[q] = p.bias ? p.bias[ic] : 0.0f;
+        const size_t row = (size_t)b * N + ic;
+        xq0[q] = act[q] ? p.x[row] : 0.0f;
+        xq1[q] = (act[q] && T > 1) ? p.x[BN + row] : 0.0f;
+        word[q] = 0;
+    }
+    for (int j = tid; j < N; j += BS) {
+#pragma unroll
+        for (int w = 0; w < 2 * HW; ++w) hist[(size_t)w * N + j] = 0ull;
+        s_l[j] = p.s ? p.s[j] : p.s_uniform;
+        base_l[j] = HYB ? p.base[j] : 0.0f;
+    }
+    __syncthreads();
+
+    const int NC = (N + 15) >> 4;
+    uint32_t wa[NPT][16], da[NPT][16], wb2[NPT][16], db2[NPT][16];
+    auto fetch = [&](int c, uint32_t (&cw)[NPT][16], uint32_t (&cd)[NPT][16]) {
+#pragma unroll
+        for (int q = 0; q < NPT; ++q) {
+            const size_t blk = (size_t)c * N + (act[q] ? idx[q] : 0);
+            const int nw = wbf ? 2 : 4;
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                if (h < nw) {
+                    const uint4 x4 = static_cast<const uint4*>(p.Wr)[blk * nw + h];
+                    cw[q][4 * h] = x4.x; cw[q][4 * h + 1] = x4.y; cw[q][4 * h + 2] = x4.z; cw[q][4 * h + 3] = x4.w;
+                }
+            }
+            if (HYB) {
+                const uint4 x4 = reinterpret_cast<const uint4*>(p.offr)[blk];
+                cd[q][0] = x4.x; cd[q][1] = x4.y; cd[q][2] = x4.z; cd[q][3] = x4.w;
+            } else {
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const uint4 x4 = reinterpret_cast<const uint4*>(p.dr)[blk * 4 + h];
+                    cd[q][4 * h] = x4.x; cd[q][4 * h + 1] = x4.y; cd[q][4 * h + 2] = x4.z; cd[q][4 * h + 3] = x4.w;
+                }
+            }
+        }
+    };
+
+    for (int t = 0; t < T; ++t) {
+        const uint64_t* hc = hist + (size_t)(t & 1) * HW * N;          // history through t - 1
+        uint64_t* hn = hist + (size_t)((t + 1) & 1) * HW * N;
+        float acc[NPT];
+#pragma unroll
+        for (int q = 0; q < NPT; ++q) acc[q] = 0.0f;
+
+        auto gather = [&](int c, const uint32_t (&w32)[NPT][16], const uint32_t (&d32)[NPT][16]) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int j = c * 16 + e;
+                if (j >= N) break;
+                uint64_t h[HW];
+                bool any = false;
+#pragma unroll
+                for (int w = 0; w < HW; ++w) {
+                    h[w] = hc[(size_t)w * N + j];
+                    any = any || h[w] != 0ull;
+                }
+                if (!any) continue;                    // j silent over the whole window
+                const float sj = s_l[j];
+                const float isj = 1.0f / (sj * sj);
+#pragma unroll
+                for (int q = 0; q < NPT; ++q) {
+                    const float wv = wbf ? __uint_as_float((e & 1) ? (w32[q][e >> 1] & 0xFFFF0000u)
+                                                                   : (w32[q][e >> 1] << 16))
+                                         : __uint_as_float(w32[q][e]);
+                    float dv;
+                    if (HYB) {
+                        const int off = ((int)(d32[q][e >> 2] << (24 - 8 * (e & 3)))) >> 24;
+                        dv = base_l[j] + 0.0f + 1.0f * (float)off;
+                    } else {
+                        dv = __uint_as_float(d32[q][e]);
+                    }
+                    const float cc = 1.0f + dv;
+                    const int lo = max(1, (int)ceilf(cc - sj));
+                    uint32_t win = hist_window<HW>(h, lo - 1) & wmask;
+                    float a = 0.0f;
+                    while (win) {
+                        const int bpos = __ffs(win) - 1;
+                        win &= win - 1u;
+                        a += fmaxf(sj - fabsf((float)(lo + bpos) - cc), 0.0f);
+                    }
+                    acc[q] = fmaf(wv, a * isj, acc[q]);
+                }
+            }
+        };
+        fetch(0, wa, da);
+        for (int c = 0; c < NC; c += 2) {
+            if (c + 1 < NC) fetch(c + 1, wb2, db2);
+            gather(c, wa, da);
+            if (c + 1 < NC) {
+                if (c + 2 < NC) fetch(c + 2, wa, da);
+                gather(c + 1, wb2, db2);
+            }
+        }
+
+#pragma unroll
+        for (int q = 0; q < NPT; ++q) {
+            const float xv = xq0[q];
+            xq0[q] = xq1[q];
+            const size_t row = (size_t)b * N + (act[q] ? idx[q] : 0);
+            if (act[q] && t + 2 < T) xq1[q] = p.x[(size_t)(t + 2) * BN + row];
+            const float r = acc[q] + bias[q];
+            const float a = xv + r * m[q];
+            const float u = lif_charge(k, v[q], a);
+            const float y = act[q] ? lif_fire(k, u) : 0.0f;
+            v[q] = lif_reset(k, u, y);
+            const uint32_t yb = y != 0.0f ? 1u : 0u;
+            word[q] |= yb << (t & 31);
+            if (act[q]) {
+                const int i = idx[q];
+                const size_t o = (size_t)t * BN + row;
+                p.y[o] = y;
+                p.u[o] = u;
+                if ((t & 31) == 31 || t == T - 1) p.bits[((size_t)b * TW + (t >> 5)) * N + i] = word[q];
+                uint64_t carry = yb;
+#pragma unroll
+                for (int w = 0; w < HW; ++w) {
+                    const uint64_t old = hc[(size_t)w * N + i];
+                    hn[(size_t)w * N + i] = (old << 1) | carry;
+                    carry = old >> 63;
+                }
+            }
+            if ((t & 31) == 31) word[q] = 0;
+        }
+        __syncthreads();
     }
 }
 
@@ -379,18 +586,49 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_kernel(SynBwd p) {
         if (act[q]) p.part[(size_t)b * N + idx[q]] = dbacc[q];
 }
 
+template <int NPT>
+void launch_syn_fwd_n(const SynFwd& a, int block, size_t lds, hipStream_t stream) {
+    if (a.gring) {
+        (void)hipFuncSetAttribute((const void*)syn_fwd_kernel<NPT, true>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipLaunchKernelGGL((syn_fwd_kernel<NPT, true>), dim3(a.B), dim3(block), lds, stream, a);
+    } else {
+        (void)hipFuncSetAttribute((const void*)syn_fwd_kernel<NPT, false>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipLaunchKernelGGL((syn_fwd_kernel<NPT, false>), dim3(a.B), dim3(block), lds, stream, a);
+    }
+}
+
+template <int NPT, bool HYB, int HW>
+void launch_syn_fwd_g(const SynFwd& a, int block, size_t lds, hipStream_t stream) {
+    (void)hipFuncSetAttribute((const void*)syn_fwd_gather_kernel<NPT, HYB, HW>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL((syn_fwd_gather_kernel<NPT, HYB, HW>), dim3(a.B), dim3(block), lds, stream, a);
+}
+
+template <int NPT>
+void launch_syn_fwd_gather(const SynFwd& a, int block, size_t lds, hipStream_t stream) {
+    const bool hyb = a.offr != nullptr;
+    if (a.HW == 1) {
+        if (hyb) launch_syn_fwd_g<NPT, true, 1>(a, block, lds, stream);
+        else launch_syn_fwd_g<NPT, false, 1>(a, block, lds, stream);
+    } else {
+        if (hyb) launch_syn_fwd_g<NPT, true, 2>(a, block, lds, stream);
+        else launch_syn_fwd_g<NPT, false, 2>(a, block, lds, stream);
+    }
+}
+
 void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream) {
     const int npt = (a.N + block - 1) / block;
-    if (npt == 1) {
-        (void)hipFuncSetAttribute((const void*)syn_fwd_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(syn_fwd_kernel<1>, dim3(a.B), dim3(block), lds, stream, a);
-    } else if (npt == 2) {
-        (void)hipFuncSetAttribute((const void*)syn_fwd_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(syn_fwd_kernel<2>, dim3(a.B), dim3(block), lds, stream, a);
-    } else {
-        (void)hipFuncSetAttribute((const void*)syn_fwd_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(syn_fwd_kernel<4>, dim3(a.B), dim3(block), lds, stream, a);
+    if (a.Wr) {
+        if (npt == 1) launch_syn_fwd_gather<1>(a, block, lds, stream);
+        else if (npt == 2) launch_syn_fwd_gather<2>(a, block, lds, stream);
+        else launch_syn_fwd_gather<4>(a, block, lds, stream);
+        return;
     }
+    if (npt == 1) launch_syn_fwd_n<1>(a, block, lds, stream);
+    else if (npt == 2) launch_syn_fwd_n<2>(a, block, lds, stream);
+    else launch_syn_fwd_n<4>(a, block, lds, stream);
 }
 
 template <int NPT, int KT, bool HYB, int MAXT>

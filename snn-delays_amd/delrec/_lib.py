@@ -67,7 +67,7 @@ class SynFwdArgs(ctypes.Structure):
     _fields_ = [('T', c_i32), ('B', c_i32), ('N', c_i32), ('L', c_i32),
                 ('x', c_vp), ('W', c_vp), ('w_bf16', c_i32), ('bias', c_vp), ('d', c_vp),
                 ('base', c_vp), ('offsets', c_vp), ('s', c_vp), ('s_uniform', c_f32),
-                ('drop', c_vp), ('lif', Lif), ('y', c_vp), ('u', c_vp), ('bits', c_vp),
+                ('s_max', c_f32), ('drop', c_vp), ('lif', Lif), ('y', c_vp), ('u', c_vp), ('bits', c_vp),
                 ('workspace', c_vp), ('workspace_bytes', c_size)]
 
 

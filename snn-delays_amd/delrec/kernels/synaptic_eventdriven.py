@@ -48,8 +48,8 @@ def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop,
     args = _lib.SynFwdArgs(
         T=T, B=B, N=N, L=L, x=_lib.ptr(xc), W=_lib.ptr(Wc), w_bf16=w_bf16, bias=_lib.ptr(bias),
         d=_lib.ptr(d_eff), base=_lib.ptr(base), offsets=_lib.ptr(offsets), s=_lib.ptr(s_vec),
-        s_uniform=float(s_uniform), drop=_lib.ptr(drop), lif=lif, y=_lib.ptr(y), u=_lib.ptr(u),
-        bits=_lib.ptr(bits), workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
+        s_uniform=float(s_uniform), s_max=float(s_max), drop=_lib.ptr(drop), lif=lif, y=_lib.ptr(y),
+        u=_lib.ptr(u), bits=_lib.ptr(bits), workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
     _lib.call('delrec_syn_fwd', args, _lib.stream_of(xc))
     return y, u, bits, L, Wc, w_bf16, float(s_max)
 

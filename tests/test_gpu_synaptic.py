@@ -17,7 +17,8 @@ SYN_CASES = [
     (16, 2, 48, 6.0, 0.8, {'decay_input': True}),
     (12, 2, 96, 4.0, 4.0, {}),                  # wide triangle
     (12, 2, 40, 6.0, 8.0, {}),                  # half-width 9: runtime tap count
-    (70, 2, 600, 60.0, 1.0, {}),                # backward ring too large for LDS: workspace ring
+    (70, 2, 700, 60.0, 1.0, {}),                # rings too large for LDS: gather forward, workspace ring
+    (130, 2, 400, 110.0, 1.0, {}),              # as above with a two-word spike history
 ]
 
 
@@ -99,6 +100,7 @@ HYB_CASES = [
     (16, 2, 48, (0.0, 10.0), 8, True, 0.0),      # bf16 W_rec, fp32 state
     (16, 2, 40, (-1.0, 7.0), 3, False, 0.7),     # mid-anneal triangle, four taps per column
     (12, 2, 32, (0.0, 6.0), 3, False, 8.0),      # half-width 9: runtime tap count
+    (80, 2, 700, (0.0, 55.0), 8, True, 0.0),     # gather forward (two history words), workspace ring
 ]
 
 
