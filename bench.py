@@ -236,13 +236,18 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    with _lib.timing() as rec, _lib.scan_timing(2 * args.steps + 8) as scans_t:
+    with _lib.scan_timing(2 * args.steps + 8) as scans_t:
         t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / args.steps
+    # per entry point (scan + reductions + GEMMs), from a few extra steps outside the timed region
+    with _lib.timing() as rec:
+        for _ in range(min(5, args.steps)):
+            step()
+        torch.cuda.synchronize()
     per_entry, per_scan = {}, {}
     for name, s, e in rec:
         per_entry.setdefault(name, []).append(s.elapsed_time(e))

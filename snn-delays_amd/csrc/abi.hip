@@ -342,6 +342,19 @@ void scan_release() {
 
 }  // namespace
 
+void delrec::ensure_lds(const void* fn, size_t bytes) {
+    static std::vector<std::pair<const void*, size_t>> done;
+    for (auto& e : done)
+        if (e.first == fn) {
+            if (e.second >= bytes) return;
+            (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+            e.second = bytes;
+            return;
+        }
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    done.emplace_back(fn, bytes);
+}
+
 extern "C" {
 
 const char* delrec_version(void) { return "delrec-mi355x 0.1.0 (gfx950)"; }

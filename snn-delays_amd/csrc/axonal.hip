@@ -719,13 +719,11 @@ __global__ void __launch_bounds__(1024) reduce_rows_kernel(const float* part, in
 #define DELREC_AX_CASE(CHV, RESV, HWV)                                                      \
     if (ch == CHV && res == RESV && hw == HWV) {                                            \
         if (fwd) {                                                                          \
-            (void)hipFuncSetAttribute((const void*)axonal_fwd_kernel<CHV, RESV, HWV>,             \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);      \
+            ensure_lds((const void*)axonal_fwd_kernel<CHV, RESV, HWV>, lds);        \
             hipLaunchKernelGGL((axonal_fwd_kernel<CHV, RESV, HWV>), dim3(grid), dim3(block), \
                                lds, stream, *fa);                                           \
         } else {                                                                            \
-            (void)hipFuncSetAttribute((const void*)axonal_bwd_kernel<CHV, RESV, HWV>,             \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);      \
+            ensure_lds((const void*)axonal_bwd_kernel<CHV, RESV, HWV>, lds);        \
             hipLaunchKernelGGL((axonal_bwd_kernel<CHV, RESV, HWV>), dim3(grid), dim3(block), \
                                lds, stream, *ba);                                           \
         }                                                                                   \
@@ -744,13 +742,11 @@ bool launch_axonal(bool fwd, const AxFwd* fa, const AxBwd* ba, int ch, bool res,
 #define DELREC_AXT_CASE(RIV, NJV, HWV)                                                      \
     if (ri == RIV && nj == NJV && hw == HWV) {                                              \
         if (fwd) {                                                                          \
-            (void)hipFuncSetAttribute((const void*)axonal_fwd_tiled<RIV, NJV, HWV>,         \
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+            ensure_lds((const void*)axonal_fwd_tiled<RIV, NJV, HWV>, lds);   \
             hipLaunchKernelGGL((axonal_fwd_tiled<RIV, NJV, HWV>), dim3(grid), dim3(block),   \
                                lds, stream, *fa);                                           \
         } else {                                                                            \
-            (void)hipFuncSetAttribute((const void*)axonal_bwd_tiled<RIV, NJV, HWV>,         \
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+            ensure_lds((const void*)axonal_bwd_tiled<RIV, NJV, HWV>, lds);   \
             hipLaunchKernelGGL((axonal_bwd_tiled<RIV, NJV, HWV>), dim3(grid), dim3(block),   \
                                lds, stream, *ba);                                           \
         }                                                                                   \

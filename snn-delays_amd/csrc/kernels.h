@@ -128,6 +128,10 @@ struct LagBf16 {
     float* ps;                   // [KS][N][N] partial sum_l dh/ds * C_l, or NULL
 };
 
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel and size (cached; the
+// library is used from one host thread at a time)
+void ensure_lds(const void* fn, size_t bytes);
+
 bool launch_axonal(bool fwd, const AxFwd* fa, const AxBwd* ba, int ch, bool res, int hw,
                    int grid, int block, size_t lds, hipStream_t stream);
 bool launch_axonal_tiled(bool fwd, const AxFwd* fa, const AxBwd* ba, int ri, int nj, int hw,

@@ -589,20 +589,17 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_kernel(SynBwd p) {
 template <int NPT>
 void launch_syn_fwd_n(const SynFwd& a, int block, size_t lds, hipStream_t stream) {
     if (a.gring) {
-        (void)hipFuncSetAttribute((const void*)syn_fwd_kernel<NPT, true>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        ensure_lds((const void*)syn_fwd_kernel<NPT, true>, lds);
         hipLaunchKernelGGL((syn_fwd_kernel<NPT, true>), dim3(a.B), dim3(block), lds, stream, a);
     } else {
-        (void)hipFuncSetAttribute((const void*)syn_fwd_kernel<NPT, false>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        ensure_lds((const void*)syn_fwd_kernel<NPT, false>, lds);
         hipLaunchKernelGGL((syn_fwd_kernel<NPT, false>), dim3(a.B), dim3(block), lds, stream, a);
     }
 }
 
 template <int NPT, bool HYB, int HW>
 void launch_syn_fwd_g(const SynFwd& a, int block, size_t lds, hipStream_t stream) {
-    (void)hipFuncSetAttribute((const void*)syn_fwd_gather_kernel<NPT, HYB, HW>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    ensure_lds((const void*)syn_fwd_gather_kernel<NPT, HYB, HW>, lds);
     hipLaunchKernelGGL((syn_fwd_gather_kernel<NPT, HYB, HW>), dim3(a.B), dim3(block), lds, stream, a);
 }
 
@@ -636,8 +633,7 @@ void launch_syn_bwd_k(const SynBwd& a, int block, size_t lds, hipStream_t stream
     if (a.gring) {
         hipLaunchKernelGGL((syn_bwd_kernel<NPT, KT, HYB, MAXT, true>), dim3(a.B), dim3(block), 0, stream, a);
     } else {
-        (void)hipFuncSetAttribute((const void*)syn_bwd_kernel<NPT, KT, HYB, MAXT, false>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        ensure_lds((const void*)syn_bwd_kernel<NPT, KT, HYB, MAXT, false>, lds);
         hipLaunchKernelGGL((syn_bwd_kernel<NPT, KT, HYB, MAXT, false>), dim3(a.B), dim3(block), lds, stream, a);
     }
 }

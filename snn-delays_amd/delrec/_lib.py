@@ -144,11 +144,23 @@ def make_lif(tau, v_threshold, v_reset, decay_input, detach_reset, surr_id, gamm
                gamma=float(gamma), alpha=float(alpha))
 
 
+_WS_SIZES = {}
+
+
+def workspace_bytes(kind, T, B, N, L, flags):
+    """``delrec_query_workspace`` (memoised: the size is a pure function of the arguments)."""
+    key = (kind, T, B, N, L, flags)
+    n = _WS_SIZES.get(key)
+    if n is None:
+        size = c_size(0)
+        _check('delrec_query_workspace', load().delrec_query_workspace(kind, T, B, N, L, flags,
+                                                                       ctypes.byref(size)))
+        n = _WS_SIZES[key] = max(int(size.value), 1)
+    return n
+
+
 def workspace(kind, T, B, N, L, flags, device):
-    size = c_size(0)
-    _check('delrec_query_workspace', load().delrec_query_workspace(kind, T, B, N, L, flags,
-                                                                   ctypes.byref(size)))
-    return torch.empty(max(int(size.value), 1), dtype=torch.uint8, device=device)
+    return torch.empty(workspace_bytes(kind, T, B, N, L, flags), dtype=torch.uint8, device=device)
 
 
 class _Timing:

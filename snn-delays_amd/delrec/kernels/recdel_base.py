@@ -45,6 +45,12 @@ class AxonalRecdelHip(torch.autograd.Function):
         z = torch.empty_like(y)
         bits = torch.empty(bits_shape(T, B, N), device=dev, dtype=torch.int32)
         ws = _lib.workspace(_lib.WS_AXONAL_FWD, T, B, N, 2, w_bf16, dev)   # size does not depend on L
+        args = _lib.AxonalFwdArgs(
+            T=T, B=B, N=N, L=2, x=_lib.ptr(xc), W=_lib.ptr(Wc), w_bf16=w_bf16, bias=_lib.ptr(bc),
+            d=_lib.ptr(dc), s=_lib.ptr(s_vec), s_uniform=1.0 + sigma, drop=_lib.ptr(m), taps=0,
+            lif=lif, y=_lib.ptr(y), u=_lib.ptr(u), rec=None, z=_lib.ptr(z), bits=_lib.ptr(bits),
+            workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
+        stream = _lib.stream_of(xc)
 
         # The window length needs max d (and max s): the one device-to-host read of the call,
         # taken after the host work above so that it overlaps the GPU work still queued.
@@ -67,13 +73,14 @@ class AxonalRecdelHip(torch.autograd.Function):
         else:
             L = window_length_f32(d_max, s_max)
             taps, mode = _lib.DELREC_TAPS_SOFT, _lib.DELREC_BWD_SOFT
-        L = max(L, 2)
-        args = _lib.AxonalFwdArgs(
-            T=T, B=B, N=N, L=L, x=_lib.ptr(xc), W=_lib.ptr(Wc), w_bf16=w_bf16, bias=_lib.ptr(bc),
-            d=_lib.ptr(dc), s=_lib.ptr(s_vec), s_uniform=1.0 + sigma, drop=_lib.ptr(m), taps=taps,
-            lag=_lib.ptr(lag), frac=_lib.ptr(frac), lif=lif, y=_lib.ptr(y), u=_lib.ptr(u), rec=None,
-            z=_lib.ptr(z), bits=_lib.ptr(bits), workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
-        _lib.call('delrec_axonal_fwd', args, _lib.stream_of(xc))
+        args.L = max(L, 2)
+        args.taps = taps
+        if lag is not None:
+            args.lag = lag.data_ptr()
+        if frac is not None:
+            args.frac = frac.data_ptr()
+        _lib.call('delrec_axonal_fwd', args, stream)
+        L = args.L
 
         ctx.save_for_backward(u, z, bits, Wc, dc, s_vec, m, lag, p_spread)
         ctx.meta = (T, B, N, L, w_bf16, sigma, bool(use_sig_p), mode, W.dtype)
