@@ -91,31 +91,39 @@ bool axonal_layout(int N, int L, AxLayout& o) {
     else if (lags <= 256) o.hw = 4;
     else return false;
     if (N <= 256) {
-        // NJ chunk lanes of 16 sources per receiver group (a power of two <= 16), RI
-        // receivers per lane: the smallest RI that fits the lanes in 1024 threads.
-        constexpr int kCJ = 16, kCJP = 20;
+        // CJ sources per lane chunk (32 for 128 < N <= 256: 4 x 32 tiles reduce over 8-lane
+        // groups; DELREC_AXONAL_CJ=16 selects the 8 x 16 tiles), NJ chunk lanes per receiver
+        // group (a power of two), RI receivers per lane with RI <= NJ: neuron i runs on lane
+        // (i / RI, i % RI) of its own group.
+        int cj = N > 128 ? 32 : 16;
+        if (const char* e = getenv("DELREC_AXONAL_CJ"))
+            if (atoi(e) == 16) cj = 16;
         int nj = 1;
-        while (nj * kCJ < N) nj <<= 1;
-        // RI = 8 runs 512 threads (2 waves per SIMD, 256 VGPRs per wave)
+        while (nj * cj < N) nj <<= 1;
         int ri = 1;
-        while (ri < 8 && ((N + ri - 1) / ri) * nj > (ri >= 8 ? 512 : 1024)) ri <<= 1;
-        if (ri == 4 && nj == 16) ri = 8;
-        if (const char* e = getenv("DELREC_AXONAL_RI")) {
-            const int want = atoi(e);
-            if (nj == 16 && (want == 2 || want == 4 || want == 8) &&
-                ((N + want - 1) / want) * nj <= (want >= 8 ? 512 : 1024))
-                ri = want;
+        if (cj == 32) {
+            ri = 4;
+        } else {
+            // the smallest RI whose lanes fit the block (RI x CJ >= 128 runs 512 threads)
+            while (ri < 8 && ((N + ri - 1) / ri) * nj > (ri * cj >= 128 ? 512 : 1024)) ri <<= 1;
+            if (ri == 4 && nj == 16) ri = 8;
+            if (const char* e = getenv("DELREC_AXONAL_RI")) {
+                const int want = atoi(e);
+                if (nj == 16 && (want == 2 || want == 4 || want == 8) &&
+                    ((N + want - 1) / want) * nj <= (want * cj >= 128 ? 512 : 1024))
+                    ri = want;
+            }
         }
         const int lanes = ((N + ri - 1) / ri) * nj;
-        if (lanes > (ri >= 8 ? 512 : 1024)) return false;
+        if (lanes > (ri * cj >= 128 ? 512 : 1024) || ri > nj) return false;
         o.res = true;
         o.G = nj;
         o.ri = ri;
-        o.CH = kCJ;
-        o.CHS = kCJ;
-        o.NZ = nj * kCJP;
-        o.block = std::max((N + 63) / 64 * 64, (lanes + 63) / 64 * 64);
-        o.np = std::max(N, (o.block / nj) * ri);   // every lane group's RI rows are in bounds
+        o.CH = cj;
+        o.CHS = cj;
+        o.NZ = nj * (cj + 4);
+        o.block = (lanes + 63) / 64 * 64;
+        o.np = N;
     } else {
         o.res = false;
         o.ri = 0;
@@ -406,7 +414,7 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
     if (a->taps == DELREC_TAPS_INTERP && !a->frac) return DELREC_ERR_ARG;
     AxLayout lay;
     if (!axonal_layout(a->N, a->L, lay)) return DELREC_ERR_WINDOW;
-    const size_t lds = ((size_t)2 * lay.NZ + (lay.res ? (size_t)lay.np : 0)) * sizeof(float);
+    const size_t lds = (size_t)2 * lay.NZ * sizeof(float);
     if (lds > (size_t)max_lds_bytes()) return DELREC_ERR_WINDOW;
     hipStream_t s = static_cast<hipStream_t>(stream);
     AxFwd p{};
@@ -425,7 +433,7 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
         p.Wt = wt;
     }
     const bool timed = scan_begin(DELREC_WS_AXONAL_FWD, s);
-    const bool ok = lay.res ? launch_axonal_tiled(true, &p, nullptr, lay.ri, lay.G, lay.hw, a->B, lay.block, lds, s)
+    const bool ok = lay.res ? launch_axonal_tiled(true, &p, nullptr, lay.ri, lay.G, lay.CH, lay.hw, a->B, lay.block, lds, s)
                             : launch_axonal(true, &p, nullptr, lay.CH, lay.res, lay.hw, a->B, lay.block, lds, s);
     scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;
@@ -443,7 +451,8 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     // the tiled backward reads kMaxTaps consecutive ring slots from the first tap lag on
     const int R = std::max(a->L, 2) + (lay.res ? kMaxTaps : 0);
     const int NP = lay.res ? lay.np : a->N;
-    const size_t lds = ((size_t)2 * lay.NZ + (size_t)(R + kMaxTaps) * NP) * sizeof(float);
+    // tiled: grbuf + ring; streamed: grbuf + ring + tap-weight table
+    const size_t lds = ((size_t)2 * lay.NZ + (size_t)(R + (lay.res ? 0 : kMaxTaps)) * NP) * sizeof(float);
     if (lds > (size_t)max_lds_bytes()) return DELREC_ERR_WINDOW;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int T = a->T, B = a->B, N = a->N;
@@ -463,7 +472,7 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     p.mode = a->mode; p.lag = a->lag; p.lif = make_lif(a->lif);
     p.dx = a->dx; p.gr = need_gr ? grbuf : nullptr; p.part = part;
     const bool timed = scan_begin(DELREC_WS_AXONAL_BWD, s);
-    const bool ok = lay.res ? launch_axonal_tiled(false, nullptr, &p, lay.ri, lay.G, lay.hw, B, lay.block, lds, s)
+    const bool ok = lay.res ? launch_axonal_tiled(false, nullptr, &p, lay.ri, lay.G, lay.CH, lay.hw, B, lay.block, lds, s)
                             : launch_axonal(false, nullptr, &p, lay.CH, lay.res, lay.hw, B, lay.block, lds, s);
     scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;

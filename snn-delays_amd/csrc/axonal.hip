@@ -374,41 +374,61 @@ __global__ void __launch_bounds__(1024) axonal_bwd_kernel(AxBwd p) {
 
 // ---------------------------------------------------------------------------------------
 // Tiled forms for N <= 256 (the fast path). The GEMV lanes hold an RI x CJ tile of W in
-// VGPRs: lane (grp, jcg) owns receivers grp*RI .. +RI and sources jcg*CJ .. +CJ; the NJ
-// chunk lanes of a group sit in one 16-lane DPP row and reduce there. Per-neuron work
-// (LIF, trace, stores) runs on lanes tid < N only. z / gr are broadcast through LDS with
-// a chunk pitch of CJ + 4 floats so the NJ chunk reads of a row hit distinct banks.
-constexpr int kCJ = 16;
-constexpr int kCJP = kCJ + 4;
+// VGPRs: lane (grp, jcg) owns receivers grp*RI .. +RI and sources jcg*CJ .. +CJ, the NJ
+// chunk lanes of a group sit in one DPP row and reduce there with a butterfly that leaves
+// the RI row sums in every lane of the group. Neuron i = grp*RI + a lives on lane
+// (grp, jcg = a) of its own group, so the recurrent input reaches it inside the wave;
+// only z (forward) / gr (backward) cross waves, through LDS with a chunk pitch of CJ + 4
+// floats (the NJ chunk reads of a row hit distinct banks): one barrier per step.
+template <int CJ>
+__device__ __forceinline__ int zpos(int j) { return (j / CJ) * (CJ + 4) + (j % CJ); }
 
-__device__ __forceinline__ int zpos(int j) { return (j / kCJ) * kCJP + (j % kCJ); }
+template <int RI> struct TiledThreads { static constexpr int value = RI >= 4 ? 512 : 1024; };
 
-template <int RI> struct TiledThreads { static constexpr int value = RI >= 8 ? 512 : 1024; };
+// acc[a] of the lane's group for the lane's own a: a dot product with the lane's constant
+// one-hot mask (exact for finite sums; a select chain on a lane index would be lowered to
+// an indexed scratch access)
+template <int RI>
+struct OneHot {
+    float m[RI];
+    __device__ __forceinline__ void init(int sel) {
+#pragma unroll
+        for (int a = 0; a < RI; ++a) m[a] = (sel == a) ? 1.0f : 0.0f;
+    }
+    __device__ __forceinline__ float pick(const float (&acc)[RI]) const {
+        float r = acc[0] * m[0];
+#pragma unroll
+        for (int a = 1; a < RI; ++a) r = fmaf(acc[a], m[a], r);
+        return r;
+    }
+};
 
-template <int RI, int NJ, int HW>
+template <int RI, int NJ, int HW, int CJ>
 __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_fwd_tiled(AxFwd p) {
     extern __shared__ float smem[];
+    constexpr int CJP = CJ + 4;
     const int N = p.N, T = p.T, B = p.B, NZ = p.NZ;
-    float* zbuf = smem;                 // [2][NZ], NZ = NJ * kCJP
-    float* rbuf = smem + 2 * NZ;        // [N] recurrent input of this step
+    float* zbuf = smem;                 // [2][NZ], NZ = NJ * CJP
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
     const int grp = tid / NJ, jcg = tid - (tid / NJ) * NJ;
     const Lif k = p.lif;
     const int TW = (T + 31) >> 5;
 
-    float w[RI][kCJ];
+    float w[RI][CJ];
 #pragma unroll
     for (int a = 0; a < RI; ++a)
 #pragma unroll
-        for (int c = 0; c < kCJ; ++c) {
-            const int i = grp * RI + a, j = jcg * kCJ + c;
+        for (int c = 0; c < CJ; ++c) {
+            const int i = grp * RI + a, j = jcg * CJ + c;
             w[a][c] = (i < N && j < N) ? load_w(p.W, p.w_bf16, (size_t)i * N + j) : 0.0f;
         }
 
-    // per-neuron lanes
-    const bool nl = tid < N;
-    const int i = nl ? tid : 0;
+    // neuron lanes: neuron i = grp * RI + jcg on the lanes jcg < RI
+    const bool nl = jcg < RI && grp * RI + jcg < N;
+    OneHot<RI> sel;
+    sel.init(jcg);
+    const int i = nl ? grp * RI + jcg : 0;
     const float c = 1.0f + p.d[i];
     const float s = p.s ? p.s[i] : p.s_uniform;
     const float s2 = s * s;
@@ -441,12 +461,12 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_fwd_tiled(AxFw
     // one time step; `xs` is this step's prefetch slot, refilled with x[t + kPrefetch]
     auto step = [&](const int t, float& xs) {
         // GEMV: r_i = sum_j W[i, j] z_j over this lane's tile, reduced across the row
-        const float4* z4 = reinterpret_cast<const float4*>(zbuf + (t & 1) * NZ + jcg * kCJP);
+        const float4* z4 = reinterpret_cast<const float4*>(zbuf + (t & 1) * NZ + jcg * CJP);
         float acc[RI];
 #pragma unroll
         for (int a = 0; a < RI; ++a) acc[a] = 0.0f;
 #pragma unroll
-        for (int q = 0; q < kCJ / 4; ++q) {
+        for (int q = 0; q < CJ / 4; ++q) {
             const float4 zz = z4[q];
 #pragma unroll
             for (int a = 0; a < RI; ++a) {
@@ -458,16 +478,11 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_fwd_tiled(AxFw
         }
 #pragma unroll
         for (int a = 0; a < RI; ++a) acc[a] = group_sum_t<NJ>(acc[a]);
-        if (jcg == 0) {
-#pragma unroll
-            for (int a = 0; a < RI; ++a) rbuf[grp * RI + a] = acc[a];   // rbuf padded to the lane groups
-        }
-        barrier_lds();
 
         if (nl) {
             const float xv = xs;
             xs = (t + kPrefetch < T) ? p.x[(size_t)(t + kPrefetch) * BN + row] : 0.0f;
-            const float r = rbuf[i] + bias;
+            const float r = sel.pick(acc) + bias;
             const float a = xv + r * m;
             const float u = lif_charge(k, v, a);
             const float y = lif_fire(k, u);
@@ -493,7 +508,7 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_fwd_tiled(AxFw
                 } else {
                     zn = axonal_trace<HW>(hist, p.taps, c, s, s2, lo, hi, lag, frac);
                 }
-                zbuf[((t + 1) & 1) * NZ + zpos(i)] = zn;
+                zbuf[((t + 1) & 1) * NZ + zpos<CJ>(i)] = zn;
                 if (p.z) p.z[(size_t)(t + 1) * BN + row] = zn;
             }
         }
@@ -507,13 +522,13 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_fwd_tiled(AxFw
     }
 }
 
-template <int RI, int NJ, int HW>
+template <int RI, int NJ, int HW, int CJ>
 __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBwd p) {
     extern __shared__ float smem[];
+    constexpr int CJP = CJ + 4;
     const int N = p.N, T = p.T, B = p.B, NZ = p.NZ, R = p.R, NP = p.NP;
     float* grbuf = smem;                 // [2][NZ]
-    float* ring = smem + 2 * NZ;         // [R][NP] gz of the future steps (R >= L + kMaxTaps)
-    float* htab = ring + R * NP;         // [kMaxTaps][NP] tap weights of each source
+    float* ring = smem + 2 * NZ;         // [R][NP]: column j holds gz_j of the future steps
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
     const int grp = tid / NJ, jcg = tid - (tid / NJ) * NJ;
@@ -521,21 +536,24 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
     const int TW = (T + 31) >> 5;
 
     // tile of W^T: sources grp*RI + a (rows of the GEMV), receivers jcg*CJ + c (columns)
-    float w[RI][kCJ];
+    float w[RI][CJ];
 #pragma unroll
     for (int a = 0; a < RI; ++a)
 #pragma unroll
-        for (int cc = 0; cc < kCJ; ++cc) {
-            const int j = grp * RI + a, i = jcg * kCJ + cc;
+        for (int cc = 0; cc < CJ; ++cc) {
+            const int j = grp * RI + a, i = jcg * CJ + cc;
             w[a][cc] = (i < N && j < N) ? load_w(p.W, p.w_bf16, (size_t)i * N + j) : 0.0f;
         }
 
-    // Lanes [0, N) run the LIF chain of source j = tid; lanes [N, 2N) (when the block has
-    // them) accumulate the delay / half-width gradient of source j = tid - N concurrently.
-    const bool split = (int)blockDim.x >= 2 * N;
-    const bool nl = tid < N;                                  // LIF lanes
-    const bool dl = split ? (tid >= N && tid < 2 * N) : nl;   // delay-gradient lanes
-    const int j = nl ? tid : (dl ? tid - N : 0);
+    // Source j = grp*RI + a runs its LIF chain on lane (grp, a); when the group has 2*RI
+    // lanes, lane (grp, RI + a) accumulates its delay / half-width gradient concurrently.
+    const bool split = NJ >= 2 * RI;
+    const int ja = grp * RI + (jcg % RI);
+    const bool nl = jcg < RI && ja < N;                                    // LIF lanes
+    const bool dl = split ? (jcg >= RI && jcg < 2 * RI && ja < N) : nl;    // delay-gradient lanes
+    const int j = (nl || dl) ? ja : 0;
+    OneHot<RI> sel;
+    sel.init(jcg % RI);
     const float c = 1.0f + p.d[j];
     const float s = p.s ? p.s[j] : p.s_uniform;
     const float s2 = s * s;
@@ -545,18 +563,16 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
     const bool soft = p.mode == DELREC_BWD_SOFT;
     const bool fast = soft && nt <= kMaxTaps && HW == 1;
     const bool need_ds = p.s != nullptr;
-    float dsg[kMaxTaps];
+    float dsg[kMaxTaps], wq[kMaxTaps];
 #pragma unroll
-    for (int q = 0; q < kMaxTaps; ++q) dsg[q] = (q < nt) ? tri_dsign((float)(lo + q), c, s) : 0.0f;
+    for (int q = 0; q < kMaxTaps; ++q) {
+        dsg[q] = (q < nt) ? tri_dsign((float)(lo + q), c, s) : 0.0f;
+        wq[q] = (q < nt) ? tri_weight((float)(lo + q), c, s, s2) : 0.0f;
+    }
     const int lag = p.lag ? p.lag[j] : 1;
     const float m = p.drop ? p.drop[(size_t)b * N + j] : 1.0f;
 
     for (int q = tid; q < 2 * NZ + R * NP; q += blockDim.x) smem[q] = 0.0f;
-    if (nl) {
-#pragma unroll
-        for (int q = 0; q < kMaxTaps; ++q)
-            htab[q * NP + j] = (q < nt) ? tri_weight((float)(lo + q), c, s, s2) : 0.0f;
-    }
     __syncthreads();
 
     History<HW> past;   // delay lanes: bit(l) = y[tw - l] for the window time tw
@@ -600,35 +616,58 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
         }
     };
 
-    int tmod = (T - 1) % R;
+    // gz(t+1) of this lane's source: W^T-tile contraction of gr(t+1), reduced in the group
+    auto contract = [&](int buf) {
+        const float4* g4 = reinterpret_cast<const float4*>(grbuf + buf * NZ + jcg * CJP);
+        float acc[RI];
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc[a] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < CJ / 4; ++q) {
+            const float4 gg = g4[q];
+#pragma unroll
+            for (int a = 0; a < RI; ++a) {
+                acc[a] = fmaf(w[a][4 * q + 0], gg.x, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 1], gg.y, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 2], gg.z, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 3], gg.w, acc[a]);
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc[a] = group_sum_t<NJ>(acc[a]);
+        return sel.pick(acc);
+    };
+
+    int tn1 = T % R;                                   // slot of time t + 1
     // one reverse step; `gs`, `us` are this step's prefetch slots, refilled with step t - P
     auto step = [&](const int t, float& gs, float& us) {
+        const float gz1 = contract((t + 1) & 1);       // gz(t+1); gr(T) = 0
+        const int tm = tn1 == 0 ? R - 1 : tn1 - 1;     // slot of time t
+        if (nl) ring[tn1 * NP + j] = gz1;
         if (dl && t < T - 1) {
-            int s1 = tmod + 1;
-            if (s1 >= R) s1 -= R;
-            delay_grad(ring[s1 * NP + j]);                     // gz_{t+1} with the window of t+1
+            delay_grad(gz1);                           // gz(t+1) with the window of t+1
             past.pull(oldest.bit(t - 64 * HW));
         }
         if (nl) {
             float gfut = 0.0f;
             if (fast) {
-                // taps past the support weigh 0 and ring slots of times >= T still hold 0
-                int sb = tmod + lo;
+                // taps past the support weigh 0 and ring slots of times >= T hold 0
+                int sb = tm + lo;
                 if (sb >= R) sb -= R;
 #pragma unroll
                 for (int q = 0; q < kMaxTaps; ++q) {
                     int slot = sb + q;
                     if (slot >= R) slot -= R;
-                    gfut += htab[q * NP + j] * ring[slot * NP + j];
+                    gfut += wq[q] * ring[slot * NP + j];
                 }
             } else if (soft) {
                 for (int l = lo; l <= hi && t + l < T; ++l) {
-                    int slot = tmod + l;
+                    int slot = tm + l;
                     if (slot >= R) slot -= R;
                     gfut += tri_weight((float)l, c, s, s2) * ring[slot * NP + j];
                 }
             } else if (t + lag < T) {
-                int slot = tmod + lag;
+                int slot = tm + lag;
                 if (slot >= R) slot -= R;
                 gfut = ring[slot * NP + j];
             }
@@ -645,35 +684,11 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
             const size_t o = (size_t)t * BN + rowj;
             p.dx[o] = da;
             if (p.gr) p.gr[o] = gr;
-            grbuf[(t & 1) * NZ + zpos(j)] = gr;
+            grbuf[(t & 1) * NZ + zpos<CJ>(j)] = gr;
             db_acc += gr;
         }
         barrier_lds();
-
-        // gz_j = sum_i gr_i W[i, j]
-        const float4* g4 = reinterpret_cast<const float4*>(grbuf + (t & 1) * NZ + jcg * kCJP);
-        float acc[RI];
-#pragma unroll
-        for (int a = 0; a < RI; ++a) acc[a] = 0.0f;
-#pragma unroll
-        for (int q = 0; q < kCJ / 4; ++q) {
-            const float4 gg = g4[q];
-#pragma unroll
-            for (int a = 0; a < RI; ++a) {
-                acc[a] = fmaf(w[a][4 * q + 0], gg.x, acc[a]);
-                acc[a] = fmaf(w[a][4 * q + 1], gg.y, acc[a]);
-                acc[a] = fmaf(w[a][4 * q + 2], gg.z, acc[a]);
-                acc[a] = fmaf(w[a][4 * q + 3], gg.w, acc[a]);
-            }
-        }
-#pragma unroll
-        for (int a = 0; a < RI; ++a) acc[a] = group_sum_t<NJ>(acc[a]);
-        if (jcg == 0) {
-#pragma unroll
-            for (int a = 0; a < RI; ++a) ring[tmod * NP + grp * RI + a] = acc[a];   // NP >= groups * RI
-        }
-        barrier_lds();
-        tmod = tmod == 0 ? R - 1 : tmod - 1;
+        tn1 = tm;
     };
 
     // steps T-1, T-2, ... in groups of kPrefetchBwd; slot q holds step T-1-(n*P+q)
@@ -682,10 +697,9 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
         for (int q = 0; q < kPrefetchBwd; ++q)
             if (t0 - q >= 0) step(t0 - q, gq[q], uq[q]);
     }
+    const float gz0 = contract(0);                     // gz(0) with the window of 0
     if (dl) {
-        int s0 = tmod + 1;
-        if (s0 >= R) s0 -= R;
-        delay_grad(ring[s0 * NP + j]);                          // gz_0 with the window of 0
+        delay_grad(gz0);
         p.part[(size_t)1 * B * N + rowj] = soft ? dd_acc / s2 : dd_acc;
         p.part[(size_t)2 * B * N + rowj] = ds_acc;
     }
@@ -739,27 +753,28 @@ bool launch_axonal(bool fwd, const AxFwd* fa, const AxBwd* ba, int ch, bool res,
     return false;
 }
 
-#define DELREC_AXT_CASE(RIV, NJV, HWV)                                                      \
-    if (ri == RIV && nj == NJV && hw == HWV) {                                              \
+#define DELREC_AXT_CASE(RIV, NJV, HWV, CJV)                                                 \
+    if (ri == RIV && nj == NJV && hw == HWV && cj == CJV) {                                  \
         if (fwd) {                                                                          \
-            ensure_lds((const void*)axonal_fwd_tiled<RIV, NJV, HWV>, lds);   \
-            hipLaunchKernelGGL((axonal_fwd_tiled<RIV, NJV, HWV>), dim3(grid), dim3(block),   \
+            ensure_lds((const void*)axonal_fwd_tiled<RIV, NJV, HWV, CJV>, lds);              \
+            hipLaunchKernelGGL((axonal_fwd_tiled<RIV, NJV, HWV, CJV>), dim3(grid), dim3(block), \
                                lds, stream, *fa);                                           \
         } else {                                                                            \
-            ensure_lds((const void*)axonal_bwd_tiled<RIV, NJV, HWV>, lds);   \
-            hipLaunchKernelGGL((axonal_bwd_tiled<RIV, NJV, HWV>), dim3(grid), dim3(block),   \
+            ensure_lds((const void*)axonal_bwd_tiled<RIV, NJV, HWV, CJV>, lds);              \
+            hipLaunchKernelGGL((axonal_bwd_tiled<RIV, NJV, HWV, CJV>), dim3(grid), dim3(block), \
                                lds, stream, *ba);                                           \
         }                                                                                   \
         return true;                                                                        \
     }
-#define DELREC_AXT_HW(RIV, NJV) \
-    DELREC_AXT_CASE(RIV, NJV, 1) DELREC_AXT_CASE(RIV, NJV, 2) DELREC_AXT_CASE(RIV, NJV, 4)
+#define DELREC_AXT_HW(RIV, NJV, CJV) \
+    DELREC_AXT_CASE(RIV, NJV, 1, CJV) DELREC_AXT_CASE(RIV, NJV, 2, CJV) DELREC_AXT_CASE(RIV, NJV, 4, CJV)
 
-// (RI, NJ) pairs chosen by the host layout for N <= 256
-bool launch_axonal_tiled(bool fwd, const AxFwd* fa, const AxBwd* ba, int ri, int nj, int hw,
+// (RI, NJ, CJ) triples chosen by the host layout for N <= 256
+bool launch_axonal_tiled(bool fwd, const AxFwd* fa, const AxBwd* ba, int ri, int nj, int cj, int hw,
                          int grid, int block, size_t lds, hipStream_t stream) {
-    DELREC_AXT_HW(1, 1) DELREC_AXT_HW(1, 2) DELREC_AXT_HW(1, 4) DELREC_AXT_HW(1, 8)
-    DELREC_AXT_HW(2, 16) DELREC_AXT_HW(4, 16) DELREC_AXT_HW(8, 16)
+    DELREC_AXT_HW(1, 1, 16) DELREC_AXT_HW(1, 2, 16) DELREC_AXT_HW(1, 4, 16) DELREC_AXT_HW(1, 8, 16)
+    DELREC_AXT_HW(2, 16, 16) DELREC_AXT_HW(4, 16, 16) DELREC_AXT_HW(8, 16, 16)
+    DELREC_AXT_HW(4, 8, 32)
     return false;
 }
 

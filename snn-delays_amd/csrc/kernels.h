@@ -134,7 +134,7 @@ void ensure_lds(const void* fn, size_t bytes);
 
 bool launch_axonal(bool fwd, const AxFwd* fa, const AxBwd* ba, int ch, bool res, int hw,
                    int grid, int block, size_t lds, hipStream_t stream);
-bool launch_axonal_tiled(bool fwd, const AxFwd* fa, const AxBwd* ba, int ri, int nj, int hw,
+bool launch_axonal_tiled(bool fwd, const AxFwd* fa, const AxBwd* ba, int ri, int nj, int cj, int hw,
                          int grid, int block, size_t lds, hipStream_t stream);
 void launch_reduce_rows(const float* part, int B, int N, float* o0, float* o1, float* o2,
                         hipStream_t stream);

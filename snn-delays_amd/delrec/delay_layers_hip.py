@@ -28,8 +28,15 @@ class AxonalHipScans:
             drop = self.dropout(torch.ones(B, N, device=x_seq.device, dtype=x_seq.dtype))
         else:
             drop = None
-        p_spread = (self.p_spread if self.use_sig_p
-                    else torch.zeros(N, device=x_seq.device, dtype=x_seq.dtype))
+        if self.use_sig_p:
+            p_spread = self.p_spread
+        else:
+            # a zero spread the Function differentiates nothing against: kept, not re-made
+            p_spread = getattr(self, '_zero_spread', None)
+            if p_spread is None or p_spread.shape != (N,) or p_spread.device != x_seq.device \
+                    or p_spread.dtype != x_seq.dtype:
+                p_spread = torch.zeros(N, device=x_seq.device, dtype=x_seq.dtype)
+                self._zero_spread = p_spread
         bias = self.recurrent_bias if self.use_rec_bias else None
         if ste_mode:
             ste_mode = 1 if getattr(self.config, 'ste_round_forward', True) else 2

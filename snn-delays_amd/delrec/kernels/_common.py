@@ -26,6 +26,27 @@ def lif_struct(neuron, surrogate_function, gamma=None):
                          sid, g, alpha)
 
 
+_PINNED = {}
+
+
+def read_scalars(*vals):
+    """Copy a few 0-dim device tensors to the host through a pinned buffer and wait for them
+    by polling an event: the one device-to-host read of a forward, with a short wake-up."""
+    dev = vals[0].device
+    buf = _PINNED.get(dev)
+    if buf is None:
+        buf = _PINNED[dev] = (torch.empty(8, dtype=torch.float32, pin_memory=True),
+                              torch.cuda.Event())
+    host, ev = buf
+    n = len(vals)
+    stacked = vals[0].reshape(1) if n == 1 else torch.stack([v.reshape(()) for v in vals])
+    host[:n].copy_(stacked.to(torch.float32), non_blocking=True)
+    ev.record()
+    while not ev.query():
+        pass
+    return host[:n].tolist()
+
+
 def window_length_f32(d_max, s_max):
     """``L = ceil(1 + max d + max s) + 1`` with the sum rounded to fp32 after each addition,
     as the reference's fp32 tensors compute it (``delays.build_mask``, reference

@@ -18,7 +18,8 @@ Modes (reference ``recdel_base.py:361-383``):
 import torch
 
 from .. import _lib
-from ._common import bits_shape, drop_bn, require_device, round_half_even_f32, weights, window_length_f32
+from ._common import (bits_shape, drop_bn, read_scalars, require_device, round_half_even_f32, weights,
+                      window_length_f32)
 from .delays import build_lag, build_lag_interp
 
 
@@ -55,9 +56,9 @@ class AxonalRecdelHip(torch.autograd.Function):
         # The window length needs max d (and max s): the one device-to-host read of the call,
         # taken after the host work above so that it overlaps the GPU work still queued.
         if use_sig_p:
-            d_max, s_max = torch.stack([dc.max(), s_vec.max()]).tolist()
+            d_max, s_max = read_scalars(dc.max(), s_vec.max())
         else:
-            d_max, s_max = dc.max().item(), 1.0 + sigma
+            (d_max,), s_max = read_scalars(dc.max()), 1.0 + sigma
         lag = frac = None
         if ste_mode:
             L = window_length_f32(d_max, s_max)

@@ -12,7 +12,7 @@ followed by the lag-correlation GEMM, which folds ``dW = sum_l h * C_l`` and
 import torch
 
 from .. import _lib
-from ._common import bits_shape, drop_bn, lif_struct, require_device, weights, window_length_f64
+from ._common import bits_shape, drop_bn, lif_struct, read_scalars, require_device, weights, window_length_f64
 
 
 def _spread(layer, device):
@@ -39,9 +39,9 @@ def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop,
     # the window length needs max d (and max s): the one device-to-host read of the call,
     # taken after the host work above so that it overlaps the GPU work still queued
     if s_vec is not None:
-        d_max, s_max = torch.stack([d_all.max(), s_vec.max()]).tolist()
+        d_max, s_max = read_scalars(d_all.max(), s_vec.max())
     else:
-        d_max, s_max = d_all.max().item(), s_uniform
+        (d_max,), s_max = read_scalars(d_all.max()), s_uniform
     L = max(window_length_f64(d_max, s_max), 2)
     flags = w_bf16 | (2 if d_eff is None else 0)
     ws = _lib.workspace(_lib.WS_SYN_FWD, T, B, N, L, flags, dev)
