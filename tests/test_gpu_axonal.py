@@ -25,6 +25,9 @@ CASES = [
     (16, 3, 40, 6.0, 0.7, {'detach': True}),
     (16, 3, 40, 6.0, 0.7, {'sig_p': True}),
     (16, 3, 40, 6.0, 0.7, {'v_reset': -0.2}),
+    (16, 2, 200, 20.0, 1.0, {'bias': True}),     # 4 x 32 tiles with padded rows (128 < N < 256)
+    (16, 2, 136, 12.0, 0.6, {'sig_p': True}),
+    (16, 2, 256, 32.0, 1.0, {'cj16': True}),     # the 8 x 16 tile layout at the same size
     (16, 2, 300, 10.0, 0.5, {}),                 # streamed-weight layout (N > 256)
     (12, 2, 24, 70.0, 0.0, {}),                  # window > 64 lags: two history words
 ]
@@ -61,9 +64,11 @@ def _run(dev, T, B, N, dmax, sigma, extra, seed=0):
 @pytest.mark.gpu
 @pytest.mark.parametrize('case', CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}d{c[3]}s{c[4]}{"".join(c[5])}'
                                             for c in CASES])
-def test_axonal_fwd_bwd_matches_oracle(dev, case):
+def test_axonal_fwd_bwd_matches_oracle(dev, case, monkeypatch):
     T, B, N, dmax, sigma, extra = case
     print(f'case {case}', flush=True)
+    if extra.get('cj16'):
+        monkeypatch.setenv('DELREC_AXONAL_CJ', '16')
     y, y_ref, u_ref, gref, leaves, bg, pg, lif = _run(dev, T, B, N, dmax, sigma, extra)
     flip = first_flip(y, y_ref, u_ref, lif.v_threshold)
     assert flip is None, f'near-threshold flip at t={flip}; pick another seed'
