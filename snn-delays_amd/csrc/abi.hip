@@ -148,10 +148,12 @@ bool axonal_layout(int N, int L, AxLayout& o) {
 }
 
 // split-K count of the dW GEMM: about one 64x64-tile workgroup per CU, chunks >= 256 rows
+// k splits of the dW GEMM: about two 128x128-tile workgroups per CU (one hides the other's
+// load latency), chunks of >= 128 rows
 int dw_splits(int T, int B, int N) {
-    const int tiles = (N + 63) / 64;
-    return std::max(1, std::min((num_cus() + tiles * tiles - 1) / (tiles * tiles),
-                                std::max(1, T * B / 256)));
+    const int tiles = (N + 127) / 128;
+    const int want = (2 * num_cus() + tiles * tiles - 1) / (tiles * tiles);
+    return std::max(1, std::min(want, std::max(1, T * B / 128)));
 }
 
 template <class C>

@@ -1,72 +1,91 @@
-// MFMA (fp32, v_mfma_f32_16x16x4f32) reductions over the (t, b) axis of the backward.
+// Reductions over the (t, b) axis of the axonal backward, and the sums of split partials.
 //
 //   dw_gemm     dW[i,j] = sum_{t,b} gr[t,b,i] * z[t,b,j]: the axonal weight gradient, the
-//               reference's host GEMM at recdel_base.py:327-330. 128x128 tiles, split-K
-//               into deterministic partials (no atomics), summed by sum_partials.
+//               reference's host GEMM at recdel_base.py:327-330, on bf16 MFMA with split
+//               fp32 operands. 128x128 tiles, split-K into deterministic partials (no
+//               atomics), summed by sum_partials.
 //   lag_finish  dW, dd (and ds) from the split partials of the lag-correlation GEMM.
-//
-// MFMA 16x16x4 f32 operand layout (wave64): lane l supplies A[l%16][l/16] and
-// B[l/16][l%16]; accumulator register r of lane l holds D[4*(l/16) + r][l%16].
 #include "kernels.h"
 
 namespace delrec {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kDwTile = 64;
-constexpr int kDwKt = 32;
-constexpr int kDwPitch = kDwTile + 4;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// 64x64 output tile per workgroup (4 waves of 32x32, 2x2 MFMA blocks each); the K range
-// of the split is staged through two LDS buffers 32 rows at a time, the next stage's
-// global loads (float4) held in registers while the current stage is multiplied.
+constexpr int kDwTile = 128;   // output tile (i and j) per workgroup
+constexpr int kDwKt = 32;      // rows of k per stage (one MFMA K)
+
+__device__ __forceinline__ uint32_t dw_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// dW[i, j] = sum_k A[k, i] * Bm[k, j] on bf16 MFMA (v_mfma_f32_16x16x32_bf16) with both fp32
+// operands split into bf16 halves, x = hi + lo with hi = bf16(x), lo = bf16(x - hi): each
+// tile takes hi*hi + hi*lo + lo*hi (the lo*lo term is below 2^-32 of the product), so a
+// product carries a relative error of about 2^-16, accumulated in fp32. 128x128 output
+// tile per workgroup (4 waves of 64x64), split over k (blockIdx.z) into deterministic
+// partials. Each stage of 32 rows is read from global memory as 8-row runs of one column
+// (coalesced across the workgroup's columns), split, and stored in LDS k-blocked -- the 8
+// consecutive k of one column as 16 bytes, the run an MFMA lane supplies -- while the
+// previous stage is multiplied.
+// MFMA lane layout: lane l supplies A[l%16][8g .. 8g+7], B[8g .. 8g+7][l%16] (g = l/16, the
+// same k order for both operands); accumulator register r of lane l holds D[4g + r][l%16].
 __global__ void __launch_bounds__(256) dw_gemm_kernel(const float* __restrict__ A,
                                                       const float* __restrict__ Bm, int K, int N,
                                                       int kchunk, float* __restrict__ partial) {
-    __shared__ float sA[2][kDwKt][kDwPitch];
-    __shared__ float sB[2][kDwKt][kDwPitch];
+    // [buffer][operand A/B][hi/lo][k block][column] of 16-byte runs
+    __shared__ uint4 sm[2][2][2][kDwKt / 8][kDwTile];
     const int i0 = blockIdx.x * kDwTile, j0 = blockIdx.y * kDwTile, ks = blockIdx.z;
     const int kb = ks * kchunk, ke = min(K, kb + kchunk);
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int wi = w >> 1, wj = w & 1;
-    const int lr = lane >> 4, lc = lane & 15;
-    const bool vec = (N & 3) == 0;
-    // staging assignment: 32 rows x 16 float4 per matrix = 512 float4, 2 per thread
-    const int r0 = threadIdx.x >> 4, c4 = (threadIdx.x & 15) * 4;
-    floatx4 acc[2][2];
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int c = 0; c < 2; ++c) acc[a][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int g = lane >> 4, lc = lane & 15;
+    // staging: per operand 4 k-blocks x 128 columns = 512 runs, two per thread
+    const int col = tid & (kDwTile - 1), kq = tid >> 7;
 
-    float4 ra[2], rb[2];
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[a][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    float ra[2][8], rb[2][8];
     auto fetch = [&](int k0) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int k = k0 + r0 + 16 * h;
-            const bool kin = k < ke;
-            if (vec) {
-                ra[h] = (kin && i0 + c4 < N) ? *reinterpret_cast<const float4*>(A + (size_t)k * N + i0 + c4)
-                                             : float4{0.f, 0.f, 0.f, 0.f};
-                rb[h] = (kin && j0 + c4 < N) ? *reinterpret_cast<const float4*>(Bm + (size_t)k * N + j0 + c4)
-                                             : float4{0.f, 0.f, 0.f, 0.f};
-            } else {
-                float a4[4], b4[4];
+            const int kbase = k0 + (kq + 2 * h) * 8;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    a4[e] = (kin && i0 + c4 + e < N) ? A[(size_t)k * N + i0 + c4 + e] : 0.0f;
-                    b4[e] = (kin && j0 + c4 + e < N) ? Bm[(size_t)k * N + j0 + c4 + e] : 0.0f;
-                }
-                ra[h] = float4{a4[0], a4[1], a4[2], a4[3]};
-                rb[h] = float4{b4[0], b4[1], b4[2], b4[3]};
+            for (int e = 0; e < 8; ++e) {
+                const int k = kbase + e;
+                const bool kin = k < ke;
+                ra[h][e] = (kin && i0 + col < N) ? A[(size_t)k * N + i0 + col] : 0.0f;
+                rb[h][e] = (kin && j0 + col < N) ? Bm[(size_t)k * N + j0 + col] : 0.0f;
             }
         }
     };
     auto stash = [&](int buf) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            *reinterpret_cast<float4*>(&sA[buf][r0 + 16 * h][c4]) = ra[h];
-            *reinterpret_cast<float4*>(&sB[buf][r0 + 16 * h][c4]) = rb[h];
+            uint32_t ah[4], al[4], bh[4], bl[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const uint32_t a0 = dw_bf16_bits(ra[h][e]), a1 = dw_bf16_bits(ra[h][e + 1]);
+                const uint32_t b0 = dw_bf16_bits(rb[h][e]), b1 = dw_bf16_bits(rb[h][e + 1]);
+                ah[e / 2] = a0 | (a1 << 16);
+                bh[e / 2] = b0 | (b1 << 16);
+                al[e / 2] = dw_bf16_bits(ra[h][e] - __uint_as_float(a0 << 16)) |
+                            (dw_bf16_bits(ra[h][e + 1] - __uint_as_float(a1 << 16)) << 16);
+                bl[e / 2] = dw_bf16_bits(rb[h][e] - __uint_as_float(b0 << 16)) |
+                            (dw_bf16_bits(rb[h][e + 1] - __uint_as_float(b1 << 16)) << 16);
+            }
+            const int kbk = kq + 2 * h;
+            sm[buf][0][0][kbk][col] = uint4{ah[0], ah[1], ah[2], ah[3]};
+            sm[buf][0][1][kbk][col] = uint4{al[0], al[1], al[2], al[3]};
+            sm[buf][1][0][kbk][col] = uint4{bh[0], bh[1], bh[2], bh[3]};
+            sm[buf][1][1][kbk][col] = uint4{bl[0], bl[1], bl[2], bl[3]};
         }
     };
 
@@ -79,50 +98,94 @@ __global__ void __launch_bounds__(256) dw_gemm_kernel(const float* __restrict__ 
     for (int k0 = kb; k0 < ke; k0 += kDwKt) {
         const bool more = k0 + kDwKt < ke;
         if (more) fetch(k0 + kDwKt);
+        bf16x8 fah[4], fal[4], fbh[4], fbl[4];
 #pragma unroll
-        for (int kk = 0; kk < kDwKt; kk += 4) {
-            float av[2], bv[2];
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                av[q] = sA[buf][kk + lr][wi * 32 + q * 16 + lc];
-                bv[q] = sB[buf][kk + lr][wj * 32 + q * 16 + lc];
-            }
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int c = 0; c < 2; ++c)
-                    acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[c], acc[a][c], 0, 0, 0);
+        for (int q = 0; q < 4; ++q) {
+            fah[q] = __builtin_bit_cast(bf16x8, sm[buf][0][0][g][wi * 64 + q * 16 + lc]);
+            fal[q] = __builtin_bit_cast(bf16x8, sm[buf][0][1][g][wi * 64 + q * 16 + lc]);
+            fbh[q] = __builtin_bit_cast(bf16x8, sm[buf][1][0][g][wj * 64 + q * 16 + lc]);
+            fbl[q] = __builtin_bit_cast(bf16x8, sm[buf][1][1][g][wj * 64 + q * 16 + lc]);
         }
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fah[a], fbh[c], acc[a][c], 0, 0, 0);
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fah[a], fbl[c], acc[a][c], 0, 0, 0);
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fal[a], fbh[c], acc[a][c], 0, 0, 0);
+            }
         if (more) stash(buf ^ 1);
         __syncthreads();
         buf ^= 1;
     }
     float* P = partial + (size_t)ks * N * N;
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int i = i0 + wi * 32 + a * 16 + 4 * lr + r;
-                const int j = j0 + wj * 32 + c * 16 + lc;
+                const int i = i0 + wi * 64 + a * 16 + 4 * g + r;
+                const int j = j0 + wj * 64 + c * 16 + lc;
                 if (i < N && j < N) P[(size_t)i * N + j] = acc[a][c][r];
             }
 }
 
-__global__ void sum_partials_kernel(const float* __restrict__ partial, int ks, size_t count,
-                                    float* __restrict__ out) {
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= count) return;
-    float acc = 0.0f;
-    for (int k = 0; k < ks; ++k) acc += partial[(size_t)k * count + idx];
-    out[idx] = acc;
+// out[idx] = sum_k partial[k][idx]. A workgroup owns 64 float4 of the output; wave w sums
+// the partials k = w, w + 4, ... (loads issued together), and wave 0 adds the four in
+// order, so the result does not depend on timing.
+__global__ void __launch_bounds__(256) sum_partials_kernel(const float* __restrict__ partial, int ks,
+                                                           size_t count, float* __restrict__ out) {
+    __shared__ float4 red[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const size_t idx = ((size_t)blockIdx.x * 64 + lane) * 4;
+    const bool full = idx + 4 <= count;
+    float4 acc = float4{0.f, 0.f, 0.f, 0.f};
+    if (full) {
+        int k = w;
+        for (; k + 12 < ks; k += 16) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                v[u] = *reinterpret_cast<const float4*>(partial + (size_t)(k + 4 * u) * count + idx);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+            }
+        }
+        for (; k < ks; k += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(partial + (size_t)k * count + idx);
+            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+        }
+    } else {
+        float t4[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int k = w; k < ks; k += 4)
+            for (int e = 0; e < 4; ++e)
+                if (idx + e < count) t4[e] += partial[(size_t)k * count + idx + e];
+        acc = float4{t4[0], t4[1], t4[2], t4[3]};
+    }
+    red[w][lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+        float4 r = red[0][lane];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) {
+            r.x += red[q][lane].x; r.y += red[q][lane].y; r.z += red[q][lane].z; r.w += red[q][lane].w;
+        }
+        if (full) {
+            *reinterpret_cast<float4*>(out + idx) = r;
+        } else {
+            const float rr[4] = {r.x, r.y, r.z, r.w};
+            for (int e = 0; e < 4; ++e)
+                if (idx + e < count) out[idx + e] = rr[e];
+        }
+    }
 }
 
 void launch_dw_gemm(const float* A, const float* Bm, int K, int N, int ks, float* partial,
                     hipStream_t stream) {
     const int tiles = (N + kDwTile - 1) / kDwTile;
-    const int kchunk = (K + ks - 1) / ks;
+    const int kchunk = ((K + ks - 1) / ks + kDwKt - 1) / kDwKt * kDwKt;   // whole stages
     hipLaunchKernelGGL(dw_gemm_kernel, dim3(tiles, tiles, ks), dim3(256), 0, stream, A, Bm, K,
                        N, kchunk, partial);
 }
