@@ -161,7 +161,10 @@ void axonal_bwd_ws(C& c, int T, int B, int N, const AxLayout& lay) {
     c.template take<float>((size_t)3 * B * N);          // per-row partials
     c.template take<float>((size_t)T * B * N);          // gr (dropout / decay_input)
     c.template take<float>((size_t)dw_splits(T, B, N) * N * N);   // dW split-K partials
-    (void)lay;
+    if (lay.res) {
+        c.template take<float>((size_t)T * B * N);                                    // gz
+        c.template take<float>((size_t)2 * axonal_delay_segments(T) * B * N);         // dd, ds partials
+    }
 }
 
 // ------------------------------------------------------------------ synaptic layout ----
@@ -463,7 +466,10 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     float* grbuf = cv.take<float>((size_t)T * B * N);
     const int ks = dw_splits(T, B, N);
     float* gemm_part = cv.take<float>((size_t)ks * N * N);
-    if (!part || !grbuf || !gemm_part) return DELREC_ERR_WORKSPACE;
+    float* gzbuf = lay.res ? cv.take<float>((size_t)T * B * N) : nullptr;
+    const int segs = axonal_delay_segments(T);
+    float* dpart = lay.res ? cv.take<float>((size_t)2 * segs * B * N) : nullptr;
+    if (!part || !grbuf || !gemm_part || (lay.res && (!gzbuf || !dpart))) return DELREC_ERR_WORKSPACE;
     const bool need_gr = a->drop != nullptr || a->lif.decay_input;
 
     AxBwd p{};
@@ -472,7 +478,7 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     p.gy = a->gy; p.u = a->u; p.bits = a->bits; p.W = a->W; p.w_bf16 = a->w_bf16;
     p.d = a->d; p.s = a->s; p.s_uniform = a->s_uniform; p.drop = a->drop;
     p.mode = a->mode; p.lag = a->lag; p.lif = make_lif(a->lif);
-    p.dx = a->dx; p.gr = need_gr ? grbuf : nullptr; p.part = part;
+    p.dx = a->dx; p.gr = need_gr ? grbuf : nullptr; p.part = part; p.gz = gzbuf; p.dpart = dpart;
     const bool timed = scan_begin(DELREC_WS_AXONAL_BWD, s);
     const bool ok = lay.res ? launch_axonal_tiled(false, nullptr, &p, lay.ri, lay.G, lay.CH, lay.hw, B, lay.block, lds, s)
                             : launch_axonal(false, nullptr, &p, lay.CH, lay.res, lay.hw, B, lay.block, lds, s);
@@ -480,7 +486,16 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();
     if (st) return st;
-    launch_reduce_rows(part, B, N, a->db, a->dd, a->ds, s);
+    if (lay.res) {
+        // the tiled scan leaves db partials; dd / ds come from the segment pass
+        launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
+        if (a->dd || a->ds) {
+            launch_axonal_delay_grad(p, s);
+            launch_reduce_rows(dpart, segs * B, N, a->dd, a->ds, nullptr, s);
+        }
+    } else {
+        launch_reduce_rows(part, B, N, a->db, a->dd, a->ds, s);
+    }
     if (a->dW) {
         launch_dw_gemm(need_gr ? grbuf : a->dx, a->z, T * B, N, ks, gemm_part, s);
         launch_sum_partials(gemm_part, ks, (size_t)N * N, a->dW, s);

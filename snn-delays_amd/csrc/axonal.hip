@@ -545,13 +545,10 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
             w[a][cc] = (i < N && j < N) ? load_w(p.W, p.w_bf16, (size_t)i * N + j) : 0.0f;
         }
 
-    // Source j = grp*RI + a runs its LIF chain on lane (grp, a); when the group has 2*RI
-    // lanes, lane (grp, RI + a) accumulates its delay / half-width gradient concurrently.
-    const bool split = NJ >= 2 * RI;
-    const int ja = grp * RI + (jcg % RI);
-    const bool nl = jcg < RI && ja < N;                                    // LIF lanes
-    const bool dl = split ? (jcg >= RI && jcg < 2 * RI && ja < N) : nl;    // delay-gradient lanes
-    const int j = (nl || dl) ? ja : 0;
+    // Source j = grp*RI + a runs its LIF chain on lane (grp, a). Its dL/dz is stored (gz)
+    // for the delay-gradient pass, which keeps that work off the sequential scan.
+    const bool nl = jcg < RI && grp * RI + jcg < N;                      // LIF lanes
+    const int j = nl ? grp * RI + jcg : 0;
     OneHot<RI> sel;
     sel.init(jcg % RI);
     const float c = 1.0f + p.d[j];
@@ -562,26 +559,14 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
     const int nt = hi - lo + 1;
     const bool soft = p.mode == DELREC_BWD_SOFT;
     const bool fast = soft && nt <= kMaxTaps && HW == 1;
-    const bool need_ds = p.s != nullptr;
-    float dsg[kMaxTaps], wq[kMaxTaps];
+    float wq[kMaxTaps];
 #pragma unroll
-    for (int q = 0; q < kMaxTaps; ++q) {
-        dsg[q] = (q < nt) ? tri_dsign((float)(lo + q), c, s) : 0.0f;
-        wq[q] = (q < nt) ? tri_weight((float)(lo + q), c, s, s2) : 0.0f;
-    }
+    for (int q = 0; q < kMaxTaps; ++q) wq[q] = (q < nt) ? tri_weight((float)(lo + q), c, s, s2) : 0.0f;
     const int lag = p.lag ? p.lag[j] : 1;
     const float m = p.drop ? p.drop[(size_t)b * N + j] : 1.0f;
 
     for (int q = tid; q < 2 * NZ + R * NP; q += blockDim.x) smem[q] = 0.0f;
     __syncthreads();
-
-    History<HW> past;   // delay lanes: bit(l) = y[tw - l] for the window time tw
-    past.clear();
-    SpikeStream oldest; // the bit that enters the window at lag 64*HW
-    if (dl) {
-        for (int l = 64 * HW; l >= 1; --l) past.push(spike_bit(p.bits, TW, N, b, T - 1 - l, j));
-        oldest.init(p.bits, TW, N, b, j, T - 2 - 64 * HW);
-    }
 
     const size_t BN = (size_t)B * N;
     const size_t rowj = (size_t)b * N + j;
@@ -592,29 +577,7 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
         gq[q] = (nl && tt >= 0) ? p.gy[(size_t)tt * BN + rowj] : 0.0f;
         uq[q] = (nl && tt >= 0) ? p.u[(size_t)tt * BN + rowj] : 0.0f;
     }
-    float lam = 0.0f, db_acc = 0.0f, dd_acc = 0.0f, ds_acc = 0.0f;
-
-    // dd / ds contribution of gz at the window time: dL/dh[j,l] = gz * y[tw-l]
-    auto delay_grad = [&](float gz) {
-        if (fast && !need_ds) {
-            const uint32_t ps = (uint32_t)(past.w[0] >> (lo - 1));
-            float sd = 0.0f;
-#pragma unroll
-            for (int q = 0; q < kMaxTaps; ++q) sd += ((ps >> q) & 1u) ? dsg[q] : 0.0f;
-            dd_acc += gz * sd;
-        } else if (soft) {
-            float sd = 0.0f, sds = 0.0f;
-            for (int l = lo; l <= hi; ++l) {
-                const float yv = past.bit(l);
-                sd += tri_dsign((float)l, c, s) * yv;
-                if (need_ds) sds += tri_ds((float)l, c, s, s2) * yv;
-            }
-            dd_acc += gz * sd;
-            ds_acc += gz * sds;
-        } else {
-            dd_acc += gz * (past.bit(lag + 1) - past.bit(lag));
-        }
-    };
+    float lam = 0.0f, db_acc = 0.0f;
 
     // gz(t+1) of this lane's source: W^T-tile contraction of gr(t+1), reduced in the group
     auto contract = [&](int buf) {
@@ -643,12 +606,9 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
     auto step = [&](const int t, float& gs, float& us) {
         const float gz1 = contract((t + 1) & 1);       // gz(t+1); gr(T) = 0
         const int tm = tn1 == 0 ? R - 1 : tn1 - 1;     // slot of time t
-        if (nl) ring[tn1 * NP + j] = gz1;
-        if (dl && t < T - 1) {
-            delay_grad(gz1);                           // gz(t+1) with the window of t+1
-            past.pull(oldest.bit(t - 64 * HW));
-        }
         if (nl) {
+            ring[tn1 * NP + j] = gz1;
+            if (t + 1 < T) p.gz[(size_t)(t + 1) * BN + rowj] = gz1;
             float gfut = 0.0f;
             if (fast) {
                 // taps past the support weigh 0 and ring slots of times >= T hold 0
@@ -697,13 +657,108 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
         for (int q = 0; q < kPrefetchBwd; ++q)
             if (t0 - q >= 0) step(t0 - q, gq[q], uq[q]);
     }
-    const float gz0 = contract(0);                     // gz(0) with the window of 0
-    if (dl) {
-        delay_grad(gz0);
-        p.part[(size_t)1 * B * N + rowj] = soft ? dd_acc / s2 : dd_acc;
-        p.part[(size_t)2 * B * N + rowj] = ds_acc;
+    const float gz0 = contract(0);                     // gz(0)
+    if (nl) {
+        p.gz[rowj] = gz0;
+        p.part[(size_t)0 * B * N + rowj] = db_acc;
     }
-    if (nl) p.part[(size_t)0 * B * N + rowj] = db_acc;
+}
+
+// Delay / half-width gradient partials after the tiled scan, one (32-step segment, b, j)
+// per thread:
+//   dd_j += sum_t gz_j(t) sum_l dh/dd(l) y_j(t - l)   (soft: the closed-form triangle
+//   derivative / s^2; straight: y(t - lag - 1) - y(t - lag)),  ds_j likewise with dh/ds.
+// A thread first pushes the 64*HW spikes before its segment into a History register (as
+// the forward does), loads its 32 gz values together, then walks the segment; the
+// segment partials are summed with the batch rows by reduce_rows.
+constexpr int kDelaySeg = 32;
+
+__host__ __device__ int axonal_delay_segments(int T) { return (T + kDelaySeg - 1) / kDelaySeg; }
+
+template <int HW>
+__global__ void __launch_bounds__(256) axonal_delay_grad_kernel(AxBwd p) {
+    const int N = p.N, T = p.T, B = p.B;
+    const size_t BN = (size_t)B * N;
+    const int S = axonal_delay_segments(T);
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (size_t)S * BN) return;
+    const int seg = (int)(q / BN);
+    const size_t rem = q - (size_t)seg * BN;
+    const int b = (int)(rem / N), j = (int)(rem - (size_t)b * N);
+    const float c = 1.0f + p.d[j];
+    const float s = p.s ? p.s[j] : p.s_uniform;
+    const float s2 = s * s;
+    int lo, hi;
+    tap_range(c, s, p.L, lo, hi);
+    const int nt = hi - lo + 1;
+    const bool soft = p.mode == DELREC_BWD_SOFT;
+    const bool need_ds = p.s != nullptr;
+    const bool fast = soft && !need_ds && nt <= kMaxTaps && HW == 1;
+    const int lag = p.lag ? p.lag[j] : 1;
+    float dsg[kMaxTaps];
+#pragma unroll
+    for (int k = 0; k < kMaxTaps; ++k) dsg[k] = (k < nt) ? tri_dsign((float)(lo + k), c, s) : 0.0f;
+    const int TW = (T + 31) >> 5;
+    const int t0 = seg * kDelaySeg;
+
+    float gzq[kDelaySeg];
+#pragma unroll
+    for (int e = 0; e < kDelaySeg; ++e)
+        gzq[e] = (t0 + e < T) ? p.gz[(size_t)(t0 + e) * BN + rem] : 0.0f;
+
+    // bit(l) = y(t0 - l): word w of the row holds steps 32w .. 32w + 31 (bit k = step 32w + k),
+    // so lags 1..32 are the bit-reversed word seg - 1, lags 33..64 word seg - 2, and so on
+    History<HW> past;
+    const uint32_t* col = p.bits + (size_t)b * TW * N + j;
+#pragma unroll
+    for (int h = 0; h < HW; ++h) {
+        const int w1 = seg - 2 * h - 1, w2 = seg - 2 * h - 2;
+        const uint32_t a1 = w1 >= 0 ? col[(size_t)w1 * N] : 0u;
+        const uint32_t a2 = w2 >= 0 ? col[(size_t)w2 * N] : 0u;
+        past.w[h] = (uint64_t)__brev(a1) | ((uint64_t)__brev(a2) << 32);
+    }
+    const uint32_t word = col[(size_t)seg * N];                        // steps t0 .. t0 + 31
+
+    float dd = 0.0f, ds = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kDelaySeg; ++e) {
+        if (t0 + e >= T) break;
+        const float gz = gzq[e];
+        if (fast) {
+            const uint32_t ps = (uint32_t)(past.w[0] >> (lo - 1));
+            float sd = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kMaxTaps; ++k) sd += ((ps >> k) & 1u) ? dsg[k] : 0.0f;
+            dd += gz * sd;
+        } else if (soft) {
+            float sd = 0.0f, sds = 0.0f;
+            for (int l = lo; l <= hi; ++l) {
+                const float yv = past.bit(l);
+                sd += tri_dsign((float)l, c, s) * yv;
+                if (need_ds) sds += tri_ds((float)l, c, s, s2) * yv;
+            }
+            dd += gz * sd;
+            ds += gz * sds;
+        } else {
+            dd += gz * (past.bit(lag + 1) - past.bit(lag));
+        }
+        past.push((word >> e) & 1u);
+    }
+    const size_t SBN = (size_t)S * BN;
+    p.dpart[q] = soft ? dd / s2 : dd;
+    p.dpart[SBN + q] = ds;
+}
+
+void launch_axonal_delay_grad(const AxBwd& p, hipStream_t stream) {
+    const size_t n = (size_t)axonal_delay_segments(p.T) * p.B * p.N;
+    const unsigned blocks = (unsigned)((n + 255) / 256);
+    const int lags = std::max(p.L - 1, 1);
+    if (lags <= 64)
+        hipLaunchKernelGGL(axonal_delay_grad_kernel<1>, dim3(blocks), dim3(256), 0, stream, p);
+    else if (lags <= 128)
+        hipLaunchKernelGGL(axonal_delay_grad_kernel<2>, dim3(blocks), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(axonal_delay_grad_kernel<4>, dim3(blocks), dim3(256), 0, stream, p);
 }
 
 // Sum the per-row partials over the batch: out_k[j] = sum_b part[k][b][j]. Block (64, 16):

@@ -46,6 +46,8 @@ struct AxBwd {
     float* dx;
     float* gr;                 // (T,B,N) dL/drec, written when it differs from dx, else NULL
     float* part;               // [3][B][N] per-row partials of db, dd, ds
+    float* gz;                 // (T,B,N) dL/dz of the tiled scan, read by the delay-gradient pass
+    float* dpart;              // [2][S*B][N] dd, ds partials of the delay-gradient pass
 };
 
 struct SynFwd {
@@ -136,6 +138,9 @@ bool launch_axonal(bool fwd, const AxFwd* fa, const AxBwd* ba, int ch, bool res,
                    int grid, int block, size_t lds, hipStream_t stream);
 bool launch_axonal_tiled(bool fwd, const AxFwd* fa, const AxBwd* ba, int ri, int nj, int cj, int hw,
                          int grid, int block, size_t lds, hipStream_t stream);
+// dd / ds partials per (32-step segment, b, j) from the tiled scan's gz and the spike bits
+__host__ __device__ int axonal_delay_segments(int T);
+void launch_axonal_delay_grad(const AxBwd& p, hipStream_t stream);
 void launch_reduce_rows(const float* part, int B, int N, float* o0, float* o1, float* o2,
                         hipStream_t stream);
 
