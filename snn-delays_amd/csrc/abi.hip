@@ -147,6 +147,17 @@ bool axonal_layout(int N, int L, AxLayout& o) {
     return true;
 }
 
+// The spike-driven forward (axonal_fwd_wave) serves N <= 256 unless DELREC_AXONAL_FWD=tiled
+// selects the dense tiled scan (kept for comparison).
+bool axonal_fwd_wave_on() {
+    static int on = -1;
+    if (on < 0) {
+        const char* e = getenv("DELREC_AXONAL_FWD");
+        on = (e && strcmp(e, "tiled") == 0) ? 0 : 1;
+    }
+    return on == 1;
+}
+
 // split-K count of the dW GEMM: about one 64x64-tile workgroup per CU, chunks >= 256 rows
 // k splits of the dW GEMM: about two 128x128-tile workgroups per CU (one hides the other's
 // load latency), chunks of >= 128 rows
@@ -438,8 +449,28 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
         p.Wt = wt;
     }
     const bool timed = scan_begin(DELREC_WS_AXONAL_FWD, s);
-    const bool ok = lay.res ? launch_axonal_tiled(true, &p, nullptr, lay.ri, lay.G, lay.CH, lay.hw, a->B, lay.block, lds, s)
-                            : launch_axonal(true, &p, nullptr, lay.CH, lay.res, lay.hw, a->B, lay.block, lds, s);
+    bool ok;
+    if (lay.res && axonal_fwd_wave_on()) {
+        // spike-driven form: ceil(N/32) waves of 32 source columns, RI receivers per lane
+        const int nw = (a->N + 31) / 32;
+        const int ri = a->N > 128 ? 4 : (a->N > 64 ? 2 : 1);
+        // the straight-line variant: soft taps of a uniform half-width (kf >= ceil(2s) lags
+        // of non-zero weight), one history word, decay charge, hard reset to 0, no rec
+        const float span = ceilf(2.0f * a->s_uniform);
+        const int kf = span <= 2.0f ? 2 : (span <= 4.0f ? 4 : 8);
+        const bool common = a->taps == DELREC_TAPS_SOFT && lay.hw == 1 && !a->s &&
+                            a->s_uniform > 0.0f && span <= 8.0f && !a->lif.decay_input &&
+                            !a->lif.soft_reset && a->lif.v_reset == 0.0f && !a->rec;
+        if (common) {
+            ok = launch_axonal_fwd_wave_fast(p, ri, kf, nw, a->B, s);
+        } else {
+            const size_t lds_w = (size_t)2 * nw * 64 * ri * sizeof(float);
+            ok = launch_axonal_fwd_wave(p, ri, lay.hw, nw, a->B, lds_w, s);
+        }
+    } else {
+        ok = lay.res ? launch_axonal_tiled(true, &p, nullptr, lay.ri, lay.G, lay.CH, lay.hw, a->B, lay.block, lds, s)
+                     : launch_axonal(true, &p, nullptr, lay.CH, lay.res, lay.hw, a->B, lay.block, lds, s);
+    }
     scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     return finish_launch();
@@ -480,8 +511,23 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     p.mode = a->mode; p.lag = a->lag; p.lif = make_lif(a->lif);
     p.dx = a->dx; p.gr = need_gr ? grbuf : nullptr; p.part = part; p.gz = gzbuf; p.dpart = dpart;
     const bool timed = scan_begin(DELREC_WS_AXONAL_BWD, s);
-    const bool ok = lay.res ? launch_axonal_tiled(false, nullptr, &p, lay.ri, lay.G, lay.CH, lay.hw, B, lay.block, lds, s)
-                            : launch_axonal(false, nullptr, &p, lay.CH, lay.res, lay.hw, B, lay.block, lds, s);
+    // the straight-line tiled backward: soft taps of a uniform half-width (kf >= ceil(2s)
+    // lags of non-zero weight), one history word, ATan, decay charge, hard reset to 0
+    const float span = ceilf(2.0f * a->s_uniform);
+    const int kf = span <= 2.0f ? 2 : (span <= 4.0f ? 4 : 8);
+    const bool common = lay.res && axonal_fwd_wave_on() && a->mode == DELREC_BWD_SOFT && lay.hw == 1 &&
+                        !a->s && a->s_uniform > 0.0f && span <= 8.0f && a->lif.surrogate == 1 &&
+                        !a->lif.decay_input && !a->lif.soft_reset && a->lif.v_reset == 0.0f &&
+                        !a->lif.detach_reset;
+    bool ok;
+    if (common) {
+        const size_t lds_f = ((size_t)2 * lay.NZ + (size_t)(R + kf - 1) * NP) * sizeof(float);
+        ok = lds_f <= (size_t)max_lds_bytes() &&
+             launch_axonal_bwd_tiled_fast(p, lay.ri, lay.G, lay.CH, kf, B, lay.block, lds_f, s);
+    } else {
+        ok = lay.res ? launch_axonal_tiled(false, nullptr, &p, lay.ri, lay.G, lay.CH, lay.hw, B, lay.block, lds, s)
+                     : launch_axonal(false, nullptr, &p, lay.CH, lay.res, lay.hw, B, lay.block, lds, s);
+    }
     scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();

@@ -416,13 +416,10 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_fwd_tiled(AxFw
     const int TW = (T + 31) >> 5;
 
     float w[RI][CJ];
-#pragma unroll
-    for (int a = 0; a < RI; ++a)
-#pragma unroll
-        for (int c = 0; c < CJ; ++c) {
-            const int i = grp * RI + a, j = jcg * CJ + c;
-            w[a][c] = (i < N && j < N) ? load_w(p.W, p.w_bf16, (size_t)i * N + j) : 0.0f;
-        }
+    load_w_tile<RI, CJ>(w, p.W, p.w_bf16, N, [&](int a, int c, int& i, int& j) {
+        i = grp * RI + a;
+        j = jcg * CJ + c;
+    });
 
     // neuron lanes: neuron i = grp * RI + jcg on the lanes jcg < RI
     const bool nl = jcg < RI && grp * RI + jcg < N;
@@ -522,6 +519,312 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_fwd_tiled(AxFw
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Spike-driven forward for N <= 256. Wave w owns the source block j = 32w .. 32w + 31 for
+// every receiver (lane l holds W[RI*l + a][32w + c] in VGPRs) and runs the LIF chain of
+// those 32 neurons on its lanes 0..31. Its delayed trace z(t) stays in the lane of the
+// source; a wave ballot of z != 0 gives the active columns of the block, and the
+// contraction walks only those (the column index is wave-uniform, so the weight column
+// is picked with GPR-index addressing and z with readlane). At typical firing rates that
+// is a small fraction of the dense product. The per-wave partial sums of every receiver
+// cross waves through LDS: one barrier per step, no z traffic through memory.
+constexpr int kPrefetchWave = 8;   // steps of x loaded ahead of use
+
+typedef float wcol32 __attribute__((ext_vector_type(32)));
+
+template <int RI>
+__device__ __forceinline__ void store_partials(float* dst, const float (&acc)[RI]) {
+    if constexpr (RI == 4) {
+        *reinterpret_cast<float4*>(dst) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    } else if constexpr (RI == 2) {
+        *reinterpret_cast<float2*>(dst) = make_float2(acc[0], acc[1]);
+    } else {
+        dst[0] = acc[0];
+    }
+}
+
+template <int RI, int HW>
+__global__ void __launch_bounds__(512) axonal_fwd_wave(AxFwd p) {
+    extern __shared__ float smem[];
+    constexpr int ROWS = 64 * RI;                  // receivers covered by one wave's lanes
+    const int N = p.N, T = p.T, B = p.B;
+    const int NW = blockDim.x >> 6;                // waves = source blocks of 32
+    float* part = smem;                            // [2][NW][ROWS]
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6, l = tid & 63;
+    const Lif k = p.lif;
+    const int TW = (T + 31) >> 5;
+
+    wcol32 w[RI];
+    load_w_tile<RI, 32>(w, p.W, p.w_bf16, N, [&](int a, int c, int& i, int& j) {
+        i = RI * l + a;
+        j = 32 * wv + c;
+    });
+
+    // neuron lanes: neuron i = 32 * wv + l on lanes l < 32
+    const bool nl = l < 32 && 32 * wv + l < N;
+    const int i = nl ? 32 * wv + l : 0;
+    const float c = 1.0f + p.d[i];
+    const float s = p.s ? p.s[i] : p.s_uniform;
+    const float s2 = s * s;
+    int lo, hi;
+    tap_range(c, s, p.L, lo, hi);
+    const int nt = hi - lo + 1;
+    const bool fast = p.taps == DELREC_TAPS_SOFT && nt <= kMaxTaps && HW == 1;
+    float wq[kMaxTaps];
+#pragma unroll
+    for (int q = 0; q < kMaxTaps; ++q) wq[q] = (q < nt) ? tri_weight((float)(lo + q), c, s, s2) : 0.0f;
+    const int lag = p.lag ? p.lag[i] : 1;
+    const float frac = p.frac ? p.frac[i] : 0.0f;
+    const float m = p.drop ? p.drop[(size_t)b * N + i] : 1.0f;
+    const float bias = p.bias ? p.bias[i] : 0.0f;
+
+    History<HW> hist;
+    hist.clear();
+    float v = k.v0;
+    uint32_t word = 0;
+    const size_t BN = (size_t)B * N;
+    const size_t row = (size_t)b * N + i;
+    float xq[kPrefetchWave];
+#pragma unroll
+    for (int q = 0; q < kPrefetchWave; ++q) xq[q] = (nl && q < T) ? p.x[(size_t)q * BN + row] : 0.0f;
+    if (nl && p.z) p.z[row] = 0.0f;
+
+    float zcur = 0.0f;         // z(t) of this lane's source (0 off the neuron lanes)
+    uint32_t zmask = 0;        // lanes of this wave whose z(t) != 0 (wave-uniform)
+
+    // one time step; `xs` is this step's prefetch slot, refilled with x[t + kPrefetchWave]
+    // (static slots: a register with a load in flight is never moved)
+    auto step = [&](const int t, float& xs) {
+        float acc[RI];
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc[a] = 0.0f;
+        uint32_t mk = __builtin_amdgcn_readfirstlane(zmask);
+        while (mk) {
+            const int cc = __builtin_ctz(mk);
+            mk &= mk - 1u;
+            const float zc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(zcur), cc));
+#pragma unroll
+            for (int a = 0; a < RI; ++a) acc[a] = fmaf(w[a][cc], zc, acc[a]);
+        }
+        float* pt = part + (t & 1) * NW * ROWS;
+        store_partials<RI>(pt + wv * ROWS + RI * l, acc);
+        // refill the slot on every lane, outside the divergent region and with a clamped
+        // (always valid) step, so the load never has to land before a later step reads it
+        const float xv = xs;
+        xs = p.x[(size_t)min(t + kPrefetchWave, T - 1) * BN + row];
+        barrier_lds();
+
+        float zn = 0.0f;
+        if (nl && t < T) {
+            float r = 0.0f;
+            for (int q = 0; q < NW; ++q) r += pt[q * ROWS + i];
+            r += bias;
+            const float a = xv + r * m;
+            const float u = lif_charge(k, v, a);
+            const float y = lif_fire(k, u);
+            v = lif_reset(k, u, y);
+            const uint32_t yb = y != 0.0f ? 1u : 0u;
+            hist.push(yb);
+            word |= yb << (t & 31);
+            const size_t o = (size_t)t * BN + row;
+            p.y[o] = y;
+            p.u[o] = u;
+            if (p.rec) p.rec[o] = r;
+            if ((t & 31) == 31 || t == T - 1) {
+                p.bits[((size_t)b * TW + (t >> 5)) * N + i] = word;
+                word = 0;
+            }
+            if (t + 1 < T) {
+                if (fast) {
+                    const uint32_t hs = (uint32_t)(hist.w[0] >> (lo - 1));
+#pragma unroll
+                    for (int q = 0; q < kMaxTaps; ++q) zn += ((hs >> q) & 1u) ? wq[q] : 0.0f;
+                } else {
+                    zn = axonal_trace<HW>(hist, p.taps, c, s, s2, lo, hi, lag, frac);
+                }
+                if (p.z) p.z[(size_t)(t + 1) * BN + row] = zn;
+            }
+        }
+        zcur = zn;
+        zmask = (uint32_t)__ballot(zn != 0.0f);
+    };
+
+    // whole blocks of kPrefetchWave steps (a step t >= T does no neuron work): a guard
+    // around a step would make its prefetch slot a merge that waits for the load
+    for (int t0 = 0; t0 < T; t0 += kPrefetchWave) {
+#pragma unroll
+        for (int q = 0; q < kPrefetchWave; ++q) step(t0 + q, xq[q]);
+    }
+}
+
+// The same spike-driven scan specialised for the common regime (chosen by the host):
+// soft triangle taps of a uniform half-width s with at most KF lags of non-zero weight
+// (KF >= ceil(2s)) inside one 64-step history word, charge u = decay * v + a, hard reset
+// to 0, no recurrent-input output.
+//
+// The step is software-pipelined around the one dependency that really crosses a step:
+// a source whose first non-zero tap is at lag 1 ("fast", d < 2 + ... ) needs this step's
+// spike to form its z(t+1); every other source's z(t+1) is fixed by spikes up to t-1.
+// So while the LDS reads of r(t)'s partial sums are in flight, each wave forms the
+// pre-step traces zpre(t+1) and contracts its slow active columns for step t+1; after
+// the LIF only the fast sources' lag-1 term and their (few) columns remain on the
+// critical path. Stores and the x prefetch use buffer descriptors in SGPRs.
+template <int RI, int KF>
+__global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
+    extern __shared__ float smem[];
+    constexpr int ROWS = 64 * RI;
+    constexpr int NWMAX = 8;
+    const int N = p.N, T = p.T, B = p.B;
+    float* part = smem;                            // [2][NWMAX][ROWS]
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6, l = tid & 63;
+    const int TW = (T + 31) >> 5;
+    const float decay = p.lif.decay, vth = p.lif.vth;
+
+    wcol32 w[RI];
+    load_w_tile<RI, 32>(w, p.W, p.w_bf16, N, [&](int a, int c, int& i, int& j) {
+        i = RI * l + a;
+        j = 32 * wv + c;
+    });
+
+    const bool nl = l < 32 && 32 * wv + l < N;
+    const int i = nl ? 32 * wv + l : 0;
+    const float c = 1.0f + p.d[i];
+    const float s = p.s_uniform;
+    const float s2 = s * s;
+    // lags of non-zero weight: l > c - s, l >= 1 (at most KF of them: l < c + s)
+    const int lof = max(1, (int)floorf(c - s) + 1);
+    int wq[KF];                // tap weights as bit patterns (masked by the spike bits)
+#pragma unroll
+    for (int q = 0; q < KF; ++q) {
+        const int lq = lof + q;
+        wq[q] = __float_as_int(lq <= p.L - 1 ? tri_weight((float)lq, c, s, s2) : 0.0f);
+    }
+    const bool fastn = nl && lof == 1;             // z(t+1) needs y(t)
+    const bool slown = nl && lof >= 2;
+    const float w0 = fastn ? __int_as_float(wq[0]) : 0.0f;
+    const float m = p.drop ? p.drop[(size_t)b * N + i] : 1.0f;
+    const float bias = p.bias ? p.bias[i] : 0.0f;
+
+    for (int q = tid; q < 2 * NWMAX * ROWS; q += blockDim.x) part[q] = 0.0f;
+    __syncthreads();
+
+    // hist bit k = y(t-1-k) at the start of step t. zpre(t+1) = sum_q w_q y(t+1-lof-q)
+    // over the known spikes: bit (lof - 2 + q); for a fast source the q = 0 term is y(t).
+    uint64_t hist = 0;
+    float v = 0.0f;
+    uint32_t word = 0;
+    const size_t BN = (size_t)B * N;
+    const uint32_t row_bytes = (uint32_t)BN * 4u;  // one step of a (T, B, N) tensor
+    const int voff = (b * N + i) * 4;              // this lane's byte offset within a step
+    // stores of lanes without a neuron go past the buffer end (dropped): every memory
+    // operation of a step is unconditional, so the compiler's counts of outstanding
+    // loads / stores are exact and a prefetched value never waits on later stores
+    const int soff = nl ? voff : kOutOfRange;
+    const int boff = nl ? (b * TW * N + i) * 4 : kOutOfRange;   // spike-bit word of step 0
+    float* const zout = p.z;
+    float xq[kPrefetchWave];
+#pragma unroll
+    for (int q = 0; q < kPrefetchWave; ++q)
+        xq[q] = raw_buffer_load_f32(buffer_rsrc(p.x + (size_t)q * BN, q < T ? row_bytes : 0u), voff, 0, 0);
+    if (nl && zout) zout[(size_t)b * N + i] = 0.0f;
+
+    float zcur = 0.0f;                             // z(t) of this lane's source
+    uint32_t mkf = 0;                              // fast sources with z(t) != 0
+    float acc_s[RI];                               // slow columns of W z(t)
+#pragma unroll
+    for (int a = 0; a < RI; ++a) acc_s[a] = 0.0f;
+
+    auto step = [&](const int t, float& xs) {
+        // fast columns of z(t) on top of the slow part formed during the previous step
+        float acc[RI];
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc[a] = acc_s[a];
+        uint32_t mk = __builtin_amdgcn_readfirstlane(mkf);
+        while (mk) {
+            const int cc = __builtin_ctz(mk);
+            mk &= mk - 1u;
+            const float zc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(zcur), cc));
+            float wt[RI];
+#pragma unroll
+            for (int a = 0; a < RI; ++a) wt[a] = w[a][cc];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int a = 0; a < RI; ++a) acc[a] = fmaf(wt[a], zc, acc[a]);
+        }
+        float* pt = part + (t & 1) * NWMAX * ROWS;
+        store_partials<RI>(pt + wv * ROWS + RI * l, acc);
+        barrier_lds();
+        float pr[NWMAX];                           // r(t) partials, read before the slow work
+#pragma unroll
+        for (int q = 0; q < NWMAX; ++q) pr[q] = pt[q * ROWS + i];
+
+        // in the shadow of those reads: zpre(t+1) and the slow columns of W z(t+1)
+        const uint64_t hk = lof >= 2 ? (hist >> (lof - 2)) : (hist << 1);
+        const uint32_t hs = (uint32_t)hk;
+        float zpre = 0.0f;
+#pragma unroll
+        for (int q = 0; q < KF; ++q) zpre += __int_as_float(wq[q] & -(int)((hs >> q) & 1u));
+        const bool next = t + 1 < T;
+        zpre = next ? zpre : 0.0f;
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc_s[a] = 0.0f;
+        uint32_t ms = __builtin_amdgcn_readfirstlane((uint32_t)__ballot(slown && zpre != 0.0f));
+        while (ms) {
+            const int cc = __builtin_ctz(ms);
+            ms &= ms - 1u;
+            const float zc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(zpre), cc));
+            float wt[RI];
+#pragma unroll
+            for (int a = 0; a < RI; ++a) wt[a] = w[a][cc];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int a = 0; a < RI; ++a) acc_s[a] = fmaf(wt[a], zc, acc_s[a]);
+        }
+
+        // r(t) and the LIF step
+        float r = pr[0];
+#pragma unroll
+        for (int q = 1; q < NWMAX; ++q) r += pr[q];
+        r += bias;
+        const float a = xs + r * m;
+        const float u = v * decay + a;
+        const bool fire = u - vth >= 0.0f;
+        v = fire ? 0.0f : u;
+        hist = (hist << 1) | (uint64_t)(fire ? 1u : 0u);
+        word |= (fire ? 1u : 0u) << (t & 31);
+        // z(t+1): the fast sources add their lag-1 tap
+        float zn = (fastn && fire) ? w0 + zpre : zpre;
+        zn = (nl && next) ? zn : 0.0f;
+        mkf = (uint32_t)__ballot(fastn && zn != 0.0f);
+        zcur = zn;
+
+        // outputs; steps t >= T store nothing (their descriptors have no records)
+        const uint32_t live = t < T ? row_bytes : 0u;
+        raw_buffer_store_f32(fire ? 1.0f : 0.0f, buffer_rsrc(p.y + (size_t)t * BN, live), soff, 0, 0);
+        raw_buffer_store_f32(u, buffer_rsrc(p.u + (size_t)t * BN, live), soff, 0, 0);
+        raw_buffer_store_f32(zn, buffer_rsrc(zout + (size_t)(t + 1) * BN, (zout && next) ? row_bytes : 0u),
+                             soff, 0, 0);
+        // the spike-bit word of steps 32k .. 32k+31, written at its last step
+        const bool flush = ((t & 31) == 31 || t == T - 1) && t < T;
+        raw_buffer_store_f32(__uint_as_float(word),
+                             buffer_rsrc(p.bits + (size_t)(t >> 5) * N, flush ? (uint32_t)((size_t)B * TW * N * 4u) : 0u),
+                             boff, 0, 0);
+        if ((t & 31) == 31) word = 0;
+        // refill the slot after its value is used (no copy, so no wait on the load)
+        const int tn = t + kPrefetchWave;
+        xs = raw_buffer_load_f32(buffer_rsrc(p.x + (size_t)tn * BN, tn < T ? row_bytes : 0u), voff, 0, 0);
+    };
+
+    for (int t0 = 0; t0 < T; t0 += kPrefetchWave) {
+#pragma unroll
+        for (int q = 0; q < kPrefetchWave; ++q) step(t0 + q, xq[q]);
+    }
+}
+
 template <int RI, int NJ, int HW, int CJ>
 __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBwd p) {
     extern __shared__ float smem[];
@@ -537,13 +840,10 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
 
     // tile of W^T: sources grp*RI + a (rows of the GEMV), receivers jcg*CJ + c (columns)
     float w[RI][CJ];
-#pragma unroll
-    for (int a = 0; a < RI; ++a)
-#pragma unroll
-        for (int cc = 0; cc < CJ; ++cc) {
-            const int j = grp * RI + a, i = jcg * CJ + cc;
-            w[a][cc] = (i < N && j < N) ? load_w(p.W, p.w_bf16, (size_t)i * N + j) : 0.0f;
-        }
+    load_w_tile<RI, CJ>(w, p.W, p.w_bf16, N, [&](int a, int cc, int& i, int& j) {
+        j = grp * RI + a;
+        i = jcg * CJ + cc;
+    });
 
     // Source j = grp*RI + a runs its LIF chain on lane (grp, a). Its dL/dz is stored (gz)
     // for the delay-gradient pass, which keeps that work off the sequential scan.
@@ -661,6 +961,154 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
     if (nl) {
         p.gz[rowj] = gz0;
         p.part[(size_t)0 * B * N + rowj] = db_acc;
+    }
+}
+
+// The tiled backward specialised for the common regime (chosen by the host): soft taps of
+// a uniform half-width s (KF >= ceil(2s) lags of non-zero weight, one history word), the
+// ATan surrogate, decay charge, hard reset to 0, reset not detached.
+//
+// Per step: the W^T-tile contraction and row butterfly, then straight-line lane work:
+// the future-gradient taps read KF consecutive ring slots from one address (the ring
+// keeps a mirror of its first KF - 1 slots after its end, so a run of taps never wraps),
+// the LIF backward without mode switches (the surrogate takes a hardware reciprocal:
+// 1-2 ulp), and unconditional buffer loads / stores (lanes without a source and steps
+// outside [0, T) address past the buffer end), so the compiler's counts of outstanding
+// memory operations are exact and a prefetched value never waits on later stores.
+constexpr int kPrefetchBwdFast = 4;
+
+template <int RI, int NJ, int CJ, int KF>
+__global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled_fast(AxBwd p) {
+    extern __shared__ float smem[];
+    constexpr int CJP = CJ + 4;
+    const int N = p.N, T = p.T, B = p.B, NZ = p.NZ, R = p.R, NP = p.NP;
+    float* grbuf = smem;                 // [2][NZ]
+    float* ring = smem + 2 * NZ;         // [R + KF - 1][NP]: slot (time mod R), mirrored
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int grp = tid / NJ, jcg = tid - (tid / NJ) * NJ;
+
+    float w[RI][CJ];
+    load_w_tile<RI, CJ>(w, p.W, p.w_bf16, N, [&](int a, int cc, int& i, int& j) {
+        j = grp * RI + a;
+        i = jcg * CJ + cc;
+    });
+
+    const bool nl = jcg < RI && grp * RI + jcg < N;
+    const int j = nl ? grp * RI + jcg : 0;
+    OneHot<RI> sel;
+    sel.init(jcg % RI);
+    const float c = 1.0f + p.d[j];
+    const float s = p.s_uniform;
+    const float s2 = s * s;
+    const int lof = max(1, (int)floorf(c - s) + 1);
+    float wq[KF];
+#pragma unroll
+    for (int q = 0; q < KF; ++q) {
+        const int lq = lof + q;
+        wq[q] = lq <= p.L - 1 ? tri_weight((float)lq, c, s, s2) : 0.0f;
+    }
+    const float m = p.drop ? p.drop[(size_t)b * N + j] : 1.0f;
+    const float decay = p.lif.decay, vth = p.lif.vth;
+    const float half_alpha = 0.5f * p.lif.alpha, za = 1.5707963267948966f * p.lif.alpha;
+
+    for (int q = tid; q < 2 * NZ + (R + KF - 1) * NP; q += blockDim.x) smem[q] = 0.0f;
+    __syncthreads();
+
+    const size_t BN = (size_t)B * N;
+    const uint32_t row_bytes = (uint32_t)BN * 4u;
+    const int voff = (b * N + j) * 4;
+    const int soff = nl ? voff : kOutOfRange;
+    float* const grout = p.gr;
+
+    float gq[kPrefetchBwdFast], uq[kPrefetchBwdFast];
+#pragma unroll
+    for (int q = 0; q < kPrefetchBwdFast; ++q) {
+        const int tt = T - 1 - q;
+        const uint32_t nb = tt >= 0 ? row_bytes : 0u;
+        gq[q] = raw_buffer_load_f32(buffer_rsrc(p.gy + (size_t)max(tt, 0) * BN, nb), voff, 0, 0);
+        uq[q] = raw_buffer_load_f32(buffer_rsrc(p.u + (size_t)max(tt, 0) * BN, nb), voff, 0, 0);
+    }
+    float lam = 0.0f, db_acc = 0.0f;
+
+    auto contract = [&](int buf) {
+        const float4* g4 = reinterpret_cast<const float4*>(grbuf + buf * NZ + jcg * CJP);
+        float acc[RI];
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc[a] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < CJ / 4; ++q) {
+            const float4 gg = g4[q];
+#pragma unroll
+            for (int a = 0; a < RI; ++a) {
+                acc[a] = fmaf(w[a][4 * q + 0], gg.x, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 1], gg.y, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 2], gg.z, acc[a]);
+                acc[a] = fmaf(w[a][4 * q + 3], gg.w, acc[a]);
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < RI; ++a) acc[a] = group_sum_t<NJ>(acc[a]);
+        return sel.pick(acc);
+    };
+
+    // byte address of ring slot (t + lof) mod R in this lane's column, for the current t
+    const int slot_bytes = NP * 4;
+    int tn1 = T % R;                                   // slot of time t + 1
+    int tap = (T - 1 + lof) % R * slot_bytes + j * 4;  // slot of time t + lof, t = T - 1
+
+    auto step = [&](const int t, float& gs, float& us) {
+        const float gz1 = contract((t + 1) & 1);       // gz(t+1); gr(T) = 0
+        const int tm = tn1 == 0 ? R - 1 : tn1 - 1;     // slot of time t
+        // publish gz(t+1) in its slot (and the mirror) and for the delay-gradient pass
+        if (nl) {
+            ring[tn1 * NP + j] = gz1;
+            if (tn1 < KF - 1) ring[(tn1 + R) * NP + j] = gz1;
+        }
+        raw_buffer_store_f32(gz1, buffer_rsrc(p.gz + (size_t)(t + 1) * BN, t + 1 < T ? row_bytes : 0u),
+                             soff, 0, 0);
+        // taps of the future gradient: times t + lof + q (slots of times >= T hold 0)
+        float gfut = 0.0f;
+        const float* rp = reinterpret_cast<const float*>(reinterpret_cast<const char*>(ring) + tap);
+#pragma unroll
+        for (int q = 0; q < KF; ++q) gfut = fmaf(wq[q], rp[q * NP], gfut);
+        // LIF backward (hard reset to 0, ATan surrogate, reset not detached)
+        const float u = us;
+        const float y = (u - vth >= 0.0f) ? 1.0f : 0.0f;
+        const float gY = gs + gfut;
+        const float zz = za * (u - vth);
+        const float sg = half_alpha * __builtin_amdgcn_rcpf(1.0f + zz * zz);
+        const float gS = gY - lam * u;
+        const float du = lam * (1.0f - y) + gS * sg;
+        lam = decay * du;
+        const float gr = du * m;
+        // steps t < 0 (the tail of the last group) contribute nothing and must not
+        // overwrite gr(0), which the final contraction reads
+        db_acc += t >= 0 ? gr : 0.0f;
+        if (nl && t >= 0) grbuf[(t & 1) * NZ + zpos<CJ>(j)] = gr;   // LDS only: no memory counter
+        const uint32_t live = t >= 0 ? row_bytes : 0u;
+        raw_buffer_store_f32(du, buffer_rsrc(p.dx + (size_t)t * BN, live), soff, 0, 0);
+        raw_buffer_store_f32(gr, buffer_rsrc(grout + (size_t)t * BN, grout ? live : 0u), soff, 0, 0);
+        // refill the prefetch slots with step t - P (after their values are used)
+        const int tp = t - kPrefetchBwdFast;
+        const uint32_t nb = tp >= 0 ? row_bytes : 0u;
+        gs = raw_buffer_load_f32(buffer_rsrc(p.gy + (size_t)max(tp, 0) * BN, nb), voff, 0, 0);
+        us = raw_buffer_load_f32(buffer_rsrc(p.u + (size_t)max(tp, 0) * BN, nb), voff, 0, 0);
+        barrier_lds();
+        tn1 = tm;
+        tap -= slot_bytes;
+        if (tap < j * 4) tap += R * slot_bytes;
+    };
+
+    // steps T-1, T-2, ... in whole groups of P (a step t < 0 stores nothing)
+    for (int t0 = T - 1; t0 >= 0; t0 -= kPrefetchBwdFast) {
+#pragma unroll
+        for (int q = 0; q < kPrefetchBwdFast; ++q) step(t0 - q, gq[q], uq[q]);
+    }
+    const float gz0 = contract(0);                     // gz(0)
+    if (nl) {
+        p.gz[(size_t)b * N + j] = gz0;
+        p.part[(size_t)0 * B * N + (size_t)b * N + j] = db_acc;
     }
 }
 
@@ -830,6 +1278,51 @@ bool launch_axonal_tiled(bool fwd, const AxFwd* fa, const AxBwd* ba, int ri, int
     DELREC_AXT_HW(1, 1, 16) DELREC_AXT_HW(1, 2, 16) DELREC_AXT_HW(1, 4, 16) DELREC_AXT_HW(1, 8, 16)
     DELREC_AXT_HW(2, 16, 16) DELREC_AXT_HW(4, 16, 16) DELREC_AXT_HW(8, 16, 16)
     DELREC_AXT_HW(4, 8, 32)
+    return false;
+}
+
+#define DELREC_AXW_CASE(RIV, HWV)                                                         \
+    if (ri == RIV && hw == HWV) {                                                           \
+        ensure_lds((const void*)axonal_fwd_wave<RIV, HWV>, lds);                            \
+        hipLaunchKernelGGL((axonal_fwd_wave<RIV, HWV>), dim3(grid), dim3(64 * nw), lds, stream, p); \
+        return true;                                                                        \
+    }
+
+bool launch_axonal_fwd_wave_fast(const AxFwd& p, int ri, int kf, int nw, int grid, hipStream_t stream) {
+    const size_t lds = (size_t)2 * 8 * 64 * ri * sizeof(float);
+#define DELREC_AXWF_CASE(RIV, KFV)                                                          \
+    if (ri == RIV && kf == KFV) {                                                           \
+        ensure_lds((const void*)axonal_fwd_wave_fast<RIV, KFV>, lds);                       \
+        hipLaunchKernelGGL((axonal_fwd_wave_fast<RIV, KFV>), dim3(grid), dim3(64 * nw), lds, stream, p); \
+        return true;                                                                        \
+    }
+    DELREC_AXWF_CASE(1, 2) DELREC_AXWF_CASE(2, 2) DELREC_AXWF_CASE(4, 2)
+    DELREC_AXWF_CASE(1, 4) DELREC_AXWF_CASE(2, 4) DELREC_AXWF_CASE(4, 4)
+    DELREC_AXWF_CASE(1, 8) DELREC_AXWF_CASE(2, 8) DELREC_AXWF_CASE(4, 8)
+    return false;
+}
+
+bool launch_axonal_fwd_wave(const AxFwd& p, int ri, int hw, int nw, int grid, size_t lds,
+                            hipStream_t stream) {
+    DELREC_AXW_CASE(1, 1) DELREC_AXW_CASE(1, 2) DELREC_AXW_CASE(1, 4)
+    DELREC_AXW_CASE(2, 1) DELREC_AXW_CASE(2, 2) DELREC_AXW_CASE(2, 4)
+    DELREC_AXW_CASE(4, 1) DELREC_AXW_CASE(4, 2) DELREC_AXW_CASE(4, 4)
+    return false;
+}
+
+bool launch_axonal_bwd_tiled_fast(const AxBwd& p, int ri, int nj, int cj, int kf, int grid, int block,
+                                  size_t lds, hipStream_t stream) {
+#define DELREC_AXBF_CASE(RIV, NJV, CJV, KFV)                                                 \
+    if (ri == RIV && nj == NJV && cj == CJV && kf == KFV) {                                  \
+        ensure_lds((const void*)axonal_bwd_tiled_fast<RIV, NJV, CJV, KFV>, lds);            \
+        hipLaunchKernelGGL((axonal_bwd_tiled_fast<RIV, NJV, CJV, KFV>), dim3(grid), dim3(block), lds, stream, p); \
+        return true;                                                                         \
+    }
+#define DELREC_AXBF_KF(RIV, NJV, CJV) \
+    DELREC_AXBF_CASE(RIV, NJV, CJV, 2) DELREC_AXBF_CASE(RIV, NJV, CJV, 4) DELREC_AXBF_CASE(RIV, NJV, CJV, 8)
+    DELREC_AXBF_KF(1, 1, 16) DELREC_AXBF_KF(1, 2, 16) DELREC_AXBF_KF(1, 4, 16) DELREC_AXBF_KF(1, 8, 16)
+    DELREC_AXBF_KF(2, 16, 16) DELREC_AXBF_KF(4, 16, 16) DELREC_AXBF_KF(8, 16, 16)
+    DELREC_AXBF_KF(4, 8, 32)
     return false;
 }
 

@@ -134,6 +134,65 @@ __device__ __forceinline__ float load_w(const void* W, int bf16, size_t idx) {
     return bf16 ? bf16_to_f32(((const uint16_t*)W)[idx]) : ((const float*)W)[idx];
 }
 
+// Fill a register tile t[a][c] = W[i][j] (0 outside the N x N matrix) with idx(a, c, i, j)
+// giving the matrix indices. fp32 weights go through a buffer descriptor straight into
+// the tile registers (an index outside W reads 0 from the hardware bounds check), so all
+// loads are in flight before the first wait; bf16 weights are widened after loading.
+template <int R, int C, class Tile, class Idx>
+__device__ __forceinline__ void load_w_tile(Tile& t, const void* W, int bf16, int N, Idx idx);
+
+// ---------------------------------------------------------------- buffer addressing ---
+// Raw buffer loads / stores through a resource descriptor held in SGPRs: the per-lane
+// offset is a VGPR that stays constant across steps while the (uniform) base moves, so
+// address arithmetic costs no vector instructions. Accesses at or beyond `bytes` are
+// dropped (stores) or return 0 (loads).
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ void raw_buffer_store_f32(float v, i32x4 rsrc, int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.buffer.store.f32");
+__device__ float raw_buffer_load_f32(i32x4 rsrc, int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.f32");
+
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    i32x4 r;
+    r.x = (int32_t)(uint32_t)a;
+    r.y = (int32_t)((uint32_t)(a >> 32) & 0xffffu);   // stride 0
+    r.z = (int32_t)bytes;                              // num_records
+    r.w = 0x00020000;                                  // gfx9 family: 32-bit data format
+    return r;
+}
+
+constexpr int kOutOfRange = 0x7ffffff0;   // a byte offset past every buffer used here
+
+template <int R, int C, class Tile, class Idx>
+__device__ __forceinline__ void load_w_tile(Tile& t, const void* W, int bf16, int N, Idx idx) {
+    if (bf16) {
+        const uint16_t* Wh = (const uint16_t*)W;
+#pragma unroll
+        for (int a = 0; a < R; ++a)
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                int i, j;
+                idx(a, c, i, j);
+                const bool ok = i < N && j < N;
+                const float v = bf16_to_f32(Wh[ok ? (size_t)i * N + j : 0]);
+                t[a][c] = ok ? v : 0.0f;
+            }
+    } else {
+        const i32x4 rs = buffer_rsrc(W, (uint32_t)((size_t)N * N * 4u));
+#pragma unroll
+        for (int a = 0; a < R; ++a)
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                int i, j;
+                idx(a, c, i, j);
+                const int off = (i < N && j < N) ? (i * N + j) * 4 : kOutOfRange;
+                t[a][c] = raw_buffer_load_f32(rs, off, 0, 0);
+            }
+    }
+}
+
 // ---------------------------------------------------------------- wave helpers --------
 
 __device__ __forceinline__ float wave_xor(float v, int mask) {

@@ -138,6 +138,18 @@ bool launch_axonal(bool fwd, const AxFwd* fa, const AxBwd* ba, int ch, bool res,
                    int grid, int block, size_t lds, hipStream_t stream);
 bool launch_axonal_tiled(bool fwd, const AxFwd* fa, const AxBwd* ba, int ri, int nj, int cj, int hw,
                          int grid, int block, size_t lds, hipStream_t stream);
+// spike-driven forward for N <= 256: nw waves of 32 source columns, ri receivers per lane
+bool launch_axonal_fwd_wave(const AxFwd& p, int ri, int hw, int nw, int grid, size_t lds,
+                            hipStream_t stream);
+// its specialisation for soft taps of a uniform half-width (kf >= ceil(2s) lags of
+// non-zero weight, one history word), decay charge, hard reset to 0, no recurrent-input
+// output
+bool launch_axonal_fwd_wave_fast(const AxFwd& p, int ri, int kf, int nw, int grid, hipStream_t stream);
+// tiled backward for soft taps of a uniform half-width (kf >= ceil(2s) lags of non-zero
+// weight, one history word), ATan surrogate, decay charge, hard reset to 0, not detached;
+// the ring holds R + kf - 1 slots
+bool launch_axonal_bwd_tiled_fast(const AxBwd& p, int ri, int nj, int cj, int kf, int grid, int block,
+                                  size_t lds, hipStream_t stream);
 // dd / ds partials per (32-step segment, b, j) from the tiled scan's gz and the spike bits
 __host__ __device__ int axonal_delay_segments(int T);
 void launch_axonal_delay_grad(const AxBwd& p, hipStream_t stream);

@@ -30,6 +30,11 @@ CASES = [
     (16, 2, 256, 32.0, 1.0, {'cj16': True}),     # the 8 x 16 tile layout at the same size
     (16, 2, 300, 10.0, 0.5, {}),                 # streamed-weight layout (N > 256)
     (12, 2, 24, 70.0, 0.0, {}),                  # window > 64 lags: two history words
+    # straight-line kernels (soft taps, ATan, hard reset): long sequences crossing the
+    # 32-step spike words and the prefetch blocks with a ragged tail, recurrent dropout
+    (75, 2, 256, 32.0, 1.0, {}),
+    (45, 3, 100, 12.0, 0.5, {'drop': True}),
+    (37, 2, 160, 3.0, 0.0, {'bias': True, 'drop': True}),   # many sources with a lag-1 tap
 ]
 
 
@@ -46,13 +51,15 @@ def _run(dev, T, B, N, dmax, sigma, extra, seed=0):
     surr = ('triangle', 1.0) if extra.get('triangle') else ('atan', 2.0)
     lif = lif_params(tau=2.0, v_reset=v_reset, decay_input=extra.get('decay_input', False),
                      detach_reset=extra.get('detach', False), surrogate=surr)
+    drop = (torch.rand(B, N, generator=g) > 0.2).float() / 0.8 if extra.get('drop') else None
     y_ref, u_ref, gref = oracle_axonal(x, W, d, lif, sigma, gy, bias=bias, p=p,
-                                       use_sig_p=p is not None)
+                                       use_sig_p=p is not None, drop=drop)
 
     leaves = [t.to(dev).requires_grad_(True) for t in (x, W, d)]
     bg = bias.to(dev).requires_grad_(True) if bias is not None else None
     pg = p.to(dev).requires_grad_(True) if p is not None else torch.zeros(N, device=dev)
-    y = AxonalRecdelHip.apply(leaves[0], leaves[1], bg, leaves[2], pg, None, sigma, lif.tau,
+    dg = drop.to(dev) if drop is not None else None
+    y = AxonalRecdelHip.apply(leaves[0], leaves[1], bg, leaves[2], pg, dg, sigma, lif.tau,
                               lif.v_threshold, lif.v_reset, p is not None, lif.detach_reset,
                               0 if surr[0] == 'triangle' else 1, 1.0, False, 0, 2.0,
                               lif.decay_input)
