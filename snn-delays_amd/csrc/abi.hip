@@ -147,6 +147,37 @@ bool axonal_layout(int N, int L, AxLayout& o) {
     return true;
 }
 
+// A second stream per device (default priority) for work that can run beside the
+// caller's stream inside one entry point: forked after the caller's queued work and
+// joined back before the entry point returns. Kept per host thread.
+struct SideStream {
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    bool ok = false;
+};
+
+SideStream* side_stream(hipStream_t main) {
+    static thread_local SideStream per_dev[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    SideStream& ss = per_dev[dev];
+    if (!ss.ok) {
+        if (hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
+        if (hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess)
+            return nullptr;
+        ss.ok = true;
+    }
+    if (hipEventRecord(ss.fork, main) != hipSuccess || hipStreamWaitEvent(ss.stream, ss.fork, 0) != hipSuccess)
+        return nullptr;
+    return &ss;
+}
+
+void join_side_stream(SideStream* ss, hipStream_t main) {
+    hipEventRecord(ss->join, ss->stream);
+    hipStreamWaitEvent(main, ss->join, 0);
+}
+
 // The spike-driven forward (axonal_fwd_wave) serves N <= 256 unless DELREC_AXONAL_FWD=tiled
 // selects the dense tiled scan (kept for comparison).
 bool axonal_fwd_wave_on() {
@@ -172,10 +203,7 @@ void axonal_bwd_ws(C& c, int T, int B, int N, const AxLayout& lay) {
     c.template take<float>((size_t)3 * B * N);          // per-row partials
     c.template take<float>((size_t)T * B * N);          // gr (dropout / decay_input)
     c.template take<float>((size_t)dw_splits(T, B, N) * N * N);   // dW split-K partials
-    if (lay.res) {
-        c.template take<float>((size_t)T * B * N);                                    // gz
-        c.template take<float>((size_t)2 * axonal_delay_segments(T) * B * N);         // dd, ds partials
-    }
+    if (lay.res) c.template take<float>((size_t)T * B * N);                         // gz
 }
 
 // ------------------------------------------------------------------ synaptic layout ----
@@ -498,9 +526,7 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     const int ks = dw_splits(T, B, N);
     float* gemm_part = cv.take<float>((size_t)ks * N * N);
     float* gzbuf = lay.res ? cv.take<float>((size_t)T * B * N) : nullptr;
-    const int segs = axonal_delay_segments(T);
-    float* dpart = lay.res ? cv.take<float>((size_t)2 * segs * B * N) : nullptr;
-    if (!part || !grbuf || !gemm_part || (lay.res && (!gzbuf || !dpart))) return DELREC_ERR_WORKSPACE;
+    if (!part || !grbuf || !gemm_part || (lay.res && !gzbuf)) return DELREC_ERR_WORKSPACE;
     const bool need_gr = a->drop != nullptr || a->lif.decay_input;
 
     AxBwd p{};
@@ -509,7 +535,7 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     p.gy = a->gy; p.u = a->u; p.bits = a->bits; p.W = a->W; p.w_bf16 = a->w_bf16;
     p.d = a->d; p.s = a->s; p.s_uniform = a->s_uniform; p.drop = a->drop;
     p.mode = a->mode; p.lag = a->lag; p.lif = make_lif(a->lif);
-    p.dx = a->dx; p.gr = need_gr ? grbuf : nullptr; p.part = part; p.gz = gzbuf; p.dpart = dpart;
+    p.dx = a->dx; p.gr = need_gr ? grbuf : nullptr; p.part = part; p.gz = gzbuf;
     const bool timed = scan_begin(DELREC_WS_AXONAL_BWD, s);
     // the straight-line tiled backward: soft taps of a uniform half-width (kf >= ceil(2s)
     // lags of non-zero weight), one history word, ATan, decay charge, hard reset to 0
@@ -532,20 +558,23 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();
     if (st) return st;
+    // dW = sum_{t,b} gr (x) z on a side stream, beside the delay-gradient pass and the
+    // batch reductions (both only read what the scan wrote); the caller's stream waits for it
+    SideStream* side = a->dW ? side_stream(s) : nullptr;
+    if (a->dW) {
+        hipStream_t g = side ? side->stream : s;
+        launch_dw_gemm(need_gr ? grbuf : a->dx, a->z, T * B, N, ks, gemm_part, g);
+        launch_sum_partials(gemm_part, ks, (size_t)N * N, a->dW, g);
+    }
     if (lay.res) {
-        // the tiled scan leaves db partials; dd / ds come from the segment pass
-        launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
-        if (a->dd || a->ds) {
-            launch_axonal_delay_grad(p, s);
-            launch_reduce_rows(dpart, segs * B, N, a->dd, a->ds, nullptr, s);
-        }
+        // the tiled scan leaves db partials (part[0]); the segment pass adds dd / ds (part[1..2])
+        const bool delays = a->dd || a->ds;
+        if (delays) launch_axonal_delay_grad(p, s);
+        launch_reduce_rows(part, B, N, a->db, delays ? a->dd : nullptr, delays ? a->ds : nullptr, s);
     } else {
         launch_reduce_rows(part, B, N, a->db, a->dd, a->ds, s);
     }
-    if (a->dW) {
-        launch_dw_gemm(need_gr ? grbuf : a->dx, a->z, T * B, N, ks, gemm_part, s);
-        launch_sum_partials(gemm_part, ks, (size_t)N * N, a->dW, s);
-    }
+    if (side) join_side_stream(side, s);
     return finish_launch();
 }
 

@@ -732,6 +732,11 @@ __global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
         xq[q] = raw_buffer_load_f32(buffer_rsrc(p.x + (size_t)q * BN, q < T ? row_bytes : 0u), voff, 0, 0);
     if (nl && zout) zout[(size_t)b * N + i] = 0.0f;
 
+    // byte addresses of step t of x (prefetch: t + P), y, u and z (t + 1), advanced per step
+    const uint64_t step_b = (uint64_t)row_bytes;
+    uint64_t xa = (uint64_t)p.x + (uint64_t)kPrefetchWave * step_b;
+    uint64_t ya = (uint64_t)p.y, ua = (uint64_t)p.u, za = (uint64_t)zout + step_b;
+    const uint32_t zbytes = zout ? row_bytes : 0u;
     float zcur = 0.0f;                             // z(t) of this lane's source
     uint32_t mkf = 0;                              // fast sources with z(t) != 0
     float acc_s[RI];                               // slow columns of W z(t)
@@ -804,10 +809,12 @@ __global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
 
         // outputs; steps t >= T store nothing (their descriptors have no records)
         const uint32_t live = t < T ? row_bytes : 0u;
-        raw_buffer_store_f32(fire ? 1.0f : 0.0f, buffer_rsrc(p.y + (size_t)t * BN, live), soff, 0, 0);
-        raw_buffer_store_f32(u, buffer_rsrc(p.u + (size_t)t * BN, live), soff, 0, 0);
-        raw_buffer_store_f32(zn, buffer_rsrc(zout + (size_t)(t + 1) * BN, (zout && next) ? row_bytes : 0u),
-                             soff, 0, 0);
+        raw_buffer_store_f32(fire ? 1.0f : 0.0f, step_rsrc(ya, live), soff, 0, 0);
+        raw_buffer_store_f32(u, step_rsrc(ua, live), soff, 0, 0);
+        raw_buffer_store_f32(zn, step_rsrc(za, next ? zbytes : 0u), soff, 0, 0);
+        ya += step_b;
+        ua += step_b;
+        za += step_b;
         // the spike-bit word of steps 32k .. 32k+31, written at its last step
         const bool flush = ((t & 31) == 31 || t == T - 1) && t < T;
         raw_buffer_store_f32(__uint_as_float(word),
@@ -816,7 +823,8 @@ __global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
         if ((t & 31) == 31) word = 0;
         // refill the slot after its value is used (no copy, so no wait on the load)
         const int tn = t + kPrefetchWave;
-        xs = raw_buffer_load_f32(buffer_rsrc(p.x + (size_t)tn * BN, tn < T ? row_bytes : 0u), voff, 0, 0);
+        xs = raw_buffer_load_f32(step_rsrc(xa, tn < T ? row_bytes : 0u), voff, 0, 0);
+        xa += step_b;
     };
 
     for (int t0 = 0; t0 < T; t0 += kPrefetchWave) {
@@ -1052,6 +1060,14 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled_fast
         return sel.pick(acc);
     };
 
+    // byte addresses walked backwards in time: gz of step t + 1, dx and gr of step t, and
+    // the prefetch of gy / u at step t - P
+    const uint64_t step_b = (uint64_t)row_bytes;
+    uint64_t gza = (uint64_t)p.gz + (uint64_t)T * step_b, dxa = (uint64_t)p.dx + (uint64_t)(T - 1) * step_b;
+    uint64_t gra = (uint64_t)grout + (uint64_t)(T - 1) * step_b;
+    const int tp0 = T - 1 - kPrefetchBwdFast;
+    uint64_t gya = (uint64_t)p.gy + (uint64_t)max(tp0, 0) * step_b, uau = (uint64_t)p.u + (uint64_t)max(tp0, 0) * step_b;
+    const uint32_t grbytes = grout ? row_bytes : 0u;
     // byte address of ring slot (t + lof) mod R in this lane's column, for the current t
     const int slot_bytes = NP * 4;
     int tn1 = T % R;                                   // slot of time t + 1
@@ -1065,8 +1081,8 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled_fast
             ring[tn1 * NP + j] = gz1;
             if (tn1 < KF - 1) ring[(tn1 + R) * NP + j] = gz1;
         }
-        raw_buffer_store_f32(gz1, buffer_rsrc(p.gz + (size_t)(t + 1) * BN, t + 1 < T ? row_bytes : 0u),
-                             soff, 0, 0);
+        raw_buffer_store_f32(gz1, step_rsrc(gza, t + 1 < T ? row_bytes : 0u), soff, 0, 0);
+        gza -= step_b;
         // taps of the future gradient: times t + lof + q (slots of times >= T hold 0)
         float gfut = 0.0f;
         const float* rp = reinterpret_cast<const float*>(reinterpret_cast<const char*>(ring) + tap);
@@ -1086,14 +1102,21 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled_fast
         // overwrite gr(0), which the final contraction reads
         db_acc += t >= 0 ? gr : 0.0f;
         if (nl && t >= 0) grbuf[(t & 1) * NZ + zpos<CJ>(j)] = gr;   // LDS only: no memory counter
-        const uint32_t live = t >= 0 ? row_bytes : 0u;
-        raw_buffer_store_f32(du, buffer_rsrc(p.dx + (size_t)t * BN, live), soff, 0, 0);
-        raw_buffer_store_f32(gr, buffer_rsrc(grout + (size_t)t * BN, grout ? live : 0u), soff, 0, 0);
-        // refill the prefetch slots with step t - P (after their values are used)
+        const bool live = t >= 0;
+        raw_buffer_store_f32(du, step_rsrc(dxa, live ? row_bytes : 0u), soff, 0, 0);
+        raw_buffer_store_f32(gr, step_rsrc(gra, live ? grbytes : 0u), soff, 0, 0);
+        dxa -= step_b;
+        gra -= step_b;
+        // refill the prefetch slots with step t - P (after their values are used); the
+        // addresses stop at step 0 (those loads return 0)
         const int tp = t - kPrefetchBwdFast;
         const uint32_t nb = tp >= 0 ? row_bytes : 0u;
-        gs = raw_buffer_load_f32(buffer_rsrc(p.gy + (size_t)max(tp, 0) * BN, nb), voff, 0, 0);
-        us = raw_buffer_load_f32(buffer_rsrc(p.u + (size_t)max(tp, 0) * BN, nb), voff, 0, 0);
+        gs = raw_buffer_load_f32(step_rsrc(gya, nb), voff, 0, 0);
+        us = raw_buffer_load_f32(step_rsrc(uau, nb), voff, 0, 0);
+        if (tp > 0) {
+            gya -= step_b;
+            uau -= step_b;
+        }
         barrier_lds();
         tn1 = tm;
         tap -= slot_bytes;
@@ -1112,27 +1135,31 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled_fast
     }
 }
 
-// Delay / half-width gradient partials after the tiled scan, one (32-step segment, b, j)
-// per thread:
+// Delay / half-width gradient partials after the tiled scan, per (b, j):
 //   dd_j += sum_t gz_j(t) sum_l dh/dd(l) y_j(t - l)   (soft: the closed-form triangle
 //   derivative / s^2; straight: y(t - lag - 1) - y(t - lag)),  ds_j likewise with dh/ds.
-// A thread first pushes the 64*HW spikes before its segment into a History register (as
-// the forward does), loads its 32 gz values together, then walks the segment; the
-// segment partials are summed with the batch rows by reduce_rows.
+// The sequence is cut into 32-step segments; a thread handles one segment at a time: it
+// first pushes the 64*HW spikes before its segment into a History register (as the
+// forward does), loads its 32 gz values together, then walks the segment. Block (64 j,
+// kDelayY segment lanes) of one batch row: the segment lanes' sums are added in a fixed
+// order through LDS, and the per-row partials part[1][b][j] (dd), part[2][b][j] (ds) are
+// summed over the batch by reduce_rows together with the scan's db partials.
 constexpr int kDelaySeg = 32;
+constexpr int kDelayY = 4;
 
 __host__ __device__ int axonal_delay_segments(int T) { return (T + kDelaySeg - 1) / kDelaySeg; }
 
 template <int HW>
-__global__ void __launch_bounds__(256) axonal_delay_grad_kernel(AxBwd p) {
+__global__ void __launch_bounds__(64 * kDelayY) axonal_delay_grad_kernel(AxBwd p) {
+    __shared__ float red[2][kDelayY][64];
     const int N = p.N, T = p.T, B = p.B;
     const size_t BN = (size_t)B * N;
     const int S = axonal_delay_segments(T);
-    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= (size_t)S * BN) return;
-    const int seg = (int)(q / BN);
-    const size_t rem = q - (size_t)seg * BN;
-    const int b = (int)(rem / N), j = (int)(rem - (size_t)b * N);
+    const int b = blockIdx.y;
+    const int jr = blockIdx.x * 64 + threadIdx.x;
+    const bool act = jr < N;
+    const int j = act ? jr : 0;
+    const size_t rem = (size_t)b * N + j;
     const float c = 1.0f + p.d[j];
     const float s = p.s ? p.s[j] : p.s_uniform;
     const float s2 = s * s;
@@ -1147,66 +1174,80 @@ __global__ void __launch_bounds__(256) axonal_delay_grad_kernel(AxBwd p) {
 #pragma unroll
     for (int k = 0; k < kMaxTaps; ++k) dsg[k] = (k < nt) ? tri_dsign((float)(lo + k), c, s) : 0.0f;
     const int TW = (T + 31) >> 5;
-    const int t0 = seg * kDelaySeg;
-
-    float gzq[kDelaySeg];
-#pragma unroll
-    for (int e = 0; e < kDelaySeg; ++e)
-        gzq[e] = (t0 + e < T) ? p.gz[(size_t)(t0 + e) * BN + rem] : 0.0f;
-
-    // bit(l) = y(t0 - l): word w of the row holds steps 32w .. 32w + 31 (bit k = step 32w + k),
-    // so lags 1..32 are the bit-reversed word seg - 1, lags 33..64 word seg - 2, and so on
-    History<HW> past;
     const uint32_t* col = p.bits + (size_t)b * TW * N + j;
-#pragma unroll
-    for (int h = 0; h < HW; ++h) {
-        const int w1 = seg - 2 * h - 1, w2 = seg - 2 * h - 2;
-        const uint32_t a1 = w1 >= 0 ? col[(size_t)w1 * N] : 0u;
-        const uint32_t a2 = w2 >= 0 ? col[(size_t)w2 * N] : 0u;
-        past.w[h] = (uint64_t)__brev(a1) | ((uint64_t)__brev(a2) << 32);
-    }
-    const uint32_t word = col[(size_t)seg * N];                        // steps t0 .. t0 + 31
 
     float dd = 0.0f, ds = 0.0f;
+    for (int seg = threadIdx.y; seg < S; seg += kDelayY) {
+        const int t0 = seg * kDelaySeg;
+        float gzq[kDelaySeg];
 #pragma unroll
-    for (int e = 0; e < kDelaySeg; ++e) {
-        if (t0 + e >= T) break;
-        const float gz = gzq[e];
-        if (fast) {
-            const uint32_t ps = (uint32_t)(past.w[0] >> (lo - 1));
-            float sd = 0.0f;
+        for (int e = 0; e < kDelaySeg; ++e)
+            gzq[e] = (t0 + e < T) ? p.gz[(size_t)(t0 + e) * BN + rem] : 0.0f;
+
+        // bit(l) = y(t0 - l): word w of the row holds steps 32w .. 32w + 31 (bit k = step
+        // 32w + k), so lags 1..32 are the bit-reversed word seg - 1, lags 33..64 word seg - 2
+        History<HW> past;
 #pragma unroll
-            for (int k = 0; k < kMaxTaps; ++k) sd += ((ps >> k) & 1u) ? dsg[k] : 0.0f;
-            dd += gz * sd;
-        } else if (soft) {
-            float sd = 0.0f, sds = 0.0f;
-            for (int l = lo; l <= hi; ++l) {
-                const float yv = past.bit(l);
-                sd += tri_dsign((float)l, c, s) * yv;
-                if (need_ds) sds += tri_ds((float)l, c, s, s2) * yv;
-            }
-            dd += gz * sd;
-            ds += gz * sds;
-        } else {
-            dd += gz * (past.bit(lag + 1) - past.bit(lag));
+        for (int h = 0; h < HW; ++h) {
+            const int w1 = seg - 2 * h - 1, w2 = seg - 2 * h - 2;
+            const uint32_t a1 = w1 >= 0 ? col[(size_t)w1 * N] : 0u;
+            const uint32_t a2 = w2 >= 0 ? col[(size_t)w2 * N] : 0u;
+            past.w[h] = (uint64_t)__brev(a1) | ((uint64_t)__brev(a2) << 32);
         }
-        past.push((word >> e) & 1u);
+        const uint32_t word = col[(size_t)seg * N];                    // steps t0 .. t0 + 31
+
+        float dds = 0.0f, dss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < kDelaySeg; ++e) {
+            if (t0 + e >= T) break;
+            const float gz = gzq[e];
+            if (fast) {
+                const uint32_t ps = (uint32_t)(past.w[0] >> (lo - 1));
+                float sd = 0.0f;
+#pragma unroll
+                for (int k = 0; k < kMaxTaps; ++k) sd += ((ps >> k) & 1u) ? dsg[k] : 0.0f;
+                dds += gz * sd;
+            } else if (soft) {
+                float sd = 0.0f, sds = 0.0f;
+                for (int l = lo; l <= hi; ++l) {
+                    const float yv = past.bit(l);
+                    sd += tri_dsign((float)l, c, s) * yv;
+                    if (need_ds) sds += tri_ds((float)l, c, s, s2) * yv;
+                }
+                dds += gz * sd;
+                dss += gz * sds;
+            } else {
+                dds += gz * (past.bit(lag + 1) - past.bit(lag));
+            }
+            past.push((word >> e) & 1u);
+        }
+        dd += soft ? dds / s2 : dds;
+        ds += dss;
     }
-    const size_t SBN = (size_t)S * BN;
-    p.dpart[q] = soft ? dd / s2 : dd;
-    p.dpart[SBN + q] = ds;
+    red[0][threadIdx.y][threadIdx.x] = dd;
+    red[1][threadIdx.y][threadIdx.x] = ds;
+    __syncthreads();
+    if (threadIdx.y == 0 && act) {
+        float a0 = red[0][0][threadIdx.x], a1 = red[1][0][threadIdx.x];
+#pragma unroll
+        for (int y = 1; y < kDelayY; ++y) {
+            a0 += red[0][y][threadIdx.x];
+            a1 += red[1][y][threadIdx.x];
+        }
+        p.part[(size_t)1 * BN + rem] = a0;
+        p.part[(size_t)2 * BN + rem] = a1;
+    }
 }
 
 void launch_axonal_delay_grad(const AxBwd& p, hipStream_t stream) {
-    const size_t n = (size_t)axonal_delay_segments(p.T) * p.B * p.N;
-    const unsigned blocks = (unsigned)((n + 255) / 256);
+    const dim3 grid((p.N + 63) / 64, p.B), block(64, kDelayY);
     const int lags = std::max(p.L - 1, 1);
     if (lags <= 64)
-        hipLaunchKernelGGL(axonal_delay_grad_kernel<1>, dim3(blocks), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(axonal_delay_grad_kernel<1>, grid, block, 0, stream, p);
     else if (lags <= 128)
-        hipLaunchKernelGGL(axonal_delay_grad_kernel<2>, dim3(blocks), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(axonal_delay_grad_kernel<2>, grid, block, 0, stream, p);
     else
-        hipLaunchKernelGGL(axonal_delay_grad_kernel<4>, dim3(blocks), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(axonal_delay_grad_kernel<4>, grid, block, 0, stream, p);
 }
 
 // Sum the per-row partials over the batch: out_k[j] = sum_b part[k][b][j]. Block (64, 16):

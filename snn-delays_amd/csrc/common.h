@@ -165,6 +165,18 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
 
 constexpr int kOutOfRange = 0x7ffffff0;   // a byte offset past every buffer used here
 
+// Descriptor of one time step of a time-major tensor, walked step by step: the base
+// address advances by a 64-bit add (device addresses fit in 48 bits, so the high word
+// needs no masking against the stride field).
+__device__ __forceinline__ i32x4 step_rsrc(uint64_t addr, uint32_t bytes) {
+    i32x4 r;
+    r.x = (int32_t)(uint32_t)addr;
+    r.y = (int32_t)(uint32_t)(addr >> 32);
+    r.z = (int32_t)bytes;
+    r.w = 0x00020000;
+    return r;
+}
+
 template <int R, int C, class Tile, class Idx>
 __device__ __forceinline__ void load_w_tile(Tile& t, const void* W, int bf16, int N, Idx idx) {
     if (bf16) {

@@ -47,7 +47,6 @@ struct AxBwd {
     float* gr;                 // (T,B,N) dL/drec, written when it differs from dx, else NULL
     float* part;               // [3][B][N] per-row partials of db, dd, ds
     float* gz;                 // (T,B,N) dL/dz of the tiled scan, read by the delay-gradient pass
-    float* dpart;              // [2][S*B][N] dd, ds partials of the delay-gradient pass
 };
 
 struct SynFwd {
@@ -150,7 +149,7 @@ bool launch_axonal_fwd_wave_fast(const AxFwd& p, int ri, int kf, int nw, int gri
 // the ring holds R + kf - 1 slots
 bool launch_axonal_bwd_tiled_fast(const AxBwd& p, int ri, int nj, int cj, int kf, int grid, int block,
                                   size_t lds, hipStream_t stream);
-// dd / ds partials per (32-step segment, b, j) from the tiled scan's gz and the spike bits
+// dd / ds per-row partials (part[1], part[2]) from the tiled scan's gz and the spike bits
 __host__ __device__ int axonal_delay_segments(int T);
 void launch_axonal_delay_grad(const AxBwd& p, hipStream_t stream);
 void launch_reduce_rows(const float* part, int B, int N, float* o0, float* o1, float* o2,
