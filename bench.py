@@ -290,8 +290,9 @@ def main():
         'layer_roofline': {'t_bound_ms': t_bound * 1e3, 'frac': t_bound / (ms * 1e-3),
                            'bytes_per_nt': work['bytes'], 'flops_per_nt': work['flops']},
         'scan_ms': scan_avg,
-        'entry_ms': avg,
     }
+    if avg:
+        line['entry_ms'] = avg
     if not args.no_cpu:
         line['cpu_baseline'] = cpu_baseline(layer, x, w)
     print(json.dumps(line), flush=True)

@@ -450,8 +450,19 @@ int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_
     return DELREC_OK;
 }
 
+// The straight-line forward applies: soft taps of a uniform half-width (at most 8 lags of
+// non-zero weight), decay charge, hard reset to 0, no recurrent-input output, N <= 256.
+bool axonal_fwd_common(const delrec_axonal_fwd_args* a) {
+    const float span = ceilf(2.0f * a->s_uniform);
+    return a->N <= 256 && axonal_fwd_wave_on() && a->taps == DELREC_TAPS_SOFT && !a->s &&
+           a->s_uniform > 0.0f && span <= 8.0f && !a->lif.decay_input && !a->lif.soft_reset &&
+           a->lif.v_reset == 0.0f && !a->rec;
+}
+
 int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
-    if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
+    if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 0) return DELREC_ERR_ARG;
+    // L = 0 (window not read by the caller) only where the kernel sizes its own history
+    if (a->L == 0 && !axonal_fwd_common(a)) return DELREC_ERR_ARG;
     if (!a->x || !a->W || !a->d || !a->y || !a->u || !a->bits || !lif_ok(a->lif)) return DELREC_ERR_ARG;
     if (a->taps < 0 || a->taps > 2) return DELREC_ERR_ARG;
     if (a->taps != DELREC_TAPS_SOFT && !a->lag) return DELREC_ERR_ARG;
@@ -482,14 +493,11 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
         // spike-driven form: ceil(N/32) waves of 32 source columns, RI receivers per lane
         const int nw = (a->N + 31) / 32;
         const int ri = a->N > 128 ? 4 : (a->N > 64 ? 2 : 1);
-        // the straight-line variant: soft taps of a uniform half-width (kf >= ceil(2s) lags
-        // of non-zero weight), one history word, decay charge, hard reset to 0, no rec
+        // the straight-line variant (kf >= ceil(2s) lags of non-zero weight; it takes its
+        // history length, one or four 64-step words, from d)
         const float span = ceilf(2.0f * a->s_uniform);
         const int kf = span <= 2.0f ? 2 : (span <= 4.0f ? 4 : 8);
-        const bool common = a->taps == DELREC_TAPS_SOFT && lay.hw == 1 && !a->s &&
-                            a->s_uniform > 0.0f && span <= 8.0f && !a->lif.decay_input &&
-                            !a->lif.soft_reset && a->lif.v_reset == 0.0f && !a->rec;
-        if (common) {
+        if (axonal_fwd_common(a) && lay.hw <= 4) {
             ok = launch_axonal_fwd_wave_fast(p, ri, kf, nw, a->B, s);
         } else {
             const size_t lds_w = (size_t)2 * nw * 64 * ri * sizeof(float);

@@ -671,9 +671,26 @@ __global__ void __launch_bounds__(512) axonal_fwd_wave(AxFwd p) {
 // pre-step traces zpre(t+1) and contracts its slow active columns for step t+1; after
 // the LIF only the fast sources' lag-1 term and their (few) columns remain on the
 // critical path. Stores and the x prefetch use buffer descriptors in SGPRs.
-template <int RI, int KF>
-__global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
-    extern __shared__ float smem[];
+// spike-history window of HW 64-bit words: bits sh .. sh + 31 (sh >= -1; bit -1 reads 0)
+template <int HW>
+__device__ __forceinline__ uint32_t hist_bits(const uint64_t (&h)[HW], int sh) {
+    if constexpr (HW == 1) {
+        return (uint32_t)(sh >= 0 ? (h[0] >> sh) : (h[0] << 1));
+    } else {
+        if (sh < 0) return (uint32_t)(h[0] << 1);
+        const int wi = sh >> 6, bi = sh & 63;
+        uint64_t lo = 0, hi = 0;
+#pragma unroll
+        for (int k = 0; k < HW; ++k) {
+            lo = (k == wi) ? h[k] : lo;
+            hi = (k == wi + 1) ? h[k] : hi;
+        }
+        return (uint32_t)(bi ? ((lo >> bi) | (hi << (64 - bi))) : lo);
+    }
+}
+
+template <int RI, int KF, int HW>
+__device__ __forceinline__ void axonal_fwd_wave_fast_body(const AxFwd& p, float* smem) {
     constexpr int ROWS = 64 * RI;
     constexpr int NWMAX = 8;
     const int N = p.N, T = p.T, B = p.B;
@@ -697,11 +714,14 @@ __global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
     const float s2 = s * s;
     // lags of non-zero weight: l > c - s, l >= 1 (at most KF of them: l < c + s)
     const int lof = max(1, (int)floorf(c - s) + 1);
+    // L = 0: the window was not read by the caller; every lag of non-zero weight lies
+    // below c + s <= L - 1, so the cap only matters for the lags a history cannot hold
+    const int lcap = p.L > 0 ? p.L - 1 : 64 * HW;
     int wq[KF];                // tap weights as bit patterns (masked by the spike bits)
 #pragma unroll
     for (int q = 0; q < KF; ++q) {
         const int lq = lof + q;
-        wq[q] = __float_as_int(lq <= p.L - 1 ? tri_weight((float)lq, c, s, s2) : 0.0f);
+        wq[q] = __float_as_int(lq <= lcap ? tri_weight((float)lq, c, s, s2) : 0.0f);
     }
     const bool fastn = nl && lof == 1;             // z(t+1) needs y(t)
     const bool slown = nl && lof >= 2;
@@ -714,7 +734,9 @@ __global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
 
     // hist bit k = y(t-1-k) at the start of step t. zpre(t+1) = sum_q w_q y(t+1-lof-q)
     // over the known spikes: bit (lof - 2 + q); for a fast source the q = 0 term is y(t).
-    uint64_t hist = 0;
+    uint64_t hist[HW];
+#pragma unroll
+    for (int k = 0; k < HW; ++k) hist[k] = 0;
     float v = 0.0f;
     uint32_t word = 0;
     const size_t BN = (size_t)B * N;
@@ -768,8 +790,7 @@ __global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
         for (int q = 0; q < NWMAX; ++q) pr[q] = pt[q * ROWS + i];
 
         // in the shadow of those reads: zpre(t+1) and the slow columns of W z(t+1)
-        const uint64_t hk = lof >= 2 ? (hist >> (lof - 2)) : (hist << 1);
-        const uint32_t hs = (uint32_t)hk;
+        const uint32_t hs = hist_bits<HW>(hist, lof - 2);
         float zpre = 0.0f;
 #pragma unroll
         for (int q = 0; q < KF; ++q) zpre += __int_as_float(wq[q] & -(int)((hs >> q) & 1u));
@@ -799,7 +820,9 @@ __global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
         const float u = v * decay + a;
         const bool fire = u - vth >= 0.0f;
         v = fire ? 0.0f : u;
-        hist = (hist << 1) | (uint64_t)(fire ? 1u : 0u);
+#pragma unroll
+        for (int k = HW - 1; k > 0; --k) hist[k] = (hist[k] << 1) | (hist[k - 1] >> 63);
+        hist[0] = (hist[0] << 1) | (uint64_t)(fire ? 1u : 0u);
         word |= (fire ? 1u : 0u) << (t & 31);
         // z(t+1): the fast sources add their lag-1 tap
         float zn = (fastn && fire) ? w0 + zpre : zpre;
@@ -970,6 +993,22 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
         p.gz[rowj] = gz0;
         p.part[(size_t)0 * B * N + rowj] = db_acc;
     }
+}
+
+// Picks the history length from d itself (block-uniform): one 64-step word when every
+// neuron's lags of non-zero weight fit, else four words (256 lags).
+template <int RI, int KF>
+__global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
+    extern __shared__ float smem[];
+    const int l = threadIdx.x & 63, i = 32 * (threadIdx.x >> 6) + l;
+    bool longer = false;
+    if (l < 32 && i < p.N) {
+        const float c = 1.0f + p.d[i];
+        const int lof = max(1, (int)floorf(c - p.s_uniform) + 1);
+        longer = lof + KF - 1 > 64;
+    }
+    if (__syncthreads_or(longer)) axonal_fwd_wave_fast_body<RI, KF, 4>(p, smem);
+    else axonal_fwd_wave_fast_body<RI, KF, 1>(p, smem);
 }
 
 // The tiled backward specialised for the common regime (chosen by the host): soft taps of

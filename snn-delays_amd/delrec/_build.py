@@ -46,8 +46,28 @@ def _run(cmd, verbose):
         raise RuntimeError(f'hipcc failed ({res.returncode}): {cmd[-1]}')
 
 
+EXT_SOURCE = CSRC / 'torch_ext.cpp'
+EXT_OUT = PKG / 'delrec_torch.so'
+
+
+def extension_command(out=EXT_OUT):
+    """Host-only compile of the C++ autograd Function (torch_ext.cpp) against torch and the
+    HIP library, which it finds next to itself at run time (rpath $ORIGIN)."""
+    import sysconfig
+    import torch
+    tdir = Path(torch.__file__).resolve().parent
+    return [_hipcc(), '--cuda-host-only', '-O2', '-std=c++17', '-fPIC', '-shared', str(EXT_SOURCE), '-o', str(out),
+            f'-I{tdir / "include"}', f'-I{tdir / "include" / "torch" / "csrc" / "api" / "include"}',
+            f'-I{sysconfig.get_paths()["include"]}', f'-I{INCLUDE}',
+            '-DTORCH_EXTENSION_NAME=delrec_torch', '-DTORCH_API_INCLUDE_EXTENSION_H',
+            f'-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}',
+            f'-L{tdir / "lib"}', '-ltorch', '-ltorch_cpu', '-ltorch_python', '-lc10', '-lc10_hip', '-ltorch_hip',
+            f'-L{PKG}', '-ldelrec_hip', '-Wl,-rpath,$ORIGIN', f'-Wl,-rpath,{tdir / "lib"}']
+
+
 def build(verbose=False, jobs=None):
-    """Compile every HIP source into the shared library (always recompiles)."""
+    """Compile every HIP source into the shared library, then the C++ autograd extension
+    that links it (always recompiles)."""
     jobs = jobs or min(len(SOURCES), max(1, os.cpu_count() or 1))
     with tempfile.TemporaryDirectory(prefix='delrec_build_') as tmpdir:
         objs = [os.path.join(tmpdir, Path(s).stem + '.o') for s in SOURCES]
@@ -58,6 +78,9 @@ def build(verbose=False, jobs=None):
         tmp = OUT.with_suffix('.so.tmp')
         _run([_hipcc(), f'--offload-arch={ARCH}', '-fPIC', '-shared', *objs, '-o', str(tmp)], verbose)
         os.replace(tmp, OUT)
+    tmp = EXT_OUT.with_suffix('.so.tmp')
+    _run(extension_command(tmp), verbose)
+    os.replace(tmp, EXT_OUT)
     return OUT
 
 

@@ -121,6 +121,26 @@ def load():
     return lib
 
 
+_EXT = []
+EXT_PATH = _HERE / 'delrec_torch.so'
+
+
+def torch_ext():
+    """The C++ autograd extension (``delrec_torch.so``, built next to the HIP library), or
+    None when it has not been built. It calls the same C ABI; without it the layers use the
+    Python ``autograd.Function``s over the ctypes binding."""
+    if not _EXT:
+        mod = None
+        if EXT_PATH.exists():
+            import importlib.util
+            load()
+            spec = importlib.util.spec_from_file_location('delrec_torch', str(EXT_PATH))
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+        _EXT.append(mod)
+    return _EXT[0]
+
+
 def _check(fn, status):
     if status != 0:
         raise DelrecError(fn, status, load().delrec_strerror(status).decode())

@@ -9,8 +9,11 @@ bias and learned spread, STE-rounded delays) and calls the Function. The method 
 are the reference's, so code that calls them directly keeps working.
 """
 
+import os
+
 import torch
 
+from . import _lib
 from .kernels import AxonalRecdelHip, eventdriven_trainable_forward, hybrid_trainable_forward
 from .kernels._common import require_device
 from .kernels.surrogate import surrogate_id
@@ -46,16 +49,32 @@ class AxonalHipScans:
         if self.round_delays:
             d_in = d_in + (d_in.round() - d_in).detach()
         nm = self.neuron_module
-        y = AxonalRecdelHip.apply(
-            x_seq, self.recurrent_weights, bias, d_in, p_spread, drop,
-            float(self.sigma), nm.tau, nm.v_threshold, nm.v_reset, self.use_sig_p,
-            self.config.detach_reset, sid, gamma, approx, ste_mode, alpha,
-            getattr(nm, 'decay_input', False))
+        ext = _lib.torch_ext()
+        if (ext is not None and not approx and not ste_mode and not self.use_sig_p and N <= 256
+                and x_seq.dtype == torch.float32 and nm.v_reset is not None and float(nm.v_reset) == 0.0
+                and not getattr(nm, 'decay_input', False) and 0.0 <= float(self.sigma) <= 3.0
+                and os.environ.get('DELREC_AXONAL_FWD') != 'tiled'):
+            # the common regime: the C++ autograd Function over the same C ABI (no Python on
+            # the forward or backward path, no window-length read in the forward)
+            y = ext.axonal_common(x_seq, self.recurrent_weights, d_in, bias, drop, float(self.sigma),
+                                  float(nm.tau), float(nm.v_threshold), int(sid), float(gamma),
+                                  float(alpha), bool(self.config.detach_reset))
+        else:
+            y = self._axonal_function(x_seq, d_in, bias, drop, p_spread, sid, gamma, alpha, approx,
+                                      ste_mode)
         self.x_seq = x_seq
         self.rec_now_seq = None
         if self.store_v_seq:
             self.v_seq = None
         return y
+
+    def _axonal_function(self, x_seq, d_in, bias, drop, p_spread, sid, gamma, alpha, approx, ste_mode):
+        nm = self.neuron_module
+        return AxonalRecdelHip.apply(
+            x_seq, self.recurrent_weights, bias, d_in, p_spread, drop,
+            float(self.sigma), nm.tau, nm.v_threshold, nm.v_reset, self.use_sig_p,
+            self.config.detach_reset, sid, gamma, approx, ste_mode, alpha,
+            getattr(nm, 'decay_input', False))
 
 
 class SynapticHipScans:

@@ -15,12 +15,38 @@ Modes (reference ``recdel_base.py:361-383``):
   ste_mode   1: rounded tap forward, 2: two-tap interpolated forward; soft backward.
 """
 
+import os
+
 import torch
 
 from .. import _lib
 from ._common import (bits_shape, drop_bn, read_scalars, require_device, round_half_even_f32, weights,
                       window_length_f32)
 from .delays import build_lag, build_lag_interp
+
+
+def _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v_reset):
+    """The calls the C ABI's straight-line forward takes without a window length (L = 0):
+    soft taps of a uniform half-width with at most 8 lags of non-zero weight, decay charge,
+    hard reset to 0, N <= 256."""
+    return (N <= 256 and not use_sig_p and not approx and not ste_mode and not decay_input
+            and v_reset is not None and float(v_reset) == 0.0 and 0.0 <= float(sigma) <= 3.0
+            and os.environ.get('DELREC_AXONAL_FWD') != 'tiled')
+
+
+class _AsyncScalar:
+    """A device scalar copied into pinned host memory on the current stream; value()
+    waits for that copy only (not for later work on the stream)."""
+
+    def __init__(self, t):
+        self.host = torch.empty(1, dtype=torch.float32, pin_memory=True)
+        self.host.copy_(t.reshape(1).to(torch.float32), non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record()
+
+    def value(self):
+        self.event.synchronize()
+        return float(self.host[0])
 
 
 class AxonalRecdelHip(torch.autograd.Function):
@@ -52,6 +78,21 @@ class AxonalRecdelHip(torch.autograd.Function):
             lif=lif, y=_lib.ptr(y), u=_lib.ptr(u), rec=None, z=_lib.ptr(z), bits=_lib.ptr(bits),
             workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
         stream = _lib.stream_of(xc)
+
+        # The straight-line forward sizes its spike history from d itself, so when gradients
+        # are wanted the window length is not read here: max d is copied to pinned memory
+        # ahead of the scan and read by the backward (by then the copy has long finished).
+        # Without gradients the read stays synchronous so that an over-long window raises.
+        if (any(ctx.needs_input_grad[:5])
+                and _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v_reset)):
+            pending = _AsyncScalar(dc.max())
+            args.L = 0
+            args.taps = _lib.DELREC_TAPS_SOFT
+            _lib.call('delrec_axonal_fwd', args, stream)
+            ctx.save_for_backward(u, z, bits, Wc, dc, s_vec, m, None, p_spread)
+            ctx.meta = (T, B, N, pending, w_bf16, sigma, bool(use_sig_p), _lib.DELREC_BWD_SOFT, W.dtype)
+            ctx.lif = lif
+            return y
 
         # The window length needs max d (and max s): the one device-to-host read of the call,
         # taken after the host work above so that it overlaps the GPU work still queued.
@@ -92,6 +133,8 @@ class AxonalRecdelHip(torch.autograd.Function):
     def backward(ctx, gy):
         u, z, bits, Wc, dc, s_vec, m, lag, p_spread = ctx.saved_tensors
         T, B, N, L, w_bf16, sigma, use_sig_p, mode, w_dtype = ctx.meta
+        if isinstance(L, _AsyncScalar):
+            L = max(window_length_f32(L.value(), 1.0 + sigma), 2)
         dev = u.device
         gy = gy.to(torch.float32).contiguous()
         need_W, need_b, need_d = ctx.needs_input_grad[1], ctx.needs_input_grad[2], ctx.needs_input_grad[3]

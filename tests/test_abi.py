@@ -81,3 +81,14 @@ def test_struct_layout_matches_ctypes():
         assert c[f'{st} size'] == ctypes.sizeof(cls), st
         for fname, _ in cls._fields_:
             assert c[f'{st} {fname}'] == getattr(cls, fname).offset, f'{st}.{fname}'
+
+
+def test_torch_extension_loads_and_exposes_the_axonal_function():
+    """The C++ autograd extension is built next to the HIP library, links it, and exposes
+    the axonal layer's Function (no GPU call is made)."""
+    ext = _lib.torch_ext()
+    assert ext is not None, f'{_lib.EXT_PATH} is not built'
+    assert callable(ext.axonal_common)
+    doc = ext.axonal_common.__doc__
+    for arg in ('x', 'W', 'd', 'bias', 'drop', 'sigma', 'tau', 'vth', 'surrogate', 'gamma', 'alpha', 'detach'):
+        assert f'{arg}:' in doc
