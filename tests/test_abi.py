@@ -86,6 +86,7 @@ def test_struct_layout_matches_ctypes():
 def test_torch_extension_loads_and_exposes_the_axonal_function():
     """The C++ autograd extension is built next to the HIP library, links it, and exposes
     the axonal layer's Function (no GPU call is made)."""
+    from delrec import _lib
     ext = _lib.torch_ext()
     assert ext is not None, f'{_lib.EXT_PATH} is not built'
     assert callable(ext.axonal_common)
