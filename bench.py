@@ -127,9 +127,12 @@ def algorithmic_work(w):
                            'syn_fwd_scan': 2.0 * N + 2.0 * k, 'syn_bwd_scan': 2.0 * N + 4.0 * k}}
 
 
-# kernel symbol of each time-scan kind at the benchmark shapes (for the rocprof summaries)
-SCAN_SYMBOL = {'axonal_fwd_scan': 'axonal_fwd_tiled', 'axonal_bwd_scan': 'axonal_bwd_tiled',
-               'syn_fwd_scan': 'syn_fwd_kernel', 'syn_bwd_scan': 'syn_bwd_kernel'}
+# kernel symbol of each time-scan kind at each workload's shape (for the rocprof summaries)
+SCAN_SYMBOL = {
+    'C2': {'axonal_fwd_scan': 'axonal_fwd_wave_fast', 'axonal_bwd_scan': 'axonal_bwd_tiled_fast'},
+    'C3': {'syn_fwd_scan': 'syn_fwd_kernel', 'syn_bwd_scan': 'syn_bwd_kernel'},
+    'C4': {'syn_fwd_scan': 'syn_fwd_gather_kernel', 'syn_bwd_scan': 'syn_bwd_kernel'},
+}
 
 
 def cpu_baseline(layer, x, w, budget_s=25.0):
@@ -266,7 +269,7 @@ def main():
     dur = scan_avg[dom] * 1e-3
     flops = work['scan_flops'][dom] * nt
     achieved = flops / dur
-    kernel = SCAN_SYMBOL[dom]
+    kernel = SCAN_SYMBOL[args.config][dom]
     traffic = load_traffic(kernel, args.config)
     line = {
         'metric': 'neuron-timesteps/sec fwd+BPTT per recurrent layer',
