@@ -178,6 +178,12 @@ void join_side_stream(SideStream* ss, hipStream_t main) {
     hipStreamWaitEvent(main, ss->join, 0);
 }
 
+// true unless the environment variable is set to "0" (a kernel variant kept for comparison)
+bool getenv_flag_off(const char* name) {
+    const char* e = getenv(name);
+    return !(e && strcmp(e, "0") == 0);
+}
+
 // The spike-driven forward (axonal_fwd_wave) serves N <= 256 unless DELREC_AXONAL_FWD=tiled
 // selects the dense tiled scan (kept for comparison).
 bool axonal_fwd_wave_on() {
@@ -289,6 +295,7 @@ void syn_fwd_ws(C& c, int B, int N, int L, bool hybrid, bool bf16) {
     if (bf16) c.template take<uint16_t>(nb); else c.template take<float>(nb);
     if (hybrid) c.template take<int8_t>(nb); else c.template take<float>(nb);
     if (!lay.lds_ring) c.template take<float>((size_t)B * lay.R * N);
+    if (hybrid && bf16) c.template take<uint32_t>((size_t)N * N);   // packed W^T | offsets^T
 }
 
 template <class C>
@@ -600,7 +607,8 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     void* wt = a->w_bf16 ? (void*)cv.take<uint16_t>(nb) : (void*)cv.take<float>(nb);
     void* dt = hybrid ? (void*)cv.take<int8_t>(nb) : (void*)cv.take<float>(nb);
     float* gring = lay.lds_ring ? nullptr : cv.take<float>((size_t)a->B * lay.R * N);
-    if (!wt || !dt || (!lay.lds_ring && !gring)) return DELREC_ERR_WORKSPACE;
+    uint32_t* wpk = (hybrid && a->w_bf16) ? cv.take<uint32_t>((size_t)N * N) : nullptr;
+    if (!wt || !dt || (!lay.lds_ring && !gring) || (hybrid && a->w_bf16 && !wpk)) return DELREC_ERR_WORKSPACE;
 
     SynFwd p{};
     p.T = a->T; p.B = a->B; p.N = N; p.L = a->L; p.R = lay.R; p.NP = lay.NP; p.NF = lay.NF;
@@ -632,7 +640,21 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
         p.gring = gring;
     }
     const bool timed = scan_begin(DELREC_WS_SYN_FWD, s);
-    launch_syn_fwd(p, lay.block, lds, s);
+    // the chunked event-driven scatter: ring in LDS, one receiver per lane, at most 8
+    // lags of non-zero weight per connection
+    const float smax = a->s ? a->s_max : std::max(a->s_max, a->s_uniform);
+    const float span = ceilf(2.0f * smax);
+    const int kf = span <= 2.0f ? 2 : (span <= 4.0f ? 4 : 8);
+    const int nwaves = lay.block / 64;
+    const size_t lds_s = (size_t)lay.R * lay.NP * sizeof(float) + (size_t)N * 4 * sizeof(float) +
+                         64 * sizeof(float) + (size_t)(2 * nwaves * 64 + 2 * nwaves) * sizeof(int);
+    const bool scatter = !gather && lay.lds_ring && N <= 1024 && span <= 8.0f && smax > 0.0f &&
+                         lds_s <= (size_t)max_lds_bytes() && getenv_flag_off("DELREC_SYN_SCATTER");
+    if (scatter && wpk) {
+        launch_pack_hybrid(static_cast<const uint16_t*>(a->W), a->offsets, N, wpk, s);
+        p.wpk = wpk;
+    }
+    if (!(scatter && launch_syn_fwd_scatter(p, kf, lay.block, lds_s, s))) launch_syn_fwd(p, lay.block, lds, s);
     scan_end(timed, s);
     return finish_launch();
 }

@@ -152,6 +152,10 @@ __device__ void raw_buffer_store_f32(float v, i32x4 rsrc, int voff, int soff, in
     __asm("llvm.amdgcn.raw.buffer.store.f32");
 __device__ float raw_buffer_load_f32(i32x4 rsrc, int voff, int soff, int aux)
     __asm("llvm.amdgcn.raw.buffer.load.f32");
+__device__ uint16_t raw_buffer_load_u16(i32x4 rsrc, int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i16");
+__device__ int8_t raw_buffer_load_i8(i32x4 rsrc, int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i8");
 
 __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
     const uint64_t a = (uint64_t)base;

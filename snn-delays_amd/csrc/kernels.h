@@ -72,6 +72,9 @@ struct SynFwd {
     const void* Wr;
     const float* dr;
     const int8_t* offr;
+    // hybrid with bf16 W: W^T and the offsets^T packed per connection,
+    // wpk[o*N + i] = bf16(W[i, o]) << 16 | uint8(offset[i, o]), else NULL
+    const uint32_t* wpk;
 };
 
 struct SynBwd {
@@ -162,6 +165,10 @@ void launch_dw_gemm(const float* A, const float* Bm, int K, int N, int ks, float
 void launch_sum_partials(const float* partial, int ks, size_t count, float* out, hipStream_t stream);
 
 void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream);
+// wpk[o*N + i] = W[i*N + o] (bf16 bits) << 16 | uint8(off[i*N + o])
+void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream);
+// event-driven forward, ring in LDS, one receiver per lane, kf >= ceil(2 s_max) taps
+bool launch_syn_fwd_scatter(const SynFwd& a, int kf, int block, size_t lds, hipStream_t stream);
 bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);
 int lag_bf16_splits(int T, int Bp, int Np, int cus);
 // hybrid: meta[0] = relative lags, meta[1] = smallest offset, lo[j] = first lag of column j

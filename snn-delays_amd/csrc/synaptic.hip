@@ -169,6 +169,221 @@ __global__ void __launch_bounds__(1024) syn_fwd_kernel(SynFwd p) {
     }
 }
 
+// Event-driven forward with the ring in LDS, one receiver per lane (N <= 1024), at most
+// KF lags of non-zero weight per connection (KF >= ceil(2 s_max)).
+//
+// Per step: the LIF of every receiver (its recurrent input waits in its own ring column),
+// then each wave writes the receivers that fired into its own segment of a double-buffered
+// LDS list: one barrier per step. Lane k of every wave then finds the k-th fired source
+// of the flattened list (wave segments in order) and holds its index, so the sources are
+// walked in a fixed order with readlane. The walk goes in chunks of 8 sources: the weight
+// and delay (or offset) of the next chunk's sources are loaded while the current chunk is
+// scattered, through buffer descriptors whose base is the source's column of W^T / d^T
+// (SGPRs), so a load costs no address arithmetic. Each lane adds
+// W[i,o] / s_o^2 * max(0, s_o - |l - c_io|) at lags l = lof .. lof + KF - 1 (lof the first
+// lag of non-zero weight, >= 1) into its own ring column: no atomics, no hazards between
+// lanes. x is prefetched 8 steps ahead in fixed registers and every global load / store
+// of a step is unconditional (inactive lanes address past the buffer end).
+constexpr int kScatterChunk = 8;
+constexpr int kScatterPrefetch = 8;
+
+template <int KF, bool HYB, bool WBF>
+__global__ void __launch_bounds__(1024) syn_fwd_scatter(SynFwd p) {
+    extern __shared__ float smem[];
+    constexpr bool PACKED = HYB && WBF;
+    const int N = p.N, T = p.T, B = p.B, R = p.R, NP = p.NP;
+    const int b = blockIdx.x, tid = threadIdx.x, BS = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nwaves = BS >> 6;
+    float* ring = smem;                                               // [R][NP]
+    float4* srcl = reinterpret_cast<float4*>(smem + (size_t)R * NP);  // [N] base, s, 1/s^2
+    float* dummy = reinterpret_cast<float*>(srcl + N);                // [64] writes of lanes past N
+    int* seg = reinterpret_cast<int*>(dummy + 64);                    // [2][nwaves][64]
+    int* cnt = seg + 2 * nwaves * 64;                                  // [2][nwaves]
+    const int TW = (T + 31) >> 5;
+    const size_t BN = (size_t)B * N;
+    const bool act = tid < N;
+    const int i = act ? tid : 0;
+    const float vth = p.lif.vth;
+    const Lif k = p.lif;
+    const float m = p.drop ? p.drop[(size_t)b * N + i] : 1.0f;
+    const float bias = p.bias ? p.bias[i] : 0.0f;
+
+    // the lane's ring column (lanes past N write a private dummy cell: no branches, no
+    // access to another receiver's column)
+    float* const colp = act ? ring + tid : dummy + lane;
+    const int cst = act ? NP : 0;
+    for (int r = 0; r < R; ++r) colp[r * cst] = 0.0f;
+    for (int q = tid; q < N; q += BS) {
+        const float sq = p.s ? p.s[q] : p.s_uniform;
+        srcl[q] = make_float4(HYB ? p.base[q] : 0.0f, sq, 1.0f / (sq * sq), 0.0f);
+    }
+    __syncthreads();
+
+    const uint32_t row_bytes = (uint32_t)BN * 4u;
+    const uint64_t step_b = (uint64_t)row_bytes;
+    const int voff = (b * N + i) * 4;
+    const int soff = act ? voff : kOutOfRange;
+    const int boff = act ? (b * TW * N + i) * 4 : kOutOfRange;
+    uint64_t xa = (uint64_t)p.x + (uint64_t)kScatterPrefetch * step_b;
+    uint64_t ya = (uint64_t)p.y, ua = (uint64_t)p.u;
+    float xq[kScatterPrefetch];
+#pragma unroll
+    for (int q = 0; q < kScatterPrefetch; ++q)
+        xq[q] = raw_buffer_load_f32(step_rsrc((uint64_t)p.x + (uint64_t)q * step_b, q < T ? row_bytes : 0u), voff, 0, 0);
+
+    // one descriptor per matrix; source o's column starts o * N elements in; a lane past N
+    // reads beyond the matrix (0)
+    const uint32_t nn = (uint32_t)N * (uint32_t)N;
+    const i32x4 rw = buffer_rsrc(PACKED ? (const void*)p.wpk : p.Wt, nn * (PACKED ? 4u : (WBF ? 2u : 4u)));
+    const i32x4 rd = buffer_rsrc(HYB ? (const void*)p.offt : (const void*)p.dt, nn * (HYB ? 1u : 4u));
+    const int wsz = PACKED ? 4 : (WBF ? 2 : 4), dsz = HYB ? 1 : 4;
+    const int wio = act ? i * wsz : 0x40000000, dio = act ? i * dsz : 0x40000000;
+    auto load_src = [&](int o, float& w, float& dl) {
+        if constexpr (PACKED) {
+            const uint32_t v = __float_as_uint(raw_buffer_load_f32(rw, wio + o * N * 4, 0, 0));
+            w = __uint_as_float(v & 0xFFFF0000u);
+            dl = (float)(int8_t)(v & 0xFFu);
+        } else {
+            if constexpr (WBF) w = bf16_to_f32(raw_buffer_load_u16(rw, wio + o * N * 2, 0, 0));
+            else w = raw_buffer_load_f32(rw, wio + o * N * 4, 0, 0);
+            if constexpr (HYB) dl = (float)raw_buffer_load_i8(rd, dio + o * N, 0, 0);
+            else dl = raw_buffer_load_f32(rd, dio + o * N * 4, 0, 0);
+        }
+    };
+
+    float v = k.v0;
+    uint32_t word = 0;
+    int tmod = 0;
+    auto step = [&](const int t, float& xs) {
+        // LIF of this receiver: its recurrent input for step t waits in ring slot tmod
+        float* cell = colp + tmod * cst;
+        const float rec = *cell;
+        *cell = 0.0f;
+        const float r = rec + bias;
+        const float a = xs + r * m;
+        const float u = lif_charge(k, v, a);
+        const bool fire = act && (u - vth >= 0.0f);
+        v = lif_reset(k, u, fire ? 1.0f : 0.0f);
+        word |= (fire ? 1u : 0u) << (t & 31);
+        const bool live = t < T;
+        raw_buffer_store_f32(fire ? 1.0f : 0.0f, step_rsrc(ya, live ? row_bytes : 0u), soff, 0, 0);
+        raw_buffer_store_f32(u, step_rsrc(ua, live ? row_bytes : 0u), soff, 0, 0);
+        const bool flush = ((t & 31) == 31 || t == T - 1) && live;
+        raw_buffer_store_f32(__uint_as_float(word), step_rsrc((uint64_t)p.bits + (uint64_t)(t >> 5) * N * 4u,
+                                                            flush ? (uint32_t)((size_t)B * TW * N * 4u) : 0u),
+                             boff, 0, 0);
+        if ((t & 31) == 31) word = 0;
+        ya += step_b;
+        ua += step_b;
+        const int tn = t + kScatterPrefetch;
+        xs = raw_buffer_load_f32(step_rsrc(xa, tn < T ? row_bytes : 0u), voff, 0, 0);
+        xa += step_b;
+
+        // fired receivers of this wave into its segment (buffer t & 1)
+        const int bsel = t & 1;
+        const uint64_t bal = __ballot(fire && live);
+        if (fire && live) seg[(bsel * nwaves + wave) * 64 + __popcll(bal & ((1ull << lane) - 1ull))] = tid;
+        if (lane == 0) cnt[bsel * nwaves + wave] = __popcll(bal);
+        barrier_lds();
+
+        // flattened list: lane q of every wave finds fired source number base + q
+        int total = 0;
+        int cw[16];
+#pragma unroll
+        for (int w2 = 0; w2 < 16; ++w2) {
+            cw[w2] = w2 < nwaves ? cnt[bsel * nwaves + w2] : 0;
+            total += cw[w2];
+        }
+        for (int base = 0; base < total; base += 64) {
+            int src = 0;
+            {
+                int f = base + lane, acc = 0, sgi = 0, pos = 0;
+                bool found = false;
+#pragma unroll
+                for (int w2 = 0; w2 < 16; ++w2) {
+                    if (!found && f < acc + cw[w2]) {
+                        sgi = w2;
+                        pos = f - acc;
+                        found = true;
+                    }
+                    acc += cw[w2];
+                }
+                src = found ? seg[(bsel * nwaves + sgi) * 64 + pos] : 0;
+            }
+            const int nf = min(64, total - base);
+            // chunked walk: the next chunk's weights / delays load while this one scatters
+            // (sources past nf read source 0: valid addresses, values unused; every load is
+            // unconditional so the compiler's memory counts stay exact)
+            float wn[kScatterChunk], dn[kScatterChunk];
+#pragma unroll
+            for (int e = 0; e < kScatterChunk; ++e) load_src(__builtin_amdgcn_readlane(src, e), wn[e], dn[e]);
+            for (int f0 = 0; f0 < nf; f0 += kScatterChunk) {
+                float wc[kScatterChunk], dc[kScatterChunk];
+#pragma unroll
+                for (int e = 0; e < kScatterChunk; ++e) {
+                    wc[e] = wn[e];
+                    dc[e] = dn[e];
+                }
+                if (f0 + kScatterChunk < nf) {
+#pragma unroll
+                    for (int e = 0; e < kScatterChunk; ++e)
+                        load_src(__builtin_amdgcn_readlane(src, (f0 + kScatterChunk + e) & 63), wn[e], dn[e]);
+                }
+#pragma unroll
+                for (int e = 0; e < kScatterChunk; ++e) {
+                    if (f0 + e >= nf) break;
+                    const int o = __builtin_amdgcn_readlane(src, (f0 + e) & 63);
+                    const float4 sp = srcl[o];                 // base, s, 1/s^2
+                    const float so = sp.y;
+                    const float c = HYB ? 1.0f + (sp.x + 0.0f + 1.0f * dc[e]) : 1.0f + dc[e];
+                    const float wq = wc[e] * sp.z;
+                    // lags of non-zero weight: l > c - s, l >= 1; the ring slot of t + l
+                    const int lof = max(1, (int)floorf(c - so) + 1);
+                    int sl = tmod + lof;
+                    sl = sl >= R ? sl - R : sl;
+#pragma unroll
+                    for (int q = 0; q < KF; ++q) {
+                        const float hv = fmaxf(so - fabsf((float)(lof + q) - c), 0.0f);
+                        float* cp = colp + sl * cst;
+                        *cp = *cp + wq * hv;
+                        sl = sl + 1 == R ? 0 : sl + 1;
+                    }
+                }
+            }
+        }
+        tmod = tmod + 1 == R ? 0 : tmod + 1;
+    };
+
+    for (int t0 = 0; t0 < T; t0 += kScatterPrefetch) {
+#pragma unroll
+        for (int q = 0; q < kScatterPrefetch; ++q) step(t0 + q, xq[q]);
+    }
+}
+
+// wpk[o*N + i] = W[i*N + o] << 16 | uint8(off[i*N + o]) through 32 x 32 LDS tiles
+__global__ void __launch_bounds__(256) pack_hybrid_kernel(const uint16_t* __restrict__ W,
+                                                          const int8_t* __restrict__ off, int N,
+                                                          uint32_t* __restrict__ wpk) {
+    __shared__ uint32_t tile[32][33];
+    const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
+    for (int r = threadIdx.y; r < 32; r += 8) {
+        const int i = by + r, o = bx + threadIdx.x;
+        uint32_t v = 0;
+        if (i < N && o < N) v = ((uint32_t)W[(size_t)i * N + o] << 16) | (uint8_t)off[(size_t)i * N + o];
+        tile[r][threadIdx.x] = v;
+    }
+    __syncthreads();
+    for (int r = threadIdx.y; r < 32; r += 8) {
+        const int o = bx + r, i = by + threadIdx.x;
+        if (i < N && o < N) wpk[(size_t)o * N + i] = tile[threadIdx.x][r];
+    }
+}
+
+void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream) {
+    const dim3 grid((N + 31) / 32, (N + 31) / 32), block(32, 8);
+    hipLaunchKernelGGL(pack_hybrid_kernel, grid, block, 0, stream, W, off, N, wpk);
+}
+
 // Forward in gather form, for rings too large for LDS: lane i owns receiver i and sums
 //   rec_i(t) = sum_j W_ij sum_l max(0, s_j - |l - c_ij|) / s_j^2 * y_j(t - l),  c_ij = 1 + d_ij,
 // over every source each step. The spike history of each source is a bit word in LDS
@@ -613,6 +828,21 @@ void launch_syn_fwd_gather(const SynFwd& a, int block, size_t lds, hipStream_t s
         if (hyb) launch_syn_fwd_g<NPT, true, 2>(a, block, lds, stream);
         else launch_syn_fwd_g<NPT, false, 2>(a, block, lds, stream);
     }
+}
+
+#define DELREC_SCAT_CASE(KFV, HYBV, WBFV)                                                    \
+    if (kf == KFV && hyb == HYBV && wbf == WBFV) {                                           \
+        ensure_lds((const void*)syn_fwd_scatter<KFV, HYBV, WBFV>, lds);                     \
+        hipLaunchKernelGGL((syn_fwd_scatter<KFV, HYBV, WBFV>), dim3(a.B), dim3(block), lds, stream, a); \
+        return true;                                                                         \
+    }
+#define DELREC_SCAT_KF(HYBV, WBFV) \
+    DELREC_SCAT_CASE(2, HYBV, WBFV) DELREC_SCAT_CASE(4, HYBV, WBFV) DELREC_SCAT_CASE(8, HYBV, WBFV)
+
+bool launch_syn_fwd_scatter(const SynFwd& a, int kf, int block, size_t lds, hipStream_t stream) {
+    const bool hyb = a.offt != nullptr, wbf = a.w_bf16 != 0;
+    DELREC_SCAT_KF(false, false) DELREC_SCAT_KF(false, true) DELREC_SCAT_KF(true, false) DELREC_SCAT_KF(true, true)
+    return false;
 }
 
 void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream) {
