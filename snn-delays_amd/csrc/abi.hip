@@ -711,7 +711,12 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     p.drop = a->drop; p.lif = make_lif(a->lif);
     p.dx = a->dx; p.gr = gr; p.part = part; p.gring = lay.lds_ring ? nullptr : gring;
     const bool timed = scan_begin(DELREC_WS_SYN_BWD, s);
-    const bool ok = launch_syn_bwd(p, lay.block, lay.lds, s);
+    // hybrid, ring in LDS, one source per lane: the streamlined gather (its ring covers
+    // the receivers rounded up to groups of 64)
+    const size_t lds_h = (size_t)((N + 63) / 64 * 64) * lay.RP * sizeof(float);   // groups of <= 64 receivers
+    const bool hyb_fast = hybrid && N <= 1024 && (lay.KT == 2 || lay.KT == 4) &&
+                          lds_h <= (size_t)max_lds_bytes() && getenv_flag_off("DELREC_SYN_BWD_HYB");
+    const bool ok = (hyb_fast && launch_syn_bwd_hyb(p, lay.block, lds_h, s)) || launch_syn_bwd(p, lay.block, lay.lds, s);
     scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();

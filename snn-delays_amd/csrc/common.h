@@ -156,6 +156,8 @@ __device__ uint16_t raw_buffer_load_u16(i32x4 rsrc, int voff, int soff, int aux)
     __asm("llvm.amdgcn.raw.buffer.load.i16");
 __device__ int8_t raw_buffer_load_i8(i32x4 rsrc, int voff, int soff, int aux)
     __asm("llvm.amdgcn.raw.buffer.load.i8");
+__device__ i32x4 raw_buffer_load_i32x4(i32x4 rsrc, int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
 
 __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
     const uint64_t a = (uint64_t)base;

@@ -170,6 +170,9 @@ void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* w
 // event-driven forward, ring in LDS, one receiver per lane, kf >= ceil(2 s_max) taps
 bool launch_syn_fwd_scatter(const SynFwd& a, int kf, int block, size_t lds, hipStream_t stream);
 bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);
+// hybrid backward, ring in LDS over ceil(N/64)*64 rows, one source per lane (N <= 512),
+// KT = 2 or 4; false when it does not apply
+bool launch_syn_bwd_hyb(const SynBwd& a, int block, size_t lds, hipStream_t stream);
 int lag_bf16_splits(int T, int Bp, int Np, int cus);
 // hybrid: meta[0] = relative lags, meta[1] = smallest offset, lo[j] = first lag of column j
 void launch_lag_range(const int8_t* off, const float* base, int N, int L, float s, int* meta, int* lo,

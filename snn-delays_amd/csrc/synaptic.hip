@@ -185,6 +185,7 @@ __global__ void __launch_bounds__(1024) syn_fwd_kernel(SynFwd p) {
 // lanes. x is prefetched 8 steps ahead in fixed registers and every global load / store
 // of a step is unconditional (inactive lanes address past the buffer end).
 constexpr int kScatterChunk = 8;
+constexpr int kPrefetchSynBwd = 4;   // steps of gy / u loaded ahead (hybrid backward)
 constexpr int kScatterPrefetch = 8;
 
 template <int KF, bool HYB, bool WBF>
@@ -866,6 +867,206 @@ void launch_syn_bwd_k(const SynBwd& a, int block, size_t lds, hipStream_t stream
         ensure_lds((const void*)syn_bwd_kernel<NPT, KT, HYB, MAXT, false>, lds);
         hipLaunchKernelGGL((syn_bwd_kernel<NPT, KT, HYB, MAXT, false>), dim3(a.B), dim3(block), lds, stream, a);
     }
+}
+
+// Hybrid backward with the ring in LDS, one source per lane (N <= 1024), KT = 2 or 4 taps.
+// The same dense reverse gather as syn_bwd_kernel,
+//   gfut_j = is2 * sum_f hq_j[f] * sum_i W[i,j] gr_i(t + lob_j + off_ij + f),
+// with the per-connection work cut to an offset decode, one slot add and wrap, one LDS
+// address (the 16 rows of a chunk are immediate offsets) and a KT-wide read: the lane's
+// base slot (t + lob_j + min offset) mod R is formed once per step. Receivers stream in
+// groups of 4 chunks of 16 (blocked W^T and offsets^T), the next group's operands in
+// flight while the current group is gathered; past the last chunk the descriptor bounds
+// read 0. CHK: some connection may reach a lag <= 0 (negative base), those taps weigh 0.
+template <int KT, bool WBF, int MAXT>
+__global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
+    // chunks of 16 receivers per group: two groups of operands stay in registers
+    constexpr int kBwdGroup = MAXT <= 512 ? 4 : 2;
+    extern __shared__ float smem[];
+    const int N = p.N, T = p.T, B = p.B, R = p.R, RP = p.RP;
+    const int b = blockIdx.x, tid = threadIdx.x, BS = blockDim.x;
+    float* ring = smem;                                   // [NC * 16 rows][RP]
+    const size_t BN = (size_t)B * N;
+    const bool act = tid < N;
+    const int j = act ? tid : 0;
+    const Lif k = p.lif;
+    const float m = p.drop ? p.drop[(size_t)b * N + j] : 1.0f;
+    const float sv = p.s_uniform;
+    const float is2 = 1.0f / (sv * sv);
+    const float c = 1.0f + p.base[j];
+    int lob = (int)ceilf(c - sv);
+    if (fabsf((float)(lob - 1) - c) <= sv) lob -= 1;
+    if (fabsf((float)lob - c) > sv) lob += 1;
+    float hq[KT];
+#pragma unroll
+    for (int f = 0; f < KT; ++f) hq[f] = fmaxf(sv - fabsf((float)(lob + f) - c), 0.0f);
+    const int omin = p.meta[1];
+    const int NC = (N + 15) >> 4;
+    const int NG = (NC + kBwdGroup - 1) / kBwdGroup;
+    const int rows = NG * kBwdGroup * 16;
+    const bool chk = __syncthreads_or(act && lob + min(omin, 0) < 1) != 0;
+
+    for (int q = tid; q < rows * RP; q += BS) ring[q] = 0.0f;
+    __syncthreads();
+
+    // blocked W^T: receivers 16c .. 16c+15 of source j at ((c*N + j)*16) elements
+    const uint32_t wbytes = (uint32_t)((size_t)p.NT * N * (WBF ? 2 : 4));
+    const uint32_t obytes = (uint32_t)((size_t)p.NT * N);
+    const i32x4 rw = buffer_rsrc(p.Wt, wbytes), ro = buffer_rsrc(p.offt, obytes);
+    const int wj = act ? j * 16 * (WBF ? 2 : 4) : kOutOfRange, oj = act ? j * 16 : kOutOfRange;
+    const int wcs = N * 16 * (WBF ? 2 : 4), ocs = N * 16;   // bytes per chunk
+    constexpr int WV = WBF ? 2 : 4;                          // uint4 of W per chunk
+    struct Chunk { uint4 w[WV]; uint4 o; };
+    auto fetch = [&](int cidx, Chunk& ch) {
+        const int cw = cidx * wcs, co = cidx * ocs;
+#pragma unroll
+        for (int h = 0; h < WV; ++h) {
+            const i32x4 v = raw_buffer_load_i32x4(rw, wj + cw + 16 * h, 0, 0);
+            ch.w[h] = make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+        }
+        const i32x4 ov = raw_buffer_load_i32x4(ro, oj + co, 0, 0);
+        ch.o = make_uint4((uint32_t)ov.x, (uint32_t)ov.y, (uint32_t)ov.z, (uint32_t)ov.w);
+    };
+    const uint32_t row_bytes = (uint32_t)BN * 4u;
+    const uint64_t step_b = (uint64_t)row_bytes;
+    const int voff = (b * N + j) * 4;
+    const int soff = act ? voff : kOutOfRange;
+
+    float gq[kPrefetchSynBwd], uq[kPrefetchSynBwd];
+    const int tp0 = T - 1 - kPrefetchSynBwd;
+    uint64_t gya = (uint64_t)p.gy + (uint64_t)max(tp0, 0) * step_b, uau = (uint64_t)p.u + (uint64_t)max(tp0, 0) * step_b;
+    uint64_t dxa = (uint64_t)p.dx + (uint64_t)(T - 1) * step_b, gra = (uint64_t)p.gr + (uint64_t)(T - 1) * step_b;
+#pragma unroll
+    for (int q = 0; q < kPrefetchSynBwd; ++q) {
+        const int tt = T - 1 - q;
+        const uint32_t nb = tt >= 0 ? row_bytes : 0u;
+        gq[q] = raw_buffer_load_f32(step_rsrc((uint64_t)p.gy + (uint64_t)max(tt, 0) * step_b, nb), voff, 0, 0);
+        uq[q] = raw_buffer_load_f32(step_rsrc((uint64_t)p.u + (uint64_t)max(tt, 0) * step_b, nb), voff, 0, 0);
+    }
+    float lam = 0.0f, dbacc = 0.0f;
+    int tmod = (T - 1) % R;
+    float* const own = act ? ring + (size_t)j * RP : ring + (size_t)(rows - 1) * RP;   // never read for j >= N
+
+    auto gather_group = [&](const Chunk (&cg)[kBwdGroup], int g0, int tbo, float (&acc)[KT], auto checked) {
+        constexpr bool CHK = decltype(checked)::value;
+#pragma unroll
+        for (int cc = 0; cc < kBwdGroup; ++cc) {
+            const float* rowc = ring + (size_t)(g0 + cc) * 16 * RP;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t ow = (e < 4) ? cg[cc].o.x : (e < 8) ? cg[cc].o.y : (e < 12) ? cg[cc].o.z : cg[cc].o.w;
+                const int off = ((int)(ow << (24 - 8 * (e & 3)))) >> 24;
+                int sl = tbo + off;
+                sl = sl >= R ? sl - R : sl;
+                const float* rp = rowc + e * RP + sl;
+                float wv;
+                if constexpr (WBF) {
+                    const uint4& wq = cg[cc].w[e >> 3];
+                    const int e8 = e & 7;
+                    const uint32_t w2 = (e8 < 2) ? wq.x : (e8 < 4) ? wq.y : (e8 < 6) ? wq.z : wq.w;
+                    wv = __uint_as_float((e & 1) ? (w2 & 0xFFFF0000u) : (w2 << 16));
+                } else {
+                    const uint4& wq = cg[cc].w[e >> 2];
+                    const int e4 = e & 3;
+                    wv = __uint_as_float(e4 == 0 ? wq.x : e4 == 1 ? wq.y : e4 == 2 ? wq.z : wq.w);
+                }
+                if constexpr (!CHK) {
+#pragma unroll
+                    for (int f = 0; f < KT; ++f) acc[f] = fmaf(wv, rp[f], acc[f]);
+                } else {
+#pragma unroll
+                    for (int f = 0; f < KT; ++f) {
+                        // lags <= 0 do not exist: such a tap weighs 0 (its slot holds a valid,
+                        // unrelated value)
+                        const float gv = rp[f];
+                        acc[f] = fmaf(wv, (lob + off + f >= 1) ? gv : 0.0f, acc[f]);
+                    }
+                }
+            }
+        }
+    };
+
+    auto step = [&](const int t, float& gs, float& us, auto checked) {
+        float acc[KT];
+#pragma unroll
+        for (int f = 0; f < KT; ++f) acc[f] = 0.0f;
+        // base slot of the smallest lag lob + omin (wrapped into [0, R)); a connection adds
+        // off - omin >= 0 (and one more wrap)
+        int tbo = tmod + lob + omin;
+        tbo %= R;
+        tbo = tbo < 0 ? tbo + R : tbo;
+        tbo -= omin;
+        Chunk ca[kBwdGroup], cb[kBwdGroup];
+#pragma unroll
+        for (int cc = 0; cc < kBwdGroup; ++cc) fetch(cc, ca[cc]);
+        for (int g = 0; g < NG; g += 2) {
+#pragma unroll
+            for (int cc = 0; cc < kBwdGroup; ++cc) fetch((g + 1) * kBwdGroup + cc, cb[cc]);
+            gather_group(ca, g * kBwdGroup, tbo, acc, checked);
+            if (g + 1 < NG) {
+#pragma unroll
+                for (int cc = 0; cc < kBwdGroup; ++cc) fetch((g + 2) * kBwdGroup + cc, ca[cc]);
+                gather_group(cb, (g + 1) * kBwdGroup, tbo, acc, checked);
+            }
+        }
+        float gf = 0.0f;
+#pragma unroll
+        for (int f = 0; f < KT; ++f) gf = fmaf(hq[f], acc[f], gf);
+        gf *= is2;
+        const float gyv = gs, u = us;
+        const float y = lif_fire(k, u);
+        const float du = lif_backward(k, gyv + gf, u, y, lam);
+        lam = k.decay * du;
+        const float da = lif_dx(k, du);
+        const float gr = da * m;
+        const bool live = t >= 0;
+        raw_buffer_store_f32(da, step_rsrc(dxa, live ? row_bytes : 0u), soff, 0, 0);
+        raw_buffer_store_f32(gr, step_rsrc(gra, live ? row_bytes : 0u), soff, 0, 0);
+        dxa -= step_b;
+        gra -= step_b;
+        dbacc += (live && act) ? gr : 0.0f;
+        if (act && live) {
+            own[tmod] = gr;
+            if (tmod < KT) own[tmod + R] = gr;
+        }
+        const int tp = t - kPrefetchSynBwd;
+        const uint32_t nb = tp >= 0 ? row_bytes : 0u;
+        gs = raw_buffer_load_f32(step_rsrc(gya, nb), voff, 0, 0);
+        us = raw_buffer_load_f32(step_rsrc(uau, nb), voff, 0, 0);
+        if (tp > 0) {
+            gya -= step_b;
+            uau -= step_b;
+        }
+        barrier_lds();
+        tmod = tmod == 0 ? R - 1 : tmod - 1;
+    };
+
+    auto run = [&](auto checked) {
+        for (int t0 = T - 1; t0 >= 0; t0 -= kPrefetchSynBwd) {
+#pragma unroll
+            for (int q = 0; q < kPrefetchSynBwd; ++q) step(t0 - q, gq[q], uq[q], checked);
+        }
+    };
+    if (chk) run(std::true_type{});
+    else run(std::false_type{});
+    if (act) p.part[(size_t)b * N + j] = dbacc;
+}
+
+#define DELREC_SBH_CASE(KTV, WBFV)                                                          \
+    if (kt == KTV && wbf == WBFV) {                                                          \
+        ensure_lds((const void*)syn_bwd_hyb<KTV, WBFV, 512>, lds);                           \
+        hipLaunchKernelGGL((syn_bwd_hyb<KTV, WBFV, 512>), dim3(a.B), dim3(block), lds, stream, a); \
+        return true;                                                                         \
+    }
+
+// blocks of up to 512 threads (two waves per SIMD, 256 VGPRs: the operand groups stay in
+// registers); larger blocks take syn_bwd_kernel
+bool launch_syn_bwd_hyb(const SynBwd& a, int block, size_t lds, hipStream_t stream) {
+    if (block > 512) return false;
+    const int kt = a.KT;
+    const bool wbf = a.w_bf16 != 0;
+    DELREC_SBH_CASE(2, false) DELREC_SBH_CASE(2, true) DELREC_SBH_CASE(4, false) DELREC_SBH_CASE(4, true)
+    return false;
 }
 
 // tap runs compiled for fixed lengths; other lengths take the runtime-count variant (KT = 0)
