@@ -269,18 +269,18 @@ SynBwdLayout syn_bwd_layout(int N, int L, int KT) {
     return o;
 }
 
-// the bf16 lag GEMM's packed operands: rows t * Bp + b (+ one stage of zero rows), columns
-// padded to the 128-wide output tile
+// the bf16 lag GEMM's packed operands: rows t * Bp + b with the batch padded to 32-row
+// chunks (one partial sum per chunk), columns padded to a multiple of 128
 struct LagPack {
     int Bp, Np, Kp, KS;
 };
 
 LagPack lag_pack(int T, int B, int N) {
     LagPack q;
-    q.Bp = (B + 7) / 8 * 8;
+    q.Bp = (B + 31) / 32 * 32;
     q.Np = (N + 127) / 128 * 128;
-    q.Kp = T * q.Bp + 32;
-    q.KS = lag_bf16_splits(T, q.Bp, q.Np, num_cus());
+    q.Kp = T * q.Bp;
+    q.KS = q.Bp / 32;
     return q;
 }
 
@@ -310,7 +310,7 @@ void syn_bwd_ws(C& c, int T, int B, int N, int L) {
     c.template take<uint4>(packed);                     // gr_hi
     c.template take<uint4>(packed);                     // gr_lo
     c.template take<uint4>(packed);                     // shifted spikes
-    c.template take<int>((size_t)N + 64);               // R and first lag per column
+    c.template take<int>((size_t)3 * N + 64);           // lag range per column, meta
     c.template take<float>((size_t)N * lay.NT);         // W^T (fp32 or bf16)
     c.template take<float>((size_t)N * lay.NT);         // d^T or the offsets^T
     c.template take<float>((size_t)B * N * lay.RP);     // ring when it does not fit LDS
@@ -675,6 +675,9 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     const int T = a->T, B = a->B, N = a->N;
     const LagPack q = lag_pack(T, B, N);
     const size_t packed = (size_t)q.Kp / 8 * q.Np;
+    // the lag GEMM addresses a packed operand with 32-bit byte offsets (plus a window of
+    // slices past the end)
+    if ((size_t)(T + 32) * (q.Bp / 8) * q.Np * 16 >= ((size_t)1 << 32)) return DELREC_ERR_UNSUPPORTED;
     Carver cv(a->workspace, a->workspace_bytes);
     float* gr = cv.take<float>((size_t)T * B * N);
     float* part = cv.take<float>((size_t)B * N);
@@ -682,7 +685,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     uint4* ahi = cv.take<uint4>(packed);
     uint4* alo = cv.take<uint4>(packed);
     uint4* yb = cv.take<uint4>(packed);
-    int* meta = cv.take<int>((size_t)N + 64);
+    int* meta = cv.take<int>((size_t)3 * N + 64);
     void* wt = cv.take<float>((size_t)N * wlay.NT);
     void* dt = cv.take<float>((size_t)N * wlay.NT);
     float* gring = cv.take<float>((size_t)B * N * wlay.RP);
@@ -690,14 +693,20 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         return DELREC_ERR_WORKSPACE;
 
     if (a->w_bf16) block_transpose<uint16_t>(a->W, wt, N, s); else block_transpose<float>(a->W, wt, N, s);
-    if (hybrid) {
-        block_transpose<int8_t>(a->offsets, dt, N, s);
-        // offset range (meta[0] = relative lags of the lag GEMM, meta[1] = smallest offset)
-        // and each column's first lag, read by the scan and the lag GEMM
-        launch_lag_range(a->offsets, a->base, N, a->L, a->s_uniform, meta, meta + 64, s);
-    } else {
-        block_transpose<float>(a->d, dt, N, s);
-    }
+    if (hybrid) block_transpose<int8_t>(a->offsets, dt, N, s);
+    else block_transpose<float>(a->d, dt, N, s);
+    // each column's lag range for the lag GEMM, and the smallest offset (meta[1]) the
+    // hybrid scan reads
+    const size_t NN = (size_t)N * N;
+    LagBf16 g{};
+    g.T = T; g.B = B; g.Bp = q.Bp; g.N = N; g.Np = q.Np; g.L = a->L; g.Kp = q.Kp; g.KS = q.KS;
+    g.ahi = ahi; g.alo = alo; g.yb = yb;
+    g.meta = meta; g.lo = meta + 64; g.rc = meta + 64 + N; g.om = meta + 64 + 2 * N;
+    g.d = a->d; g.base = a->base; g.off = a->offsets; g.s = a->s; g.s_uniform = a->s_uniform;
+    g.pw = lagp;
+    g.pd = lagp + (size_t)q.KS * NN;
+    g.ps = a->ds ? lagp + (size_t)2 * q.KS * NN : nullptr;
+    launch_lag_cols(g, s);
 
     SynBwd p{};
     p.T = T; p.B = B; p.N = N; p.L = a->L;
@@ -723,17 +732,6 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     if (st) return st;
     launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
     if (a->dW || a->dd || a->ds) {
-        const size_t NN = (size_t)N * N;
-        LagBf16 g{};
-        g.T = T; g.B = B; g.Bp = q.Bp; g.N = N; g.Np = q.Np; g.L = a->L; g.Kp = q.Kp; g.KS = q.KS;
-        g.R = std::max(a->L - 1, 1);
-        g.ahi = ahi; g.alo = alo; g.yb = yb;
-        g.meta = hybrid ? meta : nullptr;
-        g.lo = hybrid ? meta + 64 : nullptr;
-        g.d = a->d; g.base = a->base; g.off = a->offsets; g.s = a->s; g.s_uniform = a->s_uniform;
-        g.pw = lagp;
-        g.pd = lagp + (size_t)q.KS * NN;
-        g.ps = a->ds ? lagp + (size_t)2 * q.KS * NN : nullptr;
         launch_lag_bf16(g, gr, a->bits, s);
         LagGemm f{};
         f.N = N; f.KS = q.KS; f.W = a->W; f.w_bf16 = a->w_bf16; f.s = a->s; f.s_uniform = a->s_uniform;

@@ -114,14 +114,17 @@ struct LagGemm {
     float* ps;                  // [KS][N][N] partial sum_l dh/ds * C_l, or NULL
 };
 
-// bf16-MFMA lag-correlation GEMM (lagmm.hip): operands packed in the k-blocked layout
+// bf16-MFMA lag-correlation GEMM (lagmm.hip): operands packed in the k-blocked layout,
+// batch padded to Bp = 32n (KS = Bp / 32 chunk partials)
 struct LagBf16 {
-    int T, B, Bp, N, Np, L, Kp, KS, R;   // R: relative lags when meta == NULL
+    int T, B, Bp, N, Np, L, Kp, KS;
     const uint4* ahi;            // gr_hi (Kp, Np) k-blocked
     const uint4* alo;            // gr_lo
     const uint4* yb;             // shifted spikes Y' (Kp, Np) k-blocked
-    int* meta;                   // hybrid: meta[0] = R written by lag_range_kernel, else NULL
-    int* lo;                     // hybrid: first lag per column, else NULL (lo = 1)
+    int* meta;                   // meta[0] = widest column lag range, meta[1] = smallest offset
+    int* lo;                     // [N] first lag of each column
+    int* rc;                     // [N] number of lags of each column
+    int* om;                     // [N] smallest offset of each column (hybrid)
     const float* d;              // row-major, or NULL (hybrid)
     const float* base;
     const int8_t* off;
@@ -173,10 +176,8 @@ bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);
 // hybrid backward, ring in LDS over ceil(N/64)*64 rows, one source per lane (N <= 512),
 // KT = 2 or 4; false when it does not apply
 bool launch_syn_bwd_hyb(const SynBwd& a, int block, size_t lds, hipStream_t stream);
-int lag_bf16_splits(int T, int Bp, int Np, int cus);
-// hybrid: meta[0] = relative lags, meta[1] = smallest offset, lo[j] = first lag of column j
-void launch_lag_range(const int8_t* off, const float* base, int N, int L, float s, int* meta, int* lo,
-                      hipStream_t stream);
+// each column's lag range (lo, rc, om) and meta[0..1]
+void launch_lag_cols(const LagBf16& a, hipStream_t stream);
 // packs gr / spikes, then the lag GEMM into a.pw / a.pd / a.ps
 void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hipStream_t stream);
 // dW = sum_k pw; dd = W/s^2 * sum_k pd; ds[j] = sum_i W[i,j] * sum_k ps[i,j]

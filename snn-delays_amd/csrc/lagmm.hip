@@ -14,14 +14,14 @@
 // carries a relative error below 2^-16 of gr (fp32 accumulation). The packed operands use
 // a k-blocked layout, element (k, m) at ((k / 8) * Np + m) * 8 + k % 8, so one 16-byte load
 // holds the 8 consecutive k of one column that an MFMA lane supplies; a row k is
-// (t * Bp + b) with the batch padded to Bp = 8n, so a time shift is a whole number of
-// blocks.
+// (t * Bp + b) with the batch padded to a multiple of 32, so a 32-row batch chunk of one
+// time step is 4 whole k-blocks.
 //
 // Relative lags: column j's spike train is stored shifted by its first lag lo_j,
-// Y'[t, b, j] = y[t - lo_j, b, j], and the kernel walks r = 0 .. R-1 with l = lo_j + r.
-// Synaptic delays use lo_j = 1, R = L - 1 (every lag). A hybrid delay base[j] + offset[i,j]
-// with integer offsets puts every connection of column j within R = (max - min offset) +
-// ceil(2s) + 4 lags of lo_j, so the hybrid runs R instead of L - 1 lags.
+// Y'[t, b, j] = y[t - lo_j, b, j], and the kernel walks r = 0 .. R-1 with l = lo_j + r, where
+// [lo_j, lo_j + R_j) is the exact range of lags on the triangle support of some connection
+// of column j and R is the widest R_j of a 64-column tile (hybrid: (max - min offset) +
+// 2s, give or take one; synaptic: up to L - 1).
 //
 // MFMA v_mfma_f32_16x16x32_bf16 (wave64): lane l supplies A[l%16][8g .. 8g+7] and
 // B[8g .. 8g+7][l%16] with g = l/16 (the same k order for A and B); accumulator register r
@@ -32,10 +32,6 @@ namespace delrec {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-constexpr int kLT = 128;   // output tile (i and j) per workgroup
-constexpr int kLK = 32;    // rows of k per stage
-constexpr int kLKB = kLK / 8;
 
 __device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
     uint32_t u = __float_as_uint(f);
@@ -103,214 +99,255 @@ __global__ void pack_spikes_kernel(const uint32_t* __restrict__ bits, const int*
     }
 }
 
-// Hybrid lag range: one workgroup reduces the offsets to their min / max, then writes the
-// number of relative lags R (meta[0]), the smallest offset (meta[1]) and each column's
-// first lag lo_j.
-__global__ void __launch_bounds__(1024) lag_range_kernel(const int8_t* __restrict__ off,
-                                                         const float* __restrict__ base, int N, int L,
-                                                         float s, int* __restrict__ meta,
-                                                         int* __restrict__ lo) {
-    __shared__ int smin[16], smax[16];
-    __shared__ int s_omin, s_full;
-    const size_t NN = (size_t)N * N;
-    int mn = 127, mx = -128;
-    for (size_t q = threadIdx.x; q < NN; q += blockDim.x) {
-        const int v = off[q];
-        mn = min(mn, v);
-        mx = max(mx, v);
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        mn = min(mn, __shfl_xor(mn, o));
-        mx = max(mx, __shfl_xor(mx, o));
-    }
-    if ((threadIdx.x & 63) == 0) {
-        smin[threadIdx.x >> 6] = mn;
-        smax[threadIdx.x >> 6] = mx;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int a = 127, z = -128;
-        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
-            a = min(a, smin[w]);
-            z = max(z, smax[w]);
-        }
-        int R = (z - a) + (int)ceilf(2.0f * s) + 4;
-        const bool full = R >= L - 1;
-        if (full) R = L - 1;
-        meta[0] = max(R, 1);
-        meta[1] = a;
-        s_omin = a;
-        s_full = full ? 1 : 0;
-    }
-    __syncthreads();
-    const int omin = s_omin;
-    const bool full = s_full != 0;
-    for (int j = threadIdx.x; j < N; j += blockDim.x)
-        lo[j] = full ? 1 : max(1, (int)floorf(1.0f + base[j] + (float)omin - s) - 1);
-}
-
 __device__ __forceinline__ float lag_conn_delay(const LagBf16& p, int i, int j) {
     if (p.d) return p.d[(size_t)i * p.N + j];
     return p.base[j] + 0.0f + 1.0f * (float)p.off[(size_t)i * p.N + j];
 }
 
-// 128x128 output tile per workgroup, 4 waves of 64x64 (4x4 MFMA blocks), split over k
-// (blockIdx.z). Per relative lag r: the k range of the split (rows k < (T - r) * Bp) is
-// staged through two LDS buffers 32 rows at a time (gr_hi, gr_lo shifted by r * Bp rows,
-// Y' unshifted), the next stage's 16-byte global loads held in registers meanwhile; then
-// the tile of C_{lo_j + r} is folded into the per-element sums.
-constexpr int kCP = kLT + 4;   // pitch of the delay tile in LDS (conflict-free epilogue reads)
-
-template <bool DS>
-__global__ void __launch_bounds__(256) lag_bf16_kernel(LagBf16 p) {
-    __shared__ uint4 sbuf[2][3][kLKB * kLT];
-    __shared__ float scc[kLT * kCP];        // 1 + d_ij of the tile
-    const int N = p.N, Np = p.Np, T = p.T, Bp = p.Bp;
-    const int i0 = blockIdx.x * kLT, j0 = blockIdx.y * kLT;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int wi = w >> 1, wj = w & 1;
-    const int g = lane >> 4, lc = lane & 15;
-    const int R = p.meta ? p.meta[0] : p.R;
-    const int steps_all = (T * Bp + kLK - 1) / kLK;
-    const int per = (steps_all + (int)gridDim.z - 1) / (int)gridDim.z;
-    const int sb = (int)blockIdx.z * per, se = min(steps_all, sb + per);
-
-    for (int q = tid; q < kLT * kLT; q += 256) {
-        const int ii = q >> 7, jj = q & (kLT - 1);
-        const int i = i0 + ii, j = j0 + jj;
-        scc[ii * kCP + jj] = (i < N && j < N) ? 1.0f + lag_conn_delay(p, i, j) : 0.0f;
+// Lag range of each column: the first and last integer lag l in [1, L-1] on the closed
+// support |l - (1 + d_ij)| <= s_j of some connection (i, j), decided by the fp32 test the
+// fold uses (tap_range), so a lag outside [lo_j, lo_j + rc_j) has zero weight and zero
+// derivative for every receiver. Also each column's smallest offset (hybrid). A workgroup
+// covers 64 columns with 16 lanes over the receivers.
+__global__ void __launch_bounds__(1024) lag_cols_kernel(LagBf16 p) {
+    __shared__ int sa[16][64], sz[16][64], so[16][64];
+    const int jl = threadIdx.x & 63, il = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + jl;
+    int a = 0x7fffffff, z = -0x7fffffff, om = 127;
+    if (j < p.N) {
+        const float s = p.s ? p.s[j] : p.s_uniform;
+        for (int i = il; i < p.N; i += 16) {
+            int l0, l1;
+            tap_range(1.0f + lag_conn_delay(p, i, j), s, p.L, l0, l1);
+            if (l0 <= l1) {
+                a = min(a, l0);
+                z = max(z, l1);
+            }
+            if (p.off) om = min(om, (int)p.off[(size_t)i * p.N + j]);
+        }
     }
-    // this lane's output elements: i = i0 + wi*64 + mb*16 + 4g + e, j = j0 + wj*64 + nb*16 + lc
-    float sj[4];
-    int loj[4];
+    sa[il][jl] = a;
+    sz[il][jl] = z;
+    so[il][jl] = om;
+    __syncthreads();
+    if (il == 0 && j < p.N) {
+        for (int q = 1; q < 16; ++q) {
+            a = min(a, sa[q][jl]);
+            z = max(z, sz[q][jl]);
+            om = min(om, so[q][jl]);
+        }
+        p.lo[j] = a <= z ? a : 1;
+        p.rc[j] = a <= z ? z - a + 1 : 0;
+        p.om[j] = om;
+    }
+}
+
+// meta[0] = widest column lag range, meta[1] = smallest offset (hybrid)
+__global__ void __launch_bounds__(1024) lag_meta_kernel(const int* __restrict__ rc,
+                                                        const int* __restrict__ om, int N,
+                                                        int* __restrict__ meta) {
+    __shared__ int sr[16], so[16];
+    int r = 0, o = 127;
+    for (int j = threadIdx.x; j < N; j += blockDim.x) {
+        r = max(r, rc[j]);
+        o = min(o, om[j]);
+    }
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-        const int j = j0 + wj * 64 + nb * 16 + lc;
+    for (int k = 32; k >= 1; k >>= 1) {
+        r = max(r, __shfl_xor(r, k));
+        o = min(o, __shfl_xor(o, k));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sr[threadIdx.x >> 6] = r;
+        so[threadIdx.x >> 6] = o;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) {
+            r = max(r, sr[w]);
+            o = min(o, so[w]);
+        }
+        meta[0] = r;
+        meta[1] = o;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Windowed lag GEMM. Workgroup: a 64 x 64 output tile (4 waves of 32 x 32, 2 x 2 MFMA
+// blocks each) and one 32-row batch chunk bc of every time step (the k split: partial
+// sums per chunk). A time slice of an operand is the chunk's 4 k-blocks at time t.
+//
+// For the relative lags r = q0 .. q0 + RL - 1 of one pass, C_r = sum_tau A(tau) Y'(tau - r)
+// with A = (gr_hi, gr_lo). Step n reads the gr slice tau = q0 + n once and multiplies it
+// with the spike slices n - r', r' < RL, which stay in registers: a window of kWY slots
+// holds slice sigma in slot sigma mod kWY, so step n refills slot (n + P) mod kWY (slice
+// n + P, P = kWY - RL ahead) after its last reader, step n - 1, and the gr slices rotate
+// through kWA slots (kWA - 1 ahead). The loop body is unrolled over kWY steps, so every
+// slot is a fixed register set and each load is waited for only where it is first read.
+// One descriptor per operand spans the chunk's slices 0 .. T-1, so slices at or past T
+// read as zeros; slice t is the byte offset t * (Bp / 8) * Np * 16 plus the lane's column.
+constexpr int kWT = 64;    // output tile (i and j)
+constexpr int kWA = 4;     // gr-slice registers (3 slices ahead)
+
+__device__ __forceinline__ bf16x8 load16(i32x4 rs, int voff) {
+    return __builtin_bit_cast(bf16x8, raw_buffer_load_i32x4(rs, voff, 0, 0));
+}
+
+template <int RL, int kWY, bool DS>
+__device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, int bc, int rt) {
+    constexpr int P = kWY - RL;   // spike slices loaded ahead
+    static_assert(kWY % kWA == 0 && P >= 1, "window slots");
+    const int N = p.N, Np = p.Np, T = p.T;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int wi = w >> 1, wj = w & 1, g = lane >> 4, lc = lane & 15;
+    const uint32_t slice = (uint32_t)(p.Bp / 8) * Np * 16;   // bytes per time slice
+    const size_t chunk = (size_t)bc * 4 * Np;                  // uint4 offset of the chunk
+    const uint32_t span = (uint32_t)T * slice - (uint32_t)(chunk * 16);
+    const i32x4 rhi = buffer_rsrc(p.ahi + chunk, span);
+    const i32x4 rlo = buffer_rsrc(p.alo + chunk, span);
+    const i32x4 ryb = buffer_rsrc(p.yb + chunk, span);
+    // lane offsets of the first 16-column block; the second is 256 bytes further
+    const uint32_t va = (uint32_t)(g * Np + i0 + wi * 32 + lc) * 16;
+    const uint32_t vy = (uint32_t)(g * Np + j0 + wj * 32 + lc) * 16;
+    float sj[2];
+    int loj[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const int j = j0 + wj * 32 + nb * 16 + lc;
         const int jc = j < N ? j : 0;
         sj[nb] = p.s ? p.s[jc] : p.s_uniform;
-        loj[nb] = p.lo ? p.lo[jc] : 1;
+        loj[nb] = p.lo[jc];
     }
-    float ow[4][4][4], od[4][4][4], os[DS ? 4 : 1][4][4];
+    const bf16x8 zero = __builtin_bit_cast(bf16x8, i32x4{0, 0, 0, 0});
+    const size_t NN = (size_t)N * N;
+
+    for (int q0 = 0; q0 < max(rt, 1) && q0 < T; q0 += RL) {
+        floatx4 acc[RL][2][2];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+        for (int r = 0; r < RL; ++r)
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+            for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                ow[mb][nb][e] = 0.0f;
-                od[mb][nb][e] = 0.0f;
-                if (DS) os[DS ? mb : 0][nb][e] = 0.0f;
+                for (int nb = 0; nb < 2; ++nb) acc[r][mb][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        bf16x8 yw[kWY][2], ah[kWA][2], al[kWA][2];
+#pragma unroll
+        for (int sl = 0; sl < kWY; ++sl) {
+            if (sl < P) {   // slices 0 .. P-1; the other slots hold slices -RL+1 .. -1
+                const uint32_t o = vy + (uint32_t)sl * slice;
+                yw[sl][0] = load16(ryb, o);
+                yw[sl][1] = load16(ryb, o + 256);
+            } else {
+                yw[sl][0] = zero;
+                yw[sl][1] = zero;
             }
-
-    // staging: each operand stage is kLKB * kLT = 512 uint4, two per thread
-    uint4 st[3][2];
-    auto fetch = [&](int step, size_t ashift_blocks) {
-        const size_t kb0 = (size_t)step * kLKB;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int c = tid + h * 256;
-            const int kb = c >> 7, m = c & (kLT - 1);
-            st[0][h] = p.ahi[(kb0 + ashift_blocks + kb) * Np + i0 + m];
-            st[1][h] = p.alo[(kb0 + ashift_blocks + kb) * Np + i0 + m];
-            st[2][h] = p.yb[(kb0 + kb) * Np + j0 + m];
         }
-    };
-    auto stash = [&](int buf) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int c = tid + h * 256;
-            sbuf[buf][0][c] = st[0][h];
-            sbuf[buf][1][c] = st[1][h];
-            sbuf[buf][2][c] = st[2][h];
+        for (int sl = 0; sl < kWA - 1; ++sl) {
+            const uint32_t o = va + (uint32_t)(q0 + sl) * slice;
+            ah[sl][0] = load16(rhi, o);
+            ah[sl][1] = load16(rhi, o + 256);
+            al[sl][0] = load16(rlo, o);
+            al[sl][1] = load16(rlo, o + 256);
         }
-    };
-
-    for (int r = 0; r < R; ++r) {
-        const int kend = (T - r) * Bp;              // rows k with t + r < T
-        const int se_r = min(se, (kend + kLK - 1) / kLK);
-        if (se_r <= sb) break;                      // later lags have fewer rows still
-        const size_t ashift = (size_t)r * (Bp / 8); // blocks of the gr shift r * Bp
-        floatx4 acc[4][4];
+        const int nsteps = T - q0;
+        // running offsets of the next spike slice (n + P) and the next gr slice (q0 + n + kWA - 1)
+        uint32_t oy = vy + (uint32_t)P * slice;
+        uint32_t oa = va + (uint32_t)(q0 + kWA - 1) * slice;
+        for (int n0 = 0; n0 < nsteps; n0 += kWY) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-        fetch(sb, ashift);
-        stash(0);
-        __syncthreads();
-        int buf = 0;
-        for (int step = sb; step < se_r; ++step) {
-            const bool more = step + 1 < se_r;
-            if (more) fetch(step + 1, ashift);
-            bf16x8 ah[4], al[4], bv[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                ah[q] = __builtin_bit_cast(bf16x8, sbuf[buf][0][g * kLT + wi * 64 + q * 16 + lc]);
-                al[q] = __builtin_bit_cast(bf16x8, sbuf[buf][1][g * kLT + wi * 64 + q * 16 + lc]);
-                bv[q] = __builtin_bit_cast(bf16x8, sbuf[buf][2][g * kLT + wj * 64 + q * 16 + lc]);
-            }
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-                for (int nb = 0; nb < 4; ++nb) {
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[mb], bv[nb], acc[mb][nb], 0, 0, 0);
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[mb], bv[nb], acc[mb][nb], 0, 0, 0);
+            for (int u = 0; u < kWY; ++u) {
+                {
+                    yw[(u + P) % kWY][0] = load16(ryb, oy);
+                    yw[(u + P) % kWY][1] = load16(ryb, oy + 256);
+                    ah[(u + kWA - 1) % kWA][0] = load16(rhi, oa);
+                    ah[(u + kWA - 1) % kWA][1] = load16(rhi, oa + 256);
+                    al[(u + kWA - 1) % kWA][0] = load16(rlo, oa);
+                    al[(u + kWA - 1) % kWA][1] = load16(rlo, oa + 256);
+                    oy += slice;
+                    oa += slice;
                 }
-            if (more) stash(buf ^ 1);
-            __syncthreads();
-            buf ^= 1;
+                // keep the refills at the top of the step, ahead of this step's products
+                __builtin_amdgcn_sched_barrier(0);
+                const int sa = u % kWA;
+#pragma unroll
+                for (int r = 0; r < RL; ++r)
+#pragma unroll
+                    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb)
+                            acc[r][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                ah[sa][mb], yw[(u - r + kWY) % kWY][nb], acc[r][mb][nb], 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < RL; ++r)
+#pragma unroll
+                    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb)
+                            acc[r][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                al[sa][mb], yw[(u - r + kWY) % kWY][nb], acc[r][mb][nb], 0, 0, 0);
+            }
         }
 
-        // fold C_l, l = lo_j + r, into the per-element sums (lags past L - 1 do not exist)
+        // fold C_l, l = lo_j + q0 + r, into this chunk's partial sums (lags past L - 1 do
+        // not exist)
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-            const int l = loj[nb] + r;
-            const float lf = (float)l;
-            const bool in = l <= p.L - 1;
+        for (int nb = 0; nb < 2; ++nb) {
+            const int j = j0 + wj * 32 + nb * 16 + lc;
             const float sv = sj[nb], s2 = sv * sv;
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+            for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float C = in ? acc[mb][nb][e] : 0.0f;
-                    const float cv = scc[(wi * 64 + mb * 16 + 4 * g + e) * kCP + wj * 64 + nb * 16 + lc];
-                    ow[mb][nb][e] += tri_weight(lf, cv, sv, s2) * C;
-                    od[mb][nb][e] += tri_dsign(lf, cv, sv) * C;
-                    if (DS) os[DS ? mb : 0][nb][e] += tri_ds(lf, cv, sv, s2) * C;
+                    const int i = i0 + wi * 32 + mb * 16 + 4 * g + e;
+                    if (i >= N || j >= N) continue;
+                    const float cv = 1.0f + lag_conn_delay(p, i, j);
+                    float ow = 0.0f, od = 0.0f, os = 0.0f;
+#pragma unroll
+                    for (int r = 0; r < RL; ++r) {
+                        const int l = loj[nb] + q0 + r;
+                        const float C = l <= p.L - 1 ? acc[r][mb][nb][e] : 0.0f;
+                        const float lf = (float)l;
+                        ow += tri_weight(lf, cv, sv, s2) * C;
+                        od += tri_dsign(lf, cv, sv) * C;
+                        if (DS) os += tri_ds(lf, cv, sv, s2) * C;
+                    }
+                    const size_t o = (size_t)bc * NN + (size_t)i * N + j;
+                    if (q0 > 0) {
+                        ow += p.pw[o];
+                        od += p.pd[o];
+                        if (DS) os += p.ps[o];
+                    }
+                    p.pw[o] = ow;
+                    p.pd[o] = od;
+                    if (DS) p.ps[o] = os;
                 }
         }
     }
-
-    const size_t NN = (size_t)N * N;
-    const size_t base_o = (size_t)blockIdx.z * NN;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int i = i0 + wi * 64 + mb * 16 + 4 * g + e;
-                const int j = j0 + wj * 64 + nb * 16 + lc;
-                if (i >= N || j >= N) continue;
-                const size_t o = base_o + (size_t)i * N + j;
-                p.pw[o] = ow[mb][nb][e];
-                p.pd[o] = od[mb][nb][e];
-                if (DS) p.ps[o] = os[DS ? mb : 0][nb][e];
-            }
 }
 
-void launch_lag_range(const int8_t* off, const float* base, int N, int L, float s, int* meta, int* lo,
-                      hipStream_t stream) {
-    hipLaunchKernelGGL(lag_range_kernel, dim3(1), dim3(1024), 0, stream, off, base, N, L, s, meta, lo);
+// one workgroup per (output tile, batch chunk); the chunk is the fastest index, so with 8
+// chunks the workgroups of one chunk share an XCD (workgroups are dealt to the XCDs in
+// turn) and its L2 holds the slices they all stream. Tiles of at most 10 lags run the
+// 10-lag passes and wider ones 12-lag passes; the launch of each variant skips the other's
+// tiles (each variant gets the whole register file to itself).
+template <int RL, bool DS>
+__global__ void __launch_bounds__(256) lag_win_kernel(LagBf16 p) {
+    const int nbc = p.Bp / 32;
+    const int bc = (int)blockIdx.x % nbc, tile = (int)blockIdx.x / nbc;
+    const int tj = p.Np / kWT;
+    const int i0 = (tile / tj) * kWT, j0 = (tile % tj) * kWT;
+    const int j = j0 + (int)(threadIdx.x & 63);
+    int rt = j < p.N ? p.rc[j] : 0;   // the tile's lags: the widest range among its columns
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) rt = max(rt, __shfl_xor(rt, k));
+    rt = __builtin_amdgcn_readfirstlane(rt);
+    if ((rt <= 10) != (RL == 10)) return;
+    lag_win_body<RL, RL == 10 ? 12 : 16, DS>(p, i0, j0, bc, rt);
 }
 
-int lag_bf16_splits(int T, int Bp, int Np, int cus) {
-    const int tiles = (Np / kLT) * (Np / kLT);
-    const int steps = (T * Bp + kLK - 1) / kLK;
-    const int want = (cus + tiles - 1) / tiles;
-    return std::max(1, std::min(want, steps / 8 > 0 ? steps / 8 : 1));
+void launch_lag_cols(const LagBf16& a, hipStream_t stream) {
+    hipLaunchKernelGGL(lag_cols_kernel, dim3((a.N + 63) / 64), dim3(1024), 0, stream, a);
+    hipLaunchKernelGGL(lag_meta_kernel, dim3(1), dim3(1024), 0, stream, a.rc, a.om, a.N, a.meta);
 }
 
 void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hipStream_t stream) {
@@ -320,11 +357,15 @@ void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hi
                        a.Np, a.Kp, const_cast<uint4*>(a.ahi), const_cast<uint4*>(a.alo));
     hipLaunchKernelGGL(pack_spikes_kernel, dim3(blocks), dim3(256), 0, stream, bits, a.lo, a.T, a.B,
                        a.Bp, a.N, a.Np, a.Kp, const_cast<uint4*>(a.yb));
-    const dim3 grid(a.Np / kLT, a.Np / kLT, a.KS);
-    if (a.ps)
-        hipLaunchKernelGGL(lag_bf16_kernel<true>, grid, dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL(lag_bf16_kernel<false>, grid, dim3(256), 0, stream, a);
+    const int tiles = (a.Np / kWT) * (a.Np / kWT);
+    const dim3 grid((unsigned)(tiles * (a.Bp / 32)));
+    if (a.ps) {
+        hipLaunchKernelGGL((lag_win_kernel<10, true>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((lag_win_kernel<12, true>), grid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((lag_win_kernel<10, false>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((lag_win_kernel<12, false>), grid, dim3(256), 0, stream, a);
+    }
 }
 
 }  // namespace delrec
