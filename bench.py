@@ -130,7 +130,7 @@ def algorithmic_work(w):
 # kernel symbol of each time-scan kind at each workload's shape (for the rocprof summaries)
 SCAN_SYMBOL = {
     'C2': {'axonal_fwd_scan': 'axonal_fwd_wave_fast', 'axonal_bwd_scan': 'axonal_bwd_tiled_fast'},
-    'C3': {'syn_fwd_scan': 'syn_fwd_kernel', 'syn_bwd_scan': 'syn_bwd_kernel'},
+    'C3': {'syn_fwd_scan': 'syn_fwd_scatter', 'syn_bwd_scan': 'syn_bwd_hyb'},
     'C4': {'syn_fwd_scan': 'syn_fwd_gather_kernel', 'syn_bwd_scan': 'syn_bwd_kernel'},
 }
 
