@@ -288,8 +288,54 @@ LagPack lag_pack(int T, int B, int N) {
 int syn_gather_words(int L) { return L - 1 <= 64 ? 1 : (L - 1 <= 128 ? 2 : 0); }
 int syn_gather_taps(float s_max) { return (int)std::floor(2.0f * s_max) + 2; }
 
+// The lag-stacked per-step GEMM scans (lagstep.hip) run where the rings of the gather /
+// scatter scans do not fit one CU's LDS; DELREC_SYN_LAGSTEP=1 forces them (any size),
+// =0 turns them off. Operands are addressed with 32-bit byte offsets.
+struct LagStepDims {
+    int Nk, Np, Lw, Kt, KS;
+    size_t lda;         // history row pitch (elements): (T + Lw) * Nk
+    size_t plane;       // uint4 per packed M plane
+    bool ok;
+};
+
+LagStepDims lagstep_dims(int T, int B, int N, int L) {
+    LagStepDims q{};
+    q.Nk = (N + 31) / 32 * 32;
+    q.Np = (N + 127) / 128 * 128;
+    q.Lw = std::max(L - 1, 1);
+    q.Kt = q.Lw * q.Nk;
+    q.lda = (size_t)(T + q.Lw) * q.Nk;
+    q.plane = (size_t)(q.Kt / 8) * q.Np;
+    q.KS = lagstep_splits(B, q.Np, q.Kt, num_cus());
+    const size_t Bpad = (size_t)(B + 127) / 128 * 128;
+    q.ok = Bpad * q.lda * 2 < ((size_t)1 << 32) && q.plane * 16 < ((size_t)1 << 32);
+    return q;
+}
+
+bool syn_lagstep(int T, int B, int N, int L) {
+    const char* e = getenv("DELREC_SYN_LAGSTEP");
+    if (e && e[0] == '0') return false;
+    if (!lagstep_dims(T, B, N, L).ok) return false;
+    if (e && e[0] == '1') return true;
+    return !syn_layout(N, L, true).lds_ring;
+}
+
 template <class C>
-void syn_fwd_ws(C& c, int B, int N, int L, bool hybrid, bool bf16) {
+void lagstep_ws(C& c, int T, int B, int N, int L, bool fwd) {
+    const LagStepDims q = lagstep_dims(T, B, N, L);
+    c.template take<uint4>(2 * q.plane);                         // M planes
+    c.template take<uint16_t>((size_t)B * q.lda);                // history (spikes / gr hi)
+    if (!fwd) c.template take<uint16_t>((size_t)B * q.lda);      // gr lo
+    c.template take<float>((size_t)q.KS * B * q.Np);             // split-K partials
+    c.template take<float>((size_t)B * N);                       // v / lambda
+}
+
+template <class C>
+void syn_fwd_ws(C& c, int T, int B, int N, int L, bool hybrid, bool bf16) {
+    if (syn_lagstep(T, B, N, L)) {
+        lagstep_ws(c, T, B, N, L, true);
+        return;
+    }
     const SynLayout lay = syn_layout(N, L, true);
     const size_t nb = (size_t)((N + 15) / 16) * 16 * N;   // blocked copies
     if (bf16) c.template take<uint16_t>(nb); else c.template take<float>(nb);
@@ -311,6 +357,10 @@ void syn_bwd_ws(C& c, int T, int B, int N, int L) {
     c.template take<uint4>(packed);                     // gr_lo
     c.template take<uint4>(packed);                     // shifted spikes
     c.template take<int>((size_t)3 * N + 64);           // lag range per column, meta
+    if (syn_lagstep(T, B, N, L)) {
+        lagstep_ws(c, T, B, N, L, false);
+        return;
+    }
     c.template take<float>((size_t)N * lay.NT);         // W^T (fp32 or bf16)
     c.template take<float>((size_t)N * lay.NT);         // d^T or the offsets^T
     c.template take<float>((size_t)B * N * lay.RP);     // ring when it does not fit LDS
@@ -449,7 +499,7 @@ int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_
             axonal_bwd_ws(c, T, B, N, lay);
             break;
         }
-        case DELREC_WS_SYN_FWD: syn_fwd_ws(c, B, N, L, (flags & 2) != 0, bf16); break;
+        case DELREC_WS_SYN_FWD: syn_fwd_ws(c, T, B, N, L, (flags & 2) != 0, bf16); break;
         case DELREC_WS_SYN_BWD: syn_bwd_ws(c, T, B, N, L); break;
         default: return DELREC_ERR_ARG;
     }
@@ -593,6 +643,40 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     return finish_launch();
 }
 
+// forward as one lag-stacked GEMM + one LIF launch per step
+int syn_fwd_lagstep(const delrec_syn_fwd_args* a, hipStream_t s) {
+    const int T = a->T, B = a->B, N = a->N;
+    const LagStepDims q = lagstep_dims(T, B, N, a->L);
+    Carver cv(a->workspace, a->workspace_bytes);
+    uint4* planes = cv.take<uint4>(2 * q.plane);
+    uint16_t* hist = cv.take<uint16_t>((size_t)B * q.lda);
+    float* part = cv.take<float>((size_t)q.KS * B * q.Np);
+    float* state = cv.take<float>((size_t)B * N);
+    if (!planes || !hist || !part || !state) return DELREC_ERR_WORKSPACE;
+    LagStepPack pk{};
+    pk.N = N; pk.Nk = q.Nk; pk.Np = q.Np; pk.Lw = q.Lw;
+    pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.d = a->d; pk.base = a->base; pk.off = a->offsets;
+    pk.s = a->s; pk.s_uniform = a->s_uniform; pk.out = planes;
+    launch_pack_lagw(pk, true, s);
+    launch_hist_zero(hist, B, q.lda, q.Nk, 0, q.Lw, s);   // spikes before t = 0
+    LagStepGemm g{};
+    g.a0 = hist; g.a1 = nullptr; g.lda = q.lda; g.B = B;
+    g.p0 = planes; g.p1 = planes + q.plane; g.Np = q.Np; g.Kt = q.Kt; g.KS = q.KS; g.part = part;
+    LagStepLif l{};
+    l.T = T; l.B = B; l.N = N; l.Nk = q.Nk; l.Np = q.Np; l.KS = q.KS; l.Lw = q.Lw; l.lda = q.lda;
+    l.part = part; l.x = a->x; l.bias = a->bias; l.drop = a->drop; l.lif = make_lif(a->lif);
+    l.state = state; l.y = a->y; l.u = a->u; l.bits = a->bits; l.hist = hist;
+    const bool timed = scan_begin(DELREC_WS_SYN_FWD, s);
+    for (int t = 0; t < T; ++t) {
+        g.aoff = (size_t)t * q.Nk;      // window: spikes t - Lw .. t - 1
+        launch_lagstep_gemm(g, 1, s);
+        l.t = t;
+        launch_lagstep_lif(l, true, s);
+    }
+    scan_end(timed, s);
+    return finish_launch();
+}
+
 int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
     if (!a->x || !a->W || !a->y || !a->u || !a->bits || !lif_ok(a->lif)) return DELREC_ERR_ARG;
@@ -602,6 +686,7 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     const SynLayout lay = syn_layout(a->N, a->L, true);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int N = a->N;
+    if (syn_lagstep(a->T, a->B, N, a->L)) return syn_fwd_lagstep(a, s);
     const size_t nb = (size_t)((N + 15) / 16) * 16 * N;
     Carver cv(a->workspace, a->workspace_bytes);
     void* wt = a->w_bf16 ? (void*)cv.take<uint16_t>(nb) : (void*)cv.take<float>(nb);
@@ -686,15 +771,23 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     uint4* alo = cv.take<uint4>(packed);
     uint4* yb = cv.take<uint4>(packed);
     int* meta = cv.take<int>((size_t)3 * N + 64);
-    void* wt = cv.take<float>((size_t)N * wlay.NT);
-    void* dt = cv.take<float>((size_t)N * wlay.NT);
-    float* gring = cv.take<float>((size_t)B * N * wlay.RP);
-    if (!gr || !part || !lagp || !ahi || !alo || !yb || !meta || !wt || !dt || !gring)
-        return DELREC_ERR_WORKSPACE;
+    const bool lagstep = syn_lagstep(T, B, N, a->L);
+    void* wt = nullptr;
+    void* dt = nullptr;
+    float* gring = nullptr;
+    if (!lagstep) {
+        wt = cv.take<float>((size_t)N * wlay.NT);
+        dt = cv.take<float>((size_t)N * wlay.NT);
+        gring = cv.take<float>((size_t)B * N * wlay.RP);
+        if (!wt || !dt || !gring) return DELREC_ERR_WORKSPACE;
+    }
+    if (!gr || !part || !lagp || !ahi || !alo || !yb || !meta) return DELREC_ERR_WORKSPACE;
 
-    if (a->w_bf16) block_transpose<uint16_t>(a->W, wt, N, s); else block_transpose<float>(a->W, wt, N, s);
-    if (hybrid) block_transpose<int8_t>(a->offsets, dt, N, s);
-    else block_transpose<float>(a->d, dt, N, s);
+    if (!lagstep) {
+        if (a->w_bf16) block_transpose<uint16_t>(a->W, wt, N, s); else block_transpose<float>(a->W, wt, N, s);
+        if (hybrid) block_transpose<int8_t>(a->offsets, dt, N, s);
+        else block_transpose<float>(a->d, dt, N, s);
+    }
     // each column's lag range for the lag GEMM, and the smallest offset (meta[1]) the
     // hybrid scan reads
     const size_t NN = (size_t)N * N;
@@ -707,6 +800,52 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     g.pd = lagp + (size_t)q.KS * NN;
     g.ps = a->ds ? lagp + (size_t)2 * q.KS * NN : nullptr;
     launch_lag_cols(g, s);
+
+    if (lagstep) {
+        // reverse-time scan as one lag-stacked GEMM + one LIF launch per step
+        const LagStepDims ls = lagstep_dims(T, B, N, a->L);
+        uint4* planes = cv.take<uint4>(2 * ls.plane);
+        uint16_t* ghi = cv.take<uint16_t>((size_t)B * ls.lda);
+        uint16_t* glo = cv.take<uint16_t>((size_t)B * ls.lda);
+        float* lpart = cv.take<float>((size_t)ls.KS * B * ls.Np);
+        float* state = cv.take<float>((size_t)B * N);
+        if (!planes || !ghi || !glo || !lpart || !state) return DELREC_ERR_WORKSPACE;
+        LagStepPack pk{};
+        pk.N = N; pk.Nk = ls.Nk; pk.Np = ls.Np; pk.Lw = ls.Lw;
+        pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.d = a->d; pk.base = a->base; pk.off = a->offsets;
+        pk.s = a->s; pk.s_uniform = a->s_uniform; pk.out = planes;
+        launch_pack_lagw(pk, false, s);
+        launch_hist_zero(ghi, B, ls.lda, ls.Nk, T, T + ls.Lw, s);   // gr past the last step
+        launch_hist_zero(glo, B, ls.lda, ls.Nk, T, T + ls.Lw, s);
+        LagStepGemm gg{};
+        gg.a0 = ghi; gg.a1 = glo; gg.lda = ls.lda; gg.B = B;
+        gg.p0 = planes; gg.p1 = planes + ls.plane; gg.Np = ls.Np; gg.Kt = ls.Kt; gg.KS = ls.KS;
+        gg.part = lpart;
+        LagStepLif l{};
+        l.T = T; l.B = B; l.N = N; l.Nk = ls.Nk; l.Np = ls.Np; l.KS = ls.KS; l.Lw = ls.Lw;
+        l.lda = ls.lda; l.part = lpart; l.drop = a->drop; l.lif = make_lif(a->lif);
+        l.state = state; l.u = const_cast<float*>(a->u); l.hist = ghi; l.hist2 = glo;
+        l.gy = a->gy; l.dx = a->dx; l.gr = gr; l.dbp = part;
+        const bool timed = scan_begin(DELREC_WS_SYN_BWD, s);
+        for (int t = T - 1; t >= 0; --t) {
+            gg.aoff = (size_t)(t + 1) * ls.Nk;   // window: gr t + 1 .. t + Lw
+            launch_lagstep_gemm(gg, 2, s);
+            l.t = t;
+            launch_lagstep_lif(l, false, s);
+        }
+        scan_end(timed, s);
+        int st = finish_launch();
+        if (st) return st;
+        launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
+        if (a->dW || a->dd || a->ds) {
+            launch_lag_bf16(g, gr, a->bits, s);
+            LagGemm f{};
+            f.N = N; f.KS = q.KS; f.W = a->W; f.w_bf16 = a->w_bf16; f.s = a->s; f.s_uniform = a->s_uniform;
+            f.pw = g.pw; f.pd = g.pd; f.ps = g.ps;
+            launch_lag_finish(f, a->dW, a->dd, a->ds, s);
+        }
+        return finish_launch();
+    }
 
     SynBwd p{};
     p.T = T; p.B = B; p.N = N; p.L = a->L;

@@ -135,6 +135,58 @@ struct LagBf16 {
     float* ps;                   // [KS][N][N] partial sum_l dh/ds * C_l, or NULL
 };
 
+// lag-stacked per-step GEMM scans (lagstep.hip)
+struct LagStepPack {             // M_l planes (hi, lo) of the forward or backward operand
+    int N, Nk, Np, Lw;
+    const void* W;
+    int w_bf16;
+    const float* d;              // row-major, or NULL (hybrid)
+    const float* base;
+    const int8_t* off;
+    const float* s;
+    float s_uniform;
+    uint4* out;                  // 2 planes of (Lw * Nk / 8) x Np uint4
+};
+
+struct LagStepGemm {
+    const uint16_t* a0;          // history (bf16), row b at b * lda; k = 0 at element aoff
+    const uint16_t* a1;          // its lo plane (backward), or NULL
+    size_t lda;
+    size_t aoff;
+    int B;
+    const uint4* p0;             // packed M planes
+    const uint4* p1;
+    int Np, Kt, KS;
+    float* part;                 // [KS][B][Np]
+};
+
+struct LagStepLif {
+    int T, B, N, Nk, Np, KS, t, Lw;
+    size_t lda;
+    const float* part;
+    const float* x;              // forward input
+    const float* bias;
+    const float* drop;
+    Lif lif;
+    float* state;                // [B][N]: v (forward) or lambda (backward)
+    float* y;
+    float* u;                    // forward output / backward input
+    uint32_t* bits;
+    uint16_t* hist;              // forward: spikes; backward: gr hi
+    uint16_t* hist2;             // backward: gr lo
+    const float* gy;
+    float* dx;
+    float* gr;
+    float* dbp;                  // [B][N] db partials
+};
+
+int lagstep_splits(int B, int Np, int Kt, int cus);
+size_t lagstep_gemm_lds(int pa);
+void launch_pack_lagw(const LagStepPack& a, bool fwd, hipStream_t stream);
+void launch_hist_zero(uint16_t* h, int B, size_t lda, int Nk, int t0, int t1, hipStream_t stream);
+void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream);
+void launch_lagstep_lif(const LagStepLif& l, bool fwd, hipStream_t stream);
+
 // hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel and size (cached; the
 // library is used from one host thread at a time)
 void ensure_lds(const void* fn, size_t bytes);

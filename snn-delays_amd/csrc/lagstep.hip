@@ -1,0 +1,341 @@
+// Synaptic / hybrid scans as one lag-stacked GEMM per time step, on bf16 MFMA (gfx950).
+//
+// With per-connection weights M_l[i,j] = W_ij * h(l; d_ij, s_j) (h = max(0, s - |l - c|) / s^2,
+// c = 1 + d, the triangle of reference delays.py:48-63), the recurrent input of step t and
+// the future gradient of the backward are
+//   rec(t)[b, i]  = sum_{l=1..Lw} sum_j y(t - l)[b, j]  M_l[i, j]
+//   gfut(t)[b, j] = sum_{l=1..Lw} sum_i gr(t + l)[b, i] M_l[i, j],      Lw = L - 1,
+// i.e. a (B x Lw*N) by (Lw*N x N) product per step whose left operand is a window of a
+// batch-major history: with the history stored [b][time][N], the window of step t is a
+// plain strided matrix (row b at b * lda, k = lag slot * N + neuron). Each step is one split-K
+// GEMM launch (partial sums per k split) and one LIF launch that reduces the partials in a
+// fixed order and advances the neurons, so every lag of every connection is a dense MFMA
+// product: the triangle's empty lags cost MFMA time instead of per-tap VALU work.
+// This replaces the per-connection gathers of the reference's scans
+// (synaptic_eventdriven.py:106-164, :323-364) where their rings do not fit one CU's LDS.
+//
+// Precision: spikes are exact in bf16. M is stored as two bf16 planes, M ~ hi + lo (relative
+// error about 2^-17); the backward also splits gr into hi + lo and takes hi*hi + hi*lo + lo*hi
+// (about 2^-16). Accumulation is fp32.
+//
+// Layouts. A packed operand P with K rows and Np columns is k-blocked: element (k, n) at
+// ((k / 8) * Np + n) * 8 + k % 8, so one 16-byte load holds the 8 consecutive k of one column
+// that an MFMA lane supplies. Forward: k = q * Nk + j with lag l = Lw - q (q ascending is
+// time ascending), columns i. Backward: k = q * Nk + i with lag l = q + 1, columns j. The
+// neuron count is padded to Nk = 32n so a 32-row k stage never straddles two lags.
+#include "kernels.h"
+
+namespace delrec {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float lagw_delay(const LagStepPack& p, int i, int j) {
+    if (p.d) return p.d[(size_t)i * p.N + j];
+    return p.base[j] + 0.0f + 1.0f * (float)p.off[(size_t)i * p.N + j];
+}
+
+// One thread per (8-block of the contracted neuron, output column); it reads its 8
+// connections' weight, delay and half-width once and writes their 16-byte runs for every
+// lag of both planes.
+template <bool FWD>
+__global__ void __launch_bounds__(256) pack_lagw_kernel(LagStepPack p) {
+    const int NB = p.Nk / 8;
+    const size_t total = (size_t)NB * p.Np;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int kb = (int)(idx / p.Np), col = (int)(idx - (size_t)kb * p.Np);
+    float w[8], c[8], sv[8], s2[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int i = FWD ? col : kb * 8 + e;
+        const int j = FWD ? kb * 8 + e : col;
+        const bool ok = i < p.N && j < p.N;
+        const int ic = ok ? i : 0, jc = ok ? j : 0;
+        w[e] = ok ? load_w(p.W, p.w_bf16, (size_t)ic * p.N + jc) : 0.0f;
+        c[e] = 1.0f + lagw_delay(p, ic, jc);
+        sv[e] = p.s ? p.s[jc] : p.s_uniform;
+        s2[e] = sv[e] * sv[e];
+    }
+    const size_t plane = (size_t)p.Lw * NB * p.Np;
+    for (int q = 0; q < p.Lw; ++q) {
+        const float l = (float)(FWD ? p.Lw - q : q + 1);
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            uint32_t h2[2], l2[2];
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+                const float m = w[e + f] * tri_weight(l, c[e + f], sv[e + f], s2[e + f]);
+                h2[f] = bf16_bits_rne(m);
+                l2[f] = bf16_bits_rne(m - __uint_as_float(h2[f] << 16));
+            }
+            hi[e / 2] = h2[0] | (h2[1] << 16);
+            lo[e / 2] = l2[0] | (l2[1] << 16);
+        }
+        const size_t o = ((size_t)q * NB + kb) * p.Np + col;
+        p.out[o] = uint4{hi[0], hi[1], hi[2], hi[3]};
+        p.out[plane + o] = uint4{lo[0], lo[1], lo[2], lo[3]};
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Split-K GEMM of one step: part[ks][b][n] = sum over the split's k of A[b][k] * P[k][n].
+// Workgroup: 128 rows x 128 columns (4 waves of 64 x 64, 4 x 4 MFMA blocks each) and one
+// k split; 32-k stages go global -> registers (S stages ahead, fixed register slots:
+// the loop is unrolled over S) -> LDS (double-buffered, one barrier per stage).
+// PA = 1: A x (P_hi + P_lo). PA = 2: A_hi x P_hi + A_hi x P_lo + A_lo x P_hi.
+// Block order: the workgroups that share a k split and column tile sit NT * KS apart, a
+// multiple of 8, so they land on the same XCD and share its L2 for the streamed P tile.
+template <int PA, int S>
+__global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
+    extern __shared__ uint4 lds_u4[];
+    constexpr int PL = PA + 2;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int wi = w >> 1, wj = w & 1, g = lane >> 4, lc = lane & 15;
+    const int NT = p.Np / 128;
+    const int id = (int)blockIdx.x;
+    const int bt = id / (NT * p.KS), rest = id - bt * (NT * p.KS);
+    const int ks = rest / NT, nt = rest - ks * NT;
+    const int b0 = bt * 128, n0 = nt * 128;
+    const int nst = p.Kt / 32;
+    const int per = (nst + p.KS - 1) / p.KS;
+    const int s0 = ks * per;
+    const int ns = max(min(nst, s0 + per) - s0, 0);
+
+    i32x4 ra[PA], rb[2];
+    const uint32_t abytes = (uint32_t)((size_t)p.B * p.lda * 2);
+    ra[0] = buffer_rsrc(p.a0, abytes);
+    if (PA > 1) ra[PA - 1] = buffer_rsrc(p.a1, abytes);
+    const uint32_t pbytes = (uint32_t)((size_t)(p.Kt / 8) * p.Np * 16);
+    rb[0] = buffer_rsrc(p.p0, pbytes);
+    rb[1] = buffer_rsrc(p.p1, pbytes);
+    // staging: thread tid stages uint4 c = tid + 256 h (k-block c >> 7, row / column c & 127)
+    uint32_t oa[2], ob[2];
+    const uint32_t bstep = (uint32_t)(4 * p.Np * 16);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = tid + 256 * h, kb = c >> 7, r = c & 127;
+        oa[h] = (uint32_t)(((size_t)(b0 + r) * p.lda + p.aoff + (size_t)s0 * 32 + kb * 8) * 2);
+        ob[h] = (uint32_t)((((size_t)s0 * 4 + kb) * p.Np + n0 + r) * 16);
+    }
+    uint4 st[S][PL][2];
+    auto issue = [&](int slot) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int q = 0; q < PA; ++q)
+                st[slot][q][h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(ra[q], (int)oa[h], 0, 0));
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                st[slot][PA + q][h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rb[q], (int)ob[h], 0, 0));
+            oa[h] += 64;
+            ob[h] += bstep;
+        }
+    };
+    auto stash = [&](int slot, int buf) {
+#pragma unroll
+        for (int q = 0; q < PL; ++q)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) lds_u4[(buf * PL + q) * 512 + tid + 256 * h] = st[slot][q][h];
+    };
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int q = 0; q < S; ++q) issue(q);
+    stash(0, 0);
+    __syncthreads();
+    static_assert(S % 2 == 0, "an even number of register stages keeps the LDS buffer static");
+    for (int s = 0; s < ns; s += S) {
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            issue(u);   // stage s + u + S into the slot stage s + u left (stashed a stage ago)
+            if (s + u < ns) {
+                const int buf = u & 1;
+                bf16x8 av[PA][4], bv[2][4];
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+#pragma unroll
+                    for (int q = 0; q < PA; ++q)
+                        av[q][x] = __builtin_bit_cast(bf16x8, lds_u4[(buf * PL + q) * 512 + g * 128 + wi * 64 + x * 16 + lc]);
+#pragma unroll
+                    for (int q = 0; q < 2; ++q)
+                        bv[q][x] = __builtin_bit_cast(bf16x8, lds_u4[(buf * PL + PA + q) * 512 + g * 128 + wj * 64 + x * 16 + lc]);
+                }
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0][mb], bv[0][nb], acc[mb][nb], 0, 0, 0);
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0][mb], bv[1][nb], acc[mb][nb], 0, 0, 0);
+                if (PA > 1) {
+#pragma unroll
+                    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                        for (int nb = 0; nb < 4; ++nb)
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[PA - 1][mb], bv[0][nb], acc[mb][nb], 0, 0, 0);
+                }
+            }
+            stash((u + 1) % S, (u + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    float* out = p.part + (size_t)ks * p.B * p.Np;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = b0 + wi * 64 + mb * 16 + 4 * g + e;
+            if (r >= p.B) continue;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) out[(size_t)r * p.Np + n0 + wj * 64 + nb * 16 + lc] = acc[mb][nb][e];
+        }
+}
+
+// ---------------------------------------------------------------------------------------
+// LIF steps. One thread per (b, neuron) over the padded width Nk: the history columns past
+// N are written as zeros.
+
+// forward step t: rec = sum_ks part + bias; u = charge(v, x + rec * m); spike, reset; outputs
+// y, u, the spike bit, and y(t) into the history at time index t + Lw
+__global__ void __launch_bounds__(256) lagstep_lif_fwd_kernel(LagStepLif p) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)p.B * p.Nk) return;
+    const int b = (int)(idx / p.Nk), i = (int)(idx - (size_t)b * p.Nk);
+    const int t = p.t;
+    uint16_t* hrow = p.hist + (size_t)b * p.lda + (size_t)(t + p.Lw) * p.Nk;
+    if (i >= p.N) {
+        hrow[i] = 0;
+        return;
+    }
+    const Lif k = p.lif;
+    const size_t bi = (size_t)b * p.N + i;
+    float r = 0.0f;
+    for (int q = 0; q < p.KS; ++q) r += p.part[((size_t)q * p.B + b) * p.Np + i];
+    r += p.bias ? p.bias[i] : 0.0f;
+    const float m = p.drop ? p.drop[bi] : 1.0f;
+    const size_t o = (size_t)t * p.B * p.N + bi;
+    const float a = p.x[o] + r * m;
+    const float v = t == 0 ? k.v0 : p.state[bi];
+    const float u = lif_charge(k, v, a);
+    const float y = lif_fire(k, u);
+    p.state[bi] = lif_reset(k, u, y);
+    p.y[o] = y;
+    p.u[o] = u;
+    const int TW = (p.T + 31) >> 5;
+    uint32_t* wp = p.bits + ((size_t)b * TW + (t >> 5)) * p.N + i;
+    const uint32_t bit = (y != 0.0f ? 1u : 0u) << (t & 31);
+    *wp = (t & 31) == 0 ? bit : (*wp | bit);
+    hrow[i] = y != 0.0f ? 0x3F80 : 0;
+}
+
+// backward step t: gfut = sum_ks part; du = LIF backward (gy + gfut, u, y, lam); dx, gr, the
+// db partial, and gr(t) split into the hi / lo histories
+__global__ void __launch_bounds__(256) lagstep_lif_bwd_kernel(LagStepLif p) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)p.B * p.Nk) return;
+    const int b = (int)(idx / p.Nk), j = (int)(idx - (size_t)b * p.Nk);
+    const int t = p.t;
+    const size_t ho = (size_t)b * p.lda + (size_t)t * p.Nk + j;
+    if (j >= p.N) {
+        p.hist[ho] = 0;
+        p.hist2[ho] = 0;
+        return;
+    }
+    const Lif k = p.lif;
+    const size_t bj = (size_t)b * p.N + j;
+    float gf = 0.0f;
+    for (int q = 0; q < p.KS; ++q) gf += p.part[((size_t)q * p.B + b) * p.Np + j];
+    const size_t o = (size_t)t * p.B * p.N + bj;
+    const float u = p.u[o];
+    const float y = lif_fire(k, u);
+    const bool last = t == p.T - 1;
+    const float lam = last ? 0.0f : p.state[bj];
+    const float du = lif_backward(k, p.gy[o] + gf, u, y, lam);
+    p.state[bj] = k.decay * du;
+    const float da = lif_dx(k, du);
+    const float gr = da * (p.drop ? p.drop[bj] : 1.0f);
+    p.dx[o] = da;
+    p.gr[o] = gr;
+    p.dbp[bj] = last ? gr : p.dbp[bj] + gr;
+    const uint32_t hi = bf16_bits_rne(gr);
+    p.hist[ho] = (uint16_t)hi;
+    p.hist2[ho] = (uint16_t)bf16_bits_rne(gr - __uint_as_float(hi << 16));
+}
+
+// h[b * lda + off0 + e] = 0 for b < B, e < n
+__global__ void fill_rows_u16_kernel(uint16_t* __restrict__ h, int B, size_t lda, size_t off0, size_t n) {
+    const size_t total = (size_t)B * n;
+    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += (size_t)gridDim.x * blockDim.x) {
+        const size_t b = q / n;
+        h[b * lda + off0 + (q - b * n)] = 0;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+
+int lagstep_splits(int B, int Np, int Kt, int cus) {
+    const int tiles = ((B + 127) / 128) * (Np / 128);
+    const int nst = Kt / 32;
+    const int want = (cus + tiles - 1) / tiles;
+    return std::max(1, std::min(want, std::max(1, nst / 8)));
+}
+
+void launch_pack_lagw(const LagStepPack& a, bool fwd, hipStream_t stream) {
+    const size_t total = (size_t)(a.Nk / 8) * a.Np;
+    const unsigned blocks = (unsigned)((total + 255) / 256);
+    if (fwd)
+        hipLaunchKernelGGL(pack_lagw_kernel<true>, dim3(blocks), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(pack_lagw_kernel<false>, dim3(blocks), dim3(256), 0, stream, a);
+}
+
+// zero rows [t0, t1) of every batch row of a [B][lda / Nk][Nk] history
+void launch_hist_zero(uint16_t* h, int B, size_t lda, int Nk, int t0, int t1, hipStream_t stream) {
+    const size_t n = (size_t)(t1 - t0) * Nk;
+    if (n == 0) return;
+    const unsigned blocks = (unsigned)std::min<size_t>(((size_t)B * n + 255) / 256, 4096);
+    hipLaunchKernelGGL(fill_rows_u16_kernel, dim3(blocks), dim3(256), 0, stream, h, B, lda, (size_t)t0 * Nk, n);
+}
+
+constexpr int kLagStepStages = 4;
+
+size_t lagstep_gemm_lds(int pa) { return (size_t)2 * (pa + 2) * 512 * sizeof(uint4); }
+
+void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream) {
+    const int grid = ((g.B + 127) / 128) * (g.Np / 128) * g.KS;
+    const size_t lds = lagstep_gemm_lds(pa);
+    if (pa == 1) {
+        ensure_lds((const void*)lagstep_gemm_kernel<1, kLagStepStages>, lds);
+        hipLaunchKernelGGL((lagstep_gemm_kernel<1, kLagStepStages>), dim3(grid), dim3(256), lds, stream, g);
+    } else {
+        ensure_lds((const void*)lagstep_gemm_kernel<2, kLagStepStages>, lds);
+        hipLaunchKernelGGL((lagstep_gemm_kernel<2, kLagStepStages>), dim3(grid), dim3(256), lds, stream, g);
+    }
+}
+
+void launch_lagstep_lif(const LagStepLif& l, bool fwd, hipStream_t stream) {
+    const size_t n = (size_t)l.B * l.Nk;
+    const unsigned blocks = (unsigned)((n + 255) / 256);
+    if (fwd)
+        hipLaunchKernelGGL(lagstep_lif_fwd_kernel, dim3(blocks), dim3(256), 0, stream, l);
+    else
+        hipLaunchKernelGGL(lagstep_lif_bwd_kernel, dim3(blocks), dim3(256), 0, stream, l);
+}
+
+}  // namespace delrec

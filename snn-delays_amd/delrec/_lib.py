@@ -168,8 +168,9 @@ _WS_SIZES = {}
 
 
 def workspace_bytes(kind, T, B, N, L, flags):
-    """``delrec_query_workspace`` (memoised: the size is a pure function of the arguments)."""
-    key = (kind, T, B, N, L, flags)
+    """``delrec_query_workspace`` (memoised: the size is a function of the arguments and of
+    DELREC_SYN_LAGSTEP, which picks the synaptic scans' form)."""
+    key = (kind, T, B, N, L, flags, os.environ.get('DELREC_SYN_LAGSTEP'))
     n = _WS_SIZES.get(key)
     if n is None:
         size = c_size(0)

@@ -93,6 +93,28 @@ def test_synaptic_fwd_bwd_matches_oracle(dev, case):
         assert_close(pg.grad, gref['p'], RTOL, scale(gref['p']), 'dp')
 
 
+# the lag-stacked per-step GEMM scans (taken by default only where the rings do not fit
+# LDS, the last two cases above) forced at every size; the same oracle and tolerances
+LAGSTEP_CASES = [SYN_CASES[i] for i in (0, 1, 2, 3, 4, 5, 6, 7)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', LAGSTEP_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}d{c[3]}s{c[4]}{"".join(c[5])}'
+                                                    for c in LAGSTEP_CASES])
+def test_synaptic_lagstep_matches_oracle(dev, case, monkeypatch):
+    monkeypatch.setenv('DELREC_SYN_LAGSTEP', '1')
+    test_synaptic_fwd_bwd_matches_oracle(dev, case)
+
+
+# the per-connection gather forward and workspace-ring backward at the sizes that take the
+# lag-stacked scans by default
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', SYN_CASES[-2:], ids=[f'T{c[0]}B{c[1]}N{c[2]}d{c[3]}' for c in SYN_CASES[-2:]])
+def test_synaptic_gather_path_matches_oracle(dev, case, monkeypatch):
+    monkeypatch.setenv('DELREC_SYN_LAGSTEP', '0')
+    test_synaptic_fwd_bwd_matches_oracle(dev, case)
+
+
 HYB_CASES = [
     # T, B, N, base range (lo, hi), max offset, bf16 weights, sigma
     (20, 3, 32, (0.0, 8.0), 4, False, 0.0),
@@ -163,6 +185,20 @@ def test_hybrid_fwd_bwd_matches_oracle(dev, case):
     assert_close(layer.recurrent_weights.grad.float(), gref['W'], rtol, scale(gref['W']), 'dW')
     assert_close(layer.parametrizations.recurrent_delays.original.grad, gref['base'], rtol,
                  scale(gref['base']), 'dbase')
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', HYB_CASES[:5], ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}{"bf16" if c[5] else ""}s{c[6]}'
+                                                    for c in HYB_CASES[:5]])
+def test_hybrid_lagstep_matches_oracle(dev, case, monkeypatch):
+    monkeypatch.setenv('DELREC_SYN_LAGSTEP', '1')
+    test_hybrid_fwd_bwd_matches_oracle(dev, case)
+
+
+@pytest.mark.gpu
+def test_hybrid_gather_path_matches_oracle(dev, monkeypatch):
+    monkeypatch.setenv('DELREC_SYN_LAGSTEP', '0')
+    test_hybrid_fwd_bwd_matches_oracle(dev, HYB_CASES[-1])
 
 
 @pytest.mark.gpu
