@@ -292,7 +292,9 @@ int syn_gather_taps(float s_max) { return (int)std::floor(2.0f * s_max) + 2; }
 // scatter scans do not fit one CU's LDS; DELREC_SYN_LAGSTEP=1 forces them (any size),
 // =0 turns them off. Operands are addressed with 32-bit byte offsets.
 struct LagStepDims {
-    int Nk, Np, Lw, Kt, KS;
+    int Nk, Np, Lw, Kt;
+    int P, Lf;          // steps per block (= near lags), far lags Lw - P
+    int KS, KSF;        // k splits of the per-step near GEMM and of the per-block far GEMM
     size_t lda;         // history row pitch (elements): (T + Lw) * Nk
     size_t plane;       // uint4 per packed M plane
     bool ok;
@@ -304,11 +306,14 @@ LagStepDims lagstep_dims(int T, int B, int N, int L) {
     q.Np = (N + 127) / 128 * 128;
     q.Lw = std::max(L - 1, 1);
     q.Kt = q.Lw * q.Nk;
+    q.P = std::min(lagstep_block(), q.Lw);
+    q.Lf = q.Lw - q.P;
     q.lda = (size_t)(T + q.Lw) * q.Nk;
     q.plane = (size_t)(q.Kt / 8) * q.Np;
-    q.KS = lagstep_splits(B, q.Np, q.Kt, num_cus());
-    const size_t Bpad = (size_t)(B + 127) / 128 * 128;
-    q.ok = Bpad * q.lda * 2 < ((size_t)1 << 32) && q.plane * 16 < ((size_t)1 << 32);
+    q.KS = lagstep_splits(B, q.Np, q.P * q.Nk, num_cus());
+    q.KSF = q.Lf > 0 ? lagstep_splits(B * q.P, q.Np, q.Lf * q.Nk, num_cus()) : 0;
+    // byte offsets of every history row a GEMM may address (incl. rows of a partial tile)
+    q.ok = (size_t)(B + 128) * q.lda * 2 < ((size_t)1 << 32) && q.plane * 16 < ((size_t)1 << 32);
     return q;
 }
 
@@ -326,7 +331,8 @@ void lagstep_ws(C& c, int T, int B, int N, int L, bool fwd) {
     c.template take<uint4>(2 * q.plane);                         // M planes
     c.template take<uint16_t>((size_t)B * q.lda);                // history (spikes / gr hi)
     if (!fwd) c.template take<uint16_t>((size_t)B * q.lda);      // gr lo
-    c.template take<float>((size_t)q.KS * B * q.Np);             // split-K partials
+    c.template take<float>((size_t)q.KS * B * q.Np);             // near-lag partials
+    c.template take<float>((size_t)std::max(q.KSF, 1) * B * q.P * q.Np);   // far-lag partials
     c.template take<float>((size_t)B * N);                       // v / lambda
 }
 
@@ -651,27 +657,42 @@ int syn_fwd_lagstep(const delrec_syn_fwd_args* a, hipStream_t s) {
     uint4* planes = cv.take<uint4>(2 * q.plane);
     uint16_t* hist = cv.take<uint16_t>((size_t)B * q.lda);
     float* part = cv.take<float>((size_t)q.KS * B * q.Np);
+    float* fpart = cv.take<float>((size_t)std::max(q.KSF, 1) * B * q.P * q.Np);
     float* state = cv.take<float>((size_t)B * N);
-    if (!planes || !hist || !part || !state) return DELREC_ERR_WORKSPACE;
+    if (!planes || !hist || !part || !fpart || !state) return DELREC_ERR_WORKSPACE;
     LagStepPack pk{};
     pk.N = N; pk.Nk = q.Nk; pk.Np = q.Np; pk.Lw = q.Lw;
     pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.d = a->d; pk.base = a->base; pk.off = a->offsets;
     pk.s = a->s; pk.s_uniform = a->s_uniform; pk.out = planes;
     launch_pack_lagw(pk, true, s);
     launch_hist_zero(hist, B, q.lda, q.Nk, 0, q.Lw, s);   // spikes before t = 0
-    LagStepGemm g{};
-    g.a0 = hist; g.a1 = nullptr; g.lda = q.lda; g.B = B;
-    g.p0 = planes; g.p1 = planes + q.plane; g.Np = q.Np; g.Kt = q.Kt; g.KS = q.KS; g.part = part;
+    // packed k order: lag Lw first, lag 1 last; the far lags Lw .. P + 1 come first
+    const size_t kfar = (size_t)q.Lf * q.Nk / 8 * q.Np;   // uint4 offset of the near lags
+    LagStepGemm g{};   // near lags of one step: spikes t - P .. t - 1
+    g.a0 = hist; g.a1 = nullptr; g.lda = q.lda; g.rs = 0; g.B = B; g.rows = B; g.rp = 1;
+    g.p0 = planes + kfar; g.p1 = planes + q.plane + kfar; g.Np = q.Np; g.Kt = q.P * q.Nk;
+    g.KS = q.KS; g.part = part;
+    LagStepGemm gf = g;   // far lags of a block of P steps: row (b, tt) reads spikes t0 + tt - Lw ..
+    gf.rows = B * q.P; gf.rp = q.P; gf.rs = q.Nk;
+    gf.p0 = planes; gf.p1 = planes + q.plane; gf.Kt = q.Lf * q.Nk; gf.KS = q.KSF; gf.part = fpart;
     LagStepLif l{};
     l.T = T; l.B = B; l.N = N; l.Nk = q.Nk; l.Np = q.Np; l.KS = q.KS; l.Lw = q.Lw; l.lda = q.lda;
-    l.part = part; l.x = a->x; l.bias = a->bias; l.drop = a->drop; l.lif = make_lif(a->lif);
+    l.part = part; l.fpart = q.Lf > 0 ? fpart : nullptr; l.KSF = q.Lf > 0 ? q.KSF : 0; l.P = q.P;
+    l.x = a->x; l.bias = a->bias; l.drop = a->drop; l.lif = make_lif(a->lif);
     l.state = state; l.y = a->y; l.u = a->u; l.bits = a->bits; l.hist = hist;
     const bool timed = scan_begin(DELREC_WS_SYN_FWD, s);
-    for (int t = 0; t < T; ++t) {
-        g.aoff = (size_t)t * q.Nk;      // window: spikes t - Lw .. t - 1
-        launch_lagstep_gemm(g, 1, s);
-        l.t = t;
-        launch_lagstep_lif(l, true, s);
+    for (int t0 = 0; t0 < T; t0 += q.P) {
+        if (q.Lf > 0) {
+            gf.aoff = (size_t)t0 * q.Nk;
+            launch_lagstep_gemm(gf, 1, s);
+        }
+        for (int t = t0; t < std::min(T, t0 + q.P); ++t) {
+            g.aoff = (size_t)(t + q.Lf) * q.Nk;
+            launch_lagstep_gemm(g, 1, s);
+            l.t = t;
+            l.tt = t - t0;
+            launch_lagstep_lif(l, true, s);
+        }
     }
     scan_end(timed, s);
     return finish_launch();
@@ -808,8 +829,9 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         uint16_t* ghi = cv.take<uint16_t>((size_t)B * ls.lda);
         uint16_t* glo = cv.take<uint16_t>((size_t)B * ls.lda);
         float* lpart = cv.take<float>((size_t)ls.KS * B * ls.Np);
+        float* fpart = cv.take<float>((size_t)std::max(ls.KSF, 1) * B * ls.P * ls.Np);
         float* state = cv.take<float>((size_t)B * N);
-        if (!planes || !ghi || !glo || !lpart || !state) return DELREC_ERR_WORKSPACE;
+        if (!planes || !ghi || !glo || !lpart || !fpart || !state) return DELREC_ERR_WORKSPACE;
         LagStepPack pk{};
         pk.N = N; pk.Nk = ls.Nk; pk.Np = ls.Np; pk.Lw = ls.Lw;
         pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.d = a->d; pk.base = a->base; pk.off = a->offsets;
@@ -817,21 +839,37 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         launch_pack_lagw(pk, false, s);
         launch_hist_zero(ghi, B, ls.lda, ls.Nk, T, T + ls.Lw, s);   // gr past the last step
         launch_hist_zero(glo, B, ls.lda, ls.Nk, T, T + ls.Lw, s);
-        LagStepGemm gg{};
-        gg.a0 = ghi; gg.a1 = glo; gg.lda = ls.lda; gg.B = B;
-        gg.p0 = planes; gg.p1 = planes + ls.plane; gg.Np = ls.Np; gg.Kt = ls.Kt; gg.KS = ls.KS;
+        // packed k order: lag 1 first; the near lags 1 .. P come first
+        const size_t kfar = (size_t)ls.P * ls.Nk / 8 * ls.Np;
+        LagStepGemm gg{};   // near lags of one step: gr t + 1 .. t + P
+        gg.a0 = ghi; gg.a1 = glo; gg.lda = ls.lda; gg.rs = 0; gg.B = B; gg.rows = B; gg.rp = 1;
+        gg.p0 = planes; gg.p1 = planes + ls.plane; gg.Np = ls.Np; gg.Kt = ls.P * ls.Nk; gg.KS = ls.KS;
         gg.part = lpart;
+        LagStepGemm gf = gg;   // far lags of a block: row (b, tt) of step tb + tt reads gr from tb + tt + P + 1
+        gf.rows = B * ls.P; gf.rp = ls.P; gf.rs = ls.Nk;
+        gf.p0 = planes + kfar; gf.p1 = planes + ls.plane + kfar; gf.Kt = ls.Lf * ls.Nk; gf.KS = ls.KSF;
+        gf.part = fpart;
         LagStepLif l{};
         l.T = T; l.B = B; l.N = N; l.Nk = ls.Nk; l.Np = ls.Np; l.KS = ls.KS; l.Lw = ls.Lw;
-        l.lda = ls.lda; l.part = lpart; l.drop = a->drop; l.lif = make_lif(a->lif);
+        l.lda = ls.lda; l.part = lpart; l.fpart = ls.Lf > 0 ? fpart : nullptr;
+        l.KSF = ls.Lf > 0 ? ls.KSF : 0; l.P = ls.P;
+        l.drop = a->drop; l.lif = make_lif(a->lif);
         l.state = state; l.u = const_cast<float*>(a->u); l.hist = ghi; l.hist2 = glo;
         l.gy = a->gy; l.dx = a->dx; l.gr = gr; l.dbp = part;
         const bool timed = scan_begin(DELREC_WS_SYN_BWD, s);
-        for (int t = T - 1; t >= 0; --t) {
-            gg.aoff = (size_t)(t + 1) * ls.Nk;   // window: gr t + 1 .. t + Lw
-            launch_lagstep_gemm(gg, 2, s);
-            l.t = t;
-            launch_lagstep_lif(l, false, s);
+        for (int t1 = T - 1; t1 >= 0; t1 -= ls.P) {
+            const int tb = t1 - ls.P + 1;   // the block's first step (rows of steps < 0 are unused)
+            if (ls.Lf > 0) {
+                gf.aoff = (size_t)(t1 + 2) * ls.Nk;
+                launch_lagstep_gemm(gf, 2, s);
+            }
+            for (int t = t1; t >= std::max(tb, 0); --t) {
+                gg.aoff = (size_t)(t + 1) * ls.Nk;
+                launch_lagstep_gemm(gg, 2, s);
+                l.t = t;
+                l.tt = t - tb;
+                launch_lagstep_lif(l, false, s);
+            }
         }
         scan_end(timed, s);
         int st = finish_launch();

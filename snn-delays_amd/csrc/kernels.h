@@ -149,21 +149,24 @@ struct LagStepPack {             // M_l planes (hi, lo) of the forward or backwa
 };
 
 struct LagStepGemm {
-    const uint16_t* a0;          // history (bf16), row b at b * lda; k = 0 at element aoff
-    const uint16_t* a1;          // its lo plane (backward), or NULL
-    size_t lda;
+    const uint16_t* a0;          // history (bf16); output row r reads k = 0 at element
+    const uint16_t* a1;          //   (r / rp) * lda + (r % rp) * rs + aoff; a1: lo plane or NULL
+    size_t lda, rs;
     size_t aoff;
-    int B;
-    const uint4* p0;             // packed M planes
+    int B;                       // batch rows of the history
+    int rows, rp;                // output rows (B * rp), rows per batch row
+    const uint4* p0;             // packed M planes (first k-block of the product's lags)
     const uint4* p1;
     int Np, Kt, KS;
-    float* part;                 // [KS][B][Np]
+    float* part;                 // [KS][rows][Np]
 };
 
 struct LagStepLif {
     int T, B, N, Nk, Np, KS, t, Lw;
     size_t lda;
-    const float* part;
+    const float* part;           // [KS][B][Np] near-lag partials of step t
+    const float* fpart;          // [KSF][B * P][Np] far-lag partials of step t's block, or NULL
+    int KSF, P, tt;              // far splits, steps per block, t's row in its block
     const float* x;              // forward input
     const float* bias;
     const float* drop;
@@ -181,6 +184,7 @@ struct LagStepLif {
 };
 
 int lagstep_splits(int B, int Np, int Kt, int cus);
+int lagstep_block();
 size_t lagstep_gemm_lds(int pa);
 void launch_pack_lagw(const LagStepPack& a, bool fwd, hipStream_t stream);
 void launch_hist_zero(uint16_t* h, int B, size_t lda, int Nk, int t0, int t1, hipStream_t stream);

@@ -7,10 +7,16 @@
 //   gfut(t)[b, j] = sum_{l=1..Lw} sum_i gr(t + l)[b, i] M_l[i, j],      Lw = L - 1,
 // i.e. a (B x Lw*N) by (Lw*N x N) product per step whose left operand is a window of a
 // batch-major history: with the history stored [b][time][N], the window of step t is a
-// plain strided matrix (row b at b * lda, k = lag slot * N + neuron). Each step is one split-K
-// GEMM launch (partial sums per k split) and one LIF launch that reduces the partials in a
-// fixed order and advances the neurons, so every lag of every connection is a dense MFMA
-// product: the triangle's empty lags cost MFMA time instead of per-tap VALU work.
+// plain strided matrix (row b at b * lda, k = lag slot * N + neuron). Every lag of every
+// connection is a dense MFMA product: the triangle's empty lags cost MFMA time instead of
+// per-tap VALU work.
+//
+// Time blocking. Streaming all of M every step would make the scan HBM-bound, so the steps
+// go in blocks of P: the lags l > P of a whole block depend only on spikes (gradients)
+// from before (after) the block, so one GEMM with B * P rows (row (b, step of the block))
+// covers them and reads their part of M once per block; each step then runs a split-K GEMM
+// over its P near lags (their part of M stays in cache) and one LIF launch that adds both
+// sets of partial sums in a fixed order and advances the neurons.
 // This replaces the per-connection gathers of the reference's scans
 // (synaptic_eventdriven.py:106-164, :323-364) where their rings do not fit one CU's LDS.
 //
@@ -89,10 +95,15 @@ __global__ void __launch_bounds__(256) pack_lagw_kernel(LagStepPack p) {
 // Split-K GEMM of one step: part[ks][b][n] = sum over the split's k of A[b][k] * P[k][n].
 // Workgroup: 128 rows x 128 columns (4 waves of 64 x 64, 4 x 4 MFMA blocks each) and one
 // k split; 32-k stages go global -> registers (S stages ahead, fixed register slots:
-// the loop is unrolled over S) -> LDS (double-buffered, one barrier per stage).
+// the loop is unrolled over S) -> LDS (double-buffered, one barrier per stage) -> fragment
+// registers (double-buffered: the next stage's fragments load while this stage multiplies).
 // PA = 1: A x (P_hi + P_lo). PA = 2: A_hi x P_hi + A_hi x P_lo + A_lo x P_hi.
-// Block order: the workgroups that share a k split and column tile sit NT * KS apart, a
-// multiple of 8, so they land on the same XCD and share its L2 for the streamed P tile.
+// Block order: workgroups are dealt to the 8 XCDs in turn (XCD = id mod 8), so when KS is a
+// multiple of 8 each XCD takes KS / 8 whole k splits with all their row and column tiles:
+// the A tile of a (row tile, split) and the P tile of a (column tile, split) are then
+// fetched into one L2 and shared there by every workgroup that reads them. Otherwise (the
+// per-block GEMM: many row tiles, few splits) each XCD takes a quarter of the row tiles
+// times half of the column tiles, so each A tile is fetched by 2 XCDs and each P tile by 4.
 template <int PA, int S>
 __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
     extern __shared__ uint4 lds_u4[];
@@ -100,9 +111,29 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int wi = w >> 1, wj = w & 1, g = lane >> 4, lc = lane & 15;
     const int NT = p.Np / 128;
+    const int BT = (p.rows + 127) / 128;
     const int id = (int)blockIdx.x;
-    const int bt = id / (NT * p.KS), rest = id - bt * (NT * p.KS);
-    const int ks = rest / NT, nt = rest - ks * NT;
+    int bt, nt, ks;
+    if ((p.KS & 7) == 0) {
+        const int xcd = id & 7, slot = id >> 3;
+        const int kl = slot / (BT * NT), rem = slot - kl * (BT * NT);
+        ks = xcd * (p.KS >> 3) + kl;
+        bt = rem / NT;
+        nt = rem - bt * NT;
+    } else if ((BT & 3) == 0 && (NT & 1) == 0) {
+        // each XCD takes a (BT / 4) x (NT / 2) block of tiles with every k split
+        const int xcd = id & 7, slot = id >> 3;
+        const int bb = BT >> 2, nn = NT >> 1;
+        ks = slot / (bb * nn);
+        const int rem = slot - ks * (bb * nn);
+        bt = (xcd >> 1) * bb + rem / nn;
+        nt = (xcd & 1) * nn + rem % nn;
+    } else {
+        bt = id / (NT * p.KS);
+        const int rest = id - bt * (NT * p.KS);
+        ks = rest / NT;
+        nt = rest - ks * NT;
+    }
     const int b0 = bt * 128, n0 = nt * 128;
     const int nst = p.Kt / 32;
     const int per = (nst + p.KS - 1) / p.KS;
@@ -122,7 +153,9 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int c = tid + 256 * h, kb = c >> 7, r = c & 127;
-        oa[h] = (uint32_t)(((size_t)(b0 + r) * p.lda + p.aoff + (size_t)s0 * 32 + kb * 8) * 2);
+        const int rr = b0 + r;   // rows past p.rows land past the descriptor's end: zeros
+        oa[h] = (uint32_t)(((size_t)(rr / p.rp) * p.lda + (size_t)(rr % p.rp) * p.rs + p.aoff +
+                            (size_t)s0 * 32 + kb * 8) * 2);
         ob[h] = (uint32_t)((((size_t)s0 * 4 + kb) * p.Np + n0 + r) * 16);
     }
     uint4 st[S][PL][2];
@@ -151,57 +184,66 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+    bf16x8 fa[2][PA][4], fb[2][2][4];   // fragments: the stage being multiplied and the next
+    auto frags = [&](int f, int buf) {
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+#pragma unroll
+            for (int q = 0; q < PA; ++q)
+                fa[f][q][x] = __builtin_bit_cast(bf16x8, lds_u4[(buf * PL + q) * 512 + g * 128 + wi * 64 + x * 16 + lc]);
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                fb[f][q][x] = __builtin_bit_cast(bf16x8, lds_u4[(buf * PL + PA + q) * 512 + g * 128 + wj * 64 + x * 16 + lc]);
+        }
+    };
+
 #pragma unroll
     for (int q = 0; q < S; ++q) issue(q);
     stash(0, 0);
-    __syncthreads();
-    static_assert(S % 2 == 0, "an even number of register stages keeps the LDS buffer static");
+    stash(1, 1);
+    barrier_lds();
+    frags(0, 0);
+    static_assert(S % 2 == 0 && S >= 4, "an even number of register stages keeps the LDS buffer static");
+    // iteration i: fragments of stage i + 1 are read (LDS buffer (i + 1) % 2, ready since the
+    // last barrier) while stage i's are multiplied; stage i + 2 goes into buffer i % 2, whose
+    // stage i is already in registers; the global loads run S stages ahead
     for (int s = 0; s < ns; s += S) {
 #pragma unroll
         for (int u = 0; u < S; ++u) {
-            issue(u);   // stage s + u + S into the slot stage s + u left (stashed a stage ago)
+            issue(u);   // stage s + u + S into the slot stage s + u left (stashed two stages ago)
+            frags((u + 1) & 1, (u + 1) & 1);
             if (s + u < ns) {
-                const int buf = u & 1;
-                bf16x8 av[PA][4], bv[2][4];
-#pragma unroll
-                for (int x = 0; x < 4; ++x) {
-#pragma unroll
-                    for (int q = 0; q < PA; ++q)
-                        av[q][x] = __builtin_bit_cast(bf16x8, lds_u4[(buf * PL + q) * 512 + g * 128 + wi * 64 + x * 16 + lc]);
-#pragma unroll
-                    for (int q = 0; q < 2; ++q)
-                        bv[q][x] = __builtin_bit_cast(bf16x8, lds_u4[(buf * PL + PA + q) * 512 + g * 128 + wj * 64 + x * 16 + lc]);
-                }
+                const int f = u & 1;
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
                     for (int nb = 0; nb < 4; ++nb)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0][mb], bv[0][nb], acc[mb][nb], 0, 0, 0);
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][0][mb], fb[f][0][nb], acc[mb][nb], 0, 0, 0);
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
                     for (int nb = 0; nb < 4; ++nb)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0][mb], bv[1][nb], acc[mb][nb], 0, 0, 0);
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][0][mb], fb[f][1][nb], acc[mb][nb], 0, 0, 0);
                 if (PA > 1) {
 #pragma unroll
                     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
                         for (int nb = 0; nb < 4; ++nb)
-                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[PA - 1][mb], bv[0][nb], acc[mb][nb], 0, 0, 0);
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][PA - 1][mb], fb[f][0][nb], acc[mb][nb], 0, 0, 0);
                 }
             }
-            stash((u + 1) % S, (u + 1) & 1);
-            __syncthreads();
+            stash((u + 2) % S, u & 1);
+            barrier_lds();
         }
     }
 
-    float* out = p.part + (size_t)ks * p.B * p.Np;
+    float* out = p.part + (size_t)ks * p.rows * p.Np;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int r = b0 + wi * 64 + mb * 16 + 4 * g + e;
-            if (r >= p.B) continue;
+            if (r >= p.rows) continue;
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb) out[(size_t)r * p.Np + n0 + wj * 64 + nb * 16 + lc] = acc[mb][nb][e];
         }
@@ -227,6 +269,7 @@ __global__ void __launch_bounds__(256) lagstep_lif_fwd_kernel(LagStepLif p) {
     const size_t bi = (size_t)b * p.N + i;
     float r = 0.0f;
     for (int q = 0; q < p.KS; ++q) r += p.part[((size_t)q * p.B + b) * p.Np + i];
+    for (int q = 0; q < p.KSF; ++q) r += p.fpart[((size_t)q * p.B * p.P + (size_t)b * p.P + p.tt) * p.Np + i];
     r += p.bias ? p.bias[i] : 0.0f;
     const float m = p.drop ? p.drop[bi] : 1.0f;
     const size_t o = (size_t)t * p.B * p.N + bi;
@@ -261,6 +304,7 @@ __global__ void __launch_bounds__(256) lagstep_lif_bwd_kernel(LagStepLif p) {
     const size_t bj = (size_t)b * p.N + j;
     float gf = 0.0f;
     for (int q = 0; q < p.KS; ++q) gf += p.part[((size_t)q * p.B + b) * p.Np + j];
+    for (int q = 0; q < p.KSF; ++q) gf += p.fpart[((size_t)q * p.B * p.P + (size_t)b * p.P + p.tt) * p.Np + j];
     const size_t o = (size_t)t * p.B * p.N + bj;
     const float u = p.u[o];
     const float y = lif_fire(k, u);
@@ -314,11 +358,13 @@ void launch_hist_zero(uint16_t* h, int B, size_t lda, int Nk, int t0, int t1, hi
 }
 
 constexpr int kLagStepStages = 4;
+constexpr int kLagStepBlock = 8;   // steps per block (near lags per step)
+int lagstep_block() { return kLagStepBlock; }
 
 size_t lagstep_gemm_lds(int pa) { return (size_t)2 * (pa + 2) * 512 * sizeof(uint4); }
 
 void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream) {
-    const int grid = ((g.B + 127) / 128) * (g.Np / 128) * g.KS;
+    const int grid = ((g.rows + 127) / 128) * (g.Np / 128) * g.KS;
     const size_t lds = lagstep_gemm_lds(pa);
     if (pa == 1) {
         ensure_lds((const void*)lagstep_gemm_kernel<1, kLagStepStages>, lds);
