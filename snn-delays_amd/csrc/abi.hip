@@ -311,7 +311,7 @@ LagStepDims lagstep_dims(int T, int B, int N, int L) {
     q.lda = (size_t)(T + q.Lw) * q.Nk;
     q.plane = (size_t)(q.Kt / 8) * q.Np;
     q.KS = lagstep_splits(B, q.Np, q.P * q.Nk, num_cus());
-    q.KSF = q.Lf > 0 ? lagstep_splits(B * q.P, q.Np, q.Lf * q.Nk, num_cus()) : 0;
+    q.KSF = q.Lf > 0 ? lagblock_splits(B, q.Np, q.Nk, num_cus()) : 0;
     // byte offsets of every history row a GEMM may address (incl. rows of a partial tile)
     q.ok = (size_t)(B + 128) * q.lda * 2 < ((size_t)1 << 32) && q.plane * 16 < ((size_t)1 << 32);
     return q;
@@ -665,13 +665,13 @@ int syn_fwd_lagstep(const delrec_syn_fwd_args* a, hipStream_t s) {
     pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.d = a->d; pk.base = a->base; pk.off = a->offsets;
     pk.s = a->s; pk.s_uniform = a->s_uniform; pk.out = planes;
     launch_pack_lagw(pk, true, s);
-    launch_hist_zero(hist, B, q.lda, q.Nk, 0, q.Lw, s);   // spikes before t = 0
+    launch_hist_clear(hist, B, q.lda, s);   // incl. the spikes before t = 0
     // packed k order: lag Lw first, lag 1 last; the far lags Lw .. P + 1 come first
     const size_t kfar = (size_t)q.Lf * q.Nk / 8 * q.Np;   // uint4 offset of the near lags
     LagStepGemm g{};   // near lags of one step: spikes t - P .. t - 1
     g.a0 = hist; g.a1 = nullptr; g.lda = q.lda; g.rs = 0; g.B = B; g.rows = B; g.rp = 1;
     g.p0 = planes + kfar; g.p1 = planes + q.plane + kfar; g.Np = q.Np; g.Kt = q.P * q.Nk;
-    g.KS = q.KS; g.part = part;
+    g.KS = q.KS; g.Nk = q.Nk; g.part = part;
     LagStepGemm gf = g;   // far lags of a block of P steps: row (b, tt) reads spikes t0 + tt - Lw ..
     gf.rows = B * q.P; gf.rp = q.P; gf.rs = q.Nk;
     gf.p0 = planes; gf.p1 = planes + q.plane; gf.Kt = q.Lf * q.Nk; gf.KS = q.KSF; gf.part = fpart;
@@ -684,7 +684,7 @@ int syn_fwd_lagstep(const delrec_syn_fwd_args* a, hipStream_t s) {
     for (int t0 = 0; t0 < T; t0 += q.P) {
         if (q.Lf > 0) {
             gf.aoff = (size_t)t0 * q.Nk;
-            launch_lagstep_gemm(gf, 1, s);
+            launch_lagblock(gf, 1, s);
         }
         for (int t = t0; t < std::min(T, t0 + q.P); ++t) {
             g.aoff = (size_t)(t + q.Lf) * q.Nk;
@@ -837,14 +837,14 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.d = a->d; pk.base = a->base; pk.off = a->offsets;
         pk.s = a->s; pk.s_uniform = a->s_uniform; pk.out = planes;
         launch_pack_lagw(pk, false, s);
-        launch_hist_zero(ghi, B, ls.lda, ls.Nk, T, T + ls.Lw, s);   // gr past the last step
-        launch_hist_zero(glo, B, ls.lda, ls.Nk, T, T + ls.Lw, s);
+        launch_hist_clear(ghi, B, ls.lda, s);   // incl. gr past the last step
+        launch_hist_clear(glo, B, ls.lda, s);
         // packed k order: lag 1 first; the near lags 1 .. P come first
         const size_t kfar = (size_t)ls.P * ls.Nk / 8 * ls.Np;
         LagStepGemm gg{};   // near lags of one step: gr t + 1 .. t + P
         gg.a0 = ghi; gg.a1 = glo; gg.lda = ls.lda; gg.rs = 0; gg.B = B; gg.rows = B; gg.rp = 1;
         gg.p0 = planes; gg.p1 = planes + ls.plane; gg.Np = ls.Np; gg.Kt = ls.P * ls.Nk; gg.KS = ls.KS;
-        gg.part = lpart;
+        gg.Nk = ls.Nk; gg.part = lpart;
         LagStepGemm gf = gg;   // far lags of a block: row (b, tt) of step tb + tt reads gr from tb + tt + P + 1
         gf.rows = B * ls.P; gf.rp = ls.P; gf.rs = ls.Nk;
         gf.p0 = planes + kfar; gf.p1 = planes + ls.plane + kfar; gf.Kt = ls.Lf * ls.Nk; gf.KS = ls.KSF;
@@ -861,7 +861,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
             const int tb = t1 - ls.P + 1;   // the block's first step (rows of steps < 0 are unused)
             if (ls.Lf > 0) {
                 gf.aoff = (size_t)(t1 + 2) * ls.Nk;
-                launch_lagstep_gemm(gf, 2, s);
+                launch_lagblock(gf, 2, s);
             }
             for (int t = t1; t >= std::max(tb, 0); --t) {
                 gg.aoff = (size_t)(t + 1) * ls.Nk;

@@ -158,6 +158,7 @@ struct LagStepGemm {
     const uint4* p0;             // packed M planes (first k-block of the product's lags)
     const uint4* p1;
     int Np, Kt, KS;
+    int Nk;                      // padded neurons per history slice / lag slice
     float* part;                 // [KS][rows][Np]
 };
 
@@ -188,8 +189,11 @@ int lagstep_block();
 size_t lagstep_gemm_lds(int pa);
 void launch_pack_lagw(const LagStepPack& a, bool fwd, hipStream_t stream);
 void launch_hist_zero(uint16_t* h, int B, size_t lda, int Nk, int t0, int t1, hipStream_t stream);
+void launch_hist_clear(uint16_t* h, int B, size_t lda, hipStream_t stream);
 void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream);
 void launch_lagstep_lif(const LagStepLif& l, bool fwd, hipStream_t stream);
+int lagblock_splits(int B, int Np, int Nk, int cus);
+void launch_lagblock(const LagStepGemm& g, int pa, hipStream_t stream);
 
 // hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel and size (cached; the
 // library is used from one host thread at a time)

@@ -42,6 +42,10 @@ __device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
     return u >> 16;
 }
 
+__device__ __forceinline__ bf16x8 load16(i32x4 rs, uint32_t voff) {
+    return __builtin_bit_cast(bf16x8, raw_buffer_load_i32x4(rs, (int)voff, 0, 0));
+}
+
 __device__ __forceinline__ float lagw_delay(const LagStepPack& p, int i, int j) {
     if (p.d) return p.d[(size_t)i * p.N + j];
     return p.base[j] + 0.0f + 1.0f * (float)p.off[(size_t)i * p.N + j];
@@ -250,6 +254,148 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// Far lags of a block of P steps without LDS:
+//   out[tt][b][n] = sum_q sum_k H[b][(base + tt + q) * Nk + k] * M[q][k][n],  q < Lf, tt < P,
+// the Hankel form of the block rows (row tt reads the history shifted by tt slices). For a
+// 32-k chunk the loop walks q: M(q) is loaded once and multiplied by the P history slices
+// q .. q + P - 1, which stay in a register window of W slots (slice sigma in slot sigma mod W,
+// refilled W - P slices ahead after its last reader, like the windowed lag GEMM), the M
+// slices rotating through SM slots. A wave owns 32 rows x 32 columns x P block rows (the P
+// accumulator sets in AGPRs); slices of q >= Lf read zeros through the M descriptor's bound.
+template <int PA, int P, int W, int SM>
+__global__ void __launch_bounds__(256) lagblock_kernel(LagStepGemm p) {
+    static_assert(W % SM == 0 && W > P, "window slots");
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int wi = w >> 1, wj = w & 1, g = lane >> 4, lc = lane & 15;
+    const int BT = (p.B + 63) / 64, NT = p.Np / 64;
+    const int id = (int)blockIdx.x;
+    int bt, nt, ks;
+    if ((BT * NT * p.KS) % 8 == 0 && (NT * p.KS) % 8 == 0) {
+        // the BT row tiles that share an M tile (column tile, split) sit on one XCD
+        const int xcd = id & 7, slot = id >> 3;
+        bt = slot % BT;
+        const int pair = (slot / BT) * 8 + xcd;
+        ks = pair / NT;
+        nt = pair - ks * NT;
+    } else {
+        bt = id % BT;
+        const int rest = id / BT;
+        nt = rest % NT;
+        ks = rest / NT;
+    }
+    const int b0 = bt * 64 + wi * 32, n0 = nt * 64 + wj * 32;
+    const int nch = p.Nk / 32;                       // 32-k chunks of one lag slice
+    const int per = (nch + p.KS - 1) / p.KS;
+    const int c0 = ks * per, c1 = min(nch, c0 + per);
+    const int Lf = p.Kt / p.Nk;
+
+    i32x4 rh[PA], rm[2];
+    const uint32_t hbytes = (uint32_t)((size_t)p.B * p.lda * 2);
+    rh[0] = buffer_rsrc(p.a0, hbytes);
+    if (PA > 1) rh[PA - 1] = buffer_rsrc(p.a1, hbytes);
+    const uint32_t qstep = (uint32_t)((size_t)(p.Nk / 8) * p.Np * 16);   // bytes per lag slice
+    rm[0] = buffer_rsrc(p.p0, (uint32_t)Lf * qstep);
+    rm[1] = buffer_rsrc(p.p1, (uint32_t)Lf * qstep);
+    const uint32_t hstep = (uint32_t)p.Nk * 2;                           // bytes per history slice
+    uint32_t vh[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+        vh[mb] = (uint32_t)(((size_t)(b0 + mb * 16 + lc) * p.lda + p.aoff + 8 * g) * 2);
+    const uint32_t vm = (uint32_t)((size_t)g * p.Np + n0 + lc) * 16;
+
+    floatx4 acc[P][2][2];
+#pragma unroll
+    for (int t = 0; t < P; ++t)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) acc[t][mb][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    for (int c = c0; c < c1; ++c) {
+        bf16x8 hw[W][PA][2], mw[SM][2][2];
+        // history slices 0 .. W - 2 of this chunk, M slices 0 .. SM - 2
+        uint32_t oh = (uint32_t)c * 64;   // byte offset of the chunk within a slice
+        uint32_t om = vm + (uint32_t)c * 4 * p.Np * 16;
+#pragma unroll
+        for (int sl = 0; sl < W - 1; ++sl) {
+#pragma unroll
+            for (int q = 0; q < PA; ++q)
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) hw[sl][q][mb] = load16(rh[q], vh[mb] + oh);
+            oh += hstep;
+        }
+#pragma unroll
+        for (int sl = 0; sl < SM - 1; ++sl) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                mw[sl][q][0] = load16(rm[q], om);
+                mw[sl][q][1] = load16(rm[q], om + 256);
+            }
+            om += qstep;
+        }
+        for (int q0 = 0; q0 < Lf; q0 += W) {
+#pragma unroll
+            for (int u = 0; u < W; ++u) {
+                // refill: history slice q + W - 1 into the slot slice q - 1 left, M(q + SM - 1)
+#pragma unroll
+                for (int q = 0; q < PA; ++q)
+#pragma unroll
+                    for (int mb = 0; mb < 2; ++mb) hw[(u + W - 1) % W][q][mb] = load16(rh[q], vh[mb] + oh);
+                oh += hstep;
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    mw[(u + SM - 1) % SM][q][0] = load16(rm[q], om);
+                    mw[(u + SM - 1) % SM][q][1] = load16(rm[q], om + 256);
+                }
+                om += qstep;
+                __builtin_amdgcn_sched_barrier(0);
+                const int sm = u % SM;
+#pragma unroll
+                for (int t = 0; t < P; ++t)
+#pragma unroll
+                    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb)
+                            acc[t][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                hw[(u + t) % W][0][mb], mw[sm][0][nb], acc[t][mb][nb], 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < P; ++t)
+#pragma unroll
+                    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb)
+                            acc[t][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                hw[(u + t) % W][0][mb], mw[sm][1][nb], acc[t][mb][nb], 0, 0, 0);
+                if (PA > 1) {
+#pragma unroll
+                    for (int t = 0; t < P; ++t)
+#pragma unroll
+                        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                            for (int nb = 0; nb < 2; ++nb)
+                                acc[t][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                    hw[(u + t) % W][PA - 1][mb], mw[sm][0][nb], acc[t][mb][nb], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    float* out = p.part + (size_t)ks * p.rows * p.Np;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int b = b0 + mb * 16 + 4 * g + e;
+            if (b >= p.B) continue;
+#pragma unroll
+            for (int t = 0; t < P; ++t)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+                    out[((size_t)b * P + t) * p.Np + n0 + nb * 16 + lc] = acc[t][mb][nb][e];
+        }
+}
+
+// ---------------------------------------------------------------------------------------
 // LIF steps. One thread per (b, neuron) over the padded width Nk: the history columns past
 // N are written as zeros.
 
@@ -322,6 +468,11 @@ __global__ void __launch_bounds__(256) lagstep_lif_bwd_kernel(LagStepLif p) {
     p.hist2[ho] = (uint16_t)bf16_bits_rne(gr - __uint_as_float(hi << 16));
 }
 
+__global__ void fill_u4_kernel(uint4* __restrict__ p, size_t n) {
+    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < n; q += (size_t)gridDim.x * blockDim.x)
+        p[q] = uint4{0u, 0u, 0u, 0u};
+}
+
 // h[b * lda + off0 + e] = 0 for b < B, e < n
 __global__ void fill_rows_u16_kernel(uint16_t* __restrict__ h, int B, size_t lda, size_t off0, size_t n) {
     const size_t total = (size_t)B * n;
@@ -357,6 +508,14 @@ void launch_hist_zero(uint16_t* h, int B, size_t lda, int Nk, int t0, int t1, hi
     hipLaunchKernelGGL(fill_rows_u16_kernel, dim3(blocks), dim3(256), 0, stream, h, B, lda, (size_t)t0 * Nk, n);
 }
 
+// the whole history (B * lda bf16; lda is a multiple of 32): the far-lag kernel's window
+// reads a few slices past its last lag, which must hold finite values (0 * NaN is NaN)
+void launch_hist_clear(uint16_t* h, int B, size_t lda, hipStream_t stream) {
+    const size_t n = (size_t)B * lda / 8;
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(fill_u4_kernel, dim3(blocks), dim3(256), 0, stream, reinterpret_cast<uint4*>(h), n);
+}
+
 constexpr int kLagStepStages = 4;
 constexpr int kLagStepBlock = 8;   // steps per block (near lags per step)
 int lagstep_block() { return kLagStepBlock; }
@@ -373,6 +532,22 @@ void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream) {
         ensure_lds((const void*)lagstep_gemm_kernel<2, kLagStepStages>, lds);
         hipLaunchKernelGGL((lagstep_gemm_kernel<2, kLagStepStages>), dim3(grid), dim3(256), lds, stream, g);
     }
+}
+
+// far lags of a block: rows (b, tt) of g.part with g.rp == kLagStepBlock
+int lagblock_splits(int B, int Np, int Nk, int cus) {
+    const int tiles = ((B + 63) / 64) * (Np / 64);
+    const int nch = Nk / 32;
+    const int want = (cus + tiles - 1) / tiles;
+    return std::max(1, std::min(want, nch));
+}
+
+void launch_lagblock(const LagStepGemm& g, int pa, hipStream_t stream) {
+    const int grid = ((g.B + 63) / 64) * (g.Np / 64) * g.KS;
+    if (pa == 1)
+        hipLaunchKernelGGL((lagblock_kernel<1, kLagStepBlock, 12, 4>), dim3(grid), dim3(256), 0, stream, g);
+    else
+        hipLaunchKernelGGL((lagblock_kernel<2, kLagStepBlock, 10, 2>), dim3(grid), dim3(256), 0, stream, g);
 }
 
 void launch_lagstep_lif(const LagStepLif& l, bool fwd, hipStream_t stream) {
