@@ -131,7 +131,9 @@ def algorithmic_work(w):
 SCAN_SYMBOL = {
     'C2': {'axonal_fwd_scan': 'axonal_fwd_wave_fast', 'axonal_bwd_scan': 'axonal_bwd_tiled_fast'},
     'C3': {'syn_fwd_scan': 'syn_fwd_scatter', 'syn_bwd_scan': 'syn_bwd_hyb'},
-    'C4': {'syn_fwd_scan': 'syn_fwd_gather_kernel', 'syn_bwd_scan': 'syn_bwd_kernel'},
+    # C4's scans are sequences of launches (per 8-step block one lagblock_kernel, per step one
+    # lagstep_gemm_kernel + one LIF kernel): the scan time is the whole sequence's
+    'C4': {'syn_fwd_scan': 'lagstep_fwd_sequence', 'syn_bwd_scan': 'lagstep_bwd_sequence'},
 }
 
 
