@@ -241,16 +241,22 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    with _lib.scan_timing(2 * args.steps + 8) as scans_t:
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / args.steps
+    # per scan kernel (HIP events on the kernels' stream) and per entry point (scan +
+    # reductions + GEMMs), from a few extra steps outside the timed region: the event
+    # pairs would otherwise add their own gaps to the timed steps
+    n_extra = min(5, args.steps)
+    with _lib.scan_timing(2 * n_extra + 8) as scans_t:
+        for _ in range(n_extra):
             step()
         torch.cuda.synchronize()
-        t1 = time.perf_counter()
-    ms = (t1 - t0) * 1e3 / args.steps
-    # per entry point (scan + reductions + GEMMs), from a few extra steps outside the timed region
     with _lib.timing() as rec:
-        for _ in range(min(5, args.steps)):
+        for _ in range(n_extra):
             step()
         torch.cuda.synchronize()
     per_entry, per_scan = {}, {}
