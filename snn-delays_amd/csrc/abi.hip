@@ -42,6 +42,8 @@ struct Counter {
     void take(size_t count) { used += align_up(count * sizeof(T)); }
 };
 
+// dynamic LDS a launch may request: the per-workgroup limit less 1 KB, which holds the
+// kernels' own static LDS (a __syncthreads_or takes 256 bytes)
 int max_lds_bytes() {
     static int cached = -1;
     if (cached < 0) {
@@ -49,7 +51,7 @@ int max_lds_bytes() {
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
             v = 65536;
-        cached = v;
+        cached = v - 1024;
     }
     return cached;
 }
@@ -362,7 +364,7 @@ void syn_bwd_ws(C& c, int T, int B, int N, int L) {
     c.template take<uint4>(packed);                     // gr_hi
     c.template take<uint4>(packed);                     // gr_lo
     c.template take<uint4>(packed);                     // shifted spikes
-    c.template take<int>((size_t)3 * N + 64);           // lag range per column, meta
+    c.template take<int>((size_t)4 * N + 64);           // lag range per column, meta
     if (syn_lagstep(T, B, N, L)) {
         lagstep_ws(c, T, B, N, L, false);
         return;
@@ -791,7 +793,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     uint4* ahi = cv.take<uint4>(packed);
     uint4* alo = cv.take<uint4>(packed);
     uint4* yb = cv.take<uint4>(packed);
-    int* meta = cv.take<int>((size_t)3 * N + 64);
+    int* meta = cv.take<int>((size_t)4 * N + 64);
     const bool lagstep = syn_lagstep(T, B, N, a->L);
     void* wt = nullptr;
     void* dt = nullptr;
@@ -815,7 +817,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     LagBf16 g{};
     g.T = T; g.B = B; g.Bp = q.Bp; g.N = N; g.Np = q.Np; g.L = a->L; g.Kp = q.Kp; g.KS = q.KS;
     g.ahi = ahi; g.alo = alo; g.yb = yb;
-    g.meta = meta; g.lo = meta + 64; g.rc = meta + 64 + N; g.om = meta + 64 + 2 * N;
+    g.meta = meta; g.lo = meta + 64; g.rc = meta + 64 + N; g.om = meta + 64 + 2 * N; g.ox = meta + 64 + 3 * N;
     g.d = a->d; g.base = a->base; g.off = a->offsets; g.s = a->s; g.s_uniform = a->s_uniform;
     g.pw = lagp;
     g.pd = lagp + (size_t)q.KS * NN;
@@ -899,10 +901,16 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     const bool timed = scan_begin(DELREC_WS_SYN_BWD, s);
     // hybrid, ring in LDS, one source per lane: the streamlined gather (its ring covers
     // the receivers rounded up to groups of 64)
-    const size_t lds_h = (size_t)((N + 63) / 64 * 64) * lay.RP * sizeof(float);   // groups of <= 64 receivers
+    const size_t hrows = (size_t)((N + 63) / 64 * 64);   // groups of <= 64 receivers
+    const size_t lds_h = hrows * lay.RP * sizeof(float);
     const bool hyb_fast = hybrid && N <= 1024 && (lay.KT == 2 || lay.KT == 4) &&
                           lds_h <= (size_t)max_lds_bytes() && getenv_flag_off("DELREC_SYN_BWD_HYB");
-    const bool ok = (hyb_fast && launch_syn_bwd_hyb(p, lay.block, lds_h, s)) || launch_syn_bwd(p, lay.block, lay.lds, s);
+    // room for rows that also mirror the offset span (up to L more slots): the kernel
+    // takes the no-wrap form when the span it finds fits
+    const size_t lds_hx = std::max(lds_h, std::min((size_t)max_lds_bytes(),
+                                                   hrows * (size_t)(2 * lay.R + lay.KT + 1) * sizeof(float)));
+    p.ldsf = (int)(lds_hx / sizeof(float));
+    const bool ok = (hyb_fast && launch_syn_bwd_hyb(p, lay.block, lds_hx, s)) || launch_syn_bwd(p, lay.block, lay.lds, s);
     scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();

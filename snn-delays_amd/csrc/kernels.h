@@ -100,6 +100,7 @@ struct SynBwd {
     float* gr;                  // (T,B,N) dL/drec (always written: the dW / dd GEMM reads it)
     float* part;                // [B][N] db partials
     float* gring;               // global ring [B][N][RP] when it does not fit LDS, else NULL
+    int ldsf;                   // floats of LDS the hybrid backward was given
 };
 
 // the split partials of the lag GEMM and what dd / ds are formed from
@@ -121,10 +122,12 @@ struct LagBf16 {
     const uint4* ahi;            // gr_hi (Kp, Np) k-blocked
     const uint4* alo;            // gr_lo
     const uint4* yb;             // shifted spikes Y' (Kp, Np) k-blocked
-    int* meta;                   // meta[0] = widest column lag range, meta[1] = smallest offset
+    int* meta;                   // meta[0] = widest column lag range, meta[1] / [2] = smallest /
+                                 // largest offset
     int* lo;                     // [N] first lag of each column
     int* rc;                     // [N] number of lags of each column
     int* om;                     // [N] smallest offset of each column (hybrid)
+    int* ox;                     // [N] largest offset of each column (hybrid)
     const float* d;              // row-major, or NULL (hybrid)
     const float* base;
     const int8_t* off;

@@ -110,10 +110,10 @@ __device__ __forceinline__ float lag_conn_delay(const LagBf16& p, int i, int j) 
 // derivative for every receiver. Also each column's smallest offset (hybrid). A workgroup
 // covers 64 columns with 16 lanes over the receivers.
 __global__ void __launch_bounds__(1024) lag_cols_kernel(LagBf16 p) {
-    __shared__ int sa[16][64], sz[16][64], so[16][64];
+    __shared__ int sa[16][64], sz[16][64], so[16][64], sx[16][64];
     const int jl = threadIdx.x & 63, il = threadIdx.x >> 6;
     const int j = blockIdx.x * 64 + jl;
-    int a = 0x7fffffff, z = -0x7fffffff, om = 127;
+    int a = 0x7fffffff, z = -0x7fffffff, om = 127, ox = -128;
     if (j < p.N) {
         const float s = p.s ? p.s[j] : p.s_uniform;
         for (int i = il; i < p.N; i += 16) {
@@ -123,52 +123,65 @@ __global__ void __launch_bounds__(1024) lag_cols_kernel(LagBf16 p) {
                 a = min(a, l0);
                 z = max(z, l1);
             }
-            if (p.off) om = min(om, (int)p.off[(size_t)i * p.N + j]);
+            if (p.off) {
+                const int o = p.off[(size_t)i * p.N + j];
+                om = min(om, o);
+                ox = max(ox, o);
+            }
         }
     }
     sa[il][jl] = a;
     sz[il][jl] = z;
     so[il][jl] = om;
+    sx[il][jl] = ox;
     __syncthreads();
     if (il == 0 && j < p.N) {
         for (int q = 1; q < 16; ++q) {
             a = min(a, sa[q][jl]);
             z = max(z, sz[q][jl]);
             om = min(om, so[q][jl]);
+            ox = max(ox, sx[q][jl]);
         }
         p.lo[j] = a <= z ? a : 1;
         p.rc[j] = a <= z ? z - a + 1 : 0;
         p.om[j] = om;
+        p.ox[j] = ox;
     }
 }
 
-// meta[0] = widest column lag range, meta[1] = smallest offset (hybrid)
+// meta[0] = widest column lag range, meta[1] / meta[2] = smallest / largest offset (hybrid)
 __global__ void __launch_bounds__(1024) lag_meta_kernel(const int* __restrict__ rc,
-                                                        const int* __restrict__ om, int N,
+                                                        const int* __restrict__ om,
+                                                        const int* __restrict__ ox, int N,
                                                         int* __restrict__ meta) {
-    __shared__ int sr[16], so[16];
-    int r = 0, o = 127;
+    __shared__ int sr[16], so[16], sx[16];
+    int r = 0, o = 127, x = -128;
     for (int j = threadIdx.x; j < N; j += blockDim.x) {
         r = max(r, rc[j]);
         o = min(o, om[j]);
+        x = max(x, ox[j]);
     }
 #pragma unroll
     for (int k = 32; k >= 1; k >>= 1) {
         r = max(r, __shfl_xor(r, k));
         o = min(o, __shfl_xor(o, k));
+        x = max(x, __shfl_xor(x, k));
     }
     if ((threadIdx.x & 63) == 0) {
         sr[threadIdx.x >> 6] = r;
         so[threadIdx.x >> 6] = o;
+        sx[threadIdx.x >> 6] = x;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) {
             r = max(r, sr[w]);
             o = min(o, so[w]);
+            x = max(x, sx[w]);
         }
         meta[0] = r;
         meta[1] = o;
+        meta[2] = x;
     }
 }
 
@@ -347,7 +360,7 @@ __global__ void __launch_bounds__(256) lag_win_kernel(LagBf16 p) {
 
 void launch_lag_cols(const LagBf16& a, hipStream_t stream) {
     hipLaunchKernelGGL(lag_cols_kernel, dim3((a.N + 63) / 64), dim3(1024), 0, stream, a);
-    hipLaunchKernelGGL(lag_meta_kernel, dim3(1), dim3(1024), 0, stream, a.rc, a.om, a.N, a.meta);
+    hipLaunchKernelGGL(lag_meta_kernel, dim3(1), dim3(1024), 0, stream, a.rc, a.om, a.ox, a.N, a.meta);
 }
 
 void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hipStream_t stream) {

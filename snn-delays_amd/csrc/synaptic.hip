@@ -905,8 +905,14 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     const int NG = (NC + kBwdGroup - 1) / kBwdGroup;
     const int rows = NG * kBwdGroup * 16;
     const bool chk = __syncthreads_or(act && lob + min(omin, 0) < 1) != 0;
+    // no-wrap form: each ring row mirrors its first E = (max - min offset) + KT slots after
+    // slot R - 1, so a connection's slot needs no wrap (when the longer rows fit the LDS)
+    const int E = p.meta[2] - omin + KT;
+    const int RPn = (R + E) | 1;
+    const bool nowrap = !chk && E <= R && rows * RPn <= p.ldsf;
+    const int RPu = nowrap ? RPn : RP;
 
-    for (int q = tid; q < rows * RP; q += BS) ring[q] = 0.0f;
+    for (int q = tid; q < rows * RPu; q += BS) ring[q] = 0.0f;
     __syncthreads();
 
     // blocked W^T: receivers 16c .. 16c+15 of source j at ((c*N + j)*16) elements
@@ -945,20 +951,23 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     }
     float lam = 0.0f, dbacc = 0.0f;
     int tmod = (T - 1) % R;
-    float* const own = act ? ring + (size_t)j * RP : ring + (size_t)(rows - 1) * RP;   // never read for j >= N
+    float* const own = act ? ring + (size_t)j * RPu : ring + (size_t)(rows - 1) * RPu;   // never read for j >= N
+    const int mirror = nowrap ? E : KT;   // slots written twice
 
-    auto gather_group = [&](const Chunk (&cg)[kBwdGroup], int g0, int tbo, float (&acc)[KT], auto checked) {
+    auto gather_group = [&](const Chunk (&cg)[kBwdGroup], int g0, int tbo, float (&acc)[KT], auto checked,
+                            auto nowrapped) {
         constexpr bool CHK = decltype(checked)::value;
+        constexpr bool NW = decltype(nowrapped)::value;
 #pragma unroll
         for (int cc = 0; cc < kBwdGroup; ++cc) {
-            const float* rowc = ring + (size_t)(g0 + cc) * 16 * RP;
+            const float* rowc = ring + (size_t)(g0 + cc) * 16 * RPu;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const uint32_t ow = (e < 4) ? cg[cc].o.x : (e < 8) ? cg[cc].o.y : (e < 12) ? cg[cc].o.z : cg[cc].o.w;
                 const int off = ((int)(ow << (24 - 8 * (e & 3)))) >> 24;
                 int sl = tbo + off;
-                sl = sl >= R ? sl - R : sl;
-                const float* rp = rowc + e * RP + sl;
+                if (!NW) sl = sl >= R ? sl - R : sl;
+                const float* rp = rowc + e * RPu + sl;
                 float wv;
                 if constexpr (WBF) {
                     const uint4& wq = cg[cc].w[e >> 3];
@@ -986,7 +995,7 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
         }
     };
 
-    auto step = [&](const int t, float& gs, float& us, auto checked) {
+    auto step = [&](const int t, float& gs, float& us, auto checked, auto nowrapped) {
         float acc[KT];
 #pragma unroll
         for (int f = 0; f < KT; ++f) acc[f] = 0.0f;
@@ -1002,11 +1011,11 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
         for (int g = 0; g < NG; g += 2) {
 #pragma unroll
             for (int cc = 0; cc < kBwdGroup; ++cc) fetch((g + 1) * kBwdGroup + cc, cb[cc]);
-            gather_group(ca, g * kBwdGroup, tbo, acc, checked);
+            gather_group(ca, g * kBwdGroup, tbo, acc, checked, nowrapped);
             if (g + 1 < NG) {
 #pragma unroll
                 for (int cc = 0; cc < kBwdGroup; ++cc) fetch((g + 2) * kBwdGroup + cc, ca[cc]);
-                gather_group(cb, (g + 1) * kBwdGroup, tbo, acc, checked);
+                gather_group(cb, (g + 1) * kBwdGroup, tbo, acc, checked, nowrapped);
             }
         }
         float gf = 0.0f;
@@ -1027,7 +1036,7 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
         dbacc += (live && act) ? gr : 0.0f;
         if (act && live) {
             own[tmod] = gr;
-            if (tmod < KT) own[tmod + R] = gr;
+            if (tmod < mirror) own[tmod + R] = gr;
         }
         const int tp = t - kPrefetchSynBwd;
         const uint32_t nb = tp >= 0 ? row_bytes : 0u;
@@ -1041,14 +1050,15 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
         tmod = tmod == 0 ? R - 1 : tmod - 1;
     };
 
-    auto run = [&](auto checked) {
+    auto run = [&](auto checked, auto nowrapped) {
         for (int t0 = T - 1; t0 >= 0; t0 -= kPrefetchSynBwd) {
 #pragma unroll
-            for (int q = 0; q < kPrefetchSynBwd; ++q) step(t0 - q, gq[q], uq[q], checked);
+            for (int q = 0; q < kPrefetchSynBwd; ++q) step(t0 - q, gq[q], uq[q], checked, nowrapped);
         }
     };
-    if (chk) run(std::true_type{});
-    else run(std::false_type{});
+    if (chk) run(std::true_type{}, std::false_type{});
+    else if (nowrap) run(std::false_type{}, std::true_type{});
+    else run(std::false_type{}, std::false_type{});
     if (act) p.part[(size_t)b * N + j] = dbacc;
 }
 
