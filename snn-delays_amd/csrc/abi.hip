@@ -372,6 +372,7 @@ void syn_bwd_ws(C& c, int T, int B, int N, int L) {
     c.template take<float>((size_t)N * lay.NT);         // W^T (fp32 or bf16)
     c.template take<float>((size_t)N * lay.NT);         // d^T or the offsets^T
     c.template take<float>((size_t)B * N * lay.RP);     // ring when it does not fit LDS
+    c.template take<uint8_t>((size_t)N * lay.NT);       // byte slot offsets (hybrid)
 }
 
 // out[c * op + r] = in[r * n + c] for an (n, n) matrix; output columns r in [n, op) are 0
@@ -798,11 +799,13 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     void* wt = nullptr;
     void* dt = nullptr;
     float* gring = nullptr;
+    uint8_t* offq = nullptr;
     if (!lagstep) {
         wt = cv.take<float>((size_t)N * wlay.NT);
         dt = cv.take<float>((size_t)N * wlay.NT);
         gring = cv.take<float>((size_t)B * N * wlay.RP);
-        if (!wt || !dt || !gring) return DELREC_ERR_WORKSPACE;
+        offq = cv.take<uint8_t>((size_t)N * wlay.NT);
+        if (!wt || !dt || !gring || !offq) return DELREC_ERR_WORKSPACE;
     }
     if (!gr || !part || !lagp || !ahi || !alo || !yb || !meta) return DELREC_ERR_WORKSPACE;
 
@@ -823,6 +826,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     g.pd = lagp + (size_t)q.KS * NN;
     g.ps = a->ds ? lagp + (size_t)2 * q.KS * NN : nullptr;
     launch_lag_cols(g, s);
+    if (hybrid && !lagstep) launch_pack_offq(static_cast<const int8_t*>(dt), (size_t)N * lay.NT, meta, offq, s);
 
     if (lagstep) {
         // reverse-time scan as one lag-stacked GEMM + one LIF launch per step
@@ -910,6 +914,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     const size_t lds_hx = std::max(lds_h, std::min((size_t)max_lds_bytes(),
                                                    hrows * (size_t)(2 * lay.R + lay.KT + 1) * sizeof(float)));
     p.ldsf = (int)(lds_hx / sizeof(float));
+    p.offq = hybrid ? offq : nullptr;
     const bool ok = (hyb_fast && launch_syn_bwd_hyb(p, lay.block, lds_hx, s)) || launch_syn_bwd(p, lay.block, lay.lds, s);
     scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;

@@ -101,6 +101,7 @@ struct SynBwd {
     float* part;                // [B][N] db partials
     float* gring;               // global ring [B][N][RP] when it does not fit LDS, else NULL
     int ldsf;                   // floats of LDS the hybrid backward was given
+    const uint8_t* offq;        // blocked (offset - smallest offset) * 4 as bytes (hybrid), or NULL
 };
 
 // the split partials of the lag GEMM and what dd / ds are formed from
@@ -238,6 +239,8 @@ bool launch_syn_fwd_scatter(const SynFwd& a, int kf, int block, size_t lds, hipS
 bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);
 // hybrid backward, ring in LDS over ceil(N/64)*64 rows, one source per lane (N <= 512),
 // KT = 2 or 4; false when it does not apply
+// offq[q] = (offt[q] - meta[1]) * 4 (the byte slot offsets of the hybrid backward)
+void launch_pack_offq(const int8_t* offt, size_t n, const int* meta, uint8_t* offq, hipStream_t stream);
 bool launch_syn_bwd_hyb(const SynBwd& a, int block, size_t lds, hipStream_t stream);
 // each column's lag range (lo, rc, om) and meta[0..1]
 void launch_lag_cols(const LagBf16& a, hipStream_t stream);

@@ -909,7 +909,8 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     // slot R - 1, so a connection's slot needs no wrap (when the longer rows fit the LDS)
     const int E = p.meta[2] - omin + KT;
     const int RPn = (R + E) | 1;
-    const bool nowrap = !chk && E <= R && rows * RPn <= p.ldsf;
+    // it reads the offsets as byte slot offsets (offset - smallest) * 4, which needs a span <= 63
+    const bool nowrap = !chk && E <= R && rows * RPn <= p.ldsf && p.offq && p.meta[2] - omin <= 63;
     const int RPu = nowrap ? RPn : RP;
 
     for (int q = tid; q < rows * RPu; q += BS) ring[q] = 0.0f;
@@ -918,7 +919,7 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     // blocked W^T: receivers 16c .. 16c+15 of source j at ((c*N + j)*16) elements
     const uint32_t wbytes = (uint32_t)((size_t)p.NT * N * (WBF ? 2 : 4));
     const uint32_t obytes = (uint32_t)((size_t)p.NT * N);
-    const i32x4 rw = buffer_rsrc(p.Wt, wbytes), ro = buffer_rsrc(p.offt, obytes);
+    const i32x4 rw = buffer_rsrc(p.Wt, wbytes), ro = buffer_rsrc(nowrap ? (const void*)p.offq : (const void*)p.offt, obytes);
     const int wj = act ? j * 16 * (WBF ? 2 : 4) : kOutOfRange, oj = act ? j * 16 : kOutOfRange;
     const int wcs = N * 16 * (WBF ? 2 : 4), ocs = N * 16;   // bytes per chunk
     constexpr int WV = WBF ? 2 : 4;                          // uint4 of W per chunk
@@ -964,10 +965,18 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const uint32_t ow = (e < 4) ? cg[cc].o.x : (e < 8) ? cg[cc].o.y : (e < 12) ? cg[cc].o.z : cg[cc].o.w;
-                const int off = ((int)(ow << (24 - 8 * (e & 3)))) >> 24;
-                int sl = tbo + off;
-                if (!NW) sl = sl >= R ? sl - R : sl;
-                const float* rp = rowc + e * RPu + sl;
+                const float* rp;
+                int off = 0;
+                if constexpr (NW) {
+                    // tbo holds the base slot in bytes; one byte-select add per connection
+                    const uint32_t sl4 = (uint32_t)tbo + ((ow >> (8 * (e & 3))) & 0xFFu);
+                    rp = reinterpret_cast<const float*>(reinterpret_cast<const char*>(rowc + e * RPu) + sl4);
+                } else {
+                    off = ((int)(ow << (24 - 8 * (e & 3)))) >> 24;
+                    int sl = tbo + off;
+                    sl = sl >= R ? sl - R : sl;
+                    rp = rowc + e * RPu + sl;
+                }
                 float wv;
                 if constexpr (WBF) {
                     const uint4& wq = cg[cc].w[e >> 3];
@@ -1004,7 +1013,8 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
         int tbo = tmod + lob + omin;
         tbo %= R;
         tbo = tbo < 0 ? tbo + R : tbo;
-        tbo -= omin;
+        if constexpr (decltype(nowrapped)::value) tbo *= 4;   // bytes; offsets arrive as (off - omin) * 4
+        else tbo -= omin;
         Chunk ca[kBwdGroup], cb[kBwdGroup];
 #pragma unroll
         for (int cc = 0; cc < kBwdGroup; ++cc) fetch(cc, ca[cc]);
@@ -1060,6 +1070,18 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     else if (nowrap) run(std::false_type{}, std::true_type{});
     else run(std::false_type{}, std::false_type{});
     if (act) p.part[(size_t)b * N + j] = dbacc;
+}
+
+__global__ void pack_offq_kernel(const int8_t* __restrict__ offt, size_t n, const int* __restrict__ meta,
+                                 uint8_t* __restrict__ offq) {
+    const int omin = meta[1];
+    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < n; q += (size_t)gridDim.x * blockDim.x)
+        offq[q] = (uint8_t)(((int)offt[q] - omin) * 4);
+}
+
+void launch_pack_offq(const int8_t* offt, size_t n, const int* meta, uint8_t* offq, hipStream_t stream) {
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(pack_offq_kernel, dim3(blocks), dim3(256), 0, stream, offt, n, meta, offq);
 }
 
 #define DELREC_SBH_CASE(KTV, WBFV)                                                          \
