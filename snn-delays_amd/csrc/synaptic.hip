@@ -880,15 +880,21 @@ void launch_syn_bwd_k(const SynBwd& a, int block, size_t lds, hipStream_t stream
 // read 0. CHK: some connection may reach a lag <= 0 (negative base), those taps weigh 0.
 template <int KT, bool WBF, int MAXT>
 __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
+    // SPLIT (1024-thread blocks): lanes l and l + 32 of a wave hold the same source and
+    // gather over the two halves of the receivers, so four waves share each SIMD (128 VGPRs)
+    constexpr bool SPLIT = MAXT > 512;
     // chunks of 16 receivers per group: two groups of operands stay in registers
-    constexpr int kBwdGroup = MAXT <= 512 ? 4 : 2;
+    constexpr int kBwdGroup = SPLIT ? 1 : 4;
     extern __shared__ float smem[];
     const int N = p.N, T = p.T, B = p.B, R = p.R, RP = p.RP;
     const int b = blockIdx.x, tid = threadIdx.x, BS = blockDim.x;
-    float* ring = smem;                                   // [NC * 16 rows][RP]
+    float* ring = smem;                                   // [rows][RP]
     const size_t BN = (size_t)B * N;
-    const bool act = tid < N;
-    const int j = act ? tid : 0;
+    const int half = SPLIT ? (tid >> 5) & 1 : 0;
+    const int jloc = SPLIT ? (tid >> 6) * 32 + (tid & 31) : tid;
+    const bool act = jloc < N;
+    const bool writer = act && half == 0;                 // the lane that stores for source j
+    const int j = act ? jloc : 0;
     const Lif k = p.lif;
     const float m = p.drop ? p.drop[(size_t)b * N + j] : 1.0f;
     const float sv = p.s_uniform;
@@ -901,9 +907,11 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
 #pragma unroll
     for (int f = 0; f < KT; ++f) hq[f] = fmaxf(sv - fabsf((float)(lob + f) - c), 0.0f);
     const int omin = p.meta[1];
-    const int NC = (N + 15) >> 4;
+    const int NC0 = (N + 15) >> 4;
+    const int NC = SPLIT ? (NC0 + 1) / 2 : NC0;           // chunks of 16 receivers per lane
     const int NG = (NC + kBwdGroup - 1) / kBwdGroup;
-    const int rows = NG * kBwdGroup * 16;
+    const int rows = (SPLIT ? 2 : 1) * NG * kBwdGroup * 16;
+    const int cbase = half * NC;                          // the lane's first chunk
     const bool chk = __syncthreads_or(act && lob + min(omin, 0) < 1) != 0;
     // no-wrap form: each ring row mirrors its first E = (max - min offset) + KT slots after
     // slot R - 1, so a connection's slot needs no wrap (when the longer rows fit the LDS)
@@ -920,8 +928,9 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     const uint32_t wbytes = (uint32_t)((size_t)p.NT * N * (WBF ? 2 : 4));
     const uint32_t obytes = (uint32_t)((size_t)p.NT * N);
     const i32x4 rw = buffer_rsrc(p.Wt, wbytes), ro = buffer_rsrc(nowrap ? (const void*)p.offq : (const void*)p.offt, obytes);
-    const int wj = act ? j * 16 * (WBF ? 2 : 4) : kOutOfRange, oj = act ? j * 16 : kOutOfRange;
     const int wcs = N * 16 * (WBF ? 2 : 4), ocs = N * 16;   // bytes per chunk
+    const int wj = act ? j * 16 * (WBF ? 2 : 4) + cbase * wcs : kOutOfRange;
+    const int oj = act ? j * 16 + cbase * ocs : kOutOfRange;
     constexpr int WV = WBF ? 2 : 4;                          // uint4 of W per chunk
     struct Chunk { uint4 w[WV]; uint4 o; };
     auto fetch = [&](int cidx, Chunk& ch) {
@@ -937,7 +946,7 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     const uint32_t row_bytes = (uint32_t)BN * 4u;
     const uint64_t step_b = (uint64_t)row_bytes;
     const int voff = (b * N + j) * 4;
-    const int soff = act ? voff : kOutOfRange;
+    const int soff = writer ? voff : kOutOfRange;
 
     float gq[kPrefetchSynBwd], uq[kPrefetchSynBwd];
     const int tp0 = T - 1 - kPrefetchSynBwd;
@@ -961,7 +970,7 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
         constexpr bool NW = decltype(nowrapped)::value;
 #pragma unroll
         for (int cc = 0; cc < kBwdGroup; ++cc) {
-            const float* rowc = ring + (size_t)(g0 + cc) * 16 * RPu;
+            const float* rowc = ring + (size_t)(cbase + g0 + cc) * 16 * RPu;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const uint32_t ow = (e < 4) ? cg[cc].o.x : (e < 8) ? cg[cc].o.y : (e < 12) ? cg[cc].o.z : cg[cc].o.w;
@@ -1028,6 +1037,10 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
                 gather_group(cb, (g + 1) * kBwdGroup, tbo, acc, checked, nowrapped);
             }
         }
+        if constexpr (SPLIT) {
+#pragma unroll
+            for (int f = 0; f < KT; ++f) acc[f] += __shfl_xor(acc[f], 32);
+        }
         float gf = 0.0f;
 #pragma unroll
         for (int f = 0; f < KT; ++f) gf = fmaf(hq[f], acc[f], gf);
@@ -1044,7 +1057,7 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
         dxa -= step_b;
         gra -= step_b;
         dbacc += (live && act) ? gr : 0.0f;
-        if (act && live) {
+        if (writer && live) {
             own[tmod] = gr;
             if (tmod < mirror) own[tmod + R] = gr;
         }
@@ -1069,7 +1082,7 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     if (chk) run(std::true_type{}, std::false_type{});
     else if (nowrap) run(std::false_type{}, std::true_type{});
     else run(std::false_type{}, std::false_type{});
-    if (act) p.part[(size_t)b * N + j] = dbacc;
+    if (writer) p.part[(size_t)b * N + j] = dbacc;
 }
 
 __global__ void pack_offq_kernel(const int8_t* __restrict__ offt, size_t n, const int* __restrict__ meta,
@@ -1086,15 +1099,24 @@ void launch_pack_offq(const int8_t* offt, size_t n, const int* meta, uint8_t* of
 
 #define DELREC_SBH_CASE(KTV, WBFV)                                                          \
     if (kt == KTV && wbf == WBFV) {                                                          \
-        ensure_lds((const void*)syn_bwd_hyb<KTV, WBFV, 512>, lds);                           \
-        hipLaunchKernelGGL((syn_bwd_hyb<KTV, WBFV, 512>), dim3(a.B), dim3(block), lds, stream, a); \
+        if (split) {                                                                         \
+            ensure_lds((const void*)syn_bwd_hyb<KTV, WBFV, 1024>, lds);                      \
+            hipLaunchKernelGGL((syn_bwd_hyb<KTV, WBFV, 1024>), dim3(a.B), dim3(block), lds, stream, a); \
+        } else {                                                                             \
+            ensure_lds((const void*)syn_bwd_hyb<KTV, WBFV, 512>, lds);                       \
+            hipLaunchKernelGGL((syn_bwd_hyb<KTV, WBFV, 512>), dim3(a.B), dim3(block), lds, stream, a); \
+        }                                                                                    \
         return true;                                                                         \
     }
 
 // blocks of up to 512 threads (two waves per SIMD, 256 VGPRs: the operand groups stay in
 // registers); larger blocks take syn_bwd_kernel
 bool launch_syn_bwd_hyb(const SynBwd& a, int block, size_t lds, hipStream_t stream) {
-    if (block > 512) return false;
+    // up to 512 sources: the split form, two lanes per source (DELREC_SYN_BWD_SPLIT=0: one)
+    const char* e = getenv("DELREC_SYN_BWD_SPLIT");
+    const bool split = a.N <= 512 && !(e && e[0] == '0');
+    if (split) block = 2 * ((a.N + 31) / 32 * 32);
+    else if (block > 512) return false;
     const int kt = a.KT;
     const bool wbf = a.w_bf16 != 0;
     DELREC_SBH_CASE(2, false) DELREC_SBH_CASE(2, true) DELREC_SBH_CASE(4, false) DELREC_SBH_CASE(4, true)
