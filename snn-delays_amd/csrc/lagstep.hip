@@ -413,8 +413,11 @@ __global__ void __launch_bounds__(256) lagstep_lif_fwd_kernel(LagStepLif p) {
     }
     const Lif k = p.lif;
     const size_t bi = (size_t)b * p.N + i;
+    // the partial sums in a fixed order; unrolled so that their loads are in flight together
     float r = 0.0f;
+#pragma unroll 8
     for (int q = 0; q < p.KS; ++q) r += p.part[((size_t)q * p.B + b) * p.Np + i];
+#pragma unroll 4
     for (int q = 0; q < p.KSF; ++q) r += p.fpart[((size_t)q * p.B * p.P + (size_t)b * p.P + p.tt) * p.Np + i];
     r += p.bias ? p.bias[i] : 0.0f;
     const float m = p.drop ? p.drop[bi] : 1.0f;
@@ -449,7 +452,9 @@ __global__ void __launch_bounds__(256) lagstep_lif_bwd_kernel(LagStepLif p) {
     const Lif k = p.lif;
     const size_t bj = (size_t)b * p.N + j;
     float gf = 0.0f;
+#pragma unroll 8
     for (int q = 0; q < p.KS; ++q) gf += p.part[((size_t)q * p.B + b) * p.Np + j];
+#pragma unroll 4
     for (int q = 0; q < p.KSF; ++q) gf += p.fpart[((size_t)q * p.B * p.P + (size_t)b * p.P + p.tt) * p.Np + j];
     const size_t o = (size_t)t * p.B * p.N + bj;
     const float u = p.u[o];
