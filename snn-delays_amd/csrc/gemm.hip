@@ -202,6 +202,7 @@ __global__ void lag_finish_kernel(LagGemm p, float* dW, float* dd) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= NN) return;
     float aw = 0.0f, ad = 0.0f;
+#pragma unroll 8
     for (int k = 0; k < p.KS; ++k) {
         aw += p.pw[(size_t)k * NN + idx];
         if (p.pd) ad += p.pd[(size_t)k * NN + idx];
