@@ -106,18 +106,19 @@ bool axonal_layout(int N, int L, AxLayout& o) {
         if (cj == 32) {
             ri = 4;
         } else {
-            // the smallest RI whose lanes fit the block (RI x CJ >= 128 runs 512 threads)
-            while (ri < 8 && ((N + ri - 1) / ri) * nj > (ri * cj >= 128 ? 512 : 1024)) ri <<= 1;
+            // the smallest RI whose lanes fit the block (kernels with RI >= 4 run at most 512
+            // threads, TiledThreads in axonal.hip)
+            while (ri < 8 && ((N + ri - 1) / ri) * nj > (ri >= 4 ? 512 : 1024)) ri <<= 1;
             if (ri == 4 && nj == 16) ri = 8;
             if (const char* e = getenv("DELREC_AXONAL_RI")) {
                 const int want = atoi(e);
                 if (nj == 16 && (want == 2 || want == 4 || want == 8) &&
-                    ((N + want - 1) / want) * nj <= (want * cj >= 128 ? 512 : 1024))
+                    ((N + want - 1) / want) * nj <= (want >= 4 ? 512 : 1024))
                     ri = want;
             }
         }
         const int lanes = ((N + ri - 1) / ri) * nj;
-        if (lanes > (ri * cj >= 128 ? 512 : 1024) || ri > nj) return false;
+        if (lanes > (ri >= 4 ? 512 : 1024) || ri > nj) return false;
         o.res = true;
         o.G = nj;
         o.ri = ri;
