@@ -95,7 +95,10 @@ def test_synaptic_fwd_bwd_matches_oracle(dev, case):
 
 # the lag-stacked per-step GEMM scans (taken by default only where the rings do not fit
 # LDS, the last two cases above) forced at every size; the same oracle and tolerances
-LAGSTEP_CASES = [SYN_CASES[i] for i in (0, 1, 2, 3, 4, 5, 6, 7)]
+LAGSTEP_CASES = [SYN_CASES[i] for i in (0, 1, 2, 3, 4, 5, 6, 7)] + [
+    (5, 2, 64, 20.0, 1.0, {}),     # a run shorter than one 8-step block, far lags present
+    (40, 3, 200, 30.0, 2.0, {}),   # several blocks, N not a multiple of the 128-wide tiles
+]
 
 
 @pytest.mark.gpu
@@ -123,6 +126,7 @@ HYB_CASES = [
     (16, 2, 40, (-1.0, 7.0), 3, False, 0.7),     # mid-anneal triangle, four taps per column
     (12, 2, 32, (0.0, 6.0), 3, False, 8.0),      # half-width 9: runtime tap count
     (80, 2, 700, (0.0, 55.0), 8, True, 0.0),     # gather forward (two history words), workspace ring
+    (24, 2, 300, (0.0, 20.0), 5, True, 0.0),     # split backward: 640 threads, an odd chunk count
 ]
 
 
@@ -188,8 +192,8 @@ def test_hybrid_fwd_bwd_matches_oracle(dev, case):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('case', HYB_CASES[:5], ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}{"bf16" if c[5] else ""}s{c[6]}'
-                                                    for c in HYB_CASES[:5]])
+@pytest.mark.parametrize('case', HYB_CASES[:5] + HYB_CASES[6:], ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}{"bf16" if c[5] else ""}s{c[6]}'
+                                                    for c in HYB_CASES[:5] + HYB_CASES[6:]])
 def test_hybrid_lagstep_matches_oracle(dev, case, monkeypatch):
     monkeypatch.setenv('DELREC_SYN_LAGSTEP', '1')
     test_hybrid_fwd_bwd_matches_oracle(dev, case)
@@ -198,7 +202,16 @@ def test_hybrid_lagstep_matches_oracle(dev, case, monkeypatch):
 @pytest.mark.gpu
 def test_hybrid_gather_path_matches_oracle(dev, monkeypatch):
     monkeypatch.setenv('DELREC_SYN_LAGSTEP', '0')
-    test_hybrid_fwd_bwd_matches_oracle(dev, HYB_CASES[-1])
+    test_hybrid_fwd_bwd_matches_oracle(dev, HYB_CASES[5])
+
+
+# the hybrid backward with one lane per source (the split form is the default for N <= 512)
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', [HYB_CASES[i] for i in (0, 2, 3, 6)],
+                         ids=[f'T{c[0]}B{c[1]}N{c[2]}' for c in [HYB_CASES[i] for i in (0, 2, 3, 6)]])
+def test_hybrid_unsplit_backward_matches_oracle(dev, case, monkeypatch):
+    monkeypatch.setenv('DELREC_SYN_BWD_SPLIT', '0')
+    test_hybrid_fwd_bwd_matches_oracle(dev, case)
 
 
 @pytest.mark.gpu
