@@ -15,6 +15,7 @@ SYN_CASES = [
     (16, 2, 48, 6.0, 0.8, {'sig_p': True}),
     (16, 2, 48, 6.0, 0.8, {'soft': True, 'triangle': True}),
     (16, 2, 48, 6.0, 0.8, {'decay_input': True}),
+    (18, 3, 40, 6.0, 0.5, {'drop': True, 'bias': True}),   # fixed-mask recurrent dropout
     (12, 2, 96, 4.0, 4.0, {}),                  # wide triangle
     (12, 2, 40, 6.0, 8.0, {}),                  # half-width 9: runtime tap count
     (70, 2, 700, 60.0, 1.0, {}),                # rings too large for LDS: gather forward, workspace ring
@@ -68,16 +69,18 @@ def test_synaptic_fwd_bwd_matches_oracle(dev, case):
     T, B, N, dmax, sigma, extra = case
     print(f'case {case}', flush=True)
     x, W, d, gy, bias, p = _syn_inputs(T, B, N, dmax, extra, seed=1)
+    drop = (torch.rand(B, N, generator=gen(7)) > 0.2).float() / 0.8 if extra.get('drop') else None
     v_reset = None if extra.get('soft') else 0.0
     surr = ('triangle', 1.0) if extra.get('triangle') else ('atan', 2.0)
     lif = lif_params(v_reset=v_reset, decay_input=extra.get('decay_input', False), surrogate=surr)
-    y_ref, u_ref, gref = oracle_synaptic(x, W, d, lif, sigma, gy, bias=bias, p=p, use_sig_p=p is not None)
+    y_ref, u_ref, gref = oracle_synaptic(x, W, d, lif, sigma, gy, bias=bias, p=p, use_sig_p=p is not None,
+                                         drop=drop)
 
     xg, Wg, dg = (t.to(dev).requires_grad_(True) for t in (x, W, d))
     bg = bias.to(dev).requires_grad_(True) if bias is not None else None
     pg = p.to(dev).requires_grad_(True) if p is not None else torch.zeros(N, device=dev)
     layer = _Layer(sigma, lif, use_sig_p=p is not None, p=pg if p is not None else None)
-    y = EventDrivenSyn.apply(xg, Wg, dg, pg, bg, None, layer)
+    y = EventDrivenSyn.apply(xg, Wg, dg, pg, bg, drop.to(dev) if drop is not None else None, layer)
     (y * gy.to(dev)).sum().backward()
     torch.cuda.synchronize()
     flip = first_flip(y.detach().cpu(), y_ref, u_ref, lif.v_threshold)
@@ -95,7 +98,7 @@ def test_synaptic_fwd_bwd_matches_oracle(dev, case):
 
 # the lag-stacked per-step GEMM scans (taken by default only where the rings do not fit
 # LDS, the last two cases above) forced at every size; the same oracle and tolerances
-LAGSTEP_CASES = [SYN_CASES[i] for i in (0, 1, 2, 3, 4, 5, 6, 7)] + [
+LAGSTEP_CASES = [SYN_CASES[i] for i in (0, 1, 2, 3, 4, 5, 6, 7, 8)] + [
     (5, 2, 64, 20.0, 1.0, {}),     # a run shorter than one 8-step block, far lags present
     (40, 3, 200, 30.0, 2.0, {}),   # several blocks, N not a multiple of the 128-wide tiles
 ]
