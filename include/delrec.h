@@ -187,7 +187,10 @@ typedef struct {
     float* dx;
 } delrec_lif_bwd_args;
 
-/* Workspace kinds for delrec_query_workspace; flags bit 0: weights are bf16. */
+/* Workspace kinds for delrec_query_workspace; flags bit 0: weights are bf16; synaptic
+ * kinds: bit 1: hybrid delays (d == NULL), bits 8..15: ceil(2 * s_max) on the float32 s_max
+ * the entry point receives (s_uniform for the hybrid), capped at 255 -- the most lags of
+ * non-zero weight per connection, which picks the scan form (and its workspace). */
 enum { DELREC_WS_AXONAL_FWD = 1, DELREC_WS_AXONAL_BWD = 2, DELREC_WS_SYN_FWD = 3,
        DELREC_WS_SYN_BWD = 4 };
 

@@ -320,12 +320,18 @@ LagStepDims lagstep_dims(int T, int B, int N, int L) {
     return q;
 }
 
-bool syn_lagstep(int T, int B, int N, int L) {
+// ceil(2 s_max): the most lags of non-zero weight a connection has (the flags' bits 8..15)
+int lag_taps(float smax) { return std::min(255, std::max(0, (int)std::ceil(2.0f * smax))); }
+
+// The lag-stacked form multiplies every lag of the window; it pays where a connection's
+// taps are a fair share of the window (measured: 46 lags at 10 taps, C4, beat the gathers
+// 7x), not for narrow triangles over long windows (the hybrid at sigma 0: 2 taps).
+bool syn_lagstep(int T, int B, int N, int L, int taps) {
     const char* e = getenv("DELREC_SYN_LAGSTEP");
     if (e && e[0] == '0') return false;
     if (!lagstep_dims(T, B, N, L).ok) return false;
     if (e && e[0] == '1') return true;
-    return !syn_layout(N, L, true).lds_ring;
+    return !syn_layout(N, L, true).lds_ring && L - 1 <= 12 * std::max(taps, 1);
 }
 
 template <class C>
@@ -340,8 +346,8 @@ void lagstep_ws(C& c, int T, int B, int N, int L, bool fwd) {
 }
 
 template <class C>
-void syn_fwd_ws(C& c, int T, int B, int N, int L, bool hybrid, bool bf16) {
-    if (syn_lagstep(T, B, N, L)) {
+void syn_fwd_ws(C& c, int T, int B, int N, int L, bool hybrid, bool bf16, int taps) {
+    if (syn_lagstep(T, B, N, L, taps)) {
         lagstep_ws(c, T, B, N, L, true);
         return;
     }
@@ -354,7 +360,7 @@ void syn_fwd_ws(C& c, int T, int B, int N, int L, bool hybrid, bool bf16) {
 }
 
 template <class C>
-void syn_bwd_ws(C& c, int T, int B, int N, int L) {
+void syn_bwd_ws(C& c, int T, int B, int N, int L, int taps) {
     // sized for the widest tap run, so the ring may always go to the workspace
     const SynBwdLayout lay = syn_bwd_layout(N, L, kSynMaxTaps);
     const LagPack q = lag_pack(T, B, N);
@@ -366,7 +372,7 @@ void syn_bwd_ws(C& c, int T, int B, int N, int L) {
     c.template take<uint4>(packed);                     // gr_lo
     c.template take<uint4>(packed);                     // shifted spikes
     c.template take<int>((size_t)4 * N + 64);           // lag range per column, meta
-    if (syn_lagstep(T, B, N, L)) {
+    if (syn_lagstep(T, B, N, L, taps)) {
         lagstep_ws(c, T, B, N, L, false);
         return;
     }
@@ -509,8 +515,8 @@ int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_
             axonal_bwd_ws(c, T, B, N, lay);
             break;
         }
-        case DELREC_WS_SYN_FWD: syn_fwd_ws(c, T, B, N, L, (flags & 2) != 0, bf16); break;
-        case DELREC_WS_SYN_BWD: syn_bwd_ws(c, T, B, N, L); break;
+        case DELREC_WS_SYN_FWD: syn_fwd_ws(c, T, B, N, L, (flags & 2) != 0, bf16, (flags >> 8) & 0xff); break;
+        case DELREC_WS_SYN_BWD: syn_bwd_ws(c, T, B, N, L, (flags >> 8) & 0xff); break;
         default: return DELREC_ERR_ARG;
     }
     *bytes = c.used;
@@ -711,7 +717,8 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     const SynLayout lay = syn_layout(a->N, a->L, true);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int N = a->N;
-    if (syn_lagstep(a->T, a->B, N, a->L)) return syn_fwd_lagstep(a, s);
+    if (syn_lagstep(a->T, a->B, N, a->L, lag_taps(a->s ? a->s_max : std::max(a->s_max, a->s_uniform))))
+        return syn_fwd_lagstep(a, s);
     const size_t nb = (size_t)((N + 15) / 16) * 16 * N;
     Carver cv(a->workspace, a->workspace_bytes);
     void* wt = a->w_bf16 ? (void*)cv.take<uint16_t>(nb) : (void*)cv.take<float>(nb);
@@ -796,7 +803,8 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     uint4* alo = cv.take<uint4>(packed);
     uint4* yb = cv.take<uint4>(packed);
     int* meta = cv.take<int>((size_t)4 * N + 64);
-    const bool lagstep = syn_lagstep(T, B, N, a->L);
+    const bool lagstep = syn_lagstep(T, B, N, a->L, lag_taps(hybrid ? a->s_uniform
+                                                                   : (a->s ? a->s_max : std::max(a->s_max, a->s_uniform))));
     void* wt = nullptr;
     void* dt = nullptr;
     float* gring = nullptr;

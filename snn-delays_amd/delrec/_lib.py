@@ -8,6 +8,7 @@ stream; scratch memory comes from torch's caching allocator, sized by
 """
 
 import ctypes
+import math
 import os
 from pathlib import Path
 
@@ -165,6 +166,13 @@ def make_lif(tau, v_threshold, v_reset, decay_input, detach_reset, surr_id, gamm
 
 
 _WS_SIZES = {}
+
+
+def lag_taps(s_max):
+    """ceil(2 s_max) on the float32 value the C ABI receives (the most lags of non-zero weight
+    per connection), for bits 8..15 of the synaptic workspace flags."""
+    s32 = ctypes.c_float(float(s_max)).value
+    return min(255, max(0, math.ceil(2.0 * s32)))
 
 
 def workspace_bytes(kind, T, B, N, L, flags):

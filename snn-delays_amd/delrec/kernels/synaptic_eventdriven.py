@@ -43,7 +43,10 @@ def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop,
     else:
         (d_max,), s_max = read_scalars(d_all.max()), s_uniform
     L = max(window_length_f64(d_max, s_max), 2)
-    flags = w_bf16 | (2 if d_eff is None else 0)
+    # the scan form follows the taps per connection: the entry point's smax (the largest
+    # per-column half-width, or the uniform one)
+    smax = float(s_max) if s_vec is not None else max(float(s_max), float(s_uniform))
+    flags = w_bf16 | (2 if d_eff is None else 0) | (_lib.lag_taps(smax) << 8)
     ws = _lib.workspace(_lib.WS_SYN_FWD, T, B, N, L, flags, dev)
     args = _lib.SynFwdArgs(
         T=T, B=B, N=N, L=L, x=_lib.ptr(xc), W=_lib.ptr(Wc), w_bf16=w_bf16, bias=_lib.ptr(bias),
@@ -66,7 +69,10 @@ def syn_backward(gy, u, y, bits, Wc, w_bf16, d_eff, base, offsets, s_vec, s_unif
     dd = torch.empty(N, N, device=dev, dtype=torch.float32) if need_d else None
     ds = torch.empty(N, device=dev, dtype=torch.float32) if need_s else None
     db = torch.empty(N, device=dev, dtype=torch.float32) if need_b else None
-    ws = _lib.workspace(_lib.WS_SYN_BWD, T, B, N, L, w_bf16, dev)
+    smax = float(s_uniform) if d_eff is None else (float(s_max) if s_vec is not None
+                                                   else max(float(s_max), float(s_uniform)))
+    flags = w_bf16 | (2 if d_eff is None else 0) | (_lib.lag_taps(smax) << 8)
+    ws = _lib.workspace(_lib.WS_SYN_BWD, T, B, N, L, flags, dev)
     args = _lib.SynBwdArgs(
         T=T, B=B, N=N, L=L, gy=_lib.ptr(gy), u=_lib.ptr(u), y=_lib.ptr(y), bits=_lib.ptr(bits),
         W=_lib.ptr(Wc), w_bf16=w_bf16, d=_lib.ptr(d_eff), base=_lib.ptr(base),

@@ -93,3 +93,26 @@ def test_torch_extension_loads_and_exposes_the_axonal_function():
     doc = ext.axonal_common.__doc__
     for arg in ('x', 'W', 'd', 'bias', 'drop', 'sigma', 'tau', 'vth', 'surrogate', 'gamma', 'alpha', 'detach'):
         assert f'{arg}:' in doc
+
+
+def test_synaptic_scan_form_follows_the_taps_per_connection():
+    """Rings too large for LDS take the lag-stacked GEMM scans only where a connection's
+    taps are a fair share of the window (flags bits 8..15 = ceil(2 s_max)): a synaptic
+    layer at sigma 4 (10 taps over 46 lags) does, a hybrid at sigma 0 (2 taps over 65 lags)
+    keeps the per-connection gathers; the lag-stacked workspace holds the (L-1) N^2 lag
+    weights and is far larger."""
+    from delrec import _lib
+    lib = _lib.load()
+    T, B, N = 32, 8, 1024
+
+    def size(kind, L, flags, taps):
+        n = ctypes.c_size_t(0)
+        assert lib.delrec_query_workspace(kind, T, B, N, L, flags | (taps << 8), ctypes.byref(n)) == 0
+        return n.value
+
+    assert _lib.lag_taps(5.0) == 10 and _lib.lag_taps(1.0) == 2 and _lib.lag_taps(1.25) == 3
+    planes = 2 * 46 * N * N * 2                       # two bf16 planes of M_l, 46 lags
+    for kind in (_lib.WS_SYN_FWD, _lib.WS_SYN_BWD):
+        wide = size(kind, 47, 0, _lib.lag_taps(5.0))         # synaptic, sigma 4
+        narrow = size(kind, 66, 2, _lib.lag_taps(1.0))       # hybrid, sigma 0
+        assert wide >= planes > narrow
