@@ -49,7 +49,9 @@ typedef enum {
     DELREC_ERR_WORKSPACE = 3,    /* workspace missing or smaller than queried          */
     DELREC_ERR_LAUNCH = 4,       /* a kernel launch failed (hipGetLastError)           */
     DELREC_ERR_WINDOW = 5,       /* window length L out of range for the on-chip ring  */
-    DELREC_ERR_DEVICE = 6        /* device query failed / not a gfx950 device          */
+    DELREC_ERR_DEVICE = 6,       /* device query failed / not a gfx950 device          */
+    DELREC_ERR_PENDING = 7,      /* delrec_max_take: the value did not arrive in time  */
+    DELREC_ERR_STALE = 8         /* delrec_max_take: the slot was reused by later posts */
 } delrec_status;
 
 /* Neuron constants (spikingjelly LIFNode semantics; reference lif.py:25-56). */
@@ -94,6 +96,9 @@ typedef struct {
     uint32_t* bits;              /* out (B, ceil(T/32), N) spike bitmask                */
     void* workspace;             /* N > 256: transposed W                               */
     size_t workspace_bytes;
+    uint32_t* dmax_ticket;       /* NULL, or out: the call also posts max d as by       */
+                                 /* delrec_max_post (from inside the scan kernel where  */
+                                 /* it can) and returns the ticket for delrec_max_take  */
 } delrec_axonal_fwd_args;
 
 /* Backward gfut modes (reference APPROX constexpr, recdel_base.py:216-233). */
@@ -205,6 +210,19 @@ int delrec_lif_bwd(const delrec_lif_bwd_args* a, void* stream);
  * with s = 1 + sigma: the reference's closed-form delay gradient test hook. */
 int delrec_delay_grad(const float* C, const float* W, const float* d, float sigma,
                       int32_t N, int32_t Lm, float* dd, void* stream);
+
+/* Host read of a device maximum without waiting for the stream. The reference sizes the
+ * delay window from max d on the host, L = ceil(1 + max d + max s) + 1 read with .item()
+ * (triton_kernels/delays.py:26, from recdel_base.py:381), which waits for all work queued
+ * before it; here only the backward needs L. delrec_max_post queues one small kernel on
+ * `stream` that writes max(x[0 .. n)) (NaN when an element is NaN) with a ticket into one
+ * of DELREC_MAX_SLOTS slots of coherent pinned host memory, as a single 8-byte store, and
+ * returns the ticket. delrec_max_take waits for that ticket's slot: DELREC_OK with *out
+ * set; DELREC_ERR_STALE when later posts have reused the slot (read the maximum again);
+ * DELREC_ERR_PENDING when it has not arrived within timeout_ms. Thread-safe. */
+enum { DELREC_MAX_SLOTS = 256 };
+int delrec_max_post(const float* x, int32_t n, uint32_t* ticket, void* stream);
+int delrec_max_take(uint32_t ticket, float* out, int32_t timeout_ms);
 
 /* Bytes of scratch the given entry point needs for these sizes and flags. */
 int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_t L,

@@ -6,9 +6,13 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <initializer_list>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <thread>
 #include <vector>
 
 #include "kernels.h"
@@ -150,37 +154,6 @@ bool axonal_layout(int N, int L, AxLayout& o) {
     return true;
 }
 
-// A second stream per device (default priority) for work that can run beside the
-// caller's stream inside one entry point: forked after the caller's queued work and
-// joined back before the entry point returns. Kept per host thread.
-struct SideStream {
-    hipStream_t stream = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
-    bool ok = false;
-};
-
-SideStream* side_stream(hipStream_t main) {
-    static thread_local SideStream per_dev[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    SideStream& ss = per_dev[dev];
-    if (!ss.ok) {
-        if (hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
-        if (hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess)
-            return nullptr;
-        ss.ok = true;
-    }
-    if (hipEventRecord(ss.fork, main) != hipSuccess || hipStreamWaitEvent(ss.stream, ss.fork, 0) != hipSuccess)
-        return nullptr;
-    return &ss;
-}
-
-void join_side_stream(SideStream* ss, hipStream_t main) {
-    hipEventRecord(ss->join, ss->stream);
-    hipStreamWaitEvent(main, ss->join, 0);
-}
-
 // true unless the environment variable is set to "0" (a kernel variant kept for comparison)
 bool getenv_flag_off(const char* name) {
     const char* e = getenv(name);
@@ -198,12 +171,12 @@ bool axonal_fwd_wave_on() {
     return on == 1;
 }
 
-// split-K count of the dW GEMM: about one 64x64-tile workgroup per CU, chunks >= 256 rows
-// k splits of the dW GEMM: about two 128x128-tile workgroups per CU (one hides the other's
-// load latency), chunks of >= 128 rows
+// k splits of the dW GEMM: about one 128x128-tile workgroup per CU (the delay-gradient
+// blocks launched beside them take the other slots; twice as many splits doubles the
+// partials' HBM traffic for no gain), chunks of >= 128 rows
 int dw_splits(int T, int B, int N) {
     const int tiles = (N + 127) / 128;
-    const int want = (2 * num_cus() + tiles * tiles - 1) / (tiles * tiles);
+    const int want = (num_cus() + tiles * tiles - 1) / (tiles * tiles);
     return std::max(1, std::min(want, std::max(1, T * B / 128)));
 }
 
@@ -465,6 +438,43 @@ void scan_release() {
     g_scan.used = 0;
 }
 
+// Ring of max readbacks: DELREC_MAX_SLOTS 8-byte slots of coherent pinned host memory, each
+// (ticket, value bits) written by one store of max_to_host_kernel. Ticket 0 marks an empty
+// slot; tickets count up from 1 (wrapping past 0).
+struct MaxRing {
+    unsigned long long* host = nullptr;
+    std::atomic<uint32_t> next{1};
+    bool ok = false;
+};
+
+MaxRing& max_ring() {
+    static MaxRing r;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        void* p = nullptr;
+        const size_t bytes = (size_t)DELREC_MAX_SLOTS * sizeof(unsigned long long);
+        if (hipHostMalloc(&p, bytes, hipHostMallocCoherent | hipHostMallocMapped | hipHostMallocPortable) ==
+            hipSuccess) {
+            memset(p, 0, bytes);
+            r.host = static_cast<unsigned long long*>(p);
+            r.ok = true;
+        }
+    });
+    return r;
+}
+
+// a fresh ticket and the device address of its slot
+int max_slot(uint32_t& t, unsigned long long*& dslot) {
+    MaxRing& r = max_ring();
+    if (!r.ok) return DELREC_ERR_DEVICE;
+    t = r.next.fetch_add(1);
+    if (t == 0) t = r.next.fetch_add(1);
+    void* dbase = nullptr;
+    if (hipHostGetDevicePointer(&dbase, r.host, 0) != hipSuccess || !dbase) return DELREC_ERR_DEVICE;
+    dslot = static_cast<unsigned long long*>(dbase) + t % DELREC_MAX_SLOTS;
+    return DELREC_OK;
+}
+
 }  // namespace
 
 void delrec::ensure_lds(const void* fn, size_t bytes) {
@@ -493,6 +503,8 @@ const char* delrec_strerror(int status) {
         case DELREC_ERR_LAUNCH: return "kernel launch failed";
         case DELREC_ERR_WINDOW: return "delay window too long for this layer size";
         case DELREC_ERR_DEVICE: return "device query failed";
+        case DELREC_ERR_PENDING: return "device value not written within the time limit";
+        case DELREC_ERR_STALE: return "readback slot reused by later posts";
         default: return "unknown status";
     }
 }
@@ -560,6 +572,20 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
         if (a->w_bf16) transpose<uint16_t>(a->W, wt, a->N, s); else transpose<float>(a->W, wt, a->N, s);
         p.Wt = wt;
     }
+    // max d for the caller's host: written by the straight-line scan's first workgroup, else
+    // by a small kernel ahead of the scan
+    const bool fast = lay.res && axonal_fwd_wave_on() && axonal_fwd_common(a) && lay.hw <= 4;
+    uint32_t mx_t = 0;
+    if (a->dmax_ticket) {
+        unsigned long long* slot = nullptr;
+        if (int st = max_slot(mx_t, slot)) return st;
+        if (fast) {
+            p.mx_slot = slot;
+            p.mx_ticket = mx_t;
+        } else {
+            launch_max_to_host(a->d, a->N, mx_t, slot, s);
+        }
+    }
     const bool timed = scan_begin(DELREC_WS_AXONAL_FWD, s);
     bool ok;
     if (lay.res && axonal_fwd_wave_on()) {
@@ -570,7 +596,7 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
         // history length, one or four 64-step words, from d)
         const float span = ceilf(2.0f * a->s_uniform);
         const int kf = span <= 2.0f ? 2 : (span <= 4.0f ? 4 : 8);
-        if (axonal_fwd_common(a) && lay.hw <= 4) {
+        if (fast) {
             ok = launch_axonal_fwd_wave_fast(p, ri, kf, nw, a->B, s);
         } else {
             const size_t lds_w = (size_t)2 * nw * 64 * ri * sizeof(float);
@@ -582,6 +608,7 @@ int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {
     }
     scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;
+    if (a->dmax_ticket) *a->dmax_ticket = mx_t;
     return finish_launch();
 }
 
@@ -639,23 +666,30 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();
     if (st) return st;
-    // dW = sum_{t,b} gr (x) z on a side stream, beside the delay-gradient pass and the
-    // batch reductions (both only read what the scan wrote); the caller's stream waits for it
-    SideStream* side = a->dW ? side_stream(s) : nullptr;
+    // dW = sum_{t,b} gr (x) z beside the delay-gradient pass (the tiled scan leaves db
+    // partials in part[0], the segment pass adds dd / ds in part[1..2]; the streamed scan
+    // writes all three), then the split-K sums beside the batch reductions
+    const bool delays = lay.res && (a->dd || a->ds);
+    AxTail q{};
+    q.nbx = (N + 63) / 64;
+    q.ndelay = delays ? q.nbx * B : 0;
     if (a->dW) {
-        hipStream_t g = side ? side->stream : s;
-        launch_dw_gemm(need_gr ? grbuf : a->dx, a->z, T * B, N, ks, gemm_part, g);
-        launch_sum_partials(gemm_part, ks, (size_t)N * N, a->dW, g);
+        q.A = need_gr ? grbuf : a->dx;
+        q.Bz = a->z;
+        q.K = T * B;
+        q.ks = ks;
+        q.tiles = (N + 127) / 128;
+        q.kchunk = ((q.K + ks - 1) / ks + 31) / 32 * 32;   // whole 32-row stages
+        q.gpart = gemm_part;
+        q.dW = a->dW;
+        q.ndw = q.tiles * q.tiles * ks;
+        q.nsum = (int)(((size_t)N * N + 255) / 256);
     }
-    if (lay.res) {
-        // the tiled scan leaves db partials (part[0]); the segment pass adds dd / ds (part[1..2])
-        const bool delays = a->dd || a->ds;
-        if (delays) launch_axonal_delay_grad(p, s);
-        launch_reduce_rows(part, B, N, a->db, delays ? a->dd : nullptr, delays ? a->ds : nullptr, s);
-    } else {
-        launch_reduce_rows(part, B, N, a->db, a->dd, a->ds, s);
-    }
-    if (side) join_side_stream(side, s);
+    q.o0 = a->db;
+    q.o1 = lay.res && !delays ? nullptr : a->dd;
+    q.o2 = lay.res && !delays ? nullptr : a->ds;
+    launch_axonal_bwd_tail(p, q, s);
+    launch_axonal_bwd_sums(q, part, B, N, s);
     return finish_launch();
 }
 
@@ -959,6 +993,40 @@ int delrec_delay_grad(const float* C, const float* W, const float* d, float sigm
     if (!C || !W || !d || !dd || N <= 0 || Lm < 1 || !(sigma >= 0.0f)) return DELREC_ERR_ARG;
     launch_delay_grad(C, W, d, sigma, N, Lm, dd, static_cast<hipStream_t>(stream));
     return finish_launch();
+}
+
+int delrec_max_post(const float* x, int32_t n, uint32_t* ticket, void* stream) {
+    if (!x || n <= 0 || !ticket) return DELREC_ERR_ARG;
+    uint32_t t = 0;
+    unsigned long long* slot = nullptr;
+    if (int st = max_slot(t, slot)) return st;
+    launch_max_to_host(x, n, t, slot, static_cast<hipStream_t>(stream));
+    *ticket = t;
+    return finish_launch();
+}
+
+int delrec_max_take(uint32_t ticket, float* out, int32_t timeout_ms) {
+    if (!out || ticket == 0) return DELREC_ERR_ARG;
+    MaxRing& r = max_ring();
+    if (!r.ok) return DELREC_ERR_DEVICE;
+    const unsigned long long* slot = r.host + ticket % DELREC_MAX_SLOTS;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (uint64_t spin = 1;; ++spin) {
+        const unsigned long long v = __atomic_load_n(slot, __ATOMIC_ACQUIRE);
+        const uint32_t t = (uint32_t)v;
+        if (t == ticket) {
+            const uint32_t bits = (uint32_t)(v >> 32);
+            memcpy(out, &bits, sizeof(bits));
+            return DELREC_OK;
+        }
+        if (t != 0 && (int32_t)(t - ticket) > 0) return DELREC_ERR_STALE;   // a later post's value
+        if ((spin & 1023) == 0) {
+            const auto ms = std::chrono::duration_cast<std::chrono::milliseconds>(
+                                std::chrono::steady_clock::now() - t0).count();
+            if (ms >= timeout_ms) return DELREC_ERR_PENDING;
+            if (ms >= 1) std::this_thread::yield();
+        }
+    }
 }
 
 int delrec_scan_timing(int32_t capacity) {

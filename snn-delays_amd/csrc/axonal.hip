@@ -13,6 +13,7 @@
 // autograd through build_mask (:327-342, :421-435) folded into per-neuron accumulators.
 #include "common.h"
 #include "kernels.h"
+#include "dw_gemm.h"
 
 namespace delrec {
 
@@ -996,10 +997,13 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
 }
 
 // Picks the history length from d itself (block-uniform): one 64-step word when every
-// neuron's lags of non-zero weight fit, else four words (256 lags).
+// neuron's lags of non-zero weight fit, else four words (256 lags). When the caller asked
+// for max d on the host, workgroup 0 first writes it into the readback slot (the store's
+// trip to host memory then overlaps the scan).
 template <int RI, int KF>
 __global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
     extern __shared__ float smem[];
+    if (p.mx_slot && blockIdx.x == 0) block_max_to_host(p.d, p.N, p.mx_ticket, p.mx_slot);
     const int l = threadIdx.x & 63, i = 32 * (threadIdx.x >> 6) + l;
     bool longer = false;
     if (l < 32 && i < p.N) {
@@ -1188,14 +1192,14 @@ constexpr int kDelayY = 4;
 
 __host__ __device__ int axonal_delay_segments(int T) { return (T + kDelaySeg - 1) / kDelaySeg; }
 
+// Block (bx, b): sources 64 bx .. 64 bx + 63 of batch row b; thread (tx, ty) of 64 x kDelayY.
 template <int HW>
-__global__ void __launch_bounds__(64 * kDelayY) axonal_delay_grad_kernel(AxBwd p) {
-    __shared__ float red[2][kDelayY][64];
+__device__ __forceinline__ void axonal_delay_grad_block(const AxBwd& p, int bx, int b, int tx, int ty,
+                                                        float (&red)[2][kDelayY][64]) {
     const int N = p.N, T = p.T, B = p.B;
     const size_t BN = (size_t)B * N;
     const int S = axonal_delay_segments(T);
-    const int b = blockIdx.y;
-    const int jr = blockIdx.x * 64 + threadIdx.x;
+    const int jr = bx * 64 + tx;
     const bool act = jr < N;
     const int j = act ? jr : 0;
     const size_t rem = (size_t)b * N + j;
@@ -1216,7 +1220,7 @@ __global__ void __launch_bounds__(64 * kDelayY) axonal_delay_grad_kernel(AxBwd p
     const uint32_t* col = p.bits + (size_t)b * TW * N + j;
 
     float dd = 0.0f, ds = 0.0f;
-    for (int seg = threadIdx.y; seg < S; seg += kDelayY) {
+    for (int seg = ty; seg < S; seg += kDelayY) {
         const int t0 = seg * kDelaySeg;
         float gzq[kDelaySeg];
 #pragma unroll
@@ -1263,52 +1267,104 @@ __global__ void __launch_bounds__(64 * kDelayY) axonal_delay_grad_kernel(AxBwd p
         dd += soft ? dds / s2 : dds;
         ds += dss;
     }
-    red[0][threadIdx.y][threadIdx.x] = dd;
-    red[1][threadIdx.y][threadIdx.x] = ds;
+    red[0][ty][tx] = dd;
+    red[1][ty][tx] = ds;
     __syncthreads();
-    if (threadIdx.y == 0 && act) {
-        float a0 = red[0][0][threadIdx.x], a1 = red[1][0][threadIdx.x];
+    if (ty == 0 && act) {
+        float a0 = red[0][0][tx], a1 = red[1][0][tx];
 #pragma unroll
         for (int y = 1; y < kDelayY; ++y) {
-            a0 += red[0][y][threadIdx.x];
-            a1 += red[1][y][threadIdx.x];
+            a0 += red[0][y][tx];
+            a1 += red[1][y][tx];
         }
         p.part[(size_t)1 * BN + rem] = a0;
         p.part[(size_t)2 * BN + rem] = a1;
     }
 }
 
-void launch_axonal_delay_grad(const AxBwd& p, hipStream_t stream) {
-    const dim3 grid((p.N + 63) / 64, p.B), block(64, kDelayY);
-    const int lags = std::max(p.L - 1, 1);
-    if (lags <= 64)
-        hipLaunchKernelGGL(axonal_delay_grad_kernel<1>, grid, block, 0, stream, p);
-    else if (lags <= 128)
-        hipLaunchKernelGGL(axonal_delay_grad_kernel<2>, grid, block, 0, stream, p);
-    else
-        hipLaunchKernelGGL(axonal_delay_grad_kernel<4>, grid, block, 0, stream, p);
+// Sum the per-row partials over the batch: out_k[j] = sum_b part[k][b][j]. Block (bx, kk) of
+// threads (tx, ty) of CW x 16: CW consecutive neurons x 16 batch stripes, reduced through
+// LDS in stripe order (the same sums for every CW).
+template <int CW>
+__device__ __forceinline__ void reduce_rows_block(const float* part, int B, int N, float* o0, float* o1,
+                                                  float* o2, int bx, int kk, int tx, int ty,
+                                                  float (&red)[16][CW + 1]) {
+    float* out = kk == 0 ? o0 : (kk == 1 ? o1 : o2);
+    if (!out) return;   // uniform over the block
+    const int j = bx * CW + tx;
+    const float* src = part + (size_t)kk * B * N;
+    float acc = 0.0f;
+    if (j < N) {
+#pragma unroll 4
+        for (int b = ty; b < B; b += 16) acc += src[(size_t)b * N + j];
+    }
+    red[ty][tx] = acc;
+    __syncthreads();
+    if (ty == 0 && j < N) {
+        float t = 0.0f;
+        for (int r = 0; r < 16; ++r) t += red[r][tx];
+        out[j] = t;
+    }
 }
 
-// Sum the per-row partials over the batch: out_k[j] = sum_b part[k][b][j]. Block (64, 16):
-// 64 consecutive neurons x 16 batch stripes, reduced through LDS.
 __global__ void __launch_bounds__(1024) reduce_rows_kernel(const float* part, int B, int N,
                                                            float* o0, float* o1, float* o2) {
     __shared__ float red[16][65];
-    const int kk = blockIdx.y;
-    float* out = kk == 0 ? o0 : (kk == 1 ? o1 : o2);
-    if (!out) return;
-    const int j = blockIdx.x * 64 + threadIdx.x;
-    const float* src = part + (size_t)kk * B * N;
-    float acc = 0.0f;
-    if (j < N)
-        for (int b = threadIdx.y; b < B; b += 16) acc += src[(size_t)b * N + j];
-    red[threadIdx.y][threadIdx.x] = acc;
-    __syncthreads();
-    if (threadIdx.y == 0 && j < N) {
-        float t = 0.0f;
-        for (int r = 0; r < 16; ++r) t += red[r][threadIdx.x];
-        out[j] = t;
+    reduce_rows_block<64>(part, B, N, o0, o1, o2, blockIdx.x, blockIdx.y, threadIdx.x, threadIdx.y, red);
+}
+
+// The reductions after the axonal backward scan, as two launches on the caller's stream (no
+// second stream: its fork and join cost more than the overlap they buy):
+//   tail: blocks [0, ndw) the dW GEMM tiles (tile (ti, tj) of k chunk kz at block
+//         (kz * tiles + tj) * tiles + ti), then the delay / half-width gradient rows;
+//   sums: blocks [0, nsum) the dW split-K sums, then the batch reductions of db, dd, ds
+//         (16 neurons per block).
+// Both job kinds of a launch only read what earlier launches wrote, so they run side by
+// side; the longer dW blocks go first so that all of them start in the first round.
+template <int HW>
+__global__ void __launch_bounds__(kDwThreads, 3) axonal_bwd_tail_kernel(AxBwd p, AxTail q) {
+    __shared__ DwStage sm;   // 32 KiB: one dW stage, or the delay blocks' 2 KiB of partials
+    int bid = blockIdx.x;
+    if (bid < q.ndw) {
+        const int tt = q.tiles * q.tiles;
+        const int kz = bid / tt, r = bid - kz * tt;
+        dw_gemm_tile(q.A, q.Bz, q.K, p.N, q.kchunk, q.gpart, r % q.tiles, r / q.tiles, kz, sm);
+        return;
     }
+    bid -= q.ndw;
+    axonal_delay_grad_block<HW>(p, bid % q.nbx, bid / q.nbx, threadIdx.x & 63, threadIdx.x >> 6,
+                                *reinterpret_cast<float(*)[2][kDelayY][64]>(&sm));
+}
+
+__global__ void __launch_bounds__(kDwThreads) axonal_bwd_sums_kernel(AxTail q, const float* part, int B,
+                                                                     int N) {
+    __shared__ float4 sm[4][64];   // 4 KiB: the partial sums' wave totals, or the row stripes
+    int bid = blockIdx.x;
+    if (bid < q.nsum) {
+        sum_partials_block(q.gpart, q.ks, (size_t)N * N, q.dW, bid, sm);
+        return;
+    }
+    bid -= q.nsum;
+    const int nb16 = (N + 15) / 16;
+    reduce_rows_block<16>(part, B, N, q.o0, q.o1, q.o2, bid % nb16, bid / nb16, threadIdx.x & 15,
+                          threadIdx.x >> 4, *reinterpret_cast<float(*)[16][17]>(&sm));
+}
+
+void launch_axonal_bwd_tail(const AxBwd& p, const AxTail& q, hipStream_t stream) {
+    const int blocks = q.ndelay + q.ndw;
+    if (blocks <= 0) return;
+    const int lags = std::max(p.L - 1, 1);
+    if (lags <= 64)
+        hipLaunchKernelGGL(axonal_bwd_tail_kernel<1>, dim3(blocks), dim3(kDwThreads), 0, stream, p, q);
+    else if (lags <= 128)
+        hipLaunchKernelGGL(axonal_bwd_tail_kernel<2>, dim3(blocks), dim3(kDwThreads), 0, stream, p, q);
+    else
+        hipLaunchKernelGGL(axonal_bwd_tail_kernel<4>, dim3(blocks), dim3(kDwThreads), 0, stream, p, q);
+}
+
+void launch_axonal_bwd_sums(const AxTail& q, const float* part, int B, int N, hipStream_t stream) {
+    const int blocks = q.nsum + 3 * ((N + 15) / 16);
+    hipLaunchKernelGGL(axonal_bwd_sums_kernel, dim3(blocks), dim3(kDwThreads), 0, stream, q, part, B, N);
 }
 
 // ---------------------------------------------------------------------------------------

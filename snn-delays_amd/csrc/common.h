@@ -255,4 +255,32 @@ __device__ __forceinline__ float group_sum_t(float v) {
 
 constexpr int kMaxTaps = 8;   // register-resident tap weights per neuron (fast path)
 
+// max(x[0 .. n)) over the workgroup (NaN when an element is NaN, as torch.max), written by
+// thread 0 with `ticket` into a slot of host memory, (ticket | value bits << 32), as one
+// 8-byte system-scope store: a host reader sees either the old pair or the new one. Every
+// thread of the workgroup (a multiple of 64 threads, at most 1024) calls it: it holds a
+// barrier.
+__device__ __forceinline__ void block_max_to_host(const float* x, int n, uint32_t ticket,
+                                                  unsigned long long* slot) {
+    __shared__ float wmax[16];
+    float m = -INFINITY;
+    int nan = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        nan |= v != v;
+        m = fmaxf(m, v);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    nan = __syncthreads_or(nan);
+    if (threadIdx.x == 0) {
+        float r = wmax[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = fmaxf(r, wmax[w]);
+        if (nan) r = __builtin_nanf("");
+        const unsigned long long v = (unsigned long long)ticket | ((unsigned long long)__float_as_uint(r) << 32);
+        __hip_atomic_store(slot, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 }  // namespace delrec

@@ -26,6 +26,8 @@ struct AxFwd {
     float* rec;
     float* z;
     uint32_t* bits;
+    unsigned long long* mx_slot;   // NULL, or the readback slot workgroup 0 writes max d into
+    uint32_t mx_ticket;
 };
 
 struct AxBwd {
@@ -219,17 +221,33 @@ bool launch_axonal_fwd_wave_fast(const AxFwd& p, int ri, int kf, int nw, int gri
 // the ring holds R + kf - 1 slots
 bool launch_axonal_bwd_tiled_fast(const AxBwd& p, int ri, int nj, int cj, int kf, int grid, int block,
                                   size_t lds, hipStream_t stream);
-// dd / ds per-row partials (part[1], part[2]) from the tiled scan's gz and the spike bits
 __host__ __device__ int axonal_delay_segments(int T);
-void launch_axonal_delay_grad(const AxBwd& p, hipStream_t stream);
 void launch_reduce_rows(const float* part, int B, int N, float* o0, float* o1, float* o2,
                         hipStream_t stream);
 
-// dW[i,j] = sum_k A[k,i] * Bm[k,j] over K rows (split K into ks chunks of partials).
-void launch_dw_gemm(const float* A, const float* Bm, int K, int N, int ks, float* partial,
-                    hipStream_t stream);
-// out[idx] = sum_k partial[k][idx] for idx < count
-void launch_sum_partials(const float* partial, int ks, size_t count, float* out, hipStream_t stream);
+// The reductions after the axonal backward scan, in two launches:
+//   launch_axonal_bwd_tail: the dd / ds per-row partials (part[1], part[2]) from the tiled
+//     scan's gz and the spike bits (ndelay blocks), beside the dW GEMM
+//     dW[i,j] = sum_k A[k,i] * Bz[k,j] over K rows, split into ks chunks of partials (ndw
+//     blocks);
+//   launch_axonal_bwd_sums: dW = the sum of those partials (nsum blocks), beside the batch
+//     sums of the per-row partials into o0, o1, o2 (3 * ceil(N / 16) blocks; a null output is
+//     skipped).
+struct AxTail {
+    const float* A;     // (K, N): dL/drec
+    const float* Bz;    // (K, N): z
+    int K, kchunk, ks, tiles;
+    float* gpart;       // [ks][N][N]
+    float* dW;
+    int ndw, ndelay, nsum, nbx;
+    float* o0;
+    float* o1;
+    float* o2;
+};
+void launch_axonal_bwd_tail(const AxBwd& p, const AxTail& q, hipStream_t stream);
+// *slot = ticket | max(x[0 .. n)) bits << 32, one system-scope 8-byte store (host memory)
+void launch_max_to_host(const float* x, int n, uint32_t ticket, unsigned long long* slot, hipStream_t stream);
+void launch_axonal_bwd_sums(const AxTail& q, const float* part, int B, int N, hipStream_t stream);
 
 void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream);
 // wpk[o*N + i] = W[i*N + o] (bf16 bits) << 16 | uint8(off[i*N + o])

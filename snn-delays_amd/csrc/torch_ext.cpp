@@ -7,18 +7,17 @@
 // the regime the straight-line kernels serve: soft triangle taps of a uniform half-width,
 // decay charge, hard reset to 0, no learned spread, no STE / rounded taps, N <= 256.
 //
-// The forward does not read the window length: it copies max d into a slot of a small
-// pinned ring (with an event) ahead of the scan and calls delrec_axonal_fwd with L = 0;
-// the backward waits for that copy only. A slot carries a generation number, so a slot
-// taken over by later forwards before this backward runs is detected and max d is read
-// again (synchronously).
+// The forward does not read the window length: delrec_axonal_fwd runs with L = 0 and writes
+// max d into a slot of pinned host memory from inside the scan (no copy, no event); the
+// backward takes that slot by its ticket. A slot reused by later forwards before
+// this backward runs, or a value that does not arrive, makes the backward read max d again
+// (synchronously).
 #include <torch/extension.h>
 
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime.h>
 
 #include <cmath>
-#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -36,61 +35,11 @@ void check(int status, const char* fn) {
                                  delrec_strerror(status) + ")");
 }
 
-// ---- pinned ring of max-d readbacks -----------------------------------------------------
-constexpr int kSlots = 64;
-constexpr int kDevices = 64;
-
-struct Ring {
-    float* host = nullptr;          // kSlots floats, pinned
-    hipEvent_t ev[kSlots] = {};
-    uint64_t gen[kSlots] = {};
-    uint64_t next = 1;
-    bool ok = false;
-};
-
-std::mutex g_mutex;
-Ring g_rings[kDevices];
-
-Ring& ring_for(int dev) {
-    Ring& r = g_rings[dev];
-    if (!r.ok) {
-        if (hipHostMalloc((void**)&r.host, kSlots * sizeof(float), hipHostMallocDefault) != hipSuccess)
-            throw std::runtime_error("delrec_torch: pinned allocation failed");
-        for (int k = 0; k < kSlots; ++k)
-            if (hipEventCreateWithFlags(&r.ev[k], hipEventDisableTiming) != hipSuccess)
-                throw std::runtime_error("delrec_torch: event creation failed");
-        r.ok = true;
-    }
-    return r;
-}
-
-// copy the device scalar `v` (fp32) into a slot on `stream`; returns (slot, generation)
-std::pair<int64_t, int64_t> post_scalar(const Tensor& v, hipStream_t stream) {
-    std::lock_guard<std::mutex> lock(g_mutex);
-    const int dev = v.get_device();
-    Ring& r = ring_for(dev);
-    const uint64_t g = r.next++;
-    const int k = (int)(g % kSlots);
-    if (hipMemcpyAsync(r.host + k, v.data_ptr(), sizeof(float), hipMemcpyDeviceToHost, stream) != hipSuccess ||
-        hipEventRecord(r.ev[k], stream) != hipSuccess)
-        throw std::runtime_error("delrec_torch: max-d readback failed");
-    r.gen[k] = g;
-    return {k, (int64_t)g};
-}
-
-// the posted value, or a fresh synchronous read of `fallback` when the slot was reused
-float take_scalar(int dev, int64_t k, int64_t g, const Tensor& fallback) {
-    {
-        std::unique_lock<std::mutex> lock(g_mutex);
-        Ring& r = g_rings[dev];
-        if (r.ok && r.gen[k] == (uint64_t)g) {
-            hipEvent_t ev = r.ev[k];
-            lock.unlock();
-            if (hipEventSynchronize(ev) != hipSuccess) throw std::runtime_error("delrec_torch: event wait failed");
-            lock.lock();
-            if (r.gen[k] == (uint64_t)g) return r.host[k];
-        }
-    }
+// max d posted by the forward (its ticket for delrec_max_take), or a fresh synchronous read of
+// `fallback` when the slot was reused or the value did not arrive
+float take_max(int64_t ticket, const Tensor& fallback) {
+    float v = 0.0f;
+    if (delrec_max_take((uint32_t)ticket, &v, 10000) == DELREC_OK) return v;
     return fallback.max().item<float>();
 }
 
@@ -141,8 +90,6 @@ struct AxonalCommon : public torch::autograd::Function<AxonalCommon> {
         Tensor bits = at::empty({B, (T + 31) / 32, N}, x.options().dtype(at::kInt));
         hipStream_t stream = c10::hip::getCurrentHIPStream(x.get_device()).stream();
 
-        Tensor dmax = dc.max();
-        const auto slot = post_scalar(dmax, stream);
 
         delrec_axonal_fwd_args a{};
         a.T = T; a.B = B; a.N = N; a.L = 0;
@@ -153,14 +100,15 @@ struct AxonalCommon : public torch::autograd::Function<AxonalCommon> {
         a.y = (float*)y.data_ptr(); a.u = (float*)u.data_ptr(); a.rec = nullptr; a.z = (float*)z.data_ptr();
         a.bits = (uint32_t*)bits.data_ptr();
         a.workspace = nullptr; a.workspace_bytes = 0;
+        uint32_t ticket = 0;
+        a.dmax_ticket = &ticket;
         check(delrec_axonal_fwd(&a, stream), "delrec_axonal_fwd");
 
         ctx->save_for_backward({u, z, bits, Wc, dc, bc, mc});
         ctx->saved_data["T"] = (int64_t)T;
         ctx->saved_data["B"] = (int64_t)B;
         ctx->saved_data["N"] = (int64_t)N;
-        ctx->saved_data["slot"] = slot.first;
-        ctx->saved_data["gen"] = slot.second;
+        ctx->saved_data["ticket"] = (int64_t)ticket;
         ctx->saved_data["sigma"] = sigma;
         ctx->saved_data["tau"] = tau;
         ctx->saved_data["vth"] = vth;
@@ -179,8 +127,7 @@ struct AxonalCommon : public torch::autograd::Function<AxonalCommon> {
         const int T = (int)ctx->saved_data["T"].toInt(), B = (int)ctx->saved_data["B"].toInt(),
                   N = (int)ctx->saved_data["N"].toInt();
         const double sigma = ctx->saved_data["sigma"].toDouble();
-        const float d_max = take_scalar(u.get_device(), ctx->saved_data["slot"].toInt(),
-                                        ctx->saved_data["gen"].toInt(), dc);
+        const float d_max = take_max(ctx->saved_data["ticket"].toInt(), dc);
         const int L = std::max(window_length(d_max, (float)(1.0 + sigma)), 2);
         const bool w_bf16 = Wc.scalar_type() == at::kBFloat16;
         const auto f32 = u.options();

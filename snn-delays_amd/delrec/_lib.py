@@ -29,7 +29,8 @@ WS_AXONAL_FWD, WS_AXONAL_BWD, WS_SYN_FWD, WS_SYN_BWD = 1, 2, 3, 4
 # Every symbol include/delrec.h declares (checked by the CPU test suite).
 EXPORTS = ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_syn_fwd', 'delrec_syn_bwd',
            'delrec_lif_fwd', 'delrec_lif_bwd', 'delrec_delay_grad', 'delrec_query_workspace',
-           'delrec_strerror', 'delrec_version', 'delrec_scan_timing', 'delrec_scan_timing_read')
+           'delrec_strerror', 'delrec_version', 'delrec_scan_timing', 'delrec_scan_timing_read',
+           'delrec_max_post', 'delrec_max_take')
 
 
 class DelrecError(RuntimeError):
@@ -52,7 +53,8 @@ class AxonalFwdArgs(ctypes.Structure):
                 ('s', c_vp), ('s_uniform', c_f32), ('drop', c_vp), ('taps', c_i32),
                 ('lag', c_vp), ('frac', c_vp), ('lif', Lif),
                 ('y', c_vp), ('u', c_vp), ('rec', c_vp), ('z', c_vp), ('bits', c_vp),
-                ('workspace', c_vp), ('workspace_bytes', c_size)]
+                ('workspace', c_vp), ('workspace_bytes', c_size),
+                ('dmax_ticket', ctypes.POINTER(ctypes.c_uint32))]
 
 
 class AxonalBwdArgs(ctypes.Structure):
@@ -118,6 +120,10 @@ def load():
     lib.delrec_scan_timing.argtypes = [c_i32]
     lib.delrec_scan_timing_read.restype = c_i32
     lib.delrec_scan_timing_read.argtypes = [ctypes.POINTER(c_f32), ctypes.POINTER(c_i32), c_i32]
+    lib.delrec_max_post.restype = c_i32
+    lib.delrec_max_post.argtypes = [c_vp, c_i32, ctypes.POINTER(ctypes.c_uint32), c_vp]
+    lib.delrec_max_take.restype = c_i32
+    lib.delrec_max_take.argtypes = [ctypes.c_uint32, ctypes.POINTER(c_f32), c_i32]
     _lib = lib
     return lib
 
@@ -250,6 +256,33 @@ class scan_timing:
             _check('delrec_scan_timing_read', -n)
         self.launches = [(SCAN_KINDS.get(kinds[k], str(kinds[k])), ms[k]) for k in range(n)]
         return False
+
+
+DELREC_OK = 0
+
+
+class PostedMax:
+    """max of a contiguous fp32 device vector, written into pinned host memory by a kernel
+    queued on the current stream (``delrec_max_post``); ``value()`` waits for that kernel's
+    store only, and reads the maximum again (synchronously) if the slot was reused by later
+    posts or the value did not arrive."""
+
+    def __init__(self, t, ticket=None):
+        """Post max(t) now, or adopt the ``ticket`` an entry point returned for max(t)."""
+        assert t.dtype == torch.float32 and t.is_contiguous() and t.numel() > 0
+        self.t = t
+        if ticket is None:
+            tk = ctypes.c_uint32(0)
+            _check('delrec_max_post', load().delrec_max_post(ptr(t), t.numel(), ctypes.byref(tk),
+                                                             stream_of(t)))
+            ticket = tk.value
+        self.ticket = int(ticket)
+
+    def value(self):
+        out = c_f32(0.0)
+        if load().delrec_max_take(self.ticket, ctypes.byref(out), 10000) == DELREC_OK:
+            return float(out.value)
+        return float(self.t.max())
 
 
 def delay_grad(C, W, d, sigma, N, Lm, out, stream):

@@ -15,6 +15,7 @@ Modes (reference ``recdel_base.py:361-383``):
   ste_mode   1: rounded tap forward, 2: two-tap interpolated forward; soft backward.
 """
 
+import ctypes
 import os
 
 import torch
@@ -32,21 +33,6 @@ def _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v
     return (N <= 256 and not use_sig_p and not approx and not ste_mode and not decay_input
             and v_reset is not None and float(v_reset) == 0.0 and 0.0 <= float(sigma) <= 3.0
             and os.environ.get('DELREC_AXONAL_FWD') != 'tiled')
-
-
-class _AsyncScalar:
-    """A device scalar copied into pinned host memory on the current stream; value()
-    waits for that copy only (not for later work on the stream)."""
-
-    def __init__(self, t):
-        self.host = torch.empty(1, dtype=torch.float32, pin_memory=True)
-        self.host.copy_(t.reshape(1).to(torch.float32), non_blocking=True)
-        self.event = torch.cuda.Event()
-        self.event.record()
-
-    def value(self):
-        self.event.synchronize()
-        return float(self.host[0])
 
 
 class AxonalRecdelHip(torch.autograd.Function):
@@ -80,15 +66,18 @@ class AxonalRecdelHip(torch.autograd.Function):
         stream = _lib.stream_of(xc)
 
         # The straight-line forward sizes its spike history from d itself, so when gradients
-        # are wanted the window length is not read here: max d is copied to pinned memory
-        # ahead of the scan and read by the backward (by then the copy has long finished).
-        # Without gradients the read stays synchronous so that an over-long window raises.
+        # are wanted the window length is not read here: the scan's first workgroup writes
+        # max d into pinned host memory, and the backward reads it (by then it has long
+        # arrived). Without gradients the read stays synchronous so that an over-long window
+        # raises.
         if (any(ctx.needs_input_grad[:5])
                 and _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v_reset)):
-            pending = _AsyncScalar(dc.max())
+            ticket = ctypes.c_uint32(0)
             args.L = 0
             args.taps = _lib.DELREC_TAPS_SOFT
+            args.dmax_ticket = ctypes.pointer(ticket)
             _lib.call('delrec_axonal_fwd', args, stream)
+            pending = _lib.PostedMax(dc, ticket.value)
             ctx.save_for_backward(u, z, bits, Wc, dc, s_vec, m, None, p_spread)
             ctx.meta = (T, B, N, pending, w_bf16, sigma, bool(use_sig_p), _lib.DELREC_BWD_SOFT, W.dtype)
             ctx.lif = lif
@@ -133,7 +122,7 @@ class AxonalRecdelHip(torch.autograd.Function):
     def backward(ctx, gy):
         u, z, bits, Wc, dc, s_vec, m, lag, p_spread = ctx.saved_tensors
         T, B, N, L, w_bf16, sigma, use_sig_p, mode, w_dtype = ctx.meta
-        if isinstance(L, _AsyncScalar):
+        if isinstance(L, _lib.PostedMax):
             L = max(window_length_f32(L.value(), 1.0 + sigma), 2)
         dev = u.device
         gy = gy.to(torch.float32).contiguous()

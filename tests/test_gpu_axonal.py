@@ -127,3 +127,67 @@ def test_axonal_forward_membrane_and_trace_via_abi(dev):
     t = torch.arange(T)
     unpacked = (b[:, t // 32, :] >> (t % 32).view(1, T, 1)) & 1         # (B, T, N)
     assert torch.equal(unpacked.permute(1, 0, 2).float(), y_ref)
+
+
+@pytest.mark.gpu
+def test_posted_max_matches_torch_max_and_detects_reused_slots(dev):
+    """delrec_max_post / delrec_max_take (the forward's host read of max d, taken by the
+    backward): the value torch.max gives, NaN included, for several posts outstanding at
+    once and taken in reverse order; a slot reused by later posts is reported stale and
+    PostedMax.value() then reads the maximum again."""
+    import ctypes
+    import math
+
+    from delrec import _lib
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    xs = [torch.randn(n, device=dev, generator=g) * 10 for n in (1, 7, 256, 1000, 4099)]
+    xs.append(torch.full((5,), -3.0, device=dev))
+    posts = [_lib.PostedMax(x) for x in xs]
+    for x, p in reversed(list(zip(xs, posts))):
+        assert p.value() == float(x.max())
+    nan = torch.tensor([1.0, float('nan'), 2.0], device=dev)
+    assert math.isnan(_lib.PostedMax(nan).value())
+
+    first = _lib.PostedMax(xs[2])
+    for _ in range(256):                       # DELREC_MAX_SLOTS later posts
+        _lib.PostedMax(xs[0])
+    torch.cuda.synchronize()
+    out = ctypes.c_float(0.0)
+    assert _lib.load().delrec_max_take(first.ticket, ctypes.byref(out), 1000) == 8   # DELREC_ERR_STALE
+    assert first.value() == float(xs[2].max())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('fused', [True, False], ids=['in-scan', 'before-scan'])
+def test_axonal_forward_posts_max_delay(dev, fused):
+    """delrec_axonal_fwd with dmax_ticket: max d arrives in its readback slot, written by the
+    straight-line scan's first workgroup (L = 0) or by the small kernel ahead of another
+    scan (here the recurrent-input output rules out the straight-line form)."""
+    import ctypes
+
+    from delrec import _lib
+    from delrec.kernels._common import bits_shape
+    T, B, N, sigma = 20, 3, 64, 1.0
+    g = gen(4)
+    xs = (torch.randn(T, B, N, generator=g) * 1.2 + 0.3).to(dev)
+    Ws = (torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)).to(dev)
+    ds = (torch.rand(N, generator=g) * 10.0).to(dev)
+    y = torch.empty(T, B, N, device=dev)
+    u, z, rec = torch.empty_like(y), torch.empty_like(y), torch.empty_like(y)
+    bits = torch.zeros(bits_shape(T, B, N), device=dev, dtype=torch.int32)
+    L = 0 if fused else 14
+    ws = _lib.workspace(_lib.WS_AXONAL_FWD, T, B, N, max(L, 2), 0, dev)
+    ticket = ctypes.c_uint32(0)
+    args = _lib.AxonalFwdArgs(T=T, B=B, N=N, L=L, x=_lib.ptr(xs), W=_lib.ptr(Ws), w_bf16=0,
+                              bias=None, d=_lib.ptr(ds), s=None, s_uniform=1.0 + sigma, drop=None,
+                              taps=0, lag=None, frac=None,
+                              lif=_lib.make_lif(2.0, 1.0, 0.0, False, False, 1, 1.0, 2.0),
+                              y=_lib.ptr(y), u=_lib.ptr(u), rec=None if fused else _lib.ptr(rec),
+                              z=_lib.ptr(z), bits=_lib.ptr(bits), workspace=_lib.ptr(ws),
+                              workspace_bytes=ws.numel(), dmax_ticket=ctypes.pointer(ticket))
+    _lib.call('delrec_axonal_fwd', args, _lib.stream_of(xs))
+    assert ticket.value != 0
+    out = ctypes.c_float(0.0)
+    assert _lib.load().delrec_max_take(ticket.value, ctypes.byref(out), 5000) == 0
+    assert out.value == float(ds.max())
