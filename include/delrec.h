@@ -74,9 +74,10 @@ enum { DELREC_TAPS_SOFT = 0, DELREC_TAPS_ROUND = 1, DELREC_TAPS_INTERP = 2 };
 typedef struct {
     int32_t T, B, N, L;          /* L: window length, ceil(1 + max d + max s) + 1; 0:   */
                                  /* not read by the caller (soft taps, uniform s, decay */
-                                 /* charge, hard reset to 0, no rec, N <= 256): the     */
-                                 /* kernel takes its history length from d, up to 256   */
-                                 /* lags; the caller checks L before the backward       */
+                                 /* charge, hard reset to 0, no rec, N <= 256,          */
+                                 /* T*B*N <= 2^28): the kernel takes its history length */
+                                 /* from d, up to 256 lags; the caller checks L before  */
+                                 /* the backward                                        */
     const float* x;              /* (T,B,N)                                             */
     const void* W;               /* (N,N) fp32 or bf16                                  */
     int32_t w_bf16;

@@ -539,9 +539,11 @@ int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_
 // non-zero weight), decay charge, hard reset to 0, no recurrent-input output, N <= 256.
 bool axonal_fwd_common(const delrec_axonal_fwd_args* a) {
     const float span = ceilf(2.0f * a->s_uniform);
+    // (the straight-line scan addresses each (T, B, N) output with 32-bit offsets: <= 1 GiB)
     return a->N <= 256 && axonal_fwd_wave_on() && a->taps == DELREC_TAPS_SOFT && !a->s &&
            a->s_uniform > 0.0f && span <= 8.0f && !a->lif.decay_input && !a->lif.soft_reset &&
-           a->lif.v_reset == 0.0f && !a->rec;
+           a->lif.v_reset == 0.0f && !a->rec &&
+           (size_t)a->T * a->B * a->N * sizeof(float) <= ((size_t)1 << 30);
 }
 
 int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream) {

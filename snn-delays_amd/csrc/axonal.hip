@@ -11,6 +11,8 @@
 // Reference behaviour replaced: recdel_fwd_kernel / recdel_bwd_kernel
 // (src/delrec/triton_kernels/recdel_base.py:34-129, :189-285), with the dmask loop and
 // autograd through build_mask (:327-342, :421-435) folded into per-neuron accumulators.
+#include <utility>
+
 #include "common.h"
 #include "kernels.h"
 #include "dw_gemm.h"
@@ -672,6 +674,13 @@ __global__ void __launch_bounds__(512) axonal_fwd_wave(AxFwd p) {
 // pre-step traces zpre(t+1) and contracts its slow active columns for step t+1; after
 // the LIF only the fast sources' lag-1 term and their (few) columns remain on the
 // critical path. Stores and the x prefetch use buffer descriptors in SGPRs.
+// f(std::integral_constant<int, Q>{}) for Q = 0, 1, ... in order (an unrolled loop whose
+// index is a compile-time constant in the body)
+template <class F, int... Q>
+__device__ __forceinline__ void unroll_steps(std::integer_sequence<int, Q...>, F&& f) {
+    (f(std::integral_constant<int, Q>{}), ...);
+}
+
 // spike-history window of HW 64-bit words: bits sh .. sh + 31 (sh >= -1; bit -1 reads 0)
 template <int HW>
 __device__ __forceinline__ uint32_t hist_bits(const uint64_t (&h)[HW], int sh) {
@@ -742,31 +751,37 @@ __device__ __forceinline__ void axonal_fwd_wave_fast_body(const AxFwd& p, float*
     uint32_t word = 0;
     const size_t BN = (size_t)B * N;
     const uint32_t row_bytes = (uint32_t)BN * 4u;  // one step of a (T, B, N) tensor
-    const int voff = (b * N + i) * 4;              // this lane's byte offset within a step
-    // stores of lanes without a neuron go past the buffer end (dropped): every memory
-    // operation of a step is unconditional, so the compiler's counts of outstanding
-    // loads / stores are exact and a prefetched value never waits on later stores
-    const int soff = nl ? voff : kOutOfRange;
-    const int boff = nl ? (b * TW * N + i) * 4 : kOutOfRange;   // spike-bit word of step 0
+    const uint32_t all_bytes = (uint32_t)T * row_bytes;   // at most 1 GiB (host check)
+    const uint32_t voff = (uint32_t)(b * N + i) * 4u;     // this lane's byte offset within a step
+    // One descriptor per tensor for the whole scan and one moving byte offset per lane: the
+    // offset of step t is voff + t * row_bytes, which lies past the buffer end for steps
+    // t >= T (stores dropped, loads read 0). Lanes without a neuron start past the end and
+    // stay there (no wrap: twice the tensor plus a few steps fits 32 bits). Every memory
+    // operation of a step is unconditional, so the compiler's counts of outstanding loads /
+    // stores are exact and a prefetched value never waits on later stores.
     float* const zout = p.z;
+    const i32x4 xr = buffer_rsrc(p.x, all_bytes), yr = buffer_rsrc(p.y, all_bytes);
+    const i32x4 ur = buffer_rsrc(p.u, all_bytes), zr = buffer_rsrc(zout, zout ? all_bytes : 0u);
+    const i32x4 br = buffer_rsrc(p.bits, (uint32_t)B * TW * N * 4u);
+    const uint32_t boff = nl ? (uint32_t)(b * TW * N + i) * 4u : (uint32_t)kOutOfRange;   // word of steps 0..31
+    const uint32_t n4 = (uint32_t)N * 4u;
+    uint32_t vo = nl ? voff : all_bytes;           // y, u of step t; z of step t + 1 one row on
+    uint32_t vx = voff + (uint32_t)kPrefetchWave * row_bytes;   // x of step t + P
     float xq[kPrefetchWave];
 #pragma unroll
-    for (int q = 0; q < kPrefetchWave; ++q)
-        xq[q] = raw_buffer_load_f32(buffer_rsrc(p.x + (size_t)q * BN, q < T ? row_bytes : 0u), voff, 0, 0);
+    for (int q = 0; q < kPrefetchWave; ++q) xq[q] = raw_buffer_load_f32(xr, voff + (uint32_t)q * row_bytes, 0, 0);
     if (nl && zout) zout[(size_t)b * N + i] = 0.0f;
 
-    // byte addresses of step t of x (prefetch: t + P), y, u and z (t + 1), advanced per step
-    const uint64_t step_b = (uint64_t)row_bytes;
-    uint64_t xa = (uint64_t)p.x + (uint64_t)kPrefetchWave * step_b;
-    uint64_t ya = (uint64_t)p.y, ua = (uint64_t)p.u, za = (uint64_t)zout + step_b;
-    const uint32_t zbytes = zout ? row_bytes : 0u;
     float zcur = 0.0f;                             // z(t) of this lane's source
     uint32_t mkf = 0;                              // fast sources with z(t) != 0
     float acc_s[RI];                               // slow columns of W z(t)
 #pragma unroll
     for (int a = 0; a < RI; ++a) acc_s[a] = 0.0f;
 
-    auto step = [&](const int t, float& xs) {
+    // step t = t0 + Q of a group of kPrefetchWave (Q a compile-time constant: only the last
+    // step of a group can end a 32-step spike word)
+    auto step = [&](const int t, float& xs, auto qc) {
+        constexpr int Q = decltype(qc)::value;
         // fast columns of z(t) on top of the slow part formed during the previous step
         float acc[RI];
 #pragma unroll
@@ -831,30 +846,26 @@ __device__ __forceinline__ void axonal_fwd_wave_fast_body(const AxFwd& p, float*
         mkf = (uint32_t)__ballot(fastn && zn != 0.0f);
         zcur = zn;
 
-        // outputs; steps t >= T store nothing (their descriptors have no records)
-        const uint32_t live = t < T ? row_bytes : 0u;
-        raw_buffer_store_f32(fire ? 1.0f : 0.0f, step_rsrc(ya, live), soff, 0, 0);
-        raw_buffer_store_f32(u, step_rsrc(ua, live), soff, 0, 0);
-        raw_buffer_store_f32(zn, step_rsrc(za, next ? zbytes : 0u), soff, 0, 0);
-        ya += step_b;
-        ua += step_b;
-        za += step_b;
+        // outputs; steps t >= T store nothing (their offsets lie past the buffer end)
+        raw_buffer_store_f32(fire ? 1.0f : 0.0f, yr, vo, 0, 0);
+        raw_buffer_store_f32(u, ur, vo, 0, 0);
+        raw_buffer_store_f32(zn, zr, vo + row_bytes, 0, 0);
+        vo += row_bytes;
         // the spike-bit word of steps 32k .. 32k+31, written at its last step
-        const bool flush = ((t & 31) == 31 || t == T - 1) && t < T;
-        raw_buffer_store_f32(__uint_as_float(word),
-                             buffer_rsrc(p.bits + (size_t)(t >> 5) * N, flush ? (uint32_t)((size_t)B * TW * N * 4u) : 0u),
-                             boff, 0, 0);
-        if ((t & 31) == 31) word = 0;
+        bool flush = t == T - 1;
+        if constexpr (Q == kPrefetchWave - 1) flush = flush || ((t & 31) == 31 && t < T);
+        if (flush) raw_buffer_store_f32(__uint_as_float(word), br, boff + (uint32_t)(t >> 5) * n4, 0, 0);
+        if constexpr (Q == kPrefetchWave - 1) {
+            if ((t & 31) == 31) word = 0;
+        }
         // refill the slot after its value is used (no copy, so no wait on the load)
-        const int tn = t + kPrefetchWave;
-        xs = raw_buffer_load_f32(step_rsrc(xa, tn < T ? row_bytes : 0u), voff, 0, 0);
-        xa += step_b;
+        xs = raw_buffer_load_f32(xr, vx, 0, 0);
+        vx += row_bytes;
     };
 
-    for (int t0 = 0; t0 < T; t0 += kPrefetchWave) {
-#pragma unroll
-        for (int q = 0; q < kPrefetchWave; ++q) step(t0 + q, xq[q]);
-    }
+    for (int t0 = 0; t0 < T; t0 += kPrefetchWave)
+        unroll_steps(std::make_integer_sequence<int, kPrefetchWave>{},
+                     [&](auto qc) { step(t0 + decltype(qc)::value, xq[decltype(qc)::value], qc); });
 }
 
 template <int RI, int NJ, int HW, int CJ>
@@ -1117,6 +1128,14 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled_fast
     int tap = (T - 1 + lof) % R * slot_bytes + j * 4;  // slot of time t + lof, t = T - 1
 
     auto step = [&](const int t, float& gs, float& us) {
+        // taps of the future gradient, times t + lof + q (slots of times >= T hold 0), read
+        // before the contraction: they are this lane's own slots of earlier steps, except the
+        // first tap of a lag-1 source, time t + 1, which is gz(t+1) itself (with R >= L + 8
+        // ring slots no other tap reaches the slot written in this step)
+        const float* rp = reinterpret_cast<const float*>(reinterpret_cast<const char*>(ring) + tap);
+        float rq[KF];
+#pragma unroll
+        for (int q = 0; q < KF; ++q) rq[q] = rp[q * NP];
         const float gz1 = contract((t + 1) & 1);       // gz(t+1); gr(T) = 0
         const int tm = tn1 == 0 ? R - 1 : tn1 - 1;     // slot of time t
         // publish gz(t+1) in its slot (and the mirror) and for the delay-gradient pass
@@ -1126,11 +1145,10 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled_fast
         }
         raw_buffer_store_f32(gz1, step_rsrc(gza, t + 1 < T ? row_bytes : 0u), soff, 0, 0);
         gza -= step_b;
-        // taps of the future gradient: times t + lof + q (slots of times >= T hold 0)
+        rq[0] = lof == 1 ? gz1 : rq[0];
         float gfut = 0.0f;
-        const float* rp = reinterpret_cast<const float*>(reinterpret_cast<const char*>(ring) + tap);
 #pragma unroll
-        for (int q = 0; q < KF; ++q) gfut = fmaf(wq[q], rp[q * NP], gfut);
+        for (int q = 0; q < KF; ++q) gfut = fmaf(wq[q], rq[q], gfut);
         // LIF backward (hard reset to 0, ATan surrogate, reset not detached)
         const float u = us;
         const float y = (u - vth >= 0.0f) ? 1.0f : 0.0f;

@@ -16,6 +16,7 @@ import torch
 from . import _lib
 from .kernels import AxonalRecdelHip, eventdriven_trainable_forward, hybrid_trainable_forward
 from .kernels._common import require_device
+from .kernels.recdel_base import STRAIGHT_LINE_MAX_ELEMS
 from .kernels.surrogate import surrogate_id
 
 
@@ -51,7 +52,7 @@ class AxonalHipScans:
         nm = self.neuron_module
         ext = _lib.torch_ext()
         if (ext is not None and not approx and not ste_mode and not self.use_sig_p and N <= 256
-                and x_seq.dtype == torch.float32 and nm.v_reset is not None and float(nm.v_reset) == 0.0
+                and x_seq.numel() <= STRAIGHT_LINE_MAX_ELEMS and x_seq.dtype == torch.float32 and nm.v_reset is not None and float(nm.v_reset) == 0.0
                 and not getattr(nm, 'decay_input', False) and 0.0 <= float(self.sigma) <= 3.0
                 and os.environ.get('DELREC_AXONAL_FWD') != 'tiled'):
             # the common regime: the C++ autograd Function over the same C ABI (no Python on

@@ -26,11 +26,15 @@ from ._common import (bits_shape, drop_bn, read_scalars, require_device, round_h
 from .delays import build_lag, build_lag_interp
 
 
-def _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v_reset):
+STRAIGHT_LINE_MAX_ELEMS = 1 << 28   # (T, B, N) fp32 outputs addressed with 32-bit offsets
+
+
+def _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v_reset, TB=1):
     """The calls the C ABI's straight-line forward takes without a window length (L = 0):
     soft taps of a uniform half-width with at most 8 lags of non-zero weight, decay charge,
-    hard reset to 0, N <= 256."""
-    return (N <= 256 and not use_sig_p and not approx and not ste_mode and not decay_input
+    hard reset to 0, N <= 256, T * B * N <= 2^28 (each output at most 1 GiB)."""
+    return (N <= 256 and TB * N <= STRAIGHT_LINE_MAX_ELEMS and not use_sig_p and not approx
+            and not ste_mode and not decay_input
             and v_reset is not None and float(v_reset) == 0.0 and 0.0 <= float(sigma) <= 3.0
             and os.environ.get('DELREC_AXONAL_FWD') != 'tiled')
 
@@ -71,7 +75,8 @@ class AxonalRecdelHip(torch.autograd.Function):
         # arrived). Without gradients the read stays synchronous so that an over-long window
         # raises.
         if (any(ctx.needs_input_grad[:5])
-                and _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v_reset)):
+                and _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v_reset,
+                                           T * B)):
             ticket = ctypes.c_uint32(0)
             args.L = 0
             args.taps = _lib.DELREC_TAPS_SOFT
