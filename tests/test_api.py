@@ -206,3 +206,15 @@ def test_fixed_models_freeze_delays():
         leaf = learned_delay_parameter(layer, 'recurrent_delays')
         assert not leaf.requires_grad and layer.sigma == 0.0
         assert torch.equal(leaf, leaf.round())
+
+
+def test_straight_line_forward_keeps_outputs_within_32_bit_offsets():
+    """The straight-line axonal forward (L = 0, no host read of max d) addresses each
+    (T, B, N) fp32 output with 32-bit byte offsets: larger calls take the general forward."""
+    from delrec.kernels.recdel_base import STRAIGHT_LINE_MAX_ELEMS, _straight_line_forward
+    assert STRAIGHT_LINE_MAX_ELEMS * 4 <= 1 << 30
+    args = (256, 1.0, False, False, 0, False, 0.0)
+    assert _straight_line_forward(*args, TB=128 * 128)
+    assert _straight_line_forward(*args, TB=STRAIGHT_LINE_MAX_ELEMS // 256)
+    assert not _straight_line_forward(*args, TB=STRAIGHT_LINE_MAX_ELEMS // 256 + 1)
+    assert not _straight_line_forward(257, 1.0, False, False, 0, False, 0.0, TB=1)
