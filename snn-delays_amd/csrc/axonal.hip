@@ -1333,8 +1333,8 @@ __global__ void __launch_bounds__(1024) reduce_rows_kernel(const float* part, in
 
 // The reductions after the axonal backward scan, as two launches on the caller's stream (no
 // second stream: its fork and join cost more than the overlap they buy):
-//   tail: blocks [0, ndw) the dW GEMM tiles (tile (ti, tj) of k chunk kz at block
-//         (kz * tiles + tj) * tiles + ti), then the delay / half-width gradient rows;
+//   tail: blocks [0, ndw) the dW GEMM tiles (tile (ti, tj) of k chunk kz; the tiles of
+//         one chunk on one XCD), then the delay / half-width gradient rows;
 //   sums: blocks [0, nsum) the dW split-K sums, then the batch reductions of db, dd, ds
 //         (16 neurons per block).
 // Both job kinds of a launch only read what earlier launches wrote, so they run side by
@@ -1344,8 +1344,18 @@ __global__ void __launch_bounds__(kDwThreads, 3) axonal_bwd_tail_kernel(AxBwd p,
     __shared__ DwStage sm;   // 32 KiB: one dW stage, or the delay blocks' 2 KiB of partials
     int bid = blockIdx.x;
     if (bid < q.ndw) {
+        // the tiles of one k chunk read the same rows of both operands: with ks a multiple of
+        // 8 they all go to one XCD (workgroup id mod 8), so the second reads hit its L2
         const int tt = q.tiles * q.tiles;
-        const int kz = bid / tt, r = bid - kz * tt;
+        int kz, r;
+        if ((q.ks & 7) == 0) {
+            const int slot = bid >> 3;
+            kz = (slot / tt) * 8 + (bid & 7);
+            r = slot % tt;
+        } else {
+            kz = bid / tt;
+            r = bid - kz * tt;
+        }
         dw_gemm_tile(q.A, q.Bz, q.K, p.N, q.kchunk, q.gpart, r % q.tiles, r / q.tiles, kz, sm);
         return;
     }
