@@ -790,11 +790,12 @@ __device__ __forceinline__ void axonal_fwd_wave_fast_body(const AxFwd& p, float*
         while (mk) {
             const int cc = __builtin_ctz(mk);
             mk &= mk - 1u;
-            const float zc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(zcur), cc));
+            // the weight column in one indexed-register run, then the spike value
             float wt[RI];
 #pragma unroll
             for (int a = 0; a < RI; ++a) wt[a] = w[a][cc];
             __builtin_amdgcn_sched_barrier(0);
+            const float zc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(zcur), cc));
 #pragma unroll
             for (int a = 0; a < RI; ++a) acc[a] = fmaf(wt[a], zc, acc[a]);
         }
@@ -818,11 +819,11 @@ __device__ __forceinline__ void axonal_fwd_wave_fast_body(const AxFwd& p, float*
         while (ms) {
             const int cc = __builtin_ctz(ms);
             ms &= ms - 1u;
-            const float zc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(zpre), cc));
             float wt[RI];
 #pragma unroll
             for (int a = 0; a < RI; ++a) wt[a] = w[a][cc];
             __builtin_amdgcn_sched_barrier(0);
+            const float zc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(zpre), cc));
 #pragma unroll
             for (int a = 0; a < RI; ++a) acc_s[a] = fmaf(wt[a], zc, acc_s[a]);
         }
