@@ -353,6 +353,7 @@ void syn_bwd_ws(C& c, int T, int B, int N, int L, int taps) {
     c.template take<float>((size_t)N * lay.NT);         // d^T or the offsets^T
     c.template take<float>((size_t)B * N * lay.RP);     // ring when it does not fit LDS
     c.template take<uint8_t>((size_t)N * lay.NT);       // byte slot offsets (hybrid)
+    c.template take<int>((size_t)N);                    // sources in first-lag order (hybrid)
 }
 
 // out[c * op + r] = in[r * n + c] for an (n, n) matrix; output columns r in [n, op) are 0
@@ -377,13 +378,16 @@ __global__ void transpose_kernel(const E* __restrict__ in, E* __restrict__ out, 
 //   rows (ROWS = true): lane i reads j = 16c .. 16c+15 of row i,
 //       out[((j / 16) * n + i) * 16 + j % 16] = in[i * n + j];
 // a wave's lanes read adjacent runs; entries past n are zero (ceil(n / 16) runs per lane).
+// With `order` (columns form only) lane slot k holds column order[k].
 template <class E, bool ROWS>
-__global__ void block_copy_kernel(const E* __restrict__ in, E* __restrict__ out, int n) {
+__global__ void block_copy_kernel(const E* __restrict__ in, E* __restrict__ out, int n,
+                                  const int* __restrict__ order) {
     const int nc = (n + 15) / 16;
     const size_t total = (size_t)nc * n;
     for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total;
          q += (size_t)gridDim.x * blockDim.x) {
-        const int c = (int)(q / n), lane = (int)(q - (size_t)c * n);
+        const int c = (int)(q / n), slot = (int)(q - (size_t)c * n);
+        const int lane = (!ROWS && order) ? order[slot] : slot;
         E v[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -396,11 +400,11 @@ __global__ void block_copy_kernel(const E* __restrict__ in, E* __restrict__ out,
 }
 
 template <class E, bool ROWS = false>
-void block_transpose(const void* in, void* out, int n, hipStream_t s) {
+void block_transpose(const void* in, void* out, int n, hipStream_t s, const int* order = nullptr) {
     const size_t total = (size_t)((n + 15) / 16) * n;
     const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 65535);
     hipLaunchKernelGGL((block_copy_kernel<E, ROWS>), dim3(blocks), dim3(256), 0, s,
-                       static_cast<const E*>(in), static_cast<E*>(out), n);
+                       static_cast<const E*>(in), static_cast<E*>(out), n, order);
 }
 
 template <class E>
@@ -845,18 +849,32 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     void* dt = nullptr;
     float* gring = nullptr;
     uint8_t* offq = nullptr;
+    int* order = nullptr;
     if (!lagstep) {
         wt = cv.take<float>((size_t)N * wlay.NT);
         dt = cv.take<float>((size_t)N * wlay.NT);
         gring = cv.take<float>((size_t)B * N * wlay.RP);
         offq = cv.take<uint8_t>((size_t)N * wlay.NT);
-        if (!wt || !dt || !gring || !offq) return DELREC_ERR_WORKSPACE;
+        order = cv.take<int>((size_t)N);
+        if (!wt || !dt || !gring || !offq || !order) return DELREC_ERR_WORKSPACE;
     }
     if (!gr || !part || !lagp || !ahi || !alo || !yb || !meta) return DELREC_ERR_WORKSPACE;
 
+    // the streamlined hybrid backward (syn_bwd_hyb: ring in LDS over the receivers rounded up
+    // to groups of 64, one source per lane, N <= 512). Its lanes take the sources in
+    // first-lag order: the 32 lanes an LDS access serves together then gather from nearby
+    // slots of one ring row, which keeps them in distinct banks (any assignment gives the
+    // same sums: each source's gather runs in its own lane); its blocked W^T and offsets are
+    // laid out in that order, so a lane's runs stay adjacent to its neighbours'.
+    const size_t hrows = (size_t)((N + 63) / 64 * 64);
+    const size_t lds_h = hrows * lay.RP * sizeof(float);
+    const bool hyb_fast = hybrid && !lagstep && N <= 512 && (lay.KT == 2 || lay.KT == 4) &&
+                          lds_h <= (size_t)max_lds_bytes() && getenv_flag_off("DELREC_SYN_BWD_HYB");
     if (!lagstep) {
-        if (a->w_bf16) block_transpose<uint16_t>(a->W, wt, N, s); else block_transpose<float>(a->W, wt, N, s);
-        if (hybrid) block_transpose<int8_t>(a->offsets, dt, N, s);
+        if (hyb_fast) launch_sort_by_first_lag(a->base, a->s_uniform, N, order, s);
+        const int* ord = hyb_fast ? order : nullptr;
+        if (a->w_bf16) block_transpose<uint16_t>(a->W, wt, N, s, ord); else block_transpose<float>(a->W, wt, N, s, ord);
+        if (hybrid) block_transpose<int8_t>(a->offsets, dt, N, s, ord);
         else block_transpose<float>(a->d, dt, N, s);
     }
     // each column's lag range for the lag GEMM, and the smallest offset (meta[1]) the
@@ -948,19 +966,15 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     p.drop = a->drop; p.lif = make_lif(a->lif);
     p.dx = a->dx; p.gr = gr; p.part = part; p.gring = lay.lds_ring ? nullptr : gring;
     const bool timed = scan_begin(DELREC_WS_SYN_BWD, s);
-    // hybrid, ring in LDS, one source per lane: the streamlined gather (its ring covers
-    // the receivers rounded up to groups of 64)
-    const size_t hrows = (size_t)((N + 63) / 64 * 64);   // groups of <= 64 receivers
-    const size_t lds_h = hrows * lay.RP * sizeof(float);
-    const bool hyb_fast = hybrid && N <= 1024 && (lay.KT == 2 || lay.KT == 4) &&
-                          lds_h <= (size_t)max_lds_bytes() && getenv_flag_off("DELREC_SYN_BWD_HYB");
     // room for rows that also mirror the offset span (up to L more slots): the kernel
     // takes the no-wrap form when the span it finds fits
     const size_t lds_hx = std::max(lds_h, std::min((size_t)max_lds_bytes(),
                                                    hrows * (size_t)(2 * lay.R + lay.KT + 1) * sizeof(float)));
     p.ldsf = (int)(lds_hx / sizeof(float));
     p.offq = hybrid ? offq : nullptr;
-    const bool ok = (hyb_fast && launch_syn_bwd_hyb(p, lay.block, lds_hx, s)) || launch_syn_bwd(p, lay.block, lay.lds, s);
+    p.order = hyb_fast ? order : nullptr;
+    // (no fallback from the hybrid kernel: its operands are in first-lag order)
+    const bool ok = hyb_fast ? launch_syn_bwd_hyb(p, lay.block, lds_hx, s) : launch_syn_bwd(p, lay.block, lay.lds, s);
     scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();

@@ -103,6 +103,7 @@ struct SynBwd {
     float* part;                // [B][N] db partials
     float* gring;               // global ring [B][N][RP] when it does not fit LDS, else NULL
     int ldsf;                   // floats of LDS the hybrid backward was given
+    const int* order;           // hybrid: source of each lane slot (first-lag order), or NULL
     const uint8_t* offq;        // blocked (offset - smallest offset) * 4 as bytes (hybrid), or NULL
 };
 
@@ -259,6 +260,9 @@ bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);
 // KT = 2 or 4; false when it does not apply
 // offq[q] = (offt[q] - meta[1]) * 4 (the byte slot offsets of the hybrid backward)
 void launch_pack_offq(const int8_t* offt, size_t n, const int* meta, uint8_t* offq, hipStream_t stream);
+// order[k] = the source with the k-th smallest (first lag lob, index) of the hybrid backward
+// (one workgroup; N <= 1024)
+void launch_sort_by_first_lag(const float* base, float s, int N, int* order, hipStream_t stream);
 bool launch_syn_bwd_hyb(const SynBwd& a, int block, size_t lds, hipStream_t stream);
 // each column's lag range (lo, rc, om) and meta[0..1]
 void launch_lag_cols(const LagBf16& a, hipStream_t stream);

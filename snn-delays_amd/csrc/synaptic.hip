@@ -894,7 +894,7 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     const int jloc = SPLIT ? (tid >> 6) * 32 + (tid & 31) : tid;
     const bool act = jloc < N;
     const bool writer = act && half == 0;                 // the lane that stores for source j
-    const int j = act ? jloc : 0;
+    const int j = act ? (p.order ? p.order[jloc] : jloc) : 0;   // this lane's source
     const Lif k = p.lif;
     const float m = p.drop ? p.drop[(size_t)b * N + j] : 1.0f;
     const float sv = p.s_uniform;
@@ -929,8 +929,9 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     const uint32_t obytes = (uint32_t)((size_t)p.NT * N);
     const i32x4 rw = buffer_rsrc(p.Wt, wbytes), ro = buffer_rsrc(nowrap ? (const void*)p.offq : (const void*)p.offt, obytes);
     const int wcs = N * 16 * (WBF ? 2 : 4), ocs = N * 16;   // bytes per chunk
-    const int wj = act ? j * 16 * (WBF ? 2 : 4) + cbase * wcs : kOutOfRange;
-    const int oj = act ? j * 16 + cbase * ocs : kOutOfRange;
+    // the blocked operands are laid out by lane slot (jloc), in the order the host chose
+    const int wj = act ? jloc * 16 * (WBF ? 2 : 4) + cbase * wcs : kOutOfRange;
+    const int oj = act ? jloc * 16 + cbase * ocs : kOutOfRange;
     constexpr int WV = WBF ? 2 : 4;                          // uint4 of W per chunk
     struct Chunk { uint4 w[WV]; uint4 o; };
     auto fetch = [&](int cidx, Chunk& ch) {
@@ -1090,6 +1091,34 @@ __global__ void pack_offq_kernel(const int8_t* __restrict__ offt, size_t n, cons
     const int omin = meta[1];
     for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < n; q += (size_t)gridDim.x * blockDim.x)
         offq[q] = (uint8_t)(((int)offt[q] - omin) * 4);
+}
+
+// order[k] = the source with the k-th smallest key (first lag lob, index): the first lag of
+// non-zero weight of each hybrid source, computed as syn_bwd_hyb does. One workgroup.
+__global__ void __launch_bounds__(1024) sort_by_first_lag_kernel(const float* base, float sv, int N,
+                                                                 int* order) {
+    __shared__ int key[1024];
+    for (int j = threadIdx.x; j < N; j += blockDim.x) {
+        const float c = 1.0f + base[j];
+        int lob = (int)ceilf(c - sv);
+        if (fabsf((float)(lob - 1) - c) <= sv) lob -= 1;
+        if (fabsf((float)lob - c) > sv) lob += 1;
+        key[j] = lob;
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < N; j += blockDim.x) {
+        const int kj = key[j];
+        int pos = 0;
+        for (int q = 0; q < N; ++q) {
+            const int kq = key[q];
+            pos += (kq < kj || (kq == kj && q < j)) ? 1 : 0;
+        }
+        order[pos] = j;
+    }
+}
+
+void launch_sort_by_first_lag(const float* base, float s, int N, int* order, hipStream_t stream) {
+    hipLaunchKernelGGL(sort_by_first_lag_kernel, dim3(1), dim3(1024), 0, stream, base, s, N, order);
 }
 
 void launch_pack_offq(const int8_t* offt, size_t n, const int* meta, uint8_t* offq, hipStream_t stream) {
