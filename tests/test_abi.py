@@ -48,6 +48,10 @@ def test_query_workspace_and_argument_errors_without_gpu():
     assert lib.delrec_axonal_fwd(ctypes.byref(args), None) == 1          # null tensors
     assert lib.delrec_syn_bwd(None, None) == 1
     assert lib.delrec_delay_grad(None, None, None, 0.0, 4, 3, None, None) == 1
+    ticket, value = ctypes.c_uint32(0), ctypes.c_float(0.0)
+    assert lib.delrec_max_post(None, 4, ctypes.byref(ticket), None) == 1     # null vector
+    assert lib.delrec_max_take(0, ctypes.byref(value), 10) == 1              # ticket 0 is never issued
+    assert lib.delrec_max_take(5, None, 10) == 1
 
 
 _STRUCTS = ['delrec_lif', 'delrec_axonal_fwd_args', 'delrec_axonal_bwd_args', 'delrec_syn_fwd_args',

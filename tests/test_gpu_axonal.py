@@ -156,6 +156,8 @@ def test_posted_max_matches_torch_max_and_detects_reused_slots(dev):
     out = ctypes.c_float(0.0)
     assert _lib.load().delrec_max_take(first.ticket, ctypes.byref(out), 1000) == 8   # DELREC_ERR_STALE
     assert first.value() == float(xs[2].max())
+    # a ticket not posted yet: the wait ends at its time limit
+    assert _lib.load().delrec_max_take(first.ticket + 100000, ctypes.byref(out), 50) == 7   # DELREC_ERR_PENDING
 
 
 @pytest.mark.gpu
