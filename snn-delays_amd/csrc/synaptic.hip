@@ -239,16 +239,26 @@ __global__ void __launch_bounds__(1024) syn_fwd_scatter(SynFwd p) {
     const i32x4 rd = buffer_rsrc(HYB ? (const void*)p.offt : (const void*)p.dt, nn * (HYB ? 1u : 4u));
     const int wsz = PACKED ? 4 : (WBF ? 2 : 4), dsz = HYB ? 1 : 4;
     const int wio = act ? i * wsz : 0x40000000, dio = act ? i * dsz : 0x40000000;
-    auto load_src = [&](int o, float& w, float& dl) {
+    // a source's weight and delay (or offset) as loaded, decoded only where they are used:
+    // a decode right after the load would make the prefetch wait for it
+    auto load_src = [&](int o, uint32_t& w, uint32_t& dl) {
         if constexpr (PACKED) {
-            const uint32_t v = __float_as_uint(raw_buffer_load_f32(rw, wio + o * N * 4, 0, 0));
-            w = __uint_as_float(v & 0xFFFF0000u);
-            dl = (float)(int8_t)(v & 0xFFu);
+            w = __float_as_uint(raw_buffer_load_f32(rw, wio + o * N * 4, 0, 0));
+            dl = 0u;
         } else {
-            if constexpr (WBF) w = bf16_to_f32(raw_buffer_load_u16(rw, wio + o * N * 2, 0, 0));
-            else w = raw_buffer_load_f32(rw, wio + o * N * 4, 0, 0);
-            if constexpr (HYB) dl = (float)raw_buffer_load_i8(rd, dio + o * N, 0, 0);
-            else dl = raw_buffer_load_f32(rd, dio + o * N * 4, 0, 0);
+            if constexpr (WBF) w = (uint32_t)raw_buffer_load_u16(rw, wio + o * N * 2, 0, 0);
+            else w = __float_as_uint(raw_buffer_load_f32(rw, wio + o * N * 4, 0, 0));
+            if constexpr (HYB) dl = (uint32_t)(int32_t)raw_buffer_load_i8(rd, dio + o * N, 0, 0);
+            else dl = __float_as_uint(raw_buffer_load_f32(rd, dio + o * N * 4, 0, 0));
+        }
+    };
+    auto decode_src = [&](uint32_t w, uint32_t dl, float& wf, float& df) {
+        if constexpr (PACKED) {
+            wf = __uint_as_float(w & 0xFFFF0000u);
+            df = (float)(int8_t)(w & 0xFFu);
+        } else {
+            wf = WBF ? __uint_as_float(w << 16) : __uint_as_float(w);
+            df = HYB ? (float)(int32_t)dl : __uint_as_float(dl);
         }
     };
 
@@ -315,11 +325,11 @@ __global__ void __launch_bounds__(1024) syn_fwd_scatter(SynFwd p) {
             // chunked walk: the next chunk's weights / delays load while this one scatters
             // (sources past nf read source 0: valid addresses, values unused; every load is
             // unconditional so the compiler's memory counts stay exact)
-            float wn[kScatterChunk], dn[kScatterChunk];
+            uint32_t wn[kScatterChunk], dn[kScatterChunk];
 #pragma unroll
             for (int e = 0; e < kScatterChunk; ++e) load_src(__builtin_amdgcn_readlane(src, e), wn[e], dn[e]);
             for (int f0 = 0; f0 < nf; f0 += kScatterChunk) {
-                float wc[kScatterChunk], dc[kScatterChunk];
+                uint32_t wc[kScatterChunk], dc[kScatterChunk];
 #pragma unroll
                 for (int e = 0; e < kScatterChunk; ++e) {
                     wc[e] = wn[e];
@@ -336,8 +346,10 @@ __global__ void __launch_bounds__(1024) syn_fwd_scatter(SynFwd p) {
                     const int o = __builtin_amdgcn_readlane(src, (f0 + e) & 63);
                     const float4 sp = srcl[o];                 // base, s, 1/s^2
                     const float so = sp.y;
-                    const float c = HYB ? 1.0f + (sp.x + 0.0f + 1.0f * dc[e]) : 1.0f + dc[e];
-                    const float wq = wc[e] * sp.z;
+                    float wv, dv;
+                    decode_src(wc[e], dc[e], wv, dv);
+                    const float c = HYB ? 1.0f + (sp.x + 0.0f + 1.0f * dv) : 1.0f + dv;
+                    const float wq = wv * sp.z;
                     // lags of non-zero weight: l > c - s, l >= 1; the ring slot of t + l
                     const int lof = max(1, (int)floorf(c - so) + 1);
                     int sl = tmod + lof;
