@@ -354,12 +354,20 @@ __global__ void __launch_bounds__(1024) syn_fwd_scatter(SynFwd p) {
                     const int lof = max(1, (int)floorf(c - so) + 1);
                     int sl = tmod + lof;
                     sl = sl >= R ? sl - R : sl;
+                    // the KF taps land in distinct slots (KF < R): read them all, then write
+                    float* cp[KF];
+                    float old[KF];
+#pragma unroll
+                    for (int q = 0; q < KF; ++q) {
+                        cp[q] = colp + __umul24((uint32_t)sl, (uint32_t)cst);   // slot * pitch < 2^24
+                        sl = sl + 1 == R ? 0 : sl + 1;
+                    }
+#pragma unroll
+                    for (int q = 0; q < KF; ++q) old[q] = *cp[q];
 #pragma unroll
                     for (int q = 0; q < KF; ++q) {
                         const float hv = fmaxf(so - fabsf((float)(lof + q) - c), 0.0f);
-                        float* cp = colp + sl * cst;
-                        *cp = *cp + wq * hv;
-                        sl = sl + 1 == R ? 0 : sl + 1;
+                        *cp[q] = old[q] + wq * hv;
                     }
                 }
             }
