@@ -101,6 +101,7 @@ def test_synaptic_fwd_bwd_matches_oracle(dev, case):
 LAGSTEP_CASES = [SYN_CASES[i] for i in (0, 1, 2, 3, 4, 5, 6, 7, 8)] + [
     (5, 2, 64, 20.0, 1.0, {}),     # a run shorter than one 8-step block, far lags present
     (40, 3, 200, 30.0, 2.0, {}),   # several blocks, N not a multiple of the 128-wide tiles
+    (14, 2, 50, 8.0, 1.0, {'bias': True}),   # N not a multiple of 4: one neuron per LIF thread
 ]
 
 
