@@ -35,6 +35,10 @@ CASES = [
     (75, 2, 256, 32.0, 1.0, {}),
     (45, 3, 100, 12.0, 0.5, {'drop': True}),
     (37, 2, 160, 3.0, 0.0, {'bias': True, 'drop': True}),   # many sources with a lag-1 tap
+    # T * B >= 1024: the dW GEMM's k splits come in multiples of 8, so the tiles of one k
+    # chunk are grouped on one XCD (one 64-wide tile; then 2 x 2 tiles of 128)
+    (32, 32, 64, 8.0, 1.0, {}),
+    (64, 64, 256, 32.0, 1.0, {}),
 ]
 
 
