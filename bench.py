@@ -18,7 +18,8 @@ Workloads (synthetic data of the stated shape, random-init weights):
       U[0,40], sigma=4, fp32, 35-way readout
 
 Reported beside the GPU number: the roofline fraction of the dominant kernel (HIP-event
-durations on the kernels' stream during the timed steps) and a CPU baseline, the oracle's
+durations on the kernels' stream, recorded in a few extra steps after the timed ones so that
+the events do not slow the timed steps) and a CPU baseline, the oracle's
 pure-PyTorch scan with autograd BPTT timed on the host cores over a bounded sample.
 """
 
