@@ -1027,6 +1027,23 @@ __global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
     else axonal_fwd_wave_fast_body<RI, KF, 1>(p, smem);
 }
 
+// The sum over the 8 lanes of a group of a[jcg & 3] (jcg = lane mod 8, bits b1 b0): lanes i
+// and 7 - i add all four values (half-row mirror), then the quad halves them: keep two values
+// and add the partner's (lane ^ 2), keep one and add the partner's (lane ^ 1). 13 VALU in
+// place of a butterfly over all four values and a one-hot pick (16).
+__device__ __forceinline__ float reduce_scatter_4x8(float (&a)[4], bool b1, bool b0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] += dpp<0x141>(a[k]);   // row_half_mirror: lane 7 - i
+    float x0 = b1 ? a[2] : a[0], x1 = b1 ? a[3] : a[1];
+    const float y0 = b1 ? a[0] : a[2], y1 = b1 ? a[1] : a[3];
+    x0 += dpp<0x4E>(y0);                                     // quad_perm [2,3,0,1]: lane ^ 2
+    x1 += dpp<0x4E>(y1);
+    float x = b0 ? x1 : x0;
+    const float y = b0 ? x0 : x1;
+    x += dpp<0xB1>(y);                                       // quad_perm [1,0,3,2]: lane ^ 1
+    return x;
+}
+
 // The tiled backward specialised for the common regime (chosen by the host): soft taps of
 // a uniform half-width s (KF >= ceil(2s) lags of non-zero weight, one history word), the
 // ATan surrogate, decay charge, hard reset to 0, reset not detached.
@@ -1110,9 +1127,13 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled_fast
                 acc[a] = fmaf(w[a][4 * q + 3], gg.w, acc[a]);
             }
         }
+        if constexpr (RI == 4 && NJ == 8) {
+            return reduce_scatter_4x8(acc, (jcg & 2) != 0, (jcg & 1) != 0);
+        } else {
 #pragma unroll
-        for (int a = 0; a < RI; ++a) acc[a] = group_sum_t<NJ>(acc[a]);
-        return sel.pick(acc);
+            for (int a = 0; a < RI; ++a) acc[a] = group_sum_t<NJ>(acc[a]);
+            return sel.pick(acc);
+        }
     };
 
     // byte addresses walked backwards in time: gz of step t + 1, dx and gr of step t, and
