@@ -1,31 +1,42 @@
 """Benchmark of the recurrent delayed-LIF layer: forward + BPTT backward throughput.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3|C4] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C1..C5] [--extra C2,C3]
+                    [--no-cpu]
 
-One step is one forward + backward of the recurrent layer over one batch of synthetic
-input, driven by a fixed upstream gradient captured once from the full model's loss
-(projection -> recurrent layer -> readout -> time mean -> cross-entropy). Inputs, weights
-and the upstream gradient are resident in HBM before the timed region. The metric is
-neuron-timesteps per second, T * B * N / (seconds per step).
+One step is one forward + backward of every recurrent layer of the workload over one
+batch of synthetic input, each layer driven by its own fixed input and a fixed upstream
+gradient captured once from the full model's loss (projection -> recurrent layer(s), with
+the inter-layer Linear between stacked layers -> readout -> time mean -> cross-entropy).
+Inputs, weights and upstream gradients are resident in HBM before the timed region. The
+metric is neuron-timesteps per second, sum over layers of T * B * N / (seconds per step).
 
 Workloads (synthetic data of the stated shape, random-init weights):
+  C1  axonal, T=32 B=64 N=64: batch of 64 from 256 samples of 8 Bernoulli(0.1) input
+      channels, delays U[0,16], sigma=0, orthogonal W (gain 0.5), leaky-integrator readout
+      of 4 classes, fp32                         (the CPU-runnable memorisation config)
   C2  axonal, T=128 B=128 N=256, 9 analog inputs N(0,1) smoothed by a causal 5-tap mean,
       delays U[0,32], sigma=1, tau=10 (leak 0.9), threshold 1, fp32 Kaiming-uniform W,
-      6-way readout                                           (default, N=1 headline)
+      6-way readout
   C3  hybrid, T=256 B=256 N=512, 700 Bernoulli(0.02) inputs, base U[0,40] + offsets
       {0..8}, sigma=0, bf16 W / fp32 state, 20-way readout
   C4  synaptic, T=250 B=256 N=1024, 700 Bernoulli(0.02) inputs, per-connection delays
-      U[0,40], sigma=4, fp32, 35-way readout
+      U[0,40], sigma=4, fp32, 35-way readout, hidden firing about 5 %
+  C5  two stacked hybrid layers, T=1024 B=512 N=2048 each with a Linear(2048 -> 2048)
+      between them: 1 analog input U[0,1] per step, base U[0,60] + offsets {0..4}, sigma=0,
+      bf16 W / fp32 accumulate, hidden firing 2-5 % in both layers, 10-way readout
+      (default: the largest configuration that fits one GPU)
 
-Reported beside the GPU number: the roofline fraction of the dominant kernel (HIP-event
-durations on the kernels' stream, recorded in a few extra steps after the timed ones so that
-the events do not slow the timed steps) and a CPU baseline, the oracle's
-pure-PyTorch scan with autograd BPTT timed on the host cores over a bounded sample.
+Reported beside the GPU number: the roofline of the dominant time scan (HIP-event
+durations on the kernels' stream, recorded in a few extra steps after the timed ones so
+that the events do not slow the timed steps), priced against the workload's binding
+roofline (C2, C4: FP32; C3: HBM; C5: BF16 MFMA), and a CPU baseline, the oracle's
+pure-PyTorch scan with autograd BPTT timed on the host cores over bounded samples.
 """
 
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 
@@ -40,17 +51,27 @@ PEAK_FP32 = 157.3e12       # MI355X dense FP32 (vector and MFMA), flop/s
 PEAK_BF16 = 2.5e15         # MI355X dense BF16 MFMA, flop/s
 
 WORKLOADS = {
+    'C1': dict(kind='axonal', T=32, B=64, N=64, C_in=8, classes=4, dmax=16.0, sigma=0.0, tau=2.0,
+               inputs='bernoulli_pool', p_in=0.1, pool=256, gain=3.0, w_init='orthogonal',
+               w_gain=0.5, w_bf16=False, readout='li', seed=1001, bound='cpu',
+               label='recurrent axonal-delay LIF, T32 B64 N64, delays U[0,16], sigma 0, fp32, LI readout'),
     'C2': dict(kind='axonal', T=128, B=128, N=256, C_in=9, classes=6, dmax=32.0, sigma=1.0, tau=10.0,
-               inputs='analog_smoothed', gain=1.0, w_bf16=False, seed=1002,
+               inputs='analog_smoothed', gain=1.0, w_bf16=False, seed=1002, bound='fp32',
                label='recurrent axonal-delay LIF, T128 B128 N256, delays U[0,32], sigma 1, fp32'),
     'C3': dict(kind='hybrid', T=256, B=256, N=512, C_in=700, classes=20, dmax=40.0, sigma=0.0, tau=2.0,
-               inputs='bernoulli', p_in=0.02, gain=6.0, offset_max=8, w_bf16=True, seed=1003,
+               inputs='bernoulli', p_in=0.02, gain=6.0, offset_max=8, w_bf16=True, seed=1003, bound='hbm',
                label='recurrent hybrid-delay LIF, T256 B256 N512, base U[0,40] + offsets {0..8}, '
                      'sigma 0, bf16 W'),
     'C4': dict(kind='synaptic', T=250, B=256, N=1024, C_in=700, classes=35, dmax=40.0, sigma=4.0,
-               tau=2.0, inputs='bernoulli', p_in=0.02, gain=6.0, w_bf16=False, seed=1004,
+               tau=2.0, inputs='bernoulli', p_in=0.02, gain=7.5, w_bf16=False, seed=1004, bound='fp32',
                label='recurrent synaptic-delay LIF, T250 B256 N1024, delays U[0,40], sigma 4, fp32'),
+    'C5': dict(kind='hybrid', layers=2, T=1024, B=512, N=2048, C_in=1, classes=10, dmax=60.0, sigma=0.0,
+               tau=2.0, inputs='uniform', gain=2.0, gain2=12.0, offset_max=4, w_bf16=True, seed=1005,
+               bound='bf16',
+               label='two stacked recurrent hybrid-delay LIF layers, T1024 B512 N2048, base U[0,60] + '
+                     'offsets {0..4}, sigma 0, bf16 W, Linear(2048->2048) between'),
 }
+DEFAULT_CONFIG = 'C5'
 
 
 def make_config(w):
@@ -58,7 +79,8 @@ def make_config(w):
     cfg = Config()
     cfg.tau = w['tau']
     cfg.sigma_init = w['sigma']
-    cfg.init_rec_weights = 'kaiming_uniform'
+    cfg.init_rec_weights = w.get('w_init', 'kaiming_uniform')
+    cfg.rec_delay_init_gain = w.get('w_gain', cfg.rec_delay_init_gain)
     cfg.init_rec_delay = 'uniform'
     cfg.init_recdel_offset = 0.0
     cfg.max_rec_delay = w['dmax']
@@ -67,86 +89,175 @@ def make_config(w):
     return cfg
 
 
-def build(w, device):
-    """Input projection, recurrent layer, readout and the synthetic batch."""
+class Model:
+    """The workload's modules and synthetic batch: ``layers`` (recurrent), ``inter`` (the
+    Linear between stacked layers), ``readout``, ``x`` (input of the first recurrent layer,
+    already projected) and ``labels``."""
+
+
+def build(w, device, T=None, B=None):
+    """Input projection, recurrent layer(s), readout and the synthetic batch. ``T`` / ``B``
+    shorten the batch (parity tests at the workload's N, delays, sigma and W dtype); the
+    modules are the same."""
     from delrec.delay_layers import axonal_recdel, synaptic_recdel
     from delrec.networks import _reparametrize_recurrent_delay
     torch.manual_seed(0)
     cfg = make_config(w)
-    proj = torch.nn.Linear(w['C_in'], w['N'], bias=False)
-    if w['kind'] == 'axonal':
-        layer = axonal_recdel(cfg, w['N'])
-    else:
-        layer = synaptic_recdel(cfg, w['N'])
-        if w['kind'] == 'hybrid':
-            _reparametrize_recurrent_delay(layer, w['offset_max'], torch.Generator().manual_seed(123), cfg)
-    if w['w_bf16']:
-        layer.recurrent_weights = torch.nn.Parameter(layer.recurrent_weights.detach().bfloat16())
-    readout = torch.nn.Linear(w['N'], w['classes'], bias=False)
+    N = w['N']
+    proj = torch.nn.Linear(w['C_in'], N, bias=False)
+    layers, inter = [], []
+    offsets_gen = torch.Generator().manual_seed(123)      # one generator, layers in module order
+    for k in range(w.get('layers', 1)):
+        if k > 0:
+            inter.append(torch.nn.Linear(N, N, bias=False))
+        if w['kind'] == 'axonal':
+            layer = axonal_recdel(cfg, N)
+        else:
+            layer = synaptic_recdel(cfg, N)
+            if w['kind'] == 'hybrid':
+                _reparametrize_recurrent_delay(layer, w['offset_max'], offsets_gen, cfg)
+        if w['w_bf16']:
+            layer.recurrent_weights = torch.nn.Parameter(layer.recurrent_weights.detach().bfloat16())
+        layers.append(layer)
+    readout = torch.nn.Linear(N, w['classes'], bias=False)
     g = torch.Generator().manual_seed(w['seed'])
-    T, B = w['T'], w['B']
+    T = T or w['T']
+    B = B or w['B']
+    C = w['C_in']
     if w['inputs'] == 'analog_smoothed':
-        raw = torch.randn(T, B, w['C_in'], generator=g)
-        pad = torch.cat([torch.zeros(4, B, w['C_in']), raw], 0)
+        raw = torch.randn(T, B, C, generator=g)
+        pad = torch.cat([torch.zeros(4, B, C), raw], 0)
         inp = sum(pad[4 - k:4 - k + T] for k in range(5)) / 5.0
+        labels = torch.randint(w['classes'], (B,), generator=g)
+    elif w['inputs'] == 'bernoulli_pool':
+        # a batch drawn from a fixed pool of seeded samples
+        pool = (torch.rand(w['pool'], T, C, generator=g) < w['p_in']).float()
+        pool_labels = torch.randint(w['classes'], (w['pool'],), generator=g)
+        idx = torch.randperm(w['pool'], generator=torch.Generator().manual_seed(0))[:B]
+        inp = pool[idx].transpose(0, 1).contiguous()
+        labels = pool_labels[idx]
+    elif w['inputs'] == 'uniform':
+        inp = torch.rand(T, B, C, generator=g)
+        labels = torch.randint(w['classes'], (B,), generator=g)
     else:
-        inp = (torch.rand(T, B, w['C_in'], generator=g) < w['p_in']).float()
-    labels = torch.randint(w['classes'], (B,), generator=g)
-    proj, layer, readout = proj.to(device), layer.to(device), readout.to(device)
+        inp = (torch.rand(T, B, C, generator=g) < w['p_in']).float()
+        labels = torch.randint(w['classes'], (B,), generator=g)
+    proj = proj.to(device)
+    m = Model()
+    m.w, m.cfg = w, cfg
+    m.layers = [layer.to(device) for layer in layers]
+    m.inter = [lin.to(device) for lin in inter]
+    m.readout = readout.to(device)
     with torch.no_grad():
-        x = (proj(inp.to(device)) * w['gain']).contiguous()
-    return layer, readout, x, labels.to(device), cfg
+        m.x = (proj(inp.to(device)) * w['gain']).contiguous()
+    m.labels = labels.to(device)
+    return m
 
 
-def upstream_gradient(layer, readout, x, labels):
-    """dLoss/dy of the full model's loss, captured once."""
-    y = layer(x)
-    y_ = y.detach().requires_grad_(True)
-    loss = torch.nn.functional.cross_entropy(readout(y_).mean(0), labels)
-    (gy,) = torch.autograd.grad(loss, y_)
-    return y.detach(), gy.contiguous()
+def loss_of(m, y):
+    """Readout -> time mean -> cross-entropy (C1: a non-spiking leaky integrator, the
+    membrane of a LIF with an unreachable threshold, then its time mean)."""
+    logits = m.readout(y)
+    if m.w.get('readout') == 'li':
+        decay = 1.0 - 1.0 / m.w['tau']
+        v = torch.zeros_like(logits[0])
+        acc = torch.zeros_like(logits[0])
+        for t in range(logits.shape[0]):
+            v = v * decay + logits[t]
+            acc = acc + v
+        out = acc / logits.shape[0]
+    else:
+        out = logits.mean(0)
+    return torch.nn.functional.cross_entropy(out, m.labels)
+
+
+def layer_inputs(m):
+    """Each recurrent layer's fixed input and the upstream gradient dLoss/dy of the full
+    model at it (captured once), and each layer's firing rate."""
+    xs, ys = [], []
+    x = m.x
+    for k, layer in enumerate(m.layers):
+        if k > 0:
+            with torch.no_grad():
+                x = (m.inter[k - 1](ys[-1]) * m.w['gain2']).contiguous()
+        xs.append(x.detach())
+        with torch.no_grad():
+            ys.append(layer(x).detach())
+    # backward through the stack: gy of the last layer from the loss, then through each
+    # layer and Linear in turn
+    y_last = ys[-1].clone().requires_grad_(True)
+    (g,) = torch.autograd.grad(loss_of(m, y_last), y_last)
+    gys = [None] * len(m.layers)
+    gys[-1] = g.contiguous()
+    for k in range(len(m.layers) - 1, 0, -1):
+        xk = xs[k].clone().requires_grad_(True)
+        m.layers[k](xk).backward(gys[k])
+        yprev = ys[k - 1].clone().requires_grad_(True)
+        xin = m.inter[k - 1](yprev) * m.w['gain2']
+        (gprev,) = torch.autograd.grad(xin, yprev, xk.grad)
+        gys[k - 1] = gprev.contiguous()
+        m.layers[k].zero_grad(set_to_none=True)
+    firing = [float(y.mean()) for y in ys]
+    return xs, gys, firing
 
 
 def algorithmic_work(w):
-    """Algorithmic bytes and flops per neuron-timestep, for the whole fwd+BPTT and for each
-    time-scan kernel.
+    """Algorithmic bytes and flops per neuron-timestep of one layer, for the whole fwd+BPTT
+    and for each time scan.
 
-    Bytes: x read, y write, gy read, dx write in fp32 (16 B). Flops are useful MACs x 2
-    with no sparsity credit; k = non-zero triangle taps = 2(1 + sigma). Axonal and hybrid
-    (the hybrid's integer offsets only shift which step of z_j a connection reads):
-    6N + 6k in total = forward scan 2N + 2k (contraction W z, taps of z) + backward scan
-    2N + 4k (W^T gr, taps of the future gradient, delay-gradient taps) + dW GEMM 2N.
-    Synaptic: 8kN in total = forward scan 2kN + backward scan 2kN + lag GEMM 4kN.
+    Bytes: x read, y write (forward scan), gy read, dx write (backward scan), fp32: 16 B.
+    Flops are useful MACs x 2 with no sparsity credit; k = non-zero triangle taps =
+    2(1 + sigma). Axonal and hybrid (the hybrid's integer offsets only shift which step of
+    z_j a connection reads): 6N + 6k in total = forward scan 2N + 2k (contraction W z, taps
+    of z) + backward scan 2N + 4k (W^T gr, taps of the future gradient, delay-gradient taps)
+    + dW GEMM 2N. Synaptic: 8kN in total = forward scan 2kN + backward scan 2kN + lag GEMM 4kN.
     """
     N, sigma = w['N'], w['sigma']
     k = 2.0 * (1.0 + sigma)
+    scan_bytes = {'fwd': 8.0, 'bwd': 8.0}
     if w['kind'] == 'synaptic':
-        return {'bytes': 16.0, 'flops': 8.0 * k * N,
-                'scan_flops': {'syn_fwd_scan': 2.0 * k * N, 'syn_bwd_scan': 2.0 * k * N}}
-    return {'bytes': 16.0, 'flops': 6.0 * N + 6.0 * k,
-            'scan_flops': {'axonal_fwd_scan': 2.0 * N + 2.0 * k, 'axonal_bwd_scan': 2.0 * N + 4.0 * k,
-                           'syn_fwd_scan': 2.0 * N + 2.0 * k, 'syn_bwd_scan': 2.0 * N + 4.0 * k}}
+        return {'bytes': 16.0, 'flops': 8.0 * k * N, 'scan_bytes': scan_bytes,
+                'scan_flops': {'fwd': 2.0 * k * N, 'bwd': 2.0 * k * N}}
+    return {'bytes': 16.0, 'flops': 6.0 * N + 6.0 * k, 'scan_bytes': scan_bytes,
+            'scan_flops': {'fwd': 2.0 * N + 2.0 * k, 'bwd': 2.0 * N + 4.0 * k}}
 
 
-# kernel symbol of each time-scan kind at each workload's shape (for the rocprof summaries)
+def peak_of(w):
+    return {'fp32': PEAK_FP32, 'bf16': PEAK_BF16, 'hbm': PEAK_HBM}.get(w['bound'])
+
+
+# kernel symbol of each time-scan kind at each workload's shape (for the rocprof summaries);
+# a sequence is a scan run as per-step launches, timed as a whole
 SCAN_SYMBOL = {
+    'C1': {'axonal_fwd_scan': 'axonal_fwd_wave_fast', 'axonal_bwd_scan': 'axonal_bwd_tiled_fast'},
     'C2': {'axonal_fwd_scan': 'axonal_fwd_wave_fast', 'axonal_bwd_scan': 'axonal_bwd_tiled_fast'},
     'C3': {'syn_fwd_scan': 'syn_fwd_scatter', 'syn_bwd_scan': 'syn_bwd_hyb'},
-    # C4's scans are sequences of launches (per 8-step block one lagblock_kernel, per step one
-    # lagstep_gemm_kernel + one LIF kernel): the scan time is the whole sequence's
     'C4': {'syn_fwd_scan': 'lagstep_fwd_sequence', 'syn_bwd_scan': 'lagstep_bwd_sequence'},
+    'C5': {'syn_fwd_scan': 'hybstep_fwd_sequence', 'syn_bwd_scan': 'hybstep_bwd_sequence'},
 }
 
 
+def cpu_model():
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or 'unknown'
+
+
 def cpu_baseline(layer, x, w, budget_s=25.0):
-    """The oracle (pure-PyTorch v2 scan, autograd BPTT, fp32) on the host cores, on a
-    bounded sample of the same workload: the layer's own weights and delays and the first
-    T' steps of the same input at full B and N, scaled to neuron-timesteps/s."""
+    """The oracle (pure-PyTorch v2 scan, autograd BPTT, fp32) on the host cores, on bounded
+    samples of the same workload: the layer's own weights and delays and the first T' steps
+    of the same input at full B and N, scaled to neuron-timesteps/s. Two sample lengths
+    T' and 2T' check that the time per step does not depend on T' (the scaling assumed)."""
     from oracle import neuron as oneuron, scans
     from oracle.delays import hybrid_delays
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    cores = max(1, len(os.sched_getaffinity(0)))
     torch.set_num_threads(cores)
-    T, B, N = w['T'], w['B'], w['N']
+    T, B, N = x.shape
     lif = oneuron.LIFParams(tau=w['tau'])
     W = layer.recurrent_weights.detach().float().cpu()
     if w['kind'] == 'axonal':
@@ -169,20 +280,27 @@ def cpu_baseline(layer, x, w, budget_s=25.0):
         y.sum().backward()
         return time.perf_counter() - t0
 
-    Tp = min(T, 16)
+    # T': the whole run where it fits the budget, else the longest power of two (>= 8) whose
+    # runs fit; then T' / 2 for the linearity check
+    Tp = min(T, 8)
     t_probe = one(Tp)
-    # grow the sample while 3 timed runs stay within the budget (the probe is the warmup)
-    while Tp < T and t_probe * 2 * 3 < budget_s:
+    while Tp < T and t_probe * (2 if 2 * Tp <= T else T / Tp) * 4 < budget_s:
         Tp = min(T, Tp * 2)
         t_probe = one(Tp)
-    times = sorted(one(Tp) for _ in range(3))
-    t_med = times[1]
-    nts = Tp * B * N / t_med
+    Th = max(1, Tp // 2)
+    t_full = sorted(one(Tp) for _ in range(2))[0]
+    t_half = sorted(one(Th) for _ in range(2))[0]
+    nts = Tp * B * N / t_full
+    per_step_full, per_step_half = t_full / Tp, t_half / Th
     return {'value': nts, 'unit': 'neuron-timesteps/s', 'cores': cores, 'kind': 'port',
+            'cpu_model': cpu_model(),
             'sample': f'oracle v2 scan + autograd BPTT, fp32, same weights/delays/input, full B={B} '
-                      f'N={N}, first {Tp} of T={T} steps, median of 3 (after a warmup), scaled per '
-                      f'neuron-timestep',
-            'seconds_per_sample': t_med}
+                      f'N={N}, first {Tp} of T={T} steps (best of 2 after a warmup), scaled per '
+                      f'neuron-timestep; one layer (stacked layers have the same shape)',
+            'seconds_per_sample': t_full,
+            'linearity': {'T_short': Th, 'T_long': Tp, 's_per_step_short': per_step_half,
+                          's_per_step_long': per_step_full,
+                          'ratio': per_step_full / per_step_half}}
 
 
 def calibrate_copy(mib):
@@ -201,16 +319,109 @@ def load_traffic(kernel, config):
     p = os.path.join(ROOT, 'profiles', f'traffic_{kernel}_{config}.json')
     if os.path.exists(p):
         with open(p) as f:
-            return json.load(f).get('bytes_per_launch')
-    return None
+            return json.load(f).get('bytes_per_launch'), os.path.relpath(p, ROOT)
+    return None, None
+
+
+def measure(name, steps, warmup, with_cpu):
+    """Time one workload; returns its JSON record."""
+    from delrec import _lib
+    w = WORKLOADS[name]
+    dev = torch.device('cuda:0')
+    m = build(w, dev)
+    xs, gys, firing = layer_inputs(m)
+    T, B, N = xs[0].shape
+    nl = len(m.layers)
+    xins = [x.detach().clone().requires_grad_(True) for x in xs]
+
+    def step():
+        for layer, xin, gy in zip(m.layers, xins, gys):
+            layer.zero_grad(set_to_none=True)
+            xin.grad = None
+            layer(xin).backward(gy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / steps
+    # per scan kernel (HIP events on the kernels' stream) and per entry point (scan +
+    # reductions + GEMMs), from a few extra steps outside the timed region: the event
+    # pairs would otherwise add their own gaps to the timed steps
+    n_extra = min(3, max(1, steps))
+    with _lib.scan_timing(2 * n_extra * nl + 8) as scans_t:
+        for _ in range(n_extra):
+            step()
+        torch.cuda.synchronize()
+    with _lib.timing() as rec:
+        for _ in range(n_extra):
+            step()
+        torch.cuda.synchronize()
+    per_entry, per_scan = {}, {}
+    for ename, s, e in rec:
+        per_entry.setdefault(ename, []).append(s.elapsed_time(e))
+    for kind, dt in scans_t.launches:
+        per_scan.setdefault(kind, []).append(dt)
+    avg = {k: sum(v) / len(v) for k, v in per_entry.items()}
+    scan_avg = {k: sum(v) / len(v) for k, v in per_scan.items()}
+    nt_layer = T * B * N
+    value = nl * nt_layer / (ms * 1e-3)
+    work = algorithmic_work(w)
+    peak = peak_of(w)
+    t_bound = None
+    if w['bound'] != 'cpu':
+        peak_c = PEAK_BF16 if w['bound'] == 'bf16' else PEAK_FP32
+        t_bound = nl * max(work['bytes'] * nt_layer / PEAK_HBM, work['flops'] * nt_layer / peak_c)
+
+    # the dominant kernel: the time scan with the longest average launch, priced against
+    # the workload's binding roofline (algorithmic bytes for HBM, flops otherwise)
+    dom = max(scan_avg, key=scan_avg.get)
+    dur = scan_avg[dom] * 1e-3
+    direction = 'fwd' if dom.endswith('fwd_scan') else 'bwd'
+    kernel = SCAN_SYMBOL[name][dom]
+    traffic, traffic_src = load_traffic(kernel, name)
+    if w['bound'] == 'hbm':
+        per_launch = work['scan_bytes'][direction] * nt_layer
+        roof = {'bound': 'hbm', 'achieved': per_launch / dur / 1e9, 'peak': PEAK_HBM / 1e9, 'unit': 'GB/s',
+                'frac': per_launch / dur / PEAK_HBM, 'bytes_per_launch': per_launch}
+    else:
+        per_launch = work['scan_flops'][direction] * nt_layer
+        pk = PEAK_BF16 if w['bound'] == 'bf16' else PEAK_FP32
+        roof = {'bound': 'mfma', 'achieved': per_launch / dur / 1e12, 'peak': pk / 1e12, 'unit': 'TFLOP/s',
+                'frac': per_launch / dur / pk, 'flops_per_launch': per_launch}
+    roof.update({'traffic': traffic, 'traffic_source': traffic_src, 'kernel': kernel,
+                 'avg_launch_ms': scan_avg[dom]})
+    line = {
+        'workload': f"{name}: {w['label']}",
+        'value': value,
+        'ms_per_step': ms,
+        'layers': nl,
+        'T': T, 'B': B, 'N': N,
+        'delay_kind': w['kind'], 'sigma': w['sigma'], 'firing_rate': firing,
+        'roofline': roof,
+        'layer_roofline': None if t_bound is None else {
+            'bound': w['bound'], 't_bound_ms': t_bound * 1e3, 'frac': t_bound / (ms * 1e-3),
+            'bytes_per_nt': work['bytes'], 'flops_per_nt': work['flops']},
+        'scan_ms': scan_avg,
+        'entry_ms': avg,
+        'per_layer_value': nt_layer / (ms * 1e-3 / nl),
+    }
+    if with_cpu:
+        line['cpu_baseline'] = cpu_baseline(m.layers[0], xs[0], w)
+    return line
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=20)
-    ap.add_argument('--warmup', type=int, default=3)
-    ap.add_argument('--config', default='C2', choices=sorted(WORKLOADS))
+    ap.add_argument('--steps', type=int, default=10)
+    ap.add_argument('--warmup', type=int, default=2)
+    ap.add_argument('--config', default=DEFAULT_CONFIG, choices=sorted(WORKLOADS))
+    ap.add_argument('--extra', default='', help='comma-separated further workloads reported under "extra"')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--calibrate-copy', type=int, metavar='MIB', default=0,
                     help='only run a plain device copy of MIB MiB (counter calibration)')
@@ -223,90 +434,40 @@ def main():
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
         return
-    w = WORKLOADS[args.config]
-    dev = torch.device('cuda:0')
     from delrec import _lib
     _lib.load()
-    layer, readout, x, labels, cfg = build(w, dev)
-    T, B, N = w['T'], w['B'], w['N']
-    y0, gy = upstream_gradient(layer, readout, x, labels)
-    firing = float(y0.mean())
-    xin = x.detach().requires_grad_(True)
-
-    def step():
-        layer.zero_grad(set_to_none=True)
-        xin.grad = None
-        y = layer(xin)
-        y.backward(gy)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms = (t1 - t0) * 1e3 / args.steps
-    # per scan kernel (HIP events on the kernels' stream) and per entry point (scan +
-    # reductions + GEMMs), from a few extra steps outside the timed region: the event
-    # pairs would otherwise add their own gaps to the timed steps
-    n_extra = min(5, args.steps)
-    with _lib.scan_timing(2 * n_extra + 8) as scans_t:
-        for _ in range(n_extra):
-            step()
-        torch.cuda.synchronize()
-    with _lib.timing() as rec:
-        for _ in range(n_extra):
-            step()
-        torch.cuda.synchronize()
-    per_entry, per_scan = {}, {}
-    for name, s, e in rec:
-        per_entry.setdefault(name, []).append(s.elapsed_time(e))
-    for kind, dt in scans_t.launches:
-        per_scan.setdefault(kind, []).append(dt)
-    avg = {k: sum(v) / len(v) for k, v in per_entry.items()}
-    scan_avg = {k: sum(v) / len(v) for k, v in per_scan.items()}
-    nt = T * B * N
-    value = nt / (ms * 1e-3)
-    work = algorithmic_work(w)
-    peak_c = PEAK_BF16 if (w['w_bf16'] and w['kind'] != 'synaptic') else PEAK_FP32
-    t_bound = max(work['bytes'] * nt / PEAK_HBM, work['flops'] * nt / peak_c)
-
-    # the dominant kernel: the time-scan kernel with the longest average launch
-    dom = max(scan_avg, key=scan_avg.get)
-    dur = scan_avg[dom] * 1e-3
-    flops = work['scan_flops'][dom] * nt
-    achieved = flops / dur
-    kernel = SCAN_SYMBOL[args.config][dom]
-    traffic = load_traffic(kernel, args.config)
+    rec = measure(args.config, args.steps, args.warmup, not args.no_cpu)
+    w = WORKLOADS[args.config]
     line = {
-        'metric': 'neuron-timesteps/sec fwd+BPTT per recurrent layer',
-        'value': value,
+        'metric': 'neuron-timesteps/sec fwd+BPTT per recurrent layer; % HBM GB/s or MFMA peak',
+        'value': rec['value'],
         'unit': 'neuron-timesteps/s',
         'n_gpus': 1,
         'steps': args.steps,
         'warmup': args.warmup,
-        'ms_per_step': ms,
+        'ms_per_step': rec['ms_per_step'],
         'higher_is_better': True,
         'scaling': 'weak',
         'vs_baseline': None,
         'dtype': 'bf16-weights/f32' if w['w_bf16'] else 'f32',
         'data': 'synthetic (seeded inputs of the stated shape, random-init weights)',
-        'config': {'workload': f"{args.config}: {w['label']}", 'T': T, 'B': B, 'N': N,
-                   'delay_kind': w['kind'], 'sigma': w['sigma'], 'firing_rate': firing},
-        'roofline': {'bound': 'mfma', 'achieved': achieved / 1e12, 'peak': PEAK_FP32 / 1e12,
-                     'unit': 'TFLOP/s', 'frac': achieved / PEAK_FP32, 'traffic': traffic,
-                     'kernel': kernel, 'avg_launch_ms': scan_avg[dom],
-                     'flops_per_launch': flops},
-        'layer_roofline': {'t_bound_ms': t_bound * 1e3, 'frac': t_bound / (ms * 1e-3),
-                           'bytes_per_nt': work['bytes'], 'flops_per_nt': work['flops']},
-        'scan_ms': scan_avg,
+        'config': {'workload': rec['workload'], 'layers': rec['layers'], 'T': rec['T'], 'B': rec['B'],
+                   'N': rec['N'], 'delay_kind': rec['delay_kind'], 'sigma': rec['sigma'],
+                   'firing_rate': rec['firing_rate']},
+        'roofline': rec['roofline'],
+        'layer_roofline': rec['layer_roofline'],
+        'per_layer_value': rec['per_layer_value'],
+        'scan_ms': rec['scan_ms'],
+        'entry_ms': rec['entry_ms'],
     }
-    if avg:
-        line['entry_ms'] = avg
-    if not args.no_cpu:
-        line['cpu_baseline'] = cpu_baseline(layer, x, w)
+    if 'cpu_baseline' in rec:
+        line['cpu_baseline'] = rec['cpu_baseline']
+    extra = [c for c in args.extra.split(',') if c]
+    if extra:
+        line['extra'] = {}
+        for c in extra:
+            print(f'[bench] extra workload {c}', file=sys.stderr, flush=True)
+            line['extra'][c] = measure(c, args.steps, args.warmup, not args.no_cpu)
     print(json.dumps(line), flush=True)
 
 

@@ -20,9 +20,10 @@ Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``b
 may import this package, and only as the checker or the timed CPU baseline. The product
 (``snn-delays_amd/delrec``) never imports it and has no CPU fallback.
 
-Pinning status of each function is stated in its docstring. Functions pinned by closed
-forms, known-answer inputs from the reference's own tests, invariants or golden vectors
-written by the reference's own ``v2`` code are listed in ``tests/test_oracle_*.py``.
+Pinning status of each function is stated in its docstring. The pins -- closed forms,
+the known-answer inputs of the reference's own tests, invariants and hand-derived golden
+vectors (``tests/golden/make_fixtures.py``; no reference code is run) -- are in
+``tests/test_oracle_*.py``.
 Parity unpinned: the spikingjelly LIF op order for ``v_reset != 0`` and ``decay_input``
 (spikingjelly is not installed; the restatement follows its published source).
 """

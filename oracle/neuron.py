@@ -96,9 +96,15 @@ def lif_initial_v(p, like):
     return torch.full_like(like, v0)
 
 
-def lif_step(p, x, v):
+def lif_step(p, x, v, forced=None):
     """One single-step LIF update. Returns ``(spike, h, v_next)``; ``h`` is the pre-reset
-    membrane the BPTT needs."""
+    membrane the BPTT needs.
+
+    ``forced`` (teacher forcing, a test device of this oracle, not of the reference): the
+    spike takes the given 0/1 values instead of ``h >= v_threshold`` while its gradient is
+    still the surrogate's at ``h``; the reset uses the forced spike. A run forced with a
+    kernel's own spike train follows that train's membrane trajectory exactly, so the
+    kernel's spikes can be checked at every step against ``h >= v_threshold`` of that run."""
     tau = p.tau
     reset0 = p.v_reset is None or p.v_reset == 0.0
     if p.decay_input:
@@ -106,6 +112,8 @@ def lif_step(p, x, v):
     else:
         h = v * (1.0 - 1.0 / tau) + x if reset0 else v - (v - p.v_reset) / tau + x
     spike = p.fire(h)
+    if forced is not None:
+        spike = spike + (forced.to(spike.dtype) - spike).detach()
     spike_d = spike.detach() if p.detach_reset else spike
     if p.v_reset is None:
         v_next = h - spike_d * p.v_threshold

@@ -21,8 +21,9 @@ Each function returns ``(y, extras)`` with ``extras = {'u': pre-reset membranes,
 'rec': recurrent inputs before dropout, 'L': window length}``.
 Pinned by: the closed-form delay semantics and triangle weights, W = 0 closed forms,
 v1 == v2, hybrid(offsets=0) == axonal, broadcast synaptic == axonal, integer-offset time
-shift, an independent hand-written scalar BPTT (tests/test_oracle_*.py), and golden
-vectors written by the reference's own v2 code (tests/golden/).
+shift, an independent hand-written scalar BPTT (tests/test_oracle_*.py), and hand-derived
+golden vectors (tests/golden/, written by tests/golden/make_fixtures.py from closed forms;
+nothing of the reference is run).
 """
 
 import torch
@@ -40,9 +41,10 @@ def _drop(drop, B, N, like):
 
 
 def axonal_v2(x, W, d, lif, sigma=0.0, bias=None, drop=None, p_spread=None,
-              use_sig_p=False, round_delays=False):
+              use_sig_p=False, round_delays=False, forced=None):
     """Dense sliding-window axonal scan. ``drop`` is the fixed ``(B, N)`` recurrent
-    dropout multiplier (ones when off), applied to ``rec`` (after the bias)."""
+    dropout multiplier (ones when off), applied to ``rec`` (after the bias). ``forced``: an
+    optional ``(T, B, N)`` spike train the neurons are teacher-forced with (``lif_step``)."""
     T, B, N = x.shape
     d = _ste_round(d.to(x.dtype), round_delays)
     mask, L = axonal_mask(d, sigma, p_spread, use_sig_p)        # (N, L)
@@ -61,7 +63,7 @@ def axonal_v2(x, W, d, lif, sigma=0.0, bias=None, drop=None, p_spread=None,
         if bias is not None:
             rec = rec + bias
         recs.append(rec)
-        y, h, v = lif_step(lif, x[t] + rec * m, v)
+        y, h, v = lif_step(lif, x[t] + rec * m, v, None if forced is None else forced[t])
         if L >= 2:
             window = torch.cat([window[..., 1:], y.unsqueeze(-1)], dim=-1)
         ys.append(y)
@@ -70,10 +72,10 @@ def axonal_v2(x, W, d, lif, sigma=0.0, bias=None, drop=None, p_spread=None,
 
 
 def synaptic_v2(x, W, d, lif, sigma=0.0, bias=None, drop=None, p_spread=None,
-                use_sig_p=False, round_delays=False):
+                use_sig_p=False, round_delays=False, forced=None):
     """Dense sliding-window synaptic scan: one ``B x N(L-1)`` by ``N(L-1) x N`` product per
     step against the lag-reversed ``W * h`` stack. Hybrid delays are passed materialised,
-    ``d = base[None, :] + offsets``."""
+    ``d = base[None, :] + offsets``. ``forced``: as in ``axonal_v2``."""
     T, B, N = x.shape
     d = _ste_round(d.to(x.dtype), round_delays)
     mask, L = syn_mask(d, sigma, p_spread, use_sig_p)           # (N, N, L)
@@ -91,7 +93,7 @@ def synaptic_v2(x, W, d, lif, sigma=0.0, bias=None, drop=None, p_spread=None,
         if bias is not None:
             rec = rec + bias
         recs.append(rec)
-        y, h, v = lif_step(lif, x[t] + rec * m, v)
+        y, h, v = lif_step(lif, x[t] + rec * m, v, None if forced is None else forced[t])
         if L >= 2:
             window = torch.cat([window[..., 1:], y.unsqueeze(-1)], dim=-1)
         ys.append(y)

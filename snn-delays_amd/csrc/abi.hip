@@ -49,26 +49,24 @@ struct Counter {
 // dynamic LDS a launch may request: the per-workgroup limit less 1 KB, which holds the
 // kernels' own static LDS (a __syncthreads_or takes 256 bytes)
 int max_lds_bytes() {
-    static int cached = -1;
-    if (cached < 0) {
+    static const int cached = [] {
         int dev = 0, v = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
             v = 65536;
-        cached = v - 1024;
-    }
+        return v - 1024;
+    }();
     return cached;
 }
 
 int num_cus() {
-    static int cached = -1;
-    if (cached < 0) {
+    static const int cached = [] {
         int dev = 0, v = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             v = 256;
-        cached = v;
-    }
+        return v;
+    }();
     return cached;
 }
 
@@ -161,14 +159,10 @@ bool getenv_flag_off(const char* name) {
 }
 
 // The spike-driven forward (axonal_fwd_wave) serves N <= 256 unless DELREC_AXONAL_FWD=tiled
-// selects the dense tiled scan (kept for comparison).
+// selects the dense tiled scan (kept for comparison; read on every call).
 bool axonal_fwd_wave_on() {
-    static int on = -1;
-    if (on < 0) {
-        const char* e = getenv("DELREC_AXONAL_FWD");
-        on = (e && strcmp(e, "tiled") == 0) ? 0 : 1;
-    }
-    return on == 1;
+    const char* e = getenv("DELREC_AXONAL_FWD");
+    return !(e && strcmp(e, "tiled") == 0);
 }
 
 // k splits of the dW GEMM: about one 128x128-tile workgroup per CU (the delay-gradient
@@ -482,7 +476,11 @@ int max_slot(uint32_t& t, unsigned long long*& dslot) {
 }  // namespace
 
 void delrec::ensure_lds(const void* fn, size_t bytes) {
+    // launches may come from several host threads (the autograd engine runs backward passes
+    // on its own device thread)
+    static std::mutex mu;
     static std::vector<std::pair<const void*, size_t>> done;
+    std::lock_guard<std::mutex> lock(mu);
     for (auto& e : done)
         if (e.first == fn) {
             if (e.second >= bytes) return;

@@ -1012,16 +1012,39 @@ __global__ void __launch_bounds__(TiledThreads<RI>::value) axonal_bwd_tiled(AxBw
 // neuron's lags of non-zero weight fit, else four words (256 lags). When the caller asked
 // for max d on the host, workgroup 0 first writes it into the readback slot (the store's
 // trip to host memory then overlaps the scan).
+//
+// Without a window length from the caller (L = 0) a neuron with a lag of non-zero weight
+// beyond 256 cannot be held: the scan then writes NaN into y, u (and z) instead of dropping
+// those taps, and posts NaN as max d, which the backward's window-length read rejects.
+// (Every workgroup tests all N neurons, so the decision is the same in all of them.)
 template <int RI, int KF>
 __global__ void __launch_bounds__(512) axonal_fwd_wave_fast(AxFwd p) {
     extern __shared__ float smem[];
-    if (p.mx_slot && blockIdx.x == 0) block_max_to_host(p.d, p.N, p.mx_ticket, p.mx_slot);
     const int l = threadIdx.x & 63, i = 32 * (threadIdx.x >> 6) + l;
-    bool longer = false;
+    bool longer = false, beyond = false;
     if (l < 32 && i < p.N) {
         const float c = 1.0f + p.d[i];
-        const int lof = max(1, (int)floorf(c - p.s_uniform) + 1);
+        const float s = p.s_uniform, s2 = s * s;
+        const int lof = max(1, (int)floorf(c - s) + 1);
         longer = lof + KF - 1 > 64;
+#pragma unroll
+        for (int q = 0; q < KF; ++q) {
+            const int lq = lof + q;
+            beyond |= p.L == 0 && lq > 256 && tri_weight((float)lq, c, s, s2) > 0.0f;
+        }
+    }
+    beyond = __syncthreads_or(beyond);
+    if (p.mx_slot && blockIdx.x == 0) block_max_to_host(p.d, p.N, p.mx_ticket, p.mx_slot, beyond);
+    if (beyond) {
+        const float nan = __builtin_nanf("");
+        const size_t BN = (size_t)p.B * p.N;
+        for (size_t q = threadIdx.x; q < (size_t)p.T * p.N; q += blockDim.x) {
+            const size_t t = q / p.N, o = t * BN + (size_t)blockIdx.x * p.N + (q - t * p.N);
+            p.y[o] = nan;
+            p.u[o] = nan;
+            if (p.z) p.z[o] = nan;
+        }
+        return;
     }
     if (__syncthreads_or(longer)) axonal_fwd_wave_fast_body<RI, KF, 4>(p, smem);
     else axonal_fwd_wave_fast_body<RI, KF, 1>(p, smem);

@@ -260,8 +260,10 @@ constexpr int kMaxTaps = 8;   // register-resident tap weights per neuron (fast 
 // 8-byte system-scope store: a host reader sees either the old pair or the new one. Every
 // thread of the workgroup (a multiple of 64 threads, at most 1024) calls it: it holds a
 // barrier.
+// With `poison` the posted value is NaN whatever x holds (a caller that found the
+// maximum unusable, e.g. a window its kernel cannot hold).
 __device__ __forceinline__ void block_max_to_host(const float* x, int n, uint32_t ticket,
-                                                  unsigned long long* slot) {
+                                                  unsigned long long* slot, bool poison = false) {
     __shared__ float wmax[16];
     float m = -INFINITY;
     int nan = 0;
@@ -277,7 +279,7 @@ __device__ __forceinline__ void block_max_to_host(const float* x, int n, uint32_
     if (threadIdx.x == 0) {
         float r = wmax[0];
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = fmaxf(r, wmax[w]);
-        if (nan) r = __builtin_nanf("");
+        if (nan || poison) r = __builtin_nanf("");
         const unsigned long long v = (unsigned long long)ticket | ((unsigned long long)__float_as_uint(r) << 32);
         __hip_atomic_store(slot, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }

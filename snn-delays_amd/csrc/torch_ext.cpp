@@ -128,6 +128,10 @@ struct AxonalCommon : public torch::autograd::Function<AxonalCommon> {
                   N = (int)ctx->saved_data["N"].toInt();
         const double sigma = ctx->saved_data["sigma"].toDouble();
         const float d_max = take_max(ctx->saved_data["ticket"].toInt(), dc);
+        // NaN: a NaN delay, or a window the forward could not hold (it wrote NaN outputs)
+        if (!(d_max == d_max))
+            throw std::runtime_error("axonal_common backward: the delay window exceeds the 256 lags the "
+                                     "forward holds without a window length, or a delay is NaN");
         const int L = std::max(window_length(d_max, (float)(1.0 + sigma)), 2);
         const bool w_bf16 = Wc.scalar_type() == at::kBFloat16;
         const auto f32 = u.options();

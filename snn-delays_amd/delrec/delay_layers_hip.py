@@ -51,10 +51,7 @@ class AxonalHipScans:
             d_in = d_in + (d_in.round() - d_in).detach()
         nm = self.neuron_module
         ext = _lib.torch_ext()
-        if (ext is not None and not approx and not ste_mode and not self.use_sig_p and N <= 256
-                and x_seq.numel() <= STRAIGHT_LINE_MAX_ELEMS and x_seq.dtype == torch.float32 and nm.v_reset is not None and float(nm.v_reset) == 0.0
-                and not getattr(nm, 'decay_input', False) and 0.0 <= float(self.sigma) <= 3.0
-                and os.environ.get('DELREC_AXONAL_FWD') != 'tiled'):
+        if ext is not None and self._cpp_function_applies(x_seq, d_in, bias, approx, ste_mode):
             # the common regime: the C++ autograd Function over the same C ABI (no Python on
             # the forward or backward path, no window-length read in the forward)
             y = ext.axonal_common(x_seq, self.recurrent_weights, d_in, bias, drop, float(self.sigma),
@@ -68,6 +65,24 @@ class AxonalHipScans:
         if self.store_v_seq:
             self.v_seq = None
         return y
+
+    def _cpp_function_applies(self, x_seq, d_in, bias, approx, ste_mode):
+        """Whether the call takes the C++ autograd Function: the common regime (soft taps of
+        a uniform half-width up to 8 lags of non-zero weight, decay charge, hard reset to 0,
+        N <= 256) and gradients wanted. Its forward does not read the window length (its
+        backward does, and rejects a window the forward could not hold); without gradients
+        the Python Function reads the window length first, so an over-long window raises at
+        the forward."""
+        nm = self.neuron_module
+        N = x_seq.shape[-1]
+        wants_grad = torch.is_grad_enabled() and (
+            x_seq.requires_grad or self.recurrent_weights.requires_grad or d_in.requires_grad
+            or (bias is not None and bias.requires_grad))
+        return (wants_grad and not approx and not ste_mode and not self.use_sig_p and N <= 256
+                and x_seq.numel() <= STRAIGHT_LINE_MAX_ELEMS and x_seq.dtype == torch.float32
+                and nm.v_reset is not None and float(nm.v_reset) == 0.0
+                and not getattr(nm, 'decay_input', False) and 0.0 <= float(self.sigma) <= 3.0
+                and os.environ.get('DELREC_AXONAL_FWD') != 'tiled')
 
     def _axonal_function(self, x_seq, d_in, bias, drop, p_spread, sid, gamma, alpha, approx, ste_mode):
         nm = self.neuron_module

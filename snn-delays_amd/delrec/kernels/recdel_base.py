@@ -128,7 +128,13 @@ class AxonalRecdelHip(torch.autograd.Function):
         u, z, bits, Wc, dc, s_vec, m, lag, p_spread = ctx.saved_tensors
         T, B, N, L, w_bf16, sigma, use_sig_p, mode, w_dtype = ctx.meta
         if isinstance(L, _lib.PostedMax):
-            L = max(window_length_f32(L.value(), 1.0 + sigma), 2)
+            d_max = L.value()
+            if d_max != d_max:
+                # a NaN delay, or a window the forward could not hold without its length
+                # (it then wrote NaN outputs)
+                raise _lib.DelrecError('delrec_axonal_bwd', _lib.DELREC_ERR_WINDOW,
+                                       'delay window beyond the 256 lags the forward holds, or a NaN delay')
+            L = max(window_length_f32(d_max, 1.0 + sigma), 2)
         dev = u.device
         gy = gy.to(torch.float32).contiguous()
         need_W, need_b, need_d = ctx.needs_input_grad[1], ctx.needs_input_grad[2], ctx.needs_input_grad[3]

@@ -218,3 +218,27 @@ def test_straight_line_forward_keeps_outputs_within_32_bit_offsets():
     assert _straight_line_forward(*args, TB=STRAIGHT_LINE_MAX_ELEMS // 256)
     assert not _straight_line_forward(*args, TB=STRAIGHT_LINE_MAX_ELEMS // 256 + 1)
     assert not _straight_line_forward(257, 1.0, False, False, 0, False, 0.0, TB=1)
+
+
+def test_cpp_function_only_when_gradients_are_wanted():
+    """The C++ autograd Function's forward does not read the window length (its backward
+    rejects a window the forward could not hold), so it is taken only when gradients are
+    wanted; without them the Python Function reads the window first and raises on an
+    over-long one."""
+    from delrec.delay_layers import axonal_recdel
+    cfg = base_config(0)
+    cfg.sigma_init = 1.0
+    layer = axonal_recdel(cfg, 32)
+    x = torch.zeros(T, B, 32)
+    d = layer.recurrent_delays
+    assert layer._cpp_function_applies(x.requires_grad_(True), d, None, False, 0)
+    assert layer._cpp_function_applies(torch.zeros(T, B, 32), d, None, False, 0)   # W, d require grad
+    with torch.no_grad():
+        assert not layer._cpp_function_applies(x, d, None, False, 0)
+    for p in layer.parameters():
+        p.requires_grad_(False)
+    assert not layer._cpp_function_applies(torch.zeros(T, B, 32), d, None, False, 0)
+    for p in layer.parameters():
+        p.requires_grad_(True)
+    assert not layer._cpp_function_applies(x, d, None, True, 0)      # approx
+    assert not layer._cpp_function_applies(x, d, None, False, 1)     # STE

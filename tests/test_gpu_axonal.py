@@ -197,3 +197,33 @@ def test_axonal_forward_posts_max_delay(dev, fused):
     out = ctypes.c_float(0.0)
     assert _lib.load().delrec_max_take(ticket.value, ctypes.byref(out), 5000) == 0
     assert out.value == float(ds.max())
+
+
+@pytest.mark.gpu
+def test_window_beyond_256_lags_fails_loudly(dev):
+    """Delays whose taps reach past 256 lags: the forward without a window length cannot hold
+    them. Under gradients (the C++ Function) it writes NaN outputs and the backward raises;
+    without gradients the Python Function reads the window length and raises at once."""
+    from delrec.delay_layers import axonal_recdel
+    from delrec import _lib
+    from configs.perf_MEM import Config
+    cfg = Config()
+    cfg.sigma_init = 0.5
+    torch.manual_seed(0)
+    layer = axonal_recdel(cfg, 64).to(dev)
+    with torch.no_grad():
+        layer.recurrent_delays[5] = 300.0
+    x = torch.randn(20, 2, 64, generator=gen(3)).to(dev)
+    print('no_grad forward', flush=True)
+    with torch.no_grad():
+        with pytest.raises(_lib.DelrecError) as err:
+            layer(x)
+    assert err.value.status == _lib.DELREC_ERR_WINDOW
+    print('forward + backward with gradients', flush=True)
+    xg = x.clone().requires_grad_(True)
+    y = layer(xg)
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(y).all()), 'the forward must not return spikes it could not compute'
+    with pytest.raises(Exception, match='256 lags'):
+        y.sum().backward()
+    torch.cuda.synchronize()
