@@ -63,10 +63,10 @@ WORKLOADS = {
                label='recurrent hybrid-delay LIF, T256 B256 N512, base U[0,40] + offsets {0..8}, '
                      'sigma 0, bf16 W'),
     'C4': dict(kind='synaptic', T=250, B=256, N=1024, C_in=700, classes=35, dmax=40.0, sigma=4.0,
-               tau=2.0, inputs='bernoulli', p_in=0.02, gain=7.5, w_bf16=False, seed=1004, bound='fp32',
+               tau=2.0, inputs='bernoulli', p_in=0.02, gain=7.0, w_bf16=False, seed=1004, bound='fp32',
                label='recurrent synaptic-delay LIF, T250 B256 N1024, delays U[0,40], sigma 4, fp32'),
     'C5': dict(kind='hybrid', layers=2, T=1024, B=512, N=2048, C_in=1, classes=10, dmax=60.0, sigma=0.0,
-               tau=2.0, inputs='uniform', gain=2.0, gain2=12.0, offset_max=4, w_bf16=True, seed=1005,
+               tau=2.0, inputs='uniform', gain=1.0, gain2=8.0, offset_max=4, w_bf16=True, seed=1005,
                bound='bf16',
                label='two stacked recurrent hybrid-delay LIF layers, T1024 B512 N2048, base U[0,60] + '
                      'offsets {0..4}, sigma 0, bf16 W, Linear(2048->2048) between'),

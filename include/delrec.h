@@ -148,6 +148,13 @@ typedef struct {
     uint32_t* bits;
     void* workspace;
     size_t workspace_bytes;
+    /* hybrid only (0 otherwise): the offset range and the smallest delay, for the
+     * offset-stacked scans, which apply when off_count > 0 (off_count = largest - smallest
+     * offset + 1, at most 16) and d_min >= s_uniform - 1 (every tap at a lag >= 1). The
+     * caller reads them with the window length (d_min = min over base[j] + offsets[i,j]). */
+    float d_min;
+    int32_t off_min;
+    int32_t off_count;
 } delrec_syn_fwd_args;
 
 typedef struct {
@@ -173,6 +180,9 @@ typedef struct {
     float* db;                   /* out (N) or NULL                                      */
     void* workspace;
     size_t workspace_bytes;
+    float d_min;                 /* hybrid: as in delrec_syn_fwd_args                    */
+    int32_t off_min;
+    int32_t off_count;
 } delrec_syn_bwd_args;
 
 /* Plain multi-step LIF layer (no recurrence). */
@@ -196,7 +206,9 @@ typedef struct {
 /* Workspace kinds for delrec_query_workspace; flags bit 0: weights are bf16; synaptic
  * kinds: bit 1: hybrid delays (d == NULL), bits 8..15: ceil(2 * s_max) on the float32 s_max
  * the entry point receives (s_uniform for the hybrid), capped at 255 -- the most lags of
- * non-zero weight per connection, which picks the scan form (and its workspace). */
+ * non-zero weight per connection, which picks the scan form (and its workspace); hybrid:
+ * bit 2: d_min >= s_uniform - 1, bits 16..23: off_count (the fields of the entry point's
+ * arguments, which also pick the scan form). */
 enum { DELREC_WS_AXONAL_FWD = 1, DELREC_WS_AXONAL_BWD = 2, DELREC_WS_SYN_FWD = 3,
        DELREC_WS_SYN_BWD = 4 };
 

@@ -24,8 +24,9 @@ Pinning status of each function is stated in its docstring. The pins -- closed f
 the known-answer inputs of the reference's own tests, invariants and hand-derived golden
 vectors (``tests/golden/make_fixtures.py``; no reference code is run) -- are in
 ``tests/test_oracle_*.py``.
-Parity unpinned: the spikingjelly LIF op order for ``v_reset != 0`` and ``decay_input``
-(spikingjelly is not installed; the restatement follows its published source).
+Parity unpinned: only spikingjelly's fp32 operation order inside the ``v_reset != 0`` and
+``decay_input`` charge forms (spikingjelly is not installed; the forms themselves are
+pinned by their closed forms at zero recurrent weight).
 """
 
 from . import neuron, delays, scans, model  # noqa: F401

@@ -18,8 +18,11 @@ module restates its published LIF:
 
 The first branch is the one every configuration here uses; it is pinned by the
 reference's own comment ``configs/perf_HAR.py:71-73`` ("LIFNode with decay_input=False,
-v_reset=0 gives v = (1-1/tau)*v + x") and by ``triton_kernels/lif.py:25-33``.
-The other three branches are parity unpinned (spikingjelly absent).
+v_reset=0 gives v = (1-1/tau)*v + x") and by ``triton_kernels/lif.py:25-33``. All four are
+pinned by their closed forms at zero recurrent weight (a constant input relaxes the
+membrane geometrically from v_reset to its fixed point, and a hard reset restarts the same
+curve; tests/test_oracle_scans.py). What stays unpinned (spikingjelly absent) is only
+spikingjelly's fp32 operation order inside the decay_input / v_reset != 0 forms.
 """
 
 import math

@@ -40,23 +40,67 @@ def _drop(drop, B, N, like):
     return torch.ones(B, N, dtype=like.dtype, device=like.device) if drop is None else drop
 
 
+def hard_lags(d, L, taps):
+    """Per-source integer lag (and interpolation weight) of the reference's hard-tap
+    forwards (``triton_kernels/delays.py:32-44``): ``approx`` / ``ste_round``:
+    lag = clamp(round(d) + 1, 1, L - 1) (round half to even, as ``torch.round``);
+    ``ste_interp``: lag = clamp(floor(1 + d), 1, L - 1), frac = clamp(1 + d - lag, 0, 1)."""
+    d = d.detach()
+    if taps in ('approx', 'ste_round'):
+        return (torch.round(d).long() + 1).clamp(1, max(1, L - 1)), None
+    pos = 1.0 + d
+    lag = torch.floor(pos).long().clamp(1, max(1, L - 1))
+    return lag, (pos - lag.to(d.dtype)).clamp(0.0, 1.0)
+
+
 def axonal_v2(x, W, d, lif, sigma=0.0, bias=None, drop=None, p_spread=None,
-              use_sig_p=False, round_delays=False, forced=None):
+              use_sig_p=False, round_delays=False, forced=None, taps='soft'):
     """Dense sliding-window axonal scan. ``drop`` is the fixed ``(B, N)`` recurrent
     dropout multiplier (ones when off), applied to ``rec`` (after the bias). ``forced``: an
-    optional ``(T, B, N)`` spike train the neurons are teacher-forced with (``lif_step``)."""
+    optional ``(T, B, N)`` spike train the neurons are teacher-forced with (``lif_step``).
+
+    ``taps`` selects the reference fused kernel's forward modes (``recdel_base.py:55-99,
+    361-383``): ``soft`` the triangle over every lag; ``approx`` one rounded tap
+    z = y(t - lag) with the window of ``round(max d) + 2`` lags, its single-tap backward
+    and the straight-through delay gradient dz/dd = y(t - lag - 1) - y(t - lag)
+    (``recdel_base.py:219-224, 266-285``), no spread gradient; ``ste_round`` / ``ste_interp``
+    the rounded tap or the two-tap interpolation (1 - frac) y(t - lag) + frac y(t - lag - 1)
+    in the forward with the soft triangle's gradients in the backward
+    (``recdel_base.py:363-378``)."""
     T, B, N = x.shape
+    assert taps in ('soft', 'approx', 'ste_round', 'ste_interp'), taps
     d = _ste_round(d.to(x.dtype), round_delays)
     mask, L = axonal_mask(d, sigma, p_spread, use_sig_p)        # (N, L)
+    lag = frac = None
+    if taps == 'approx':
+        L = int(torch.round(d.detach()).max().item()) + 2
+    if taps != 'soft':
+        # the hard taps read their own history of lags 1 .. Lh (the reference kernel loads
+        # y(t - lag - 1) from the whole spike tensor, one lag past its window)
+        lag, frac = hard_lags(d, L, taps)
+        Lh = int(lag.max()) + 1
+        hist = torch.zeros(B, N, Lh, dtype=x.dtype, device=x.device)       # oldest .. newest
+        idx0 = (Lh - lag).view(1, N, 1).expand(B, N, 1)      # slot of y(t - lag)
+        idx1 = idx0 - 1                                      # slot of y(t - lag - 1)
     m = _drop(drop, B, N, x)
     v = lif_initial_v(lif, x[0])
     ys, us, recs = [], [], []
     if L >= 2:
-        k_rev = mask[:, 1:L].flip(-1).unsqueeze(0)                # (1, N, L-1): lag L-1 .. 1
+        k_rev = mask[:, 1:L].flip(-1).unsqueeze(0) if taps != 'approx' else None   # lag L-1 .. 1
         window = torch.zeros(B, N, L - 1, dtype=x.dtype, device=x.device)          # oldest .. newest
     for t in range(T):
         if L >= 2:
-            z = (k_rev * window).sum(-1)                          # (B, N)
+            if taps == 'soft':
+                z = (k_rev * window).sum(-1)                      # (B, N)
+            else:
+                y0 = hist.gather(-1, idx0).squeeze(-1)
+                y1 = hist.gather(-1, idx1).squeeze(-1)
+                if taps == 'approx':
+                    z = y0 + (d - d.detach()) * (y1 - y0).detach()
+                else:
+                    hard = y0 if taps == 'ste_round' else (1.0 - frac) * y0 + frac * y1
+                    soft = (k_rev * window).sum(-1)
+                    z = soft + (hard - soft).detach()
             rec = torch.matmul(W.unsqueeze(0), z.unsqueeze(-1)).squeeze(-1)
         else:
             rec = torch.zeros(B, N, dtype=x.dtype, device=x.device)
@@ -66,6 +110,8 @@ def axonal_v2(x, W, d, lif, sigma=0.0, bias=None, drop=None, p_spread=None,
         y, h, v = lif_step(lif, x[t] + rec * m, v, None if forced is None else forced[t])
         if L >= 2:
             window = torch.cat([window[..., 1:], y.unsqueeze(-1)], dim=-1)
+            if taps != 'soft':
+                hist = torch.cat([hist[..., 1:], y.unsqueeze(-1)], dim=-1)
         ys.append(y)
         us.append(h)
     return torch.stack(ys), {'u': torch.stack(us), 'rec': torch.stack(recs), 'L': L}

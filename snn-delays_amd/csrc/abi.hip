@@ -312,8 +312,40 @@ void lagstep_ws(C& c, int T, int B, int N, int L, bool fwd) {
     c.template take<float>((size_t)B * N);                       // v / lambda
 }
 
+// The offset-stacked hybrid scans (hybstep.hip): hybrid delays of one uniform half-width
+// whose taps all lie at lags >= 1 (lags_ok: d_min >= s - 1), D = off_count offsets (at most
+// 16), KF = ceil(2 s) taps per source (at most 8) and a window of at most 128 lags, where
+// the rings of the per-connection scans do not fit one CU's LDS. DELREC_SYN_HYBSTEP=1
+// forces them at any size (parity tests), =0 turns them off.
+bool syn_hybstep(int T, int B, int N, int L, bool hybrid, int off_count, int taps, bool lags_ok) {
+    const char* e = getenv("DELREC_SYN_HYBSTEP");
+    if (e && e[0] == '0') return false;
+    if (!hybrid || off_count <= 0 || !lags_ok) return false;
+    if (!hybstep_dims(T, B, N, L, off_count, taps, num_cus()).ok) return false;
+    if (e && e[0] == '1') return true;
+    return !syn_layout(N, L, true).lds_ring;
+}
+
 template <class C>
-void syn_fwd_ws(C& c, int T, int B, int N, int L, bool hybrid, bool bf16, int taps) {
+void hybstep_ws(C& c, int T, int B, int N, int L, int D, int KF, bool fwd, bool bf16) {
+    const HybStepDims q = hybstep_dims(T, B, N, L, D, KF, num_cus());
+    c.template take<uint4>((bf16 ? 1 : 2) * q.plane);           // W^(e) planes
+    c.template take<uint16_t>((size_t)B * q.lda);               // history hi (z or gr)
+    c.template take<uint16_t>((size_t)B * q.lda);               // history lo
+    c.template take<float>((size_t)q.KS * B * q.Np);            // split-K partials
+    c.template take<float>((size_t)B * N);                      // v / lambda
+    c.template take<int>((size_t)N);                            // first lag per source
+    c.template take<float>((size_t)KF * N);                     // tap weights per source
+    if (fwd) c.template take<uint64_t>((size_t)q.HW * B * N);   // spike-history words
+    else c.template take<float>((size_t)KF * q.R * N * B);      // deliveries of h * G
+}
+
+template <class C>
+void syn_fwd_ws(C& c, int T, int B, int N, int L, bool hybrid, bool bf16, int taps, int offc, bool lags_ok) {
+    if (syn_hybstep(T, B, N, L, hybrid, offc, taps, lags_ok)) {
+        hybstep_ws(c, T, B, N, L, offc, taps, true, bf16);
+        return;
+    }
     if (syn_lagstep(T, B, N, L, taps)) {
         lagstep_ws(c, T, B, N, L, true);
         return;
@@ -327,7 +359,7 @@ void syn_fwd_ws(C& c, int T, int B, int N, int L, bool hybrid, bool bf16, int ta
 }
 
 template <class C>
-void syn_bwd_ws(C& c, int T, int B, int N, int L, int taps) {
+void syn_bwd_ws(C& c, int T, int B, int N, int L, int taps, bool hybrid, bool bf16, int offc, bool lags_ok) {
     // sized for the widest tap run, so the ring may always go to the workspace
     const SynBwdLayout lay = syn_bwd_layout(N, L, kSynMaxTaps);
     const LagPack q = lag_pack(T, B, N);
@@ -336,9 +368,14 @@ void syn_bwd_ws(C& c, int T, int B, int N, int L, int taps) {
     c.template take<float>((size_t)B * N);              // db partials
     c.template take<float>((size_t)3 * q.KS * N * N);   // lag-GEMM partials
     c.template take<uint4>(packed);                     // gr_hi
+    c.template take<uint4>(packed);                     // gr_mid
     c.template take<uint4>(packed);                     // gr_lo
     c.template take<uint4>(packed);                     // shifted spikes
     c.template take<int>((size_t)4 * N + 64);           // lag range per column, meta
+    if (syn_hybstep(T, B, N, L, hybrid, offc, taps, lags_ok)) {
+        hybstep_ws(c, T, B, N, L, offc, taps, false, bf16);
+        return;
+    }
     if (syn_lagstep(T, B, N, L, taps)) {
         lagstep_ws(c, T, B, N, L, false);
         return;
@@ -529,8 +566,14 @@ int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_
             axonal_bwd_ws(c, T, B, N, lay);
             break;
         }
-        case DELREC_WS_SYN_FWD: syn_fwd_ws(c, T, B, N, L, (flags & 2) != 0, bf16, (flags >> 8) & 0xff); break;
-        case DELREC_WS_SYN_BWD: syn_bwd_ws(c, T, B, N, L, (flags >> 8) & 0xff); break;
+        case DELREC_WS_SYN_FWD:
+            syn_fwd_ws(c, T, B, N, L, (flags & 2) != 0, bf16, (flags >> 8) & 0xff, (flags >> 16) & 0xff,
+                       (flags & 4) != 0);
+            break;
+        case DELREC_WS_SYN_BWD:
+            syn_bwd_ws(c, T, B, N, L, (flags >> 8) & 0xff, (flags & 2) != 0, bf16, (flags >> 16) & 0xff,
+                       (flags & 4) != 0);
+            break;
         default: return DELREC_ERR_ARG;
     }
     *bytes = c.used;
@@ -746,6 +789,50 @@ int syn_fwd_lagstep(const delrec_syn_fwd_args* a, hipStream_t s) {
     return finish_launch();
 }
 
+// forward as one offset-stacked GEMM + one LIF launch per step (hybstep.hip)
+int syn_fwd_hybstep(const delrec_syn_fwd_args* a, int KF, hipStream_t s) {
+    const int T = a->T, B = a->B, N = a->N;
+    const HybStepDims q = hybstep_dims(T, B, N, a->L, a->off_count, KF, num_cus());
+    const int planes = a->w_bf16 ? 1 : 2;
+    Carver cv(a->workspace, a->workspace_bytes);
+    uint4* P = cv.take<uint4>(planes * q.plane);
+    uint16_t* hhi = cv.take<uint16_t>((size_t)B * q.lda);
+    uint16_t* hlo = cv.take<uint16_t>((size_t)B * q.lda);
+    float* part = cv.take<float>((size_t)q.KS * B * q.Np);
+    float* state = cv.take<float>((size_t)B * N);
+    int* lof = cv.take<int>((size_t)N);
+    float* h = cv.take<float>((size_t)KF * N);
+    uint64_t* hist = cv.take<uint64_t>((size_t)q.HW * B * N);
+    if (!P || !hhi || !hlo || !part || !state || !lof || !h || !hist) return DELREC_ERR_WORKSPACE;
+    HybPack pk{};
+    pk.N = N; pk.Nk = q.Nk; pk.Np = q.Np; pk.D = q.D; pk.omin = a->off_min; pk.planes = planes;
+    pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.off = a->offsets; pk.out = P;
+    launch_hyb_pack(pk, true, s);
+    HybTaps tp{};
+    tp.N = N; tp.KF = KF; tp.omin = a->off_min; tp.s = a->s_uniform; tp.base = a->base; tp.lof = lof; tp.h = h;
+    launch_hyb_taps(tp, s);
+    launch_hist_clear(hhi, B, q.lda, s);   // z before t = 0, and the slices past the last step
+    launch_hist_clear(hlo, B, q.lda, s);
+    LagStepGemm g{};   // step t: rec(t) from history slices t .. t + D - 1 = z(t - D + 1 .. t)
+    g.a0 = hhi; g.a1 = hlo; g.lda = q.lda; g.rs = 0; g.B = B; g.rows = B; g.rp = 1;
+    g.p0 = P; g.p1 = planes > 1 ? P + q.plane : nullptr; g.Np = q.Np; g.Kt = q.Kt; g.KS = q.KS;
+    g.Nk = q.Nk; g.part = part;
+    HybLif l{};
+    l.T = T; l.B = B; l.N = N; l.Nk = q.Nk; l.Np = q.Np; l.KS = q.KS; l.D = q.D; l.KF = KF; l.R = q.R;
+    l.lda = q.lda; l.part = part; l.lof = lof; l.h = h; l.bias = a->bias; l.drop = a->drop;
+    l.lif = make_lif(a->lif); l.state = state; l.hhi = hhi; l.hlo = hlo;
+    l.x = a->x; l.y = a->y; l.u = a->u; l.bits = a->bits; l.hist = hist;
+    const bool timed = scan_begin(DELREC_WS_SYN_FWD, s);
+    for (int t = 0; t < T; ++t) {
+        g.aoff = (size_t)t * q.Nk;
+        launch_lagstep_gemm(g, 2, s, planes);
+        l.t = t;
+        launch_hyb_lif(l, true, q.HW, s);
+    }
+    scan_end(timed, s);
+    return finish_launch();
+}
+
 int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
     if (!a->x || !a->W || !a->y || !a->u || !a->bits || !lif_ok(a->lif)) return DELREC_ERR_ARG;
@@ -755,6 +842,9 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     const SynLayout lay = syn_layout(a->N, a->L, true);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int N = a->N;
+    if (syn_hybstep(a->T, a->B, N, a->L, hybrid && !a->s, a->off_count, lag_taps(a->s_uniform),
+                    a->d_min >= a->s_uniform - 1.0f))
+        return syn_fwd_hybstep(a, lag_taps(a->s_uniform), s);
     if (syn_lagstep(a->T, a->B, N, a->L, lag_taps(a->s ? a->s_max : std::max(a->s_max, a->s_uniform))))
         return syn_fwd_lagstep(a, s);
     const size_t nb = (size_t)((N + 15) / 16) * 16 * N;
@@ -838,17 +928,20 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     float* part = cv.take<float>((size_t)B * N);
     float* lagp = cv.take<float>((size_t)3 * q.KS * N * N);
     uint4* ahi = cv.take<uint4>(packed);
+    uint4* amd = cv.take<uint4>(packed);
     uint4* alo = cv.take<uint4>(packed);
     uint4* yb = cv.take<uint4>(packed);
     int* meta = cv.take<int>((size_t)4 * N + 64);
-    const bool lagstep = syn_lagstep(T, B, N, a->L, lag_taps(hybrid ? a->s_uniform
-                                                                   : (a->s ? a->s_max : std::max(a->s_max, a->s_uniform))));
+    const int taps = lag_taps(hybrid ? a->s_uniform : (a->s ? a->s_max : std::max(a->s_max, a->s_uniform)));
+    const bool hybstep = syn_hybstep(T, B, N, a->L, hybrid && !a->s, a->off_count, taps,
+                                     a->d_min >= a->s_uniform - 1.0f);
+    const bool lagstep = !hybstep && syn_lagstep(T, B, N, a->L, taps);
     void* wt = nullptr;
     void* dt = nullptr;
     float* gring = nullptr;
     uint8_t* offq = nullptr;
     int* order = nullptr;
-    if (!lagstep) {
+    if (!lagstep && !hybstep) {
         wt = cv.take<float>((size_t)N * wlay.NT);
         dt = cv.take<float>((size_t)N * wlay.NT);
         gring = cv.take<float>((size_t)B * N * wlay.RP);
@@ -856,7 +949,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         order = cv.take<int>((size_t)N);
         if (!wt || !dt || !gring || !offq || !order) return DELREC_ERR_WORKSPACE;
     }
-    if (!gr || !part || !lagp || !ahi || !alo || !yb || !meta) return DELREC_ERR_WORKSPACE;
+    if (!gr || !part || !lagp || !ahi || !amd || !alo || !yb || !meta) return DELREC_ERR_WORKSPACE;
 
     // the streamlined hybrid backward (syn_bwd_hyb: ring in LDS over the receivers rounded up
     // to groups of 64, one source per lane, N <= 512). Its lanes take the sources in
@@ -866,9 +959,9 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     // laid out in that order, so a lane's runs stay adjacent to its neighbours'.
     const size_t hrows = (size_t)((N + 63) / 64 * 64);
     const size_t lds_h = hrows * lay.RP * sizeof(float);
-    const bool hyb_fast = hybrid && !lagstep && N <= 512 && (lay.KT == 2 || lay.KT == 4) &&
+    const bool hyb_fast = hybrid && !lagstep && !hybstep && N <= 512 && (lay.KT == 2 || lay.KT == 4) &&
                           lds_h <= (size_t)max_lds_bytes() && getenv_flag_off("DELREC_SYN_BWD_HYB");
-    if (!lagstep) {
+    if (!lagstep && !hybstep) {
         if (hyb_fast) launch_sort_by_first_lag(a->base, a->s_uniform, N, order, s);
         const int* ord = hyb_fast ? order : nullptr;
         if (a->w_bf16) block_transpose<uint16_t>(a->W, wt, N, s, ord); else block_transpose<float>(a->W, wt, N, s, ord);
@@ -880,14 +973,69 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     const size_t NN = (size_t)N * N;
     LagBf16 g{};
     g.T = T; g.B = B; g.Bp = q.Bp; g.N = N; g.Np = q.Np; g.L = a->L; g.Kp = q.Kp; g.KS = q.KS;
-    g.ahi = ahi; g.alo = alo; g.yb = yb;
+    g.ahi = ahi; g.amd = amd; g.alo = alo; g.yb = yb;
     g.meta = meta; g.lo = meta + 64; g.rc = meta + 64 + N; g.om = meta + 64 + 2 * N; g.ox = meta + 64 + 3 * N;
     g.d = a->d; g.base = a->base; g.off = a->offsets; g.s = a->s; g.s_uniform = a->s_uniform;
     g.pw = lagp;
     g.pd = lagp + (size_t)q.KS * NN;
     g.ps = a->ds ? lagp + (size_t)2 * q.KS * NN : nullptr;
     launch_lag_cols(g, s);
-    if (hybrid && !lagstep) launch_pack_offq(static_cast<const int8_t*>(dt), (size_t)N * lay.NT, meta, offq, s);
+    if (hybrid && !lagstep && !hybstep) launch_pack_offq(static_cast<const int8_t*>(dt), (size_t)N * lay.NT, meta, offq, s);
+
+    if (hybstep) {
+        // reverse-time scan as one offset-stacked GEMM + one LIF launch per step
+        const int KF = taps;
+        const HybStepDims hq = hybstep_dims(T, B, N, a->L, a->off_count, KF, num_cus());
+        const int planes = a->w_bf16 ? 1 : 2;
+        uint4* P = cv.take<uint4>(planes * hq.plane);
+        uint16_t* ghi = cv.take<uint16_t>((size_t)B * hq.lda);
+        uint16_t* glo = cv.take<uint16_t>((size_t)B * hq.lda);
+        float* hpart = cv.take<float>((size_t)hq.KS * B * hq.Np);
+        float* state = cv.take<float>((size_t)B * N);
+        int* lof = cv.take<int>((size_t)N);
+        float* h = cv.take<float>((size_t)KF * N);
+        float* dbuf = cv.take<float>((size_t)KF * hq.R * N * B);
+        if (!P || !ghi || !glo || !hpart || !state || !lof || !h || !dbuf) return DELREC_ERR_WORKSPACE;
+        HybPack pk{};
+        pk.N = N; pk.Nk = hq.Nk; pk.Np = hq.Np; pk.D = hq.D; pk.omin = a->off_min; pk.planes = planes;
+        pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.off = a->offsets; pk.out = P;
+        launch_hyb_pack(pk, false, s);
+        HybTaps tp{};
+        tp.N = N; tp.KF = KF; tp.omin = a->off_min; tp.s = a->s_uniform; tp.base = a->base; tp.lof = lof; tp.h = h;
+        launch_hyb_taps(tp, s);
+        launch_hist_clear(ghi, B, hq.lda, s);   // gr past the last step
+        launch_hist_clear(glo, B, hq.lda, s);
+        // gr == dx unless a dropout mask scales it
+        const bool need_gr = a->drop != nullptr;
+        LagStepGemm gg{};   // step t: G(t + 1) from history slices t + 1 .. t + D = gr(t + 1 .. t + D)
+        gg.a0 = ghi; gg.a1 = glo; gg.lda = hq.lda; gg.rs = 0; gg.B = B; gg.rows = B; gg.rp = 1;
+        gg.p0 = P; gg.p1 = planes > 1 ? P + hq.plane : nullptr; gg.Np = hq.Np; gg.Kt = hq.Kt; gg.KS = hq.KS;
+        gg.Nk = hq.Nk; gg.part = hpart;
+        HybLif l{};
+        l.T = T; l.B = B; l.N = N; l.Nk = hq.Nk; l.Np = hq.Np; l.KS = hq.KS; l.D = hq.D; l.KF = KF; l.R = hq.R;
+        l.lda = hq.lda; l.part = hpart; l.lof = lof; l.h = h; l.bias = nullptr; l.drop = a->drop;
+        l.lif = make_lif(a->lif); l.state = state; l.hhi = ghi; l.hlo = glo;
+        l.u_in = a->u; l.gy = a->gy; l.dx = a->dx; l.gr = need_gr ? gr : nullptr; l.dbp = part; l.dbuf = dbuf;
+        const bool timed = scan_begin(DELREC_WS_SYN_BWD, s);
+        for (int t = T - 1; t >= 0; --t) {
+            gg.aoff = (size_t)(t + 1) * hq.Nk;
+            launch_lagstep_gemm(gg, 2, s, planes);
+            l.t = t;
+            launch_hyb_lif(l, false, hq.HW, s);
+        }
+        scan_end(timed, s);
+        int st = finish_launch();
+        if (st) return st;
+        launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
+        if (a->dW || a->dd || a->ds) {
+            launch_lag_bf16(g, need_gr ? gr : a->dx, a->bits, s);
+            LagGemm f{};
+            f.N = N; f.KS = q.KS; f.W = a->W; f.w_bf16 = a->w_bf16; f.s = a->s; f.s_uniform = a->s_uniform;
+            f.pw = g.pw; f.pd = g.pd; f.ps = g.ps;
+            launch_lag_finish(f, a->dW, a->dd, a->ds, s);
+        }
+        return finish_launch();
+    }
 
     if (lagstep) {
         // reverse-time scan as one lag-stacked GEMM + one LIF launch per step

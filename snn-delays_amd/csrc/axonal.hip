@@ -1385,8 +1385,8 @@ __global__ void __launch_bounds__(1024) reduce_rows_kernel(const float* part, in
 // Both job kinds of a launch only read what earlier launches wrote, so they run side by
 // side; the longer dW blocks go first so that all of them start in the first round.
 template <int HW>
-__global__ void __launch_bounds__(kDwThreads, 3) axonal_bwd_tail_kernel(AxBwd p, AxTail q) {
-    __shared__ DwStage sm;   // 32 KiB: one dW stage, or the delay blocks' 2 KiB of partials
+__global__ void __launch_bounds__(kDwThreads, 2) axonal_bwd_tail_kernel(AxBwd p, AxTail q) {
+    __shared__ DwStage sm;   // 48 KiB: one dW stage, or the delay blocks' 2 KiB of partials
     int bid = blockIdx.x;
     if (bid < q.ndw) {
         // the tiles of one k chunk read the same rows of both operands: with ks a multiple of

@@ -2,7 +2,7 @@
 // the launches that run them beside other reductions of the backward.
 //
 //   dw_gemm_tile   dW[i,j] = sum_{t,b} gr[t,b,i] * z[t,b,j]: the reference's host GEMM at
-//                  recdel_base.py:327-330, on bf16 MFMA with split fp32 operands; one
+//                  recdel_base.py:327-330, on bf16 MFMA with three-term fp32 operands; one
 //                  128x128 output tile over one k chunk per workgroup, written as a
 //                  deterministic partial (no atomics).
 //   sum_partials_block  out[idx] = sum_k partial[k][idx] in a fixed order.
@@ -19,9 +19,9 @@ constexpr int kDwTile = 128;   // output tile (i and j) per workgroup
 constexpr int kDwKt = 32;      // rows of k per stage (one MFMA K)
 constexpr int kDwThreads = 256;
 
-// LDS of one stage: [operand A/B][hi/lo][k block][column] of 16-byte runs (32 KiB)
+// LDS of one stage: [operand A/B][hi/mid/lo][k block][column] of 16-byte runs (48 KiB)
 struct DwStage {
-    uint4 v[2][2][kDwKt / 8][kDwTile];
+    uint4 v[2][3][kDwKt / 8][kDwTile];
 };
 
 __device__ __forceinline__ uint32_t dw_bf16_bits(float f) {
@@ -31,9 +31,11 @@ __device__ __forceinline__ uint32_t dw_bf16_bits(float f) {
 }
 
 // dW[i, j] = sum_k A[k, i] * Bm[k, j] on bf16 MFMA (v_mfma_f32_16x16x32_bf16) with both fp32
-// operands split into bf16 halves, x = hi + lo with hi = bf16(x), lo = bf16(x - hi): each
-// tile takes hi*hi + hi*lo + lo*hi (the lo*lo term is below 2^-32 of the product), so a
-// product carries a relative error of about 2^-16, accumulated in fp32. Tile (ti, tj) of
+// operands split into three bf16 terms, x = hi + mid + lo with hi = bf16(x),
+// mid = bf16(x - hi), lo = bf16(x - hi - mid) (x is held to about 2^-27): each tile takes
+// the six products whose order is at least 2^-16 of the whole (hi*hi, hi*mid, mid*hi,
+// hi*lo, mid*mid, lo*hi), dropping mid*lo, lo*mid and lo*lo (about 2^-24 together), so a
+// product is as accurate as an fp32 one, accumulated in fp32. Tile (ti, tj) of
 // 128x128 outputs (4 waves of 64x64) over k chunk kz. Each stage of 32 rows is read from
 // global memory as 8-row runs of one column (coalesced across the workgroup's columns) into
 // registers while the previous stage is multiplied, then split and stored in LDS k-blocked
@@ -71,26 +73,32 @@ __device__ __forceinline__ void dw_gemm_tile(const float* __restrict__ A, const 
             }
         }
     };
+    // x = hi + mid + lo as the bf16 bit patterns of one pair of consecutive k
+    auto split3 = [](float x0, float x1, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+        const uint32_t h0 = dw_bf16_bits(x0), h1 = dw_bf16_bits(x1);
+        const float r0 = x0 - __uint_as_float(h0 << 16), r1 = x1 - __uint_as_float(h1 << 16);
+        const uint32_t m0 = dw_bf16_bits(r0), m1 = dw_bf16_bits(r1);
+        const uint32_t l0 = dw_bf16_bits(r0 - __uint_as_float(m0 << 16));
+        const uint32_t l1 = dw_bf16_bits(r1 - __uint_as_float(m1 << 16));
+        hi = h0 | (h1 << 16);
+        mid = m0 | (m1 << 16);
+        lo = l0 | (l1 << 16);
+    };
     auto stash = [&]() {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            uint32_t ah[4], al[4], bh[4], bl[4];
+            uint32_t a3[3][4], b3[3][4];
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
-                const uint32_t a0 = dw_bf16_bits(ra[h][e]), a1 = dw_bf16_bits(ra[h][e + 1]);
-                const uint32_t b0 = dw_bf16_bits(rb[h][e]), b1 = dw_bf16_bits(rb[h][e + 1]);
-                ah[e / 2] = a0 | (a1 << 16);
-                bh[e / 2] = b0 | (b1 << 16);
-                al[e / 2] = dw_bf16_bits(ra[h][e] - __uint_as_float(a0 << 16)) |
-                            (dw_bf16_bits(ra[h][e + 1] - __uint_as_float(a1 << 16)) << 16);
-                bl[e / 2] = dw_bf16_bits(rb[h][e] - __uint_as_float(b0 << 16)) |
-                            (dw_bf16_bits(rb[h][e + 1] - __uint_as_float(b1 << 16)) << 16);
+                split3(ra[h][e], ra[h][e + 1], a3[0][e / 2], a3[1][e / 2], a3[2][e / 2]);
+                split3(rb[h][e], rb[h][e + 1], b3[0][e / 2], b3[1][e / 2], b3[2][e / 2]);
             }
             const int kbk = kq + 2 * h;
-            sm.v[0][0][kbk][col] = uint4{ah[0], ah[1], ah[2], ah[3]};
-            sm.v[0][1][kbk][col] = uint4{al[0], al[1], al[2], al[3]};
-            sm.v[1][0][kbk][col] = uint4{bh[0], bh[1], bh[2], bh[3]};
-            sm.v[1][1][kbk][col] = uint4{bl[0], bl[1], bl[2], bl[3]};
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {
+                sm.v[0][q][kbk][col] = uint4{a3[q][0], a3[q][1], a3[q][2], a3[q][3]};
+                sm.v[1][q][kbk][col] = uint4{b3[q][0], b3[q][1], b3[q][2], b3[q][3]};
+            }
         }
     };
 
@@ -102,23 +110,26 @@ __device__ __forceinline__ void dw_gemm_tile(const float* __restrict__ A, const 
     for (int k0 = kb; k0 < ke; k0 += kDwKt) {
         const bool more = k0 + kDwKt < ke;
         if (more) fetch(k0 + kDwKt);
-        dw_bf16x8 fah[4], fal[4], fbh[4], fbl[4];
+        dw_bf16x8 fa[3][4], fb[3][4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            fah[q] = __builtin_bit_cast(dw_bf16x8, sm.v[0][0][g][wi * 64 + q * 16 + lc]);
-            fal[q] = __builtin_bit_cast(dw_bf16x8, sm.v[0][1][g][wi * 64 + q * 16 + lc]);
-            fbh[q] = __builtin_bit_cast(dw_bf16x8, sm.v[1][0][g][wj * 64 + q * 16 + lc]);
-            fbl[q] = __builtin_bit_cast(dw_bf16x8, sm.v[1][1][g][wj * 64 + q * 16 + lc]);
-        }
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                fa[pl][q] = __builtin_bit_cast(dw_bf16x8, sm.v[0][pl][g][wi * 64 + q * 16 + lc]);
+                fb[pl][q] = __builtin_bit_cast(dw_bf16x8, sm.v[1][pl][g][wj * 64 + q * 16 + lc]);
+            }
         // every wave holds its fragments in registers before the stage is overwritten
         __syncthreads();
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fah[a], fbh[c], acc[a][c], 0, 0, 0);
-                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fah[a], fbl[c], acc[a][c], 0, 0, 0);
-                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fal[a], fbh[c], acc[a][c], 0, 0, 0);
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[0][a], fb[2][c], acc[a][c], 0, 0, 0);
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[1][a], fb[1][c], acc[a][c], 0, 0, 0);
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[2][a], fb[0][c], acc[a][c], 0, 0, 0);
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[0][a], fb[1][c], acc[a][c], 0, 0, 0);
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[1][a], fb[0][c], acc[a][c], 0, 0, 0);
+                acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[0][a], fb[0][c], acc[a][c], 0, 0, 0);
             }
         if (more) stash();
         __syncthreads();

@@ -1,0 +1,302 @@
+// Hybrid scans with the integer offsets as the lag axis, on bf16 MFMA (gfx950): the form for
+// hybrid delays d_ij = base_j + off_ij whose rings do not fit one CU's LDS. The reference runs
+// the hybrid as its per-connection scatter / gather (synaptic_eventdriven.py:106-164,
+// :323-364, launched by synaptic_hybrid.py:139-211).
+//
+// Write off_ij = omin + e_ij with e in [0, D), and give each source the triangle of its
+// smallest delay, c_j = 1 + (base_j + omin), with its KF taps h_j(lof_j + f), f < KF (every
+// lag >= 1: the entry point checks d_min >= s - 1). Connection (i, j)'s taps are then the
+// source's, shifted by e_ij steps:
+//   rec_i(t)  = sum_j W_ij sum_f h_j(lof_j + f) y_j(t - lof_j - f - e_ij)
+//             = sum_e sum_j W^(e)_ij z_j(t - e),  z_j(t) = sum_f h_j(lof_j + f) y_j(t - lof_j - f),
+//   gfut_j(t) = sum_i W_ij sum_f h_j(lof_j + f) gr_i(t + lof_j + f + e_ij)
+//             = sum_f h_j(lof_j + f) G_j(t + lof_j + f),  G_j(tau) = sum_e sum_i W^(e)_ij gr_i(tau + e),
+// with W^(e) = W * [off - omin == e] (exact in bf16 for bf16 W). z_j is the source's axonal
+// trace and G the offset-stacked product. Each step runs one (B x D*N) by (D*N x N) product
+// over a batch-major history window -- the lag-stacked GEMM of lagstep.hip with the D offsets
+// in place of the L - 1 lags (C5: 5 products per connection instead of 66) -- and one LIF
+// launch that adds the split-K partials in a fixed order.
+//
+// The per-source time shift lof_j sits on the contracted side in the forward (z_j is formed
+// by the LIF thread that owns neuron j, from its own spike-history word), and on the output
+// side in the backward: G_j(tau) is needed by steps tau - lof_j - f, different for every j. The
+// backward LIF therefore delivers h_j(lof_j + f) * G_j(t + 1) at once into ring f at the step
+// that will consume it, in a [slot][j][b] layout (b fastest): both the delivery (slot fixed by
+// j) and the consumption (slot fixed by t) are then whole 256-byte rows, through an LDS
+// transpose of the tile.
+//
+// Precision: spikes are exact; z and gr are split into bf16 hi + lo planes (relative error
+// about 2^-16); W^(e) is one bf16 plane for bf16 W, or hi + lo planes for fp32 W
+// (hi*hi + hi*lo + lo*hi). Accumulation is fp32. Connection (i, j)'s triangle is evaluated at
+// c_j + e_ij where the reference evaluates 1 + fp32(base_j + off_ij): the two differ only when
+// that sum rounds in fp32, by at most half an ulp of the delay (about 4e-6 at d = 60).
+#include "kernels.h"
+
+namespace delrec {
+
+namespace {
+
+typedef __bf16 bf16x8h __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint32_t hyb_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+}  // namespace
+
+// P[(q, kk), col] for q < D offset slices of the contracted neuron kk:
+//   forward  (contracted j, output i): W_ij when off_ij - omin == D - 1 - q (slice q ascending
+//            is time ascending: history slice t + q of step t holds z(t - D + 1 + q));
+//   backward (contracted i, output j): W_ij when off_ij - omin == q.
+// One thread per (8-block of the contracted neuron, output column), k-blocked layout
+// ((k / 8) * Np + col) * 8 + k % 8; planes: hi (and lo for fp32 W).
+template <bool FWD>
+__global__ void __launch_bounds__(256) hyb_pack_kernel(HybPack p) {
+    const int NB = p.Nk / 8;
+    const size_t total = (size_t)NB * p.Np;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int kb = (int)(idx / p.Np), col = (int)(idx - (size_t)kb * p.Np);
+    float w[8];
+    int e8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int i = FWD ? col : kb * 8 + e;
+        const int j = FWD ? kb * 8 + e : col;
+        const bool ok = i < p.N && j < p.N;
+        const size_t c = ok ? (size_t)i * p.N + j : 0;
+        w[e] = ok ? load_w(p.W, p.w_bf16, c) : 0.0f;
+        e8[e] = ok ? (int)p.off[c] - p.omin : -1;
+    }
+    const size_t plane = (size_t)p.D * NB * p.Np;
+    for (int q = 0; q < p.D; ++q) {
+        const int want = FWD ? p.D - 1 - q : q;
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            uint32_t h2[2], l2[2];
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+                const float m = e8[e + f] == want ? w[e + f] : 0.0f;
+                h2[f] = hyb_bf16_rne(m);
+                l2[f] = hyb_bf16_rne(m - __uint_as_float(h2[f] << 16));
+            }
+            hi[e / 2] = h2[0] | (h2[1] << 16);
+            lo[e / 2] = l2[0] | (l2[1] << 16);
+        }
+        const size_t o = ((size_t)q * NB + kb) * p.Np + col;
+        p.out[o] = uint4{hi[0], hi[1], hi[2], hi[3]};
+        if (p.planes > 1) p.out[plane + o] = uint4{lo[0], lo[1], lo[2], lo[3]};
+    }
+}
+
+// Each source's first lag of non-zero weight lof_j and its KF tap weights h[f * N + j] at the
+// smallest offset: c_j = 1 + (base_j + 0 + 1 * omin), the parametrisation's fp32 sum.
+__global__ void __launch_bounds__(256) hyb_taps_kernel(HybTaps p) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= p.N) return;
+    const float c = 1.0f + (p.base[j] + 0.0f + 1.0f * (float)p.omin);
+    const float s = p.s, s2 = s * s;
+    const int lof = max(1, (int)floorf(c - s) + 1);
+    p.lof[j] = lof;
+    for (int f = 0; f < p.KF; ++f) p.h[(size_t)f * p.N + j] = tri_weight((float)(lof + f), c, s, s2);
+}
+
+// Forward step t, one thread per (b, neuron i) over the padded width Nk: rec = sum_ks part +
+// bias; u = charge(v, x + rec * m); spike, reset; outputs y, u and the spike bit; the
+// neuron's spike-history word(s) (bit k = y(t - k)) and, as a source, its trace z(t + 1)
+// split into the hi / lo history planes at slice t + D.
+template <int HW>
+__global__ void __launch_bounds__(256) hyb_lif_fwd_kernel(HybLif p) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)p.B * p.Nk) return;
+    const int b = (int)(idx / p.Nk), i = (int)(idx - (size_t)b * p.Nk);
+    const int t = p.t;
+    const size_t ho = (size_t)b * p.lda + (size_t)(t + p.D) * p.Nk + i;
+    if (i >= p.N) {
+        p.hhi[ho] = 0;
+        p.hlo[ho] = 0;
+        return;
+    }
+    const Lif k = p.lif;
+    const size_t BN = (size_t)p.B * p.N, bi = (size_t)b * p.N + i;
+    float r = 0.0f;
+#pragma unroll 8
+    for (int q = 0; q < p.KS; ++q) r += p.part[((size_t)q * p.B + b) * p.Np + i];
+    r += p.bias ? p.bias[i] : 0.0f;
+    const float m = p.drop ? p.drop[bi] : 1.0f;
+    const size_t o = (size_t)t * BN + bi;
+    const float a = p.x[o] + r * m;
+    const float v = t == 0 ? k.v0 : p.state[bi];
+    const float u = lif_charge(k, v, a);
+    const float y = lif_fire(k, u);
+    p.state[bi] = lif_reset(k, u, y);
+    p.y[o] = y;
+    p.u[o] = u;
+    const int TW = (p.T + 31) >> 5;
+    uint32_t* wp = p.bits + ((size_t)b * TW + (t >> 5)) * p.N + i;
+    const uint32_t yb = y != 0.0f ? 1u : 0u;
+    *wp = (t & 31) == 0 ? (yb << (t & 31)) : (*wp | (yb << (t & 31)));
+    uint64_t h[HW];
+#pragma unroll
+    for (int w = 0; w < HW; ++w) h[w] = t == 0 ? 0ull : p.hist[(size_t)w * BN + bi];
+#pragma unroll
+    for (int w = HW - 1; w > 0; --w) h[w] = (h[w] << 1) | (h[w - 1] >> 63);
+    h[0] = (h[0] << 1) | (uint64_t)yb;
+#pragma unroll
+    for (int w = 0; w < HW; ++w) p.hist[(size_t)w * BN + bi] = h[w];
+    // z(t + 1) = sum_f h(lof + f) y(t + 1 - lof - f): bit lof + f - 1 of the history
+    const int lof = p.lof[i];
+    float z = 0.0f;
+    for (int f = 0; f < p.KF; ++f) {
+        const int kb = lof + f - 1;
+        const uint64_t word = HW == 1 ? h[0] : (kb < 64 ? h[0] : h[HW - 1]);
+        const float hf = p.h[(size_t)f * p.N + i];
+        z += ((word >> (kb & 63)) & 1ull) ? hf : 0.0f;
+    }
+    const uint32_t hi = hyb_bf16_rne(z);
+    p.hhi[ho] = (uint16_t)hi;
+    p.hlo[ho] = (uint16_t)hyb_bf16_rne(z - __uint_as_float(hi << 16));
+}
+
+// Backward step t over a tile of 64 batch rows x 64 neurons (256 threads), three phases:
+//  1 (row-major, as the partials lie): G_j(t + 1) = sum_ks part[ks][b][j] into LDS;
+//  2 (transposed: one neuron j per wave, its 64 batch rows on the lanes): deliver
+//    h_j(lof_j + f) * G_j(t + 1) into ring f at the consuming step t + 1 - lof_j - f (kept in a
+//    register when that step is t itself), then gfut_j(t) = sum_f ring f at slot t (0 where
+//    the contribution's G index t + lof_j + f lies past T, which no step delivers);
+//  3 (row-major): the LIF backward on gy + gfut, outputs dx (and gr when it differs), the db
+//    partial, and gr(t) split into the hi / lo history planes at slice t.
+__global__ void __launch_bounds__(256) hyb_lif_bwd_kernel(HybLif p) {
+    __shared__ float sg[64][65];
+    __shared__ float sf[64][65];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j0 = blockIdx.x * 64, b0 = blockIdx.y * 64;
+    const int t = p.t, N = p.N, B = p.B;
+    // phase 1
+    {
+        const int j = j0 + lane;
+#pragma unroll 4
+        for (int e = 0; e < 16; ++e) {
+            const int b = b0 + w + 4 * e;
+            float g = 0.0f;
+            if (b < B && j < N) {
+#pragma unroll 8
+                for (int q = 0; q < p.KS; ++q) g += p.part[((size_t)q * B + b) * p.Np + j];
+            }
+            sg[lane][w + 4 * e] = g;
+        }
+    }
+    __syncthreads();
+    // phase 2
+    {
+        const int b = b0 + lane;
+        const int slot_t = t % p.R;
+        for (int e = 0; e < 16; ++e) {
+            const int jl = w + 4 * e, j = j0 + jl;
+            float gf = 0.0f;
+            if (j < N) {
+                const float g = sg[jl][lane];
+                const int lof = p.lof[j];
+                for (int f = 0; f < p.KF; ++f) {
+                    const float hf = p.h[(size_t)f * N + j];
+                    float* ring = p.dbuf + (size_t)f * p.R * N * B;
+                    const int s = t + 1 - lof - f;   // the step that consumes G_j(t + 1) through tap f
+                    if (s == t) {
+                        gf += hf * g;
+                    } else {
+                        if (s >= 0 && b < B) ring[((size_t)(s % p.R) * N + j) * B + b] = hf * g;
+                        if (t + lof + f <= p.T && b < B) gf += ring[((size_t)slot_t * N + j) * B + b];
+                    }
+                }
+            }
+            sf[jl][lane] = gf;
+        }
+    }
+    __syncthreads();
+    // phase 3
+    {
+        const Lif k = p.lif;
+        const int j = j0 + lane;
+        const size_t BN = (size_t)B * N;
+        for (int e = 0; e < 16; ++e) {
+            const int b = b0 + w + 4 * e;
+            if (b >= B || j >= p.Nk) continue;
+            const size_t ho = (size_t)b * p.lda + (size_t)t * p.Nk + j;
+            if (j >= N) {
+                p.hhi[ho] = 0;
+                p.hlo[ho] = 0;
+                continue;
+            }
+            const float gf = sf[lane][w + 4 * e];
+            const size_t bj = (size_t)b * N + j, o = (size_t)t * BN + bj;
+            const float u = p.u_in[o];
+            const float y = lif_fire(k, u);
+            const bool last = t == p.T - 1;
+            const float lam = last ? 0.0f : p.state[bj];
+            const float du = lif_backward(k, p.gy[o] + gf, u, y, lam);
+            p.state[bj] = k.decay * du;
+            const float da = lif_dx(k, du);
+            const float gr = da * (p.drop ? p.drop[bj] : 1.0f);
+            p.dx[o] = da;
+            if (p.gr) p.gr[o] = gr;
+            p.dbp[bj] = last ? gr : p.dbp[bj] + gr;
+            const uint32_t hi = hyb_bf16_rne(gr);
+            p.hhi[ho] = (uint16_t)hi;
+            p.hlo[ho] = (uint16_t)hyb_bf16_rne(gr - __uint_as_float(hi << 16));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+
+HybStepDims hybstep_dims(int T, int B, int N, int L, int D, int KF, int cus) {
+    HybStepDims q{};
+    q.Nk = (N + 31) / 32 * 32;
+    q.Np = (N + 127) / 128 * 128;
+    q.D = D;
+    q.KF = KF;
+    q.R = std::max(L, 2);
+    q.HW = (std::max(L - 1, 1) + 63) / 64;
+    q.Kt = D * q.Nk;
+    q.lda = (size_t)(T + D + 1) * q.Nk;
+    q.plane = (size_t)(q.Kt / 8) * q.Np;
+    q.KS = lagstep_splits(B, q.Np, q.Kt, cus);
+    // offsets of 16 or fewer, taps of 8 or fewer, a spike history of two 64-bit words, and
+    // 32-bit byte offsets for every operand a GEMM addresses (incl. rows of a partial tile)
+    q.ok = D >= 1 && D <= 16 && KF >= 1 && KF <= 8 && q.HW <= 2 &&
+           (size_t)(B + 128) * q.lda * 2 < ((size_t)1 << 32) && q.plane * 16 < ((size_t)1 << 32);
+    return q;
+}
+
+void launch_hyb_pack(const HybPack& a, bool fwd, hipStream_t stream) {
+    const size_t total = (size_t)(a.Nk / 8) * a.Np;
+    const unsigned blocks = (unsigned)((total + 255) / 256);
+    if (fwd)
+        hipLaunchKernelGGL(hyb_pack_kernel<true>, dim3(blocks), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(hyb_pack_kernel<false>, dim3(blocks), dim3(256), 0, stream, a);
+}
+
+void launch_hyb_taps(const HybTaps& a, hipStream_t stream) {
+    hipLaunchKernelGGL(hyb_taps_kernel, dim3((a.N + 255) / 256), dim3(256), 0, stream, a);
+}
+
+void launch_hyb_lif(const HybLif& l, bool fwd, int hw, hipStream_t stream) {
+    if (fwd) {
+        const size_t n = (size_t)l.B * l.Nk;
+        const unsigned blocks = (unsigned)((n + 255) / 256);
+        if (hw == 1)
+            hipLaunchKernelGGL(hyb_lif_fwd_kernel<1>, dim3(blocks), dim3(256), 0, stream, l);
+        else
+            hipLaunchKernelGGL(hyb_lif_fwd_kernel<2>, dim3(blocks), dim3(256), 0, stream, l);
+    } else {
+        const dim3 grid((l.Nk + 63) / 64, (l.B + 63) / 64);
+        hipLaunchKernelGGL(hyb_lif_bwd_kernel, grid, dim3(256), 0, stream, l);
+    }
+}
+
+}  // namespace delrec

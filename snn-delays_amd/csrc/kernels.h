@@ -124,6 +124,7 @@ struct LagGemm {
 struct LagBf16 {
     int T, B, Bp, N, Np, L, Kp, KS;
     const uint4* ahi;            // gr_hi (Kp, Np) k-blocked
+    const uint4* amd;            // gr_mid
     const uint4* alo;            // gr_lo
     const uint4* yb;             // shifted spikes Y' (Kp, Np) k-blocked
     int* meta;                   // meta[0] = widest column lag range, meta[1] / [2] = smallest /
@@ -191,13 +192,69 @@ struct LagStepLif {
     float* dbp;                  // [B][N] db partials
 };
 
+// offset-stacked hybrid scans (hybstep.hip)
+struct HybPack {                 // W^(e) planes of the forward or backward operand
+    int N, Nk, Np, D, omin, planes;
+    const void* W;
+    int w_bf16;
+    const int8_t* off;
+    uint4* out;                  // planes of (D * Nk / 8) x Np uint4
+};
+
+struct HybTaps {                 // each source's first lag and tap weights at the smallest offset
+    int N, KF, omin;
+    float s;
+    const float* base;
+    int* lof;                    // [N]
+    float* h;                    // [KF][N]
+};
+
+struct HybLif {
+    int T, B, N, Nk, Np, KS, t, D, KF, R;
+    size_t lda;                  // history row pitch (elements): (T + D + 1) * Nk
+    const float* part;           // [KS][B][Np] partials of step t's product
+    const int* lof;
+    const float* h;
+    const float* bias;
+    const float* drop;
+    Lif lif;
+    float* state;                // [B][N]: v (forward) or lambda (backward)
+    uint16_t* hhi;               // forward: z history hi plane; backward: gr history hi plane
+    uint16_t* hlo;
+    // forward
+    const float* x;
+    float* y;
+    float* u;
+    uint32_t* bits;
+    uint64_t* hist;              // [HW][B][N] spike-history words
+    // backward
+    const float* u_in;
+    const float* gy;
+    float* dx;
+    float* gr;                   // (T, B, N) when it differs from dx, else NULL
+    float* dbp;                  // [B][N] db partials
+    float* dbuf;                 // [KF][R][N][B] deliveries of h * G to their consuming step
+};
+
+struct HybStepDims {
+    int Nk, Np, D, KF, R, HW, Kt, KS;
+    size_t lda, plane;
+    bool ok;
+};
+
+HybStepDims hybstep_dims(int T, int B, int N, int L, int D, int KF, int cus);
+void launch_hyb_pack(const HybPack& a, bool fwd, hipStream_t stream);
+void launch_hyb_taps(const HybTaps& a, hipStream_t stream);
+void launch_hyb_lif(const HybLif& l, bool fwd, int hw, hipStream_t stream);
+
 int lagstep_splits(int B, int Np, int Kt, int cus);
 int lagstep_block();
-size_t lagstep_gemm_lds(int pa);
+size_t lagstep_gemm_lds(int pa, int pb = 2);
 void launch_pack_lagw(const LagStepPack& a, bool fwd, hipStream_t stream);
 void launch_hist_zero(uint16_t* h, int B, size_t lda, int Nk, int t0, int t1, hipStream_t stream);
 void launch_hist_clear(uint16_t* h, int B, size_t lda, hipStream_t stream);
-void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream);
+// pb = 1: one P plane (p1 unused)
+void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream, int pb = 2);
 void launch_lagstep_lif(const LagStepLif& l, bool fwd, hipStream_t stream);
 int lagblock_splits(int B, int Np, int Nk, int cus);
 void launch_lagblock(const LagStepGemm& g, int pa, hipStream_t stream);

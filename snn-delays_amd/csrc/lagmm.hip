@@ -9,9 +9,10 @@
 //   ps[i,j] += dh/ds(l; d_ij, s_j) C_l[i,j]  (use_sig_p)
 // so the stack never exists.
 //
-// Operands are bf16. Spikes are exactly 0 or 1 in bf16. gr is split into gr_hi =
-// bf16(gr) and gr_lo = bf16(gr - gr_hi), and each tile takes both products, so a term
-// carries a relative error below 2^-16 of gr (fp32 accumulation). The packed operands use
+// Operands are bf16. Spikes are exactly 0 or 1 in bf16. gr is split into three terms,
+// gr_hi = bf16(gr), gr_mid = bf16(gr - gr_hi), gr_lo = bf16(gr - gr_hi - gr_mid), and each
+// tile takes all three products, so a term is as accurate as gr itself in fp32 (the
+// split holds gr to about 2^-27; fp32 accumulation). The packed operands use
 // a k-blocked layout, element (k, m) at ((k / 8) * Np + m) * 8 + k % 8, so one 16-byte load
 // holds the 8 consecutive k of one column that an MFMA lane supplies; a row k is
 // (t * Bp + b) with the batch padded to a multiple of 32, so a 32-row batch chunk of one
@@ -39,31 +40,35 @@ __device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
     return u >> 16;
 }
 
-// gr (T, B, N) fp32 -> gr_hi, gr_lo in the k-blocked layout (Kp rows, Np columns; padding
-// rows and columns are zero).
+// gr (T, B, N) fp32 -> gr_hi, gr_mid, gr_lo in the k-blocked layout (Kp rows, Np columns;
+// padding rows and columns are zero).
 __global__ void pack_gr_kernel(const float* __restrict__ gr, int T, int B, int Bp, int N, int Np,
-                               int Kp, uint4* __restrict__ hi, uint4* __restrict__ lo) {
+                               int Kp, uint4* __restrict__ hi, uint4* __restrict__ mid,
+                               uint4* __restrict__ lo) {
     const size_t total = (size_t)(Kp / 8) * Np;
     for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total;
          q += (size_t)gridDim.x * blockDim.x) {
         const int kb = (int)(q / Np), m = (int)(q - (size_t)kb * Np);
-        uint32_t h[4], l[4];
+        uint32_t h[4], md[4], l[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-            float v[2];
+            uint32_t hb[2], mb[2], lb[2];
 #pragma unroll
             for (int f = 0; f < 2; ++f) {
                 const int k = kb * 8 + e + f;
                 const int t = k / Bp, b = k - (k / Bp) * Bp;
-                v[f] = (t < T && b < B && m < N) ? gr[((size_t)t * B + b) * N + m] : 0.0f;
+                const float v = (t < T && b < B && m < N) ? gr[((size_t)t * B + b) * N + m] : 0.0f;
+                hb[f] = bf16_rne_bits(v);
+                const float r = v - __uint_as_float(hb[f] << 16);
+                mb[f] = bf16_rne_bits(r);
+                lb[f] = bf16_rne_bits(r - __uint_as_float(mb[f] << 16));
             }
-            const uint32_t h0 = bf16_rne_bits(v[0]), h1 = bf16_rne_bits(v[1]);
-            const uint32_t l0 = bf16_rne_bits(v[0] - __uint_as_float(h0 << 16));
-            const uint32_t l1 = bf16_rne_bits(v[1] - __uint_as_float(h1 << 16));
-            h[e / 2] = h0 | (h1 << 16);
-            l[e / 2] = l0 | (l1 << 16);
+            h[e / 2] = hb[0] | (hb[1] << 16);
+            md[e / 2] = mb[0] | (mb[1] << 16);
+            l[e / 2] = lb[0] | (lb[1] << 16);
         }
         hi[q] = uint4{h[0], h[1], h[2], h[3]};
+        mid[q] = uint4{md[0], md[1], md[2], md[3]};
         lo[q] = uint4{l[0], l[1], l[2], l[3]};
     }
 }
@@ -191,7 +196,7 @@ __global__ void __launch_bounds__(1024) lag_meta_kernel(const int* __restrict__ 
 // sums per chunk). A time slice of an operand is the chunk's 4 k-blocks at time t.
 //
 // For the relative lags r = q0 .. q0 + RL - 1 of one pass, C_r = sum_tau A(tau) Y'(tau - r)
-// with A = (gr_hi, gr_lo). Step n reads the gr slice tau = q0 + n once and multiplies it
+// with A = (gr_hi, gr_mid, gr_lo). Step n reads the gr slice tau = q0 + n once and multiplies it
 // with the spike slices n - r', r' < RL, which stay in registers: a window of kWY slots
 // holds slice sigma in slot sigma mod kWY, so step n refills slot (n + P) mod kWY (slice
 // n + P, P = kWY - RL ahead) after its last reader, step n - 1, and the gr slices rotate
@@ -200,13 +205,12 @@ __global__ void __launch_bounds__(1024) lag_meta_kernel(const int* __restrict__ 
 // One descriptor per operand spans the chunk's slices 0 .. T-1, so slices at or past T
 // read as zeros; slice t is the byte offset t * (Bp / 8) * Np * 16 plus the lane's column.
 constexpr int kWT = 64;    // output tile (i and j)
-constexpr int kWA = 4;     // gr-slice registers (3 slices ahead)
 
 __device__ __forceinline__ bf16x8 load16(i32x4 rs, int voff) {
     return __builtin_bit_cast(bf16x8, raw_buffer_load_i32x4(rs, voff, 0, 0));
 }
 
-template <int RL, int kWY, bool DS>
+template <int RL, int kWY, int kWA, bool DS>
 __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, int bc, int rt) {
     constexpr int P = kWY - RL;   // spike slices loaded ahead
     static_assert(kWY % kWA == 0 && P >= 1, "window slots");
@@ -217,6 +221,7 @@ __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, i
     const size_t chunk = (size_t)bc * 4 * Np;                  // uint4 offset of the chunk
     const uint32_t span = (uint32_t)T * slice - (uint32_t)(chunk * 16);
     const i32x4 rhi = buffer_rsrc(p.ahi + chunk, span);
+    const i32x4 rmd = buffer_rsrc(p.amd + chunk, span);
     const i32x4 rlo = buffer_rsrc(p.alo + chunk, span);
     const i32x4 ryb = buffer_rsrc(p.yb + chunk, span);
     // lane offsets of the first 16-column block; the second is 256 bytes further
@@ -242,7 +247,7 @@ __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, i
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) acc[r][mb][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
-        bf16x8 yw[kWY][2], ah[kWA][2], al[kWA][2];
+        bf16x8 yw[kWY][2], ah[kWA][2], am[kWA][2], al[kWA][2];
 #pragma unroll
         for (int sl = 0; sl < kWY; ++sl) {
             if (sl < P) {   // slices 0 .. P-1; the other slots hold slices -RL+1 .. -1
@@ -259,6 +264,8 @@ __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, i
             const uint32_t o = va + (uint32_t)(q0 + sl) * slice;
             ah[sl][0] = load16(rhi, o);
             ah[sl][1] = load16(rhi, o + 256);
+            am[sl][0] = load16(rmd, o);
+            am[sl][1] = load16(rmd, o + 256);
             al[sl][0] = load16(rlo, o);
             al[sl][1] = load16(rlo, o + 256);
         }
@@ -274,6 +281,8 @@ __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, i
                     yw[(u + P) % kWY][1] = load16(ryb, oy + 256);
                     ah[(u + kWA - 1) % kWA][0] = load16(rhi, oa);
                     ah[(u + kWA - 1) % kWA][1] = load16(rhi, oa + 256);
+                    am[(u + kWA - 1) % kWA][0] = load16(rmd, oa);
+                    am[(u + kWA - 1) % kWA][1] = load16(rmd, oa + 256);
                     al[(u + kWA - 1) % kWA][0] = load16(rlo, oa);
                     al[(u + kWA - 1) % kWA][1] = load16(rlo, oa + 256);
                     oy += slice;
@@ -290,6 +299,14 @@ __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, i
                         for (int nb = 0; nb < 2; ++nb)
                             acc[r][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                                 ah[sa][mb], yw[(u - r + kWY) % kWY][nb], acc[r][mb][nb], 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < RL; ++r)
+#pragma unroll
+                    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb)
+                            acc[r][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                am[sa][mb], yw[(u - r + kWY) % kWY][nb], acc[r][mb][nb], 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < RL; ++r)
 #pragma unroll
@@ -355,7 +372,9 @@ __global__ void __launch_bounds__(256) lag_win_kernel(LagBf16 p) {
     for (int k = 32; k >= 1; k >>= 1) rt = max(rt, __shfl_xor(rt, k));
     rt = __builtin_amdgcn_readfirstlane(rt);
     if ((rt <= 10) != (RL == 10)) return;
-    lag_win_body<RL, RL == 10 ? 12 : 16, DS>(p, i0, j0, bc, rt);
+    // gr-slice registers: 3 slots (2 slices ahead) beside the 12-slot spike window, 4 slots
+    // (3 ahead) beside the 16-slot one
+    lag_win_body<RL, RL == 10 ? 12 : 16, RL == 10 ? 3 : 4, DS>(p, i0, j0, bc, rt);
 }
 
 void launch_lag_cols(const LagBf16& a, hipStream_t stream) {
@@ -367,7 +386,8 @@ void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hi
     const size_t total = (size_t)(a.Kp / 8) * a.Np;
     const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 65535u * 4);
     hipLaunchKernelGGL(pack_gr_kernel, dim3(blocks), dim3(256), 0, stream, gr, a.T, a.B, a.Bp, a.N,
-                       a.Np, a.Kp, const_cast<uint4*>(a.ahi), const_cast<uint4*>(a.alo));
+                       a.Np, a.Kp, const_cast<uint4*>(a.ahi), const_cast<uint4*>(a.amd),
+                       const_cast<uint4*>(a.alo));
     hipLaunchKernelGGL(pack_spikes_kernel, dim3(blocks), dim3(256), 0, stream, bits, a.lo, a.T, a.B,
                        a.Bp, a.N, a.Np, a.Kp, const_cast<uint4*>(a.yb));
     const int tiles = (a.Np / kWT) * (a.Np / kWT);

@@ -101,17 +101,18 @@ __global__ void __launch_bounds__(256) pack_lagw_kernel(LagStepPack p) {
 // k split; 32-k stages go global -> registers (S stages ahead, fixed register slots:
 // the loop is unrolled over S) -> LDS (double-buffered, one barrier per stage) -> fragment
 // registers (double-buffered: the next stage's fragments load while this stage multiplies).
-// PA = 1: A x (P_hi + P_lo). PA = 2: A_hi x P_hi + A_hi x P_lo + A_lo x P_hi.
+// PA = 1: A x (P_hi + P_lo). PA = 2: A_hi x P_hi + A_hi x P_lo + A_lo x P_hi. PB = 1 (a one-
+// plane P, e.g. bf16 weights): A x P, or A_hi x P + A_lo x P.
 // Block order: workgroups are dealt to the 8 XCDs in turn (XCD = id mod 8), so when KS is a
 // multiple of 8 each XCD takes KS / 8 whole k splits with all their row and column tiles:
 // the A tile of a (row tile, split) and the P tile of a (column tile, split) are then
 // fetched into one L2 and shared there by every workgroup that reads them. Otherwise (the
 // per-block GEMM: many row tiles, few splits) each XCD takes a quarter of the row tiles
 // times half of the column tiles, so each A tile is fetched by 2 XCDs and each P tile by 4.
-template <int PA, int S>
+template <int PA, int PB, int S>
 __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
     extern __shared__ uint4 lds_u4[];
-    constexpr int PL = PA + 2;
+    constexpr int PL = PA + PB;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int wi = w >> 1, wj = w & 1, g = lane >> 4, lc = lane & 15;
     const int NT = p.Np / 128;
@@ -144,13 +145,13 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
     const int s0 = ks * per;
     const int ns = max(min(nst, s0 + per) - s0, 0);
 
-    i32x4 ra[PA], rb[2];
+    i32x4 ra[PA], rb[PB];
     const uint32_t abytes = (uint32_t)((size_t)p.B * p.lda * 2);
     ra[0] = buffer_rsrc(p.a0, abytes);
     if (PA > 1) ra[PA - 1] = buffer_rsrc(p.a1, abytes);
     const uint32_t pbytes = (uint32_t)((size_t)(p.Kt / 8) * p.Np * 16);
     rb[0] = buffer_rsrc(p.p0, pbytes);
-    rb[1] = buffer_rsrc(p.p1, pbytes);
+    if (PB > 1) rb[PB - 1] = buffer_rsrc(p.p1, pbytes);
     // staging: thread tid stages uint4 c = tid + 256 h (k-block c >> 7, row / column c & 127)
     uint32_t oa[2], ob[2];
     const uint32_t bstep = (uint32_t)(4 * p.Np * 16);
@@ -170,7 +171,7 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
             for (int q = 0; q < PA; ++q)
                 st[slot][q][h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(ra[q], (int)oa[h], 0, 0));
 #pragma unroll
-            for (int q = 0; q < 2; ++q)
+            for (int q = 0; q < PB; ++q)
                 st[slot][PA + q][h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rb[q], (int)ob[h], 0, 0));
             oa[h] += 64;
             ob[h] += bstep;
@@ -188,7 +189,7 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    bf16x8 fa[2][PA][4], fb[2][2][4];   // fragments: the stage being multiplied and the next
+    bf16x8 fa[2][PA][4], fb[2][PB][4];  // fragments: the stage being multiplied and the next
     auto frags = [&](int f, int buf) {
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
@@ -196,7 +197,7 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
             for (int q = 0; q < PA; ++q)
                 fa[f][q][x] = __builtin_bit_cast(bf16x8, lds_u4[(buf * PL + q) * 512 + g * 128 + wi * 64 + x * 16 + lc]);
 #pragma unroll
-            for (int q = 0; q < 2; ++q)
+            for (int q = 0; q < PB; ++q)
                 fb[f][q][x] = __builtin_bit_cast(bf16x8, lds_u4[(buf * PL + PA + q) * 512 + g * 128 + wj * 64 + x * 16 + lc]);
         }
     };
@@ -223,11 +224,13 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
 #pragma unroll
                     for (int nb = 0; nb < 4; ++nb)
                         acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][0][mb], fb[f][0][nb], acc[mb][nb], 0, 0, 0);
+                if (PB > 1) {
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb)
+                    for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-                    for (int nb = 0; nb < 4; ++nb)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][0][mb], fb[f][1][nb], acc[mb][nb], 0, 0, 0);
+                        for (int nb = 0; nb < 4; ++nb)
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][0][mb], fb[f][PB - 1][nb], acc[mb][nb], 0, 0, 0);
+                }
                 if (PA > 1) {
 #pragma unroll
                     for (int mb = 0; mb < 4; ++mb)
@@ -525,18 +528,22 @@ constexpr int kLagStepStages = 4;
 constexpr int kLagStepBlock = 8;   // steps per block (near lags per step)
 int lagstep_block() { return kLagStepBlock; }
 
-size_t lagstep_gemm_lds(int pa) { return (size_t)2 * (pa + 2) * 512 * sizeof(uint4); }
+size_t lagstep_gemm_lds(int pa, int pb) { return (size_t)2 * (pa + pb) * 512 * sizeof(uint4); }
 
-void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream) {
-    const int grid = ((g.rows + 127) / 128) * (g.Np / 128) * g.KS;
-    const size_t lds = lagstep_gemm_lds(pa);
-    if (pa == 1) {
-        ensure_lds((const void*)lagstep_gemm_kernel<1, kLagStepStages>, lds);
-        hipLaunchKernelGGL((lagstep_gemm_kernel<1, kLagStepStages>), dim3(grid), dim3(256), lds, stream, g);
-    } else {
-        ensure_lds((const void*)lagstep_gemm_kernel<2, kLagStepStages>, lds);
-        hipLaunchKernelGGL((lagstep_gemm_kernel<2, kLagStepStages>), dim3(grid), dim3(256), lds, stream, g);
+#define DELREC_LAGSTEP_GEMM(PAV, PBV)                                                          \
+    if (pa == PAV && pb == PBV) {                                                              \
+        ensure_lds((const void*)lagstep_gemm_kernel<PAV, PBV, kLagStepStages>, lds);          \
+        hipLaunchKernelGGL((lagstep_gemm_kernel<PAV, PBV, kLagStepStages>), dim3(grid), dim3(256), lds, \
+                           stream, g);                                                         \
+        return;                                                                                \
     }
+
+void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream, int pb) {
+    const int grid = ((g.rows + 127) / 128) * (g.Np / 128) * g.KS;
+    const size_t lds = lagstep_gemm_lds(pa, pb);
+    DELREC_LAGSTEP_GEMM(1, 2)
+    DELREC_LAGSTEP_GEMM(2, 2)
+    DELREC_LAGSTEP_GEMM(2, 1)
 }
 
 // far lags of a block: rows (b, tt) of g.part with g.rp == kLagStepBlock

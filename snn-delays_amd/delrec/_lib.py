@@ -73,7 +73,8 @@ class SynFwdArgs(ctypes.Structure):
                 ('x', c_vp), ('W', c_vp), ('w_bf16', c_i32), ('bias', c_vp), ('d', c_vp),
                 ('base', c_vp), ('offsets', c_vp), ('s', c_vp), ('s_uniform', c_f32),
                 ('s_max', c_f32), ('drop', c_vp), ('lif', Lif), ('y', c_vp), ('u', c_vp), ('bits', c_vp),
-                ('workspace', c_vp), ('workspace_bytes', c_size)]
+                ('workspace', c_vp), ('workspace_bytes', c_size),
+                ('d_min', c_f32), ('off_min', c_i32), ('off_count', c_i32)]
 
 
 class SynBwdArgs(ctypes.Structure):
@@ -82,7 +83,8 @@ class SynBwdArgs(ctypes.Structure):
                 ('w_bf16', c_i32), ('d', c_vp), ('base', c_vp), ('offsets', c_vp), ('s', c_vp),
                 ('s_uniform', c_f32), ('s_max', c_f32), ('drop', c_vp), ('lif', Lif),
                 ('dx', c_vp), ('dW', c_vp), ('dd', c_vp), ('ds', c_vp), ('db', c_vp),
-                ('workspace', c_vp), ('workspace_bytes', c_size)]
+                ('workspace', c_vp), ('workspace_bytes', c_size),
+                ('d_min', c_f32), ('off_min', c_i32), ('off_count', c_i32)]
 
 
 class LifFwdArgs(ctypes.Structure):

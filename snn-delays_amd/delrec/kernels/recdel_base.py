@@ -17,6 +17,7 @@ Modes (reference ``recdel_base.py:361-383``):
 
 import ctypes
 import os
+import threading
 
 import torch
 
@@ -39,7 +40,17 @@ def _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v
             and os.environ.get('DELREC_AXONAL_FWD') != 'tiled')
 
 
+# the caller's grad mode at apply() (forward() itself runs with gradients disabled, and
+# ctx.needs_input_grad follows the inputs' requires_grad even under torch.no_grad())
+_APPLY_STATE = threading.local()
+
+
 class AxonalRecdelHip(torch.autograd.Function):
+    @classmethod
+    def apply(cls, *args, **kwargs):
+        _APPLY_STATE.grad = torch.is_grad_enabled()
+        return super().apply(*args, **kwargs)
+
     @staticmethod
     def forward(ctx, x, W, bias, d, p_spread, drop, sigma, tau, v_th, v_reset, use_sig_p,
                 detach_reset, surr_id, gamma=1.0, approx=False, ste_mode=0, alpha=2.0,
@@ -74,7 +85,7 @@ class AxonalRecdelHip(torch.autograd.Function):
         # max d into pinned host memory, and the backward reads it (by then it has long
         # arrived). Without gradients the read stays synchronous so that an over-long window
         # raises.
-        if (any(ctx.needs_input_grad[:5])
+        if (getattr(_APPLY_STATE, 'grad', True) and any(ctx.needs_input_grad[:5])
                 and _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v_reset,
                                            T * B)):
             ticket = ctypes.c_uint32(0)

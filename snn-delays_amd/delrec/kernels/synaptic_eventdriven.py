@@ -9,6 +9,7 @@ followed by the lag-correlation GEMM, which folds ``dW = sum_l h * C_l`` and
 ``(N, N, L)`` lag stack.
 """
 
+import numpy as np
 import torch
 
 from .. import _lib
@@ -23,11 +24,26 @@ def _spread(layer, device):
     return None
 
 
-def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop, lif):
+def hybrid_form(d_min, s_uniform, off_range):
+    """The hybrid's scan-form fields: ``(d_min, off_min, off_count, flags)`` for the argument
+    structs and the workspace query (bit 2: every tap at a lag >= 1, i.e. d_min >= s - 1 in
+    float32 as the entry point compares; bits 16..23: the offset count); zeros when the
+    offset range is unknown (``off_range`` None)."""
+    if off_range is None:
+        return 0.0, 0, 0, 0
+    off_min, off_count = off_range
+    d32, s32 = np.float32(d_min), np.float32(s_uniform)
+    lags_ok = bool(d32 >= np.float32(s32 - np.float32(1.0)))
+    return float(d32), int(off_min), int(off_count), (4 if lags_ok else 0) | (min(int(off_count), 255) << 16)
+
+
+def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop, lif, off_range=None):
     """Launch ``delrec_syn_fwd`` with per-connection delays ``d_eff`` (N, N), or with the
     hybrid ``base`` (N) + int8 ``offsets`` (N, N) when ``d_eff`` is None; ``d_all`` is a
-    device tensor holding every effective delay (for the window length). Returns
-    ``(y, u, bits, L, Wc, w_bf16, s_max)``."""
+    device tensor holding every effective delay (for the window length); ``off_range`` =
+    (smallest offset, offset count) of the hybrid's int8 offsets. Returns
+    ``(y, u, bits, L, Wc, w_bf16, s_max, hyb)`` with ``hyb`` the hybrid's scan-form fields
+    (``hybrid_form``) for the backward."""
     require_device(x)
     T, B, N = x.shape
     dev = x.device
@@ -40,27 +56,33 @@ def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop,
     # taken after the host work above so that it overlaps the GPU work still queued
     if s_vec is not None:
         d_max, s_max = read_scalars(d_all.max(), s_vec.max())
+        d_min = d_max
+    elif off_range is not None:
+        (d_max, d_min), s_max = read_scalars(d_all.max(), d_all.min()), s_uniform
     else:
         (d_max,), s_max = read_scalars(d_all.max()), s_uniform
+        d_min = d_max
     L = max(window_length_f64(d_max, s_max), 2)
+    hyb = hybrid_form(d_min, s_uniform, off_range if d_eff is None and s_vec is None else None)
     # the scan form follows the taps per connection: the entry point's smax (the largest
     # per-column half-width, or the uniform one)
     smax = float(s_max) if s_vec is not None else max(float(s_max), float(s_uniform))
-    flags = w_bf16 | (2 if d_eff is None else 0) | (_lib.lag_taps(smax) << 8)
+    flags = w_bf16 | (2 if d_eff is None else 0) | (_lib.lag_taps(smax) << 8) | hyb[3]
     ws = _lib.workspace(_lib.WS_SYN_FWD, T, B, N, L, flags, dev)
     args = _lib.SynFwdArgs(
         T=T, B=B, N=N, L=L, x=_lib.ptr(xc), W=_lib.ptr(Wc), w_bf16=w_bf16, bias=_lib.ptr(bias),
         d=_lib.ptr(d_eff), base=_lib.ptr(base), offsets=_lib.ptr(offsets), s=_lib.ptr(s_vec),
         s_uniform=float(s_uniform), s_max=float(s_max), drop=_lib.ptr(drop), lif=lif, y=_lib.ptr(y),
-        u=_lib.ptr(u), bits=_lib.ptr(bits), workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
+        u=_lib.ptr(u), bits=_lib.ptr(bits), workspace=_lib.ptr(ws), workspace_bytes=ws.numel(),
+        d_min=hyb[0], off_min=hyb[1], off_count=hyb[2])
     _lib.call('delrec_syn_fwd', args, _lib.stream_of(xc))
-    return y, u, bits, L, Wc, w_bf16, float(s_max)
+    return y, u, bits, L, Wc, w_bf16, float(s_max), hyb
 
 
 def syn_backward(gy, u, y, bits, Wc, w_bf16, d_eff, base, offsets, s_vec, s_uniform, s_max, drop, lif,
-                 L, need_W, need_d, need_s, need_b):
-    """Launch ``delrec_syn_bwd``. Returns ``(dx, dW, dd, ds, db)`` (``None`` where not
-    requested)."""
+                 L, need_W, need_d, need_s, need_b, hyb=(0.0, 0, 0, 0)):
+    """Launch ``delrec_syn_bwd`` (``hyb``: the forward's hybrid scan-form fields). Returns
+    ``(dx, dW, dd, ds, db)`` (``None`` where not requested)."""
     T, B, N = u.shape
     dev = u.device
     gy = gy.to(torch.float32).contiguous()
@@ -71,14 +93,14 @@ def syn_backward(gy, u, y, bits, Wc, w_bf16, d_eff, base, offsets, s_vec, s_unif
     db = torch.empty(N, device=dev, dtype=torch.float32) if need_b else None
     smax = float(s_uniform) if d_eff is None else (float(s_max) if s_vec is not None
                                                    else max(float(s_max), float(s_uniform)))
-    flags = w_bf16 | (2 if d_eff is None else 0) | (_lib.lag_taps(smax) << 8)
+    flags = w_bf16 | (2 if d_eff is None else 0) | (_lib.lag_taps(smax) << 8) | hyb[3]
     ws = _lib.workspace(_lib.WS_SYN_BWD, T, B, N, L, flags, dev)
     args = _lib.SynBwdArgs(
         T=T, B=B, N=N, L=L, gy=_lib.ptr(gy), u=_lib.ptr(u), y=_lib.ptr(y), bits=_lib.ptr(bits),
         W=_lib.ptr(Wc), w_bf16=w_bf16, d=_lib.ptr(d_eff), base=_lib.ptr(base),
         offsets=_lib.ptr(offsets), s=_lib.ptr(s_vec), s_uniform=float(s_uniform), s_max=float(s_max),
         drop=_lib.ptr(drop), lif=lif, dx=_lib.ptr(dx), dW=_lib.ptr(dW), dd=_lib.ptr(dd), ds=_lib.ptr(ds), db=_lib.ptr(db),
-        workspace=_lib.ptr(ws), workspace_bytes=ws.numel())
+        workspace=_lib.ptr(ws), workspace_bytes=ws.numel(), d_min=hyb[0], off_min=hyb[1], off_count=hyb[2])
     _lib.call('delrec_syn_bwd', args, _lib.stream_of(gy))
     return dx, dW, dd, ds, db
 
@@ -99,8 +121,8 @@ class EventDrivenSyn(torch.autograd.Function):
         m = drop_bn(drop, T, B, N)
         bc = None if bias is None else bias.detach().to(torch.float32).contiguous()
         lif = layer_lif(layer)
-        y, u, bits, L, Wc, w_bf16, s_max = syn_forward(x, W, d_eff, None, None, s_vec, s_uniform, d_eff,
-                                                       bc, m, lif)
+        y, u, bits, L, Wc, w_bf16, s_max, _ = syn_forward(x, W, d_eff, None, None, s_vec, s_uniform, d_eff,
+                                                          bc, m, lif)
         ctx.save_for_backward(u, y, bits, Wc, d_eff, s_vec, m, p_spread)
         ctx.meta = (L, w_bf16, s_uniform, s_max, float(layer.sigma), bool(layer.use_sig_p),
                     bias is not None, W.dtype)

@@ -31,31 +31,37 @@ def hybrid_kernel_usable(layer, x_seq):
 
 
 def _int8_offsets(layer):
-    """``(base, int8 offsets)`` read from the hybrid parametrisation, or ``(None, None)``."""
+    """``(base, int8 offsets, (smallest offset, offset count))`` read from the hybrid
+    parametrisation, or ``(None, None, None)``. The offsets are frozen: their int8 copy and
+    range are computed once per tensor version."""
     from torch.nn.utils import parametrize
     if layer.round_delays or not parametrize.is_parametrized(layer, 'recurrent_delays'):
-        return None, None
+        return None, None, None
     plist = layer.parametrizations.recurrent_delays
     if len(plist) != 1:
-        return None, None
+        return None, None, None
     par = plist[0]
     if not hasattr(par, 'offsets') or getattr(par, 'position_shift', 0.0) != 0.0 \
             or getattr(par, 'position_sign', 1.0) != 1.0:
-        return None, None
+        return None, None, None
     off = par.offsets
     cache = getattr(layer, '_delrec_off8', None)
     key = (off.data_ptr(), off._version, off.device)
     if cache is None or cache[0] != key:
         ok = bool(((off == off.round()) & (off >= -128) & (off <= 127)).all())
         off8 = off.detach().to(torch.int8).contiguous() if ok else None
-        cache = (key, off8)
+        rng = None
+        if off8 is not None:
+            lo, hi = (int(v) for v in torch.stack([off8.min(), off8.max()]).tolist())
+            rng = (lo, hi - lo + 1)
+        cache = (key, off8, rng)
         layer._delrec_off8 = cache
     if cache[1] is None:
-        return None, None
+        return None, None, None
     base = plist.original
     if base.dim() != 1:
-        return None, None
-    return base.detach().to(torch.float32).contiguous(), cache[1]
+        return None, None, None
+    return base.detach().to(torch.float32).contiguous(), cache[1], cache[2]
 
 
 class HybridSynDelay(torch.autograd.Function):
@@ -66,26 +72,27 @@ class HybridSynDelay(torch.autograd.Function):
         T, B, N = x.shape
         d_det = d.detach()
         d_eff = (d_det.round() if layer.round_delays else d_det).to(torch.float32).contiguous()
-        base, off8 = _int8_offsets(layer)
+        base, off8, off_range = _int8_offsets(layer)
         s = 1.0 + float(layer.sigma)
         m = drop_bn(drop, T, B, N)
         bc = None if bias is None else bias.detach().to(torch.float32).contiguous()
         lif = layer_lif(layer)
         d_arg = None if base is not None else d_eff
-        y, u, bits, L, Wc, w_bf16, _ = syn_forward(x, W, d_arg, base, off8, None, s, d_eff, bc, m, lif)
+        y, u, bits, L, Wc, w_bf16, _, hyb = syn_forward(x, W, d_arg, base, off8, None, s, d_eff, bc, m, lif,
+                                                        off_range=off_range)
         ctx.save_for_backward(u, y, bits, Wc, d_arg, base, off8, m)
-        ctx.meta = (L, w_bf16, s, bias is not None, W.dtype)
+        ctx.meta = (L, w_bf16, s, bias is not None, W.dtype, hyb)
         ctx.lif = lif
         return y
 
     @staticmethod
     def backward(ctx, gy):
         u, y, bits, Wc, d_arg, base, off8, m = ctx.saved_tensors
-        L, w_bf16, s, use_bias, w_dtype = ctx.meta
+        L, w_bf16, s, use_bias, w_dtype, hyb = ctx.meta
         dx, dW, dd, _, db = syn_backward(
             gy, u, y, bits, Wc, w_bf16, d_arg, base, off8, None, s, s, m, ctx.lif, L,
             ctx.needs_input_grad[1], ctx.needs_input_grad[2], False,
-            use_bias and ctx.needs_input_grad[3])
+            use_bias and ctx.needs_input_grad[3], hyb=hyb)
         if dW is not None and w_dtype != torch.float32:
             dW = dW.to(w_dtype)
         return dx, dW, dd, db, None, None

@@ -178,7 +178,7 @@ def test_hybrid_fwd_bwd_matches_oracle(dev, case):
 
     layer = hybrid_layer(N, W, base, offsets, dev, bf16=bf16, sigma_init=sigma)
     assert layer.sigma == sigma
-    base8, _ = sh._int8_offsets(layer)
+    base8, _, _ = sh._int8_offsets(layer)
     assert base8 is not None, 'the base + int8 offsets path was not taken'
     xg = x.to(dev).requires_grad_(True)
     y = layer.multi_step_forward_hybrid_triton(xg)
@@ -207,6 +207,24 @@ def test_hybrid_lagstep_matches_oracle(dev, case, monkeypatch):
 def test_hybrid_gather_path_matches_oracle(dev, monkeypatch):
     monkeypatch.setenv('DELREC_SYN_LAGSTEP', '0')
     test_hybrid_fwd_bwd_matches_oracle(dev, HYB_CASES[5])
+
+
+# the offset-stacked hybrid scans (taken by default where the rings do not fit LDS, as at
+# N = 2048) forced at small sizes: bases >= s - 1 (every tap at a lag >= 1), offsets up to 8,
+# fp32 and bf16 weights, one and two spike-history words (windows of 65+ lags), a triangle of
+# three taps (sigma 0.5)
+HYBSTEP_CASES = [HYB_CASES[i] for i in (0, 2, 5, 6)] + [
+    (20, 2, 64, (1.0, 12.0), 4, False, 0.5),
+    (33, 3, 130, (0.0, 25.0), 2, True, 0.0),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', HYBSTEP_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}{"bf16" if c[5] else ""}s{c[6]}'
+                                                    for c in HYBSTEP_CASES])
+def test_hybrid_offset_stacked_matches_oracle(dev, case, monkeypatch):
+    monkeypatch.setenv('DELREC_SYN_HYBSTEP', '1')
+    test_hybrid_fwd_bwd_matches_oracle(dev, case)
 
 
 # the hybrid backward with one lane per source (the split form is the default for N <= 512)

@@ -210,3 +210,173 @@ def test_soft_reset_and_bias_and_dropout_plumbing():
         s = (u - 1.0 >= 0).double()
         v = u - s * 1.0
     assert torch.equal(y, torch.stack([(e['u'][t] - 1.0 >= 0).double() for t in range(x.shape[0])]))
+
+
+# ---------------------------------------------------------------------------------------
+# The hard-tap forwards of the reference's fused kernel (approx, STE) and the other scans.
+
+def _grads(fn, x, W, d, gy, **kw):
+    xr, Wr, dr = (t.clone().requires_grad_(True) for t in (x, W, d))
+    y, e = fn(xr, Wr, dr, neuron.LIFParams(), **kw)
+    (y * gy).sum().backward()
+    return y.detach(), e['u'].detach(), xr.grad, Wr.grad, dr.grad
+
+
+@pytest.mark.parametrize('taps', ['approx', 'ste_round', 'ste_interp'])
+def test_hard_taps_reduce_to_the_soft_triangle_at_integer_delays(taps):
+    """sigma = 0 with integer d: the triangle is one tap of weight 1 at lag d + 1, which is
+    what every hard-tap forward takes, so values agree exactly; the STE backward is the soft
+    one (all gradients agree), the approx backward is the single tap (x and W agree; its
+    straight-through dd does not follow the triangle)."""
+    g, x, W = _inputs(21)
+    d = torch.tensor([0.0, 1.0, 2.0, 3.0, 5.0, 1.0], dtype=torch.float64)
+    gy = torch.randn(x.shape, generator=g, dtype=torch.float64)
+    ref = _grads(scans.axonal_v2, x, W, d, gy, sigma=0.0)
+    got = _grads(scans.axonal_v2, x, W, d, gy, sigma=0.0, taps=taps)
+    assert torch.equal(got[0], ref[0])
+    assert 0 < float(ref[0].mean()) < 1
+    torch.testing.assert_close(got[1], ref[1], rtol=0, atol=0)
+    for a, b in zip(got[2:4], ref[2:4]):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+    if taps != 'approx':
+        torch.testing.assert_close(got[4], ref[4], rtol=1e-12, atol=1e-12)
+
+
+def test_ste_interp_is_the_soft_triangle_at_sigma_0():
+    """At sigma = 0 the triangle over lags floor(1 + d), +1 has the weights 1 - frac, frac:
+    the two-tap interpolated forward equals the soft one for any d >= 0 (to rounding)."""
+    g, x, W = _inputs(22)
+    d = torch.rand(6, generator=g, dtype=torch.float64) * 6
+    gy = torch.randn(x.shape, generator=g, dtype=torch.float64)
+    ref = _grads(scans.axonal_v2, x, W, d, gy, sigma=0.0)
+    got = _grads(scans.axonal_v2, x, W, d, gy, sigma=0.0, taps='ste_interp')
+    assert torch.equal(got[0], ref[0])
+    for a, b in zip(got[1:], ref[1:]):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+
+
+def _scalar_axonal_approx(x, W, d, gy, tau=2.0, th=1.0):
+    """The approx mode as explicit scalar recursions (no autograd): one tap at
+    lag = max(1, round(d) + 1) forward and backward, hard reset to 0, ATan(2), and the
+    straight-through dd_j = sum_t gz_j(t) (y_j(t - lag - 1) - y_j(t - lag))."""
+    T, N = len(x), len(W)
+    decay = 1.0 - 1.0 / tau
+    lmax = round(max(d)) + 2
+    lag = [min(max(1, round(dj) + 1), lmax - 1) for dj in d]
+    yat = lambda y, t, j: y[t][j] if t >= 0 else 0.0
+    y = [[0.0] * N for _ in range(T)]
+    u = [[0.0] * N for _ in range(T)]
+    z = [[0.0] * N for _ in range(T)]
+    v = [0.0] * N
+    for t in range(T):
+        for j in range(N):
+            z[t][j] = yat(y, t - lag[j], j)
+        for i in range(N):
+            u[t][i] = v[i] * decay + x[t][i] + sum(W[i][j] * z[t][j] for j in range(N))
+            y[t][i] = 1.0 if u[t][i] - th >= 0 else 0.0
+            v[i] = 0.0 if y[t][i] else u[t][i]
+    gz = [[0.0] * N for _ in range(T)]
+    grs = [None] * T
+    dx = [[0.0] * N for _ in range(T)]
+    lam = [0.0] * N
+    for t in range(T - 1, -1, -1):
+        gr = [0.0] * N
+        for j in range(N):
+            gfut = gz[t + lag[j]][j] if t + lag[j] < T else 0.0
+            sg = 1.0 / (1.0 + (math.pi * (u[t][j] - th)) ** 2)
+            du = lam[j] * (1.0 - y[t][j]) + (gy[t][j] + gfut - lam[j] * u[t][j]) * sg
+            lam[j] = decay * du
+            dx[t][j] = gr[j] = du
+        for j in range(N):
+            gz[t][j] = sum(gr[i] * W[i][j] for i in range(N))
+        grs[t] = gr
+    dW = [[sum(grs[t][i] * z[t][j] for t in range(T)) for j in range(N)] for i in range(N)]
+    dd = [sum(gz[t][j] * (yat(y, t - lag[j] - 1, j) - yat(y, t - lag[j], j)) for t in range(T))
+          for j in range(N)]
+    return y, dx, dW, dd
+
+
+def test_approx_matches_scalar_reverse_recursion():
+    g = torch.Generator().manual_seed(23)
+    T, N = 14, 5
+    x = torch.rand(T, 1, N, generator=g, dtype=torch.float64) * 1.5
+    W = torch.randn(N, N, generator=g, dtype=torch.float64) * 0.9
+    d = torch.tensor([0.4, 1.5, 2.5, 2.7, 4.2], dtype=torch.float64)   # incl. halves (to even)
+    gy = torch.randn(T, 1, N, generator=g, dtype=torch.float64)
+    y, _, gx, gW, gd = _grads(scans.axonal_v2, x, W, d, gy, sigma=0.0, taps='approx')
+    ys, dx, dW, dd = _scalar_axonal_approx(x[:, 0].tolist(), W.tolist(), d.tolist(), gy[:, 0].tolist())
+    assert y[:, 0].tolist() == ys
+    assert 0 < sum(map(sum, ys)) < T * N
+    torch.testing.assert_close(gx[:, 0], torch.tensor(dx, dtype=torch.float64), rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(gW, torch.tensor(dW, dtype=torch.float64), rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(gd, torch.tensor(dd, dtype=torch.float64), rtol=1e-10, atol=1e-12)
+    assert any(abs(v) > 1e-6 for v in dd)
+
+
+@pytest.mark.parametrize('decay_input', [False, True])
+@pytest.mark.parametrize('v_reset', [0.0, -0.3, 0.25])
+def test_charge_forms_follow_their_closed_forms_at_zero_weights(decay_input, v_reset):
+    """W = 0, constant input x per neuron and a threshold out of reach: the membrane relaxes
+    from v_reset geometrically with ratio (1 - 1/tau) to its fixed point,
+        decay_input=False:  h_t = v_r + tau x - tau x (1 - 1/tau)^(t+1)
+        decay_input=True:   h_t = v_r + x - x (1 - 1/tau)^(t+1),
+    the solutions of v <- v - (v - v_r)/tau + x and v <- v + (x - (v - v_r))/tau."""
+    tau, T, N = 3.0, 20, 4
+    x = torch.tensor([0.1, -0.2, 0.35, 0.0], dtype=torch.float64).expand(T, 1, N).contiguous()
+    lif = neuron.LIFParams(tau=tau, v_threshold=50.0, v_reset=v_reset, decay_input=decay_input)
+    _, e = scans.axonal_v2(x, torch.zeros(N, N, dtype=torch.float64), torch.ones(N, dtype=torch.float64),
+                           lif, sigma=0.0)
+    r = 1.0 - 1.0 / tau
+    t = torch.arange(T, dtype=torch.float64).view(T, 1, 1)
+    amp = x if decay_input else tau * x
+    expected = v_reset + amp - amp * r ** (t + 1)
+    torch.testing.assert_close(e['u'], expected, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize('decay_input', [False, True])
+def test_hard_reset_to_nonzero_restarts_the_closed_form(decay_input):
+    """A spike resets v to v_reset, after which the membrane follows the same closed form
+    again from step 0 (checked at a threshold the constant input crosses periodically)."""
+    tau, T, v_reset, th = 2.0, 24, 0.2, 0.9
+    xv = 0.45 if not decay_input else 1.1
+    x = torch.full((T, 1, 1), xv, dtype=torch.float64)
+    lif = neuron.LIFParams(tau=tau, v_threshold=th, v_reset=v_reset, decay_input=decay_input)
+    y, e = scans.axonal_v2(x, torch.zeros(1, 1, dtype=torch.float64), torch.ones(1, dtype=torch.float64), lif,
+                           sigma=0.0)
+    r = 1.0 - 1.0 / tau
+    amp = xv if decay_input else tau * xv
+    k = 0
+    for t in range(T):
+        h = v_reset + amp - amp * r ** (k + 1)
+        assert float(e['u'][t, 0, 0]) == pytest.approx(h, abs=1e-12)
+        fired = h >= th
+        assert float(y[t, 0, 0]) == (1.0 if fired else 0.0)
+        k = 0 if fired else k + 1
+    assert 0 < float(y.sum()) < T
+
+
+def test_vanilla_is_the_axonal_scan_at_zero_delay_with_w_transposed():
+    """rec(t) = y(t-1) W (the reference's product order, delay_layers_pytorch.py:34) is the
+    axonal scan with every delay 0 (one tap at lag 1), sigma 0 and the weights transposed."""
+    g, x, W = _inputs(24)
+    gy = torch.randn(x.shape, generator=g, dtype=torch.float64)
+    xv, Wv = x.clone().requires_grad_(True), W.clone().requires_grad_(True)
+    yv, ev = scans.vanilla(xv, Wv, neuron.LIFParams())
+    (yv * gy).sum().backward()
+    xa, Wa = x.clone().requires_grad_(True), W.clone().requires_grad_(True)
+    ya, ea = scans.axonal_v2(xa, Wa.t(), torch.zeros(6, dtype=torch.float64), neuron.LIFParams(), sigma=0.0)
+    (ya * gy).sum().backward()
+    assert torch.equal(yv, ya)
+    assert 0 < float(ya.detach().mean()) < 1
+    torch.testing.assert_close(ev['u'], ea['u'], rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(xv.grad, xa.grad, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(Wv.grad, Wa.grad, rtol=1e-12, atol=1e-12)
+
+
+def test_plain_lif_layer_is_the_recurrent_scan_without_weights():
+    g, x, _ = _inputs(25)
+    lif = neuron.LIFParams(tau=2.5)
+    y0, e0 = scans.lif_layer(x, lif)
+    y1, e1 = scans.axonal_v2(x, torch.zeros(6, 6, dtype=torch.float64), torch.ones(6, dtype=torch.float64), lif)
+    assert torch.equal(y0, y1)
+    torch.testing.assert_close(e0['u'], e1['u'], rtol=0, atol=0)
