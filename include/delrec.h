@@ -51,7 +51,8 @@ typedef enum {
     DELREC_ERR_WINDOW = 5,       /* window length L out of range for the on-chip ring  */
     DELREC_ERR_DEVICE = 6,       /* device query failed / not a gfx950 device          */
     DELREC_ERR_PENDING = 7,      /* delrec_max_take: the value did not arrive in time  */
-    DELREC_ERR_STALE = 8         /* delrec_max_take: the slot was reused by later posts */
+    DELREC_ERR_STALE = 8,        /* delrec_max_take: the slot was reused by later posts */
+    DELREC_ERR_SCRATCH = 9       /* delrec_axonal_bwd_noalloc: sizes beyond its scratch   */
 } delrec_status;
 
 /* Neuron constants (spikingjelly LIFNode semantics; reference lif.py:25-56). */
@@ -214,6 +215,15 @@ enum { DELREC_WS_AXONAL_FWD = 1, DELREC_WS_AXONAL_BWD = 2, DELREC_WS_SYN_FWD = 3
 
 int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream);
 int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream);
+/* delrec_axonal_bwd without a caller workspace: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). Same arguments and results as delrec_axonal_bwd;
+ * a->workspace / workspace_bytes are ignored. Scratch is a 64 MiB array of the library's own
+ * device memory, one per GPU, held until the process ends (looked up on the first call on a
+ * device); sizes whose workspace (delrec_query_workspace, DELREC_WS_AXONAL_BWD) exceeds it
+ * return DELREC_ERR_SCRATCH. Calls on one GPU share that array: calls that overlap on one
+ * GPU (other streams, other threads) race and must not be issued. Allocates nothing. */
+int delrec_axonal_bwd_noalloc(const delrec_axonal_bwd_args* a, void* stream);
 int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream);
 int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream);
 int delrec_lif_fwd(const delrec_lif_fwd_args* a, void* stream);

@@ -510,6 +510,40 @@ int max_slot(uint32_t& t, unsigned long long*& dslot) {
     return DELREC_OK;
 }
 
+// Scratch of delrec_axonal_bwd_noalloc: device memory that belongs to the library's code
+// object, one copy on every GPU the library runs on, held until the process ends. In host
+// code `scratch` names a host-side stand-in, never the device address: host code uses the
+// address scratch_address() looks up (per device) instead.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// The current device's copy of `scratch`, looked up once per device (with that device
+// current) on the first call that needs it.
+int scratch_address(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return DELREC_ERR_DEVICE;
+    ScratchSlot& slot = g_scratch[dev];
+    std::call_once(slot.once, [&slot] {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess) slot.ptr = p;
+    });
+    if (!slot.ptr) return DELREC_ERR_DEVICE;
+    *out = slot.ptr;
+    return DELREC_OK;
+}
+
 }  // namespace
 
 void delrec::ensure_lds(const void* fn, size_t bytes) {
@@ -544,6 +578,7 @@ const char* delrec_strerror(int status) {
         case DELREC_ERR_DEVICE: return "device query failed";
         case DELREC_ERR_PENDING: return "device value not written within the time limit";
         case DELREC_ERR_STALE: return "readback slot reused by later posts";
+        case DELREC_ERR_SCRATCH: return "sizes need more scratch than the no-alloc entry point holds (64 MiB)";
         default: return "unknown status";
     }
 }
@@ -738,6 +773,23 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream) {
     launch_axonal_bwd_tail(p, q, s);
     launch_axonal_bwd_sums(q, part, B, N, s);
     return finish_launch();
+}
+
+int delrec_axonal_bwd_noalloc(const delrec_axonal_bwd_args* a, void* stream) {
+    if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
+    AxLayout lay;
+    if (!axonal_layout(a->N, a->L, lay)) return DELREC_ERR_WINDOW;
+    Counter c;
+    axonal_bwd_ws(c, a->T, a->B, a->N, lay);
+    if (c.used > kNoAllocScratchBytes) return DELREC_ERR_SCRATCH;
+    void* ws = nullptr;
+    if (int st = scratch_address(&ws)) return st;
+    // the same launches as delrec_axonal_bwd, with this GPU's scratch as the workspace (every
+    // workspace word is written before it is read, so nothing needs clearing between calls)
+    delrec_axonal_bwd_args b = *a;
+    b.workspace = ws;
+    b.workspace_bytes = kNoAllocScratchBytes;
+    return delrec_axonal_bwd(&b, stream);
 }
 
 // forward as one lag-stacked GEMM + one LIF launch per step

@@ -25,10 +25,11 @@ c_size = ctypes.c_size_t
 DELREC_TAPS_SOFT, DELREC_TAPS_ROUND, DELREC_TAPS_INTERP = 0, 1, 2
 DELREC_BWD_SOFT, DELREC_BWD_STRAIGHT = 0, 1
 DELREC_ERR_WINDOW = 5
+DELREC_ERR_SCRATCH = 9
 WS_AXONAL_FWD, WS_AXONAL_BWD, WS_SYN_FWD, WS_SYN_BWD = 1, 2, 3, 4
 
 # Every symbol include/delrec.h declares (checked by the CPU test suite).
-EXPORTS = ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_syn_fwd',
+EXPORTS = ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_axonal_bwd_noalloc', 'delrec_syn_fwd',
            'delrec_syn_bwd',
            'delrec_lif_fwd', 'delrec_lif_bwd', 'delrec_delay_grad', 'delrec_query_workspace',
            'delrec_strerror', 'delrec_version', 'delrec_scan_timing', 'delrec_scan_timing_read',
@@ -109,7 +110,7 @@ def load():
         raise ImportError(f'{LIB_PATH} is not built: run `python -c "import __graft_entry__ as g; '
                           f'g.build()"` from the repository root')
     lib = ctypes.CDLL(str(LIB_PATH))
-    for name in ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_syn_fwd',
+    for name in ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_axonal_bwd_noalloc', 'delrec_syn_fwd',
                  'delrec_syn_bwd', 'delrec_lif_fwd', 'delrec_lif_bwd'):
         getattr(lib, name).restype = c_i32
         getattr(lib, name).argtypes = [c_vp, c_vp]
