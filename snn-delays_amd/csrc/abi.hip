@@ -326,6 +326,33 @@ bool syn_hybstep(int T, int B, int N, int L, bool hybrid, int off_count, int tap
     return !syn_layout(N, L, true).lds_ring;
 }
 
+// The hybrid forward as a scatter on arrival (hybstep.hip, hyb_fwd_arrive_kernel): bf16 W,
+// one uniform half-width of at most 4 taps per source, all at lags >= 1, at most 16 offsets,
+// 2048 neurons and two spike-history words; its ring of D + KF - 1 slots per receiver and
+// the arrival lists fit LDS. DELREC_HYB_FWD=0 turns it off.
+struct ArriveShape {
+    bool ok;
+    int npt, block, kf, R, RP, hw;
+    size_t lds;
+};
+ArriveShape syn_arrive(int N, int L, bool hybrid, bool bf16, int off_count, int taps, bool lags_ok) {
+    ArriveShape a{};
+    if (!getenv_flag_off("DELREC_HYB_FWD")) return a;
+    if (!hybrid || !bf16 || !lags_ok || off_count < 1 || off_count > 16 || taps < 1 || taps > 4) return a;
+    if (N > 2048) return a;
+    a.npt = N <= 1024 ? 1 : 2;
+    a.block = a.npt == 1 ? (N + 63) / 64 * 64 : 1024;
+    a.kf = taps <= 2 ? 2 : 4;
+    a.R = off_count + a.kf - 1;
+    a.RP = a.R + a.kf - 1;
+    a.hw = (std::max(L - 1, 1) + 63) / 64;
+    const int nwaves = a.block / 64;
+    a.lds = (size_t)a.npt * a.block * a.RP * sizeof(float) +
+            (size_t)2 * nwaves * a.npt * 64 * sizeof(uint16_t) + (size_t)2 * nwaves * sizeof(int);
+    a.ok = a.hw <= 2 && a.lds <= (size_t)max_lds_bytes();
+    return a;
+}
+
 template <class C>
 void hybstep_ws(C& c, int T, int B, int N, int L, int D, int KF, bool fwd, bool bf16) {
     const HybStepDims q = hybstep_dims(T, B, N, L, D, KF, num_cus());
@@ -342,6 +369,13 @@ void hybstep_ws(C& c, int T, int B, int N, int L, int D, int KF, bool fwd, bool 
 
 template <class C>
 void syn_fwd_ws(C& c, int T, int B, int N, int L, bool hybrid, bool bf16, int taps, int offc, bool lags_ok) {
+    const ArriveShape ar = syn_arrive(N, L, hybrid, bf16, offc, taps, lags_ok);
+    if (ar.ok) {
+        c.template take<uint32_t>((size_t)N * N);   // packed W^T | offsets^T
+        c.template take<int>((size_t)N);            // first lag per source
+        c.template take<float>((size_t)ar.kf * N);  // tap weights per source
+        return;
+    }
     if (syn_hybstep(T, B, N, L, hybrid, offc, taps, lags_ok)) {
         hybstep_ws(c, T, B, N, L, offc, taps, true, bf16);
         return;
@@ -885,6 +919,29 @@ int syn_fwd_hybstep(const delrec_syn_fwd_args* a, int KF, hipStream_t s) {
     return finish_launch();
 }
 
+// forward as one event-driven scatter-on-arrival launch, one batch row per workgroup
+int syn_fwd_arrive(const delrec_syn_fwd_args* a, const ArriveShape& ar, hipStream_t s) {
+    const int N = a->N;
+    Carver cv(a->workspace, a->workspace_bytes);
+    uint32_t* wpk = cv.take<uint32_t>((size_t)N * N);
+    int* lof = cv.take<int>((size_t)N);
+    float* h = cv.take<float>((size_t)ar.kf * N);
+    if (!wpk || !lof || !h) return DELREC_ERR_WORKSPACE;
+    launch_pack_hybrid(static_cast<const uint16_t*>(a->W), a->offsets, N, wpk, s);
+    HybTaps tp{};   // kf rows: a run shorter than kf gets taps of weight 0 past its triangle
+    tp.N = N; tp.KF = ar.kf; tp.omin = a->off_min; tp.s = a->s_uniform; tp.base = a->base; tp.lof = lof; tp.h = h;
+    launch_hyb_taps(tp, s);
+    HybScat p{};
+    p.T = a->T; p.B = a->B; p.N = N; p.D = a->off_count; p.KF = ar.kf; p.R = ar.R; p.RP = ar.RP;
+    p.omin = a->off_min; p.x = a->x; p.bias = a->bias; p.drop = a->drop; p.lif = make_lif(a->lif);
+    p.wpk = wpk; p.lof = lof; p.h = h; p.y = a->y; p.u = a->u; p.bits = a->bits;
+    const bool timed = scan_begin(DELREC_WS_SYN_FWD, s);
+    const bool launched = launch_hyb_fwd_arrive(p, ar.npt, ar.hw, ar.block, ar.lds, s);
+    scan_end(timed, s);
+    if (!launched) return DELREC_ERR_UNSUPPORTED;
+    return finish_launch();
+}
+
 int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     if (!a || a->T <= 0 || a->B <= 0 || a->N <= 0 || a->L < 1) return DELREC_ERR_ARG;
     if (!a->x || !a->W || !a->y || !a->u || !a->bits || !lif_ok(a->lif)) return DELREC_ERR_ARG;
@@ -894,8 +951,11 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     const SynLayout lay = syn_layout(a->N, a->L, true);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int N = a->N;
-    if (syn_hybstep(a->T, a->B, N, a->L, hybrid && !a->s, a->off_count, lag_taps(a->s_uniform),
-                    a->d_min >= a->s_uniform - 1.0f))
+    const bool lags_ok = a->d_min >= a->s_uniform - 1.0f;
+    const ArriveShape ar = syn_arrive(N, a->L, hybrid && !a->s, a->w_bf16 != 0, a->off_count,
+                                      lag_taps(a->s_uniform), lags_ok);
+    if (ar.ok) return syn_fwd_arrive(a, ar, s);
+    if (syn_hybstep(a->T, a->B, N, a->L, hybrid && !a->s, a->off_count, lag_taps(a->s_uniform), lags_ok))
         return syn_fwd_hybstep(a, lag_taps(a->s_uniform), s);
     if (syn_lagstep(a->T, a->B, N, a->L, lag_taps(a->s ? a->s_max : std::max(a->s_max, a->s_uniform))))
         return syn_fwd_lagstep(a, s);

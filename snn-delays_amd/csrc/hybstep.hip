@@ -169,6 +169,10 @@ __global__ void __launch_bounds__(256) hyb_lif_fwd_kernel(HybLif p) {
 //    the contribution's G index t + lof_j + f lies past T, which no step delivers);
 //  3 (row-major): the LIF backward on gy + gfut, outputs dx (and gr when it differs), the db
 //    partial, and gr(t) split into the hi / lo history planes at slice t.
+// Every phase issues all of its global loads before it uses any (a tile is 16 elements per
+// thread), so a wave waits for memory once per phase rather than once per element.
+constexpr int kHybTapsMax = 8;
+
 __global__ void __launch_bounds__(256) hyb_lif_bwd_kernel(HybLif p) {
     __shared__ float sg[64][65];
     __shared__ float sf[64][65];
@@ -179,38 +183,60 @@ __global__ void __launch_bounds__(256) hyb_lif_bwd_kernel(HybLif p) {
     // phase 1
     {
         const int j = j0 + lane;
-#pragma unroll 4
-        for (int e = 0; e < 16; ++e) {
-            const int b = b0 + w + 4 * e;
-            float g = 0.0f;
-            if (b < B && j < N) {
-#pragma unroll 8
-                for (int q = 0; q < p.KS; ++q) g += p.part[((size_t)q * B + b) * p.Np + j];
+        float g[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) g[e] = 0.0f;
+        for (int q = 0; q < p.KS; ++q) {
+            float v[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int b = b0 + w + 4 * e;
+                v[e] = (b < B && j < N) ? p.part[((size_t)q * B + b) * p.Np + j] : 0.0f;
             }
-            sg[lane][w + 4 * e] = g;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) g[e] += v[e];
         }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sg[lane][w + 4 * e] = g[e];
     }
     __syncthreads();
     // phase 2
     {
         const int b = b0 + lane;
+        const bool bok = b < B;
         const int slot_t = t % p.R;
+        const size_t ringsz = (size_t)p.R * N * B;
+        const int KF = p.KF;
+#pragma unroll 2
         for (int e = 0; e < 16; ++e) {
             const int jl = w + 4 * e, j = j0 + jl;
             float gf = 0.0f;
             if (j < N) {
                 const float g = sg[jl][lane];
                 const int lof = p.lof[j];
-                for (int f = 0; f < p.KF; ++f) {
-                    const float hf = p.h[(size_t)f * N + j];
-                    float* ring = p.dbuf + (size_t)f * p.R * N * B;
-                    const int s = t + 1 - lof - f;   // the step that consumes G_j(t + 1) through tap f
-                    if (s == t) {
-                        gf += hf * g;
-                    } else {
-                        if (s >= 0 && b < B) ring[((size_t)(s % p.R) * N + j) * B + b] = hf * g;
-                        if (t + lof + f <= p.T && b < B) gf += ring[((size_t)slot_t * N + j) * B + b];
+                float hf[kHybTapsMax], got[kHybTapsMax];
+                // the consuming reads first (contributions delivered by earlier steps)
+#pragma unroll
+                for (int f = 0; f < kHybTapsMax; ++f) {
+                    got[f] = 0.0f;
+                    if (f < KF) {
+                        hf[f] = p.h[(size_t)f * N + j];
+                        if (lof + f >= 2 && t + lof + f <= p.T && bok)
+                            got[f] = p.dbuf[(size_t)f * ringsz + ((size_t)slot_t * N + j) * B + b];
                     }
+                }
+                // deliveries of G_j(t + 1) to their consuming steps
+#pragma unroll
+                for (int f = 0; f < kHybTapsMax; ++f) {
+                    if (f >= KF) break;
+                    const int s = t + 1 - lof - f;
+                    if (s != t && s >= 0 && bok)
+                        p.dbuf[(size_t)f * ringsz + ((size_t)(s % p.R) * N + j) * B + b] = hf[f] * g;
+                }
+#pragma unroll
+                for (int f = 0; f < kHybTapsMax; ++f) {
+                    if (f >= KF) break;
+                    gf += (lof + f == 1) ? hf[f] * g : got[f];
                 }
             }
             sf[jl][lane] = gf;
@@ -222,6 +248,20 @@ __global__ void __launch_bounds__(256) hyb_lif_bwd_kernel(HybLif p) {
         const Lif k = p.lif;
         const int j = j0 + lane;
         const size_t BN = (size_t)B * N;
+        const bool last = t == p.T - 1;
+        float uu[16], gyv[16], lam[16], dbv[16], mv[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int b = b0 + w + 4 * e;
+            const bool ok = b < B && j < N;
+            const size_t bj = (size_t)(ok ? b : 0) * N + (ok ? j : 0), o = (size_t)t * BN + bj;
+            uu[e] = ok ? p.u_in[o] : 0.0f;
+            gyv[e] = ok ? p.gy[o] : 0.0f;
+            lam[e] = (ok && !last) ? p.state[bj] : 0.0f;
+            dbv[e] = (ok && !last) ? p.dbp[bj] : 0.0f;
+            mv[e] = (ok && p.drop) ? p.drop[bj] : 1.0f;
+        }
+#pragma unroll
         for (int e = 0; e < 16; ++e) {
             const int b = b0 + w + 4 * e;
             if (b >= B || j >= p.Nk) continue;
@@ -233,22 +273,237 @@ __global__ void __launch_bounds__(256) hyb_lif_bwd_kernel(HybLif p) {
             }
             const float gf = sf[lane][w + 4 * e];
             const size_t bj = (size_t)b * N + j, o = (size_t)t * BN + bj;
-            const float u = p.u_in[o];
-            const float y = lif_fire(k, u);
-            const bool last = t == p.T - 1;
-            const float lam = last ? 0.0f : p.state[bj];
-            const float du = lif_backward(k, p.gy[o] + gf, u, y, lam);
+            const float y = lif_fire(k, uu[e]);
+            const float du = lif_backward(k, gyv[e] + gf, uu[e], y, lam[e]);
             p.state[bj] = k.decay * du;
             const float da = lif_dx(k, du);
-            const float gr = da * (p.drop ? p.drop[bj] : 1.0f);
+            const float gr = da * mv[e];
             p.dx[o] = da;
             if (p.gr) p.gr[o] = gr;
-            p.dbp[bj] = last ? gr : p.dbp[bj] + gr;
+            p.dbp[bj] = last ? gr : dbv[e] + gr;
             const uint32_t hi = hyb_bf16_rne(gr);
             p.hhi[ho] = (uint16_t)hi;
             p.hlo[ho] = (uint16_t)hyb_bf16_rne(gr - __uint_as_float(hi << 16));
         }
     }
+}
+
+// ---------------------------------------------------------------------------------------
+// Forward of the hybrid as an event-driven scatter on arrival, one batch row per workgroup
+// (bf16 W, at most 2048 neurons: NPT = 1 or 2 per lane, each lane's neurons being both
+// receivers and sources).
+//
+// A spike of source j at step tau reaches receiver i through tap f at tau + lof_j + f + e_ij,
+// so it "arrives" at step t = tau + lof_j and its contributions then land e_ij + f steps
+// ahead: at step t the walked sources are those with y_j(t - lof_j) = 1 (bit lof_j - 1 of the
+// source's own spike-history word), and the pending recurrent input of each receiver only
+// needs a ring of R = D + KF - 1 slots (C5: 6; the per-connection scatter needs L, 67). Ring
+// row of receiver i: R slots plus KF - 1 mirror slots after slot R - 1, so a connection's KF
+// taps are one run of consecutive slots from s = (t + e) mod R (one two-slot LDS read and write
+// for KF = 2); the mirror slot R + m is read and cleared with slot m. (C5: 7 floats per
+// receiver, 57 KB for 2048 of them, so two rows' workgroups share a CU.) Per connection: the packed word bf16(W) << 16 | offset byte (one 4-byte load),
+// the slot, and KF fused multiply-adds w * h_j(lof_j + f) into the run.
+//
+// Per step: every wave walks the arrival list of step t (flattened from per-wave segments,
+// sources in a fixed order, chunks of 8 with the next chunk's words in flight) over its own
+// receivers -- a receiver's ring row is only ever written by its own lane, so the scatter
+// needs no barrier -- then runs the LIF of its receivers on their ring slot, shifts each
+// source's spike into its history word and appends the sources arriving at t + 1 to its
+// segment of the other list buffer; one LDS barrier per step.
+constexpr int kArriveChunk = 8;
+
+template <int NPT, int KF, int HW>
+__global__ void __launch_bounds__(1024) hyb_fwd_arrive_kernel(HybScat p) {
+    extern __shared__ float smem[];
+    const int N = p.N, T = p.T, B = p.B, R = p.R, RP = p.RP;
+    const int b = blockIdx.x, tid = threadIdx.x, BS = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nwaves = BS >> 6;
+    float* ring = smem;                                                     // [NPT * BS][RP]
+    uint16_t* seg = reinterpret_cast<uint16_t*>(ring + (size_t)NPT * BS * RP);   // [2][nwaves][NPT * 64]
+    int* cnt = reinterpret_cast<int*>(seg + 2 * nwaves * NPT * 64);         // [2][nwaves]
+    const int TW = (T + 31) >> 5;
+    const size_t BN = (size_t)B * N;
+    const Lif k = p.lif;
+
+    for (int q = tid; q < NPT * BS * RP; q += BS) ring[q] = 0.0f;
+    if (tid < nwaves) cnt[tid] = 0;    // nothing arrives at step 0
+
+    int idx[NPT], lof[NPT];
+    bool act[NPT];
+    float v[NPT], m[NPT], bias[NPT];
+    uint64_t hist[NPT][HW];
+    uint32_t word[NPT];
+#pragma unroll
+    for (int c = 0; c < NPT; ++c) {
+        idx[c] = tid + c * BS;
+        act[c] = idx[c] < N;
+        const int i = act[c] ? idx[c] : 0;
+        lof[c] = p.lof[i];
+        v[c] = k.v0;
+        m[c] = p.drop ? p.drop[(size_t)b * N + i] : 1.0f;
+        bias[c] = p.bias ? p.bias[i] : 0.0f;
+#pragma unroll
+        for (int w = 0; w < HW; ++w) hist[c][w] = 0ull;
+        word[c] = 0u;
+    }
+    // one descriptor for the packed connections; source o's words start o * N in, a lane
+    // past N reads beyond the matrix (0: weight 0, no contribution)
+    const i32x4 rw = buffer_rsrc(p.wpk, (uint32_t)((size_t)N * N * 4u));
+    int wio[NPT];
+#pragma unroll
+    for (int c = 0; c < NPT; ++c) wio[c] = act[c] ? idx[c] * 4 : 0x40000000;
+    __syncthreads();
+
+    int tm = 0;   // t mod R
+    for (int t = 0; t < T; ++t) {
+        // this step's input, issued first so that the scatter hides its latency
+        float xs[NPT];
+#pragma unroll
+        for (int c = 0; c < NPT; ++c) xs[c] = act[c] ? p.x[(size_t)t * BN + (size_t)b * N + idx[c]] : 0.0f;
+
+        // ---- scatter of the sources arriving at t
+        const int bsel = t & 1;
+        int total = 0;
+        int cw[16];
+#pragma unroll
+        for (int w2 = 0; w2 < 16; ++w2) {
+            cw[w2] = w2 < nwaves ? cnt[bsel * nwaves + w2] : 0;
+            total += cw[w2];
+        }
+        for (int base = 0; base < total; base += 64) {
+            int src = 0;
+            {
+                const int f = base + lane;
+                int acc = 0, sgi = 0, pos = 0;
+                bool found = false;
+#pragma unroll
+                for (int w2 = 0; w2 < 16; ++w2) {
+                    if (!found && f < acc + cw[w2]) {
+                        sgi = w2;
+                        pos = f - acc;
+                        found = true;
+                    }
+                    acc += cw[w2];
+                }
+                src = found ? (int)seg[(bsel * nwaves + sgi) * (NPT * 64) + pos] : 0;
+            }
+            const int nf = min(64, total - base);
+            uint32_t wn[kArriveChunk][NPT];
+#pragma unroll
+            for (int e = 0; e < kArriveChunk; ++e) {
+                const int o = __builtin_amdgcn_readlane(src, e);
+#pragma unroll
+                for (int c = 0; c < NPT; ++c)
+                    wn[e][c] = __float_as_uint(raw_buffer_load_f32(rw, wio[c] + o * N * 4, 0, 0));
+            }
+            for (int f0 = 0; f0 < nf; f0 += kArriveChunk) {
+                uint32_t wc[kArriveChunk][NPT];
+#pragma unroll
+                for (int e = 0; e < kArriveChunk; ++e)
+#pragma unroll
+                    for (int c = 0; c < NPT; ++c) wc[e][c] = wn[e][c];
+                if (f0 + kArriveChunk < nf) {
+#pragma unroll
+                    for (int e = 0; e < kArriveChunk; ++e) {
+                        const int o = __builtin_amdgcn_readlane(src, (f0 + kArriveChunk + e) & 63);
+#pragma unroll
+                        for (int c = 0; c < NPT; ++c)
+                            wn[e][c] = __float_as_uint(raw_buffer_load_f32(rw, wio[c] + o * N * 4, 0, 0));
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < kArriveChunk; ++e) {
+                    if (f0 + e >= nf) break;
+                    const int o = __builtin_amdgcn_readlane(src, (f0 + e) & 63);
+                    float hf[KF];
+#pragma unroll
+                    for (int f = 0; f < KF; ++f) hf[f] = p.h[(size_t)f * N + o];
+#pragma unroll
+                    for (int c = 0; c < NPT; ++c) {
+                        const uint32_t wv = wc[e][c];
+                        // offset index in [0, D) for the offsets the caller describes; a lane
+                        // past N, or an offset outside that range, adds nothing and stays in
+                        // its own ring row
+                        int ee = (int)(int8_t)(wv & 0xFFu) - p.omin;
+                        const bool in = act[c] && (unsigned)ee < (unsigned)p.D;
+                        const float wf = in ? __uint_as_float(wv & 0xFFFF0000u) : 0.0f;
+                        ee = in ? ee : 0;
+                        int sl = tm + ee;
+                        sl = sl >= R ? sl - R : sl;
+                        float* run = ring + (size_t)idx[c] * RP + sl;
+                        float old[KF];
+#pragma unroll
+                        for (int f = 0; f < KF; ++f) old[f] = run[f];
+#pragma unroll
+                        for (int f = 0; f < KF; ++f) run[f] = fmaf(wf, hf[f], old[f]);
+                    }
+                }
+            }
+        }
+
+        // ---- LIF of this lane's receivers, then each source's history and next arrival
+        bool next[NPT];
+#pragma unroll
+        for (int c = 0; c < NPT; ++c) {
+            float* row = ring + (size_t)idx[c] * RP;
+            float rec = row[tm];
+            row[tm] = 0.0f;
+            if (tm < KF - 1) {
+                rec += row[R + tm];
+                row[R + tm] = 0.0f;
+            }
+            const float r = rec + bias[c];
+            const float a = xs[c] + r * m[c];
+            const float u = lif_charge(k, v[c], a);
+            const float yv = lif_fire(k, u);
+            const bool fire = act[c] && yv != 0.0f;
+            v[c] = lif_reset(k, u, yv);
+            if (act[c]) {
+                const size_t o = (size_t)t * BN + (size_t)b * N + idx[c];
+                p.y[o] = fire ? 1.0f : 0.0f;
+                p.u[o] = u;
+            }
+            word[c] |= (fire ? 1u : 0u) << (t & 31);
+            if (((t & 31) == 31 || t == T - 1) && act[c]) {
+                p.bits[((size_t)b * TW + (t >> 5)) * N + idx[c]] = word[c];
+                word[c] = 0u;
+            }
+#pragma unroll
+            for (int w = HW - 1; w > 0; --w) hist[c][w] = (hist[c][w] << 1) | (hist[c][w - 1] >> 63);
+            hist[c][0] = (hist[c][0] << 1) | (fire ? 1ull : 0ull);
+            // y(t + 1 - lof) is bit lof - 1 of the updated history
+            const int kb = lof[c] - 1;
+            const uint64_t hw = HW == 1 ? hist[c][0] : (kb < 64 ? hist[c][0] : hist[c][HW - 1]);
+            next[c] = act[c] && ((hw >> (kb & 63)) & 1ull);
+        }
+        const int nsel = (t + 1) & 1;
+        uint16_t* myseg = seg + (nsel * nwaves + wave) * (NPT * 64);
+        int filled = 0;
+#pragma unroll
+        for (int c = 0; c < NPT; ++c) {
+            const uint64_t bal = __ballot(next[c]);
+            if (next[c]) myseg[filled + __popcll(bal & ((1ull << lane) - 1ull))] = (uint16_t)idx[c];
+            filled += __popcll(bal);
+        }
+        if (lane == 0) cnt[nsel * nwaves + wave] = filled;
+        tm = tm + 1 == R ? 0 : tm + 1;
+        barrier_lds();
+    }
+}
+
+// wpk[o * N + i] = bf16 bits of W[i, o] << 16 | uint8(offset[i, o]) (the packing the
+// per-connection scatter uses, launch_pack_hybrid)
+bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t lds, hipStream_t stream) {
+#define DELREC_ARRIVE(NPTV, KFV, HWV)                                                             \
+    if (npt == NPTV && a.KF <= KFV && hw == HWV) {                                                \
+        ensure_lds((const void*)hyb_fwd_arrive_kernel<NPTV, KFV, HWV>, lds);                     \
+        hipLaunchKernelGGL((hyb_fwd_arrive_kernel<NPTV, KFV, HWV>), dim3(a.B), dim3(block), lds, stream, a); \
+        return true;                                                                             \
+    }
+    DELREC_ARRIVE(1, 2, 1) DELREC_ARRIVE(1, 2, 2) DELREC_ARRIVE(2, 2, 1) DELREC_ARRIVE(2, 2, 2)
+    DELREC_ARRIVE(1, 4, 1) DELREC_ARRIVE(1, 4, 2) DELREC_ARRIVE(2, 4, 1) DELREC_ARRIVE(2, 4, 2)
+#undef DELREC_ARRIVE
+    return false;
 }
 
 // ---------------------------------------------------------------------------------------

@@ -236,6 +236,21 @@ struct HybLif {
     float* dbuf;                 // [KF][R][N][B] deliveries of h * G to their consuming step
 };
 
+struct HybScat {                 // the hybrid forward as a scatter on arrival (bf16 W)
+    int T, B, N, D, KF, R, RP, omin;   // KF: the compiled run length; R = D + KF - 1 ring slots
+    const float* x;
+    const float* bias;
+    const float* drop;
+    Lif lif;
+    const uint32_t* wpk;         // wpk[o * N + i] = bf16(W[i, o]) << 16 | uint8(offset[i, o])
+    const int* lof;              // [N] first lag of each source
+    const float* h;              // [KF][N] its tap weights (0 past its triangle)
+    float* y;
+    float* u;
+    uint32_t* bits;
+};
+bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t lds, hipStream_t stream);
+
 struct HybStepDims {
     int Nk, Np, D, KF, R, HW, Kt, KS;
     size_t lda, plane;

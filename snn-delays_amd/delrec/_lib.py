@@ -186,10 +186,14 @@ def lag_taps(s_max):
     return min(255, max(0, math.ceil(2.0 * s32)))
 
 
+_FORM_ENV = ('DELREC_SYN_LAGSTEP', 'DELREC_SYN_HYBSTEP', 'DELREC_HYB_FWD')
+
+
 def workspace_bytes(kind, T, B, N, L, flags):
     """``delrec_query_workspace`` (memoised: the size is a function of the arguments and of
-    DELREC_SYN_LAGSTEP, which picks the synaptic scans' form)."""
-    key = (kind, T, B, N, L, flags, os.environ.get('DELREC_SYN_LAGSTEP'))
+    DELREC_SYN_LAGSTEP / DELREC_SYN_HYBSTEP / DELREC_HYB_FWD, which pick the synaptic scans'
+    form)."""
+    key = (kind, T, B, N, L, flags) + tuple(os.environ.get(v) for v in _FORM_ENV)
     n = _WS_SIZES.get(key)
     if n is None:
         size = c_size(0)

@@ -181,7 +181,7 @@ def test_plain_lif_layer_matches_oracle(dev, form):
 def test_axonal_dense_tiled_forward_matches_oracle(dev, idx, monkeypatch):
     import test_gpu_axonal as ax
     monkeypatch.setenv('DELREC_AXONAL_FWD', 'tiled')
-    ax.test_axonal_fwd_bwd_matches_oracle(dev, ax.CASES[idx])
+    ax.test_axonal_fwd_bwd_matches_oracle(dev, ax.CASES[idx], monkeypatch)
 
 
 @pytest.mark.gpu

@@ -163,7 +163,8 @@ def hybrid_layer(N, W, base, offsets, dev, bf16=False, **cfg_kw):
 def test_hybrid_fwd_bwd_matches_oracle(dev, case):
     """Hybrid delays through the base + int8-offset kernel path of a parametrised layer."""
     import delrec.kernels.synaptic_hybrid as sh
-    T, B, N, (lo, hi), K, bf16, sigma = case
+    T, B, N, (lo, hi), K, bf16, sigma = case[:7]
+    k0 = case[7] if len(case) > 7 else 0     # smallest offset (offsets uniform in k0 .. K)
     print(f'case {case}', flush=True)
     g = gen(2)
     x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
@@ -171,7 +172,7 @@ def test_hybrid_fwd_bwd_matches_oracle(dev, case):
     if bf16:
         W = W.bfloat16().float()
     base = lo + torch.rand(N, generator=g) * (hi - lo)
-    offsets = torch.randint(K + 1, (N, N), generator=g).float()
+    offsets = (k0 + torch.randint(K - k0 + 1, (N, N), generator=g)).float()
     gy = torch.randn(T, B, N, generator=g)
     lif = lif_params()
     y_ref, u_ref, gref = oracle_synaptic(x, W, None, lif, sigma, gy, base=base, offsets=offsets)
@@ -224,7 +225,39 @@ HYBSTEP_CASES = [HYB_CASES[i] for i in (0, 2, 5, 6)] + [
                                                     for c in HYBSTEP_CASES])
 def test_hybrid_offset_stacked_matches_oracle(dev, case, monkeypatch):
     monkeypatch.setenv('DELREC_SYN_HYBSTEP', '1')
+    monkeypatch.setenv('DELREC_HYB_FWD', '0')    # the offset-stacked forward, not the arrival scatter
     test_hybrid_fwd_bwd_matches_oracle(dev, case)
+
+
+# the hybrid forward as a scatter on arrival (the default for bf16 W, bases >= s - 1, at most
+# 16 offsets, 4 taps and 2048 neurons): two and four compiled taps (sigma 0.5 runs three taps
+# on the four-tap kernel), one and two spike-history words, two neurons per lane (N > 1024,
+# the second half of the lanes partly idle), a smallest offset of 2 under negative bases
+ARRIVE_CASES = [
+    (20, 3, 64, (0.0, 8.0), 4, True, 0.0),
+    HYB_CASES[2],
+    (20, 2, 64, (1.0, 12.0), 4, True, 0.5),
+    (24, 2, 96, (1.0, 6.0), 4, True, 1.0),
+    HYB_CASES[5],
+    (12, 2, 1100, (0.0, 30.0), 4, True, 0.0),
+    (20, 2, 64, (-1.5, 6.0), 6, True, 0.0, 2),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', ARRIVE_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}s{c[6]}k{c[7] if len(c) > 7 else 0}'
+                                                   for c in ARRIVE_CASES])
+def test_hybrid_arrival_forward_matches_oracle(dev, case, monkeypatch):
+    monkeypatch.setenv('DELREC_HYB_FWD', '1')
+    test_hybrid_fwd_bwd_matches_oracle(dev, case)
+
+
+# the per-connection forwards on the bf16 cases the arrival scatter takes by default
+@pytest.mark.gpu
+@pytest.mark.parametrize('idx', [2, 5, 6])
+def test_hybrid_per_connection_forward_matches_oracle(dev, idx, monkeypatch):
+    monkeypatch.setenv('DELREC_HYB_FWD', '0')
+    test_hybrid_fwd_bwd_matches_oracle(dev, HYB_CASES[idx])
 
 
 # the hybrid backward with one lane per source (the split form is the default for N <= 512)
