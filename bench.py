@@ -231,9 +231,9 @@ def peak_of(w):
 SCAN_SYMBOL = {
     'C1': {'axonal_fwd_scan': 'axonal_fwd_wave_fast', 'axonal_bwd_scan': 'axonal_bwd_tiled_fast'},
     'C2': {'axonal_fwd_scan': 'axonal_fwd_wave_fast', 'axonal_bwd_scan': 'axonal_bwd_tiled_fast'},
-    'C3': {'syn_fwd_scan': 'syn_fwd_scatter', 'syn_bwd_scan': 'syn_bwd_hyb'},
+    'C3': {'syn_fwd_scan': 'hyb_fwd_arrive_kernel', 'syn_bwd_scan': 'syn_bwd_hyb'},
     'C4': {'syn_fwd_scan': 'lagstep_fwd_sequence', 'syn_bwd_scan': 'lagstep_bwd_sequence'},
-    'C5': {'syn_fwd_scan': 'hybstep_fwd_sequence', 'syn_bwd_scan': 'hybstep_bwd_sequence'},
+    'C5': {'syn_fwd_scan': 'hyb_fwd_arrive_kernel', 'syn_bwd_scan': 'hybstep_bwd_sequence'},
 }
 
 
@@ -408,6 +408,7 @@ def measure(name, steps, warmup, with_cpu):
         'per_layer_value': nt_layer / (ms * 1e-3 / nl),
     }
     if with_cpu:
+        print(f'[bench] {name}: {ms:.2f} ms/step on the GPU; CPU baseline next', file=sys.stderr, flush=True)
         line['cpu_baseline'] = cpu_baseline(m.layers[0], xs[0], w)
     return line
 

@@ -346,9 +346,9 @@ ArriveShape syn_arrive(int N, int L, bool hybrid, bool bf16, int off_count, int 
     a.R = off_count + a.kf - 1;
     a.RP = a.R + a.kf - 1;
     a.hw = (std::max(L - 1, 1) + 63) / 64;
-    const int nwaves = a.block / 64;
-    a.lds = (size_t)a.npt * a.block * a.RP * sizeof(float) +
-            (size_t)2 * nwaves * a.npt * 64 * sizeof(uint16_t) + (size_t)2 * nwaves * sizeof(int);
+    // ring [RP][npt * 1024], segment counts [2][16], arrival segments [2][16][npt * 64]
+    a.lds = (size_t)a.RP * a.npt * 1024 * sizeof(float) + (size_t)2 * 16 * sizeof(int) +
+            (size_t)2 * 16 * a.npt * 64 * sizeof(uint16_t);
     a.ok = a.hw <= 2 && a.lds <= (size_t)max_lds_bytes();
     return a;
 }
@@ -927,7 +927,7 @@ int syn_fwd_arrive(const delrec_syn_fwd_args* a, const ArriveShape& ar, hipStrea
     int* lof = cv.take<int>((size_t)N);
     float* h = cv.take<float>((size_t)ar.kf * N);
     if (!wpk || !lof || !h) return DELREC_ERR_WORKSPACE;
-    launch_pack_hybrid(static_cast<const uint16_t*>(a->W), a->offsets, N, wpk, s);
+    launch_pack_hybrid(static_cast<const uint16_t*>(a->W), a->offsets, N, wpk, s, a->off_min);
     HybTaps tp{};   // kf rows: a run shorter than kf gets taps of weight 0 past its triangle
     tp.N = N; tp.KF = ar.kf; tp.omin = a->off_min; tp.s = a->s_uniform; tp.base = a->base; tp.lof = lof; tp.h = h;
     launch_hyb_taps(tp, s);

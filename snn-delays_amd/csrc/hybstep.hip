@@ -290,43 +290,50 @@ __global__ void __launch_bounds__(256) hyb_lif_bwd_kernel(HybLif p) {
 
 // ---------------------------------------------------------------------------------------
 // Forward of the hybrid as an event-driven scatter on arrival, one batch row per workgroup
-// (bf16 W, at most 2048 neurons: NPT = 1 or 2 per lane, each lane's neurons being both
-// receivers and sources).
+// (bf16 W, at most 2048 neurons: NPT = 1 or 2 per lane of a block of at most 1024 lanes,
+// each lane's neurons being both receivers and sources).
 //
 // A spike of source j at step tau reaches receiver i through tap f at tau + lof_j + f + e_ij,
 // so it "arrives" at step t = tau + lof_j and its contributions then land e_ij + f steps
 // ahead: at step t the walked sources are those with y_j(t - lof_j) = 1 (bit lof_j - 1 of the
 // source's own spike-history word), and the pending recurrent input of each receiver only
-// needs a ring of R = D + KF - 1 slots (C5: 6; the per-connection scatter needs L, 67). Ring
-// row of receiver i: R slots plus KF - 1 mirror slots after slot R - 1, so a connection's KF
-// taps are one run of consecutive slots from s = (t + e) mod R (one two-slot LDS read and write
-// for KF = 2); the mirror slot R + m is read and cleared with slot m. (C5: 7 floats per
-// receiver, 57 KB for 2048 of them, so two rows' workgroups share a CU.) Per connection: the packed word bf16(W) << 16 | offset byte (one 4-byte load),
-// the slot, and KF fused multiply-adds w * h_j(lof_j + f) into the run.
+// needs a ring of R = D + KF - 1 slots (C5: 6; the per-connection scatter needs L, 67): R
+// slots plus KF - 1 mirror slots after slot R - 1, so a connection's KF taps are the slots
+// s .. s + KF - 1 from s = (t + e) mod R with no wrap; the mirror slot R + m is read and
+// cleared with slot m. The ring is slot-major, ring[slot][receiver] with a pitch of
+// NR = NPT * 1024 receivers, so the lanes of a wave always hit 64 distinct banks whatever slot
+// each connection selects, and the taps of a run are immediate offsets of one address. (C5:
+// 7 slots of 2048 receivers, 57 KB, so two rows' workgroups share a CU.) Per connection: the
+// packed word bf16(W) << 16 | (offset - smallest offset) byte (one 4-byte load), the slot,
+// and KF read-modify-writes w * h_j(lof_j + f) of the run.
 //
 // Per step: every wave walks the arrival list of step t (flattened from per-wave segments,
-// sources in a fixed order, chunks of 8 with the next chunk's words in flight) over its own
-// receivers -- a receiver's ring row is only ever written by its own lane, so the scatter
-// needs no barrier -- then runs the LIF of its receivers on their ring slot, shifts each
+// sources in a fixed order) over its own receivers, 64 arrivals at a time: lane a of the
+// wave holds arrival a's source and tap weights, which reach the whole wave by readlane, so
+// the only memory reads of the walk are the packed words, fetched a chunk of CH arrivals
+// ahead (CH = 32 with one neuron per lane; 4 with two, whose 1024-lane blocks must keep to 64
+// VGPRs for two workgroups per CU). A receiver's ring column is only ever written by its own lane, so the scatter needs
+// no barrier; then each lane runs the LIF of its receivers on their ring slot, shifts each
 // source's spike into its history word and appends the sources arriving at t + 1 to its
-// segment of the other list buffer; one LDS barrier per step.
-constexpr int kArriveChunk = 8;
+// wave's segment of the other list buffer; one LDS barrier per step.
+constexpr int kArriveWaves = 16;   // list segments per buffer (a 1024-lane block)
 
-template <int NPT, int KF, int HW>
-__global__ void __launch_bounds__(1024) hyb_fwd_arrive_kernel(HybScat p) {
+template <int NPT, int KF, int HW, int CH>
+__global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
     extern __shared__ float smem[];
+    constexpr int NR = NPT * 1024;
     const int N = p.N, T = p.T, B = p.B, R = p.R, RP = p.RP;
     const int b = blockIdx.x, tid = threadIdx.x, BS = blockDim.x;
-    const int lane = tid & 63, wave = tid >> 6, nwaves = BS >> 6;
-    float* ring = smem;                                                     // [NPT * BS][RP]
-    uint16_t* seg = reinterpret_cast<uint16_t*>(ring + (size_t)NPT * BS * RP);   // [2][nwaves][NPT * 64]
-    int* cnt = reinterpret_cast<int*>(seg + 2 * nwaves * NPT * 64);         // [2][nwaves]
+    const int lane = tid & 63, wave = tid >> 6;
+    float* ring = smem;                                                             // [RP][NR]
+    int* cnt = reinterpret_cast<int*>(ring + (size_t)RP * NR);                      // [2][16]
+    uint16_t* seg = reinterpret_cast<uint16_t*>(cnt + 2 * kArriveWaves);            // [2][16][NPT * 64]
     const int TW = (T + 31) >> 5;
     const size_t BN = (size_t)B * N;
     const Lif k = p.lif;
 
-    for (int q = tid; q < NPT * BS * RP; q += BS) ring[q] = 0.0f;
-    if (tid < nwaves) cnt[tid] = 0;    // nothing arrives at step 0
+    for (int q = tid; q < RP * NR; q += BS) ring[q] = 0.0f;
+    if (tid < 2 * kArriveWaves) cnt[tid] = 0;    // nothing arrives at step 0; absent waves stay 0
 
     int idx[NPT], lof[NPT];
     bool act[NPT];
@@ -363,21 +370,28 @@ __global__ void __launch_bounds__(1024) hyb_fwd_arrive_kernel(HybScat p) {
 
         // ---- scatter of the sources arriving at t
         const int bsel = t & 1;
-        int total = 0;
-        int cw[16];
+        int cw[kArriveWaves];
+        {
+            const int4* c4 = reinterpret_cast<const int4*>(cnt + bsel * kArriveWaves);
 #pragma unroll
-        for (int w2 = 0; w2 < 16; ++w2) {
-            cw[w2] = w2 < nwaves ? cnt[bsel * nwaves + w2] : 0;
-            total += cw[w2];
+            for (int q = 0; q < kArriveWaves / 4; ++q) {
+                const int4 v4 = c4[q];
+                cw[4 * q] = v4.x; cw[4 * q + 1] = v4.y; cw[4 * q + 2] = v4.z; cw[4 * q + 3] = v4.w;
+            }
         }
+        int total = 0;
+#pragma unroll
+        for (int w2 = 0; w2 < kArriveWaves; ++w2) total += cw[w2];
         for (int base = 0; base < total; base += 64) {
+            // lane a: arrival base + a -- its source and tap weights
             int src = 0;
+            float hs[KF];
             {
                 const int f = base + lane;
                 int acc = 0, sgi = 0, pos = 0;
                 bool found = false;
 #pragma unroll
-                for (int w2 = 0; w2 < 16; ++w2) {
+                for (int w2 = 0; w2 < kArriveWaves; ++w2) {
                     if (!found && f < acc + cw[w2]) {
                         sgi = w2;
                         pos = f - acc;
@@ -385,58 +399,63 @@ __global__ void __launch_bounds__(1024) hyb_fwd_arrive_kernel(HybScat p) {
                     }
                     acc += cw[w2];
                 }
-                src = found ? (int)seg[(bsel * nwaves + sgi) * (NPT * 64) + pos] : 0;
+                src = found ? (int)seg[(bsel * kArriveWaves + sgi) * (NPT * 64) + pos] : 0;
+#pragma unroll
+                for (int q = 0; q < KF; ++q) hs[q] = found ? p.h[(size_t)q * N + src] : 0.0f;
             }
             const int nf = min(64, total - base);
-            uint32_t wn[kArriveChunk][NPT];
+            uint32_t wn[CH][NPT];
 #pragma unroll
-            for (int e = 0; e < kArriveChunk; ++e) {
+            for (int e = 0; e < CH; ++e) {
                 const int o = __builtin_amdgcn_readlane(src, e);
 #pragma unroll
                 for (int c = 0; c < NPT; ++c)
                     wn[e][c] = __float_as_uint(raw_buffer_load_f32(rw, wio[c] + o * N * 4, 0, 0));
             }
-            for (int f0 = 0; f0 < nf; f0 += kArriveChunk) {
-                uint32_t wc[kArriveChunk][NPT];
+            for (int f0 = 0; f0 < nf; f0 += CH) {
+                uint32_t wc[CH][NPT];
 #pragma unroll
-                for (int e = 0; e < kArriveChunk; ++e)
+                for (int e = 0; e < CH; ++e)
 #pragma unroll
                     for (int c = 0; c < NPT; ++c) wc[e][c] = wn[e][c];
-                if (f0 + kArriveChunk < nf) {
+                if (f0 + CH < nf) {
 #pragma unroll
-                    for (int e = 0; e < kArriveChunk; ++e) {
-                        const int o = __builtin_amdgcn_readlane(src, (f0 + kArriveChunk + e) & 63);
+                    for (int e = 0; e < CH; ++e) {
+                        const int o = __builtin_amdgcn_readlane(src, (f0 + CH + e) & 63);
 #pragma unroll
                         for (int c = 0; c < NPT; ++c)
                             wn[e][c] = __float_as_uint(raw_buffer_load_f32(rw, wio[c] + o * N * 4, 0, 0));
                     }
                 }
 #pragma unroll
-                for (int e = 0; e < kArriveChunk; ++e) {
+                for (int e = 0; e < CH; ++e) {
                     if (f0 + e >= nf) break;
-                    const int o = __builtin_amdgcn_readlane(src, (f0 + e) & 63);
                     float hf[KF];
 #pragma unroll
-                    for (int f = 0; f < KF; ++f) hf[f] = p.h[(size_t)f * N + o];
+                    for (int q = 0; q < KF; ++q)
+                        hf[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hs[q]), (f0 + e) & 63));
+                    // the NPT receivers of a lane lie in distinct ring columns: all their taps
+                    // are read before any is written, one LDS round trip per arrival
+                    float* run[NPT];
+                    float wf[NPT], old[NPT][KF];
 #pragma unroll
                     for (int c = 0; c < NPT; ++c) {
                         const uint32_t wv = wc[e][c];
-                        // offset index in [0, D) for the offsets the caller describes; a lane
-                        // past N, or an offset outside that range, adds nothing and stays in
-                        // its own ring row
-                        int ee = (int)(int8_t)(wv & 0xFFu) - p.omin;
-                        const bool in = act[c] && (unsigned)ee < (unsigned)p.D;
-                        const float wf = in ? __uint_as_float(wv & 0xFFFF0000u) : 0.0f;
-                        ee = in ? ee : 0;
+                        // the offset byte holds offset - smallest offset, in [0, D) for the
+                        // offsets the caller describes (clamped, so that no slot leaves the
+                        // ring); a lane past N reads the word 0: weight 0 into its own column
+                        const int ee = min((int)(wv & 0xFFu), p.D - 1);
+                        wf[c] = __uint_as_float(wv & 0xFFFF0000u);
                         int sl = tm + ee;
                         sl = sl >= R ? sl - R : sl;
-                        float* run = ring + (size_t)idx[c] * RP + sl;
-                        float old[KF];
+                        run[c] = ring + sl * NR + idx[c];
 #pragma unroll
-                        for (int f = 0; f < KF; ++f) old[f] = run[f];
-#pragma unroll
-                        for (int f = 0; f < KF; ++f) run[f] = fmaf(wf, hf[f], old[f]);
+                        for (int q = 0; q < KF; ++q) old[c][q] = run[c][q * NR];
                     }
+#pragma unroll
+                    for (int c = 0; c < NPT; ++c)
+#pragma unroll
+                        for (int q = 0; q < KF; ++q) run[c][q * NR] = fmaf(wf[c], hf[q], old[c][q]);
                 }
             }
         }
@@ -445,12 +464,12 @@ __global__ void __launch_bounds__(1024) hyb_fwd_arrive_kernel(HybScat p) {
         bool next[NPT];
 #pragma unroll
         for (int c = 0; c < NPT; ++c) {
-            float* row = ring + (size_t)idx[c] * RP;
-            float rec = row[tm];
-            row[tm] = 0.0f;
+            float* col = ring + idx[c];
+            float rec = col[tm * NR];
+            col[tm * NR] = 0.0f;
             if (tm < KF - 1) {
-                rec += row[R + tm];
-                row[R + tm] = 0.0f;
+                rec += col[(R + tm) * NR];
+                col[(R + tm) * NR] = 0.0f;
             }
             const float r = rec + bias[c];
             const float a = xs[c] + r * m[c];
@@ -477,7 +496,7 @@ __global__ void __launch_bounds__(1024) hyb_fwd_arrive_kernel(HybScat p) {
             next[c] = act[c] && ((hw >> (kb & 63)) & 1ull);
         }
         const int nsel = (t + 1) & 1;
-        uint16_t* myseg = seg + (nsel * nwaves + wave) * (NPT * 64);
+        uint16_t* myseg = seg + (nsel * kArriveWaves + wave) * (NPT * 64);
         int filled = 0;
 #pragma unroll
         for (int c = 0; c < NPT; ++c) {
@@ -485,19 +504,20 @@ __global__ void __launch_bounds__(1024) hyb_fwd_arrive_kernel(HybScat p) {
             if (next[c]) myseg[filled + __popcll(bal & ((1ull << lane) - 1ull))] = (uint16_t)idx[c];
             filled += __popcll(bal);
         }
-        if (lane == 0) cnt[nsel * nwaves + wave] = filled;
+        if (lane == 0) cnt[nsel * kArriveWaves + wave] = filled;
         tm = tm + 1 == R ? 0 : tm + 1;
         barrier_lds();
     }
 }
 
-// wpk[o * N + i] = bf16 bits of W[i, o] << 16 | uint8(offset[i, o]) (the packing the
-// per-connection scatter uses, launch_pack_hybrid)
+// wpk[o * N + i] = bf16 bits of W[i, o] << 16 | uint8(offset[i, o] - smallest offset)
+// (launch_pack_hybrid with the smallest offset)
 bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t lds, hipStream_t stream) {
 #define DELREC_ARRIVE(NPTV, KFV, HWV)                                                             \
     if (npt == NPTV && a.KF <= KFV && hw == HWV) {                                                \
-        ensure_lds((const void*)hyb_fwd_arrive_kernel<NPTV, KFV, HWV>, lds);                     \
-        hipLaunchKernelGGL((hyb_fwd_arrive_kernel<NPTV, KFV, HWV>), dim3(a.B), dim3(block), lds, stream, a); \
+        constexpr int CHV = NPTV == 1 ? 32 : 4;                                                   \
+        ensure_lds((const void*)hyb_fwd_arrive_kernel<NPTV, KFV, HWV, CHV>, lds);                \
+        hipLaunchKernelGGL((hyb_fwd_arrive_kernel<NPTV, KFV, HWV, CHV>), dim3(a.B), dim3(block), lds, stream, a); \
         return true;                                                                             \
     }
     DELREC_ARRIVE(1, 2, 1) DELREC_ARRIVE(1, 2, 2) DELREC_ARRIVE(2, 2, 1) DELREC_ARRIVE(2, 2, 2)

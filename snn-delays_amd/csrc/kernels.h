@@ -242,7 +242,7 @@ struct HybScat {                 // the hybrid forward as a scatter on arrival (
     const float* bias;
     const float* drop;
     Lif lif;
-    const uint32_t* wpk;         // wpk[o * N + i] = bf16(W[i, o]) << 16 | uint8(offset[i, o])
+    const uint32_t* wpk;         // wpk[o * N + i] = bf16(W[i, o]) << 16 | uint8(offset[i, o] - omin)
     const int* lof;              // [N] first lag of each source
     const float* h;              // [KF][N] its tap weights (0 past its triangle)
     float* y;
@@ -324,7 +324,8 @@ void launch_axonal_bwd_sums(const AxTail& q, const float* part, int B, int N, hi
 
 void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream);
 // wpk[o*N + i] = W[i*N + o] (bf16 bits) << 16 | uint8(off[i*N + o])
-void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream);
+void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream,
+                        int omin = 0);
 // event-driven forward, ring in LDS, one receiver per lane, kf >= ceil(2 s_max) taps
 bool launch_syn_fwd_scatter(const SynFwd& a, int kf, int block, size_t lds, hipStream_t stream);
 bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);

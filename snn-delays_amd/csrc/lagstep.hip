@@ -492,11 +492,18 @@ __global__ void fill_rows_u16_kernel(uint16_t* __restrict__ h, int B, size_t lda
 
 // ---------------------------------------------------------------------------------------
 
+// k splits of a per-step GEMM: enough workgroups for every CU, rounded up to a multiple of
+// 8 where the k range allows, so that each XCD takes whole splits (its L2 then holds only its
+// k slice of both operands, fetched once) -- e.g. 512 x 2048 outputs with k = 10240: 8
+// splits of 64 tiles rather than 4, which leave each XCD a column half of the operand
 int lagstep_splits(int B, int Np, int Kt, int cus) {
     const int tiles = ((B + 127) / 128) * (Np / 128);
     const int nst = Kt / 32;
-    const int want = (cus + tiles - 1) / tiles;
-    return std::max(1, std::min(want, std::max(1, nst / 8)));
+    const int cap = std::max(1, nst / 8);
+    int ks = std::max(1, std::min((cus + tiles - 1) / tiles, cap));
+    const int up = (ks + 7) / 8 * 8;
+    if (ks > 1 && up <= cap) ks = up;
+    return ks;
 }
 
 void launch_pack_lagw(const LagStepPack& a, bool fwd, hipStream_t stream) {

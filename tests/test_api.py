@@ -242,3 +242,18 @@ def test_cpp_function_only_when_gradients_are_wanted():
         p.requires_grad_(True)
     assert not layer._cpp_function_applies(x, d, None, True, 0)      # approx
     assert not layer._cpp_function_applies(x, d, None, False, 1)     # STE
+
+
+def test_reference_import_path_resolves_to_the_hip_modules():
+    """``delrec.triton_kernels`` (the reference's package, src/delrec/triton_kernels/
+    __init__.py:64-73) names the HIP implementation's modules and objects."""
+    import delrec.kernels as k
+    from delrec.triton_kernels import AxonalRecdelTriton, build_syn_mask
+    from delrec.triton_kernels.synaptic_hybrid import HybridSynDelay, hybrid_trainable_forward
+    from delrec.triton_kernels.synaptic_eventdriven import EventDrivenSyn
+    import delrec.triton_kernels.delays as tk_delays
+    assert AxonalRecdelTriton is k.AxonalRecdelTriton and build_syn_mask is k.build_syn_mask
+    assert HybridSynDelay is k.synaptic_hybrid.HybridSynDelay
+    assert hybrid_trainable_forward is k.synaptic_hybrid.hybrid_trainable_forward
+    assert EventDrivenSyn is k.synaptic_eventdriven.EventDrivenSyn
+    assert tk_delays is k.delays
