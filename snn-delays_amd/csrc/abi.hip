@@ -356,15 +356,30 @@ ArriveShape syn_arrive(int N, int L, bool hybrid, bool bf16, int off_count, int 
 template <class C>
 void hybstep_ws(C& c, int T, int B, int N, int L, int D, int KF, bool fwd, bool bf16) {
     const HybStepDims q = hybstep_dims(T, B, N, L, D, KF, num_cus());
-    c.template take<uint4>((bf16 ? 1 : 2) * q.plane);           // W^(e) planes
-    c.template take<uint16_t>((size_t)B * q.lda);               // history hi (z or gr)
-    c.template take<uint16_t>((size_t)B * q.lda);               // history lo
-    c.template take<float>((size_t)q.KS * B * q.Np);            // split-K partials
-    c.template take<float>((size_t)B * N);                      // v / lambda
-    c.template take<int>((size_t)N);                            // first lag per source
-    c.template take<float>((size_t)KF * N);                     // tap weights per source
-    if (fwd) c.template take<uint64_t>((size_t)q.HW * B * N);   // spike-history words
-    else c.template take<float>((size_t)KF * q.R * N * B);      // deliveries of h * G
+    const int planes = bf16 ? 1 : 2;
+    if (fwd) {
+        c.template take<uint4>(planes * q.plane);                // W^(e) planes
+        c.template take<uint16_t>((size_t)B * q.lda);            // z history hi
+        c.template take<uint16_t>((size_t)B * q.lda);            // z history lo
+        c.template take<float>((size_t)q.KS * B * q.Np);         // split-K partials
+        c.template take<float>((size_t)B * N);                   // v
+        c.template take<int>((size_t)N);                         // first lag per source
+        c.template take<float>((size_t)KF * N);                  // tap weights per source
+        c.template take<uint64_t>((size_t)q.HW * B * N);         // spike-history words
+        return;
+    }
+    const HybBwdSizes z = hyb_bwd_sizes(q, B, num_cus());
+    c.template take<uint4>(planes * z.planes);                   // near + far W^(e) planes
+    c.template take<uint16_t>((size_t)B * q.lda);                // gr history hi
+    c.template take<uint16_t>((size_t)B * q.lda);                // gr history lo
+    c.template take<float>(std::max<size_t>(z.npart, 1));        // near partials
+    c.template take<float>(std::max<size_t>(z.fpart, 1));        // far partials
+    c.template take<float>((size_t)B * N);                       // lambda
+    c.template take<int>((size_t)N);                             // first lag per source
+    c.template take<float>((size_t)KF * N);                      // tap weights per source
+    c.template take<int>((size_t)N);                             // source order
+    c.template take<int>((size_t)q.Nk / hyb_bwd_tile() + 1);     // near columns per tile
+    c.template take<float>((size_t)q.R * N * B);                 // ring of G
 }
 
 template <class C>
@@ -913,7 +928,7 @@ int syn_fwd_hybstep(const delrec_syn_fwd_args* a, int KF, hipStream_t s) {
         g.aoff = (size_t)t * q.Nk;
         launch_lagstep_gemm(g, 2, s, planes);
         l.t = t;
-        launch_hyb_lif(l, true, q.HW, s);
+        launch_hyb_lif(l, q.HW, s);
     }
     scan_end(timed, s);
     return finish_launch();
@@ -1095,50 +1110,106 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     if (hybrid && !lagstep && !hybstep) launch_pack_offq(static_cast<const int8_t*>(dt), (size_t)N * lay.NT, meta, offq, s);
 
     if (hybstep) {
-        // reverse-time scan as one offset-stacked GEMM + one LIF launch per step
+        // reverse-time scan, the sources split by first lag: near ones (lof < P) through one
+        // offset-stacked GEMM per step over their columns, far ones through one GEMM per block
+        // of P steps with rows (b, step of the block); one LIF launch per step
         const int KF = taps;
         const HybStepDims hq = hybstep_dims(T, B, N, a->L, a->off_count, KF, num_cus());
+        const HybBwdSizes hz = hyb_bwd_sizes(hq, B, num_cus());
         const int planes = a->w_bf16 ? 1 : 2;
-        uint4* P = cv.take<uint4>(planes * hq.plane);
+        const int P = hq.P;
+        const int JT = hyb_bwd_tile();
+        const int ntiles = hq.Nk / JT;   // LIF tiles over the padded width (Nk: a multiple of 32)
+        uint4* Pw = cv.take<uint4>(planes * hz.planes);
         uint16_t* ghi = cv.take<uint16_t>((size_t)B * hq.lda);
         uint16_t* glo = cv.take<uint16_t>((size_t)B * hq.lda);
-        float* hpart = cv.take<float>((size_t)hq.KS * B * hq.Np);
+        float* npart = cv.take<float>(std::max<size_t>(hz.npart, 1));
+        float* fpart = cv.take<float>(std::max<size_t>(hz.fpart, 1));
         float* state = cv.take<float>((size_t)B * N);
         int* lof = cv.take<int>((size_t)N);
         float* h = cv.take<float>((size_t)KF * N);
-        float* dbuf = cv.take<float>((size_t)KF * hq.R * N * B);
-        if (!P || !ghi || !glo || !hpart || !state || !lof || !h || !dbuf) return DELREC_ERR_WORKSPACE;
-        HybPack pk{};
-        pk.N = N; pk.Nk = hq.Nk; pk.Np = hq.Np; pk.D = hq.D; pk.omin = a->off_min; pk.planes = planes;
-        pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.off = a->offsets; pk.out = P;
-        launch_hyb_pack(pk, false, s);
+        int* perm = cv.take<int>((size_t)N);
+        int* ntile = cv.take<int>((size_t)ntiles + 1);
+        float* ring = cv.take<float>((size_t)hq.R * N * B);
+        if (!Pw || !ghi || !glo || !npart || !fpart || !state || !lof || !h || !perm || !ntile || !ring)
+            return DELREC_ERR_WORKSPACE;
         HybTaps tp{};
         tp.N = N; tp.KF = KF; tp.omin = a->off_min; tp.s = a->s_uniform; tp.base = a->base; tp.lof = lof; tp.h = h;
         launch_hyb_taps(tp, s);
+        // the split needs the first lags on the host: one read-back per call
+        std::vector<int> lof_h(N), perm_h(N), ntile_h(ntiles + 1);
+        if (hipMemcpyAsync(lof_h.data(), lof, (size_t)N * sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return DELREC_ERR_LAUNCH;
+        int Nn = 0;
+        for (int x = 0; x < ntiles; ++x) {
+            ntile_h[x] = Nn;
+            for (int j = x * JT; j < std::min(N, (x + 1) * JT); ++j)
+                if (lof_h[j] < P) perm_h[Nn++] = j;
+        }
+        ntile_h[ntiles] = Nn;
+        const int Nf = N - Nn;
+        for (int j = 0, c = Nn; j < N; ++j)
+            if (lof_h[j] >= P) perm_h[c++] = j;
+        if (hipMemcpyAsync(perm, perm_h.data(), (size_t)N * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipMemcpyAsync(ntile, ntile_h.data(), (size_t)(ntiles + 1) * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return DELREC_ERR_LAUNCH;
+        const int Nnp = (Nn + 127) / 128 * 128, Nfp = (Nf + 127) / 128 * 128;
+        const size_t nplane = (size_t)(hq.Kt / 8) * Nnp, fplane = (size_t)(hq.Kt / 8) * Nfp;
+        uint4* Pn = Pw;                              // near planes: hi (, lo)
+        uint4* Pf = Pw + (size_t)planes * nplane;    // far planes: hi (, lo)
+        HybPack pk{};
+        pk.N = N; pk.Nk = hq.Nk; pk.D = hq.D; pk.omin = a->off_min; pk.planes = planes;
+        pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.off = a->offsets; pk.perm = perm;
+        if (Nn > 0) {
+            pk.Np = Nnp; pk.c0 = 0; pk.nc = Nn; pk.out = Pn;
+            launch_hyb_pack(pk, false, s);
+        }
+        if (Nf > 0) {
+            pk.Np = Nfp; pk.c0 = Nn; pk.nc = Nf; pk.out = Pf;
+            launch_hyb_pack(pk, false, s);
+        }
         launch_hist_clear(ghi, B, hq.lda, s);   // gr past the last step
         launch_hist_clear(glo, B, hq.lda, s);
         // gr == dx unless a dropout mask scales it
         const bool need_gr = a->drop != nullptr;
-        LagStepGemm gg{};   // step t: G(t + 1) from history slices t + 1 .. t + D = gr(t + 1 .. t + D)
-        gg.a0 = ghi; gg.a1 = glo; gg.lda = hq.lda; gg.rs = 0; gg.B = B; gg.rows = B; gg.rp = 1;
-        gg.p0 = P; gg.p1 = planes > 1 ? P + hq.plane : nullptr; gg.Np = hq.Np; gg.Kt = hq.Kt; gg.KS = hq.KS;
-        gg.Nk = hq.Nk; gg.part = hpart;
-        HybLif l{};
-        l.T = T; l.B = B; l.N = N; l.Nk = hq.Nk; l.Np = hq.Np; l.KS = hq.KS; l.D = hq.D; l.KF = KF; l.R = hq.R;
-        l.lda = hq.lda; l.part = hpart; l.lof = lof; l.h = h; l.bias = nullptr; l.drop = a->drop;
-        l.lif = make_lif(a->lif); l.state = state; l.hhi = ghi; l.hlo = glo;
-        l.u_in = a->u; l.gy = a->gy; l.dx = a->dx; l.gr = need_gr ? gr : nullptr; l.dbp = part; l.dbuf = dbuf;
+        LagStepGemm gn{};   // step t: near G(t + 1) from history slices t + 1 .. t + D
+        gn.a0 = ghi; gn.a1 = glo; gn.lda = hq.lda; gn.rs = 0; gn.B = B; gn.rows = B; gn.rp = 1;
+        gn.p0 = Pn; gn.p1 = planes > 1 ? Pn + nplane : nullptr; gn.Np = Nnp; gn.Kt = hq.Kt;
+        gn.KS = Nn > 0 ? lagstep_splits(B, Nnp, hq.Kt, num_cus()) : 1; gn.Nk = hq.Nk; gn.part = npart;
+        LagStepGemm gf = gn;   // block t0: far G(t0 + 1 + tt), row (b, tt) shifted by tt slices
+        gf.rows = B * P; gf.rp = P; gf.rs = hq.Nk;
+        gf.p0 = Pf; gf.p1 = planes > 1 ? Pf + fplane : nullptr; gf.Np = Nfp;
+        gf.KS = Nf > 0 ? lagstep_splits(B * P, Nfp, hq.Kt, num_cus()) : 1; gf.part = fpart;
+        HybBwd l{};
+        l.T = T; l.B = B; l.N = N; l.Nk = hq.Nk; l.KF = KF; l.R = hq.R; l.P = P; l.lda = hq.lda;
+        l.npart = npart; l.KSn = Nn > 0 ? gn.KS : 0; l.Nnp = Nnp; l.ntile = ntile; l.perm = perm;
+        l.fpart = fpart; l.KSf = gf.KS; l.Nfp = Nfp; l.Nn = Nn; l.Nf = Nf;
+        l.lof = lof; l.h = h; l.drop = a->drop; l.lif = make_lif(a->lif); l.state = state;
+        l.hhi = ghi; l.hlo = glo; l.u_in = a->u; l.gy = a->gy; l.dx = a->dx;
+        l.gr = need_gr ? gr : nullptr; l.dbp = a->db ? part : nullptr; l.ring = ring;
         const bool timed = scan_begin(DELREC_WS_SYN_BWD, s);
-        for (int t = T - 1; t >= 0; --t) {
-            gg.aoff = (size_t)(t + 1) * hq.Nk;
-            launch_lagstep_gemm(gg, 2, s, planes);
-            l.t = t;
-            launch_hyb_lif(l, false, hq.HW, s);
+        for (int t0 = T - 1; t0 >= 0; t0 -= P) {
+            if (Nf > 0) {
+                gf.aoff = (size_t)(t0 + 1) * hq.Nk;
+                launch_lagstep_gemm(gf, 2, s, planes);
+                l.t0 = t0;
+                launch_hyb_bwd_far(l, s);
+            }
+            for (int t = t0; t >= std::max(t0 - P + 1, 0); --t) {
+                if (Nn > 0) {
+                    gn.aoff = (size_t)(t + 1) * hq.Nk;
+                    launch_lagstep_gemm(gn, 2, s, planes);
+                }
+                l.t = t;
+                launch_hyb_bwd_lif(l, s);
+            }
         }
         scan_end(timed, s);
         int st = finish_launch();
         if (st) return st;
-        launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
+        if (a->db) launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
         if (a->dW || a->dd || a->ds) {
             launch_lag_bf16(g, need_gr ? gr : a->dx, a->bits, s);
             LagGemm f{};

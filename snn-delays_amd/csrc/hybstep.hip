@@ -15,15 +15,20 @@
 // trace and G the offset-stacked product. Each step runs one (B x D*N) by (D*N x N) product
 // over a batch-major history window -- the lag-stacked GEMM of lagstep.hip with the D offsets
 // in place of the L - 1 lags (C5: 5 products per connection instead of 66) -- and one LIF
-// launch that adds the split-K partials in a fixed order.
+// launch that adds the split-K partials in a fixed order. (The forward of bf16 W takes the
+// scatter on arrival further down, which walks only the spikes.)
 //
 // The per-source time shift lof_j sits on the contracted side in the forward (z_j is formed
 // by the LIF thread that owns neuron j, from its own spike-history word), and on the output
-// side in the backward: G_j(tau) is needed by steps tau - lof_j - f, different for every j. The
-// backward LIF therefore delivers h_j(lof_j + f) * G_j(t + 1) at once into ring f at the step
-// that will consume it, in a [slot][j][b] layout (b fastest): both the delivery (slot fixed by
-// j) and the consumption (slot fixed by t) are then whole 256-byte rows, through an LDS
-// transpose of the tile.
+// side in the backward: G_j(tau) is first needed at step tau - lof_j. So the backward splits
+// the sources: "near" ones (lof_j < P) get G_j(t + 1) from a per-step product over their
+// columns only, "far" ones (lof_j >= P) get G_j(tau) for the P steps tau = t0 + 1 .. t0 + P of a
+// block from one product at the block's start t0 whose rows are (b, tau) -- every one of
+// those G is first read at a step <= t0, and the history it reads (gr(t0 + 1 ..)) is complete.
+// For C5 (lof_j = floor(base_j) + 1, base U[0, 60], P = 8) the per-step product shrinks to the
+// 12 % of near columns and the rest runs as 4096-row products. Both write a ring of G_j(tau)
+// in a [slot][j][b] layout (b fastest, whole 256-byte rows through an LDS transpose); the
+// per-step LIF reads G_j(t + lof_j + f) from it.
 //
 // Precision: spikes are exact; z and gr are split into bf16 hi + lo planes (relative error
 // about 2^-16); W^(e) is one bf16 plane for bf16 W, or hi + lo planes for fp32 W
@@ -61,10 +66,12 @@ __global__ void __launch_bounds__(256) hyb_pack_kernel(HybPack p) {
     const int kb = (int)(idx / p.Np), col = (int)(idx - (size_t)kb * p.Np);
     float w[8];
     int e8[8];
+    // backward columns through the optional source permutation (columns past nc are 0)
+    const int jc = (!FWD && p.perm) ? (col < p.nc ? p.perm[p.c0 + col] : p.N) : col;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int i = FWD ? col : kb * 8 + e;
-        const int j = FWD ? kb * 8 + e : col;
+        const int j = FWD ? kb * 8 + e : jc;
         const bool ok = i < p.N && j < p.N;
         const size_t c = ok ? (size_t)i * p.N + j : 0;
         w[e] = ok ? load_w(p.W, p.w_bf16, c) : 0.0f;
@@ -161,109 +168,126 @@ __global__ void __launch_bounds__(256) hyb_lif_fwd_kernel(HybLif p) {
     p.hlo[ho] = (uint16_t)hyb_bf16_rne(z - __uint_as_float(hi << 16));
 }
 
-// Backward step t over a tile of 64 batch rows x 64 neurons (256 threads), three phases:
-//  1 (row-major, as the partials lie): G_j(t + 1) = sum_ks part[ks][b][j] into LDS;
-//  2 (transposed: one neuron j per wave, its 64 batch rows on the lanes): deliver
-//    h_j(lof_j + f) * G_j(t + 1) into ring f at the consuming step t + 1 - lof_j - f (kept in a
-//    register when that step is t itself), then gfut_j(t) = sum_f ring f at slot t (0 where
-//    the contribution's G index t + lof_j + f lies past T, which no step delivers);
+// Backward step t over a tile of 32 sources / neurons j0 .. j0 + 31 x 64 batch rows (256
+// threads; 2 workgroups per CU at C5), three phases:
+//  1 G_j(t + 1) of the tile's near sources, the near product's columns ntile[x] ..
+//    ntile[x + 1] - 1: sum_ks npart[ks][b][c] in a fixed order, 16 partials in flight per
+//    thread, into LDS;
+//  2 (transposed: one source per wave at a time, its 64 batch rows on the lanes): those
+//    G(t + 1) into ring slot (t + 1) mod R; then gfut_j(t) = sum_f h_j(lof_j + f) G_j(t + lof_j
+//    + f), from LDS for tau = t + 1 (lof_j = 1, f = 0: always a near source) and from the
+//    ring otherwise (0 for tau >= T: gr past the last step is 0), all ring reads of the
+//    wave's 8 sources issued before any is used;
 //  3 (row-major): the LIF backward on gy + gfut, outputs dx (and gr when it differs), the db
 //    partial, and gr(t) split into the hi / lo history planes at slice t.
-// Every phase issues all of its global loads before it uses any (a tile is 16 elements per
-// thread), so a wave waits for memory once per phase rather than once per element.
+// The ring slot of tau is rewritten with G(tau - R) only after every step that reads G(tau)
+// (steps >= tau - L + 1) has run, for R >= L - 1; this step's reads (tau >= t + 2) and writes
+// (tau = t + 1) never share a slot.
 constexpr int kHybTapsMax = 8;
+constexpr int kHybBwdTile = 32;
 
-__global__ void __launch_bounds__(256) hyb_lif_bwd_kernel(HybLif p) {
-    __shared__ float sg[64][65];
-    __shared__ float sf[64][65];
+template <int KF>
+__global__ void __launch_bounds__(256) hyb_bwd_lif_kernel(HybBwd p) {
+    constexpr int JT = kHybBwdTile;
+    __shared__ float sg[JT][65];
+    __shared__ float sf[JT][65];
+    __shared__ int ncl[JT];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j0 = blockIdx.x * 64, b0 = blockIdx.y * 64;
-    const int t = p.t, N = p.N, B = p.B;
+    const int j0 = blockIdx.x * JT, b0 = blockIdx.y * 64;
+    const int t = p.t, N = p.N, B = p.B, T = p.T, R = p.R;
+    const int lo = p.ntile[blockIdx.x], nn = p.ntile[blockIdx.x + 1] - lo;
+    if (tid < JT) ncl[tid] = -1;
+    __syncthreads();
     // phase 1
-    {
-        const int j = j0 + lane;
-        float g[16];
+    for (int o = tid; o < nn * 64; o += 256) {
+        const int r = o / nn, cl = o - r * nn, b = b0 + r;
+        float g = 0.0f;
+        if (b < B) {
+            const float* src = p.npart + (size_t)b * p.Nnp + lo + cl;
+            const size_t qs = (size_t)B * p.Nnp;
+            int q = 0;
+            for (; q + 16 <= p.KSn; q += 16) {
+                float v[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) g[e] = 0.0f;
-        for (int q = 0; q < p.KS; ++q) {
-            float v[16];
+                for (int e = 0; e < 16; ++e) v[e] = src[(size_t)(q + e) * qs];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int b = b0 + w + 4 * e;
-                v[e] = (b < B && j < N) ? p.part[((size_t)q * B + b) * p.Np + j] : 0.0f;
+                for (int e = 0; e < 16; ++e) g += v[e];
             }
-#pragma unroll
-            for (int e = 0; e < 16; ++e) g[e] += v[e];
+            for (; q < p.KSn; ++q) g += src[(size_t)q * qs];
         }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sg[lane][w + 4 * e] = g[e];
+        sg[cl][r] = g;
+        if (r == 0) ncl[p.perm[lo + cl] - j0] = cl;
     }
     __syncthreads();
     // phase 2
     {
         const int b = b0 + lane;
         const bool bok = b < B;
-        const int slot_t = t % p.R;
-        const size_t ringsz = (size_t)p.R * N * B;
-        const int KF = p.KF;
-#pragma unroll 2
-        for (int e = 0; e < 16; ++e) {
+        const int tm = t % R;
+        const int s1 = tm + 1 == R ? 0 : tm + 1;
+        constexpr int E = JT / 4;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int cl = w + 4 * e;
+            if (cl < nn && t + 1 < T && bok) p.ring[((size_t)s1 * N + p.perm[lo + cl]) * B + b] = sg[cl][lane];
+        }
+        float got[E][KF];
+        int lofv[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int j = j0 + w + 4 * e;
+            lofv[e] = j < N ? p.lof[j] : 0;
+#pragma unroll
+            for (int f = 0; f < KF; ++f) {
+                const int d = lofv[e] + f;   // tau - t, in [1, L - 1]
+                int sl = tm + d;
+                sl = sl >= R ? sl - R : sl;
+                const bool rd = j < N && f < p.KF && d >= 2 && t + d < T && bok;
+                got[e][f] = rd ? p.ring[((size_t)sl * N + j) * B + b] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
             const int jl = w + 4 * e, j = j0 + jl;
             float gf = 0.0f;
             if (j < N) {
-                const float g = sg[jl][lane];
-                const int lof = p.lof[j];
-                float hf[kHybTapsMax], got[kHybTapsMax];
-                // the consuming reads first (contributions delivered by earlier steps)
+                const int cl = ncl[jl];
 #pragma unroll
-                for (int f = 0; f < kHybTapsMax; ++f) {
-                    got[f] = 0.0f;
-                    if (f < KF) {
-                        hf[f] = p.h[(size_t)f * N + j];
-                        if (lof + f >= 2 && t + lof + f <= p.T && bok)
-                            got[f] = p.dbuf[(size_t)f * ringsz + ((size_t)slot_t * N + j) * B + b];
-                    }
-                }
-                // deliveries of G_j(t + 1) to their consuming steps
-#pragma unroll
-                for (int f = 0; f < kHybTapsMax; ++f) {
-                    if (f >= KF) break;
-                    const int s = t + 1 - lof - f;
-                    if (s != t && s >= 0 && bok)
-                        p.dbuf[(size_t)f * ringsz + ((size_t)(s % p.R) * N + j) * B + b] = hf[f] * g;
-                }
-#pragma unroll
-                for (int f = 0; f < kHybTapsMax; ++f) {
-                    if (f >= KF) break;
-                    gf += (lof + f == 1) ? hf[f] * g : got[f];
+                for (int f = 0; f < KF; ++f) {
+                    if (f >= p.KF) break;
+                    const float hf = p.h[(size_t)f * N + j];
+                    const float v = (lofv[e] + f == 1) ? (cl >= 0 && t + 1 < T ? sg[cl][lane] : 0.0f) : got[e][f];
+                    gf = fmaf(hf, v, gf);
                 }
             }
             sf[jl][lane] = gf;
         }
     }
     __syncthreads();
-    // phase 3
+    // phase 3: column jl = lane % 32, rows 2 w + lane / 32 + 8 e
     {
         const Lif k = p.lif;
-        const int j = j0 + lane;
+        const int jl = lane & (JT - 1), j = j0 + jl;
+        const int r0 = 2 * w + (lane >> 5);
         const size_t BN = (size_t)B * N;
-        const bool last = t == p.T - 1;
-        float uu[16], gyv[16], lam[16], dbv[16], mv[16];
+        const bool last = t == T - 1;
+        constexpr int E = 64 / 8;
+        float uu[E], gyv[E], lam[E], dbv[E], mv[E];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int b = b0 + w + 4 * e;
+        for (int e = 0; e < E; ++e) {
+            const int b = b0 + r0 + 8 * e;
             const bool ok = b < B && j < N;
             const size_t bj = (size_t)(ok ? b : 0) * N + (ok ? j : 0), o = (size_t)t * BN + bj;
             uu[e] = ok ? p.u_in[o] : 0.0f;
             gyv[e] = ok ? p.gy[o] : 0.0f;
             lam[e] = (ok && !last) ? p.state[bj] : 0.0f;
-            dbv[e] = (ok && !last) ? p.dbp[bj] : 0.0f;
+            dbv[e] = (ok && !last && p.dbp) ? p.dbp[bj] : 0.0f;
             mv[e] = (ok && p.drop) ? p.drop[bj] : 1.0f;
         }
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int b = b0 + w + 4 * e;
+        for (int e = 0; e < E; ++e) {
+            const int r = r0 + 8 * e, b = b0 + r;
             if (b >= B || j >= p.Nk) continue;
             const size_t ho = (size_t)b * p.lda + (size_t)t * p.Nk + j;
             if (j >= N) {
@@ -271,7 +295,7 @@ __global__ void __launch_bounds__(256) hyb_lif_bwd_kernel(HybLif p) {
                 p.hlo[ho] = 0;
                 continue;
             }
-            const float gf = sf[lane][w + 4 * e];
+            const float gf = sf[jl][r];
             const size_t bj = (size_t)b * N + j, o = (size_t)t * BN + bj;
             const float y = lif_fire(k, uu[e]);
             const float du = lif_backward(k, gyv[e] + gf, uu[e], y, lam[e]);
@@ -280,11 +304,53 @@ __global__ void __launch_bounds__(256) hyb_lif_bwd_kernel(HybLif p) {
             const float gr = da * mv[e];
             p.dx[o] = da;
             if (p.gr) p.gr[o] = gr;
-            p.dbp[bj] = last ? gr : dbv[e] + gr;
+            if (p.dbp) p.dbp[bj] = last ? gr : dbv[e] + gr;
             const uint32_t hi = hyb_bf16_rne(gr);
             p.hhi[ho] = (uint16_t)hi;
             p.hlo[ho] = (uint16_t)hyb_bf16_rne(gr - __uint_as_float(hi << 16));
         }
+    }
+}
+
+// The far product of the block that starts at step t0 (rows (b, tt), tau = t0 + 1 + tt):
+// G_j(tau) = sum_ks fpart[ks][b * P + tt][c] for far column c (source perm[Nn + c]) into
+// ring slot tau mod R. Tile: 64 far columns x 64 batch rows of one tt, summed row-major and
+// stored through an LDS transpose as 256-byte ring rows. Its consumers are steps
+// tau - lof_j - f <= t0 (lof_j >= P), none of which has run.
+__global__ void __launch_bounds__(256) hyb_bwd_far_kernel(HybBwd p) {
+    __shared__ float sg[64][65];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c0 = blockIdx.x * 64, b0 = blockIdx.y * 64, tt = blockIdx.z;
+    const int B = p.B, N = p.N, P = p.P;
+    const int tau = p.t0 + 1 + tt;
+    if (tau >= p.T) return;   // G past the last step is 0 and never read
+    {
+        const int c = c0 + lane;
+        const bool cok = c < p.Nf;
+        float g[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) g[e] = 0.0f;
+        for (int q = 0; q < p.KSf; ++q) {
+            float v[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int b = b0 + w + 4 * e;
+                v[e] = (cok && b < B) ? p.fpart[((size_t)q * B * P + (size_t)b * P + tt) * p.Nfp + c] : 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) g[e] += v[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sg[lane][w + 4 * e] = g[e];
+    }
+    __syncthreads();
+    const int b = b0 + lane;
+    const size_t slot = (size_t)(tau % p.R) * N;
+#pragma unroll 4
+    for (int e = 0; e < 16; ++e) {
+        const int cl = w + 4 * e, c = c0 + cl;
+        if (c < p.Nf && b < B) p.ring[(slot + p.perm[p.Nn + c]) * B + b] = sg[cl][lane];
     }
 }
 
@@ -537,7 +603,9 @@ HybStepDims hybstep_dims(int T, int B, int N, int L, int D, int KF, int cus) {
     q.R = std::max(L, 2);
     q.HW = (std::max(L - 1, 1) + 63) / 64;
     q.Kt = D * q.Nk;
-    q.lda = (size_t)(T + D + 1) * q.Nk;
+    q.P = lagstep_block();
+    q.lda = (size_t)(T + D + q.P + 1) * q.Nk;   // slices past the last step read as 0 (the far
+                                                // product of the first block reaches T + P + D - 2)
     q.plane = (size_t)(q.Kt / 8) * q.Np;
     q.KS = lagstep_splits(B, q.Np, q.Kt, cus);
     // offsets of 16 or fewer, taps of 8 or fewer, a spike history of two 64-bit words, and
@@ -560,18 +628,44 @@ void launch_hyb_taps(const HybTaps& a, hipStream_t stream) {
     hipLaunchKernelGGL(hyb_taps_kernel, dim3((a.N + 255) / 256), dim3(256), 0, stream, a);
 }
 
-void launch_hyb_lif(const HybLif& l, bool fwd, int hw, hipStream_t stream) {
-    if (fwd) {
-        const size_t n = (size_t)l.B * l.Nk;
-        const unsigned blocks = (unsigned)((n + 255) / 256);
-        if (hw == 1)
-            hipLaunchKernelGGL(hyb_lif_fwd_kernel<1>, dim3(blocks), dim3(256), 0, stream, l);
-        else
-            hipLaunchKernelGGL(hyb_lif_fwd_kernel<2>, dim3(blocks), dim3(256), 0, stream, l);
-    } else {
-        const dim3 grid((l.Nk + 63) / 64, (l.B + 63) / 64);
-        hipLaunchKernelGGL(hyb_lif_bwd_kernel, grid, dim3(256), 0, stream, l);
+void launch_hyb_lif(const HybLif& l, int hw, hipStream_t stream) {
+    const size_t n = (size_t)l.B * l.Nk;
+    const unsigned blocks = (unsigned)((n + 255) / 256);
+    if (hw == 1)
+        hipLaunchKernelGGL(hyb_lif_fwd_kernel<1>, dim3(blocks), dim3(256), 0, stream, l);
+    else
+        hipLaunchKernelGGL(hyb_lif_fwd_kernel<2>, dim3(blocks), dim3(256), 0, stream, l);
+}
+
+// the LIF tiles cover Nk neurons (the history planes' padding columns are written as 0)
+void launch_hyb_bwd_lif(const HybBwd& a, hipStream_t stream) {
+    const dim3 grid(a.Nk / kHybBwdTile, (a.B + 63) / 64);
+    if (a.KF <= 2)
+        hipLaunchKernelGGL(hyb_bwd_lif_kernel<2>, grid, dim3(256), 0, stream, a);
+    else if (a.KF <= 4)
+        hipLaunchKernelGGL(hyb_bwd_lif_kernel<4>, grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(hyb_bwd_lif_kernel<8>, grid, dim3(256), 0, stream, a);
+}
+
+int hyb_bwd_tile() { return kHybBwdTile; }
+
+void launch_hyb_bwd_far(const HybBwd& a, hipStream_t stream) {
+    if (a.Nf <= 0) return;
+    const dim3 grid((a.Nf + 63) / 64, (a.B + 63) / 64, a.P);
+    hipLaunchKernelGGL(hyb_bwd_far_kernel, grid, dim3(256), 0, stream, a);
+}
+
+HybBwdSizes hyb_bwd_sizes(const HybStepDims& q, int B, int cus) {
+    HybBwdSizes z{};
+    // any padded column count of either part (multiples of 128 up to Np); the two parts'
+    // padded counts add up to at most Np + 128
+    for (int c = 128; c <= q.Np; c += 128) {
+        z.npart = std::max(z.npart, (size_t)lagstep_splits(B, c, q.Kt, cus) * B * c);
+        z.fpart = std::max(z.fpart, (size_t)lagstep_splits(B * q.P, c, q.Kt, cus) * B * q.P * c);
     }
+    z.planes = (size_t)(q.Kt / 8) * (q.Np + 128);
+    return z;
 }
 
 }  // namespace delrec

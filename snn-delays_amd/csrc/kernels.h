@@ -199,6 +199,9 @@ struct HybPack {                 // W^(e) planes of the forward or backward oper
     int w_bf16;
     const int8_t* off;
     uint4* out;                  // planes of (D * Nk / 8) x Np uint4
+    // backward only, optional: output column c holds source perm[c0 + c] for c < nc (0 past)
+    const int* perm;
+    int c0, nc;
 };
 
 struct HybTaps {                 // each source's first lag and tap weights at the smallest offset
@@ -209,32 +212,55 @@ struct HybTaps {                 // each source's first lag and tap weights at t
     float* h;                    // [KF][N]
 };
 
-struct HybLif {
+struct HybLif {                  // one forward step of the offset-stacked scan
     int T, B, N, Nk, Np, KS, t, D, KF, R;
-    size_t lda;                  // history row pitch (elements): (T + D + 1) * Nk
+    size_t lda;                  // history row pitch (elements)
     const float* part;           // [KS][B][Np] partials of step t's product
     const int* lof;
     const float* h;
     const float* bias;
     const float* drop;
     Lif lif;
-    float* state;                // [B][N]: v (forward) or lambda (backward)
-    uint16_t* hhi;               // forward: z history hi plane; backward: gr history hi plane
+    float* state;                // [B][N]: v
+    uint16_t* hhi;               // z history planes
     uint16_t* hlo;
-    // forward
     const float* x;
     float* y;
     float* u;
     uint32_t* bits;
     uint64_t* hist;              // [HW][B][N] spike-history words
-    // backward
+};
+
+// The hybrid backward with the sources split by first lag (hybstep.hip): "near" sources
+// (lof < P) take G(t + 1) from a per-step product over their columns, "far" ones (lof >= P)
+// from one product per block of P steps whose rows are (batch row, step of the block); both
+// land in a ring of G_j(tau) that the LIF launch of each step reads.
+struct HybBwd {
+    int T, B, N, Nk, t, KF, R, P;
+    size_t lda;                  // history row pitch (elements)
+    const float* npart;          // [KSn][B][Nnp] partials of the near product of step t
+    int KSn, Nnp;
+    const int* ntile;            // [Nk / tile + 1]: the near columns of source tile x start here
+    const int* perm;             // [N]: the near sources ascending, then the far ones ascending
+    const float* fpart;          // [KSf][B * P][Nfp] partials of a block's far product
+    int KSf, Nfp, Nn, Nf, t0;
+    const int* lof;
+    const float* h;              // [KF][N]
+    const float* drop;
+    Lif lif;
+    float* state;                // [B][N] lambda
+    uint16_t* hhi;               // gr history planes
+    uint16_t* hlo;
     const float* u_in;
     const float* gy;
     float* dx;
     float* gr;                   // (T, B, N) when it differs from dx, else NULL
-    float* dbp;                  // [B][N] db partials
-    float* dbuf;                 // [KF][R][N][B] deliveries of h * G to their consuming step
+    float* dbp;                  // [B][N] db partials, or NULL
+    float* ring;                 // [R][N][B]: G_j(tau) at slot tau mod R
 };
+void launch_hyb_bwd_lif(const HybBwd& a, hipStream_t stream);
+int hyb_bwd_tile();              // sources per LIF tile (the granularity of HybBwd::ntile)
+void launch_hyb_bwd_far(const HybBwd& a, hipStream_t stream);
 
 struct HybScat {                 // the hybrid forward as a scatter on arrival (bf16 W)
     int T, B, N, D, KF, R, RP, omin;   // KF: the compiled run length; R = D + KF - 1 ring slots
@@ -252,15 +278,21 @@ struct HybScat {                 // the hybrid forward as a scatter on arrival (
 bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t lds, hipStream_t stream);
 
 struct HybStepDims {
-    int Nk, Np, D, KF, R, HW, Kt, KS;
+    int Nk, Np, D, KF, R, HW, Kt, KS, P;
     size_t lda, plane;
     bool ok;
 };
+// the backward's largest near / far partials and packed planes over every split of the
+// sources (the split is only known once the first lags are)
+struct HybBwdSizes {
+    size_t npart, fpart, planes;   // floats, floats, uint4 per W plane set (near + far)
+};
+HybBwdSizes hyb_bwd_sizes(const HybStepDims& q, int B, int cus);
 
 HybStepDims hybstep_dims(int T, int B, int N, int L, int D, int KF, int cus);
 void launch_hyb_pack(const HybPack& a, bool fwd, hipStream_t stream);
 void launch_hyb_taps(const HybTaps& a, hipStream_t stream);
-void launch_hyb_lif(const HybLif& l, bool fwd, int hw, hipStream_t stream);
+void launch_hyb_lif(const HybLif& l, int hw, hipStream_t stream);   // forward step
 
 int lagstep_splits(int B, int Np, int Kt, int cus);
 int lagstep_block();
