@@ -368,7 +368,7 @@ void hybstep_ws(C& c, int T, int B, int N, int L, int D, int KF, bool fwd, bool 
         c.template take<uint64_t>((size_t)q.HW * B * N);         // spike-history words
         return;
     }
-    const HybBwdSizes z = hyb_bwd_sizes(q, B, num_cus());
+    const HybBwdSizes z = hyb_bwd_sizes(q, B, num_cus(), hyb_bwd_far_cols(planes));
     c.template take<uint4>(planes * z.planes);                   // near + far W^(e) planes
     c.template take<uint16_t>((size_t)B * q.lda);                // gr history hi
     c.template take<uint16_t>((size_t)B * q.lda);                // gr history lo
@@ -1115,8 +1115,9 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         // of P steps with rows (b, step of the block); one LIF launch per step
         const int KF = taps;
         const HybStepDims hq = hybstep_dims(T, B, N, a->L, a->off_count, KF, num_cus());
-        const HybBwdSizes hz = hyb_bwd_sizes(hq, B, num_cus());
         const int planes = a->w_bf16 ? 1 : 2;
+        const int fcol = hyb_bwd_far_cols(planes);   // the far GEMM's workgroup columns
+        const HybBwdSizes hz = hyb_bwd_sizes(hq, B, num_cus(), fcol);
         const int P = hq.P;
         const int JT = hyb_bwd_tile();
         const int ntiles = hq.Nk / JT;   // LIF tiles over the padded width (Nk: a multiple of 32)
@@ -1155,7 +1156,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
             hipMemcpyAsync(ntile, ntile_h.data(), (size_t)(ntiles + 1) * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
             hipStreamSynchronize(s) != hipSuccess)
             return DELREC_ERR_LAUNCH;
-        const int Nnp = (Nn + 127) / 128 * 128, Nfp = (Nf + 127) / 128 * 128;
+        const int Nnp = (Nn + 127) / 128 * 128, Nfp = (Nf + fcol - 1) / fcol * fcol;
         const size_t nplane = (size_t)(hq.Kt / 8) * Nnp, fplane = (size_t)(hq.Kt / 8) * Nfp;
         uint4* Pn = Pw;                              // near planes: hi (, lo)
         uint4* Pf = Pw + (size_t)planes * nplane;    // far planes: hi (, lo)
@@ -1181,7 +1182,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         LagStepGemm gf = gn;   // block t0: far G(t0 + 1 + tt), row (b, tt) shifted by tt slices
         gf.rows = B * P; gf.rp = P; gf.rs = hq.Nk;
         gf.p0 = Pf; gf.p1 = planes > 1 ? Pf + fplane : nullptr; gf.Np = Nfp;
-        gf.KS = Nf > 0 ? lagstep_splits(B * P, Nfp, hq.Kt, num_cus()) : 1; gf.part = fpart;
+        gf.KS = Nf > 0 ? lagstep_splits(B * P, Nfp, hq.Kt, num_cus(), fcol) : 1; gf.part = fpart;
         HybBwd l{};
         l.T = T; l.B = B; l.N = N; l.Nk = hq.Nk; l.KF = KF; l.R = hq.R; l.P = P; l.lda = hq.lda;
         l.npart = npart; l.KSn = Nn > 0 ? gn.KS : 0; l.Nnp = Nnp; l.ntile = ntile; l.perm = perm;
@@ -1193,7 +1194,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         for (int t0 = T - 1; t0 >= 0; t0 -= P) {
             if (Nf > 0) {
                 gf.aoff = (size_t)(t0 + 1) * hq.Nk;
-                launch_lagstep_gemm(gf, 2, s, planes);
+                launch_lagstep_gemm(gf, 2, s, planes, fcol / 2);
                 l.t0 = t0;
                 launch_hyb_bwd_far(l, s);
             }

@@ -656,15 +656,18 @@ void launch_hyb_bwd_far(const HybBwd& a, hipStream_t stream) {
     hipLaunchKernelGGL(hyb_bwd_far_kernel, grid, dim3(256), 0, stream, a);
 }
 
-HybBwdSizes hyb_bwd_sizes(const HybStepDims& q, int B, int cus) {
+int hyb_bwd_far_cols(int planes) { return planes == 1 ? 256 : 128; }
+
+HybBwdSizes hyb_bwd_sizes(const HybStepDims& q, int B, int cus, int fcol) {
     HybBwdSizes z{};
-    // any padded column count of either part (multiples of 128 up to Np); the two parts'
-    // padded counts add up to at most Np + 128
-    for (int c = 128; c <= q.Np; c += 128) {
+    // any padded column count of either part: near columns in multiples of 128 up to Np, far
+    // ones in multiples of fcol up to Np rounded up to fcol; the two parts' padded counts add
+    // up to at most N + 127 + fcol - 1 < Np + 384
+    for (int c = 128; c <= q.Np; c += 128)
         z.npart = std::max(z.npart, (size_t)lagstep_splits(B, c, q.Kt, cus) * B * c);
-        z.fpart = std::max(z.fpart, (size_t)lagstep_splits(B * q.P, c, q.Kt, cus) * B * q.P * c);
-    }
-    z.planes = (size_t)(q.Kt / 8) * (q.Np + 128);
+    for (int c = fcol; c <= (q.Np + fcol - 1) / fcol * fcol; c += fcol)
+        z.fpart = std::max(z.fpart, (size_t)lagstep_splits(B * q.P, c, q.Kt, cus, fcol) * B * q.P * c);
+    z.planes = (size_t)(q.Kt / 8) * (q.Np + 384);
     return z;
 }
 

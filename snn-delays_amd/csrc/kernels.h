@@ -287,21 +287,22 @@ struct HybStepDims {
 struct HybBwdSizes {
     size_t npart, fpart, planes;   // floats, floats, uint4 per W plane set (near + far)
 };
-HybBwdSizes hyb_bwd_sizes(const HybStepDims& q, int B, int cus);
+HybBwdSizes hyb_bwd_sizes(const HybStepDims& q, int B, int cus, int fcol);
+int hyb_bwd_far_cols(int planes);   // far columns per GEMM tile: 256 for one W plane, else 128
 
 HybStepDims hybstep_dims(int T, int B, int N, int L, int D, int KF, int cus);
 void launch_hyb_pack(const HybPack& a, bool fwd, hipStream_t stream);
 void launch_hyb_taps(const HybTaps& a, hipStream_t stream);
 void launch_hyb_lif(const HybLif& l, int hw, hipStream_t stream);   // forward step
 
-int lagstep_splits(int B, int Np, int Kt, int cus);
+int lagstep_splits(int B, int Np, int Kt, int cus, int nc = 128);   // nc: workgroup columns
 int lagstep_block();
-size_t lagstep_gemm_lds(int pa, int pb = 2);
+size_t lagstep_gemm_lds(int pa, int pb = 2, int wn = 64);
 void launch_pack_lagw(const LagStepPack& a, bool fwd, hipStream_t stream);
 void launch_hist_zero(uint16_t* h, int B, size_t lda, int Nk, int t0, int t1, hipStream_t stream);
 void launch_hist_clear(uint16_t* h, int B, size_t lda, hipStream_t stream);
 // pb = 1: one P plane (p1 unused)
-void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream, int pb = 2);
+void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream, int pb = 2, int wn = 64);
 void launch_lagstep_lif(const LagStepLif& l, bool fwd, hipStream_t stream);
 int lagblock_splits(int B, int Np, int Nk, int cus);
 void launch_lagblock(const LagStepGemm& g, int pa, hipStream_t stream);

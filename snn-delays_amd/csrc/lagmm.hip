@@ -357,9 +357,10 @@ __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, i
 
 // one workgroup per (output tile, batch chunk); the chunk is the fastest index, so with 8
 // chunks the workgroups of one chunk share an XCD (workgroups are dealt to the XCDs in
-// turn) and its L2 holds the slices they all stream. Tiles of at most 8 lags run 8-lag
-// passes, of at most 10 lags 10-lag passes, wider ones 12-lag passes; the launch of each
-// variant skips the others' tiles (each variant gets the whole register file to itself).
+// turn) and its L2 holds the slices they all stream. Tiles of at most 6 lags run 6-lag
+// passes (the hybrid of 5 offsets and 2 taps), of at most 8 lags 8-lag passes, of at most 10
+// lags 10-lag passes, wider ones 12-lag passes; the launch of each variant skips the others'
+// tiles (each variant gets the whole register file to itself).
 template <int RL, bool DS>
 __global__ void __launch_bounds__(256) lag_win_kernel(LagBf16 p) {
     const int nbc = p.Bp / 32;
@@ -372,10 +373,11 @@ __global__ void __launch_bounds__(256) lag_win_kernel(LagBf16 p) {
     for (int k = 32; k >= 1; k >>= 1) rt = max(rt, __shfl_xor(rt, k));
     rt = __builtin_amdgcn_readfirstlane(rt);
     // each launch takes the tiles whose widest range its pass width serves best
-    if (RL == 8 && rt > 8) return;
+    if (RL == 6 && rt > 6) return;
+    if (RL == 8 && (rt <= 6 || rt > 8)) return;
     if (RL == 10 && (rt <= 8 || rt > 10)) return;
     if (RL == 12 && rt <= 10) return;
-    // gr-slice registers: 3 slots (2 slices ahead) beside a 12-slot spike window (8- and
+    // gr-slice registers: 3 slots (2 slices ahead) beside a 12-slot spike window (6-, 8- and
     // 10-lag passes), 4 slots (3 ahead) beside the 16-slot one (12-lag passes)
     lag_win_body<RL, RL <= 10 ? 12 : 16, RL <= 10 ? 3 : 4, DS>(p, i0, j0, bc, rt);
 }
@@ -396,10 +398,12 @@ void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hi
     const int tiles = (a.Np / kWT) * (a.Np / kWT);
     const dim3 grid((unsigned)(tiles * (a.Bp / 32)));
     if (a.ps) {
+        hipLaunchKernelGGL((lag_win_kernel<6, true>), grid, dim3(256), 0, stream, a);
         hipLaunchKernelGGL((lag_win_kernel<8, true>), grid, dim3(256), 0, stream, a);
         hipLaunchKernelGGL((lag_win_kernel<10, true>), grid, dim3(256), 0, stream, a);
         hipLaunchKernelGGL((lag_win_kernel<12, true>), grid, dim3(256), 0, stream, a);
     } else {
+        hipLaunchKernelGGL((lag_win_kernel<6, false>), grid, dim3(256), 0, stream, a);
         hipLaunchKernelGGL((lag_win_kernel<8, false>), grid, dim3(256), 0, stream, a);
         hipLaunchKernelGGL((lag_win_kernel<10, false>), grid, dim3(256), 0, stream, a);
         hipLaunchKernelGGL((lag_win_kernel<12, false>), grid, dim3(256), 0, stream, a);

@@ -97,10 +97,13 @@ __global__ void __launch_bounds__(256) pack_lagw_kernel(LagStepPack p) {
 
 // ---------------------------------------------------------------------------------------
 // Split-K GEMM of one step: part[ks][b][n] = sum over the split's k of A[b][k] * P[k][n].
-// Workgroup: 128 rows x 128 columns (4 waves of 64 x 64, 4 x 4 MFMA blocks each) and one
-// k split; 32-k stages go global -> registers (S stages ahead, fixed register slots:
+// Workgroup: 128 rows x 2 WN columns (4 waves of 64 x WN, 4 x WN / 16 MFMA blocks each) and
+// one k split; 32-k stages go global -> registers (S stages ahead, fixed register slots:
 // the loop is unrolled over S) -> LDS (double-buffered, one barrier per stage) -> fragment
 // registers (double-buffered: the next stage's fragments load while this stage multiplies).
+// WN = 128 halves the LDS bytes read per MFMA (a wave reads 64 rows and 128 columns of a
+// stage for 32 x PA blocks) -- the form of the long products; WN = 64 keeps more workgroups
+// for the short ones.
 // PA = 1: A x (P_hi + P_lo). PA = 2: A_hi x P_hi + A_hi x P_lo + A_lo x P_hi. PB = 1 (a one-
 // plane P, e.g. bf16 weights): A x P, or A_hi x P + A_lo x P.
 // Block order: workgroups are dealt to the 8 XCDs in turn (XCD = id mod 8), so when KS is a
@@ -109,13 +112,16 @@ __global__ void __launch_bounds__(256) pack_lagw_kernel(LagStepPack p) {
 // fetched into one L2 and shared there by every workgroup that reads them. Otherwise (the
 // per-block GEMM: many row tiles, few splits) each XCD takes a quarter of the row tiles
 // times half of the column tiles, so each A tile is fetched by 2 XCDs and each P tile by 4.
-template <int PA, int PB, int S>
+template <int PA, int PB, int S, int WN>
 __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
     extern __shared__ uint4 lds_u4[];
-    constexpr int PL = PA + PB;
+    constexpr int NC = 2 * WN;            // workgroup columns
+    constexpr int NBW = WN / 16;          // MFMA column blocks per wave
+    constexpr int BH = NC / 64;           // uint4 of a P plane staged per thread per stage
+    constexpr int BUF = PA * 512 + PB * 4 * NC;   // uint4 per LDS stage buffer
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int wi = w >> 1, wj = w & 1, g = lane >> 4, lc = lane & 15;
-    const int NT = p.Np / 128;
+    const int NT = p.Np / NC;
     const int BT = (p.rows + 127) / 128;
     const int id = (int)blockIdx.x;
     int bt, nt, ks;
@@ -139,7 +145,7 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
         ks = rest / NT;
         nt = rest - ks * NT;
     }
-    const int b0 = bt * 128, n0 = nt * 128;
+    const int b0 = bt * 128, n0 = nt * NC;
     const int nst = p.Kt / 32;
     const int per = (nst + p.KS - 1) / p.KS;
     const int s0 = ks * per;
@@ -152,8 +158,9 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
     const uint32_t pbytes = (uint32_t)((size_t)(p.Kt / 8) * p.Np * 16);
     rb[0] = buffer_rsrc(p.p0, pbytes);
     if (PB > 1) rb[PB - 1] = buffer_rsrc(p.p1, pbytes);
-    // staging: thread tid stages uint4 c = tid + 256 h (k-block c >> 7, row / column c & 127)
-    uint32_t oa[2], ob[2];
+    // staging: thread tid stages A uint4 c = tid + 256 h (k-block c >> 7, row c & 127) and
+    // P uint4 c = tid + 256 h (k-block c / NC, column c % NC)
+    uint32_t oa[2], ob[BH];
     const uint32_t bstep = (uint32_t)(4 * p.Np * 16);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -161,45 +168,57 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
         const int rr = b0 + r;   // rows past p.rows land past the descriptor's end: zeros
         oa[h] = (uint32_t)(((size_t)(rr / p.rp) * p.lda + (size_t)(rr % p.rp) * p.rs + p.aoff +
                             (size_t)s0 * 32 + kb * 8) * 2);
+    }
+#pragma unroll
+    for (int h = 0; h < BH; ++h) {
+        const int c = tid + 256 * h, kb = c / NC, r = c % NC;
         ob[h] = (uint32_t)((((size_t)s0 * 4 + kb) * p.Np + n0 + r) * 16);
     }
-    uint4 st[S][PL][2];
+    uint4 sa[S][PA][2], sb[S][PB][BH];
     auto issue = [&](int slot) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int q = 0; q < PA; ++q)
-                st[slot][q][h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(ra[q], (int)oa[h], 0, 0));
+                sa[slot][q][h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(ra[q], (int)oa[h], 0, 0));
+            oa[h] += 64;
+        }
+#pragma unroll
+        for (int h = 0; h < BH; ++h) {
 #pragma unroll
             for (int q = 0; q < PB; ++q)
-                st[slot][PA + q][h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rb[q], (int)ob[h], 0, 0));
-            oa[h] += 64;
+                sb[slot][q][h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rb[q], (int)ob[h], 0, 0));
             ob[h] += bstep;
         }
     };
     auto stash = [&](int slot, int buf) {
 #pragma unroll
-        for (int q = 0; q < PL; ++q)
+        for (int q = 0; q < PA; ++q)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) lds_u4[(buf * PL + q) * 512 + tid + 256 * h] = st[slot][q][h];
+            for (int h = 0; h < 2; ++h) lds_u4[buf * BUF + q * 512 + tid + 256 * h] = sa[slot][q][h];
+#pragma unroll
+        for (int q = 0; q < PB; ++q)
+#pragma unroll
+            for (int h = 0; h < BH; ++h) lds_u4[buf * BUF + PA * 512 + q * 4 * NC + tid + 256 * h] = sb[slot][q][h];
     };
-    floatx4 acc[4][4];
+    floatx4 acc[4][NBW];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int nb = 0; nb < NBW; ++nb) acc[mb][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    bf16x8 fa[2][PA][4], fb[2][PB][4];  // fragments: the stage being multiplied and the next
+    bf16x8 fa[2][PA][4], fb[2][PB][NBW];  // fragments: the stage being multiplied and the next
     auto frags = [&](int f, int buf) {
 #pragma unroll
-        for (int x = 0; x < 4; ++x) {
+        for (int x = 0; x < 4; ++x)
 #pragma unroll
             for (int q = 0; q < PA; ++q)
-                fa[f][q][x] = __builtin_bit_cast(bf16x8, lds_u4[(buf * PL + q) * 512 + g * 128 + wi * 64 + x * 16 + lc]);
+                fa[f][q][x] = __builtin_bit_cast(bf16x8, lds_u4[buf * BUF + q * 512 + g * 128 + wi * 64 + x * 16 + lc]);
+#pragma unroll
+        for (int x = 0; x < NBW; ++x)
 #pragma unroll
             for (int q = 0; q < PB; ++q)
-                fb[f][q][x] = __builtin_bit_cast(bf16x8, lds_u4[(buf * PL + PA + q) * 512 + g * 128 + wj * 64 + x * 16 + lc]);
-        }
+                fb[f][q][x] = __builtin_bit_cast(bf16x8, lds_u4[buf * BUF + PA * 512 + q * 4 * NC + g * NC + wj * WN + x * 16 + lc]);
     };
 
 #pragma unroll
@@ -222,20 +241,20 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-                    for (int nb = 0; nb < 4; ++nb)
+                    for (int nb = 0; nb < NBW; ++nb)
                         acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][0][mb], fb[f][0][nb], acc[mb][nb], 0, 0, 0);
                 if (PB > 1) {
 #pragma unroll
                     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-                        for (int nb = 0; nb < 4; ++nb)
+                        for (int nb = 0; nb < NBW; ++nb)
                             acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][0][mb], fb[f][PB - 1][nb], acc[mb][nb], 0, 0, 0);
                 }
                 if (PA > 1) {
 #pragma unroll
                     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-                        for (int nb = 0; nb < 4; ++nb)
+                        for (int nb = 0; nb < NBW; ++nb)
                             acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][PA - 1][mb], fb[f][0][nb], acc[mb][nb], 0, 0, 0);
                 }
             }
@@ -252,7 +271,7 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
             const int r = b0 + wi * 64 + mb * 16 + 4 * g + e;
             if (r >= p.rows) continue;
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb) out[(size_t)r * p.Np + n0 + wj * 64 + nb * 16 + lc] = acc[mb][nb][e];
+            for (int nb = 0; nb < NBW; ++nb) out[(size_t)r * p.Np + n0 + wj * WN + nb * 16 + lc] = acc[mb][nb][e];
         }
 }
 
@@ -492,17 +511,20 @@ __global__ void fill_rows_u16_kernel(uint16_t* __restrict__ h, int B, size_t lda
 
 // ---------------------------------------------------------------------------------------
 
-// k splits of a per-step GEMM: enough workgroups for every CU, rounded up to a multiple of
-// 8 where the k range allows, so that each XCD takes whole splits (its L2 then holds only its
-// k slice of both operands, fetched once) -- e.g. 512 x 2048 outputs with k = 10240: 8
-// splits of 64 tiles rather than 4, which leave each XCD a column half of the operand
-int lagstep_splits(int B, int Np, int Kt, int cus) {
-    const int tiles = ((B + 127) / 128) * (Np / 128);
+// k splits of a per-step GEMM: none when the tiles alone fill three quarters of the CUs;
+// else enough workgroups for every CU, rounded up to a multiple of 8 where that keeps to two
+// workgroups per CU and the k range allows, so that each XCD takes whole splits (its L2 then
+// holds only its k slice of both operands, fetched once) -- e.g. 512 x 2048 outputs with
+// k = 10240: 8 splits of 64 tiles rather than 4, which leave each XCD a column half of the
+// operand
+int lagstep_splits(int B, int Np, int Kt, int cus, int nc) {
+    const int tiles = ((B + 127) / 128) * (Np / nc);
+    if (tiles * 4 >= cus * 3) return 1;
     const int nst = Kt / 32;
     const int cap = std::max(1, nst / 8);
     int ks = std::max(1, std::min((cus + tiles - 1) / tiles, cap));
     const int up = (ks + 7) / 8 * 8;
-    if (ks > 1 && up <= cap) ks = up;
+    if (ks > 1 && up <= cap && tiles * up <= 2 * cus) ks = up;
     return ks;
 }
 
@@ -535,22 +557,26 @@ constexpr int kLagStepStages = 4;
 constexpr int kLagStepBlock = 8;   // steps per block (near lags per step)
 int lagstep_block() { return kLagStepBlock; }
 
-size_t lagstep_gemm_lds(int pa, int pb) { return (size_t)2 * (pa + pb) * 512 * sizeof(uint4); }
+size_t lagstep_gemm_lds(int pa, int pb, int wn) {
+    return (size_t)2 * (pa * 512 + pb * 4 * 2 * wn) * sizeof(uint4);
+}
 
-#define DELREC_LAGSTEP_GEMM(PAV, PBV)                                                          \
-    if (pa == PAV && pb == PBV) {                                                              \
-        ensure_lds((const void*)lagstep_gemm_kernel<PAV, PBV, kLagStepStages>, lds);          \
-        hipLaunchKernelGGL((lagstep_gemm_kernel<PAV, PBV, kLagStepStages>), dim3(grid), dim3(256), lds, \
+#define DELREC_LAGSTEP_GEMM(PAV, PBV, WNV)                                                     \
+    if (pa == PAV && pb == PBV && wn == WNV) {                                                 \
+        ensure_lds((const void*)lagstep_gemm_kernel<PAV, PBV, kLagStepStages, WNV>, lds);     \
+        hipLaunchKernelGGL((lagstep_gemm_kernel<PAV, PBV, kLagStepStages, WNV>), dim3(grid), dim3(256), lds, \
                            stream, g);                                                         \
         return;                                                                                \
     }
 
-void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream, int pb) {
-    const int grid = ((g.rows + 127) / 128) * (g.Np / 128) * g.KS;
-    const size_t lds = lagstep_gemm_lds(pa, pb);
-    DELREC_LAGSTEP_GEMM(1, 2)
-    DELREC_LAGSTEP_GEMM(2, 2)
-    DELREC_LAGSTEP_GEMM(2, 1)
+// wn = 128 (128 x 256 tiles; Np a multiple of 256) for a one-plane P, else 64
+void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream, int pb, int wn) {
+    const int grid = ((g.rows + 127) / 128) * (g.Np / (2 * wn)) * g.KS;
+    const size_t lds = lagstep_gemm_lds(pa, pb, wn);
+    DELREC_LAGSTEP_GEMM(1, 2, 64)
+    DELREC_LAGSTEP_GEMM(2, 2, 64)
+    DELREC_LAGSTEP_GEMM(2, 1, 64)
+    DELREC_LAGSTEP_GEMM(2, 1, 128)
 }
 
 // far lags of a block: rows (b, tt) of g.part with g.rp == kLagStepBlock
