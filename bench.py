@@ -1,7 +1,10 @@
 """Benchmark of the recurrent delayed-LIF layer: forward + BPTT backward throughput.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C1..C5] [--extra C2,C3]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C1..C5] [--extra C1,C2,C3,C4]
                     [--no-cpu]
+
+The headline is C5 (the largest configuration that fits one GPU); the other workloads are
+reported under "extra", each with its own roofline and CPU baseline.
 
 One step is one forward + backward of every recurrent layer of the workload over one
 batch of synthetic input, each layer driven by its own fixed input and a fixed upstream
@@ -419,7 +422,9 @@ def main():
     ap.add_argument('--steps', type=int, default=10)
     ap.add_argument('--warmup', type=int, default=2)
     ap.add_argument('--config', default=DEFAULT_CONFIG, choices=sorted(WORKLOADS))
-    ap.add_argument('--extra', default='', help='comma-separated further workloads reported under "extra"')
+    ap.add_argument('--extra', default='C1,C2,C3,C4',
+                    help='comma-separated further workloads reported under "extra" (each with its own '
+                         'roofline and CPU baseline); "" for none')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--calibrate-copy', type=int, metavar='MIB', default=0,
                     help='only run a plain device copy of MIB MiB (counter calibration)')

@@ -1179,10 +1179,11 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         gn.a0 = ghi; gn.a1 = glo; gn.lda = hq.lda; gn.rs = 0; gn.B = B; gn.rows = B; gn.rp = 1;
         gn.p0 = Pn; gn.p1 = planes > 1 ? Pn + nplane : nullptr; gn.Np = Nnp; gn.Kt = hq.Kt;
         gn.KS = Nn > 0 ? lagstep_splits(B, Nnp, hq.Kt, num_cus()) : 1; gn.Nk = hq.Nk; gn.part = npart;
+        gn.cm = 1;   // the LIF reads its near columns whole
         LagStepGemm gf = gn;   // block t0: far G(t0 + 1 + tt), row (b, tt) shifted by tt slices
         gf.rows = B * P; gf.rp = P; gf.rs = hq.Nk;
         gf.p0 = Pf; gf.p1 = planes > 1 ? Pf + fplane : nullptr; gf.Np = Nfp;
-        gf.KS = Nf > 0 ? lagstep_splits(B * P, Nfp, hq.Kt, num_cus(), fcol) : 1; gf.part = fpart;
+        gf.KS = Nf > 0 ? lagstep_splits(B * P, Nfp, hq.Kt, num_cus(), fcol) : 1; gf.part = fpart; gf.cm = 0;
         HybBwd l{};
         l.T = T; l.B = B; l.N = N; l.Nk = hq.Nk; l.KF = KF; l.R = hq.R; l.P = P; l.lda = hq.lda;
         l.npart = npart; l.KSn = Nn > 0 ? gn.KS : 0; l.Nnp = Nnp; l.ntile = ntile; l.perm = perm;

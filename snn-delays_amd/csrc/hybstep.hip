@@ -171,8 +171,8 @@ __global__ void __launch_bounds__(256) hyb_lif_fwd_kernel(HybLif p) {
 // Backward step t over a tile of 32 sources / neurons j0 .. j0 + 31 x 64 batch rows (256
 // threads; 2 workgroups per CU at C5), three phases:
 //  1 G_j(t + 1) of the tile's near sources, the near product's columns ntile[x] ..
-//    ntile[x + 1] - 1: sum_ks npart[ks][b][c] in a fixed order, 16 partials in flight per
-//    thread, into LDS;
+//    ntile[x + 1] - 1: sum_ks npart[ks][c][b] in a fixed order (column-major partials, one
+//    column per wave, 16 partials in flight per lane), into LDS;
 //  2 (transposed: one source per wave at a time, its 64 batch rows on the lanes): those
 //    G(t + 1) into ring slot (t + 1) mod R; then gfut_j(t) = sum_f h_j(lof_j + f) G_j(t + lof_j
 //    + f), from LDS for tau = t + 1 (lof_j = 1, f = 0: always a near source) and from the
@@ -199,25 +199,28 @@ __global__ void __launch_bounds__(256) hyb_bwd_lif_kernel(HybBwd p) {
     const int lo = p.ntile[blockIdx.x], nn = p.ntile[blockIdx.x + 1] - lo;
     if (tid < JT) ncl[tid] = -1;
     __syncthreads();
-    // phase 1
-    for (int o = tid; o < nn * 64; o += 256) {
-        const int r = o / nn, cl = o - r * nn, b = b0 + r;
-        float g = 0.0f;
-        if (b < B) {
-            const float* src = p.npart + (size_t)b * p.Nnp + lo + cl;
-            const size_t qs = (size_t)B * p.Nnp;
-            int q = 0;
-            for (; q + 16 <= p.KSn; q += 16) {
-                float v[16];
+    // phase 1: one near column per wave at a time, its 64 batch rows on the lanes (the
+    // partials are column-major: 256 contiguous bytes per partial)
+    {
+        const int b = b0 + lane;
+        const size_t qs = (size_t)p.Nnp * B;
+        for (int cl = w; cl < nn; cl += 4) {
+            float g = 0.0f;
+            if (b < B) {
+                const float* src = p.npart + (size_t)(lo + cl) * B + b;
+                int q = 0;
+                for (; q + 16 <= p.KSn; q += 16) {
+                    float v[16];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) v[e] = src[(size_t)(q + e) * qs];
+                    for (int e = 0; e < 16; ++e) v[e] = src[(size_t)(q + e) * qs];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) g += v[e];
+                    for (int e = 0; e < 16; ++e) g += v[e];
+                }
+                for (; q < p.KSn; ++q) g += src[(size_t)q * qs];
             }
-            for (; q < p.KSn; ++q) g += src[(size_t)q * qs];
+            sg[cl][lane] = g;
+            if (lane == 0) ncl[p.perm[lo + cl] - j0] = cl;
         }
-        sg[cl][r] = g;
-        if (r == 0) ncl[p.perm[lo + cl] - j0] = cl;
     }
     __syncthreads();
     // phase 2

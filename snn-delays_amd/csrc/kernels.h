@@ -167,7 +167,8 @@ struct LagStepGemm {
     const uint4* p1;
     int Np, Kt, KS;
     int Nk;                      // padded neurons per history slice / lag slice
-    float* part;                 // [KS][rows][Np]
+    float* part;                 // [KS][rows][Np], or [KS][Np][rows] when cm
+    int cm;                      // column-major partials (a consumer that reads columns)
 };
 
 struct LagStepLif {
@@ -238,7 +239,7 @@ struct HybLif {                  // one forward step of the offset-stacked scan
 struct HybBwd {
     int T, B, N, Nk, t, KF, R, P;
     size_t lda;                  // history row pitch (elements)
-    const float* npart;          // [KSn][B][Nnp] partials of the near product of step t
+    const float* npart;          // [KSn][Nnp][B] partials of the near product of step t (column-major)
     int KSn, Nnp;
     const int* ntile;            // [Nk / tile + 1]: the near columns of source tile x start here
     const int* perm;             // [N]: the near sources ascending, then the far ones ascending

@@ -264,6 +264,27 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
     }
 
     float* out = p.part + (size_t)ks * p.rows * p.Np;
+    if (p.cm) {
+        // column-major: a lane's 4 accumulator rows are 16 contiguous bytes of its column
+        // (16-byte aligned when the row count is a multiple of 4)
+        const bool v4 = (p.rows & 3) == 0;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const int r = b0 + wi * 64 + mb * 16 + 4 * g;
+#pragma unroll
+            for (int nb = 0; nb < NBW; ++nb) {
+                float* o = out + (size_t)(n0 + wj * WN + nb * 16 + lc) * p.rows + r;
+                if (v4 && r + 3 < p.rows) {
+                    *reinterpret_cast<floatx4*>(o) = acc[mb][nb];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (r + e < p.rows) o[e] = acc[mb][nb][e];
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
