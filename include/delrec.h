@@ -225,6 +225,9 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream);
  * GPU (other streams, other threads) race and must not be issued. Allocates nothing. */
 int delrec_axonal_bwd_noalloc(const delrec_axonal_bwd_args* a, void* stream);
 int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream);
+/* The hybrid's offset-stacked backward (off_count > 0, rings beyond LDS) reads each source's
+ * first lag back to the host once per call to split the sources: that call synchronises the
+ * stream before it launches its scan. Every other path is fully asynchronous. */
 int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream);
 int delrec_lif_fwd(const delrec_lif_fwd_args* a, void* stream);
 int delrec_lif_bwd(const delrec_lif_bwd_args* a, void* stream);
