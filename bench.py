@@ -104,6 +104,7 @@ def build(w, device, T=None, B=None):
     modules are the same."""
     from delrec.delay_layers import axonal_recdel, synaptic_recdel
     from delrec.networks import _reparametrize_recurrent_delay
+    from delrec.spike_linear import SpikeLinear
     torch.manual_seed(0)
     cfg = make_config(w)
     N = w['N']
@@ -112,7 +113,7 @@ def build(w, device, T=None, B=None):
     offsets_gen = torch.Generator().manual_seed(123)      # one generator, layers in module order
     for k in range(w.get('layers', 1)):
         if k > 0:
-            inter.append(torch.nn.Linear(N, N, bias=False))
+            inter.append(SpikeLinear(N, N, bias=False))
         if w['kind'] == 'axonal':
             layer = axonal_recdel(cfg, N)
         else:
@@ -176,7 +177,8 @@ def loss_of(m, y):
 
 def layer_inputs(m):
     """Each recurrent layer's fixed input and the upstream gradient dLoss/dy of the full
-    model at it (captured once), and each layer's firing rate."""
+    model at it (captured once), each layer's firing rate, and each layer's output (which
+    carries its spike bits for the Linear that follows it)."""
     xs, ys = [], []
     x = m.x
     for k, layer in enumerate(m.layers):
@@ -185,7 +187,7 @@ def layer_inputs(m):
                 x = (m.inter[k - 1](ys[-1]) * m.w['gain2']).contiguous()
         xs.append(x.detach())
         with torch.no_grad():
-            ys.append(layer(x).detach())
+            ys.append(layer(x))
     # backward through the stack: gy of the last layer from the loss, then through each
     # layer and Linear in turn
     y_last = ys[-1].clone().requires_grad_(True)
@@ -201,7 +203,31 @@ def layer_inputs(m):
         gys[k - 1] = gprev.contiguous()
         m.layers[k].zero_grad(set_to_none=True)
     firing = [float(y.mean()) for y in ys]
-    return xs, gys, firing
+    return xs, gys, firing, ys
+
+
+def inter_linear_ms(m, ys, reps=5):
+    """The Linear between stacked layers on the first layer's spikes: the binary-activation
+    GEMM on its spike bits against torch's fp32 GEMM on the fp32 spikes (same weights),
+    average ms per call, and the largest difference between the two."""
+    lin, y = m.inter[0], ys[0]
+    y_plain = y.clone()                   # no spike bits: torch.nn.functional.linear
+    out = {}
+    with torch.no_grad():
+        for name, fn in (('spike_bits_gemm', lambda: lin(y)), ('torch_fp32', lambda: lin(y_plain))):
+            fn()
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps):
+                r = fn()
+            e.record()
+            torch.cuda.synchronize()
+            out[name] = s.elapsed_time(e) / reps
+            out[name + '_out'] = r
+        diff = float((out.pop('spike_bits_gemm_out') - out.pop('torch_fp32_out')).abs().max())
+    out['max_abs_diff'] = diff
+    return out
 
 
 def algorithmic_work(w):
@@ -329,7 +355,9 @@ def measure(name, steps, warmup, with_cpu):
     w = WORKLOADS[name]
     dev = torch.device('cuda:0')
     m = build(w, dev)
-    xs, gys, firing = layer_inputs(m)
+    xs, gys, firing, ys_out = layer_inputs(m)
+    inter_ms = inter_linear_ms(m, ys_out) if m.inter else None
+    del ys_out
     T, B, N = xs[0].shape
     nl = len(m.layers)
     xins = [x.detach().clone().requires_grad_(True) for x in xs]
@@ -410,6 +438,8 @@ def measure(name, steps, warmup, with_cpu):
         'entry_ms': avg,
         'per_layer_value': nt_layer / (ms * 1e-3 / nl),
     }
+    if inter_ms is not None:
+        line['inter_linear_ms'] = inter_ms
     if with_cpu:
         print(f'[bench] {name}: {ms:.2f} ms/step on the GPU; CPU baseline next', file=sys.stderr, flush=True)
         line['cpu_baseline'] = cpu_baseline(m.layers[0], xs[0], w)
@@ -463,6 +493,8 @@ def main():
         'scan_ms': rec['scan_ms'],
         'entry_ms': rec['entry_ms'],
     }
+    if 'inter_linear_ms' in rec:
+        line['inter_linear_ms'] = rec['inter_linear_ms']
     if 'cpu_baseline' in rec:
         line['cpu_baseline'] = rec['cpu_baseline']
     extra = [c for c in args.extra.split(',') if c]

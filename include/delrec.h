@@ -204,6 +204,22 @@ typedef struct {
     float* dx;
 } delrec_lif_bwd_args;
 
+/* Linear layer on spike inputs: out[t][b][m] = bias[m] + sum_k y[t][b][k] * W[m*K + k],
+ * the spikes y given as the scans' spike bits. Replaces torch.nn.Linear applied to a
+ * recurrent layer's spike output in the SNN_* stacks (reference networks.py:140-181, the
+ * Linear that follows each recurrent layer in the Sequential). W is read in fp32 and
+ * applied as bf16 hi + mid + lo (about 2^-25 relative per weight, fp32 accumulation). Workspace:
+ * delrec_query_workspace(DELREC_WS_SPIKE_LINEAR, T, B, K, M, 0). */
+typedef struct {
+    int32_t T, B, K, M;
+    const uint32_t* bits;        /* (B, ceil(T/32), K) spike words                        */
+    const float* W;              /* (M, K) fp32                                           */
+    const float* bias;           /* (M) or NULL                                           */
+    float* out;                  /* out (T, B, M) fp32                                    */
+    void* workspace;
+    size_t workspace_bytes;
+} delrec_spike_linear_args;
+
 /* Workspace kinds for delrec_query_workspace; flags bit 0: weights are bf16; synaptic
  * kinds: bit 1: hybrid delays (d == NULL), bits 8..15: ceil(2 * s_max) on the float32 s_max
  * the entry point receives (s_uniform for the hybrid), capped at 255 -- the most lags of
@@ -211,7 +227,7 @@ typedef struct {
  * bit 2: d_min >= s_uniform - 1, bits 16..23: off_count (the fields of the entry point's
  * arguments, which also pick the scan form). */
 enum { DELREC_WS_AXONAL_FWD = 1, DELREC_WS_AXONAL_BWD = 2, DELREC_WS_SYN_FWD = 3,
-       DELREC_WS_SYN_BWD = 4 };
+       DELREC_WS_SYN_BWD = 4, DELREC_WS_SPIKE_LINEAR = 5 /* N = K inputs, L = M outputs */ };
 
 int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream);
 int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream);
@@ -229,6 +245,7 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream);
  * first lag back to the host once per call to split the sources: that call synchronises the
  * stream before it launches its scan. Every other path is fully asynchronous. */
 int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream);
+int delrec_spike_linear_fwd(const delrec_spike_linear_args* a, void* stream);
 int delrec_lif_fwd(const delrec_lif_fwd_args* a, void* stream);
 int delrec_lif_bwd(const delrec_lif_bwd_args* a, void* stream);
 

@@ -658,6 +658,9 @@ int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_
             syn_bwd_ws(c, T, B, N, L, (flags >> 8) & 0xff, (flags & 2) != 0, bf16, (flags >> 16) & 0xff,
                        (flags & 4) != 0);
             break;
+        case DELREC_WS_SPIKE_LINEAR:
+            c.take<uint4>(spike_linear_ws(N, L) / sizeof(uint4));
+            break;
         default: return DELREC_ERR_ARG;
     }
     *bytes = c.used;
@@ -1028,6 +1031,24 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream) {
     }
     if (!(scatter && launch_syn_fwd_scatter(p, kf, lay.block, lds_s, s))) launch_syn_fwd(p, lay.block, lds, s);
     scan_end(timed, s);
+    return finish_launch();
+}
+
+int delrec_spike_linear_fwd(const delrec_spike_linear_args* a, void* stream) {
+    if (!a || a->T <= 0 || a->B <= 0 || a->K <= 0 || a->M <= 0) return DELREC_ERR_ARG;
+    if (!a->bits || !a->W || !a->out) return DELREC_ERR_ARG;
+    SpikeLinear p{};
+    p.T = a->T; p.B = a->B; p.K = a->K; p.M = a->M;
+    p.bits = a->bits; p.W = a->W; p.bias = a->bias; p.out = a->out;
+    spike_linear_dims(p);
+    // 32-bit byte offsets: the spike words, the packed planes and one output row block
+    const int TW = (p.T + 31) / 32;
+    if ((size_t)p.B * TW * p.K * 4 >= ((size_t)1 << 31) || spike_linear_ws(p.K, p.M) >= ((size_t)1 << 31))
+        return DELREC_ERR_UNSUPPORTED;
+    Carver cv(a->workspace, a->workspace_bytes);
+    uint4* wp = cv.take<uint4>(spike_linear_ws(p.K, p.M) / sizeof(uint4));
+    if (!wp) return DELREC_ERR_WORKSPACE;
+    launch_spike_linear(p, wp, static_cast<hipStream_t>(stream));
     return finish_launch();
 }
 

@@ -278,6 +278,18 @@ struct HybScat {                 // the hybrid forward as a scatter on arrival (
 };
 bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t lds, hipStream_t stream);
 
+// Linear layer on spike inputs (spikelinear.hip): out[t][b][m] = bias[m] + sum_k y W[m][k]
+struct SpikeLinear {
+    int T, B, K, M, Kp, Mp;      // Kp = K rounded up to 32, Mp = M rounded up to 128
+    const uint32_t* bits;        // (B, ceil(T/32), K) spike words
+    const float* W;              // (M, K) fp32
+    const float* bias;           // (M) or NULL
+    float* out;                  // (T, B, M) fp32
+};
+void spike_linear_dims(SpikeLinear& p);
+size_t spike_linear_ws(int K, int M);   // bytes of the packed W^T planes
+void launch_spike_linear(const SpikeLinear& p, uint4* wp, hipStream_t stream);
+
 struct HybStepDims {
     int Nk, Np, D, KF, R, HW, Kt, KS, P;
     size_t lda, plane;

@@ -1,0 +1,208 @@
+// The Linear layer that follows a recurrent delayed-LIF layer in the SNN_* stacks
+// (torch.nn.Linear in the Sequential of reference networks.py:140-181, applied to the
+// layer's spike output), as a binary-activation GEMM on bf16 MFMA (gfx950):
+//   out[t][b][m] = bias[m] + sum_k y[t][b][k] * W[m][k],   y in {0, 1},
+// read straight from the scans' spike bits (B, ceil(T/32), K) -- 1/32 of the fp32 spikes.
+//
+// The spikes are exact in bf16; W^T is split into bf16 hi + mid + lo planes (about 2^-25
+// relative per weight, below fp32's own rounding; accumulation fp32), so each tile takes
+// three products. A workgroup owns 128 consecutive steps of one batch row (four 32-step
+// spike words per neuron) by 128 output columns: per 32-neuron stage it stages the 4 x 32
+// spike words and the W planes' 32 x 128 blocks in LDS, and each lane expands its A fragment
+// (16 rows x 8 neurons) from the words.
+#include "kernels.h"
+
+namespace delrec {
+
+namespace {
+
+typedef float sl_floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 sl_bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint32_t sl_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+constexpr int kSpikeLinearPlanes = 3;
+
+}  // namespace
+
+// W^T planes, k-blocked: element (k, m) = W[m][k] at ((k / 8) * Mp + m) * 8 + k % 8, hi, mid
+// and lo planes in turn; columns m >= M and rows k >= K are 0.
+__global__ void __launch_bounds__(256) spike_linear_pack_kernel(SpikeLinear p, uint4* out) {
+    const size_t total = (size_t)(p.Kp / 8) * p.Mp;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int kb = (int)(idx / p.Mp), m = (int)(idx - (size_t)kb * p.Mp);
+    uint32_t pl[kSpikeLinearPlanes][4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        uint32_t v2[kSpikeLinearPlanes][2];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const int k = kb * 8 + e + f;
+            float r = (m < p.M && k < p.K) ? p.W[(size_t)m * p.K + k] : 0.0f;
+#pragma unroll
+            for (int q = 0; q < kSpikeLinearPlanes; ++q) {   // each plane the remainder's bf16
+                v2[q][f] = sl_bf16_rne(r);
+                r -= __uint_as_float(v2[q][f] << 16);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kSpikeLinearPlanes; ++q) pl[q][e / 2] = v2[q][0] | (v2[q][1] << 16);
+    }
+#pragma unroll
+    for (int q = 0; q < kSpikeLinearPlanes; ++q)
+        out[q * total + idx] = uint4{pl[q][0], pl[q][1], pl[q][2], pl[q][3]};
+}
+
+// Tile: 128 steps t0 .. t0 + 127 of batch row b x 128 columns n0 .. n0 + 127; 4 waves of
+// 64 x 64 (4 x 4 MFMA blocks, three W planes). Stage s covers neurons 32 s .. 32 s + 31. Loads
+// of stage s + 2 are issued while stage s multiplies; stage s + 1 goes to LDS after it; one
+// barrier per stage.
+__global__ void __launch_bounds__(256) spike_linear_kernel(SpikeLinear p, const uint4* wp) {
+    constexpr int PL = kSpikeLinearPlanes;
+    __shared__ uint4 sw[2][PL][512];     // [buffer][plane][k-block * 128 + column]
+    __shared__ __align__(16) uint32_t sa[2][4][32];   // [buffer][32-step word][neuron of the stage]
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int wi = w >> 1, wj = w & 1, g = lane >> 4, lc = lane & 15;
+    const int NT = p.Mp / 128, TT = (p.T + 127) / 128, TW = (p.T + 31) >> 5;
+    const int id = (int)blockIdx.x;
+    const int nt = id % NT, rest = id / NT, tt = rest % TT, b = rest / TT;
+    const int t0 = tt * 128, n0 = nt * 128;
+    const int nst = p.Kp / 32;
+    const size_t plane = (size_t)(p.Kp / 8) * p.Mp;
+    const i32x4 rw = buffer_rsrc(wp, (uint32_t)(PL * plane * 16));
+    const i32x4 rb = buffer_rsrc(p.bits, (uint32_t)((size_t)p.B * TW * p.K * 4));
+    // staging: W uint4 c = tid + 256 h (k-block c >> 7, column c & 127) of both planes; the
+    // spike word of (32-step block tid >> 5, neuron tid & 31) for threads below 128
+    uint32_t ow[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = tid + 256 * h, kb = c >> 7, col = c & 127;
+        ow[h] = (uint32_t)(((size_t)kb * p.Mp + n0 + col) * 16);
+    }
+    const uint32_t wstep = (uint32_t)(4 * p.Mp * 16);
+    const int tb = tid >> 5, kk = tid & 31;
+    const bool aload = tid < 128 && (t0 >> 5) + tb < TW;
+    const uint32_t oa0 = aload ? (uint32_t)((((size_t)b * TW + (t0 >> 5) + tb) * p.K + kk) * 4) : 0x7ffffff0u;
+    uint4 rwv[2][PL][2];   // [register set][plane][h]
+    uint32_t rav[2];
+    auto issue = [&](int set, int s) {
+#pragma unroll
+        for (int q = 0; q < PL; ++q)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                rwv[set][q][h] = __builtin_bit_cast(
+                    uint4, raw_buffer_load_i32x4(rw, (int)(ow[h] + (uint32_t)s * wstep + (uint32_t)q * (uint32_t)(plane * 16)), 0, 0));
+        // neurons past K read past the row: another neuron's word, weighted by the zero rows
+        // of W's padding -- unless past the buffer, which reads 0
+        rav[set] = __float_as_uint(raw_buffer_load_f32(rb, aload ? (int)(oa0 + (uint32_t)s * 128u) : 0x7ffffff0, 0, 0));
+    };
+    auto stash = [&](int set, int buf) {
+#pragma unroll
+        for (int q = 0; q < PL; ++q)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) sw[buf][q][tid + 256 * h] = rwv[set][q][h];
+        if (tid < 128) sa[buf][tb][kk] = rav[set];
+    };
+    sl_floatx4 acc[4][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = sl_floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int buf) {
+        sl_bf16x8 fa[4], fb[PL][4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int q = 0; q < PL; ++q)
+                fb[q][x] = __builtin_bit_cast(sl_bf16x8, sw[buf][q][g * 128 + wj * 64 + x * 16 + lc]);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const int row = wi * 64 + mb * 16 + lc;   // step t0 + row
+            const uint4* src = reinterpret_cast<const uint4*>(&sa[buf][row >> 5][g * 8]);
+            const uint4 w0 = src[0], w1 = src[1];
+            const int bit = row & 31;
+            const uint32_t wd[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            uint32_t pk[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t a0 = ((wd[2 * e] >> bit) & 1u) * 0x3F80u;       // bf16 1.0 or 0
+                const uint32_t a1 = ((wd[2 * e + 1] >> bit) & 1u) * 0x3F80u;
+                pk[e] = a0 | (a1 << 16);
+            }
+            fa[mb] = __builtin_bit_cast(sl_bf16x8, uint4{pk[0], pk[1], pk[2], pk[3]});
+        }
+#pragma unroll
+        for (int q = 0; q < PL; ++q)
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[mb], fb[q][nb], acc[mb][nb], 0, 0, 0);
+    };
+
+    issue(0, 0);
+    issue(1, 1);
+    stash(0, 0);
+    barrier_lds();
+    for (int s = 0; s < nst; s += 2) {
+        // stage s in LDS buffer 0, stage s + 1 in register set 1
+        issue(0, s + 2);
+        compute(0);
+        stash(1, 1);
+        barrier_lds();
+        if (s + 1 >= nst) break;
+        issue(1, s + 3);
+        compute(1);
+        stash(0, 0);
+        barrier_lds();
+    }
+
+    // epilogue: rows t = t0 + wi * 64 + mb * 16 + 4 g + e, columns n0 + wj * 64 + nb * 16 + lc
+    float bv[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+        const int m = n0 + wj * 64 + nb * 16 + lc;
+        bv[nb] = (p.bias && m < p.M) ? p.bias[m] : 0.0f;
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = t0 + wi * 64 + mb * 16 + 4 * g + e;
+            if (t >= p.T) continue;
+            float* o = p.out + ((size_t)t * p.B + b) * p.M;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) {
+                const int m = n0 + wj * 64 + nb * 16 + lc;
+                if (m < p.M) o[m] = acc[mb][nb][e] + bv[nb];
+            }
+        }
+}
+
+void spike_linear_dims(SpikeLinear& p) {
+    p.Kp = (p.K + 31) / 32 * 32;
+    p.Mp = (p.M + 127) / 128 * 128;
+}
+
+size_t spike_linear_ws(int K, int M) {
+    SpikeLinear p{};
+    p.K = K;
+    p.M = M;
+    spike_linear_dims(p);
+    return (size_t)kSpikeLinearPlanes * (p.Kp / 8) * p.Mp * sizeof(uint4);
+}
+
+void launch_spike_linear(const SpikeLinear& p, uint4* wp, hipStream_t stream) {
+    const size_t total = (size_t)(p.Kp / 8) * p.Mp;
+    hipLaunchKernelGGL(spike_linear_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, p, wp);
+    const unsigned grid = (unsigned)((size_t)p.B * ((p.T + 127) / 128) * (p.Mp / 128));
+    hipLaunchKernelGGL(spike_linear_kernel, dim3(grid), dim3(256), 0, stream, p, (const uint4*)wp);
+}
+
+}  // namespace delrec

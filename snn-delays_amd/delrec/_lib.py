@@ -26,11 +26,11 @@ DELREC_TAPS_SOFT, DELREC_TAPS_ROUND, DELREC_TAPS_INTERP = 0, 1, 2
 DELREC_BWD_SOFT, DELREC_BWD_STRAIGHT = 0, 1
 DELREC_ERR_WINDOW = 5
 DELREC_ERR_SCRATCH = 9
-WS_AXONAL_FWD, WS_AXONAL_BWD, WS_SYN_FWD, WS_SYN_BWD = 1, 2, 3, 4
+WS_AXONAL_FWD, WS_AXONAL_BWD, WS_SYN_FWD, WS_SYN_BWD, WS_SPIKE_LINEAR = 1, 2, 3, 4, 5
 
 # Every symbol include/delrec.h declares (checked by the CPU test suite).
 EXPORTS = ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_axonal_bwd_noalloc', 'delrec_syn_fwd',
-           'delrec_syn_bwd',
+           'delrec_syn_bwd', 'delrec_spike_linear_fwd',
            'delrec_lif_fwd', 'delrec_lif_bwd', 'delrec_delay_grad', 'delrec_query_workspace',
            'delrec_strerror', 'delrec_version', 'delrec_scan_timing', 'delrec_scan_timing_read',
            'delrec_max_post', 'delrec_max_take')
@@ -88,6 +88,11 @@ class SynBwdArgs(ctypes.Structure):
                 ('d_min', c_f32), ('off_min', c_i32), ('off_count', c_i32)]
 
 
+class SpikeLinearArgs(ctypes.Structure):
+    _fields_ = [('T', c_i32), ('B', c_i32), ('K', c_i32), ('M', c_i32), ('bits', c_vp), ('W', c_vp),
+                ('bias', c_vp), ('out', c_vp), ('workspace', c_vp), ('workspace_bytes', c_size)]
+
+
 class LifFwdArgs(ctypes.Structure):
     _fields_ = [('T', c_i32), ('B', c_i32), ('N', c_i32), ('x', c_vp), ('lif', Lif),
                 ('y', c_vp), ('u', c_vp)]
@@ -111,7 +116,7 @@ def load():
                           f'g.build()"` from the repository root')
     lib = ctypes.CDLL(str(LIB_PATH))
     for name in ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_axonal_bwd_noalloc', 'delrec_syn_fwd',
-                 'delrec_syn_bwd', 'delrec_lif_fwd', 'delrec_lif_bwd'):
+                 'delrec_syn_bwd', 'delrec_spike_linear_fwd', 'delrec_lif_fwd', 'delrec_lif_bwd'):
         getattr(lib, name).restype = c_i32
         getattr(lib, name).argtypes = [c_vp, c_vp]
     lib.delrec_delay_grad.restype = c_i32

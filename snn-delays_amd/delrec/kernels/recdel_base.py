@@ -22,6 +22,7 @@ import threading
 import torch
 
 from .. import _lib
+from ..spike_linear import attach_bits
 from ._common import (bits_shape, drop_bn, read_scalars, require_device, round_half_even_f32, weights,
                       window_length_f32)
 from .delays import build_lag, build_lag_interp
@@ -97,7 +98,7 @@ class AxonalRecdelHip(torch.autograd.Function):
             ctx.save_for_backward(u, z, bits, Wc, dc, s_vec, m, None, p_spread)
             ctx.meta = (T, B, N, pending, w_bf16, sigma, bool(use_sig_p), _lib.DELREC_BWD_SOFT, W.dtype)
             ctx.lif = lif
-            return y
+            return attach_bits(y, bits)
 
         # The window length needs max d (and max s): the one device-to-host read of the call,
         # taken after the host work above so that it overlaps the GPU work still queued.
@@ -132,7 +133,7 @@ class AxonalRecdelHip(torch.autograd.Function):
         ctx.save_for_backward(u, z, bits, Wc, dc, s_vec, m, lag, p_spread)
         ctx.meta = (T, B, N, L, w_bf16, sigma, bool(use_sig_p), mode, W.dtype)
         ctx.lif = lif
-        return y
+        return attach_bits(y, bits)
 
     @staticmethod
     def backward(ctx, gy):

@@ -13,6 +13,7 @@ import numpy as np
 import torch
 
 from .. import _lib
+from ..spike_linear import attach_bits
 from ._common import bits_shape, drop_bn, lif_struct, read_scalars, require_device, weights, window_length_f64
 
 
@@ -127,7 +128,7 @@ class EventDrivenSyn(torch.autograd.Function):
         ctx.meta = (L, w_bf16, s_uniform, s_max, float(layer.sigma), bool(layer.use_sig_p),
                     bias is not None, W.dtype)
         ctx.lif = lif
-        return y
+        return attach_bits(y, bits)
 
     @staticmethod
     def backward(ctx, gy):

@@ -17,6 +17,7 @@ import os
 import torch
 
 from .. import _lib
+from ..spike_linear import attach_bits
 from ._common import drop_bn, require_device
 from .synaptic_eventdriven import layer_lif, recurrent_drop, syn_backward, syn_forward
 
@@ -83,7 +84,7 @@ class HybridSynDelay(torch.autograd.Function):
         ctx.save_for_backward(u, y, bits, Wc, d_arg, base, off8, m)
         ctx.meta = (L, w_bf16, s, bias is not None, W.dtype, hyb)
         ctx.lif = lif
-        return y
+        return attach_bits(y, bits)
 
     @staticmethod
     def backward(ctx, gy):

@@ -12,6 +12,8 @@ Feedforward-delay classes ride DCLS's convolution, not this path, and are not pr
 
 import torch
 
+from .spike_linear import SpikeLinear
+
 from .delay_layers import axonal_recdel, synaptic_recdel, common_recdel
 from .neuron import Dropout
 
@@ -93,7 +95,9 @@ def _recurrent_stack(model, config, make_recurrent):
     layers = []
     dim_buffer = config.input_size
     for idx, layer_dim in enumerate(config.hidden_layers):
-        layers.append(torch.nn.Linear(dim_buffer, layer_dim, bias=config.bias))
+        # the Linear after a recurrent layer takes its spikes: the binary-activation GEMM
+        linear = torch.nn.Linear if idx == 0 else SpikeLinear
+        layers.append(linear(dim_buffer, layer_dim, bias=config.bias))
         dim_buffer = layer_dim
         layers.append(Dropout(config.feedforward_dropout_rate, step_mode='m'))
         is_last_hidden = idx == len(config.hidden_layers) - 1
@@ -104,7 +108,7 @@ def _recurrent_stack(model, config, make_recurrent):
         layers.append(spike_registrator())
         if config.use_batch_norm:
             layers.append(_batch_norm(config, layer_dim))
-    layers.append(torch.nn.Linear(dim_buffer, config.output_size, bias=config.bias))
+    layers.append(SpikeLinear(dim_buffer, config.output_size, bias=config.bias))
     model.layers = torch.nn.Sequential(*layers)
     model.init_weights()
 

@@ -257,3 +257,15 @@ def test_reference_import_path_resolves_to_the_hip_modules():
     assert hybrid_trainable_forward is k.synaptic_hybrid.hybrid_trainable_forward
     assert EventDrivenSyn is k.synaptic_eventdriven.EventDrivenSyn
     assert tk_delays is k.delays
+
+
+def test_spike_linear_falls_back_to_linear_without_bits():
+    """Without spike bits (a CPU tensor, an analog input) SpikeLinear is torch's Linear."""
+    from delrec.spike_linear import SpikeLinear
+    torch.manual_seed(0)
+    lin = SpikeLinear(12, 5)
+    ref = torch.nn.Linear(12, 5)
+    ref.load_state_dict(lin.state_dict())
+    x = torch.rand(4, 3, 12)
+    torch.testing.assert_close(lin(x), ref(x))
+    assert isinstance(lin, torch.nn.Linear)

@@ -1,0 +1,88 @@
+"""GPU parity of the binary-activation Linear (``delrec_spike_linear_fwd`` through
+``delrec.spike_linear.SpikeLinear``) against ``torch.nn.functional.linear`` in float64 on the
+same spikes and weights. The spikes are exact; W enters as bf16 hi + mid + lo (about 2^-25
+relative per weight), so the tolerance is fp32's: rtol 1e-5, atol 1e-6 relative to the
+output's magnitude. Shapes cover T, K and M off their tile multiples (128 steps, 32
+neurons, 128 outputs), with and without bias, and the bits attached by a recurrent layer.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import gen
+
+
+def pack_bits(y):
+    """(T, B, K) {0, 1} -> (B, ceil(T/32), K) spike words (bit t % 32 of word t // 32)."""
+    T, B, K = y.shape
+    TW = (T + 31) // 32
+    yy = np.zeros((TW * 32, B, K), dtype=np.uint64)
+    yy[:T] = y.numpy().astype(np.uint64)
+    words = np.zeros((B, TW, K), dtype=np.uint64)
+    for i in range(32):
+        words |= yy[i::32].transpose(1, 0, 2) << np.uint64(i)
+    return torch.from_numpy(words.astype(np.uint32).view(np.int32))
+
+
+CASES = [
+    # T, B, K, M, bias, firing rate
+    (64, 3, 64, 128, False, 0.05),
+    (70, 5, 300, 130, True, 0.1),
+    (200, 2, 33, 7, True, 0.5),
+    (129, 4, 2048, 256, False, 0.03),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', CASES, ids=[f'T{c[0]}B{c[1]}K{c[2]}M{c[3]}{"b" if c[4] else ""}' for c in CASES])
+def test_spike_linear_matches_linear(dev, case):
+    from delrec.spike_linear import SpikeLinear, attach_bits
+    T, B, K, M, bias, rate = case
+    print(f'case {case}', flush=True)
+    g = gen(11)
+    y = (torch.rand(T, B, K, generator=g) < rate).float()
+    lin = SpikeLinear(K, M, bias=bias)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(M, K, generator=g) / K ** 0.5)
+        if bias:
+            lin.bias.copy_(torch.randn(M, generator=g))
+    ref = torch.nn.functional.linear(y.double(), lin.weight.double(), None if not bias else lin.bias.double())
+    lin = lin.to(dev)
+    yg = attach_bits(y.to(dev), pack_bits(y).to(dev))
+    xg = yg.clone().requires_grad_(True)
+    xg._delrec_bits = yg._delrec_bits
+    out = lin(xg)
+    assert out.grad_fn is not None and 'SpikeLinear' in type(out.grad_fn).__name__, 'the HIP path was not taken'
+    gout = torch.randn(T, B, M, generator=g)
+    out.backward(gout.to(dev))
+    torch.cuda.synchronize()
+    scale = float(ref.abs().max())
+    torch.testing.assert_close(out.detach().cpu().double(), ref, rtol=1e-5, atol=1e-6 * max(scale, 1.0))
+    # the backward is the plain GEMM pair: against float64 autograd of the same linear
+    xr = y.double().requires_grad_(True)
+    wr = lin.weight.detach().cpu().double().requires_grad_(True)
+    torch.nn.functional.linear(xr, wr).backward(gout.double())
+    torch.testing.assert_close(xg.grad.cpu().double(), xr.grad, rtol=1e-4, atol=1e-5 * float(xr.grad.abs().max()))
+    torch.testing.assert_close(lin.weight.grad.cpu().double(), wr.grad, rtol=1e-4, atol=1e-5 * float(wr.grad.abs().max()))
+
+
+@pytest.mark.gpu
+def test_recurrent_layer_output_feeds_the_spike_gemm(dev):
+    """A hybrid layer's output carries its spike bits; the Linear after it reads them and
+    matches the fp32 GEMM on the same spikes."""
+    import bench
+    w = bench.WORKLOADS['C3']
+    m = bench.build(w, dev, T=40, B=8)
+    from delrec.spike_linear import SpikeLinear
+    with torch.no_grad():
+        y = m.layers[0](m.x)
+    bits = getattr(y, '_delrec_bits', None)
+    assert bits is not None and tuple(bits.shape) == (8, 2, w['N'])
+    lin = SpikeLinear(w['N'], 96, bias=True).to(dev)
+    with torch.no_grad():
+        out = lin(y)
+        ref = torch.nn.functional.linear(y.double(), lin.weight.double(), lin.bias.double())
+    torch.cuda.synchronize()
+    assert float(y.mean()) > 0
+    torch.testing.assert_close(out.double(), ref, rtol=1e-5, atol=1e-6 * max(float(ref.abs().max()), 1.0))
