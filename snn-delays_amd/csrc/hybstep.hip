@@ -25,8 +25,8 @@
 // columns only, "far" ones (lof_j >= P) get G_j(tau) for the P steps tau = t0 + 1 .. t0 + P of a
 // block from one product at the block's start t0 whose rows are (b, tau) -- every one of
 // those G is first read at a step <= t0, and the history it reads (gr(t0 + 1 ..)) is complete.
-// For C5 (lof_j = floor(base_j) + 1, base U[0, 60], P = 8) the per-step product shrinks to the
-// 12 % of near columns and the rest runs as 4096-row products. Both write a ring of G_j(tau)
+// For C5 (lof_j = floor(base_j) + 1, base U[0, 60], P = 4) the per-step product shrinks to the
+// 5 % of near columns and the rest runs as 2048-row products. Both write a ring of G_j(tau)
 // in a [slot][j][b] layout (b fastest, whole 256-byte rows through an LDS transpose); the
 // per-step LIF reads G_j(t + lof_j + f) from it.
 //
@@ -597,6 +597,10 @@ bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t 
 
 // ---------------------------------------------------------------------------------------
 
+// steps per block of the backward's far product: C5 measured 90 ms per scan at 4, 94 at 8,
+// 104 at 6, 114 at 16, 123 at 3
+constexpr int kHybBlock = 4;
+
 HybStepDims hybstep_dims(int T, int B, int N, int L, int D, int KF, int cus) {
     HybStepDims q{};
     q.Nk = (N + 31) / 32 * 32;
@@ -606,7 +610,7 @@ HybStepDims hybstep_dims(int T, int B, int N, int L, int D, int KF, int cus) {
     q.R = std::max(L, 2);
     q.HW = (std::max(L - 1, 1) + 63) / 64;
     q.Kt = D * q.Nk;
-    q.P = lagstep_block();
+    q.P = kHybBlock;
     q.lda = (size_t)(T + D + q.P + 1) * q.Nk;   // slices past the last step read as 0 (the far
                                                 // product of the first block reaches T + P + D - 2)
     q.plane = (size_t)(q.Kt / 8) * q.Np;

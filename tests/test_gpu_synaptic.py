@@ -213,14 +213,14 @@ def test_hybrid_gather_path_matches_oracle(dev, monkeypatch):
 # the offset-stacked hybrid scans (taken by default where the rings do not fit LDS, as at
 # N = 2048) forced at small sizes: bases >= s - 1 (every tap at a lag >= 1), offsets up to 8,
 # fp32 and bf16 weights, one and two spike-history words (windows of 65+ lags), a triangle of
-# three taps (sigma 0.5); the backward's split of the sources by first lag (near: lof < 8,
+# three taps (sigma 0.5); the backward's split of the sources by first lag (near: lof < 4,
 # per-step product; far: per-block product) with both parts, only far sources (bases >= 10)
-# and only near ones (bases < 5), runs of T not a multiple of the block
+# and only near ones (bases < 2.5), runs of T not a multiple of the block
 HYBSTEP_CASES = [HYB_CASES[i] for i in (0, 2, 5, 6)] + [
     (20, 2, 64, (1.0, 12.0), 4, False, 0.5),
     (33, 3, 130, (0.0, 25.0), 2, True, 0.0),
     (21, 2, 96, (10.0, 20.0), 3, False, 0.0),
-    (19, 3, 80, (0.0, 5.0), 3, True, 0.0),
+    (19, 3, 80, (0.0, 2.5), 3, True, 0.0),
 ]
 
 
