@@ -84,3 +84,21 @@ def oracle_synaptic(x, W, d, lif, sigma, gy, bias=None, p=None, use_sig_p=False,
                                round_delays=round_delays)
     (y * gy).sum().backward()
     return y.detach(), ext['u'].detach(), {k: v.grad for k, v in leaves.items()}
+
+
+class OracleModel(torch.nn.Module):
+    """An ``SNN_*`` model evaluated by the oracle (``oracle.model.reference_forward``) on
+    its own parameters, so a training harness can step it like the HIP model: the
+    optimiser sees the wrapped model's parameters, ``clamp_delays`` reaches them, and the
+    input is cast to the parameters' dtype (float64 runs)."""
+
+    def __init__(self, inner):
+        super().__init__()
+        self.inner = inner
+
+    def forward(self, x):
+        from oracle.model import reference_forward
+        return reference_forward(self.inner, x.to(next(self.inner.parameters()).dtype))
+
+    def clamp_delays(self):
+        self.inner.clamp_delays()

@@ -185,6 +185,42 @@ def test_sigma_schedule_clamp_and_round():
     assert layer.recurrent_delays[:3].tolist() == [0.0, 2.0, 3.0]
 
 
+def _round_up_share(model, layer, d, reps):
+    """Fraction of stochastic roundings of ``d`` that went up, over ``reps`` calls."""
+    ups, total = 0, 0
+    for _ in range(reps):
+        with torch.no_grad():
+            layer.recurrent_delays.copy_(d)
+        model.round_pos()
+        r = layer.recurrent_delays.detach()
+        assert torch.all((r == torch.floor(d)) | (r == torch.ceil(d)))
+        ups += int((r > d).sum())
+        total += r.numel()
+    return ups / total
+
+
+def test_stochastic_round_pos():
+    """``round_mode = 'stochastic'``: ``floor(d + U[0, 1))``, so a delay goes up with
+    probability frac(d), integers stay, negative ones clamp to 0 (reference
+    ``networks.py:183-199``)."""
+    from delrec import networks
+    from delrec.delay_layers import axonal_recdel
+    cfg = base_config(0)
+    cfg.round_mode = 'stochastic'
+    torch.manual_seed(0)
+    model = networks.SNN_axonal_recurrent_delays(cfg)
+    layer = [m for m in model.layers if isinstance(m, axonal_recdel)][0]
+    n = layer.recurrent_delays.numel()
+    d = torch.full((n,), 3.25)
+    share = _round_up_share(model, layer, d, 400)        # 6400 draws: sd 0.0054
+    assert abs(share - 0.25) < 0.025, share
+    with torch.no_grad():
+        layer.recurrent_delays.copy_(torch.linspace(-2.0, 5.0, n).round())
+    ints = layer.recurrent_delays.detach().clone()
+    model.round_pos()
+    assert torch.equal(layer.recurrent_delays.detach(), ints.clamp(min=0))
+
+
 def test_common_recdel_has_one_shared_delay():
     from delrec import networks
     cfg = base_config(0)

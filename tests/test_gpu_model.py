@@ -79,3 +79,63 @@ def test_model_forward_backward_matches_oracle(dev, name, sigma):
         torch.testing.assert_close(g[n], g_ref[n], atol=GRAD_ATOL, rtol=GRAD_RTOL, msg=lambda m: f'{n}: {m}')
         worst = max(worst, (g[n] - g_ref[n]).abs().max().item() / (g_ref[n].abs().max().item() + 1e-12))
     print(f'  OK, max relative gradient difference {worst:.2e} over {len(g)} parameters')
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('name', MODELS[:3])
+def test_delay_maintenance_on_device(dev, name):
+    """The delay-parameter maintenance of a training loop run on device tensors (reference
+    ``networks.py:183-199,910-933``, ``delay_layers.py:178-189``): clamp, the epoch's
+    spread, nearest rounding give on the GPU what they give on the CPU; stochastic rounding
+    lands on the floor or the ceiling; the model then still matches the oracle."""
+    from delrec import networks
+    from delrec.delay_layers import axonal_recdel
+    from delrec.networks import learned_delay_parameter
+    from delrec.training.mem import set_epoch
+    from delrec.utils import reset_states
+    from oracle.model import reference_forward
+    print(f'delay maintenance {name}', flush=True)
+    cfg = _config(sigma=1.0)
+    cfg.epochs = 20
+    torch.manual_seed(0)
+    model = getattr(networks, name)(cfg)
+    model.eval()
+    layer = [m for m in model.layers if isinstance(m, axonal_recdel)][0]
+    leaf = learned_delay_parameter(layer, 'recurrent_delays')
+    with torch.no_grad():     # off the grid, a few below 0
+        leaf.add_(torch.rand(leaf.shape, generator=gen(5)) * 3.0 - 1.0)
+    ref, hip = copy.deepcopy(model), copy.deepcopy(model).to(dev)
+    for m in (ref, hip):
+        m.clamp_delays()
+        set_epoch(m, cfg, 7)
+    lay = lambda m: [x for x in m.layers if isinstance(x, axonal_recdel)][0]
+    assert lay(hip).sigma == lay(ref).sigma == pytest.approx(cfg.sigma_init * cfg.sigma_decay ** (100 / 20 * 7))
+    l_ref, l_hip = learned_delay_parameter(lay(ref), 'recurrent_delays'), learned_delay_parameter(lay(hip), 'recurrent_delays')
+    assert l_hip.is_cuda and torch.equal(l_hip.detach().cpu(), l_ref.detach()) and float(l_ref.min()) >= 0.0
+    # stochastic rounding on device: every delay on its floor or ceiling
+    before = l_hip.detach().clone()
+    hip.config.round_mode = 'stochastic'
+    hip.round_pos()
+    after = l_hip.detach()
+    assert torch.all((after == before.floor()) | (after == before.ceil()))
+    # nearest rounding: the same on both devices
+    with torch.no_grad():
+        l_hip.copy_(before)
+    hip.config.round_mode = 'nearest'
+    for m in (ref, hip):
+        m.round_pos()
+    assert torch.equal(l_hip.detach().cpu(), l_ref.detach())
+    # the maintained model against the oracle, one forward + backward
+    x = torch.randn(T, B, cfg.input_size, generator=gen(7))
+    reset_states(ref)
+    y_ref = reference_forward(ref, x.clone())
+    y_ref.pow(2).mean().backward()
+    reset_states(hip)
+    y = hip(x.to(dev))
+    y.pow(2).mean().backward()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(y.detach().cpu(), y_ref.detach(), atol=FWD_ATOL, rtol=FWD_RTOL)
+    g, g_ref = _grads(hip), _grads(ref)
+    assert set(g) == set(g_ref)
+    for n in sorted(g_ref):
+        torch.testing.assert_close(g[n], g_ref[n], atol=GRAD_ATOL, rtol=GRAD_RTOL, msg=lambda m: f'{n}: {m}')
