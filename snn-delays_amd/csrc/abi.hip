@@ -1325,8 +1325,13 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     p.ldsf = (int)(lds_hx / sizeof(float));
     p.offq = hybrid ? offq : nullptr;
     p.order = hyb_fast ? order : nullptr;
-    // (no fallback from the hybrid kernel: its operands are in first-lag order)
-    const bool ok = hyb_fast ? launch_syn_bwd_hyb(p, lay.block, lds_hx, s) : launch_syn_bwd(p, lay.block, lay.lds, s);
+    // (no fallback from the hybrid kernels: their operands are in first-lag order). Where every
+    // lag is >= 1 and the offsets span at most 12 steps, the offset-stacked form (one MAC per
+    // connection; DELREC_SYN_BWD_HYB_G=0 keeps the per-tap gather)
+    const bool hyb_g = hyb_fast && a->d_min >= a->s_uniform - 1.0f && a->off_count > 0 &&
+                       getenv_flag_off("DELREC_SYN_BWD_HYB_G") &&
+                       launch_syn_bwd_hyb_g(p, a->off_count, (size_t)max_lds_bytes(), s);
+    const bool ok = hyb_g || (hyb_fast ? launch_syn_bwd_hyb(p, lay.block, lds_hx, s) : launch_syn_bwd(p, lay.block, lay.lds, s));
     scan_end(timed && ok, s);
     if (!ok) return DELREC_ERR_UNSUPPORTED;
     int st = finish_launch();

@@ -383,6 +383,10 @@ void launch_pack_offq(const int8_t* offt, size_t n, const int* meta, uint8_t* of
 // (one workgroup; N <= 1024)
 void launch_sort_by_first_lag(const float* base, float s, int N, int* order, hipStream_t stream);
 bool launch_syn_bwd_hyb(const SynBwd& a, int block, size_t lds, hipStream_t stream);
+// the offset-stacked form of the hybrid backward (every lag >= 1, D offsets, N <= 512); false
+// when it does not apply (the caller then takes launch_syn_bwd_hyb)
+bool launch_syn_bwd_hyb_g(const SynBwd& a, int D, size_t max_lds, hipStream_t stream);
+size_t syn_bwd_hyb_g_lds(int N, int L, int D, int* gs);
 // each column's lag range (lo, rc, om) and meta[0..1]
 void launch_lag_cols(const LagBf16& a, hipStream_t stream);
 // packs gr / spikes, then the lag GEMM into a.pw / a.pd / a.ps

@@ -1106,6 +1106,189 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
     if (writer) p.part[(size_t)b * N + j] = dbacc;
 }
 
+// The same hybrid backward in the offset-stacked form, one MAC per connection. With
+// e_ij = off_ij - omin and c_j = lob_j + omin (>= 1: the host takes this form only when every
+// lag is >= 1),
+//   gfut_j(t) = is2 * sum_f hq_j[f] * G_j(t + c_j + f),   G_j(tau) = sum_i W[i,j] gr_i(tau + e_ij).
+// Step t forms G_j(t + 1) (gr(t + 1 .. t + D) are all known) into a per-source history of
+// RG = L slots and reads the older G_j(t + c_j + f) back from it; c_j + f = 1 is this step's own
+// G. The gr ring then spans only the D steps t + 1 .. t + D: Dg = D + 1 slots per receiver row
+// (gr(t) goes to the slot no read of step t touches), each value stored twice, at slots s and
+// s + Dg, so a step's run starts at the same slot b0 = (t + 1) mod Dg in every lane and a
+// connection reads slot b0 + e_ij with no wrap. The lanes of a wave read one receiver row
+// within D consecutive slots (a broadcast over distinct banks); a connection costs the W
+// decode, one address add (the offset byte, held as e * 4) and one FMA, the row within a
+// chunk being an immediate offset (the row pitch GS >= 2 D is a compile-time constant).
+// Two lanes per source (l and l + 32 of a wave), each over half the receivers.
+// LDS: rows * GS floats of ring, then RG x (blockDim / 2) floats of G history.
+template <int KT, bool WBF, int GS>
+__global__ void __launch_bounds__(1024) syn_bwd_hyb_g(SynBwd p) {
+    extern __shared__ float smem[];
+    const int N = p.N, T = p.T, B = p.B;
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const int half = (tid >> 5) & 1;
+    const int jloc = (tid >> 6) * 32 + (tid & 31);
+    const bool act = jloc < N;
+    const bool writer = act && half == 0;                 // the lane that stores for source j
+    const int j = act ? (p.order ? p.order[jloc] : jloc) : 0;
+    const Lif k = p.lif;
+    const float m = p.drop ? p.drop[(size_t)b * N + j] : 1.0f;
+    const float sv = p.s_uniform;
+    const float is2 = 1.0f / (sv * sv);
+    const float cj = 1.0f + p.base[j];
+    int lob = (int)ceilf(cj - sv);
+    if (fabsf((float)(lob - 1) - cj) <= sv) lob -= 1;
+    if (fabsf((float)lob - cj) > sv) lob += 1;
+    float hq[KT];
+#pragma unroll
+    for (int f = 0; f < KT; ++f) hq[f] = fmaxf(sv - fabsf((float)(lob + f) - cj), 0.0f);
+    const int omin = p.meta[1];
+    const int D = p.meta[2] - omin + 1;
+    const int Dg = D + 1;
+    const int c0 = lob + omin;                            // tau - t of tap 0
+    const int NC0 = (N + 15) >> 4;
+    const int NC = (NC0 + 1) / 2;                         // chunks of 16 receivers per lane
+    const int rows = 2 * NC * 16;
+    const int NL = (int)blockDim.x / 2;                   // G-history pitch (lane slots)
+    const int RG = p.L;
+    float* ring = smem;                                   // [rows][GS]
+    float* ghist = smem + (size_t)rows * GS;              // [RG][NL]
+    // the offsets' span must fit the ring pitch (the host sized GS from the caller's
+    // off_count): a wider one makes every output NaN instead of reading other rows
+    const bool bad = 2 * D > GS || RG < 2;
+    for (int q = tid; q < rows * GS + RG * NL; q += blockDim.x) smem[q] = 0.0f;
+    __syncthreads();
+
+    const uint32_t wbytes = (uint32_t)((size_t)p.NT * N * (WBF ? 2 : 4));
+    const uint32_t obytes = (uint32_t)((size_t)p.NT * N);
+    const i32x4 rw = buffer_rsrc(p.Wt, wbytes), ro = buffer_rsrc(p.offq, obytes);
+    const int wcs = N * 16 * (WBF ? 2 : 4), ocs = N * 16;   // bytes per chunk
+    const int cbase = half * NC;                          // the lane's first chunk
+    const int wj = act ? jloc * 16 * (WBF ? 2 : 4) + cbase * wcs : kOutOfRange;
+    const int oj = act ? jloc * 16 + cbase * ocs : kOutOfRange;
+    constexpr int WV = WBF ? 2 : 4;                       // uint4 of W per chunk
+    struct Chunk { uint4 w[WV]; uint4 o; };
+    auto fetch = [&](int cidx, Chunk& ch) {
+        const int cw = cidx * wcs, co = cidx * ocs;
+#pragma unroll
+        for (int h = 0; h < WV; ++h) {
+            const i32x4 v = raw_buffer_load_i32x4(rw, wj + cw + 16 * h, 0, 0);
+            ch.w[h] = make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+        }
+        const i32x4 ov = raw_buffer_load_i32x4(ro, oj + co, 0, 0);
+        ch.o = make_uint4((uint32_t)ov.x, (uint32_t)ov.y, (uint32_t)ov.z, (uint32_t)ov.w);
+    };
+    const size_t BN = (size_t)B * N;
+    const uint32_t row_bytes = (uint32_t)BN * 4u;
+    const uint64_t step_b = (uint64_t)row_bytes;
+    const int voff = (b * N + j) * 4;
+    const int soff = writer ? voff : kOutOfRange;
+
+    float gq[kPrefetchSynBwd], uq[kPrefetchSynBwd];
+    const int tp0 = T - 1 - kPrefetchSynBwd;
+    uint64_t gya = (uint64_t)p.gy + (uint64_t)max(tp0, 0) * step_b, uau = (uint64_t)p.u + (uint64_t)max(tp0, 0) * step_b;
+    uint64_t dxa = (uint64_t)p.dx + (uint64_t)(T - 1) * step_b, gra = (uint64_t)p.gr + (uint64_t)(T - 1) * step_b;
+#pragma unroll
+    for (int q = 0; q < kPrefetchSynBwd; ++q) {
+        const int tt = T - 1 - q;
+        const uint32_t nb = tt >= 0 ? row_bytes : 0u;
+        gq[q] = raw_buffer_load_f32(step_rsrc((uint64_t)p.gy + (uint64_t)max(tt, 0) * step_b, nb), voff, 0, 0);
+        uq[q] = raw_buffer_load_f32(step_rsrc((uint64_t)p.u + (uint64_t)max(tt, 0) * step_b, nb), voff, 0, 0);
+    }
+    float lam = 0.0f, dbacc = 0.0f;
+    int b0 = T % Dg;                                      // (t + 1) mod Dg
+    int g1 = T % RG;                                      // (t + 1) mod RG
+    float* const own = ring + (size_t)(act ? j : 0) * GS; // this source's row as a receiver
+    float* const gown = ghist + jloc;
+
+    auto gather = [&](const Chunk& ch, int cidx, float acc) {
+        // the chunk's 16 receiver rows from slot b0: row e at the immediate offset e * GS
+        const char* rowc = reinterpret_cast<const char*>(ring + (size_t)(cbase + cidx) * 16 * GS + b0);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t ow = (e < 4) ? ch.o.x : (e < 8) ? ch.o.y : (e < 12) ? ch.o.z : ch.o.w;
+            const uint32_t sl4 = (ow >> (8 * (e & 3))) & 0xFFu;
+            const float gv = *reinterpret_cast<const float*>(rowc + sl4 + e * GS * 4);
+            float wv;
+            if constexpr (WBF) {
+                const uint4& wq = ch.w[e >> 3];
+                const int e8 = e & 7;
+                const uint32_t w2 = (e8 < 2) ? wq.x : (e8 < 4) ? wq.y : (e8 < 6) ? wq.z : wq.w;
+                wv = __uint_as_float((e & 1) ? (w2 & 0xFFFF0000u) : (w2 << 16));
+            } else {
+                const uint4& wq = ch.w[e >> 2];
+                const int e4 = e & 3;
+                wv = __uint_as_float(e4 == 0 ? wq.x : e4 == 1 ? wq.y : e4 == 2 ? wq.z : wq.w);
+            }
+            acc = fmaf(wv, gv, acc);
+        }
+        return acc;
+    };
+
+    auto step = [&](const int t, float& gs, float& us) {
+        float acc = 0.0f;
+        Chunk ca, cb;
+        fetch(0, ca);
+        for (int c = 0; c < NC; c += 2) {
+            fetch(c + 1, cb);
+            acc = gather(ca, c, acc);
+            if (c + 1 < NC) {
+                fetch(c + 2, ca);
+                acc = gather(cb, c + 1, acc);
+            }
+        }
+        const float G = acc + __shfl_xor(acc, 32);        // G_j(t + 1)
+        if (writer) gown[(size_t)g1 * NL] = G;
+        float gf = 0.0f;
+#pragma unroll
+        for (int f = 0; f < KT; ++f) {
+            // tau - t = c0 + f; a tap of weight 0 outside lags 1 .. L - 1 reads some slot in
+            // range, which it weighs by 0
+            const int dd = min(max(c0 + f, 1), RG);
+            int sl = g1 + dd - 1;
+            sl = sl >= RG ? sl - RG : sl;
+            const float gv = dd == 1 ? G : (t + dd < T ? gown[(size_t)sl * NL] : 0.0f);
+            gf = fmaf(hq[f], gv, gf);
+        }
+        gf *= is2;
+        const float gyv = gs, u = us;
+        const float y = lif_fire(k, u);
+        const float du = lif_backward(k, gyv + gf, u, y, lam);
+        lam = k.decay * du;
+        const float da = bad ? __builtin_nanf("") : lif_dx(k, du);
+        const float gr = da * m;
+        const bool live = t >= 0;
+        raw_buffer_store_f32(da, step_rsrc(dxa, live ? row_bytes : 0u), soff, 0, 0);
+        raw_buffer_store_f32(gr, step_rsrc(gra, live ? row_bytes : 0u), soff, 0, 0);
+        dxa -= step_b;
+        gra -= step_b;
+        dbacc += (live && act) ? gr : 0.0f;
+        // gr(t) into slot t mod Dg (no read of this step touches it) and its mirror
+        const int sw = b0 == 0 ? Dg - 1 : b0 - 1;
+        if (writer && live && !bad) {
+            own[sw] = gr;
+            if (sw + Dg < 2 * D) own[sw + Dg] = gr;
+        }
+        const int tp = t - kPrefetchSynBwd;
+        const uint32_t nb = tp >= 0 ? row_bytes : 0u;
+        gs = raw_buffer_load_f32(step_rsrc(gya, nb), voff, 0, 0);
+        us = raw_buffer_load_f32(step_rsrc(uau, nb), voff, 0, 0);
+        if (tp > 0) {
+            gya -= step_b;
+            uau -= step_b;
+        }
+        barrier_lds();
+        b0 = sw;
+        g1 = g1 == 0 ? RG - 1 : g1 - 1;
+    };
+
+    for (int t0 = T - 1; t0 >= 0; t0 -= kPrefetchSynBwd) {
+#pragma unroll
+        for (int q = 0; q < kPrefetchSynBwd; ++q) step(t0 - q, gq[q], uq[q]);
+    }
+    if (writer) p.part[(size_t)b * N + j] = dbacc;
+}
+
 __global__ void pack_offq_kernel(const int8_t* __restrict__ offt, size_t n, const int* __restrict__ meta,
                                  uint8_t* __restrict__ offq) {
     const int omin = meta[1];
@@ -1157,6 +1340,36 @@ void launch_pack_offq(const int8_t* offt, size_t n, const int* meta, uint8_t* of
         }                                                                                    \
         return true;                                                                         \
     }
+
+// LDS of syn_bwd_hyb_g for a ring pitch gs, or 0 when no compiled pitch holds 2 D slots
+size_t syn_bwd_hyb_g_lds(int N, int L, int D, int* gs) {
+    const int g = 2 * D <= 16 ? 16 : 2 * D <= 24 ? 24 : 0;
+    *gs = g;
+    if (!g || N > 512 || L < 2) return 0;
+    const int NC = ((N + 15) / 16 + 1) / 2;
+    const int block = 2 * ((N + 31) / 32 * 32);
+    return ((size_t)2 * NC * 16 * g + (size_t)L * (block / 2)) * sizeof(float);
+}
+
+#define DELREC_SBHG_CASE(KTV, WBFV, GSV)                                                    \
+    if (kt == KTV && wbf == WBFV && gs == GSV) {                                             \
+        ensure_lds((const void*)syn_bwd_hyb_g<KTV, WBFV, GSV>, lds);                         \
+        hipLaunchKernelGGL((syn_bwd_hyb_g<KTV, WBFV, GSV>), dim3(a.B), dim3(block), lds, stream, a); \
+        return true;                                                                         \
+    }
+
+bool launch_syn_bwd_hyb_g(const SynBwd& a, int D, size_t max_lds, hipStream_t stream) {
+    int gs = 0;
+    const size_t lds = syn_bwd_hyb_g_lds(a.N, a.L, D, &gs);
+    if (!lds || lds > max_lds || !a.offq || !a.meta) return false;
+    const int block = 2 * ((a.N + 31) / 32 * 32);
+    const int kt = a.KT;
+    const bool wbf = a.w_bf16 != 0;
+    DELREC_SBHG_CASE(2, true, 16) DELREC_SBHG_CASE(2, true, 24) DELREC_SBHG_CASE(2, false, 16)
+    DELREC_SBHG_CASE(2, false, 24) DELREC_SBHG_CASE(4, true, 16) DELREC_SBHG_CASE(4, true, 24)
+    DELREC_SBHG_CASE(4, false, 16) DELREC_SBHG_CASE(4, false, 24)
+    return false;
+}
 
 // blocks of up to 512 threads (two waves per SIMD, 256 VGPRs: the operand groups stay in
 // registers); larger blocks take syn_bwd_kernel

@@ -270,6 +270,36 @@ def test_hybrid_per_connection_forward_matches_oracle(dev, idx, monkeypatch):
                          ids=[f'T{c[0]}B{c[1]}N{c[2]}' for c in [HYB_CASES[i] for i in (0, 2, 3, 6)]])
 def test_hybrid_unsplit_backward_matches_oracle(dev, case, monkeypatch):
     monkeypatch.setenv('DELREC_SYN_BWD_SPLIT', '0')
+    monkeypatch.setenv('DELREC_SYN_BWD_HYB_G', '0')
+    test_hybrid_fwd_bwd_matches_oracle(dev, case)
+
+
+# the split hybrid backward in its per-tap gather form, on the cases the offset-stacked form
+# takes by default (every lag >= 1, at most 12 offsets)
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', [HYB_CASES[i] for i in (0, 2, 6)],
+                         ids=[f'T{c[0]}B{c[1]}N{c[2]}' for c in [HYB_CASES[i] for i in (0, 2, 6)]])
+def test_hybrid_tap_gather_backward_matches_oracle(dev, case, monkeypatch):
+    monkeypatch.setenv('DELREC_SYN_BWD_HYB_G', '0')
+    test_hybrid_fwd_bwd_matches_oracle(dev, case)
+
+
+# the offset-stacked hybrid backward (G_j(t + 1) per step, a G history per source; taken by
+# default where every lag is >= 1 and the offsets span at most 12): four taps at half-widths
+# 1.5 and 2 (fp32 and bf16 W), offsets spanning 6 and 12 steps (ring pitches 16 and 24), an odd
+# chunk count, bases from 0 (a zero-weight tap at lag 0); HYB_CASES 0, 2 and 6 take it too
+HYB_G_CASES = [
+    (20, 3, 64, (1.0, 12.0), 4, False, 0.5),
+    (24, 2, 96, (1.0, 6.0), 4, True, 1.0),
+    (30, 2, 80, (0.0, 14.0), 11, True, 0.0),
+    (18, 3, 200, (0.0, 9.0), 5, False, 0.0),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', HYB_G_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}s{c[6]}' for c in HYB_G_CASES])
+def test_hybrid_offset_stacked_backward_matches_oracle(dev, case, monkeypatch):
+    monkeypatch.setenv('DELREC_HYB_FWD', '0')
     test_hybrid_fwd_bwd_matches_oracle(dev, case)
 
 
