@@ -165,10 +165,14 @@ def test_hybrid_fwd_bwd_matches_oracle(dev, case):
     import delrec.kernels.synaptic_hybrid as sh
     T, B, N, (lo, hi), K, bf16, sigma = case[:7]
     k0 = case[7] if len(case) > 7 else 0     # smallest offset (offsets uniform in k0 .. K)
+    wide = len(case) > 8 and case[8]         # weights over a wide range of magnitudes
     print(f'case {case}', flush=True)
     g = gen(2)
     x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
     W = torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)
+    if wide:   # columns scaled by 2^-20 .. 2^4, entries within a column by 2^-12 .. 1
+        W = W * torch.exp2(torch.randint(-20, 5, (1, N), generator=g).float()) \
+              * torch.exp2(torch.randint(-12, 1, (N, N), generator=g).float())
     if bf16:
         W = W.bfloat16().float()
     base = lo + torch.rand(N, generator=g) * (hi - lo)
@@ -287,17 +291,20 @@ def test_hybrid_tap_gather_backward_matches_oracle(dev, case, monkeypatch):
 # the offset-stacked hybrid backward (G_j(t + 1) per step, a G history per source; taken by
 # default where every lag is >= 1 and the offsets span at most 12): four taps at half-widths
 # 1.5 and 2 (fp32 and bf16 W), offsets spanning 6 and 12 steps (ring pitches 16 and 24), an odd
-# chunk count, bases from 0 (a zero-weight tap at lag 0); HYB_CASES 0, 2 and 6 take it too
+# chunk count, bases from 0 (a zero-weight tap at lag 0), bf16 weights spread over 2^-32 .. 2^4;
+# HYB_CASES 0, 2 and 6 take it too
 HYB_G_CASES = [
     (20, 3, 64, (1.0, 12.0), 4, False, 0.5),
     (24, 2, 96, (1.0, 6.0), 4, True, 1.0),
     (30, 2, 80, (0.0, 14.0), 11, True, 0.0),
     (18, 3, 200, (0.0, 9.0), 5, False, 0.0),
+    (20, 2, 128, (0.0, 10.0), 6, True, 0.0, 0, True),
 ]
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('case', HYB_G_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}s{c[6]}' for c in HYB_G_CASES])
+@pytest.mark.parametrize('case', HYB_G_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}s{c[6]}{"w" if len(c) > 8 else ""}'
+                                                   for c in HYB_G_CASES])
 def test_hybrid_offset_stacked_backward_matches_oracle(dev, case, monkeypatch):
     monkeypatch.setenv('DELREC_HYB_FWD', '0')
     test_hybrid_fwd_bwd_matches_oracle(dev, case)
