@@ -198,7 +198,49 @@ __global__ void __launch_bounds__(256) hyb_bwd_lif_kernel(HybBwd p) {
     const int t = p.t, N = p.N, B = p.B, T = p.T, R = p.R;
     const int lo = p.ntile[blockIdx.x], nn = p.ntile[blockIdx.x + 1] - lo;
     if (tid < JT) ncl[tid] = -1;
-    __syncthreads();
+    // loads that do not wait for this step's G, issued first so that their latency overlaps
+    // phases 1 and 2: the LIF operands of phase 3 and the ring reads of phase 2
+    const int jl3 = lane & (JT - 1), j3 = j0 + jl3;
+    const int r0 = 2 * w + (lane >> 5);
+    const size_t BN = (size_t)B * N;
+    const bool last = t == T - 1;
+    constexpr int E3 = 64 / 8;
+    float uu[E3], gyv[E3], lam[E3], dbv[E3], mv[E3];
+#pragma unroll
+    for (int e = 0; e < E3; ++e) {
+        const int b = b0 + r0 + 8 * e;
+        const bool ok = b < B && j3 < N;
+        const size_t bj = (size_t)(ok ? b : 0) * N + (ok ? j3 : 0), o = (size_t)t * BN + bj;
+        uu[e] = ok ? p.u_in[o] : 0.0f;
+        gyv[e] = ok ? p.gy[o] : 0.0f;
+        lam[e] = (ok && !last) ? p.state[bj] : 0.0f;
+        dbv[e] = (ok && !last && p.dbp) ? p.dbp[bj] : 0.0f;
+        mv[e] = (ok && p.drop) ? p.drop[bj] : 1.0f;
+    }
+    constexpr int E = JT / 4;
+    const int tm = t % R;
+    float got[E][KF], hv[E][KF];
+    int lofv[E];
+    {
+        const int b = b0 + lane;
+        const bool bok = b < B;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int j = j0 + w + 4 * e;
+            lofv[e] = j < N ? p.lof[j] : 0;
+#pragma unroll
+            for (int f = 0; f < KF; ++f) {
+                hv[e][f] = (j < N && f < p.KF) ? p.h[(size_t)f * N + j] : 0.0f;
+                const int d = lofv[e] + f;   // tau - t, in [1, L - 1]
+                int sl = tm + d;
+                sl = sl >= R ? sl - R : sl;
+                // tau >= t + 2 only: slot (t + 1) mod R, written in phase 2, is never read
+                const bool rd = j < N && f < p.KF && d >= 2 && t + d < T && bok;
+                got[e][f] = rd ? p.ring[((size_t)sl * N + j) * B + b] : 0.0f;
+            }
+        }
+    }
+    barrier_lds();   // LDS only: the loads above stay in flight
     // phase 1: one near column per wave at a time, its 64 batch rows on the lanes (the
     // partials are column-major: 256 contiguous bytes per partial)
     {
@@ -222,33 +264,16 @@ __global__ void __launch_bounds__(256) hyb_bwd_lif_kernel(HybBwd p) {
             if (lane == 0) ncl[p.perm[lo + cl] - j0] = cl;
         }
     }
-    __syncthreads();
+    barrier_lds();
     // phase 2
     {
         const int b = b0 + lane;
         const bool bok = b < B;
-        const int tm = t % R;
         const int s1 = tm + 1 == R ? 0 : tm + 1;
-        constexpr int E = JT / 4;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const int cl = w + 4 * e;
             if (cl < nn && t + 1 < T && bok) p.ring[((size_t)s1 * N + p.perm[lo + cl]) * B + b] = sg[cl][lane];
-        }
-        float got[E][KF];
-        int lofv[E];
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int j = j0 + w + 4 * e;
-            lofv[e] = j < N ? p.lof[j] : 0;
-#pragma unroll
-            for (int f = 0; f < KF; ++f) {
-                const int d = lofv[e] + f;   // tau - t, in [1, L - 1]
-                int sl = tm + d;
-                sl = sl >= R ? sl - R : sl;
-                const bool rd = j < N && f < p.KF && d >= 2 && t + d < T && bok;
-                got[e][f] = rd ? p.ring[((size_t)sl * N + j) * B + b] : 0.0f;
-            }
         }
 #pragma unroll
         for (int e = 0; e < E; ++e) {
@@ -256,40 +281,20 @@ __global__ void __launch_bounds__(256) hyb_bwd_lif_kernel(HybBwd p) {
             float gf = 0.0f;
             if (j < N) {
                 const int cl = ncl[jl];
+                const float g1 = cl >= 0 && t + 1 < T ? sg[cl][lane] : 0.0f;   // near G(t + 1)
 #pragma unroll
-                for (int f = 0; f < KF; ++f) {
-                    if (f >= p.KF) break;
-                    const float hf = p.h[(size_t)f * N + j];
-                    const float v = (lofv[e] + f == 1) ? (cl >= 0 && t + 1 < T ? sg[cl][lane] : 0.0f) : got[e][f];
-                    gf = fmaf(hf, v, gf);
-                }
+                for (int f = 0; f < KF; ++f) gf = fmaf(hv[e][f], lofv[e] + f == 1 ? g1 : got[e][f], gf);
             }
             sf[jl][lane] = gf;
         }
     }
-    __syncthreads();
-    // phase 3: column jl = lane % 32, rows 2 w + lane / 32 + 8 e
+    barrier_lds();
+    // phase 3: column jl = lane % 32, rows 2 w + lane / 32 + 8 e (operands loaded on entry)
     {
         const Lif k = p.lif;
-        const int jl = lane & (JT - 1), j = j0 + jl;
-        const int r0 = 2 * w + (lane >> 5);
-        const size_t BN = (size_t)B * N;
-        const bool last = t == T - 1;
-        constexpr int E = 64 / 8;
-        float uu[E], gyv[E], lam[E], dbv[E], mv[E];
+        const int jl = jl3, j = j3;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int b = b0 + r0 + 8 * e;
-            const bool ok = b < B && j < N;
-            const size_t bj = (size_t)(ok ? b : 0) * N + (ok ? j : 0), o = (size_t)t * BN + bj;
-            uu[e] = ok ? p.u_in[o] : 0.0f;
-            gyv[e] = ok ? p.gy[o] : 0.0f;
-            lam[e] = (ok && !last) ? p.state[bj] : 0.0f;
-            dbv[e] = (ok && !last && p.dbp) ? p.dbp[bj] : 0.0f;
-            mv[e] = (ok && p.drop) ? p.drop[bj] : 1.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
+        for (int e = 0; e < E3; ++e) {
             const int r = r0 + 8 * e, b = b0 + r;
             if (b >= B || j >= p.Nk) continue;
             const size_t ho = (size_t)b * p.lda + (size_t)t * p.Nk + j;
