@@ -175,7 +175,10 @@ typedef struct {
     const float* drop;
     delrec_lif lif;
     float* dx;                   /* out (T,B,N)                                          */
-    float* dW;                   /* out (N,N) or NULL                                    */
+    float* dW;                   /* out (N,N) or NULL. With w_bf16 the lag correlation
+                                    behind dW / dd / ds takes gr to about 2^-17 per term
+                                    (fp32 W: 2^-25), below the bf16 rounding (2^-9) that
+                                    a bf16 weight's gradient gets                        */
     float* dd;                   /* out (N,N) per-connection delay gradient, or NULL     */
     float* ds;                   /* out (N) half-width gradient, or NULL                 */
     float* db;                   /* out (N) or NULL                                      */

@@ -1122,6 +1122,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     LagBf16 g{};
     g.T = T; g.B = B; g.Bp = q.Bp; g.N = N; g.Np = q.Np; g.L = a->L; g.Kp = q.Kp; g.KS = q.KS;
     g.ahi = ahi; g.amd = amd; g.alo = alo; g.yb = yb;
+    g.planes = a->w_bf16 ? 2 : 3;   // bf16 W: dW leaves rounded to bf16, two gr planes suffice
     g.meta = meta; g.lo = meta + 64; g.rc = meta + 64 + N; g.om = meta + 64 + 2 * N; g.ox = meta + 64 + 3 * N;
     g.d = a->d; g.base = a->base; g.off = a->offsets; g.s = a->s; g.s_uniform = a->s_uniform;
     g.pw = lagp;

@@ -141,6 +141,7 @@ struct LagBf16 {
     float* pw;                   // [KS][N][N] partial sum_l h * C_l
     float* pd;                   // [KS][N][N] partial sum_l sign * C_l
     float* ps;                   // [KS][N][N] partial sum_l dh/ds * C_l, or NULL
+    int planes;                  // gr planes multiplied: 3 (hi, mid, lo), or 2 (hi, mid) for bf16 W
 };
 
 // lag-stacked per-step GEMM scans (lagstep.hip)

@@ -12,7 +12,9 @@
 // Operands are bf16. Spikes are exactly 0 or 1 in bf16. gr is split into three terms,
 // gr_hi = bf16(gr), gr_mid = bf16(gr - gr_hi), gr_lo = bf16(gr - gr_hi - gr_mid), and each
 // tile takes all three products, so a term is as accurate as gr itself in fp32 (the
-// split holds gr to about 2^-27; fp32 accumulation). The packed operands use
+// split holds gr to about 2^-27; fp32 accumulation). For bf16 W the weight gradient leaves
+// as bf16 (rounded to 2^-9) and the tiles take hi and mid only (gr to about 2^-17 per term,
+// 2^8 times finer than that rounding): a third fewer products. The packed operands use
 // a k-blocked layout, element (k, m) at ((k / 8) * Np + m) * 8 + k % 8, so one 16-byte load
 // holds the 8 consecutive k of one column that an MFMA lane supplies; a row k is
 // (t * Bp + b) with the batch padded to a multiple of 32, so a 32-row batch chunk of one
@@ -210,7 +212,7 @@ __device__ __forceinline__ bf16x8 load16(i32x4 rs, int voff) {
     return __builtin_bit_cast(bf16x8, raw_buffer_load_i32x4(rs, voff, 0, 0));
 }
 
-template <int RL, int kWY, int kWA, bool DS>
+template <int RL, int kWY, int kWA, bool DS, int NP>
 __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, int bc, int rt) {
     constexpr int P = kWY - RL;   // spike slices loaded ahead
     static_assert(kWY % kWA == 0 && P >= 1, "window slots");
@@ -266,8 +268,10 @@ __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, i
             ah[sl][1] = load16(rhi, o + 256);
             am[sl][0] = load16(rmd, o);
             am[sl][1] = load16(rmd, o + 256);
-            al[sl][0] = load16(rlo, o);
-            al[sl][1] = load16(rlo, o + 256);
+            if constexpr (NP > 2) {
+                al[sl][0] = load16(rlo, o);
+                al[sl][1] = load16(rlo, o + 256);
+            }
         }
         const int nsteps = T - q0;
         // running offsets of the next spike slice (n + P) and the next gr slice (q0 + n + kWA - 1)
@@ -283,8 +287,10 @@ __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, i
                     ah[(u + kWA - 1) % kWA][1] = load16(rhi, oa + 256);
                     am[(u + kWA - 1) % kWA][0] = load16(rmd, oa);
                     am[(u + kWA - 1) % kWA][1] = load16(rmd, oa + 256);
-                    al[(u + kWA - 1) % kWA][0] = load16(rlo, oa);
-                    al[(u + kWA - 1) % kWA][1] = load16(rlo, oa + 256);
+                    if constexpr (NP > 2) {
+                        al[(u + kWA - 1) % kWA][0] = load16(rlo, oa);
+                        al[(u + kWA - 1) % kWA][1] = load16(rlo, oa + 256);
+                    }
                     oy += slice;
                     oa += slice;
                 }
@@ -307,14 +313,16 @@ __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, i
                         for (int nb = 0; nb < 2; ++nb)
                             acc[r][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                                 am[sa][mb], yw[(u - r + kWY) % kWY][nb], acc[r][mb][nb], 0, 0, 0);
+                if constexpr (NP > 2) {
 #pragma unroll
-                for (int r = 0; r < RL; ++r)
+                    for (int r = 0; r < RL; ++r)
 #pragma unroll
-                    for (int mb = 0; mb < 2; ++mb)
+                        for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                        for (int nb = 0; nb < 2; ++nb)
-                            acc[r][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                                al[sa][mb], yw[(u - r + kWY) % kWY][nb], acc[r][mb][nb], 0, 0, 0);
+                            for (int nb = 0; nb < 2; ++nb)
+                                acc[r][mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                    al[sa][mb], yw[(u - r + kWY) % kWY][nb], acc[r][mb][nb], 0, 0, 0);
+                }
             }
         }
 
@@ -361,7 +369,7 @@ __device__ __forceinline__ void lag_win_body(const LagBf16& p, int i0, int j0, i
 // passes (the hybrid of 5 offsets and 2 taps), of at most 8 lags 8-lag passes, of at most 10
 // lags 10-lag passes, wider ones 12-lag passes; the launch of each variant skips the others'
 // tiles (each variant gets the whole register file to itself).
-template <int RL, bool DS>
+template <int RL, bool DS, int NP>
 __global__ void __launch_bounds__(256) lag_win_kernel(LagBf16 p) {
     const int nbc = p.Bp / 32;
     const int bc = (int)blockIdx.x % nbc, tile = (int)blockIdx.x / nbc;
@@ -379,7 +387,15 @@ __global__ void __launch_bounds__(256) lag_win_kernel(LagBf16 p) {
     if (RL == 12 && rt <= 10) return;
     // gr-slice registers: 3 slots (2 slices ahead) beside a 12-slot spike window (6-, 8- and
     // 10-lag passes), 4 slots (3 ahead) beside the 16-slot one (12-lag passes)
-    lag_win_body<RL, RL <= 10 ? 12 : 16, RL <= 10 ? 3 : 4, DS>(p, i0, j0, bc, rt);
+    lag_win_body<RL, RL <= 10 ? 12 : 16, RL <= 10 ? 3 : 4, DS, NP>(p, i0, j0, bc, rt);
+}
+
+template <bool DS, int NP>
+void launch_lag_win(const LagBf16& a, dim3 grid, hipStream_t stream) {
+    hipLaunchKernelGGL((lag_win_kernel<6, DS, NP>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((lag_win_kernel<8, DS, NP>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((lag_win_kernel<10, DS, NP>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((lag_win_kernel<12, DS, NP>), grid, dim3(256), 0, stream, a);
 }
 
 void launch_lag_cols(const LagBf16& a, hipStream_t stream) {
@@ -397,16 +413,10 @@ void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hi
                        a.Bp, a.N, a.Np, a.Kp, const_cast<uint4*>(a.yb));
     const int tiles = (a.Np / kWT) * (a.Np / kWT);
     const dim3 grid((unsigned)(tiles * (a.Bp / 32)));
-    if (a.ps) {
-        hipLaunchKernelGGL((lag_win_kernel<6, true>), grid, dim3(256), 0, stream, a);
-        hipLaunchKernelGGL((lag_win_kernel<8, true>), grid, dim3(256), 0, stream, a);
-        hipLaunchKernelGGL((lag_win_kernel<10, true>), grid, dim3(256), 0, stream, a);
-        hipLaunchKernelGGL((lag_win_kernel<12, true>), grid, dim3(256), 0, stream, a);
+    if (a.planes == 2) {
+        if (a.ps) launch_lag_win<true, 2>(a, grid, stream); else launch_lag_win<false, 2>(a, grid, stream);
     } else {
-        hipLaunchKernelGGL((lag_win_kernel<6, false>), grid, dim3(256), 0, stream, a);
-        hipLaunchKernelGGL((lag_win_kernel<8, false>), grid, dim3(256), 0, stream, a);
-        hipLaunchKernelGGL((lag_win_kernel<10, false>), grid, dim3(256), 0, stream, a);
-        hipLaunchKernelGGL((lag_win_kernel<12, false>), grid, dim3(256), 0, stream, a);
+        if (a.ps) launch_lag_win<true, 3>(a, grid, stream); else launch_lag_win<false, 3>(a, grid, stream);
     }
 }
 
