@@ -260,7 +260,7 @@ def peak_of(w):
 SCAN_SYMBOL = {
     'C1': {'axonal_fwd_scan': 'axonal_fwd_wave_fast', 'axonal_bwd_scan': 'axonal_bwd_tiled_fast'},
     'C2': {'axonal_fwd_scan': 'axonal_fwd_wave_fast', 'axonal_bwd_scan': 'axonal_bwd_tiled_fast'},
-    'C3': {'syn_fwd_scan': 'hyb_fwd_arrive_kernel', 'syn_bwd_scan': 'syn_bwd_hyb'},
+    'C3': {'syn_fwd_scan': 'hyb_fwd_arrive_kernel', 'syn_bwd_scan': 'syn_bwd_hyb_g'},
     'C4': {'syn_fwd_scan': 'lagstep_fwd_sequence', 'syn_bwd_scan': 'lagstep_bwd_sequence'},
     'C5': {'syn_fwd_scan': 'hyb_fwd_arrive_kernel', 'syn_bwd_scan': 'hybstep_bwd_sequence'},
 }
@@ -451,14 +451,20 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=10)
     ap.add_argument('--warmup', type=int, default=2)
-    ap.add_argument('--config', default=DEFAULT_CONFIG, choices=sorted(WORKLOADS))
-    ap.add_argument('--extra', default='C1,C2,C3,C4',
+    ap.add_argument('--config', default=None, choices=sorted(WORKLOADS),
+                    help=f'the workload of the line (default {DEFAULT_CONFIG}, with the others as extras)')
+    ap.add_argument('--extra', default=None,
                     help='comma-separated further workloads reported under "extra" (each with its own '
-                         'roofline and CPU baseline); "" for none')
+                         'roofline and CPU baseline); "" for none. Default: C1,C2,C3,C4 beside the '
+                         'default workload, none beside an explicit --config')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--calibrate-copy', type=int, metavar='MIB', default=0,
                     help='only run a plain device copy of MIB MiB (counter calibration)')
     args = ap.parse_args()
+    if args.extra is None:
+        args.extra = 'C1,C2,C3,C4' if args.config is None else ''
+    if args.config is None:
+        args.config = DEFAULT_CONFIG
     if args.gpus != 1:
         print(f'bench.py measures one GPU; --gpus {args.gpus} is not supported by this build '
               f'(the layer shards over batch rows with one dW/dd all-reduce per step, not run here)',
