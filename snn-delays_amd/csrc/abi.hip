@@ -343,7 +343,8 @@ ArriveShape syn_arrive(int N, int L, bool hybrid, bool bf16, int off_count, int 
     a.npt = N <= 1024 ? 1 : 2;
     a.block = a.npt == 1 ? (N + 63) / 64 * 64 : 1024;
     a.kf = taps <= 2 ? 2 : 4;
-    a.R = off_count + a.kf - 1;
+    a.R = 1;   // D + KF - 1 slots, rounded up to a power of two (the kernel wraps by a mask)
+    while (a.R < off_count + a.kf - 1) a.R *= 2;
     a.RP = a.R + a.kf - 1;
     a.hw = (std::max(L - 1, 1) + 63) / 64;
     // ring [RP][npt * 1024], segment counts [2][16], arrival segments [2][16][npt * 64]

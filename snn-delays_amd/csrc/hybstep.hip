@@ -371,15 +371,16 @@ __global__ void __launch_bounds__(256) hyb_bwd_far_kernel(HybBwd p) {
 // so it "arrives" at step t = tau + lof_j and its contributions then land e_ij + f steps
 // ahead: at step t the walked sources are those with y_j(t - lof_j) = 1 (bit lof_j - 1 of the
 // source's own spike-history word), and the pending recurrent input of each receiver only
-// needs a ring of R = D + KF - 1 slots (C5: 6; the per-connection scatter needs L, 67): R
-// slots plus KF - 1 mirror slots after slot R - 1, so a connection's KF taps are the slots
-// s .. s + KF - 1 from s = (t + e) mod R with no wrap; the mirror slot R + m is read and
-// cleared with slot m. The ring is slot-major, ring[slot][receiver] with a pitch of
-// NR = NPT * 1024 receivers, so the lanes of a wave always hit 64 distinct banks whatever slot
-// each connection selects, and the taps of a run are immediate offsets of one address. (C5:
-// 7 slots of 2048 receivers, 57 KB, so two rows' workgroups share a CU.) Per connection: the
-// packed word bf16(W) << 16 | (offset - smallest offset) byte (one 4-byte load), the slot,
-// and KF read-modify-writes w * h_j(lof_j + f) of the run.
+// needs a ring of D + KF - 1 slots (C5: 6; the per-connection scatter needs L, 67), rounded
+// up to a power of two R (C5: 8) so that a slot wraps by a mask: R slots plus KF - 1 mirror
+// slots after slot R - 1, so a connection's KF taps are the slots s .. s + KF - 1 from
+// s = (t + e) mod R with no wrap; the mirror slot R + m is read and cleared with slot m.
+// The ring is slot-major, ring[slot][receiver] with a pitch of NR = NPT * 1024 receivers, so
+// the lanes of a wave always hit 64 distinct banks whatever slot each connection selects, and
+// the taps of a run are immediate offsets of one address. (C5: 9 slots of 2048 receivers,
+// 74 KB, so two rows' workgroups share a CU.) Per connection: the packed word
+// bf16(W) << 16 | (offset - smallest offset) byte (one 4-byte load), the slot, and KF
+// read-modify-writes w * h_j(lof_j + f) of the run.
 //
 // Per step: every wave walks the arrival list of step t (flattened from per-wave segments,
 // sources in a fixed order) over its own receivers, 64 arrivals at a time: lane a of the
@@ -516,12 +517,12 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
                     for (int c = 0; c < NPT; ++c) {
                         const uint32_t wv = wc[e][c];
                         // the offset byte holds offset - smallest offset, in [0, D) for the
-                        // offsets the caller describes (clamped, so that no slot leaves the
-                        // ring); a lane past N reads the word 0: weight 0 into its own column
-                        const int ee = min((int)(wv & 0xFFu), p.D - 1);
+                        // offsets the caller describes; R is a power of two, so the slot wraps
+                        // by a mask (one byte-add and one AND), and a byte outside that range
+                        // still lands in the ring. A lane past N reads the word 0: weight 0
+                        // into its own column
+                        const int sl = (tm + (int)(wv & 0xFFu)) & (R - 1);
                         wf[c] = __uint_as_float(wv & 0xFFFF0000u);
-                        int sl = tm + ee;
-                        sl = sl >= R ? sl - R : sl;
                         run[c] = ring + sl * NR + idx[c];
 #pragma unroll
                         for (int q = 0; q < KF; ++q) old[c][q] = run[c][q * NR];
@@ -579,7 +580,7 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
             filled += __popcll(bal);
         }
         if (lane == 0) cnt[nsel * kArriveWaves + wave] = filled;
-        tm = tm + 1 == R ? 0 : tm + 1;
+        tm = (tm + 1) & (R - 1);
         barrier_lds();
     }
 }

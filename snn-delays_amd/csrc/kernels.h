@@ -265,7 +265,7 @@ int hyb_bwd_tile();              // sources per LIF tile (the granularity of Hyb
 void launch_hyb_bwd_far(const HybBwd& a, hipStream_t stream);
 
 struct HybScat {                 // the hybrid forward as a scatter on arrival (bf16 W)
-    int T, B, N, D, KF, R, RP, omin;   // KF: the compiled run length; R = D + KF - 1 ring slots
+    int T, B, N, D, KF, R, RP, omin;   // KF: the compiled run length; R >= D + KF - 1 ring slots, a power of two
     const float* x;
     const float* bias;
     const float* drop;
