@@ -386,8 +386,8 @@ __global__ void __launch_bounds__(256) hyb_bwd_far_kernel(HybBwd p) {
 // sources in a fixed order) over its own receivers, 64 arrivals at a time: lane a of the
 // wave holds arrival a's source and tap weights, which reach the whole wave by readlane, so
 // the only memory reads of the walk are the packed words, fetched a chunk of CH arrivals
-// ahead (CH = 32 with one neuron per lane; 4 with two, whose 1024-lane blocks must keep to 64
-// VGPRs for two workgroups per CU). A receiver's ring column is only ever written by its own lane, so the scatter needs
+// ahead into the other of two word buffers (CH = 32 with one neuron per lane, 4 with two),
+// each load taking the source row's offset in its scalar offset. A receiver's ring column is only ever written by its own lane, so the scatter needs
 // no barrier; then each lane runs the LIF of its receivers on their ring slot, shifts each
 // source's spike into its history word and appends the sources arriving at t + 1 to its
 // wave's segment of the other list buffer; one LDS barrier per step.
@@ -479,29 +479,22 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
                 for (int q = 0; q < KF; ++q) hs[q] = found ? p.h[(size_t)q * N + src] : 0.0f;
             }
             const int nf = min(64, total - base);
-            uint32_t wn[CH][NPT];
+            // the words of CH arrivals from f: the source row's offset rides in the scalar
+            // offset of the load (uniform), the lane's column in the vector offset
+            auto fetch = [&](uint32_t (&wb)[CH][NPT], int f) {
 #pragma unroll
-            for (int e = 0; e < CH; ++e) {
-                const int o = __builtin_amdgcn_readlane(src, e);
+                for (int e = 0; e < CH; ++e) {
+                    const int o = __builtin_amdgcn_readlane(src, (f + e) & 63);
 #pragma unroll
-                for (int c = 0; c < NPT; ++c)
-                    wn[e][c] = __float_as_uint(raw_buffer_load_f32(rw, wio[c] + o * N * 4, 0, 0));
-            }
-            for (int f0 = 0; f0 < nf; f0 += CH) {
-                uint32_t wc[CH][NPT];
-#pragma unroll
-                for (int e = 0; e < CH; ++e)
-#pragma unroll
-                    for (int c = 0; c < NPT; ++c) wc[e][c] = wn[e][c];
-                if (f0 + CH < nf) {
-#pragma unroll
-                    for (int e = 0; e < CH; ++e) {
-                        const int o = __builtin_amdgcn_readlane(src, (f0 + CH + e) & 63);
-#pragma unroll
-                        for (int c = 0; c < NPT; ++c)
-                            wn[e][c] = __float_as_uint(raw_buffer_load_f32(rw, wio[c] + o * N * 4, 0, 0));
-                    }
+                    for (int c = 0; c < NPT; ++c)
+                        wb[e][c] = __float_as_uint(raw_buffer_load_f32(rw, wio[c], o * N * 4, 0));
                 }
+            };
+            // two word buffers in turn: chunk f0's words in one while the next chunk's load
+            // into the other
+            uint32_t wa[CH][NPT], wz[CH][NPT];
+            fetch(wa, 0);
+            auto scatter = [&](const uint32_t (&wc)[CH][NPT], int f0) {
 #pragma unroll
                 for (int e = 0; e < CH; ++e) {
                     if (f0 + e >= nf) break;
@@ -532,6 +525,13 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
 #pragma unroll
                         for (int q = 0; q < KF; ++q) run[c][q * NR] = fmaf(wf[c], hf[q], old[c][q]);
                 }
+            };
+            for (int f0 = 0; f0 < nf; f0 += 2 * CH) {
+                if (f0 + CH < nf) fetch(wz, f0 + CH);
+                scatter(wa, f0);
+                if (f0 + CH >= nf) break;
+                if (f0 + 2 * CH < nf) fetch(wa, f0 + 2 * CH);
+                scatter(wz, f0 + CH);
             }
         }
 
