@@ -387,8 +387,9 @@ __global__ void __launch_bounds__(256) hyb_bwd_far_kernel(HybBwd p) {
 // wave holds arrival a's source and tap weights, which reach the whole wave by readlane, so
 // the only memory reads of the walk are the packed words, fetched a chunk of CH arrivals
 // ahead into the other of two word buffers (CH = 32 with one neuron per lane, 4 with two),
-// each load taking the source row's offset in its scalar offset. A receiver's ring column is only ever written by its own lane, so the scatter needs
-// no barrier; then each lane runs the LIF of its receivers on their ring slot, shifts each
+// each load taking the source row's offset in its scalar offset. A receiver's ring column is
+// only ever written by its own lane, so the scatter needs no barrier; then each lane runs the
+// LIF of its receivers on their ring slot, shifts each
 // source's spike into its history word and appends the sources arriving at t + 1 to its
 // wave's segment of the other list buffer; one LDS barrier per step.
 constexpr int kArriveWaves = 16;   // list segments per buffer (a 1024-lane block)
