@@ -168,8 +168,9 @@ __global__ void __launch_bounds__(256) hyb_lif_fwd_kernel(HybLif p) {
     p.hlo[ho] = (uint16_t)hyb_bf16_rne(z - __uint_as_float(hi << 16));
 }
 
-// Backward step t over a tile of 32 sources / neurons j0 .. j0 + 31 x 64 batch rows (256
-// threads; 2 workgroups per CU at C5), three phases:
+// Backward step t over a tile of 16 sources / neurons j0 .. j0 + 15 x 64 batch rows (256
+// threads; 1024 workgroups at C5: twice the loads in flight of 32-source tiles, which were
+// 2 % slower, and 8-source tiles 9 %), three phases:
 //  1 G_j(t + 1) of the tile's near sources, the near product's columns ntile[x] ..
 //    ntile[x + 1] - 1: sum_ks npart[ks][c][b] in a fixed order (column-major partials, one
 //    column per wave, 16 partials in flight per lane), into LDS;
@@ -177,14 +178,14 @@ __global__ void __launch_bounds__(256) hyb_lif_fwd_kernel(HybLif p) {
 //    G(t + 1) into ring slot (t + 1) mod R; then gfut_j(t) = sum_f h_j(lof_j + f) G_j(t + lof_j
 //    + f), from LDS for tau = t + 1 (lof_j = 1, f = 0: always a near source) and from the
 //    ring otherwise (0 for tau >= T: gr past the last step is 0), all ring reads of the
-//    wave's 8 sources issued before any is used;
+//    wave's sources issued before any is used;
 //  3 (row-major): the LIF backward on gy + gfut, outputs dx (and gr when it differs), the db
 //    partial, and gr(t) split into the hi / lo history planes at slice t.
 // The ring slot of tau is rewritten with G(tau - R) only after every step that reads G(tau)
 // (steps >= tau - L + 1) has run, for R >= L - 1; this step's reads (tau >= t + 2) and writes
 // (tau = t + 1) never share a slot.
 constexpr int kHybTapsMax = 8;
-constexpr int kHybBwdTile = 32;
+constexpr int kHybBwdTile = 16;
 
 template <int KF>
 __global__ void __launch_bounds__(256) hyb_bwd_lif_kernel(HybBwd p) {
@@ -200,15 +201,17 @@ __global__ void __launch_bounds__(256) hyb_bwd_lif_kernel(HybBwd p) {
     if (tid < JT) ncl[tid] = -1;
     // loads that do not wait for this step's G, issued first so that their latency overlaps
     // phases 1 and 2: the LIF operands of phase 3 and the ring reads of phase 2
+    // phase 3 lays a wave over LR = 64 / JT rows of JT columns; 4 LR rows per pass
+    constexpr int LR = 64 / JT;
     const int jl3 = lane & (JT - 1), j3 = j0 + jl3;
-    const int r0 = 2 * w + (lane >> 5);
+    const int r0 = LR * w + lane / JT;
     const size_t BN = (size_t)B * N;
     const bool last = t == T - 1;
-    constexpr int E3 = 64 / 8;
+    constexpr int E3 = 64 / (4 * LR);
     float uu[E3], gyv[E3], lam[E3], dbv[E3], mv[E3];
 #pragma unroll
     for (int e = 0; e < E3; ++e) {
-        const int b = b0 + r0 + 8 * e;
+        const int b = b0 + r0 + 4 * LR * e;
         const bool ok = b < B && j3 < N;
         const size_t bj = (size_t)(ok ? b : 0) * N + (ok ? j3 : 0), o = (size_t)t * BN + bj;
         uu[e] = ok ? p.u_in[o] : 0.0f;
@@ -289,13 +292,13 @@ __global__ void __launch_bounds__(256) hyb_bwd_lif_kernel(HybBwd p) {
         }
     }
     barrier_lds();
-    // phase 3: column jl = lane % 32, rows 2 w + lane / 32 + 8 e (operands loaded on entry)
+    // phase 3: column jl = lane % JT, rows LR w + lane / JT + 4 LR e (operands loaded on entry)
     {
         const Lif k = p.lif;
         const int jl = jl3, j = j3;
 #pragma unroll
         for (int e = 0; e < E3; ++e) {
-            const int r = r0 + 8 * e, b = b0 + r;
+            const int r = r0 + 4 * LR * e, b = b0 + r;
             if (b >= B || j >= p.Nk) continue;
             const size_t ho = (size_t)b * p.lda + (size_t)t * p.Nk + j;
             if (j >= N) {
