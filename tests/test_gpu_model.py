@@ -111,7 +111,7 @@ def test_delay_maintenance_on_device(dev, name):
     lay = lambda m: [x for x in m.layers if isinstance(x, axonal_recdel)][0]
     assert lay(hip).sigma == lay(ref).sigma == pytest.approx(cfg.sigma_init * cfg.sigma_decay ** (100 / 20 * 7))
     l_ref, l_hip = learned_delay_parameter(lay(ref), 'recurrent_delays'), learned_delay_parameter(lay(hip), 'recurrent_delays')
-    assert l_hip.is_cuda and torch.equal(l_hip.detach().cpu(), l_ref.detach()) and float(l_ref.min()) >= 0.0
+    assert l_hip.is_cuda and torch.equal(l_hip.detach().cpu(), l_ref.detach()) and float(l_ref.detach().min()) >= 0.0
     # stochastic rounding on device: every delay on its floor or ceiling
     before = l_hip.detach().clone()
     hip.config.round_mode = 'stochastic'
