@@ -43,7 +43,7 @@ __device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
 }
 
 // gr (T, B, N) fp32 -> gr_hi, gr_mid, gr_lo in the k-blocked layout (Kp rows, Np columns;
-// padding rows and columns are zero).
+// padding rows and columns are zero); lo == NULL skips the third plane (two-plane tiles).
 __global__ void pack_gr_kernel(const float* __restrict__ gr, int T, int B, int Bp, int N, int Np,
                                int Kp, uint4* __restrict__ hi, uint4* __restrict__ mid,
                                uint4* __restrict__ lo) {
@@ -71,7 +71,7 @@ __global__ void pack_gr_kernel(const float* __restrict__ gr, int T, int B, int B
         }
         hi[q] = uint4{h[0], h[1], h[2], h[3]};
         mid[q] = uint4{md[0], md[1], md[2], md[3]};
-        lo[q] = uint4{l[0], l[1], l[2], l[3]};
+        if (lo) lo[q] = uint4{l[0], l[1], l[2], l[3]};
     }
 }
 
@@ -408,7 +408,7 @@ void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hi
     const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 65535u * 4);
     hipLaunchKernelGGL(pack_gr_kernel, dim3(blocks), dim3(256), 0, stream, gr, a.T, a.B, a.Bp, a.N,
                        a.Np, a.Kp, const_cast<uint4*>(a.ahi), const_cast<uint4*>(a.amd),
-                       const_cast<uint4*>(a.alo));
+                       a.planes == 2 ? nullptr : const_cast<uint4*>(a.alo));
     hipLaunchKernelGGL(pack_spikes_kernel, dim3(blocks), dim3(256), 0, stream, bits, a.lo, a.T, a.B,
                        a.Bp, a.N, a.Np, a.Kp, const_cast<uint4*>(a.yb));
     const int tiles = (a.Np / kWT) * (a.Np / kWT);
