@@ -1206,7 +1206,11 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         LagStepGemm gf = gn;   // block t0: far G(t0 + 1 + tt), row (b, tt) shifted by tt slices
         gf.rows = B * P; gf.rp = P; gf.rs = hq.Nk;
         gf.p0 = Pf; gf.p1 = planes > 1 ? Pf + fplane : nullptr; gf.Np = Nfp;
-        gf.KS = Nf > 0 ? lagstep_splits(B * P, Nfp, hq.Kt, num_cus(), fcol) : 1; gf.part = fpart; gf.cm = 0;
+        // one-plane P: 256 x 256 tiles of 8 waves (128 x 256 tiles of 4 waves with DELREC_FAR256=0)
+        const bool far256 = planes == 1 && getenv_flag_off("DELREC_FAR256");
+        gf.KS = Nf == 0 ? 1 : far256 ? lagstep_gemm256_splits(B * P, Nfp, hq.Kt, num_cus())
+                                     : lagstep_splits(B * P, Nfp, hq.Kt, num_cus(), fcol);
+        gf.part = fpart; gf.cm = 0;
         HybBwd l{};
         l.T = T; l.B = B; l.N = N; l.Nk = hq.Nk; l.KF = KF; l.R = hq.R; l.P = P; l.lda = hq.lda;
         l.npart = npart; l.KSn = Nn > 0 ? gn.KS : 0; l.Nnp = Nnp; l.ntile = ntile; l.perm = perm;
@@ -1218,7 +1222,10 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         for (int t0 = T - 1; t0 >= 0; t0 -= P) {
             if (Nf > 0) {
                 gf.aoff = (size_t)(t0 + 1) * hq.Nk;
-                launch_lagstep_gemm(gf, 2, s, planes, fcol / 2);
+                if (far256)
+                    launch_lagstep_gemm256(gf, s);
+                else
+                    launch_lagstep_gemm(gf, 2, s, planes, fcol / 2);
                 l.t0 = t0;
                 launch_hyb_bwd_far(l, s);
             }

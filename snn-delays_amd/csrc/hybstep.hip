@@ -682,8 +682,12 @@ HybBwdSizes hyb_bwd_sizes(const HybStepDims& q, int B, int cus, int fcol) {
     // up to at most N + 127 + fcol - 1 < Np + 384
     for (int c = 128; c <= q.Np; c += 128)
         z.npart = std::max(z.npart, (size_t)lagstep_splits(B, c, q.Kt, cus) * B * c);
-    for (int c = fcol; c <= (q.Np + fcol - 1) / fcol * fcol; c += fcol)
-        z.fpart = std::max(z.fpart, (size_t)lagstep_splits(B * q.P, c, q.Kt, cus, fcol) * B * q.P * c);
+    // (256-column far parts may run either far kernel: the larger split count sizes them)
+    for (int c = fcol; c <= (q.Np + fcol - 1) / fcol * fcol; c += fcol) {
+        int ks = lagstep_splits(B * q.P, c, q.Kt, cus, fcol);
+        if (fcol == 256) ks = std::max(ks, lagstep_gemm256_splits(B * q.P, c, q.Kt, cus));
+        z.fpart = std::max(z.fpart, (size_t)ks * B * q.P * c);
+    }
     z.planes = (size_t)(q.Kt / 8) * (q.Np + 384);
     return z;
 }

@@ -317,6 +317,9 @@ void launch_hist_zero(uint16_t* h, int B, size_t lda, int Nk, int t0, int t1, hi
 void launch_hist_clear(uint16_t* h, int B, size_t lda, hipStream_t stream);
 // pb = 1: one P plane (p1 unused)
 void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream, int pb = 2, int wn = 64);
+// 256 x 256 tiles for a two-plane A and a one-plane P (Np a multiple of 256)
+int lagstep_gemm256_splits(int rows, int Np, int Kt, int cus);
+void launch_lagstep_gemm256(const LagStepGemm& g, hipStream_t stream);
 void launch_lagstep_lif(const LagStepLif& l, bool fwd, hipStream_t stream);
 int lagblock_splits(int B, int Np, int Nk, int cus);
 void launch_lagblock(const LagStepGemm& g, int pa, hipStream_t stream);

@@ -296,6 +296,114 @@ __global__ void __launch_bounds__(256) lagstep_gemm_kernel(LagStepGemm p) {
         }
 }
 
+// The same product in 256 x 256 tiles for a two-plane A and a one-plane P (the hybrid's
+// per-block far product): 8 waves of 64 x 128 (4 x 8 MFMA blocks, 128 accumulator registers
+// each; a 4-wave 128 x 128 split needs all 256 AGPRs and the register allocator shuffles
+// them) and one k split per workgroup. A 32-k stage moves 256 rows x 2 planes of A and 256
+// columns of P through LDS (48 KB, double-buffered) from one register stage of global loads
+// (in flight while the previous stage multiplies): half the staged bytes per MFMA of the
+// 128 x 256 tile. Row mapping and partial layout (row-major) as lagstep_gemm_kernel.
+__global__ void __launch_bounds__(512) lagstep_gemm256_kernel(LagStepGemm p) {
+    extern __shared__ uint4 lds_u4[];
+    constexpr int TR = 256, NC = 256;
+    constexpr int ABUF = 2 * 4 * TR;      // A: plane q, k-block kb, row r at q * 1024 + kb * 256 + r
+    constexpr int BUF = ABUF + 4 * NC;    // P: k-block kb, column c at ABUF + kb * 256 + c
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int wi = w >> 1, wj = w & 1, g = lane >> 4, lc = lane & 15;
+    const int NT = p.Np / NC;
+    const int id = (int)blockIdx.x;
+    const int ks = id % p.KS, tile = id / p.KS;
+    const int bt = tile / NT, nt = tile - bt * NT;
+    const int b0 = bt * TR, n0 = nt * NC;
+    const int nst = p.Kt / 32;
+    const int per = (nst + p.KS - 1) / p.KS;
+    const int s0 = ks * per;
+    const int ns = max(min(nst, s0 + per) - s0, 0);
+
+    const uint32_t abytes = (uint32_t)((size_t)p.B * p.lda * 2);
+    const i32x4 ra0 = buffer_rsrc(p.a0, abytes), ra1 = buffer_rsrc(p.a1, abytes);
+    const uint32_t pbytes = (uint32_t)((size_t)(p.Kt / 8) * p.Np * 16);
+    const i32x4 rb = buffer_rsrc(p.p0, pbytes);
+    // staging: thread tid stages A uint4 c = tid + 512 h (k-block c >> 8, row c & 255) of both
+    // planes and P uint4 c = tid + 512 h (k-block c >> 8, column c & 255), h < 2
+    uint32_t oa[2], ob[2];
+    const uint32_t bstep = (uint32_t)(4 * p.Np * 16);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = tid + 512 * h, kb = c >> 8, r = c & 255;
+        const int rr = b0 + r;   // rows past p.rows land past the descriptor's end: zeros
+        oa[h] = (uint32_t)(((size_t)(rr / p.rp) * p.lda + (size_t)(rr % p.rp) * p.rs + p.aoff +
+                            (size_t)s0 * 32 + kb * 8) * 2);
+        ob[h] = (uint32_t)((((size_t)s0 * 4 + kb) * p.Np + n0 + r) * 16);
+    }
+    uint4 sa[2][2], sb[2];   // one register stage: [plane][h], [h]
+    auto issue = [&]() {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            sa[0][h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(ra0, (int)oa[h], 0, 0));
+            sa[1][h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(ra1, (int)oa[h], 0, 0));
+            oa[h] += 64;
+            sb[h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rb, (int)ob[h], 0, 0));
+            ob[h] += bstep;
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            lds_u4[buf * BUF + tid + 512 * h] = sa[0][h];
+            lds_u4[buf * BUF + 1024 + tid + 512 * h] = sa[1][h];
+            lds_u4[buf * BUF + ABUF + tid + 512 * h] = sb[h];
+        }
+    };
+    floatx4 acc[4][8];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int buf) {
+        bf16x8 fb[8];
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+            fb[nb] = __builtin_bit_cast(bf16x8, lds_u4[buf * BUF + ABUF + g * 256 + wj * 128 + nb * 16 + lc]);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const bf16x8 a0 = __builtin_bit_cast(bf16x8, lds_u4[buf * BUF + g * 256 + wi * 64 + mb * 16 + lc]);
+            const bf16x8 a1 = __builtin_bit_cast(bf16x8, lds_u4[buf * BUF + 1024 + g * 256 + wi * 64 + mb * 16 + lc]);
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb)
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, fb[nb], acc[mb][nb], 0, 0, 0);
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb)
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, fb[nb], acc[mb][nb], 0, 0, 0);
+        }
+    };
+
+    issue();
+    stash(0);
+    barrier_lds();
+    issue();
+    // stage s in LDS buffer s % 2 while stage s + 1's loads are in flight in the registers;
+    // those go to the other buffer after stage s multiplies, then stage s + 2's loads issue
+    // (past the last stage they read zeros or bytes no stage uses)
+    for (int s = 0; s < ns; ++s) {
+        compute(s & 1);
+        stash((s + 1) & 1);
+        barrier_lds();
+        issue();
+    }
+
+    float* out = p.part + (size_t)ks * p.rows * p.Np;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = b0 + wi * 64 + mb * 16 + 4 * g + e;
+            if (r >= p.rows) continue;
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) out[(size_t)r * p.Np + n0 + wj * 128 + nb * 16 + lc] = acc[mb][nb][e];
+        }
+}
+
 // ---------------------------------------------------------------------------------------
 // Far lags of a block of P steps without LDS:
 //   out[tt][b][n] = sum_q sum_k H[b][(base + tt + q) * Nk + k] * M[q][k][n],  q < Lf, tt < P,
@@ -598,6 +706,22 @@ void launch_lagstep_gemm(const LagStepGemm& g, int pa, hipStream_t stream, int p
     DELREC_LAGSTEP_GEMM(2, 2, 64)
     DELREC_LAGSTEP_GEMM(2, 1, 64)
     DELREC_LAGSTEP_GEMM(2, 1, 128)
+}
+
+// k splits of lagstep_gemm256_kernel: enough workgroups for the CUs, at least 8 stages each
+int lagstep_gemm256_splits(int rows, int Np, int Kt, int cus) {
+    const int tiles = ((rows + 255) / 256) * (Np / 256);
+    const int cap = std::max(1, Kt / 32 / 8);
+    return std::max(1, std::min((cus + tiles - 1) / tiles, cap));
+}
+
+size_t lagstep_gemm256_lds() { return (size_t)2 * (2 * 4 * 256 + 4 * 256) * sizeof(uint4); }
+
+void launch_lagstep_gemm256(const LagStepGemm& g, hipStream_t stream) {
+    const int grid = ((g.rows + 255) / 256) * (g.Np / 256) * g.KS;
+    const size_t lds = lagstep_gemm256_lds();
+    ensure_lds((const void*)lagstep_gemm256_kernel, lds);
+    hipLaunchKernelGGL(lagstep_gemm256_kernel, dim3(grid), dim3(512), lds, stream, g);
 }
 
 // far lags of a block: rows (b, tt) of g.part with g.rp == kLagStepBlock
