@@ -608,7 +608,8 @@ bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t 
 // ---------------------------------------------------------------------------------------
 
 // steps per block of the backward's far product: C5 measured 90 ms per scan at 4, 94 at 8,
-// 104 at 6, 114 at 16, 123 at 3
+// 104 at 6, 114 at 16, 123 at 3 (128 x 256 far tiles); 80 at 4, 93 at 8, 104 at 5, 341 at 2
+// with the 256 x 256 far tiles
 constexpr int kHybBlock = 4;
 
 HybStepDims hybstep_dims(int T, int B, int N, int L, int D, int KF, int cus) {
