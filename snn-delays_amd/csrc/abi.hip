@@ -1194,8 +1194,11 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
             pk.Np = Nfp; pk.c0 = Nn; pk.nc = Nf; pk.out = Pf;
             launch_hyb_pack(pk, false, s);
         }
-        launch_hist_clear(ghi, B, hq.lda, s);   // gr past the last step
-        launch_hist_clear(glo, B, hq.lda, s);
+        // gr past the last step (slices T ..): every column of slices 0 .. T - 1 is written by
+        // step t's LIF before a product reads it
+        const int hslices = (int)(hq.lda / hq.Nk);
+        launch_hist_zero(ghi, B, hq.lda, hq.Nk, T, hslices, s);
+        launch_hist_zero(glo, B, hq.lda, hq.Nk, T, hslices, s);
         // gr == dx unless a dropout mask scales it
         const bool need_gr = a->drop != nullptr;
         LagStepGemm gn{};   // step t: near G(t + 1) from history slices t + 1 .. t + D
