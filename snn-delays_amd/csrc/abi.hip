@@ -333,6 +333,7 @@ bool syn_hybstep(int T, int B, int N, int L, bool hybrid, int off_count, int tap
 struct ArriveShape {
     bool ok;
     int npt, block, kf, R, RP, hw;
+    int sh;   // the packed offset field's shift: log2 of a slot's bytes where R slots are 2^16 bytes, else 0
     size_t lds;
 };
 ArriveShape syn_arrive(int N, int L, bool hybrid, bool bf16, int off_count, int taps, bool lags_ok) {
@@ -346,6 +347,8 @@ ArriveShape syn_arrive(int N, int L, bool hybrid, bool bf16, int off_count, int 
     a.R = 1;   // D + KF - 1 slots, rounded up to a power of two (the kernel wraps by a mask)
     while (a.R < off_count + a.kf - 1) a.R *= 2;
     a.RP = a.R + a.kf - 1;
+    const int slot_log2 = a.npt == 1 ? 12 : 13;   // npt * 1024 receivers x 4 bytes per slot
+    a.sh = (a.R << slot_log2) == 65536 ? slot_log2 : 0;
     a.hw = (std::max(L - 1, 1) + 63) / 64;
     // ring [RP][npt * 1024], segment counts [2][16], arrival segments [2][16][npt * 64]
     a.lds = (size_t)a.RP * a.npt * 1024 * sizeof(float) + (size_t)2 * 16 * sizeof(int) +
@@ -946,12 +949,12 @@ int syn_fwd_arrive(const delrec_syn_fwd_args* a, const ArriveShape& ar, hipStrea
     int* lof = cv.take<int>((size_t)N);
     float* h = cv.take<float>((size_t)ar.kf * N);
     if (!wpk || !lof || !h) return DELREC_ERR_WORKSPACE;
-    launch_pack_hybrid(static_cast<const uint16_t*>(a->W), a->offsets, N, wpk, s, a->off_min);
+    launch_pack_hybrid(static_cast<const uint16_t*>(a->W), a->offsets, N, wpk, s, a->off_min, ar.sh);
     HybTaps tp{};   // kf rows: a run shorter than kf gets taps of weight 0 past its triangle
     tp.N = N; tp.KF = ar.kf; tp.omin = a->off_min; tp.s = a->s_uniform; tp.base = a->base; tp.lof = lof; tp.h = h;
     launch_hyb_taps(tp, s);
     HybScat p{};
-    p.T = a->T; p.B = a->B; p.N = N; p.D = a->off_count; p.KF = ar.kf; p.R = ar.R; p.RP = ar.RP;
+    p.T = a->T; p.B = a->B; p.N = N; p.D = a->off_count; p.KF = ar.kf; p.R = ar.R; p.RP = ar.RP; p.sh = ar.sh;
     p.omin = a->off_min; p.x = a->x; p.bias = a->bias; p.drop = a->drop; p.lif = make_lif(a->lif);
     p.wpk = wpk; p.lof = lof; p.h = h; p.y = a->y; p.u = a->u; p.bits = a->bits;
     const bool timed = scan_begin(DELREC_WS_SYN_FWD, s);

@@ -382,8 +382,11 @@ __global__ void __launch_bounds__(256) hyb_bwd_far_kernel(HybBwd p) {
 // the lanes of a wave always hit 64 distinct banks whatever slot each connection selects, and
 // the taps of a run are immediate offsets of one address. (C5: 9 slots of 2048 receivers,
 // 74 KB, so two rows' workgroups share a CU.) Per connection: the packed word
-// bf16(W) << 16 | (offset - smallest offset) byte (one 4-byte load), the slot, and KF
-// read-modify-writes w * h_j(lof_j + f) of the run.
+// bf16(W) << 16 | (offset - smallest offset) in the low half word (one 4-byte load), the
+// slot, and KF read-modify-writes w * h_j(lof_j + f) of the run. Where the R slots are
+// exactly 2^16 bytes (C3: 16 x 4 KB, C5: 8 x 8 KB) the low half holds the offset times the
+// slot bytes, so a 16-bit add of (t mod R) * slot bytes wraps the slot by itself and one add
+// places the receiver: two VALU instead of three (offset byte-add, mask, scale-add).
 //
 // Per step: every wave walks the arrival list of step t (flattened from per-wave segments,
 // sources in a fixed order) over its own receivers, 64 arrivals at a time: lane a of the
@@ -397,10 +400,11 @@ __global__ void __launch_bounds__(256) hyb_bwd_far_kernel(HybBwd p) {
 // wave's segment of the other list buffer; one LDS barrier per step.
 constexpr int kArriveWaves = 16;   // list segments per buffer (a 1024-lane block)
 
-template <int NPT, int KF, int HW, int CH>
+template <int NPT, int KF, int HW, int CH, bool WS>
 __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
     extern __shared__ float smem[];
     constexpr int NR = NPT * 1024;
+    constexpr int SH = NPT == 1 ? 12 : 13;   // log2 of a slot's bytes (WS: the offset field's shift)
     const int N = p.N, T = p.T, B = p.B, R = p.R, RP = p.RP;
     const int b = blockIdx.x, tid = threadIdx.x, BS = blockDim.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -518,9 +522,16 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
                         // by a mask (one byte-add and one AND), and a byte outside that range
                         // still lands in the ring. A lane past N reads the word 0: weight 0
                         // into its own column
-                        const int sl = (tm + (int)(wv & 0xFFu)) & (R - 1);
                         wf[c] = __uint_as_float(wv & 0xFFFF0000u);
-                        run[c] = ring + sl * NR + idx[c];
+                        if constexpr (WS) {
+                            // the field is the offset's slot bytes and R slots are 2^16 bytes:
+                            // a 16-bit add wraps the slot, one add places the receiver
+                            const uint32_t ab = (uint16_t)((uint16_t)wv + (uint16_t)(tm << SH));
+                            run[c] = reinterpret_cast<float*>(reinterpret_cast<char*>(ring + idx[c]) + ab);
+                        } else {
+                            const int sl = (tm + (int)(wv & 0xFFu)) & (R - 1);
+                            run[c] = ring + sl * NR + idx[c];
+                        }
 #pragma unroll
                         for (int q = 0; q < KF; ++q) old[c][q] = run[c][q * NR];
                     }
@@ -589,19 +600,22 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
     }
 }
 
-// wpk[o * N + i] = bf16 bits of W[i, o] << 16 | uint8(offset[i, o] - smallest offset)
-// (launch_pack_hybrid with the smallest offset)
+// wpk[o * N + i] = bf16 bits of W[i, o] << 16 | uint8(offset[i, o] - smallest offset) << a.sh
+// (launch_pack_hybrid with the smallest offset and a.sh: the slot bytes' log2 where R slots
+// of them are 2^16 bytes, else 0)
 bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t lds, hipStream_t stream) {
-#define DELREC_ARRIVE(NPTV, KFV, HWV)                                                             \
-    if (npt == NPTV && a.KF <= KFV && hw == HWV) {                                                \
+#define DELREC_ARRIVE_WS(NPTV, KFV, HWV, WSV)                                                     \
+    if (npt == NPTV && a.KF <= KFV && hw == HWV && (a.sh > 0) == WSV) {                          \
         constexpr int CHV = NPTV == 1 ? 32 : 4;                                                   \
-        ensure_lds((const void*)hyb_fwd_arrive_kernel<NPTV, KFV, HWV, CHV>, lds);                \
-        hipLaunchKernelGGL((hyb_fwd_arrive_kernel<NPTV, KFV, HWV, CHV>), dim3(a.B), dim3(block), lds, stream, a); \
+        ensure_lds((const void*)hyb_fwd_arrive_kernel<NPTV, KFV, HWV, CHV, WSV>, lds);           \
+        hipLaunchKernelGGL((hyb_fwd_arrive_kernel<NPTV, KFV, HWV, CHV, WSV>), dim3(a.B), dim3(block), lds, stream, a); \
         return true;                                                                             \
     }
+#define DELREC_ARRIVE(NPTV, KFV, HWV) DELREC_ARRIVE_WS(NPTV, KFV, HWV, true) DELREC_ARRIVE_WS(NPTV, KFV, HWV, false)
     DELREC_ARRIVE(1, 2, 1) DELREC_ARRIVE(1, 2, 2) DELREC_ARRIVE(2, 2, 1) DELREC_ARRIVE(2, 2, 2)
     DELREC_ARRIVE(1, 4, 1) DELREC_ARRIVE(1, 4, 2) DELREC_ARRIVE(2, 4, 1) DELREC_ARRIVE(2, 4, 2)
 #undef DELREC_ARRIVE
+#undef DELREC_ARRIVE_WS
     return false;
 }
 

@@ -266,11 +266,13 @@ void launch_hyb_bwd_far(const HybBwd& a, hipStream_t stream);
 
 struct HybScat {                 // the hybrid forward as a scatter on arrival (bf16 W)
     int T, B, N, D, KF, R, RP, omin;   // KF: the compiled run length; R >= D + KF - 1 ring slots, a power of two
+    int sh;                      // > 0: the offset field is (offset - omin) << sh, sh = log2 of the slot
+                                 // bytes, R slots being 2^16 bytes
     const float* x;
     const float* bias;
     const float* drop;
     Lif lif;
-    const uint32_t* wpk;         // wpk[o * N + i] = bf16(W[i, o]) << 16 | uint8(offset[i, o] - omin)
+    const uint32_t* wpk;         // wpk[o * N + i] = bf16(W[i, o]) << 16 | uint8(offset[i, o] - omin) << sh
     const int* lof;              // [N] first lag of each source
     const float* h;              // [KF][N] its tap weights (0 past its triangle)
     float* y;
@@ -373,9 +375,9 @@ void launch_max_to_host(const float* x, int n, uint32_t ticket, unsigned long lo
 void launch_axonal_bwd_sums(const AxTail& q, const float* part, int B, int N, hipStream_t stream);
 
 void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream);
-// wpk[o*N + i] = W[i*N + o] (bf16 bits) << 16 | uint8(off[i*N + o])
+// wpk[o*N + i] = W[i*N + o] (bf16 bits) << 16 | uint8(off[i*N + o] - omin) << sh (low 16 bits)
 void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream,
-                        int omin = 0);
+                        int omin = 0, int sh = 0);
 // event-driven forward, ring in LDS, one receiver per lane, kf >= ceil(2 s_max) taps
 bool launch_syn_fwd_scatter(const SynFwd& a, int kf, int block, size_t lds, hipStream_t stream);
 bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);

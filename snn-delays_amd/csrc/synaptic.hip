@@ -381,16 +381,19 @@ __global__ void __launch_bounds__(1024) syn_fwd_scatter(SynFwd p) {
     }
 }
 
-// wpk[o*N + i] = W[i*N + o] << 16 | uint8(off[i*N + o] - omin) through 32 x 32 LDS tiles
+// wpk[o*N + i] = W[i*N + o] << 16 | uint8(off[i*N + o] - omin) << sh (the low 16 bits)
+// through 32 x 32 LDS tiles
 __global__ void __launch_bounds__(256) pack_hybrid_kernel(const uint16_t* __restrict__ W,
                                                           const int8_t* __restrict__ off, int N, int omin,
-                                                          uint32_t* __restrict__ wpk) {
+                                                          int sh, uint32_t* __restrict__ wpk) {
     __shared__ uint32_t tile[32][33];
     const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
     for (int r = threadIdx.y; r < 32; r += 8) {
         const int i = by + r, o = bx + threadIdx.x;
         uint32_t v = 0;
-        if (i < N && o < N) v = ((uint32_t)W[(size_t)i * N + o] << 16) | (uint8_t)(off[(size_t)i * N + o] - omin);
+        if (i < N && o < N)
+            v = ((uint32_t)W[(size_t)i * N + o] << 16) |
+                (((uint32_t)(uint8_t)(off[(size_t)i * N + o] - omin) << sh) & 0xFFFFu);
         tile[r][threadIdx.x] = v;
     }
     __syncthreads();
@@ -400,9 +403,10 @@ __global__ void __launch_bounds__(256) pack_hybrid_kernel(const uint16_t* __rest
     }
 }
 
-void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream, int omin) {
+void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream, int omin,
+                        int sh) {
     const dim3 grid((N + 31) / 32, (N + 31) / 32), block(32, 8);
-    hipLaunchKernelGGL(pack_hybrid_kernel, grid, block, 0, stream, W, off, N, omin, wpk);
+    hipLaunchKernelGGL(pack_hybrid_kernel, grid, block, 0, stream, W, off, N, omin, sh, wpk);
 }
 
 // Forward in gather form, for rings too large for LDS: lane i owns receiver i and sums

@@ -240,7 +240,10 @@ def test_hybrid_offset_stacked_matches_oracle(dev, case, monkeypatch):
 # the hybrid forward as a scatter on arrival (the default for bf16 W, bases >= s - 1, at most
 # 16 offsets, 4 taps and 2048 neurons): two and four compiled taps (sigma 0.5 runs three taps
 # on the four-tap kernel), one and two spike-history words, two neurons per lane (N > 1024,
-# the second half of the lanes partly idle), a smallest offset of 2 under negative bases
+# the second half of the lanes partly idle), a smallest offset of 2 under negative bases. The
+# offset field holds slot bytes where the ring's R slots are 2^16 bytes: 16 slots of one
+# neuron per lane (9 offsets with two and with four taps), 8 slots of two (N = 1100); the
+# other cases take the offset byte
 ARRIVE_CASES = [
     (20, 3, 64, (0.0, 8.0), 4, True, 0.0),
     HYB_CASES[2],
@@ -249,6 +252,8 @@ ARRIVE_CASES = [
     HYB_CASES[5],
     (12, 2, 1100, (0.0, 30.0), 4, True, 0.0),
     (20, 2, 64, (-1.5, 6.0), 6, True, 0.0, 2),
+    (20, 2, 64, (0.0, 8.0), 9, True, 0.0),
+    (24, 2, 96, (1.0, 6.0), 9, True, 1.0),
 ]
 
 
