@@ -225,6 +225,9 @@ HYBSTEP_CASES = [HYB_CASES[i] for i in (0, 2, 5, 6)] + [
     (33, 3, 130, (0.0, 25.0), 2, True, 0.0),
     (21, 2, 96, (10.0, 20.0), 3, False, 0.0),
     (19, 3, 80, (0.0, 2.5), 3, True, 0.0),
+    # bf16 W, 9 offsets at N = 288: the far product's 81 k-stages over 10 splits of 9, the
+    # last split empty (its partial must come out zero)
+    (20, 2, 288, (0.0, 25.0), 9, True, 0.0),
 ]
 
 
