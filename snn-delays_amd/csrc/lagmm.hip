@@ -76,33 +76,47 @@ __global__ void pack_gr_kernel(const float* __restrict__ gr, int T, int B, int B
 }
 
 // spike bits (B, ceil(T/32), N) -> Y'[t, b, j] = y[t - lo_j, b, j] in bf16 (1.0 = 0x3F80),
-// k-blocked; lo == NULL means lo_j = 1.
+// k-blocked (row k = t * Bp + b, Kp = T * Bp); lo == NULL means lo_j = 1. One thread per
+// column, batch octet and 32-step chunk: each of the octet's 8 rows reads the two spike words
+// that cover the chunk's shifted steps once (steps before 0 read 0), and the chunk's 32
+// 16-byte outputs follow, consecutive columns on consecutive lanes.
 __global__ void pack_spikes_kernel(const uint32_t* __restrict__ bits, const int* __restrict__ lo,
-                                   int T, int B, int Bp, int N, int Np, int Kp,
-                                   uint4* __restrict__ out) {
+                                   int T, int B, int Bp, int N, int Np, uint4* __restrict__ out) {
     const int TW = (T + 31) >> 5;
-    const size_t total = (size_t)(Kp / 8) * Np;
+    const int BO = Bp / 8;
+    const size_t total = (size_t)TW * BO * Np;
     for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total;
          q += (size_t)gridDim.x * blockDim.x) {
-        const int kb = (int)(q / Np), j = (int)(q - (size_t)kb * Np);
+        const int j = (int)(q % (size_t)Np);
+        const size_t r = q / (size_t)Np;
+        const int bo = (int)(r % (size_t)BO), tc = (int)(r / (size_t)BO);
         const int shift = (j < N) ? (lo ? lo[j] : 1) : 0;
-        uint32_t w[4];
+        // step 32 tc + e reads y at ts0 + e, ts0 = 32 tc - shift: bits off .. off + 31 of the
+        // word pair (w0, w0 + 1), w0 = floor(ts0 / 32)
+        const int ts0 = 32 * tc - shift;
+        const int w0 = ts0 >= 0 ? ts0 / 32 : -((31 - ts0) / 32);
+        const int off = ts0 - 32 * w0;
+        uint32_t m[8];   // bit e: y(32 tc + e - shift) of batch row 8 bo + rr
 #pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            uint32_t v[2];
-#pragma unroll
-            for (int f = 0; f < 2; ++f) {
-                const int k = kb * 8 + e + f;
-                const int t = k / Bp, b = k - (k / Bp) * Bp;
-                const int ts = t - shift;
-                bool on = false;
-                if (j < N && t < T && b < B && ts >= 0)
-                    on = (bits[((size_t)b * TW + (ts >> 5)) * N + j] >> (ts & 31)) & 1u;
-                v[f] = on ? 0x3F80u : 0u;
+        for (int rr = 0; rr < 8; ++rr) {
+            const int b = 8 * bo + rr;
+            uint64_t v = 0;
+            if (j < N && b < B) {
+                const size_t row = (size_t)b * TW;
+                const uint32_t wl = (w0 >= 0 && w0 < TW) ? bits[(row + w0) * N + j] : 0u;
+                const uint32_t wh = (w0 + 1 >= 0 && w0 + 1 < TW) ? bits[(row + w0 + 1) * N + j] : 0u;
+                v = ((((uint64_t)wh) << 32) | wl) >> off;
             }
-            w[e / 2] = v[0] | (v[1] << 16);
+            m[rr] = (uint32_t)v;
         }
-        out[q] = uint4{w[0], w[1], w[2], w[3]};
+        const int ne = min(32, T - 32 * tc);
+        for (int e = 0; e < ne; ++e) {
+            uint32_t w[4];
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr)
+                w[pr] = (((m[2 * pr] >> e) & 1u) ? 0x3F80u : 0u) | (((m[2 * pr + 1] >> e) & 1u) ? 0x3F800000u : 0u);
+            out[((size_t)(32 * tc + e) * BO + bo) * Np + j] = uint4{w[0], w[1], w[2], w[3]};
+        }
     }
 }
 
@@ -409,8 +423,10 @@ void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hi
     hipLaunchKernelGGL(pack_gr_kernel, dim3(blocks), dim3(256), 0, stream, gr, a.T, a.B, a.Bp, a.N,
                        a.Np, a.Kp, const_cast<uint4*>(a.ahi), const_cast<uint4*>(a.amd),
                        a.planes == 2 ? nullptr : const_cast<uint4*>(a.alo));
-    hipLaunchKernelGGL(pack_spikes_kernel, dim3(blocks), dim3(256), 0, stream, bits, a.lo, a.T, a.B,
-                       a.Bp, a.N, a.Np, a.Kp, const_cast<uint4*>(a.yb));
+    const size_t chunks = (size_t)((a.T + 31) / 32) * (a.Bp / 8) * a.Np;
+    const unsigned sblocks = (unsigned)std::min<size_t>((chunks + 255) / 256, 65535u * 4);
+    hipLaunchKernelGGL(pack_spikes_kernel, dim3(sblocks), dim3(256), 0, stream, bits, a.lo, a.T, a.B,
+                       a.Bp, a.N, a.Np, const_cast<uint4*>(a.yb));
     const int tiles = (a.Np / kWT) * (a.Np / kWT);
     const dim3 grid((unsigned)(tiles * (a.Bp / 32)));
     if (a.planes == 2) {
