@@ -200,6 +200,42 @@ def test_hybrid_fwd_bwd_matches_oracle(dev, case):
                  scale(gref['base']), 'dbase')
 
 
+# the reference's invariant (tests/test_hybrid_delay_invariance.py:59-78) across the two HIP
+# paths: the hybrid layer with every offset 0 is the axonal layer with d = base -- the same
+# spikes, and dx, dW and dd (axonal) = dbase (hybrid) to the fp32 tolerance
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', [(24, 3, 64, (0.0, 12.0), 0.0), (24, 2, 96, (1.0, 6.0), 1.0)],
+                         ids=['T24B3N64s0', 'T24B2N96s1'])
+def test_hybrid_zero_offsets_equal_axonal_on_device(dev, case):
+    from delrec.kernels import AxonalRecdelHip
+    T, B, N, (lo, hi), sigma = case
+    g = gen(3)
+    x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
+    W = torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)
+    base = lo + torch.rand(N, generator=g) * (hi - lo)
+    gy = torch.randn(T, B, N, generator=g)
+    lif = lif_params()
+
+    layer = hybrid_layer(N, W, base, torch.zeros(N, N), dev, sigma_init=sigma)
+    xh = x.to(dev).requires_grad_(True)
+    yh = layer.multi_step_forward_hybrid_triton(xh)
+    (yh * gy.to(dev)).sum().backward()
+
+    xa, Wa, da = (t.to(dev).requires_grad_(True) for t in (x, W, base))
+    ya = AxonalRecdelHip.apply(xa, Wa, None, da, torch.zeros(N, device=dev), None, sigma, lif.tau,
+                               lif.v_threshold, lif.v_reset, False, lif.detach_reset, 1, 1.0, False, 0,
+                               2.0, lif.decay_input)
+    (ya * gy.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    assert torch.equal(yh.detach(), ya.detach()), 'spike trains differ'
+    print(f'  spikes identical ({int(ya.sum())} spikes of {ya.numel()})')
+    scale = lambda r: ATOL * max(1.0, float(r.abs().max()))
+    assert_close(xh.grad.cpu(), xa.grad.cpu(), RTOL, scale(xa.grad), 'dx')
+    assert_close(layer.recurrent_weights.grad.float().cpu(), Wa.grad.cpu(), RTOL, scale(Wa.grad), 'dW')
+    assert_close(layer.parametrizations.recurrent_delays.original.grad.cpu(), da.grad.cpu(), RTOL,
+                 scale(da.grad), 'dd / dbase')
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize('case', HYB_CASES[:5] + HYB_CASES[6:], ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}{"bf16" if c[5] else ""}s{c[6]}'
                                                     for c in HYB_CASES[:5] + HYB_CASES[6:]])
