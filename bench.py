@@ -280,10 +280,11 @@ def cpu_model():
 def cpu_baseline(layer, x, w, budget_s=60.0):
     """The oracle (pure-PyTorch v2 scan, autograd BPTT, fp32) on the host cores, on bounded
     samples of the same workload: the layer's own weights and delays and the first T' steps
-    of the same input at full B and N, scaled to neuron-timesteps/s. The whole run where one
-    pass fits a quarter of the budget (C1, C2), else T' = 32 (C3-C5: the v2 scan's work per
-    step does not depend on T); a second sample at T' / 2 checks that the time per step does
-    not depend on T' (the scaling assumed), reported as the ratio of the two per-step times."""
+    of the same input at full B and N, scaled to neuron-timesteps/s. The median of 3 samples
+    (the reference profiler's protocol is a median of repeats) at the whole T where three
+    passes fit the budget (C1-C3), else at T' = 32, 16 or 8 (C4, C5: the v2 scan's work per
+    step does not depend on T); the same at T' / 2 checks that the time per step does not
+    depend on T' (the scaling assumed), reported as the ratio of the two per-step times."""
     from oracle import neuron as oneuron, scans
     from oracle.delays import hybrid_delays
     cores = max(1, len(os.sched_getaffinity(0)))
@@ -313,16 +314,28 @@ def cpu_baseline(layer, x, w, budget_s=60.0):
 
     tw = min(T, 8)
     per_step = one(tw) / tw                       # warmup, and the cost estimate
-    Tl = T if per_step * T * 1.5 * 2 < budget_s / 2 else min(T, 32)
+    # the median of 3 samples at T' and at T' / 2: T' = T where that fits the budget,
+    # else the largest of 32, 16, 8 steps that does (one sample where none does)
+    runs = 3
+    Tl = T
+    while Tl > 8 and per_step * Tl * 1.5 * runs > budget_s:
+        Tl = min(Tl, 32) if Tl > 32 else Tl // 2
+    if per_step * Tl * 1.5 * runs > budget_s:
+        runs = 1
     Ts = max(1, Tl // 2)
-    runs = 2 if per_step * Tl * 1.5 * 2 < budget_s / 2 else 1
-    t_long = min(one(Tl) for _ in range(runs))
-    t_short = min(one(Ts) for _ in range(runs))
+
+    def median(xs):
+        xs = sorted(xs)
+        return xs[len(xs) // 2]
+
+    t_long = median([one(Tl) for _ in range(runs)])
+    t_short = median([one(Ts) for _ in range(runs)])
     nts = Tl * B * N / t_long
     return {'value': nts, 'unit': 'neuron-timesteps/s', 'cores': cores, 'kind': 'port',
             'cpu_model': cpu_model(),
             'sample': f'oracle v2 scan + autograd BPTT, fp32, same weights/delays/input, full B={B} '
-                      f'N={N}, first {Tl} of T={T} steps (best of {runs} after a warmup), scaled per '
+                      f'N={N}, first {Tl} of T={T} steps ({"median of 3" if runs == 3 else "1 sample"} '
+                      f'after a warmup), scaled per '
                       f'neuron-timestep; one layer (stacked layers have the same shape)',
             'seconds_per_sample': t_long,
             'linearity': {'T_short': Ts, 'T_long': Tl, 's_per_step_short': t_short / Ts,
@@ -339,6 +352,59 @@ def calibrate_copy(mib):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({'copy_bytes_read': n * 4, 'copy_bytes_written': n * 4, 'launches': 5}), flush=True)
+
+
+def measure_peaks():
+    """Achievable peaks on this GPU, beside the datasheet figures: HBM bandwidth of a plain
+    device copy (1 GiB read + 1 GiB written, torch's copy kernel) and the MFMA rate of a
+    register-only loop of independent bf16 / fp32 matrix instructions on every CU
+    (``delrec_peak_mfma``); each the median of 5 timed launches after a warmup, timed with
+    events on the stream the work runs on (the reference profiler's protocol,
+    experiments/profiling/profile_kernels.py:65-66,165-176, is a median of repeats)."""
+    from delrec import _lib
+    dev = torch.device('cuda:0')
+    st = torch.cuda.current_stream()
+
+    def median_ms(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(st)
+            fn()
+            b.record(st)
+            b.synchronize()
+            ts.append(a.elapsed_time(b))
+        return sorted(ts)[len(ts) // 2]
+
+    n = (1 << 30) // 4
+    src = torch.rand(n, device=dev)
+    dst = torch.empty_like(src)
+    copy_ms = median_ms(lambda: dst.copy_(src))
+    del src, dst
+    out = {'copy_GBps': 2.0 * n * 4 / (copy_ms * 1e-3) / 1e9, 'copy_bytes': 2 * n * 4}
+    sink = torch.empty(1024 * 1024, device=dev)
+    for kind, name, iters in ((0, 'mfma_bf16_TFLOPs', 20000), (1, 'mfma_fp32_TFLOPs', 20000)):
+        flops = [0.0]
+
+        def run(kind=kind, iters=iters):
+            flops[0] = _lib.peak_mfma(kind, iters, sink, st.cuda_stream)
+
+        ms = median_ms(run)
+        out[name] = flops[0] / (ms * 1e-3) / 1e12
+    out['datasheet'] = {'hbm_GBps': PEAK_HBM / 1e9, 'bf16_TFLOPs': PEAK_BF16 / 1e12, 'fp32_TFLOPs': PEAK_FP32 / 1e12}
+    return out
+
+
+def with_measured(roof, peaks):
+    """Add the measured peak of the roofline's bound and the fraction of it achieved."""
+    if roof['unit'] == 'GB/s':
+        meas = peaks['copy_GBps']
+    else:
+        meas = peaks['mfma_bf16_TFLOPs'] if roof['peak'] * 1e12 == PEAK_BF16 else peaks['mfma_fp32_TFLOPs']
+    roof['peak_measured'] = meas
+    roof['frac_of_measured'] = roof['achieved'] / meas
 
 
 def load_traffic(kernel, config):
@@ -402,7 +468,9 @@ def measure(name, steps, warmup, with_cpu):
     peak = peak_of(w)
     t_bound = None
     if w['bound'] != 'cpu':
-        peak_c = PEAK_BF16 if w['bound'] == 'bf16' else PEAK_FP32
+        # compute priced at the peak of the weights' type: BF16 MFMA for bf16 W (C3, C5),
+        # FP32 otherwise
+        peak_c = PEAK_BF16 if w['w_bf16'] else PEAK_FP32
         t_bound = nl * max(work['bytes'] * nt_layer / PEAK_HBM, work['flops'] * nt_layer / peak_c)
 
     # the dominant kernel: the time scan with the longest average launch, priced against
@@ -503,12 +571,17 @@ def main():
         line['inter_linear_ms'] = rec['inter_linear_ms']
     if 'cpu_baseline' in rec:
         line['cpu_baseline'] = rec['cpu_baseline']
+    # measured achievable peaks, and each dominant kernel's fraction of the measured one
+    peaks = measure_peaks()
+    line['peaks'] = peaks
+    with_measured(line['roofline'], peaks)
     extra = [c for c in args.extra.split(',') if c]
     if extra:
         line['extra'] = {}
         for c in extra:
             print(f'[bench] extra workload {c}', file=sys.stderr, flush=True)
             line['extra'][c] = measure(c, args.steps, args.warmup, not args.no_cpu)
+            with_measured(line['extra'][c]['roofline'], peaks)
     print(json.dumps(line), flush=True)
 
 

@@ -149,10 +149,16 @@ typedef struct {
     uint32_t* bits;
     void* workspace;
     size_t workspace_bytes;
-    /* hybrid only (0 otherwise): the offset range and the smallest delay, for the
-     * offset-stacked scans, which apply when off_count > 0 (off_count = largest - smallest
-     * offset + 1, at most 16) and d_min >= s_uniform - 1 (every tap at a lag >= 1). The
-     * caller reads them with the window length (d_min = min over base[j] + offsets[i,j]). */
+    /* hybrid only (0 otherwise): the offset range and a bound of the smallest delay, for
+     * the offset-stacked and arrival scans, which apply when off_count > 0 (off_count =
+     * largest - smallest offset + 1, at most 16) and d_min >= s_uniform - 1. Those forms give
+     * every source the triangle of base[j] + off_min, so d_min must be at most
+     * min over j of float32(base[j] + off_min) -- NOT the smallest materialised delay, which
+     * can be larger when the source of the smallest base has no connection at off_min.
+     * The caller reads them with the window length. A call that breaks either contract
+     * (an offset outside [off_min, off_min + off_count), or a source whose taps reach a lag
+     * < 1 in those forms) gets NaN in the outputs that connection or source reaches,
+     * never silently dropped taps. */
     float d_min;
     int32_t off_min;
     int32_t off_count;
@@ -283,7 +289,18 @@ int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_
 int delrec_scan_timing(int32_t capacity);
 int delrec_scan_timing_read(float* ms, int32_t* kinds, int32_t capacity);
 
+/* Benchmark hook, with no counterpart in the reference: the achievable MFMA rate. Launches
+ * on `stream` a loop of independent matrix instructions from registers only (kind 0: bf16
+ * v_mfma_f32_16x16x32_bf16, kind 1: fp32 v_mfma_f32_16x16x4_f32), `iters` iterations on two
+ * workgroups of 8 waves per CU, and writes the flops that launch issues to *flops; the
+ * caller times it (events on the same stream). sink: device scratch of at least
+ * 1024 floats per CU (DELREC_ERR_WORKSPACE otherwise). */
+int delrec_peak_mfma(int32_t kind, int32_t iters, float* sink, size_t sink_bytes, double* flops, void* stream);
+
 const char* delrec_strerror(int status);
+/* "delrec-mi355x <DELREC_ABI_VERSION> (gfx950)": a binding checks it before use (the
+ * argument structs change between versions). */
+#define DELREC_ABI_VERSION "0.3.0"
 const char* delrec_version(void);
 
 #ifdef __cplusplus

@@ -9,6 +9,7 @@
 #include <atomic>
 #include <chrono>
 #include <initializer_list>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -618,7 +619,15 @@ void delrec::ensure_lds(const void* fn, size_t bytes) {
 
 extern "C" {
 
-const char* delrec_version(void) { return "delrec-mi355x 0.1.0 (gfx950)"; }
+int delrec_peak_mfma(int32_t kind, int32_t iters, float* sink, size_t sink_bytes, double* flops, void* stream) {
+    if ((kind != 0 && kind != 1) || iters <= 0 || !sink || !flops) return DELREC_ERR_ARG;
+    const int blocks = peak_mfma_blocks(num_cus());
+    if (sink_bytes < (size_t)blocks * 512 * sizeof(float)) return DELREC_ERR_WORKSPACE;
+    *flops = launch_peak_mfma(kind, iters, sink, blocks, static_cast<hipStream_t>(stream));
+    return finish_launch();
+}
+
+const char* delrec_version(void) { return "delrec-mi355x " DELREC_ABI_VERSION " (gfx950)"; }
 
 const char* delrec_strerror(int status) {
     switch (status) {
@@ -949,7 +958,8 @@ int syn_fwd_arrive(const delrec_syn_fwd_args* a, const ArriveShape& ar, hipStrea
     int* lof = cv.take<int>((size_t)N);
     float* h = cv.take<float>((size_t)ar.kf * N);
     if (!wpk || !lof || !h) return DELREC_ERR_WORKSPACE;
-    launch_pack_hybrid(static_cast<const uint16_t*>(a->W), a->offsets, N, wpk, s, a->off_min, ar.sh);
+    launch_pack_hybrid(static_cast<const uint16_t*>(a->W), a->offsets, N, wpk, s, a->off_min, ar.sh,
+                       a->off_count);
     HybTaps tp{};   // kf rows: a run shorter than kf gets taps of weight 0 past its triangle
     tp.N = N; tp.KF = ar.kf; tp.omin = a->off_min; tp.s = a->s_uniform; tp.base = a->base; tp.lof = lof; tp.h = h;
     launch_hyb_taps(tp, s);
@@ -1217,6 +1227,11 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         gf.KS = Nf == 0 ? 1 : far256 ? lagstep_gemm256_splits(B * P, Nfp, hq.Kt, num_cus())
                                      : lagstep_splits(B * P, Nfp, hq.Kt, num_cus(), fcol);
         gf.part = fpart; gf.cm = 0;
+        if (getenv("DELREC_LOG_PLAN"))
+            fprintf(stderr, "[delrec] hybrid offset-stacked backward: T=%d B=%d N=%d D=%d P=%d; near sources %d "
+                    "(product KS=%d, %d row tiles); far sources %d (product KS=%d, %s tiles, %d row tiles); "
+                    "LIF grid %d x %d\n", T, B, N, hq.D, P, Nn, Nn > 0 ? gn.KS : 0, (B + 127) / 128, Nf,
+                    Nf > 0 ? gf.KS : 0, far256 ? "256x256" : "128x256", (B * P + 255) / 256, ntiles, (B + 63) / 64);
         HybBwd l{};
         l.T = T; l.B = B; l.N = N; l.Nk = hq.Nk; l.KF = KF; l.R = hq.R; l.P = P; l.lda = hq.lda;
         l.npart = npart; l.KSn = Nn > 0 ? gn.KS : 0; l.Nnp = Nnp; l.ntile = ntile; l.perm = perm;
@@ -1312,7 +1327,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         if (st) return st;
         launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
         if (a->dW || a->dd || a->ds) {
-            launch_lag_bf16(g, gr, a->bits, s);
+            launch_lag_bf16(g, a->drop ? gr : a->dx, a->bits, s);
             LagGemm f{};
             f.N = N; f.KS = q.KS; f.W = a->W; f.w_bf16 = a->w_bf16; f.s = a->s; f.s_uniform = a->s_uniform;
             f.pw = g.pw; f.pd = g.pd; f.ps = g.ps;
@@ -1353,7 +1368,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     if (st) return st;
     launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);
     if (a->dW || a->dd || a->ds) {
-        launch_lag_bf16(g, gr, a->bits, s);
+        launch_lag_bf16(g, a->drop ? gr : a->dx, a->bits, s);
         LagGemm f{};
         f.N = N; f.KS = q.KS; f.W = a->W; f.w_bf16 = a->w_bf16; f.s = a->s; f.s_uniform = a->s_uniform;
         f.pw = g.pw; f.pd = g.pd; f.ps = g.ps;

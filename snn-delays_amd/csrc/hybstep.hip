@@ -75,8 +75,14 @@ __global__ void __launch_bounds__(256) hyb_pack_kernel(HybPack p) {
         const bool ok = i < p.N && j < p.N;
         const size_t c = ok ? (size_t)i * p.N + j : 0;
         w[e] = ok ? load_w(p.W, p.w_bf16, c) : 0.0f;
-        e8[e] = ok ? (int)p.off[c] - p.omin : -1;
+        e8[e] = ok ? (int)p.off[c] - p.omin : -1;   // -1: no connection
+        if (ok && e8[e] < 0) e8[e] = -2;               // -2: outside the range
     }
+    // an offset outside the caller's range [omin, omin + D) would drop its connection: it is
+    // packed as a NaN weight in slice 0 instead, so that the products it enters become NaN
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        if (e8[e] >= p.D) e8[e] = -2;
     const size_t plane = (size_t)p.D * NB * p.Np;
     for (int q = 0; q < p.D; ++q) {
         const int want = FWD ? p.D - 1 - q : q;
@@ -86,7 +92,8 @@ __global__ void __launch_bounds__(256) hyb_pack_kernel(HybPack p) {
             uint32_t h2[2], l2[2];
 #pragma unroll
             for (int f = 0; f < 2; ++f) {
-                const float m = e8[e + f] == want ? w[e + f] : 0.0f;
+                const int ef = e8[e + f];
+                const float m = ef == want ? w[e + f] : (ef < -1 && q == 0 ? __builtin_nanf("") : 0.0f);
                 h2[f] = hyb_bf16_rne(m);
                 l2[f] = hyb_bf16_rne(m - __uint_as_float(h2[f] << 16));
             }
@@ -101,14 +108,21 @@ __global__ void __launch_bounds__(256) hyb_pack_kernel(HybPack p) {
 
 // Each source's first lag of non-zero weight lof_j and its KF tap weights h[f * N + j] at the
 // smallest offset: c_j = 1 + (base_j + 0 + 1 * omin), the parametrisation's fp32 sum.
+// The offset-stacked and arrival forms need that first lag >= 1 for every source (the
+// caller's d_min = min_j base_j + omin >= s - 1); a source that breaks it would lose the taps
+// of lags < 1 silently, so its taps are written as NaN instead (every output it reaches
+// becomes NaN).
 __global__ void __launch_bounds__(256) hyb_taps_kernel(HybTaps p) {
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= p.N) return;
     const float c = 1.0f + (p.base[j] + 0.0f + 1.0f * (float)p.omin);
     const float s = p.s, s2 = s * s;
-    const int lof = max(1, (int)floorf(c - s) + 1);
+    const int first = (int)floorf(c - s) + 1;
+    const int lof = max(1, first);
     p.lof[j] = lof;
-    for (int f = 0; f < p.KF; ++f) p.h[(size_t)f * p.N + j] = tri_weight((float)(lof + f), c, s, s2);
+    const bool bad = first < 1;
+    for (int f = 0; f < p.KF; ++f)
+        p.h[(size_t)f * p.N + j] = bad ? __builtin_nanf("") : tri_weight((float)(lof + f), c, s, s2);
 }
 
 // Forward step t, one thread per (b, neuron i) over the padded width Nk: rec = sum_ks part +

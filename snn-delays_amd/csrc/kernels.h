@@ -375,9 +375,14 @@ void launch_max_to_host(const float* x, int n, uint32_t ticket, unsigned long lo
 void launch_axonal_bwd_sums(const AxTail& q, const float* part, int B, int N, hipStream_t stream);
 
 void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream);
-// wpk[o*N + i] = W[i*N + o] (bf16 bits) << 16 | uint8(off[i*N + o] - omin) << sh (low 16 bits)
+// wpk[o*N + i] = W[i*N + o] (bf16 bits) << 16 | uint8(off[i*N + o] - omin) << sh (low 16 bits);
+// D > 0: a connection whose off - omin lies outside [0, D) gets a NaN weight and offset 0
+// peaks.hip: a register-only MFMA loop (kind 0: bf16 16x16x32, 1: fp32 16x16x4) over
+// `blocks` workgroups; returns the flops one launch issues. sink: blocks * 512 floats.
+int peak_mfma_blocks(int cus);
+double launch_peak_mfma(int kind, int iters, float* sink, int blocks, hipStream_t stream);
 void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream,
-                        int omin = 0, int sh = 0);
+                        int omin = 0, int sh = 0, int D = 0);
 // event-driven forward, ring in LDS, one receiver per lane, kf >= ceil(2 s_max) taps
 bool launch_syn_fwd_scatter(const SynFwd& a, int kf, int block, size_t lds, hipStream_t stream);
 bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);

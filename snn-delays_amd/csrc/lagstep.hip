@@ -617,7 +617,7 @@ __global__ void __launch_bounds__(256) lagstep_lif_bwd_kernel(LagStepLif p) {
     const float da = lif_dx(k, du);
     const float gr = da * (p.drop ? p.drop[bj] : 1.0f);
     p.dx[o] = da;
-    p.gr[o] = gr;
+    if (p.drop) p.gr[o] = gr;   // else gr == dx: the lag correlation reads dx
     p.dbp[bj] = last ? gr : p.dbp[bj] + gr;
     const uint32_t hi = bf16_bits_rne(gr);
     p.hist[ho] = (uint16_t)hi;

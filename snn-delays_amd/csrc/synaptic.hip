@@ -382,18 +382,25 @@ __global__ void __launch_bounds__(1024) syn_fwd_scatter(SynFwd p) {
 }
 
 // wpk[o*N + i] = W[i*N + o] << 16 | uint8(off[i*N + o] - omin) << sh (the low 16 bits)
-// through 32 x 32 LDS tiles
+// through 32 x 32 LDS tiles. With D > 0 the offsets must lie in [omin, omin + D) (the ring
+// the arrival forward sizes from the caller's range): a connection outside it would land in
+// another slot, so it is packed as a NaN weight at offset 0 instead (its receiver's outputs
+// become NaN as soon as its source fires).
 __global__ void __launch_bounds__(256) pack_hybrid_kernel(const uint16_t* __restrict__ W,
                                                           const int8_t* __restrict__ off, int N, int omin,
-                                                          int sh, uint32_t* __restrict__ wpk) {
+                                                          int sh, int D, uint32_t* __restrict__ wpk) {
     __shared__ uint32_t tile[32][33];
     const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
     for (int r = threadIdx.y; r < 32; r += 8) {
         const int i = by + r, o = bx + threadIdx.x;
         uint32_t v = 0;
-        if (i < N && o < N)
-            v = ((uint32_t)W[(size_t)i * N + o] << 16) |
-                (((uint32_t)(uint8_t)(off[(size_t)i * N + o] - omin) << sh) & 0xFFFFu);
+        if (i < N && o < N) {
+            const int e = (int)off[(size_t)i * N + o] - omin;
+            if (D > 0 && (e < 0 || e >= D))
+                v = 0x7FC00000u;
+            else
+                v = ((uint32_t)W[(size_t)i * N + o] << 16) | (((uint32_t)(uint8_t)e << sh) & 0xFFFFu);
+        }
         tile[r][threadIdx.x] = v;
     }
     __syncthreads();
@@ -404,9 +411,9 @@ __global__ void __launch_bounds__(256) pack_hybrid_kernel(const uint16_t* __rest
 }
 
 void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream, int omin,
-                        int sh) {
+                        int sh, int D) {
     const dim3 grid((N + 31) / 32, (N + 31) / 32), block(32, 8);
-    hipLaunchKernelGGL(pack_hybrid_kernel, grid, block, 0, stream, W, off, N, omin, sh, wpk);
+    hipLaunchKernelGGL(pack_hybrid_kernel, grid, block, 0, stream, W, off, N, omin, sh, D, wpk);
 }
 
 // Forward in gather form, for rings too large for LDS: lane i owns receiver i and sums
@@ -812,7 +819,7 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_kernel(SynBwd p) {
             const float da = lif_dx(k, du);
             const float gr = da * m[q];
             p.dx[o] = da;
-            p.gr[o] = gr;
+            if (p.drop) p.gr[o] = gr;   // else gr == dx: the lag correlation reads dx
             dbacc[q] += gr;
             float* row = ring + (size_t)j * RP;
             row[tmod] = gr;
@@ -1078,7 +1085,9 @@ __global__ void __launch_bounds__(MAXT) syn_bwd_hyb(SynBwd p) {
         const float gr = da * m;
         const bool live = t >= 0;
         raw_buffer_store_f32(da, step_rsrc(dxa, live ? row_bytes : 0u), soff, 0, 0);
-        raw_buffer_store_f32(gr, step_rsrc(gra, live ? row_bytes : 0u), soff, 0, 0);
+        // gr differs from dx only under a dropout mask: otherwise the store is dropped (a
+        // zero-sized descriptor) and the lag correlation reads dx
+        raw_buffer_store_f32(gr, step_rsrc(gra, (live && p.drop) ? row_bytes : 0u), soff, 0, 0);
         dxa -= step_b;
         gra -= step_b;
         dbacc += (live && act) ? gr : 0.0f;
@@ -1159,7 +1168,9 @@ __global__ void __launch_bounds__(1024) syn_bwd_hyb_g(SynBwd p) {
     float* ghist = smem + (size_t)rows * GS;              // [RG][NL]
     // the offsets' span must fit the ring pitch (the host sized GS from the caller's
     // off_count): a wider one makes every output NaN instead of reading other rows
-    const bool bad = 2 * D > GS || RG < 2;
+    // and every source's first lag must be >= 1 (c0 = lob + omin with the offsets' own
+    // smallest value): a caller's d_min that claimed so wrongly gives NaN, not dropped taps
+    const bool bad = 2 * D > GS || RG < 2 || __syncthreads_or(act && c0 < 1) != 0;
     for (int q = tid; q < rows * GS + RG * NL; q += blockDim.x) smem[q] = 0.0f;
     __syncthreads();
 
@@ -1263,7 +1274,9 @@ __global__ void __launch_bounds__(1024) syn_bwd_hyb_g(SynBwd p) {
         const float gr = da * m;
         const bool live = t >= 0;
         raw_buffer_store_f32(da, step_rsrc(dxa, live ? row_bytes : 0u), soff, 0, 0);
-        raw_buffer_store_f32(gr, step_rsrc(gra, live ? row_bytes : 0u), soff, 0, 0);
+        // gr differs from dx only under a dropout mask: otherwise the store is dropped (a
+        // zero-sized descriptor) and the lag correlation reads dx
+        raw_buffer_store_f32(gr, step_rsrc(gra, (live && p.drop) ? row_bytes : 0u), soff, 0, 0);
         dxa -= step_b;
         gra -= step_b;
         dbacc += (live && act) ? gr : 0.0f;

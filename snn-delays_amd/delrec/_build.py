@@ -19,8 +19,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG.parent / 'csrc'
 INCLUDE = PKG.parent.parent / 'include'
 OUT = PKG / 'libdelrec_hip.so'
-SOURCES = ('abi.hip', 'axonal.hip', 'gemm.hip', 'hybstep.hip', 'lagmm.hip', 'lagstep.hip', 'spikelinear.hip',
-           'synaptic.hip')
+SOURCES = ('abi.hip', 'axonal.hip', 'gemm.hip', 'hybstep.hip', 'lagmm.hip', 'lagstep.hip', 'peaks.hip',
+           'spikelinear.hip', 'synaptic.hip')
 ARCH = os.environ.get('DELREC_OFFLOAD_ARCH', 'gfx950')
 
 

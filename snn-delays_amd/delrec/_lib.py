@@ -33,7 +33,7 @@ EXPORTS = ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_axonal_bwd_noalloc'
            'delrec_syn_bwd', 'delrec_spike_linear_fwd',
            'delrec_lif_fwd', 'delrec_lif_bwd', 'delrec_delay_grad', 'delrec_query_workspace',
            'delrec_strerror', 'delrec_version', 'delrec_scan_timing', 'delrec_scan_timing_read',
-           'delrec_max_post', 'delrec_max_take')
+           'delrec_max_post', 'delrec_max_take', 'delrec_peak_mfma')
 
 
 class DelrecError(RuntimeError):
@@ -103,6 +103,9 @@ class LifBwdArgs(ctypes.Structure):
                 ('lif', Lif), ('dx', c_vp)]
 
 
+# the DELREC_ABI_VERSION of include/delrec.h these ctypes structs mirror
+ABI_VERSION = '0.3.0'
+
 _lib = None
 
 
@@ -134,6 +137,12 @@ def load():
     lib.delrec_max_post.argtypes = [c_vp, c_i32, ctypes.POINTER(ctypes.c_uint32), c_vp]
     lib.delrec_max_take.restype = c_i32
     lib.delrec_max_take.argtypes = [ctypes.c_uint32, ctypes.POINTER(c_f32), c_i32]
+    lib.delrec_peak_mfma.restype = c_i32
+    lib.delrec_peak_mfma.argtypes = [c_i32, c_i32, c_vp, c_size, ctypes.POINTER(ctypes.c_double), c_vp]
+    got = lib.delrec_version().decode()
+    if got.split()[1:2] != [ABI_VERSION]:
+        raise ImportError(f'{LIB_PATH} reports "{got}"; this binding lays out the argument structs of '
+                          f'ABI {ABI_VERSION}: rebuild the library')
     _lib = lib
     return lib
 
@@ -306,3 +315,12 @@ def delay_grad(C, W, d, sigma, N, Lm, out, stream):
 
 def version():
     return load().delrec_version().decode()
+
+
+def peak_mfma(kind, iters, sink, stream):
+    """Launch the register-only MFMA loop (kind 0: bf16, 1: fp32) on ``stream``; returns the
+    flops the launch issues (the caller times it)."""
+    flops = ctypes.c_double(0.0)
+    _check('delrec_peak_mfma', load().delrec_peak_mfma(kind, iters, ptr(sink), sink.numel() * sink.element_size(),
+                                                        ctypes.byref(flops), stream))
+    return flops.value

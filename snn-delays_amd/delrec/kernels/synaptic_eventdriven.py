@@ -27,9 +27,9 @@ def _spread(layer, device):
 
 def hybrid_form(d_min, s_uniform, off_range):
     """The hybrid's scan-form fields: ``(d_min, off_min, off_count, flags)`` for the argument
-    structs and the workspace query (bit 2: every tap at a lag >= 1, i.e. d_min >= s - 1 in
-    float32 as the entry point compares; bits 16..23: the offset count); zeros when the
-    offset range is unknown (``off_range`` None)."""
+    structs and the workspace query (bit 2: every source's taps at lags >= 1, i.e.
+    d_min = min_j base_j + off_min >= s - 1 in float32 as the entry point compares; bits
+    16..23: the offset count); zeros when the offset range is unknown (``off_range`` None)."""
     if off_range is None:
         return 0.0, 0, 0, 0
     off_min, off_count = off_range
@@ -59,7 +59,11 @@ def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop,
         d_max, s_max = read_scalars(d_all.max(), s_vec.max())
         d_min = d_max
     elif off_range is not None:
-        (d_max, d_min), s_max = read_scalars(d_all.max(), d_all.min()), s_uniform
+        # the offset-stacked and arrival forms give every source the triangle of its
+        # smallest possible delay, base_j + (smallest offset): they apply when that is
+        # >= s - 1 for every source, i.e. min_j base_j + off_min in fp32 (a bound of the
+        # smallest delay that also covers a source without a connection at off_min)
+        (d_max, d_min), s_max = read_scalars(d_all.max(), base.min() + float(off_range[0])), s_uniform
     else:
         (d_max,), s_max = read_scalars(d_all.max()), s_uniform
         d_min = d_max

@@ -102,3 +102,91 @@ class OracleModel(torch.nn.Module):
 
     def clamp_delays(self):
         self.inner.clamp_delays()
+
+
+# Per-element error budget of a weight gradient, beyond the fixed rtol / atol: an fp32 (or
+# split-bf16) computation of dW[i, j] = sum_k term_k carries rounding of each term's operands
+# and of the accumulation. Modelled as independent relative errors of at most EPS per term,
+# the error of the sum has a standard deviation of about EPS * sqrt(Q) / sqrt(3) with
+# Q = sum_k term_k^2 -- a per-element figure from that element's own terms. KAPPA * EPS *
+# sqrt(Q) with KAPPA = 4 is about 7 standard deviations; a dropped term or a wrong index gives
+# an error of the size of a whole term, about sqrt(Q / n) for n terms, which is
+# 1 / (KAPPA EPS sqrt(n)) > 50 times that budget for every n below 10^6 at EPS = 2^-15.
+#   EPS = 2^-15 for bf16 W: the backward takes gr as two bf16 planes (2^-16 per term) in the
+#         future-gradient product and again in the lag correlation behind dW;
+#   EPS = 2^-20 for fp32 W: three bf16 planes (2^-24) plus gr's own deviation from float64
+#         after an fp32 BPTT chain (about 1e-6 relative).
+GRAD_KAPPA = 4.0
+
+
+def grad_eps(w_bf16):
+    return 2.0 ** -15 if w_bf16 else 2.0 ** -20
+
+
+def dw_term_sq_synaptic(gr, y, h, idx):
+    """Q[i, j] = sum_l h[i, j, l]^2 sum_{t >= l, b} gr[t, b, i]^2 y[t - l, b, j] for the
+    (i, j) pairs ``idx`` (two index tensors): the squared terms of a synaptic / hybrid
+    dW = sum_l h * C_l, C_l = sum gr(t) y(t - l)^T (spikes are 0 / 1). ``h``: (N, N, L)."""
+    ii, jj = idx
+    g2 = gr[:, :, ii].double() ** 2            # (T, B, m)
+    yy = y[:, :, jj].double()                  # (T, B, m)
+    T, L = g2.shape[0], h.shape[-1]
+    q = torch.zeros(ii.numel(), dtype=torch.float64)
+    for l in range(1, min(L, T)):
+        c = (g2[l:] * yy[:T - l]).sum(dim=(0, 1))
+        q += h[ii, jj, l].double() ** 2 * c
+    return q
+
+
+def dw_term_sq_axonal(gr, y, h, idx):
+    """Q[i, j] = sum_{t, b} gr[t, b, i]^2 z[t, b, j]^2 with the delayed trace
+    z[t, b, j] = sum_l h[j, l] y[t - l, b, j] (``h``: (N, L)) for the pairs ``idx``."""
+    ii, jj = idx
+    T, L = y.shape[0], h.shape[-1]
+    yy = y[:, :, jj].double()
+    z = torch.zeros_like(yy)
+    for l in range(1, min(L, T)):
+        z[l:] += h[jj, l].double() * yy[:T - l]
+    return ((gr[:, :, ii].double() ** 2) * z ** 2).sum(dim=(0, 1))
+
+
+def check_elementwise(name, got, ref64, rtol, atol, ref32=None, term_sq=None, eps=None):
+    """``|got - ref64| <= atol + rtol |ref64| + floor`` per element. Where the fixed
+    tolerance alone is missed, the element's floor is the larger of: the fp32 oracle's own
+    distance from float64 at that element (``ref32``: a callable returning that tensor; an
+    fp32 computation is not held closer than the fp32 restatement gets there), and, for a
+    weight gradient, ``GRAD_KAPPA * eps * sqrt(Q)`` from that element's own terms
+    (``term_sq``: a callable of the missing elements' index tuple returning Q). Prints the
+    counts; asserts."""
+    got = got.detach().double().cpu()
+    ref = ref64.detach().double().cpu()
+    err = (got - ref).abs()
+    bound = atol + rtol * ref.abs()
+    miss = err > bound
+    n_miss = int(miss.sum())
+    fl32 = flq = 0.0
+    if n_miss:
+        idx = miss.nonzero(as_tuple=True)
+        floor = torch.zeros(n_miss, dtype=torch.float64)
+        if ref32 is not None:
+            d32 = (ref32().detach().double().cpu() - ref)[idx].abs()
+            floor = torch.maximum(floor, d32)
+            fl32 = float(d32.max())
+        if term_sq is not None:
+            fq = GRAD_KAPPA * eps * term_sq(idx).sqrt()
+            floor = torch.maximum(floor, fq)
+            flq = float(fq.max())
+        ok = err[idx] <= bound[idx] + floor
+        still = int((~ok).sum())
+    else:
+        still = 0
+    print(f'  {name}: max abs err {float(err.max()):.3e}, |ref|max {float(ref.abs().max()):.3e}; '
+          f'{n_miss} of {err.numel()} elements past rtol {rtol:g} / atol {atol:g}; per-element floors up '
+          f'to {fl32:.3e} (fp32 oracle) / {flq:.3e} (term budget); {still} past their floor', flush=True)
+    if still:
+        ok_all = torch.ones_like(miss)
+        ok_all[idx] = ok
+        worst = int((err - bound).masked_fill(ok_all, -1.0).argmax())
+        at = tuple(int(i) for i in torch.unravel_index(torch.tensor(worst), ref.shape))
+        raise AssertionError(f'{name}: {still} of {err.numel()} elements differ; at {at}: got '
+                             f'{float(got.reshape(-1)[worst]):.6e} ref {float(ref.reshape(-1)[worst]):.6e}')

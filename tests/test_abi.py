@@ -30,6 +30,9 @@ def test_library_loads_and_exports_every_symbol():
     for name in _declared_functions():
         assert hasattr(lib, name), name
     assert _lib.version().startswith('delrec-mi355x')
+    # the binding's struct layouts are those of the header's ABI version
+    hdr = re.search(r'#define DELREC_ABI_VERSION "([^"]+)"', open(HEADER).read()).group(1)
+    assert hdr == _lib.ABI_VERSION and _lib.version().split()[1] == hdr
     assert lib.delrec_strerror(0) == b'ok'
     assert b'workspace' in lib.delrec_strerror(3)
 

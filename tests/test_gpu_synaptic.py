@@ -377,3 +377,103 @@ def test_delay_grad_known_answer(dev):
         assert ref[:, :3].abs().max() > 0
         if sigma == 0.0:
             torch.testing.assert_close(actual, expected, atol=1e-6, rtol=1e-6)
+
+
+def _negative_base_without_smallest_offset(N, K, seed):
+    """Bases in [0, 8) except source 0 at -0.5, whose column has no connection at the
+    smallest offset 0 (every offset in column 0 is 1 .. K): its materialised delays are all
+    >= 0.5, so the smallest materialised delay (0.5 or more) is >= s - 1 = 0, while the
+    source's delay at the smallest offset, base_0 + 0 = -0.5, is not."""
+    g = gen(seed)
+    base = torch.rand(N, generator=g) * 8.0
+    base[0] = -0.5
+    offsets = torch.randint(K + 1, (N, N), generator=g).float()
+    offsets[:, 0] = 1.0 + torch.randint(K, (N,), generator=g).float()
+    assert bool((offsets[:, 1:] == 0).any())
+    return base, offsets
+
+
+def _hybrid_run(dev, T, B, N, W, base, offsets, bf16, sigma, x, gy):
+    layer = hybrid_layer(N, W, base, offsets, dev, bf16=bf16, sigma_init=sigma)
+    xg = x.to(dev).requires_grad_(True)
+    y = layer.multi_step_forward_hybrid_triton(xg)
+    (y * gy.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    return y.detach().cpu(), xg.grad.cpu(), layer
+
+
+# the source whose base is the smallest has no connection at the smallest offset: the
+# offset-stacked and arrival forms (which give a source the triangle of base_j + smallest
+# offset) must not be taken on the smallest *materialised* delay -- whatever form each
+# setting selects must match the oracle
+NEG_BASE_FORMS = [{}, {'DELREC_HYB_FWD': '1'}, {'DELREC_SYN_HYBSTEP': '1', 'DELREC_HYB_FWD': '0'},
+                  {'DELREC_SYN_HYBSTEP': '1'}, {'DELREC_SYN_BWD_HYB_G': '1'}]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('bf16', [True, False], ids=['bf16', 'fp32'])
+@pytest.mark.parametrize('env', NEG_BASE_FORMS, ids=['default', 'arrival', 'hybstep', 'hybstep_arrival', 'hyb_g'])
+def test_hybrid_negative_base_without_smallest_offset(dev, env, bf16, monkeypatch):
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    T, B, N, K = 20, 3, 64, 4
+    print(f'forms {env} bf16={bf16}', flush=True)
+    base, offsets = _negative_base_without_smallest_offset(N, K, seed=4)
+    g = gen(6)
+    x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
+    x[:, :, 0] += 1.5                      # source 0 fires often
+    W = torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)
+    if bf16:
+        W = W.bfloat16().float()
+    gy = torch.randn(T, B, N, generator=g)
+    lif = lif_params()
+    y_ref, u_ref, gref = oracle_synaptic(x, W, None, lif, 0.0, gy, base=base, offsets=offsets)
+    assert float(y_ref[:, :, 0].sum()) > 0
+    y, dx, layer = _hybrid_run(dev, T, B, N, W, base, offsets, bf16, 0.0, x, gy)
+    flip = first_flip(y, y_ref, u_ref, lif.v_threshold)
+    assert flip is None, f'near-threshold flip at t={flip}'
+    rtol = 2e-2 if bf16 else RTOL
+    scale = lambda r: ATOL * max(1.0, float(r.abs().max()))
+    assert_close(dx, gref['x'], rtol, scale(gref['x']), 'dx')
+    assert_close(layer.recurrent_weights.grad.float(), gref['W'], rtol, scale(gref['W']), 'dW')
+    assert_close(layer.parametrizations.recurrent_delays.original.grad, gref['base'], rtol,
+                 scale(gref['base']), 'dbase')
+
+
+# the same case handed to the C ABI with a d_min that wrongly claims every source's taps
+# at lags >= 1 (the smallest materialised delay instead of min_j base_j + off_min): the
+# forms that rely on it write NaN where the dropped taps would have landed -- never a
+# silently wrong result
+@pytest.mark.gpu
+@pytest.mark.parametrize('env', [{'DELREC_HYB_FWD': '1'}, {'DELREC_SYN_HYBSTEP': '1', 'DELREC_HYB_FWD': '0'},
+                                 {'DELREC_SYN_BWD_HYB_G': '1'}], ids=['arrival', 'hybstep', 'hyb_g'])
+def test_hybrid_wrong_d_min_gives_nan(dev, env, monkeypatch):
+    from delrec.kernels import synaptic_eventdriven as se
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    real = se.hybrid_form
+    monkeypatch.setattr(se, 'hybrid_form', lambda d_min, s, rng: real(0.5, s, rng))
+    T, B, N, K = 20, 3, 64, 4
+    base, offsets = _negative_base_without_smallest_offset(N, K, seed=4)
+    g = gen(6)
+    x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
+    x[:, :, 0] += 1.5
+    W = (torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)).bfloat16().float()
+    gy = torch.randn(T, B, N, generator=g)
+    seen = {}
+    fwd = se.syn_forward
+
+    def keep(*a, **k):
+        out = fwd(*a, **k)
+        seen['u'] = out[1].detach()
+        return out
+
+    import delrec.kernels.synaptic_hybrid as sh
+    monkeypatch.setattr(sh, 'syn_forward', keep)
+    y, dx, _ = _hybrid_run(dev, T, B, N, W, base, offsets, True, 0.0, x, gy)
+    u = seen['u'].cpu()
+    print(f'  NaN membranes {int(u.isnan().sum())}, NaN dx {int(dx.isnan().sum())}', flush=True)
+    if env.get('DELREC_SYN_BWD_HYB_G'):
+        assert bool(dx.isnan().all())                # the whole backward refuses
+    else:
+        assert bool(u.isnan().any()) and bool(dx.isnan().any())

@@ -380,3 +380,49 @@ def test_plain_lif_layer_is_the_recurrent_scan_without_weights():
     y1, e1 = scans.axonal_v2(x, torch.zeros(6, 6, dtype=torch.float64), torch.ones(6, dtype=torch.float64), lif)
     assert torch.equal(y0, y1)
     torch.testing.assert_close(e0['u'], e1['u'], rtol=0, atol=0)
+
+
+@pytest.mark.parametrize('kind', ['axonal', 'synaptic', 'hybrid'])
+@pytest.mark.parametrize('soft', [False, True])
+def test_teacher_forcing_with_own_spikes_reproduces_the_free_run(kind, soft):
+    """Every GPU parity test at a workload shape runs the oracle forced with the kernel's
+    spike train. Forced with the oracle's own free-run spikes it must be the free run, bit
+    for bit: spikes, membranes and every gradient (float64)."""
+    g = torch.Generator().manual_seed(31)
+    T, B, N = 14, 3, 12
+    x = (torch.randn(T, B, N, generator=g) * 1.3 + 0.4).double()
+    W = (torch.randn(N, N, generator=g) / N ** 0.5).double()
+    gy = torch.randn(T, B, N, generator=g).double()
+    lif = neuron.LIFParams(tau=2.0, v_threshold=1.0, v_reset=None if soft else 0.0)
+    if kind == 'axonal':
+        d = (torch.rand(N, generator=g) * 5.0).double()
+    elif kind == 'synaptic':
+        d = (torch.rand(N, N, generator=g) * 5.0).double()
+    else:
+        d = (torch.rand(N, generator=g) * 4.0).double()
+        off = torch.randint(3, (N, N), generator=g).double()
+
+    def run(forced):
+        lv = {'x': x.clone().requires_grad_(True), 'W': W.clone().requires_grad_(True),
+              'd': d.clone().requires_grad_(True)}
+        if kind == 'axonal':
+            y, ext = scans.axonal_v2(lv['x'], lv['W'], lv['d'], lif, sigma=0.6, forced=forced)
+        elif kind == 'synaptic':
+            y, ext = scans.synaptic_v2(lv['x'], lv['W'], lv['d'], lif, sigma=0.6, forced=forced)
+        else:
+            y, ext = scans.synaptic_v2(lv['x'], lv['W'], lv['d'] + 0.0 + 1.0 * off, lif, sigma=0.0,
+                                       forced=forced)
+        (y * gy).sum().backward()
+        return y.detach(), ext['u'].detach(), {k: v.grad for k, v in lv.items()}
+
+    y0, u0, g0 = run(None)
+    assert 0 < float(y0.sum()) < y0.numel()
+    y1, u1, g1 = run(y0.clone())
+    assert torch.equal(y0, y1) and torch.equal(u0, u1)
+    for k in g0:
+        assert torch.equal(g0[k], g1[k]), k
+    # and a forced train that differs makes the run follow it (the check is not vacuous)
+    flip = y0.clone()
+    flip[3, 1, 2] = 1.0 - flip[3, 1, 2]
+    y2, u2, _ = run(flip)
+    assert torch.equal(y2, flip) and not torch.equal(u2, u0)
