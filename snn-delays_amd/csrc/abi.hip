@@ -383,7 +383,8 @@ void hybstep_ws(C& c, int T, int B, int N, int L, int D, int KF, bool fwd, bool 
     c.template take<int>((size_t)N);                             // first lag per source
     c.template take<float>((size_t)KF * N);                      // tap weights per source
     c.template take<int>((size_t)N);                             // source order
-    c.template take<int>((size_t)q.Nk / hyb_bwd_tile() + 1);     // near columns per tile
+    c.template take<int>((size_t)N);                             // far column per source
+    c.template take<uint32_t>((size_t)kHybNearMax * kHybNearMax); // W and offsets between near neurons
     c.template take<float>((size_t)q.R * N * B);                 // ring of G
 }
 
@@ -1146,17 +1147,15 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
     if (hybrid && !lagstep && !hybstep) launch_pack_offq(static_cast<const int8_t*>(dt), (size_t)N * lay.NT, meta, offq, s);
 
     if (hybstep) {
-        // reverse-time scan, the sources split by first lag: near ones (lof < P) through one
-        // offset-stacked GEMM per step over their columns, far ones through one GEMM per block
-        // of P steps with rows (b, step of the block); one LIF launch per step
+        // reverse-time scan in blocks of P steps, the sources split by first lag: far ones
+        // (lof >= P) through one product per block whose rows are (b, step of the block) and one
+        // launch for the block's LIF backward; near ones (lof < P) through a second product per
+        // block and a per-batch-row chain through the block's steps (hybstep.hip)
         const int KF = taps;
         const HybStepDims hq = hybstep_dims(T, B, N, a->L, a->off_count, KF, num_cus());
         const int planes = a->w_bf16 ? 1 : 2;
         const int fcol = hyb_bwd_far_cols(planes);   // the far GEMM's workgroup columns
         const HybBwdSizes hz = hyb_bwd_sizes(hq, B, num_cus(), fcol);
-        const int P = hq.P;
-        const int JT = hyb_bwd_tile();
-        const int ntiles = hq.Nk / JT;   // LIF tiles over the padded width (Nk: a multiple of 32)
         uint4* Pw = cv.take<uint4>(planes * hz.planes);
         uint16_t* ghi = cv.take<uint16_t>((size_t)B * hq.lda);
         uint16_t* glo = cv.take<uint16_t>((size_t)B * hq.lda);
@@ -1166,30 +1165,39 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         int* lof = cv.take<int>((size_t)N);
         float* h = cv.take<float>((size_t)KF * N);
         int* perm = cv.take<int>((size_t)N);
-        int* ntile = cv.take<int>((size_t)ntiles + 1);
+        int* colf = cv.take<int>((size_t)N);
+        uint32_t* wnp = cv.take<uint32_t>((size_t)kHybNearMax * kHybNearMax);
         float* ring = cv.take<float>((size_t)hq.R * N * B);
-        if (!Pw || !ghi || !glo || !npart || !fpart || !state || !lof || !h || !perm || !ntile || !ring)
+        if (!Pw || !ghi || !glo || !npart || !fpart || !state || !lof || !h || !perm || !colf || !wnp || !ring)
             return DELREC_ERR_WORKSPACE;
         HybTaps tp{};
         tp.N = N; tp.KF = KF; tp.omin = a->off_min; tp.s = a->s_uniform; tp.base = a->base; tp.lof = lof; tp.h = h;
         launch_hyb_taps(tp, s);
         // the split needs the first lags on the host: one read-back per call
-        std::vector<int> lof_h(N), perm_h(N), ntile_h(ntiles + 1);
+        std::vector<int> lof_h(N), perm_h(N), colf_h(N);
         if (hipMemcpyAsync(lof_h.data(), lof, (size_t)N * sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
             hipStreamSynchronize(s) != hipSuccess)
             return DELREC_ERR_LAUNCH;
-        int Nn = 0;
-        for (int x = 0; x < ntiles; ++x) {
-            ntile_h[x] = Nn;
-            for (int j = x * JT; j < std::min(N, (x + 1) * JT); ++j)
-                if (lof_h[j] < P) perm_h[Nn++] = j;
+        // the longest block (at most kHybBlockMax steps) whose near sources the chain takes;
+        // P = 1 has none (every lof >= 1)
+        int P = kHybBlockMax, Nn = 0;
+        for (;; P /= 2) {
+            Nn = 0;
+            for (int j = 0; j < N; ++j) Nn += lof_h[j] < P ? 1 : 0;
+            if (P == 1 || (Nn <= kHybNearMax && hyb_bwd_near_lds(P, hq.D, Nn) <= (size_t)max_lds_bytes())) break;
         }
-        ntile_h[ntiles] = Nn;
         const int Nf = N - Nn;
-        for (int j = 0, c = Nn; j < N; ++j)
-            if (lof_h[j] >= P) perm_h[c++] = j;
+        for (int j = 0, cn = 0, cf = Nn; j < N; ++j) {
+            if (lof_h[j] < P) {
+                perm_h[cn++] = j;
+                colf_h[j] = -1;
+            } else {
+                colf_h[j] = cf - Nn;
+                perm_h[cf++] = j;
+            }
+        }
         if (hipMemcpyAsync(perm, perm_h.data(), (size_t)N * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
-            hipMemcpyAsync(ntile, ntile_h.data(), (size_t)(ntiles + 1) * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipMemcpyAsync(colf, colf_h.data(), (size_t)N * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
             hipStreamSynchronize(s) != hipSuccess)
             return DELREC_ERR_LAUNCH;
         const int Nnp = (Nn + 127) / 128 * 128, Nfp = (Nf + fcol - 1) / fcol * fcol;
@@ -1202,64 +1210,69 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         if (Nn > 0) {
             pk.Np = Nnp; pk.c0 = 0; pk.nc = Nn; pk.out = Pn;
             launch_hyb_pack(pk, false, s);
+            launch_hyb_near_pack(pk, wnp, s);
         }
         if (Nf > 0) {
             pk.Np = Nfp; pk.c0 = Nn; pk.nc = Nf; pk.out = Pf;
             launch_hyb_pack(pk, false, s);
         }
-        // gr past the last step (slices T ..): every column of slices 0 .. T - 1 is written by
-        // step t's LIF before a product reads it
+        // gr before the first step (front pad) and past the last one (slices PF + T ..) are 0;
+        // every column of the block's slices is written before a product reads them (the far
+        // LIF launch writes the far gr and 0 for the near columns, the near chain fills those)
         const int hslices = (int)(hq.lda / hq.Nk);
-        launch_hist_zero(ghi, B, hq.lda, hq.Nk, T, hslices, s);
-        launch_hist_zero(glo, B, hq.lda, hq.Nk, T, hslices, s);
+        launch_hist_zero(ghi, B, hq.lda, hq.Nk, 0, hq.PF, s);
+        launch_hist_zero(glo, B, hq.lda, hq.Nk, 0, hq.PF, s);
+        launch_hist_zero(ghi, B, hq.lda, hq.Nk, hq.PF + T, hslices, s);
+        launch_hist_zero(glo, B, hq.lda, hq.Nk, hq.PF + T, hslices, s);
         // gr == dx unless a dropout mask scales it
         const bool need_gr = a->drop != nullptr;
-        LagStepGemm gn{};   // step t: near G(t + 1) from history slices t + 1 .. t + D
-        gn.a0 = ghi; gn.a1 = glo; gn.lda = hq.lda; gn.rs = 0; gn.B = B; gn.rows = B; gn.rp = 1;
-        gn.p0 = Pn; gn.p1 = planes > 1 ? Pn + nplane : nullptr; gn.Np = Nnp; gn.Kt = hq.Kt;
-        gn.KS = Nn > 0 ? lagstep_splits(B, Nnp, hq.Kt, num_cus()) : 1; gn.Nk = hq.Nk; gn.part = npart;
-        gn.cm = 1;   // the LIF reads its near columns whole
-        LagStepGemm gf = gn;   // block t0: far G(t0 + 1 + tt), row (b, tt) shifted by tt slices
-        gf.rows = B * P; gf.rp = P; gf.rs = hq.Nk;
-        gf.p0 = Pf; gf.p1 = planes > 1 ? Pf + fplane : nullptr; gf.Np = Nfp;
+        LagStepGemm gf{};   // block t0: far G(t0 + 1 + tt), row (b, tt) shifted by tt slices
+        gf.a0 = ghi; gf.a1 = glo; gf.lda = hq.lda; gf.rs = hq.Nk; gf.B = B; gf.rows = B * P; gf.rp = P;
+        gf.p0 = Pf; gf.p1 = planes > 1 ? Pf + fplane : nullptr; gf.Np = Nfp; gf.Kt = hq.Kt; gf.Nk = hq.Nk;
         // one-plane P: 256 x 256 tiles of 8 waves (128 x 256 tiles of 4 waves with DELREC_FAR256=0)
         const bool far256 = planes == 1 && getenv_flag_off("DELREC_FAR256");
         gf.KS = Nf == 0 ? 1 : far256 ? lagstep_gemm256_splits(B * P, Nfp, hq.Kt, num_cus())
                                      : lagstep_splits(B * P, Nfp, hq.Kt, num_cus(), fcol);
         gf.part = fpart; gf.cm = 0;
+        LagStepGemm gn = gf;   // block t0: near G(t0 - P + 2 + tt), the block's steps' t + 1
+        gn.p0 = Pn; gn.p1 = planes > 1 ? Pn + nplane : nullptr; gn.Np = Nnp;
+        gn.KS = Nn > 0 ? lagstep_splits(B * P, Nnp, hq.Kt, num_cus()) : 1;
+        gn.part = npart;
         if (getenv("DELREC_LOG_PLAN"))
             fprintf(stderr, "[delrec] hybrid offset-stacked backward: T=%d B=%d N=%d D=%d P=%d; near sources %d "
-                    "(product KS=%d, %d row tiles); far sources %d (product KS=%d, %s tiles, %d row tiles); "
-                    "LIF grid %d x %d\n", T, B, N, hq.D, P, Nn, Nn > 0 ? gn.KS : 0, (B + 127) / 128, Nf,
-                    Nf > 0 ? gf.KS : 0, far256 ? "256x256" : "128x256", (B * P + 255) / 256, ntiles, (B + 63) / 64);
+                    "(product KS=%d, %d row tiles, chain of %d-row workgroups); far sources %d (product KS=%d, "
+                    "%s tiles, %d row tiles); far LIF grid %d x %d\n", T, B, N, hq.D, P, Nn, Nn > 0 ? gn.KS : 0,
+                    (B * P + 127) / 128, 2, Nf, Nf > 0 ? gf.KS : 0, far256 ? "256x256" : "128x256",
+                    (B * P + 255) / 256, (hq.Nk + 63) / 64, (B + 15) / 16);
         HybBwd l{};
-        l.T = T; l.B = B; l.N = N; l.Nk = hq.Nk; l.KF = KF; l.R = hq.R; l.P = P; l.lda = hq.lda;
-        l.npart = npart; l.KSn = Nn > 0 ? gn.KS : 0; l.Nnp = Nnp; l.ntile = ntile; l.perm = perm;
-        l.fpart = fpart; l.KSf = gf.KS; l.Nfp = Nfp; l.Nn = Nn; l.Nf = Nf;
+        l.T = T; l.B = B; l.N = N; l.Nk = hq.Nk; l.KF = KF; l.R = hq.R; l.P = P; l.D = hq.D; l.PF = hq.PF;
+        l.lda = hq.lda;
+        l.npart = npart; l.KSn = Nn > 0 ? gn.KS : 0; l.Nnp = Nnp; l.Nn = Nn; l.perm = perm;
+        l.fpart = fpart; l.KSf = Nf > 0 ? gf.KS : 0; l.Nfp = Nfp; l.Nf = Nf; l.colf = colf;
+        l.wnp = wnp;
         l.lof = lof; l.h = h; l.drop = a->drop; l.lif = make_lif(a->lif); l.state = state;
         l.hhi = ghi; l.hlo = glo; l.u_in = a->u; l.gy = a->gy; l.dx = a->dx;
         l.gr = need_gr ? gr : nullptr; l.dbp = a->db ? part : nullptr; l.ring = ring;
         const bool timed = scan_begin(DELREC_WS_SYN_BWD, s);
-        for (int t0 = T - 1; t0 >= 0; t0 -= P) {
+        bool ok = true;
+        for (int t0 = T - 1; t0 >= 0 && ok; t0 -= P) {
             if (Nf > 0) {
-                gf.aoff = (size_t)(t0 + 1) * hq.Nk;
+                gf.aoff = (size_t)(hq.PF + t0 + 1) * hq.Nk;
                 if (far256)
                     launch_lagstep_gemm256(gf, s);
                 else
                     launch_lagstep_gemm(gf, 2, s, planes, fcol / 2);
-                l.t0 = t0;
-                launch_hyb_bwd_far(l, s);
             }
-            for (int t = t0; t >= std::max(t0 - P + 1, 0); --t) {
-                if (Nn > 0) {
-                    gn.aoff = (size_t)(t + 1) * hq.Nk;
-                    launch_lagstep_gemm(gn, 2, s, planes);
-                }
-                l.t = t;
-                launch_hyb_bwd_lif(l, s);
+            l.t0 = t0;
+            launch_hyb_bwd_farblk(l, s);
+            if (Nn > 0) {
+                gn.aoff = (size_t)(hq.PF + t0 - P + 2) * hq.Nk;
+                launch_lagstep_gemm(gn, 2, s, planes);
+                ok = launch_hyb_bwd_near(l, s);
             }
         }
         scan_end(timed, s);
+        if (!ok) return DELREC_ERR_UNSUPPORTED;
         int st = finish_launch();
         if (st) return st;
         if (a->db) launch_reduce_rows(part, B, N, a->db, nullptr, nullptr, s);

@@ -182,201 +182,398 @@ __global__ void __launch_bounds__(256) hyb_lif_fwd_kernel(HybLif p) {
     p.hlo[ho] = (uint16_t)hyb_bf16_rne(z - __uint_as_float(hi << 16));
 }
 
-// Backward step t over a tile of 16 sources / neurons j0 .. j0 + 15 x 64 batch rows (256
-// threads; 1024 workgroups at C5: twice the loads in flight of 32-source tiles, which were
-// 2 % slower, and 8-source tiles 9 %), three phases:
-//  1 G_j(t + 1) of the tile's near sources, the near product's columns ntile[x] ..
-//    ntile[x + 1] - 1: sum_ks npart[ks][c][b] in a fixed order (column-major partials, one
-//    column per wave, 16 partials in flight per lane), into LDS;
-//  2 (transposed: one source per wave at a time, its 64 batch rows on the lanes): those
-//    G(t + 1) into ring slot (t + 1) mod R; then gfut_j(t) = sum_f h_j(lof_j + f) G_j(t + lof_j
-//    + f), from LDS for tau = t + 1 (lof_j = 1, f = 0: always a near source) and from the
-//    ring otherwise (0 for tau >= T: gr past the last step is 0), all ring reads of the
-//    wave's sources issued before any is used;
-//  3 (row-major): the LIF backward on gy + gfut, outputs dx (and gr when it differs), the db
-//    partial, and gr(t) split into the hi / lo history planes at slice t.
-// The ring slot of tau is rewritten with G(tau - R) only after every step that reads G(tau)
-// (steps >= tau - L + 1) has run, for R >= L - 1; this step's reads (tau >= t + 2) and writes
-// (tau = t + 1) never share a slot.
-constexpr int kHybTapsMax = 8;
-constexpr int kHybBwdTile = 16;
+// The backward runs in blocks of P steps t0 - P + 1 .. t0, latest block first, as four launches
+// per block (no launch per step):
+//  1 the far product (lagstep.hip): G_j(tau) of the far sources (lof_j >= P) for the P steps
+//    tau = t0 + 1 .. t0 + P, rows (b, tau); its history slices (> t0) are complete;
+//  2 hyb_bwd_farblk_kernel: those G into the ring and the whole block's LIF backward of the
+//    far sources: gfut_j(t) = sum_f h_j(f) G_j(t + lof_j + f) reads only tau >= t + P > t0;
+//    it writes the far sources' gr(t) into the history for the block's slices, and 0 for the
+//    near sources' columns there;
+//  3 the near product (lagstep.hip): G_j(t + 1) of the near sources for the block's steps t,
+//    rows (b, t + 1), which reads the block's slices with the near columns still 0;
+//  4 hyb_bwd_near_kernel: per batch row, the near sources' chain through the block, latest
+//    step first, adding the part the product could not see -- sum_i W_ij gr_i(t + 1 + e_ij)
+//    over near receivers i whose step t + 1 + e_ij lies in the block -- from an LDS window of
+//    the near gr it produces.
+// Batch rows are independent, so step 4 needs no synchronisation beyond its workgroup, and
+// the only sequential chain left inside a block is the near sources' (C5: 5 % of them).
+
+namespace {
+
+__device__ __forceinline__ float hyb_sel4(const float (&g)[kHybBlockMax], int i) {
+    float v = g[0];
+#pragma unroll
+    for (int q = 1; q < kHybBlockMax; ++q) v = i == q ? g[q] : v;
+    return v;
+}
+
+}  // namespace
+
+// Step 2: a tile of 64 neurons x 16 batch rows per workgroup, in three phases:
+//  1 (64 neurons on the lanes, 4 rows per wave: coalesced over j) the far sources' G(tau),
+//    tau = t0 + 1 .. t0 + P, summed over the product's splits (split groups of 4 loads in
+//    flight) into LDS; the LIF operands u, gy into registers; 0 into the history at the
+//    block's slices for the near and padding columns;
+//  2 (16 rows on the lanes, 4 neurons each: the ring [slot][j][b] has b fastest) those G into
+//    the ring, and each source's window of the P + KF - 1 values G_j(tau), tau = t0 - P + 1 +
+//    lof_j + w, that the block's taps read -- from LDS for tau <= t0 + P, else from the ring
+//    (written by earlier launches), 0 past the last step -- into LDS;
+//  3 (neurons on the lanes again) the LIF backward of the block's steps, latest first, with
+//    gfut_j(t) = sum_f h_j(f) window[t - (t0 - P + 1) + f].
+constexpr int kSplitGroup = 4;
+constexpr int kFarRows = 16;
 
 template <int KF>
-__global__ void __launch_bounds__(256) hyb_bwd_lif_kernel(HybBwd p) {
-    constexpr int JT = kHybBwdTile;
-    __shared__ float sg[JT][65];
-    __shared__ float sf[JT][65];
-    __shared__ int ncl[JT];
+__global__ void __launch_bounds__(256) hyb_bwd_farblk_kernel(HybBwd p) {
+    constexpr int W = kHybBlockMax + KF - 1;
+    __shared__ float sG[kHybBlockMax][kFarRows][65];
+    __shared__ float sW[W][kFarRows][65];
+    __shared__ int slof[64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j0 = blockIdx.x * JT, b0 = blockIdx.y * 64;
-    const int t = p.t, N = p.N, B = p.B, T = p.T, R = p.R;
-    const int lo = p.ntile[blockIdx.x], nn = p.ntile[blockIdx.x + 1] - lo;
-    if (tid < JT) ncl[tid] = -1;
-    // loads that do not wait for this step's G, issued first so that their latency overlaps
-    // phases 1 and 2: the LIF operands of phase 3 and the ring reads of phase 2
-    // phase 3 lays a wave over LR = 64 / JT rows of JT columns; 4 LR rows per pass
-    constexpr int LR = 64 / JT;
-    const int jl3 = lane & (JT - 1), j3 = j0 + jl3;
-    const int r0 = LR * w + lane / JT;
+    const int j0 = blockIdx.x * 64, b0 = blockIdx.y * kFarRows;
+    const int t0 = p.t0, P = p.P, T = p.T, N = p.N, B = p.B, R = p.R;
+    const int tb = max(t0 - P + 1, 0);
+    const int ns = t0 - tb + 1;                       // steps in this block
+    const int tbase = t0 - P + 1;
     const size_t BN = (size_t)B * N;
-    const bool last = t == T - 1;
-    constexpr int E3 = 64 / (4 * LR);
-    float uu[E3], gyv[E3], lam[E3], dbv[E3], mv[E3];
-#pragma unroll
-    for (int e = 0; e < E3; ++e) {
-        const int b = b0 + r0 + 4 * LR * e;
-        const bool ok = b < B && j3 < N;
-        const size_t bj = (size_t)(ok ? b : 0) * N + (ok ? j3 : 0), o = (size_t)t * BN + bj;
-        uu[e] = ok ? p.u_in[o] : 0.0f;
-        gyv[e] = ok ? p.gy[o] : 0.0f;
-        lam[e] = (ok && !last) ? p.state[bj] : 0.0f;
-        dbv[e] = (ok && !last && p.dbp) ? p.dbp[bj] : 0.0f;
-        mv[e] = (ok && p.drop) ? p.drop[bj] : 1.0f;
-    }
-    constexpr int E = JT / 4;
-    const int tm = t % R;
-    float got[E][KF], hv[E][KF];
-    int lofv[E];
+    const Lif k = p.lif;
+    const bool first = t0 == T - 1;
+    // phase 1: lane = neuron j0 + lane, rows b0 + 4 w + rr
+    const int j = j0 + lane;
+    const bool inj = j < p.Nk;
+    const int lof = j < N ? p.lof[j] : 0;
+    const bool far = j < N && lof >= P;
+    if (w == 0) slof[lane] = far ? lof : -1;
+    const int c = far ? p.colf[j] : 0;
+    constexpr int RW = kFarRows / 4;                  // rows per wave
+    float uu[RW][kHybBlockMax], gyv[RW][kHybBlockMax];
     {
-        const int b = b0 + lane;
-        const bool bok = b < B;
+        const size_t kstride = (size_t)B * P * p.Nfp;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int j = j0 + w + 4 * e;
-            lofv[e] = j < N ? p.lof[j] : 0;
+        for (int rr = 0; rr < RW; ++rr) {
+            const int r = 4 * w + rr, b = b0 + r;
+            const bool ok = far && b < B;
+            float g[kHybBlockMax];
 #pragma unroll
-            for (int f = 0; f < KF; ++f) {
-                hv[e][f] = (j < N && f < p.KF) ? p.h[(size_t)f * N + j] : 0.0f;
-                const int d = lofv[e] + f;   // tau - t, in [1, L - 1]
-                int sl = tm + d;
-                sl = sl >= R ? sl - R : sl;
-                // tau >= t + 2 only: slot (t + 1) mod R, written in phase 2, is never read
-                const bool rd = j < N && f < p.KF && d >= 2 && t + d < T && bok;
-                got[e][f] = rd ? p.ring[((size_t)sl * N + j) * B + b] : 0.0f;
+            for (int tt = 0; tt < kHybBlockMax; ++tt) g[tt] = 0.0f;
+            const float* fp = p.fpart + (size_t)(ok ? b : 0) * P * p.Nfp + c;
+            for (int k0 = 0; k0 < p.KSf; k0 += kSplitGroup) {
+                float v[kSplitGroup][kHybBlockMax];
+#pragma unroll
+                for (int q = 0; q < kSplitGroup; ++q)
+#pragma unroll
+                    for (int tt = 0; tt < kHybBlockMax; ++tt)
+                        v[q][tt] = (ok && k0 + q < p.KSf && tt < P && t0 + 1 + tt < T)
+                                       ? fp[(size_t)(k0 + q) * kstride + (size_t)tt * p.Nfp] : 0.0f;
+#pragma unroll
+                for (int q = 0; q < kSplitGroup; ++q)
+#pragma unroll
+                    for (int tt = 0; tt < kHybBlockMax; ++tt) g[tt] += v[q][tt];
             }
-        }
-    }
-    barrier_lds();   // LDS only: the loads above stay in flight
-    // phase 1: one near column per wave at a time, its 64 batch rows on the lanes (the
-    // partials are column-major: 256 contiguous bytes per partial)
-    {
-        const int b = b0 + lane;
-        const size_t qs = (size_t)p.Nnp * B;
-        for (int cl = w; cl < nn; cl += 4) {
-            float g = 0.0f;
-            if (b < B) {
-                const float* src = p.npart + (size_t)(lo + cl) * B + b;
-                int q = 0;
-                for (; q + 16 <= p.KSn; q += 16) {
-                    float v[16];
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) v[e] = src[(size_t)(q + e) * qs];
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) g += v[e];
+            for (int tt = 0; tt < kHybBlockMax; ++tt) {
+                sG[tt][r][lane] = g[tt];
+                const int t = t0 - tt;
+                const bool live = ok && tt < ns;
+                const size_t o = (size_t)(live ? t : 0) * BN + (size_t)(ok ? b : 0) * N + (far ? j : 0);
+                uu[rr][tt] = live ? p.u_in[o] : 0.0f;
+                gyv[rr][tt] = live ? p.gy[o] : 0.0f;
+            }
+            if (inj && !far && b < B) {
+                const size_t hrow = (size_t)b * p.lda + (size_t)p.PF * p.Nk + j;
+                for (int q = 0; q < ns; ++q) {
+                    p.hhi[hrow + (size_t)(t0 - q) * p.Nk] = 0;
+                    p.hlo[hrow + (size_t)(t0 - q) * p.Nk] = 0;
                 }
-                for (; q < p.KSn; ++q) g += src[(size_t)q * qs];
             }
-            sg[cl][lane] = g;
-            if (lane == 0) ncl[p.perm[lo + cl] - j0] = cl;
         }
     }
-    barrier_lds();
-    // phase 2
+    barrier_lds();   // (LDS only: no global value written here is read back in this launch)
+    // phase 2: lane = row b0 + lane % 16; neurons 16 w + 4 (lane / 16) + q
     {
-        const int b = b0 + lane;
+        const int r = lane & (kFarRows - 1), b = b0 + r;
         const bool bok = b < B;
-        const int s1 = tm + 1 == R ? 0 : tm + 1;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int cl = w + 4 * e;
-            if (cl < nn && t + 1 < T && bok) p.ring[((size_t)s1 * N + p.perm[lo + cl]) * B + b] = sg[cl][lane];
-        }
+        for (int q = 0; q < 4; ++q) {
+            const int jl = 16 * w + 4 * (lane >> 4) + q, jj = j0 + jl;
+            const int lj = slof[jl];
+            if (lj < 0 || !bok) continue;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int jl = w + 4 * e, j = j0 + jl;
-            float gf = 0.0f;
-            if (j < N) {
-                const int cl = ncl[jl];
-                const float g1 = cl >= 0 && t + 1 < T ? sg[cl][lane] : 0.0f;   // near G(t + 1)
+            for (int tt = 0; tt < kHybBlockMax; ++tt)
+                if (tt < P && t0 + 1 + tt < T)
+                    p.ring[((size_t)((t0 + 1 + tt) % R) * N + jj) * B + b] = sG[tt][r][jl];
+            float v[W];
 #pragma unroll
-                for (int f = 0; f < KF; ++f) gf = fmaf(hv[e][f], lofv[e] + f == 1 ? g1 : got[e][f], gf);
+            for (int x = 0; x < W; ++x) {
+                const int tau = tbase + lj + x;
+                const bool rd = x < P + p.KF - 1 && tau < T && tau > t0 + P;
+                v[x] = rd ? p.ring[((size_t)(tau % R) * N + jj) * B + b] : 0.0f;
             }
-            sf[jl][lane] = gf;
+#pragma unroll
+            for (int x = 0; x < W; ++x) {
+                const int tau = tbase + lj + x;
+                sW[x][r][jl] = (tau <= t0 + P && tau < T) ? sG[max(tau - t0 - 1, 0)][r][jl] : v[x];
+            }
         }
     }
     barrier_lds();
-    // phase 3: column jl = lane % JT, rows LR w + lane / JT + 4 LR e (operands loaded on entry)
-    {
-        const Lif k = p.lif;
-        const int jl = jl3, j = j3;
+    // phase 3: lane = neuron j0 + lane, rows 4 w + rr
+    if (!far) return;
+    float hv[KF];
 #pragma unroll
-        for (int e = 0; e < E3; ++e) {
-            const int r = r0 + 4 * LR * e, b = b0 + r;
-            if (b >= B || j >= p.Nk) continue;
-            const size_t ho = (size_t)b * p.lda + (size_t)t * p.Nk + j;
-            if (j >= N) {
-                p.hhi[ho] = 0;
-                p.hlo[ho] = 0;
-                continue;
-            }
-            const float gf = sf[jl][r];
-            const size_t bj = (size_t)b * N + j, o = (size_t)t * BN + bj;
-            const float y = lif_fire(k, uu[e]);
-            const float du = lif_backward(k, gyv[e] + gf, uu[e], y, lam[e]);
-            p.state[bj] = k.decay * du;
+    for (int f = 0; f < KF; ++f) hv[f] = f < p.KF ? p.h[(size_t)f * N + j] : 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+        const int r = 4 * w + rr, b = b0 + r;
+        if (b >= B) break;
+        const size_t bj = (size_t)b * N + j;
+        const size_t hrow = (size_t)b * p.lda + (size_t)p.PF * p.Nk + j;
+        float lam = first ? 0.0f : p.state[bj];
+        float db = (p.dbp && !first) ? p.dbp[bj] : 0.0f;
+        const float m = p.drop ? p.drop[bj] : 1.0f;
+#pragma unroll
+        for (int tt = 0; tt < kHybBlockMax; ++tt) {
+            if (tt >= ns) break;
+            const int t = t0 - tt, row = t - tbase;
+            float gf = 0.0f;
+#pragma unroll
+            for (int f = 0; f < KF; ++f) gf = fmaf(hv[f], sW[row + f][r][lane], gf);
+            const float y = lif_fire(k, uu[rr][tt]);
+            const float du = lif_backward(k, gyv[rr][tt] + gf, uu[rr][tt], y, lam);
+            lam = k.decay * du;
             const float da = lif_dx(k, du);
-            const float gr = da * mv[e];
+            const float gr = da * m;
+            const size_t o = (size_t)t * BN + bj;
             p.dx[o] = da;
             if (p.gr) p.gr[o] = gr;
-            if (p.dbp) p.dbp[bj] = last ? gr : dbv[e] + gr;
+            db += gr;
             const uint32_t hi = hyb_bf16_rne(gr);
-            p.hhi[ho] = (uint16_t)hi;
-            p.hlo[ho] = (uint16_t)hyb_bf16_rne(gr - __uint_as_float(hi << 16));
+            p.hhi[hrow + (size_t)t * p.Nk] = (uint16_t)hi;
+            p.hlo[hrow + (size_t)t * p.Nk] = (uint16_t)hyb_bf16_rne(gr - __uint_as_float(hi << 16));
         }
+        p.state[bj] = lam;
+        if (p.dbp) p.dbp[bj] = db;
     }
 }
 
-// The far product of the block that starts at step t0 (rows (b, tt), tau = t0 + 1 + tt):
-// G_j(tau) = sum_ks fpart[ks][b * P + tt][c] for far column c (source perm[Nn + c]) into
-// ring slot tau mod R. Tile: 64 far columns x 64 batch rows of one tt, summed row-major and
-// stored through an LDS transpose as 256-byte ring rows. Its consumers are steps
-// tau - lof_j - f <= t0 (lof_j >= P), none of which has run.
-__global__ void __launch_bounds__(256) hyb_bwd_far_kernel(HybBwd p) {
-    __shared__ float sg[64][65];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int c0 = blockIdx.x * 64, b0 = blockIdx.y * 64, tt = blockIdx.z;
-    const int B = p.B, N = p.N, P = p.P;
-    const int tau = p.t0 + 1 + tt;
-    if (tau >= p.T) return;   // G past the last step is 0 and never read
+// Step 4: RB = 2 batch rows per workgroup (one workgroup per CU at B = 512), the near sources
+// (compact index c, source perm[c]) on the threads. On entry, from global memory, all of it
+// independent of the chain: the packed near-to-near weights wnp[ci][c] into LDS, the block's
+// near product summed over its splits into LDS, and each (c, row) item's u, gy and older ring
+// values into registers. Per step t, latest first:
+//  a G_j(t + 1) = that product row + sum over near receivers ci of w * gr_ci(t + 1 + e) from
+//    the LDS window of the block's near gr (slot s = step t0 - P + 1 + s; slots >= P, steps
+//    past the block, stay 0: the product already holds those) -- one thread per near source,
+//    its RB rows together; into the ring and an LDS copy of the block's G (tau <= t0 + 1);
+//  b the LIF backward of the items: gfut from that copy (tau <= t0 + 1) or the ring (written
+//    by earlier launches), gr into the history and the window.
+constexpr int kNearRows = 2;
+constexpr int kNearItems = (kHybNearMax * kNearRows + 255) / 256;   // (c, row) items per thread
+
+namespace {
+
+// the window holds each near receiver's slots contiguously, at an odd pitch: the lanes of a
+// wave (sources c, same receiver ci) read slots row + 1 + e of one run -- distinct words in
+// distinct banks, or one broadcast word
+__host__ __device__ inline int near_ldw(int nslot) { return nslot | 1; }
+
+}  // namespace
+
+template <int KF>
+__global__ void __launch_bounds__(256) hyb_bwd_near_kernel(HybBwd p) {
+    constexpr int RB = kNearRows;
+    extern __shared__ float sm[];
+    const int Nn = p.Nn, P = p.P, D = p.D, T = p.T, N = p.N, B = p.B, R = p.R, t0 = p.t0;
+    const int nslot = P + D;
+    const int ldw = near_ldw(nslot);                  // per-receiver pitch of the window
+    const int Nn8 = (Nn + 7) & ~7;                    // receivers padded to the inner loop's groups
+    uint32_t* wl = reinterpret_cast<uint32_t*>(sm);   // [Nn8][Nn] packed weights (rows >= Nn: 0)
+    float* grw = sm + (size_t)Nn8 * Nn;               // [RB][Nn8][ldw]: gr of near receiver ci at slot s
+    float* gnp = grw + (size_t)RB * Nn8 * ldw;        // [P][RB][Nn]: the near product, summed
+    float* gq = gnp + (size_t)P * RB * Nn;            // [P][RB][Nn]: G(tau), slot tau - (t0 - P + 2)
+    const int tid = threadIdx.x;
+    const int b0 = blockIdx.x * RB;
+    const int tb = max(t0 - P + 1, 0);
+    const int ns = t0 - tb + 1;
+    const int tbase = t0 - P + 1;                     // step of window slot 0
+    // start-up: every load that does not depend on the chain, in as few round trips as the
+    // registers allow -- the items' sources, the block product's partials of this
+    // workgroup's rows (16 splits per round), the packed weights (half per round); then the
+    // items' u, gy, older ring values and state
+    const size_t BN = (size_t)B * N;
+    const Lif k = p.lif;
+    const bool first = t0 == T - 1;
+    int jv[kNearItems];
+#pragma unroll
+    for (int e = 0; e < kNearItems; ++e) {
+        const int q = tid + 256 * e, c = q % Nn, r = q / Nn;
+        jv[e] = (q < Nn * RB && b0 + r < B) ? p.perm[c] : -1;
+    }
+    constexpr int GI = (kHybBlockMax * RB * kHybNearMax + 255) / 256;   // product items per thread
+    float gs[GI];
     {
-        const int c = c0 + lane;
-        const bool cok = c < p.Nf;
-        float g[16];
+        const size_t ks_stride = (size_t)B * P * p.Nnp;
+        const int ng = P * RB * Nn;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) g[e] = 0.0f;
-        for (int q = 0; q < p.KSf; ++q) {
-            float v[16];
+        for (int e = 0; e < GI; ++e) gs[e] = 0.0f;
+        for (int k0 = 0; k0 < p.KSn; k0 += 16) {
+            float v[GI][16];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int b = b0 + w + 4 * e;
-                v[e] = (cok && b < B) ? p.fpart[((size_t)q * B * P + (size_t)b * P + tt) * p.Nfp + c] : 0.0f;
+            for (int e = 0; e < GI; ++e) {
+                const int q = tid + 256 * e, c = q % Nn, rr = q / Nn, r = rr % RB, row = rr / RB, b = b0 + r;
+                const bool ok = q < ng && b < B;
+                const float* src = p.npart + ((size_t)(ok ? b : 0) * P + (ok ? row : 0)) * p.Nnp + (ok ? c : 0);
+#pragma unroll
+                for (int x = 0; x < 16; ++x) v[e][x] = (ok && k0 + x < p.KSn) ? src[(size_t)(k0 + x) * ks_stride] : 0.0f;
             }
 #pragma unroll
-            for (int e = 0; e < 16; ++e) g[e] += v[e];
+            for (int e = 0; e < GI; ++e)
+#pragma unroll
+                for (int x = 0; x < 16; ++x) gs[e] += v[e][x];
         }
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sg[lane][w + 4 * e] = g[e];
+        for (int e = 0; e < GI; ++e) {
+            const int q = tid + 256 * e;
+            if (q < ng) gnp[q] = gs[e];
+        }
     }
-    __syncthreads();
-    const int b = b0 + lane;
-    const size_t slot = (size_t)(tau % p.R) * N;
-#pragma unroll 4
-    for (int e = 0; e < 16; ++e) {
-        const int cl = w + 4 * e, c = c0 + cl;
-        if (c < p.Nf && b < B) p.ring[(slot + p.perm[p.Nn + c]) * B + b] = sg[cl][lane];
+    {
+        constexpr int WH = (kHybNearMax * kHybNearMax + 511) / 512;      // weights per thread per round
+        const int nw = Nn * Nn;
+        for (int q = nw + tid; q < Nn8 * Nn; q += 256) wl[q] = 0u;
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            uint32_t v[WH];
+#pragma unroll
+            for (int e = 0; e < WH; ++e) {
+                const int q = (h2 * WH + e) * 256 + tid;
+                v[e] = q < nw ? p.wnp[q] : 0u;
+            }
+#pragma unroll
+            for (int e = 0; e < WH; ++e) {
+                const int q = (h2 * WH + e) * 256 + tid;
+                if (q < nw) wl[q] = v[e];
+            }
+        }
     }
+    for (int q = tid; q < RB * Nn8 * ldw; q += 256) grw[q] = 0.0f;
+    int lofv[kNearItems];
+    float hv[kNearItems][KF], uu[kNearItems][kHybBlockMax], gyv[kNearItems][kHybBlockMax];
+    float rg[kNearItems][kHybBlockMax][KF], lam[kNearItems], db[kNearItems], mv[kNearItems];
+#pragma unroll
+    for (int e = 0; e < kNearItems; ++e) {
+        const int q = tid + 256 * e, r = q / Nn, b = b0 + r;
+        const bool ok = jv[e] >= 0;
+        const int j = ok ? jv[e] : 0;
+        lofv[e] = ok ? p.lof[j] : 0;
+        const size_t bj = (size_t)(ok ? b : 0) * N + j;
+#pragma unroll
+        for (int f = 0; f < KF; ++f) hv[e][f] = (ok && f < p.KF) ? p.h[(size_t)f * N + j] : 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < kHybBlockMax; ++tt) {
+            const int t = t0 - tt;
+            const bool live = ok && tt < ns;
+            const size_t o = (size_t)(live ? t : 0) * BN + bj;
+            uu[e][tt] = live ? p.u_in[o] : 0.0f;
+            gyv[e][tt] = live ? p.gy[o] : 0.0f;
+#pragma unroll
+            for (int f = 0; f < KF; ++f) {
+                const int tau = t + lofv[e] + f;
+                const bool rd = live && f < p.KF && tau < T && tau > t0 + 1;
+                rg[e][tt][f] = rd ? p.ring[((size_t)(tau % R) * N + j) * B + b] : 0.0f;
+            }
+        }
+        lam[e] = (ok && !first) ? p.state[bj] : 0.0f;
+        db[e] = (ok && !first && p.dbp) ? p.dbp[bj] : 0.0f;
+        mv[e] = (ok && p.drop) ? p.drop[bj] : 1.0f;
+    }
+    barrier_lds();
+#pragma unroll
+    for (int tt = 0; tt < kHybBlockMax; ++tt) {
+        if (tt >= ns) break;                          // (static indices into the item arrays)
+        const int t = t0 - tt;
+        const int row = t - tbase;                    // the product's row of tau = t + 1
+        // a: G(t + 1) of the items (one near source and batch row each); the receivers in
+        // groups of 8 (rows past Nn are zero weights), their LDS reads issued together. A
+        // valid offset e < D always lands in the window: slot row + 1 + e < P + D
+#pragma unroll
+        for (int e = 0; e < kNearItems; ++e) {
+            if (jv[e] < 0) continue;
+            const int q = tid + 256 * e, c = q % Nn, r = q / Nn, b = b0 + r;
+            float acc = 0.0f;
+            const uint32_t* wc = wl + c;
+            const float* gw = grw + (size_t)r * Nn8 * ldw + row + 1;   // slot row + 1 + e of receiver ci
+            for (int c0 = 0; c0 < Nn8; c0 += 8) {
+                uint32_t pw[8];
+#pragma unroll
+                for (int x = 0; x < 8; ++x) pw[x] = wc[(size_t)(c0 + x) * Nn];
+                float gv[8];
+#pragma unroll
+                for (int x = 0; x < 8; ++x) gv[x] = gw[(size_t)(c0 + x) * ldw + (int)(pw[x] & 0xFu)];
+#pragma unroll
+                for (int x = 0; x < 8; ++x) acc = fmaf(__uint_as_float(pw[x] & ~0xFu), gv[x], acc);
+            }
+            const float sum = acc + gnp[((size_t)row * RB + r) * Nn + c];
+            gq[((size_t)row * RB + r) * Nn + c] = sum;
+            if (t + 1 < T) p.ring[((size_t)((t + 1) % R) * N + jv[e]) * B + b] = sum;
+        }
+        barrier_lds();
+        // b: the LIF backward of the items
+#pragma unroll
+        for (int e = 0; e < kNearItems; ++e) {
+            if (jv[e] < 0) continue;
+            const int q = tid + 256 * e, c = q % Nn, r = q / Nn, b = b0 + r, j = jv[e];
+            float gf = 0.0f;
+#pragma unroll
+            for (int f = 0; f < KF; ++f) {
+                const int tau = t + lofv[e] + f;
+                float gv = rg[e][tt][f];
+                if (tau <= t0 + 1) gv = tau < T ? gq[((size_t)(tau - tbase - 1) * RB + r) * Nn + c] : 0.0f;
+                gf = fmaf(hv[e][f], gv, gf);
+            }
+            const float y = lif_fire(k, uu[e][tt]);
+            const float du = lif_backward(k, gyv[e][tt] + gf, uu[e][tt], y, lam[e]);
+            lam[e] = k.decay * du;
+            const float da = lif_dx(k, du);
+            const float gr = da * mv[e];
+            const size_t bj = (size_t)b * N + j, o = (size_t)t * BN + bj;
+            p.dx[o] = da;
+            if (p.gr) p.gr[o] = gr;
+            db[e] += gr;
+            const size_t ho = (size_t)b * p.lda + (size_t)(p.PF + t) * p.Nk + j;
+            const uint32_t hi = hyb_bf16_rne(gr);
+            p.hhi[ho] = (uint16_t)hi;
+            p.hlo[ho] = (uint16_t)hyb_bf16_rne(gr - __uint_as_float(hi << 16));
+            grw[((size_t)r * Nn8 + c) * ldw + row] = gr;
+        }
+        barrier_lds();
+    }
+#pragma unroll
+    for (int e = 0; e < kNearItems; ++e) {
+        if (jv[e] < 0) continue;
+        const int q = tid + 256 * e, r = q / Nn, b = b0 + r;
+        const size_t bj = (size_t)b * N + jv[e];
+        p.state[bj] = lam[e];
+        if (p.dbp) p.dbp[bj] = db[e];
+    }
+}
+
+// wnp[ci][c]: the weight of the near connection receiver perm[ci] <- source perm[c], its low 4
+// bits replaced by the offset - omin (< 16): bf16 W exact, fp32 W to 2^-19 relative (finer than
+// the products' two bf16 planes); one thread per pair
+__global__ void __launch_bounds__(256) hyb_near_pack_kernel(HybPack p, uint32_t* __restrict__ wnp) {
+    const int Nn = p.nc;
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (size_t)Nn * Nn) return;
+    const int ci = (int)(q / Nn), c = (int)(q - (size_t)ci * Nn);
+    const size_t o = (size_t)p.perm[ci] * p.N + p.perm[c];
+    const int e = (int)p.off[o] - p.omin;
+    // an offset outside the caller's range [omin, omin + D): a NaN weight at offset 0
+    const bool bad = e < 0 || e >= p.D;
+    const float w = bad ? __builtin_nanf("") : load_w(p.W, p.w_bf16, o);
+    wnp[q] = (__float_as_uint(w) & ~0xFu) | (uint32_t)(bad ? 0 : e);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -635,11 +832,6 @@ bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t 
 
 // ---------------------------------------------------------------------------------------
 
-// steps per block of the backward's far product: C5 measured 90 ms per scan at 4, 94 at 8,
-// 104 at 6, 114 at 16, 123 at 3 (128 x 256 far tiles); 80 at 4, 93 at 8, 104 at 5, 341 at 2
-// with the 256 x 256 far tiles
-constexpr int kHybBlock = 4;
-
 HybStepDims hybstep_dims(int T, int B, int N, int L, int D, int KF, int cus) {
     HybStepDims q{};
     q.Nk = (N + 31) / 32 * 32;
@@ -649,9 +841,12 @@ HybStepDims hybstep_dims(int T, int B, int N, int L, int D, int KF, int cus) {
     q.R = std::max(L, 2);
     q.HW = (std::max(L - 1, 1) + 63) / 64;
     q.Kt = D * q.Nk;
-    q.P = kHybBlock;
-    q.lda = (size_t)(T + D + q.P + 1) * q.Nk;   // slices past the last step read as 0 (the far
-                                                // product of the first block reaches T + P + D - 2)
+    q.P = kHybBlockMax;
+    q.PF = kHybBlockMax;   // zero slices before slice 0: the near product of a last block that
+                           // starts before step 0 reads from slice t0 - P + 2 >= 2 - P
+    q.lda = (size_t)(q.PF + T + D + q.P + 1) * q.Nk;   // slices past the last step read as 0 (the
+                                                       // far product of the first block reaches
+                                                       // T + P + D - 2)
     q.plane = (size_t)(q.Kt / 8) * q.Np;
     q.KS = lagstep_splits(B, q.Np, q.Kt, cus);
     // offsets of 16 or fewer, taps of 8 or fewer, a spike history of two 64-bit words, and
@@ -683,39 +878,57 @@ void launch_hyb_lif(const HybLif& l, int hw, hipStream_t stream) {
         hipLaunchKernelGGL(hyb_lif_fwd_kernel<2>, dim3(blocks), dim3(256), 0, stream, l);
 }
 
-// the LIF tiles cover Nk neurons (the history planes' padding columns are written as 0)
-void launch_hyb_bwd_lif(const HybBwd& a, hipStream_t stream) {
-    const dim3 grid(a.Nk / kHybBwdTile, (a.B + 63) / 64);
+void launch_hyb_bwd_farblk(const HybBwd& a, hipStream_t stream) {
+    const dim3 grid((a.Nk + 63) / 64, (a.B + kFarRows - 1) / kFarRows);
     if (a.KF <= 2)
-        hipLaunchKernelGGL(hyb_bwd_lif_kernel<2>, grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(hyb_bwd_farblk_kernel<2>, grid, dim3(256), 0, stream, a);
     else if (a.KF <= 4)
-        hipLaunchKernelGGL(hyb_bwd_lif_kernel<4>, grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(hyb_bwd_farblk_kernel<4>, grid, dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL(hyb_bwd_lif_kernel<8>, grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(hyb_bwd_farblk_kernel<8>, grid, dim3(256), 0, stream, a);
 }
 
-int hyb_bwd_tile() { return kHybBwdTile; }
+size_t hyb_bwd_near_lds(int P, int D, int Nn) {
+    const size_t Nn8 = (size_t)(Nn + 7) & ~(size_t)7;
+    return (Nn8 * Nn + (size_t)kNearRows * Nn8 * near_ldw(P + D) + (size_t)2 * P * kNearRows * Nn) * sizeof(float);
+}
 
-void launch_hyb_bwd_far(const HybBwd& a, hipStream_t stream) {
-    if (a.Nf <= 0) return;
-    const dim3 grid((a.Nf + 63) / 64, (a.B + 63) / 64, a.P);
-    hipLaunchKernelGGL(hyb_bwd_far_kernel, grid, dim3(256), 0, stream, a);
+bool launch_hyb_bwd_near(const HybBwd& a, hipStream_t stream) {
+    if (a.Nn <= 0) return true;
+    if (a.Nn > kHybNearMax || a.P > kHybBlockMax || a.D > 16) return false;
+    const size_t lds = hyb_bwd_near_lds(a.P, a.D, a.Nn);   // the caller checked it fits
+    const dim3 grid((a.B + kNearRows - 1) / kNearRows);
+#define DELREC_NEAR(KFV)                                                                         \
+    ensure_lds((const void*)hyb_bwd_near_kernel<KFV>, lds);                                      \
+    hipLaunchKernelGGL(hyb_bwd_near_kernel<KFV>, grid, dim3(256), lds, stream, a);
+    if (a.KF <= 2) { DELREC_NEAR(2) } else if (a.KF <= 4) { DELREC_NEAR(4) } else { DELREC_NEAR(8) }
+#undef DELREC_NEAR
+    return true;
+}
+
+void launch_hyb_near_pack(const HybPack& a, uint32_t* wnp, hipStream_t stream) {
+    const size_t n = (size_t)a.nc * a.nc;
+    if (n == 0) return;
+    hipLaunchKernelGGL(hyb_near_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, wnp);
 }
 
 int hyb_bwd_far_cols(int planes) { return planes == 1 ? 256 : 128; }
 
 HybBwdSizes hyb_bwd_sizes(const HybStepDims& q, int B, int cus, int fcol) {
     HybBwdSizes z{};
-    // any padded column count of either part: near columns in multiples of 128 up to Np, far
-    // ones in multiples of fcol up to Np rounded up to fcol; the two parts' padded counts add
-    // up to at most N + 127 + fcol - 1 < Np + 384
-    for (int c = 128; c <= q.Np; c += 128)
-        z.npart = std::max(z.npart, (size_t)lagstep_splits(B, c, q.Kt, cus) * B * c);
-    // (256-column far parts may run either far kernel: the larger split count sizes them)
-    for (int c = fcol; c <= (q.Np + fcol - 1) / fcol * fcol; c += fcol) {
-        int ks = lagstep_splits(B * q.P, c, q.Kt, cus, fcol);
-        if (fcol == 256) ks = std::max(ks, lagstep_gemm256_splits(B * q.P, c, q.Kt, cus));
-        z.fpart = std::max(z.fpart, (size_t)ks * B * q.P * c);
+    // any block length P <= kHybBlockMax (rows B * P) and any padded column count of either
+    // part: near columns in multiples of 128 up to kHybNearMax, far ones in multiples of fcol
+    // up to Np rounded up to fcol; the two parts' padded counts add up to at most
+    // N + 127 + fcol - 1 < Np + 384
+    for (int P = 1; P <= kHybBlockMax; P *= 2) {
+        for (int c = 128; c <= std::min(q.Np, kHybNearMax); c += 128)
+            z.npart = std::max(z.npart, (size_t)lagstep_splits(B * P, c, q.Kt, cus) * B * P * c);
+        // (256-column far parts may run either far kernel: the larger split count sizes them)
+        for (int c = fcol; c <= (q.Np + fcol - 1) / fcol * fcol; c += fcol) {
+            int ks = lagstep_splits(B * P, c, q.Kt, cus, fcol);
+            if (fcol == 256) ks = std::max(ks, lagstep_gemm256_splits(B * P, c, q.Kt, cus));
+            z.fpart = std::max(z.fpart, (size_t)ks * B * P * c);
+        }
     }
     z.planes = (size_t)(q.Kt / 8) * (q.Np + 384);
     return z;

@@ -238,14 +238,18 @@ struct HybLif {                  // one forward step of the offset-stacked scan
 // from one product per block of P steps whose rows are (batch row, step of the block); both
 // land in a ring of G_j(tau) that the LIF launch of each step reads.
 struct HybBwd {
-    int T, B, N, Nk, t, KF, R, P;
+    int T, B, N, Nk, KF, R, P, D;
+    int PF;                      // zero slices before slice 0 of the gr history
     size_t lda;                  // history row pitch (elements)
-    const float* npart;          // [KSn][Nnp][B] partials of the near product of step t (column-major)
-    int KSn, Nnp;
-    const int* ntile;            // [Nk / tile + 1]: the near columns of source tile x start here
+    int t0;                      // the block's latest step (its steps are t0 - P + 1 .. t0)
+    const float* npart;          // [KSn][B * P][Nnp] partials of the block's near product
+    int KSn, Nnp, Nn;            //   (row (b, tt): G(t0 - P + 2 + tt))
     const int* perm;             // [N]: the near sources ascending, then the far ones ascending
-    const float* fpart;          // [KSf][B * P][Nfp] partials of a block's far product
-    int KSf, Nfp, Nn, Nf, t0;
+    const float* fpart;          // [KSf][B * P][Nfp] partials of the block's far product
+    int KSf, Nfp, Nf;            //   (row (b, tt): G(t0 + 1 + tt))
+    const int* colf;             // [N]: far column of source j (-1: near)
+    const uint32_t* wnp;         // [Nn][Nn] W[perm[ci], perm[c]] between near neurons, the
+                                 //   low 4 bits replaced by the offset - omin
     const int* lof;
     const float* h;              // [KF][N]
     const float* drop;
@@ -260,9 +264,12 @@ struct HybBwd {
     float* dbp;                  // [B][N] db partials, or NULL
     float* ring;                 // [R][N][B]: G_j(tau) at slot tau mod R
 };
-void launch_hyb_bwd_lif(const HybBwd& a, hipStream_t stream);
-int hyb_bwd_tile();              // sources per LIF tile (the granularity of HybBwd::ntile)
-void launch_hyb_bwd_far(const HybBwd& a, hipStream_t stream);
+constexpr int kHybBlockMax = 4;  // steps per block of the hybrid backward (P <= this)
+constexpr int kHybNearMax = 160; // near sources the per-block near chain takes (LDS)
+void launch_hyb_bwd_farblk(const HybBwd& a, hipStream_t stream);
+bool launch_hyb_bwd_near(const HybBwd& a, hipStream_t stream);
+void launch_hyb_near_pack(const HybPack& a, uint32_t* wnp, hipStream_t stream);
+size_t hyb_bwd_near_lds(int P, int D, int Nn);
 
 struct HybScat {                 // the hybrid forward as a scatter on arrival (bf16 W)
     int T, B, N, D, KF, R, RP, omin;   // KF: the compiled run length; R >= D + KF - 1 ring slots, a power of two
@@ -294,7 +301,7 @@ size_t spike_linear_ws(int K, int M);   // bytes of the packed W^T planes
 void launch_spike_linear(const SpikeLinear& p, uint4* wp, hipStream_t stream);
 
 struct HybStepDims {
-    int Nk, Np, D, KF, R, HW, Kt, KS, P;
+    int Nk, Np, D, KF, R, HW, Kt, KS, P, PF;
     size_t lda, plane;
     bool ok;
 };
