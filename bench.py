@@ -207,26 +207,47 @@ def layer_inputs(m):
 
 
 def inter_linear_ms(m, ys, reps=5):
-    """The Linear between stacked layers on the first layer's spikes: the binary-activation
-    GEMM on its spike bits against torch's fp32 GEMM on the fp32 spikes (same weights),
-    average ms per call, and the largest difference between the two."""
+    """The Linear between stacked layers on the first layer's spikes, forward and forward +
+    backward: the binary-activation GEMMs on its spike bits (forward, and dW = g^T y; dx = g W
+    is a plain GEMM) against torch's fp32 GEMMs on the fp32 spikes (same weights), average ms
+    per call, and the largest differences between the two paths' outputs and weight
+    gradients."""
+    from delrec.spike_linear import attach_bits, spike_bits
     lin, y = m.inter[0], ys[0]
-    y_plain = y.clone()                   # no spike bits: torch.nn.functional.linear
-    out = {}
-    with torch.no_grad():
-        for name, fn in (('spike_bits_gemm', lambda: lin(y)), ('torch_fp32', lambda: lin(y_plain))):
-            fn()
-            torch.cuda.synchronize()
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            for _ in range(reps):
-                r = fn()
-            e.record()
-            torch.cuda.synchronize()
-            out[name] = s.elapsed_time(e) / reps
-            out[name + '_out'] = r
-        diff = float((out.pop('spike_bits_gemm_out') - out.pop('torch_fp32_out')).abs().max())
-    out['max_abs_diff'] = diff
+    bits = spike_bits(y)
+    T, B, _ = y.shape
+    gout = torch.randn(T, B, lin.weight.shape[0], device=y.device, generator=torch.Generator(y.device).manual_seed(7))
+    inputs = {'spike_bits_gemm': lambda: attach_bits(y.detach().requires_grad_(True), bits),
+              'torch_fp32': lambda: y.detach().clone().requires_grad_(True)}
+    out, res = {}, {}
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            r = fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps, r
+
+    for name, make in inputs.items():
+        x = make()
+        with torch.no_grad():
+            out[name], o = timed(lambda: lin(x))
+
+        def fwd_bwd():
+            lin.weight.grad = None
+            xi = make()
+            lin(xi).backward(gout)
+            return lin.weight.grad
+
+        out[name + '_fwd_bwd'], dw = timed(fwd_bwd)
+        res[name] = (o, dw.clone())
+    out['max_abs_diff'] = float((res['spike_bits_gemm'][0] - res['torch_fp32'][0]).abs().max())
+    out['max_abs_diff_dW'] = float((res['spike_bits_gemm'][1] - res['torch_fp32'][1]).abs().max())
+    lin.weight.grad = None
     return out
 
 

@@ -229,6 +229,43 @@ typedef struct {
     size_t workspace_bytes;
 } delrec_spike_linear_args;
 
+/* Weight gradient of that Linear from the same spike bits: dW[m*K + k] = sum_{t,b}
+ * g[t][b][m] * y[t][b][k] (the reference computes it as the torch.nn.Linear backward,
+ * g^T x on the fp32 spikes). g is applied as bf16 hi + mid + lo (about 2^-25 relative per
+ * term, fp32 accumulation). Workspace: delrec_query_workspace(DELREC_WS_SPIKE_LINEAR_DW, T,
+ * B, K, M, 0) (0 bytes when the output tiles alone fill the GPU). */
+typedef struct {
+    int32_t T, B, K, M;
+    const uint32_t* bits;        /* (B, ceil(T/32), K) spike words                        */
+    const float* g;              /* (T, B, M) gradient of the Linear's output             */
+    float* dW;                   /* out (M, K)                                            */
+    void* workspace;
+    size_t workspace_bytes;
+} delrec_spike_linear_dw_args;
+
+/* The loss end of the SNN_* stacks, fused: the readout's output (T, B, C) reduced over time
+ * -- DELREC_READOUT_SUM (reference utils.py calc_loss_SSC), _MEAN (calc_loss_HAR,
+ * calc_loss_AL) or _MAX (calc_loss_SHD, first maximum) -- optionally after a non-spiking
+ * leaky integrator (the SHD readout LIF with threshold 1e8, networks_shd.py:187-199:
+ * integrator 1 v = decay * v + x, 2 v = v + (x - v) / tau, decay_input), then
+ * torch.nn.CrossEntropyLoss (mean over the batch). Writes the loss, its gradient with
+ * respect to the readout's output and optionally the reduced readout (B, C). Workspace: B
+ * floats. */
+enum { DELREC_READOUT_SUM = 0, DELREC_READOUT_MEAN = 1, DELREC_READOUT_MAX = 2 };
+typedef struct {
+    int32_t T, B, C;
+    const float* logits;         /* (T, B, C)                                              */
+    const int64_t* labels;       /* (B) class indices                                      */
+    int32_t reduce;              /* DELREC_READOUT_*                                       */
+    int32_t integrator;          /* 0 none, 1 leaky (decay_input False), 2 (decay_input)   */
+    float tau;                   /* integrator time constant; decay = float(1 - 1/tau)     */
+    float* out;                  /* out (B, C) reduced readout, or NULL                    */
+    float* dlogits;              /* out (T, B, C) d loss / d logits                        */
+    float* loss;                 /* out (1) mean cross-entropy                             */
+    void* workspace;
+    size_t workspace_bytes;
+} delrec_readout_ce_args;
+
 /* Workspace kinds for delrec_query_workspace; flags bit 0: weights are bf16; synaptic
  * kinds: bit 1: hybrid delays (d == NULL), bits 8..15: ceil(2 * s_max) on the float32 s_max
  * the entry point receives (s_uniform for the hybrid), capped at 255 -- the most lags of
@@ -236,7 +273,9 @@ typedef struct {
  * bit 2: d_min >= s_uniform - 1, bits 16..23: off_count (the fields of the entry point's
  * arguments, which also pick the scan form). */
 enum { DELREC_WS_AXONAL_FWD = 1, DELREC_WS_AXONAL_BWD = 2, DELREC_WS_SYN_FWD = 3,
-       DELREC_WS_SYN_BWD = 4, DELREC_WS_SPIKE_LINEAR = 5 /* N = K inputs, L = M outputs */ };
+       DELREC_WS_SYN_BWD = 4, DELREC_WS_SPIKE_LINEAR = 5 /* N = K inputs, L = M outputs */,
+       DELREC_WS_SPIKE_LINEAR_DW = 6 /* N = K inputs, L = M outputs */,
+       DELREC_WS_READOUT_CE = 7 /* N = C classes, L = 1 */ };
 
 int delrec_axonal_fwd(const delrec_axonal_fwd_args* a, void* stream);
 int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream);
@@ -255,6 +294,8 @@ int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream);
  * stream before it launches its scan. Every other path is fully asynchronous. */
 int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream);
 int delrec_spike_linear_fwd(const delrec_spike_linear_args* a, void* stream);
+int delrec_spike_linear_dw(const delrec_spike_linear_dw_args* a, void* stream);
+int delrec_readout_ce(const delrec_readout_ce_args* a, void* stream);
 int delrec_lif_fwd(const delrec_lif_fwd_args* a, void* stream);
 int delrec_lif_bwd(const delrec_lif_bwd_args* a, void* stream);
 
@@ -300,7 +341,7 @@ int delrec_peak_mfma(int32_t kind, int32_t iters, float* sink, size_t sink_bytes
 const char* delrec_strerror(int status);
 /* "delrec-mi355x <DELREC_ABI_VERSION> (gfx950)": a binding checks it before use (the
  * argument structs change between versions). */
-#define DELREC_ABI_VERSION "0.3.0"
+#define DELREC_ABI_VERSION "0.4.0"
 const char* delrec_version(void);
 
 #ifdef __cplusplus

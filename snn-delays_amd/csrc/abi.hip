@@ -675,6 +675,12 @@ int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_
         case DELREC_WS_SPIKE_LINEAR:
             c.take<uint4>(spike_linear_ws(N, L) / sizeof(uint4));
             break;
+        case DELREC_WS_SPIKE_LINEAR_DW:
+            c.take<float>(spike_linear_dw_ws(T, B, N, L, num_cus()) / sizeof(float));
+            break;
+        case DELREC_WS_READOUT_CE:
+            c.take<float>((size_t)B);
+            break;
         default: return DELREC_ERR_ARG;
     }
     *bytes = c.used;
@@ -1064,6 +1070,41 @@ int delrec_spike_linear_fwd(const delrec_spike_linear_args* a, void* stream) {
     uint4* wp = cv.take<uint4>(spike_linear_ws(p.K, p.M) / sizeof(uint4));
     if (!wp) return DELREC_ERR_WORKSPACE;
     launch_spike_linear(p, wp, static_cast<hipStream_t>(stream));
+    return finish_launch();
+}
+
+int delrec_spike_linear_dw(const delrec_spike_linear_dw_args* a, void* stream) {
+    if (!a || a->T <= 0 || a->B <= 0 || a->K <= 0 || a->M <= 0) return DELREC_ERR_ARG;
+    if (!a->bits || !a->g || !a->dW) return DELREC_ERR_ARG;
+    SpikeLinearDw p{};
+    p.T = a->T; p.B = a->B; p.K = a->K; p.M = a->M;
+    p.bits = a->bits; p.g = a->g; p.dW = a->dW;
+    spike_linear_dw_dims(p, num_cus());
+    if (p.KS > 1) {
+        Carver cv(a->workspace, a->workspace_bytes);
+        p.part = cv.take<float>((size_t)p.KS * p.M * p.K);
+        if (!p.part) return DELREC_ERR_WORKSPACE;
+    }
+    launch_spike_linear_dw(p, static_cast<hipStream_t>(stream));
+    return finish_launch();
+}
+
+int delrec_readout_ce(const delrec_readout_ce_args* a, void* stream) {
+    if (!a || a->T <= 0 || a->B <= 0 || a->C <= 0) return DELREC_ERR_ARG;
+    if (!a->logits || !a->labels || !a->dlogits || !a->loss) return DELREC_ERR_ARG;
+    if (a->reduce < DELREC_READOUT_SUM || a->reduce > DELREC_READOUT_MAX) return DELREC_ERR_ARG;
+    if (a->integrator < 0 || a->integrator > 2 || (a->integrator && !(a->tau > 0.0f))) return DELREC_ERR_ARG;
+    if ((size_t)(4 + a->C) * sizeof(float) > (size_t)max_lds_bytes()) return DELREC_ERR_UNSUPPORTED;
+    Carver cv(a->workspace, a->workspace_bytes);
+    float* rowloss = cv.take<float>((size_t)a->B);
+    if (!rowloss) return DELREC_ERR_WORKSPACE;
+    ReadoutCe p{};
+    p.T = a->T; p.B = a->B; p.C = a->C; p.logits = a->logits; p.labels = a->labels;
+    p.reduce = a->reduce; p.integrator = a->integrator; p.tau = a->tau;
+    p.decay = a->integrator ? (float)(1.0 - 1.0 / (double)a->tau) : 0.0f;
+    p.in_scale = a->integrator == 2 ? (float)(1.0 / (double)a->tau) : 1.0f;
+    p.out = a->out; p.dlogits = a->dlogits; p.rowloss = rowloss; p.loss = a->loss;
+    launch_readout_ce(p, static_cast<hipStream_t>(stream));
     return finish_launch();
 }
 

@@ -299,6 +299,29 @@ struct SpikeLinear {
 void spike_linear_dims(SpikeLinear& p);
 size_t spike_linear_ws(int K, int M);   // bytes of the packed W^T planes
 void launch_spike_linear(const SpikeLinear& p, uint4* wp, hipStream_t stream);
+struct SpikeLinearDw {           // dW[m][k] = sum_{t,b} g[t][b][m] y[t][b][k]
+    int T, B, K, M, Kp, Mp, KS;  // Kp, Mp rounded up to 128; KS splits of the (b, word) stages
+    const uint32_t* bits;        // (B, ceil(T/32), K)
+    const float* g;              // (T, B, M)
+    float* dW;                   // (M, K)
+    float* part;                 // [KS][M][K] when KS > 1
+};
+struct ReadoutCe {               // time reduction (+ leaky integrator) + cross-entropy, fused
+    int T, B, C;
+    const float* logits;         // (T, B, C)
+    const int64_t* labels;       // (B)
+    int reduce;                  // DELREC_READOUT_*
+    int integrator;              // 0 none, 1 v = decay v + x, 2 v = v + (x - v) / tau
+    float tau, decay, in_scale;  // in_scale: d v_t / d x_t (1, or 1 / tau for form 2)
+    float* out;                  // (B, C) or NULL
+    float* dlogits;              // (T, B, C)
+    float* rowloss;              // (B) workspace
+    float* loss;                 // (1)
+};
+void launch_readout_ce(const ReadoutCe& p, hipStream_t stream);
+void spike_linear_dw_dims(SpikeLinearDw& p, int cus);
+size_t spike_linear_dw_ws(int T, int B, int K, int M, int cus);
+void launch_spike_linear_dw(const SpikeLinearDw& p, hipStream_t stream);
 
 struct HybStepDims {
     int Nk, Np, D, KF, R, HW, Kt, KS, P, PF;

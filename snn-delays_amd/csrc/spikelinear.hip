@@ -12,6 +12,8 @@
 // (16 rows x 8 neurons) from the words.
 #include "kernels.h"
 
+#include <algorithm>
+
 namespace delrec {
 
 namespace {
@@ -183,6 +185,162 @@ __global__ void __launch_bounds__(256) spike_linear_kernel(SpikeLinear p, const 
                 if (m < p.M) o[m] = acc[mb][nb][e] + bv[nb];
             }
         }
+}
+
+// The weight gradient of that Linear, dW[m][k] = sum_{t,b} g[t][b][m] * y[t][b][k], as the
+// same binary-activation GEMM with the spikes on the other side: D = g^T (M x TB) . Y (TB x K).
+// The contraction runs over stages of 32 steps of one batch row -- exactly one spike word per
+// neuron -- so each lane expands its B fragment (8 steps of one neuron) from one word; g^T is
+// split into bf16 hi + mid + lo planes (about 2^-25 relative, fp32 accumulation) as it is staged.
+// Tile: 128 outputs m x 128 inputs k per workgroup, 4 waves of 64 x 64; stages of a split in
+// (batch row, word) order; loads of stage s + 1 in flight while stage s multiplies. With at
+// least one tile per CU there is no split: each workgroup writes its dW tile directly, and
+// the 16 input tiles of one output tile sit on one XCD (they stream the same g columns).
+__global__ void __launch_bounds__(256) spike_linear_dw_kernel(SpikeLinearDw p) {
+    constexpr int PL = kSpikeLinearPlanes;
+    __shared__ uint4 sa[2][PL][4 * 128];     // [buffer][plane][r-block * 128 + m]: 8 steps of g^T
+    __shared__ uint32_t sb[2][128];          // [buffer][k]: the stage's spike words
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int wi = w >> 1, wj = w & 1, g = lane >> 4, lc = lane & 15;
+    const int MT = p.Mp / 128, KT = p.Kp / 128, TW = (p.T + 31) >> 5;
+    const int id = (int)blockIdx.x;
+    int mt, kt, ks;
+    if (p.KS == 1 && MT % 8 == 0) {
+        const int xcd = id & 7, slot = id >> 3;        // the input tiles of an output tile on one XCD
+        kt = slot % KT;
+        mt = xcd + 8 * (slot / KT);
+        ks = 0;
+    } else {
+        ks = id % p.KS;
+        const int tile = id / p.KS;
+        mt = tile / KT;
+        kt = tile - mt * KT;
+    }
+    const int m0 = mt * 128, k0 = kt * 128;
+    const int nst = p.B * TW;
+    const int per = (nst + p.KS - 1) / p.KS;
+    const int s0 = ks * per, s1 = min(nst, s0 + per);
+    // staging: g^T -- thread (m = m0 + (tid & 127), steps 16 (tid >> 7) .. + 15 of the word);
+    // spikes -- thread tid < 128 loads the word of input k0 + tid
+    const int sm = tid & 127, sr = (tid >> 7) * 16;
+    const bool mok = m0 + sm < p.M;
+    const size_t gstep = (size_t)p.B * p.M;            // floats between consecutive steps
+    float rg[16];
+    uint32_t rb = 0;
+    auto issue = [&](int s) {
+        const int b = s / TW, wd = s - b * TW;
+        const int tbase = wd * 32 + sr;
+        const float* src = p.g + ((size_t)tbase * p.B + b) * p.M + m0 + sm;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) rg[e] = (s < s1 && mok && tbase + e < p.T) ? src[(size_t)e * gstep] : 0.0f;
+        rb = (s < s1 && tid < 128 && k0 + tid < p.K) ? p.bits[((size_t)b * TW + wd) * p.K + k0 + tid] : 0u;
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {       // two 8-step blocks per thread
+            uint32_t pl[PL][4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                uint32_t v2[PL][2];
+#pragma unroll
+                for (int f = 0; f < 2; ++f) {
+                    float r = rg[8 * h + e + f];
+#pragma unroll
+                    for (int q = 0; q < PL; ++q) {
+                        v2[q][f] = sl_bf16_rne(r);
+                        r -= __uint_as_float(v2[q][f] << 16);
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < PL; ++q) pl[q][e / 2] = v2[q][0] | (v2[q][1] << 16);
+            }
+            const int rblk = (sr >> 3) + h;
+#pragma unroll
+            for (int q = 0; q < PL; ++q) sa[buf][q][rblk * 128 + sm] = uint4{pl[q][0], pl[q][1], pl[q][2], pl[q][3]};
+        }
+        if (tid < 128) sb[buf][tid] = rb;
+    };
+    sl_floatx4 acc[4][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = sl_floatx4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int buf) {
+        sl_bf16x8 fb[4];
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {      // input k = k0 + wj 64 + nb 16 + lc, steps 8 g .. 8 g + 7
+            const uint32_t wd = sb[buf][wj * 64 + nb * 16 + lc] >> (8 * g);
+            uint32_t pk[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                pk[e] = (((wd >> (2 * e)) & 1u) * 0x3F80u) | ((((wd >> (2 * e + 1)) & 1u) * 0x3F80u) << 16);
+            fb[nb] = __builtin_bit_cast(sl_bf16x8, uint4{pk[0], pk[1], pk[2], pk[3]});
+        }
+#pragma unroll
+        for (int q = 0; q < PL; ++q)
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) {
+                const sl_bf16x8 fa = __builtin_bit_cast(sl_bf16x8, sa[buf][q][g * 128 + wi * 64 + mb * 16 + lc]);
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb[nb], acc[mb][nb], 0, 0, 0);
+            }
+    };
+    issue(s0);
+    stash(0);
+    barrier_lds();
+    for (int s = s0; s < s1; ++s) {
+        const int buf = (s - s0) & 1;
+        issue(s + 1);                 // past s1: zeros (no load)
+        compute(buf);
+        stash(buf ^ 1);
+        barrier_lds();
+    }
+    // rows m = m0 + wi 64 + mb 16 + 4 g + e, columns k = k0 + wj 64 + nb 16 + lc
+    float* out = p.KS == 1 ? p.dW : p.part + (size_t)ks * p.M * p.K;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int m = m0 + wi * 64 + mb * 16 + 4 * g + e;
+            if (m >= p.M) continue;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) {
+                const int k = k0 + wj * 64 + nb * 16 + lc;
+                if (k < p.K) out[(size_t)m * p.K + k] = acc[mb][nb][e];
+            }
+        }
+}
+
+// dW = sum over the splits of the partials, in split order
+__global__ void __launch_bounds__(256) spike_linear_dw_sum_kernel(SpikeLinearDw p) {
+    const size_t n = (size_t)p.M * p.K;
+    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < n; q += (size_t)gridDim.x * blockDim.x) {
+        float v = 0.0f;
+        for (int ks = 0; ks < p.KS; ++ks) v += p.part[(size_t)ks * n + q];
+        p.dW[q] = v;
+    }
+}
+
+void spike_linear_dw_dims(SpikeLinearDw& p, int cus) {
+    p.Mp = (p.M + 127) / 128 * 128;
+    p.Kp = (p.K + 127) / 128 * 128;
+    const int tiles = (p.Mp / 128) * (p.Kp / 128);
+    const int nst = p.B * ((p.T + 31) >> 5);
+    p.KS = std::max(1, std::min((cus + tiles - 1) / tiles, std::max(1, nst / 16)));   // >= 16 stages a split
+}
+
+size_t spike_linear_dw_ws(int T, int B, int K, int M, int cus) {
+    SpikeLinearDw p{};
+    p.T = T; p.B = B; p.K = K; p.M = M;
+    spike_linear_dw_dims(p, cus);
+    return p.KS > 1 ? (size_t)p.KS * M * K * sizeof(float) : 0;
+}
+
+void launch_spike_linear_dw(const SpikeLinearDw& p, hipStream_t stream) {
+    const unsigned grid = (unsigned)((p.Mp / 128) * (p.Kp / 128) * p.KS);
+    hipLaunchKernelGGL(spike_linear_dw_kernel, dim3(grid), dim3(256), 0, stream, p);
+    if (p.KS > 1) hipLaunchKernelGGL(spike_linear_dw_sum_kernel, dim3(1024), dim3(256), 0, stream, p);
 }
 
 void spike_linear_dims(SpikeLinear& p) {

@@ -20,7 +20,7 @@ CSRC = PKG.parent / 'csrc'
 INCLUDE = PKG.parent.parent / 'include'
 OUT = PKG / 'libdelrec_hip.so'
 SOURCES = ('abi.hip', 'axonal.hip', 'gemm.hip', 'hybstep.hip', 'lagmm.hip', 'lagstep.hip', 'peaks.hip',
-           'spikelinear.hip', 'synaptic.hip')
+           'readout.hip', 'spikelinear.hip', 'synaptic.hip')
 ARCH = os.environ.get('DELREC_OFFLOAD_ARCH', 'gfx950')
 
 

@@ -27,13 +27,16 @@ DELREC_BWD_SOFT, DELREC_BWD_STRAIGHT = 0, 1
 DELREC_ERR_WINDOW = 5
 DELREC_ERR_SCRATCH = 9
 WS_AXONAL_FWD, WS_AXONAL_BWD, WS_SYN_FWD, WS_SYN_BWD, WS_SPIKE_LINEAR = 1, 2, 3, 4, 5
+WS_SPIKE_LINEAR_DW, WS_READOUT_CE = 6, 7
+READOUT_SUM, READOUT_MEAN, READOUT_MAX = 0, 1, 2
 
 # Every symbol include/delrec.h declares (checked by the CPU test suite).
 EXPORTS = ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_axonal_bwd_noalloc', 'delrec_syn_fwd',
            'delrec_syn_bwd', 'delrec_spike_linear_fwd',
            'delrec_lif_fwd', 'delrec_lif_bwd', 'delrec_delay_grad', 'delrec_query_workspace',
            'delrec_strerror', 'delrec_version', 'delrec_scan_timing', 'delrec_scan_timing_read',
-           'delrec_max_post', 'delrec_max_take', 'delrec_peak_mfma')
+           'delrec_max_post', 'delrec_max_take', 'delrec_peak_mfma', 'delrec_spike_linear_dw',
+           'delrec_readout_ce')
 
 
 class DelrecError(RuntimeError):
@@ -93,6 +96,17 @@ class SpikeLinearArgs(ctypes.Structure):
                 ('bias', c_vp), ('out', c_vp), ('workspace', c_vp), ('workspace_bytes', c_size)]
 
 
+class SpikeLinearDwArgs(ctypes.Structure):
+    _fields_ = [('T', c_i32), ('B', c_i32), ('K', c_i32), ('M', c_i32), ('bits', c_vp), ('g', c_vp),
+                ('dW', c_vp), ('workspace', c_vp), ('workspace_bytes', c_size)]
+
+
+class ReadoutCeArgs(ctypes.Structure):
+    _fields_ = [('T', c_i32), ('B', c_i32), ('C', c_i32), ('logits', c_vp), ('labels', c_vp),
+                ('reduce', c_i32), ('integrator', c_i32), ('tau', c_f32), ('out', c_vp), ('dlogits', c_vp),
+                ('loss', c_vp), ('workspace', c_vp), ('workspace_bytes', c_size)]
+
+
 class LifFwdArgs(ctypes.Structure):
     _fields_ = [('T', c_i32), ('B', c_i32), ('N', c_i32), ('x', c_vp), ('lif', Lif),
                 ('y', c_vp), ('u', c_vp)]
@@ -104,7 +118,7 @@ class LifBwdArgs(ctypes.Structure):
 
 
 # the DELREC_ABI_VERSION of include/delrec.h these ctypes structs mirror
-ABI_VERSION = '0.3.0'
+ABI_VERSION = '0.4.0'
 
 _lib = None
 
@@ -119,7 +133,8 @@ def load():
                           f'g.build()"` from the repository root')
     lib = ctypes.CDLL(str(LIB_PATH))
     for name in ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_axonal_bwd_noalloc', 'delrec_syn_fwd',
-                 'delrec_syn_bwd', 'delrec_spike_linear_fwd', 'delrec_lif_fwd', 'delrec_lif_bwd'):
+                 'delrec_syn_bwd', 'delrec_spike_linear_fwd', 'delrec_spike_linear_dw', 'delrec_readout_ce',
+                 'delrec_lif_fwd', 'delrec_lif_bwd'):
         getattr(lib, name).restype = c_i32
         getattr(lib, name).argtypes = [c_vp, c_vp]
     lib.delrec_delay_grad.restype = c_i32

@@ -58,7 +58,8 @@ def test_query_workspace_and_argument_errors_without_gpu():
 
 
 _STRUCTS = ['delrec_lif', 'delrec_axonal_fwd_args', 'delrec_axonal_bwd_args', 'delrec_syn_fwd_args',
-            'delrec_syn_bwd_args', 'delrec_lif_fwd_args', 'delrec_lif_bwd_args', 'delrec_spike_linear_args']
+            'delrec_syn_bwd_args', 'delrec_lif_fwd_args', 'delrec_lif_bwd_args', 'delrec_spike_linear_args',
+            'delrec_spike_linear_dw_args', 'delrec_readout_ce_args']
 
 
 def _c_layout():
@@ -67,7 +68,8 @@ def _c_layout():
     classes = {'delrec_lif': _lib.Lif, 'delrec_axonal_fwd_args': _lib.AxonalFwdArgs,
                'delrec_axonal_bwd_args': _lib.AxonalBwdArgs, 'delrec_syn_fwd_args': _lib.SynFwdArgs,
                'delrec_syn_bwd_args': _lib.SynBwdArgs, 'delrec_lif_fwd_args': _lib.LifFwdArgs,
-               'delrec_lif_bwd_args': _lib.LifBwdArgs, 'delrec_spike_linear_args': _lib.SpikeLinearArgs}
+               'delrec_lif_bwd_args': _lib.LifBwdArgs, 'delrec_spike_linear_args': _lib.SpikeLinearArgs,
+               'delrec_spike_linear_dw_args': _lib.SpikeLinearDwArgs, 'delrec_readout_ce_args': _lib.ReadoutCeArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for st in _STRUCTS:
         lines.append(f'  printf("{st} size %zu\\n", sizeof({st}));')

@@ -305,3 +305,20 @@ def test_spike_linear_falls_back_to_linear_without_bits():
     x = torch.rand(4, 3, 12)
     torch.testing.assert_close(lin(x), ref(x))
     assert isinstance(lin, torch.nn.Linear)
+
+
+def test_spike_bits_follow_the_tensor_version():
+    """Bits attached to a spike train are dropped once the tensor is modified in place, and
+    the bits path is refused past the kernels' 32-bit addressing (CPU: no kernel runs)."""
+    import torch
+    from delrec.spike_linear import attach_bits, bits_path_fits, spike_bits
+    y = torch.zeros(4, 2, 3)
+    bits = torch.zeros(2, 1, 3, dtype=torch.int32)
+    attach_bits(y, bits)
+    assert spike_bits(y) is bits
+    y.add_(1.0)
+    assert spike_bits(y) is None
+    assert spike_bits(torch.zeros(1)) is None
+    assert bits_path_fits(1024, 512, 2048, 2048)
+    assert not bits_path_fits(32 * 2048, 512, 2048, 2048)      # spike words past 2 GiB
+    assert not bits_path_fits(32, 1, 40000, 40000)              # W planes past 2 GiB

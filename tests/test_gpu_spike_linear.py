@@ -1,8 +1,9 @@
-"""GPU parity of the binary-activation Linear (``delrec_spike_linear_fwd`` through
-``delrec.spike_linear.SpikeLinear``) against ``torch.nn.functional.linear`` in float64 on the
-same spikes and weights. The spikes are exact; W enters as bf16 hi + mid + lo (about 2^-25
-relative per weight), so the tolerance is fp32's: rtol 1e-5, atol 1e-6 relative to the
-output's magnitude. Shapes cover T, K and M off their tile multiples (128 steps, 32
+"""GPU parity of the binary-activation Linear (``delrec_spike_linear_fwd`` and
+``delrec_spike_linear_dw`` through ``delrec.spike_linear.SpikeLinear``) against
+``torch.nn.functional.linear`` and its autograd in float64 on the same spikes and weights.
+The spikes are exact; W (forward) and g (weight gradient) enter as bf16 hi + mid + lo (about
+2^-25 relative), so the tolerance is fp32's: rtol 1e-5, atol 1e-6 relative to the output's
+magnitude. Shapes cover T, K and M off their tile multiples (128 steps, 32
 neurons, 128 outputs), with and without bias, and the bits attached by a recurrent layer.
 """
 
@@ -49,9 +50,7 @@ def test_spike_linear_matches_linear(dev, case):
             lin.bias.copy_(torch.randn(M, generator=g))
     ref = torch.nn.functional.linear(y.double(), lin.weight.double(), None if not bias else lin.bias.double())
     lin = lin.to(dev)
-    yg = attach_bits(y.to(dev), pack_bits(y).to(dev))
-    xg = yg.clone().requires_grad_(True)
-    xg._delrec_bits = yg._delrec_bits
+    xg = attach_bits(y.to(dev).requires_grad_(True), pack_bits(y).to(dev))
     out = lin(xg)
     assert out.grad_fn is not None and 'SpikeLinear' in type(out.grad_fn).__name__, 'the HIP path was not taken'
     gout = torch.randn(T, B, M, generator=g)
@@ -59,7 +58,7 @@ def test_spike_linear_matches_linear(dev, case):
     torch.cuda.synchronize()
     scale = float(ref.abs().max())
     torch.testing.assert_close(out.detach().cpu().double(), ref, rtol=1e-5, atol=1e-6 * max(scale, 1.0))
-    # the backward is the plain GEMM pair: against float64 autograd of the same linear
+    # the backward (dW on the spike bits, dx a plain GEMM): against float64 autograd
     xr = y.double().requires_grad_(True)
     wr = lin.weight.detach().cpu().double().requires_grad_(True)
     torch.nn.functional.linear(xr, wr).backward(gout.double())
@@ -77,7 +76,8 @@ def test_recurrent_layer_output_feeds_the_spike_gemm(dev):
     from delrec.spike_linear import SpikeLinear
     with torch.no_grad():
         y = m.layers[0](m.x)
-    bits = getattr(y, '_delrec_bits', None)
+    from delrec.spike_linear import spike_bits
+    bits = spike_bits(y)
     assert bits is not None and tuple(bits.shape) == (8, 2, w['N'])
     lin = SpikeLinear(w['N'], 96, bias=True).to(dev)
     with torch.no_grad():
@@ -86,3 +86,41 @@ def test_recurrent_layer_output_feeds_the_spike_gemm(dev):
     torch.cuda.synchronize()
     assert float(y.mean()) > 0
     torch.testing.assert_close(out.double(), ref, rtol=1e-5, atol=1e-6 * max(float(ref.abs().max()), 1.0))
+
+
+@pytest.mark.gpu
+def test_spike_linear_weight_gradient_at_the_c5_width(dev):
+    """dW = g^T y on the bits at the inter-layer width of C5 (K = M = 2048, 512 batch rows,
+    the tile count that takes the unsplit XCD-grouped form), against float64."""
+    from delrec.spike_linear import spike_linear_dw
+    T, B, K, M = 40, 512, 2048, 2048
+    g = gen(12)
+    y = (torch.rand(T, B, K, generator=g) < 0.03).float()
+    gout = torch.randn(T, B, M, generator=g)
+    dW = spike_linear_dw(gout.to(dev), pack_bits(y).to(dev), K)
+    torch.cuda.synchronize()
+    ref = gout.reshape(-1, M).double().t() @ y.reshape(-1, K).double()
+    err = (dW.cpu().double() - ref).abs()
+    print(f'  dW max abs err {float(err.max()):.3e}, |ref|max {float(ref.abs().max()):.3e}', flush=True)
+    # fp32 accumulation of about 600 O(1) terms per entry: the fp32 bound, relative to the
+    # largest entry as in the tests above
+    torch.testing.assert_close(dW.cpu().double(), ref, rtol=1e-5, atol=1e-5 * float(ref.abs().max()))
+
+
+@pytest.mark.gpu
+def test_spike_linear_ignores_bits_of_a_modified_tensor(dev):
+    """Bits attached to a spike train describe it only until it is modified in place: after
+    that the Linear takes torch.nn.functional.linear on the tensor's current values."""
+    from delrec.spike_linear import SpikeLinear, attach_bits, spike_bits
+    T, B, K, M = 33, 2, 40, 24
+    y = (torch.rand(T, B, K, generator=gen(13)) < 0.2).float()
+    lin = SpikeLinear(K, M).to(dev)
+    yg = attach_bits(y.to(dev), pack_bits(y).to(dev))
+    assert 'SpikeLinear' in type(lin(yg.requires_grad_(True)).grad_fn).__name__
+    with torch.no_grad():
+        yg.mul_(2.0)
+    assert spike_bits(yg) is None
+    out = lin(yg)
+    assert 'SpikeLinear' not in type(out.grad_fn).__name__
+    torch.testing.assert_close(out.detach().cpu(), torch.nn.functional.linear(2.0 * y, lin.weight.detach().cpu(),
+                                                                           lin.bias.detach().cpu()))
