@@ -1168,9 +1168,13 @@ __global__ void __launch_bounds__(1024) syn_bwd_hyb_g(SynBwd p) {
     float* ghist = smem + (size_t)rows * GS;              // [RG][NL]
     // the offsets' span must fit the ring pitch (the host sized GS from the caller's
     // off_count): a wider one makes every output NaN instead of reading other rows
-    // and every source's first lag must be >= 1 (c0 = lob + omin with the offsets' own
-    // smallest value): a caller's d_min that claimed so wrongly gives NaN, not dropped taps
-    const bool bad = 2 * D > GS || RG < 2 || __syncthreads_or(act && c0 < 1) != 0;
+    // and every tap of non-zero weight must lie at a lag >= 1 (tap f at c0 + f, c0 = lob + omin
+    // with the offsets' own smallest value; lob may be a zero-weight edge tap): a caller's
+    // d_min that claimed so wrongly gives NaN, not dropped taps
+    bool low = false;
+#pragma unroll
+    for (int f = 0; f < KT; ++f) low = low || (c0 + f < 1 && hq[f] > 0.0f);
+    const bool bad = 2 * D > GS || RG < 2 || __syncthreads_or(act && low) != 0;
     for (int q = tid; q < rows * GS + RG * NL; q += blockDim.x) smem[q] = 0.0f;
     __syncthreads();
 

@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <mutex>
+#include <unordered_map>
 #include <stdexcept>
 #include <string>
 
@@ -35,12 +37,34 @@ void check(int status, const char* fn) {
                                  delrec_strerror(status) + ")");
 }
 
+// the largest delay each backward took, by the delay tensor's storage: the Python layer reads
+// it (seen_dmax) to decide whether the next forward may run before reading the window length
+std::mutex g_seen_mu;
+std::unordered_map<const void*, float> g_seen;
+
+void note_seen(const void* d, float v) {
+    std::lock_guard<std::mutex> lk(g_seen_mu);
+    g_seen[d] = v;
+}
+
+void forget_dmax(const Tensor& d) {
+    std::lock_guard<std::mutex> lk(g_seen_mu);
+    g_seen.erase(d.data_ptr());
+}
+
+double seen_dmax(const Tensor& d) {
+    std::lock_guard<std::mutex> lk(g_seen_mu);
+    const auto it = g_seen.find(d.data_ptr());
+    return it == g_seen.end() ? std::nan("") : (double)it->second;
+}
+
 // max d posted by the forward (its ticket for delrec_max_take), or a fresh synchronous read of
 // `fallback` when the slot was reused or the value did not arrive
 float take_max(int64_t ticket, const Tensor& fallback) {
     float v = 0.0f;
-    if (delrec_max_take((uint32_t)ticket, &v, 10000) == DELREC_OK) return v;
-    return fallback.max().item<float>();
+    if (delrec_max_take((uint32_t)ticket, &v, 10000) != DELREC_OK) v = fallback.max().item<float>();
+    note_seen(fallback.data_ptr(), v);
+    return v;
 }
 
 // L = ceil(1 + max d + max s) + 1 with each sum rounded to fp32 (reference delays.py:26)
@@ -181,4 +205,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("axonal_common", &axonal_common, "axonal layer forward (autograd)", py::arg("x"), py::arg("W"),
           py::arg("d"), py::arg("bias"), py::arg("drop"), py::arg("sigma"), py::arg("tau"), py::arg("vth"),
           py::arg("surrogate"), py::arg("gamma"), py::arg("alpha"), py::arg("detach"));
+    m.def("seen_dmax", &seen_dmax, "largest delay the last backward on this delay tensor took (NaN: none)",
+          py::arg("d"));
+    m.def("forget_dmax", &forget_dmax, "drop the recorded largest delay of this delay storage", py::arg("d"));
 }

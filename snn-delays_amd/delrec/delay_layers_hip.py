@@ -16,7 +16,7 @@ import torch
 from . import _lib
 from .kernels import AxonalRecdelHip, eventdriven_trainable_forward, hybrid_trainable_forward
 from .kernels._common import require_device
-from .kernels.recdel_base import STRAIGHT_LINE_MAX_ELEMS
+from .kernels.recdel_base import STRAIGHT_LINE_MAX_ELEMS, apply_with_hint, deferred_read_safe
 from .kernels.surrogate import surrogate_id
 
 
@@ -50,8 +50,12 @@ class AxonalHipScans:
         if self.round_delays:
             d_in = d_in + (d_in.round() - d_in).detach()
         nm = self.neuron_module
+        hint = self._refresh_dmax_hint(d_in)
         ext = _lib.torch_ext()
-        if ext is not None and self._cpp_function_applies(x_seq, d_in, bias, approx, ste_mode):
+        if ext is not None and self._cpp_function_applies(x_seq, d_in, bias, approx, ste_mode, hint):
+            if not getattr(self, '_dmax_from_ext', False):
+                ext.forget_dmax(d_in.detach())
+                self._dmax_from_ext = True
             # the common regime: the C++ autograd Function over the same C ABI (no Python on
             # the forward or backward path, no window-length read in the forward)
             y = ext.axonal_common(x_seq, self.recurrent_weights, d_in, bias, drop, float(self.sigma),
@@ -59,14 +63,29 @@ class AxonalHipScans:
                                   float(alpha), bool(self.config.detach_reset))
         else:
             y = self._axonal_function(x_seq, d_in, bias, drop, p_spread, sid, gamma, alpha, approx,
-                                      ste_mode)
+                                      ste_mode, hint)
         self.x_seq = x_seq
         self.rec_now_seq = None
         if self.store_v_seq:
             self.v_seq = None
         return y
 
-    def _cpp_function_applies(self, x_seq, d_in, bias, approx, ste_mode):
+    def _refresh_dmax_hint(self, d_in):
+        """The largest delay of a recent call, which lets the forward run before reading the
+        window length (None: unknown). The Python Function's read sets it; after a call of
+        the C++ Function it is the max d that Function's backward took for these delays --
+        kept by the extension per delay storage, whose entry the layer clears when it first
+        hands its delays over (an entry written before could belong to freed memory that the
+        delays now occupy)."""
+        ext = _lib.torch_ext()
+        d = d_in.detach()
+        if ext is not None and getattr(self, '_dmax_from_ext', False) and d.is_cuda:
+            v = ext.seen_dmax(d)
+            if v == v:
+                self._dmax_hint = float(v)
+        return getattr(self, '_dmax_hint', None)
+
+    def _cpp_function_applies(self, x_seq, d_in, bias, approx, ste_mode, dmax_hint=None):
         """Whether the call takes the C++ autograd Function: the common regime (soft taps of
         a uniform half-width up to 8 lags of non-zero weight, decay charge, hard reset to 0,
         N <= 256) and gradients wanted. Its forward does not read the window length (its
@@ -79,18 +98,23 @@ class AxonalHipScans:
             x_seq.requires_grad or self.recurrent_weights.requires_grad or d_in.requires_grad
             or (bias is not None and bias.requires_grad))
         return (wants_grad and not approx and not ste_mode and not self.use_sig_p and N <= 256
+                and deferred_read_safe(dmax_hint, self.sigma)
                 and x_seq.numel() <= STRAIGHT_LINE_MAX_ELEMS and x_seq.dtype == torch.float32
                 and nm.v_reset is not None and float(nm.v_reset) == 0.0
                 and not getattr(nm, 'decay_input', False) and 0.0 <= float(self.sigma) <= 3.0
                 and os.environ.get('DELREC_AXONAL_FWD') != 'tiled')
 
-    def _axonal_function(self, x_seq, d_in, bias, drop, p_spread, sid, gamma, alpha, approx, ste_mode):
+    def _axonal_function(self, x_seq, d_in, bias, drop, p_spread, sid, gamma, alpha, approx, ste_mode,
+                         dmax_hint=None):
         nm = self.neuron_module
-        return AxonalRecdelHip.apply(
-            x_seq, self.recurrent_weights, bias, d_in, p_spread, drop,
+        y, dmax = apply_with_hint(
+            dmax_hint, x_seq, self.recurrent_weights, bias, d_in, p_spread, drop,
             float(self.sigma), nm.tau, nm.v_threshold, nm.v_reset, self.use_sig_p,
             self.config.detach_reset, sid, gamma, approx, ste_mode, alpha,
             getattr(nm, 'decay_input', False))
+        if dmax is not None:
+            self._dmax_hint = dmax
+        return y
 
 
 class SynapticHipScans:

@@ -13,6 +13,11 @@ Modes (reference ``recdel_base.py:361-383``):
   approx     one rounded tap forward, the single-tap backward and the straight-through
              ``dd = sum gz * (y[t-lag-1] - y[t-lag])``;
   ste_mode   1: rounded tap forward, 2: two-tap interpolated forward; soft backward.
+
+Windows of more than 256 lags (the spike history the axonal kernels hold in registers) take
+the per-connection scans of the synaptic layer with every connection of source j at the
+source's delay, ``d[i, j] = d[j]``: the same triangle taps and the same sums, the delay
+gradient ``dd[j] = sum_i dd[i, j]`` (soft taps; the hard-tap modes raise for such windows).
 """
 
 import ctypes
@@ -29,6 +34,8 @@ from .delays import build_lag, build_lag_interp
 
 
 STRAIGHT_LINE_MAX_ELEMS = 1 << 28   # (T, B, N) fp32 outputs addressed with 32-bit offsets
+REGISTER_LAGS = 256                 # spike history the axonal kernels hold (lags 1 .. 256)
+
 
 
 def _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v_reset, TB=1):
@@ -41,9 +48,30 @@ def _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v
             and os.environ.get('DELREC_AXONAL_FWD') != 'tiled')
 
 
-# the caller's grad mode at apply() (forward() itself runs with gradients disabled, and
-# ctx.needs_input_grad follows the inputs' requires_grad even under torch.no_grad())
+def deferred_read_safe(dmax_hint, sigma, margin=16.0):
+    """Whether the straight-line forward may run before max d is read: a known recent max d
+    (``dmax_hint``, None when unknown) leaves ``margin`` steps of the register history to
+    spare. A window that jumps past it anyway still fails loudly (NaN outputs, an error in the
+    backward)."""
+    return dmax_hint is not None and window_length_f32(float(dmax_hint) + margin, 1.0 + float(sigma)) - 1 <= REGISTER_LAGS
+
+
+# per thread: the caller's grad mode at apply() (forward() itself runs with gradients disabled,
+# and ctx.needs_input_grad follows the inputs' requires_grad even under torch.no_grad()); the
+# caller's max-delay hint for this call (``dmax_hint``, set by the layer); the max d the
+# forward read (``last_dmax``, for the layer)
 _APPLY_STATE = threading.local()
+
+
+def apply_with_hint(dmax_hint, *args):
+    """``AxonalRecdelHip.apply`` with a known recent max d; returns ``(y, max d read or None)``."""
+    _APPLY_STATE.dmax_hint = dmax_hint
+    _APPLY_STATE.last_dmax = None
+    try:
+        y = AxonalRecdelHip.apply(*args)
+    finally:
+        _APPLY_STATE.dmax_hint = None
+    return y, _APPLY_STATE.last_dmax
 
 
 class AxonalRecdelHip(torch.autograd.Function):
@@ -87,6 +115,7 @@ class AxonalRecdelHip(torch.autograd.Function):
         # arrived). Without gradients the read stays synchronous so that an over-long window
         # raises.
         if (getattr(_APPLY_STATE, 'grad', True) and any(ctx.needs_input_grad[:5])
+                and deferred_read_safe(getattr(_APPLY_STATE, 'dmax_hint', None), sigma)
                 and _straight_line_forward(N, sigma, use_sig_p, approx, ste_mode, decay_input, v_reset,
                                            T * B)):
             ticket = ctypes.c_uint32(0)
@@ -106,6 +135,13 @@ class AxonalRecdelHip(torch.autograd.Function):
             d_max, s_max = read_scalars(dc.max(), s_vec.max())
         else:
             (d_max,), s_max = read_scalars(dc.max()), 1.0 + sigma
+        _APPLY_STATE.last_dmax = float(d_max)
+        if window_length_f32(d_max, s_max) - 1 > REGISTER_LAGS:
+            if approx or ste_mode:
+                raise _lib.DelrecError('delrec_axonal_fwd', _lib.DELREC_ERR_WINDOW,
+                                       f'the hard-tap modes (approx, STE) take windows of at most '
+                                       f'{REGISTER_LAGS} lags; max d = {d_max:g}')
+            return _long_window_forward(ctx, x, W, d, dc, s_vec, sigma, bc, m, lif, p_spread)
         lag = frac = None
         if ste_mode:
             L = window_length_f32(d_max, s_max)
@@ -137,6 +173,8 @@ class AxonalRecdelHip(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, gy):
+        if ctx.meta[0] == 'long':
+            return _long_window_backward(ctx, gy)
         u, z, bits, Wc, dc, s_vec, m, lag, p_spread = ctx.saved_tensors
         T, B, N, L, w_bf16, sigma, use_sig_p, mode, w_dtype = ctx.meta
         if isinstance(L, _lib.PostedMax):
@@ -174,6 +212,40 @@ class AxonalRecdelHip(torch.autograd.Function):
         if dW is not None and w_dtype != torch.float32:
             dW = dW.to(w_dtype)
         return (dx, dW, db, dd, dp) + (None,) * 13
+
+
+def _long_window_forward(ctx, x, W, d, dc, s_vec, sigma, bc, m, lif, p_spread):
+    """The axonal layer through the synaptic scans with d[i, j] = d[j] (windows beyond the
+    register history)."""
+    from .synaptic_eventdriven import syn_forward
+    N = x.shape[-1]
+    d_syn = dc.unsqueeze(0).expand(N, N).contiguous()
+    y, u, bits, L, Wc, w_bf16, s_max, _ = syn_forward(x, W, d_syn, None, None, s_vec, 1.0 + sigma, dc, bc, m, lif)
+    ctx.save_for_backward(u, y, bits, Wc, d_syn, s_vec, m, p_spread)
+    ctx.meta = ('long', L, w_bf16, sigma, s_max, W.dtype, s_vec is not None)
+    ctx.lif = lif
+    return attach_bits(y, bits)
+
+
+def _long_window_backward(ctx, gy):
+    from .synaptic_eventdriven import syn_backward
+    u, y, bits, Wc, d_syn, s_vec, m, p_spread = ctx.saved_tensors
+    _, L, w_bf16, sigma, s_max, w_dtype, use_sig_p = ctx.meta
+    need_p = use_sig_p and ctx.needs_input_grad[4]
+    dx, dW, dd, ds, db = syn_backward(gy, u, y, bits, Wc, w_bf16, d_syn, None, None, s_vec, 1.0 + sigma, s_max, m,
+                                      ctx.lif, L, ctx.needs_input_grad[1], ctx.needs_input_grad[3], need_p,
+                                      ctx.needs_input_grad[2])
+    if dd is not None:
+        dd = dd.sum(0)          # every connection of source j carries d[j]
+    dp = None
+    if need_p:
+        with torch.enable_grad():
+            p_ = p_spread.detach().to(torch.float32).requires_grad_(True)
+            (dp,) = torch.autograd.grad(1.0 + 2.0 * sigma * torch.sigmoid(p_), p_, ds)
+        dp = dp.to(p_spread.dtype)
+    if dW is not None and w_dtype != torch.float32:
+        dW = dW.to(w_dtype)
+    return (dx, dW, db, dd, dp) + (None,) * 13
 
 
 # The reference's name for this Function (``delrec.triton_kernels.AxonalRecdelTriton``).

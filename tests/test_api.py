@@ -259,25 +259,29 @@ def test_straight_line_forward_keeps_outputs_within_32_bit_offsets():
 def test_cpp_function_only_when_gradients_are_wanted():
     """The C++ autograd Function's forward does not read the window length (its backward
     rejects a window the forward could not hold), so it is taken only when gradients are
-    wanted; without them the Python Function reads the window first and raises on an
-    over-long one."""
+    wanted and the last max d seen for the delays leaves the register history room; otherwise
+    the Python Function reads the window first (and routes a long one to the synaptic scans)."""
     from delrec.delay_layers import axonal_recdel
     cfg = base_config(0)
     cfg.sigma_init = 1.0
     layer = axonal_recdel(cfg, 32)
     x = torch.zeros(T, B, 32)
     d = layer.recurrent_delays
-    assert layer._cpp_function_applies(x.requires_grad_(True), d, None, False, 0)
-    assert layer._cpp_function_applies(torch.zeros(T, B, 32), d, None, False, 0)   # W, d require grad
+    # without a known max d (no earlier call) the window is read first
+    assert not layer._cpp_function_applies(x.requires_grad_(True), d, None, False, 0, None)
+    # a known max d whose window comes near the register history
+    assert not layer._cpp_function_applies(x, d, None, False, 0, 240.0)
+    assert layer._cpp_function_applies(x, d, None, False, 0, 20.0)
+    assert layer._cpp_function_applies(torch.zeros(T, B, 32), d, None, False, 0, 20.0)   # W, d require grad
     with torch.no_grad():
-        assert not layer._cpp_function_applies(x, d, None, False, 0)
+        assert not layer._cpp_function_applies(x, d, None, False, 0, 20.0)
     for p in layer.parameters():
         p.requires_grad_(False)
-    assert not layer._cpp_function_applies(torch.zeros(T, B, 32), d, None, False, 0)
+    assert not layer._cpp_function_applies(torch.zeros(T, B, 32), d, None, False, 0, 20.0)
     for p in layer.parameters():
         p.requires_grad_(True)
-    assert not layer._cpp_function_applies(x, d, None, True, 0)      # approx
-    assert not layer._cpp_function_applies(x, d, None, False, 1)     # STE
+    assert not layer._cpp_function_applies(x, d, None, True, 0, 20.0)      # approx
+    assert not layer._cpp_function_applies(x, d, None, False, 1, 20.0)     # STE
 
 
 def test_reference_import_path_resolves_to_the_hip_modules():

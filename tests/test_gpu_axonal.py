@@ -42,7 +42,7 @@ CASES = [
 ]
 
 
-def _run(dev, T, B, N, dmax, sigma, extra, seed=0):
+def _run(dev, T, B, N, dmax, sigma, extra, seed=0, hint=False):
     from delrec.kernels import AxonalRecdelHip
     g = gen(seed)
     x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
@@ -63,24 +63,48 @@ def _run(dev, T, B, N, dmax, sigma, extra, seed=0):
     bg = bias.to(dev).requires_grad_(True) if bias is not None else None
     pg = p.to(dev).requires_grad_(True) if p is not None else torch.zeros(N, device=dev)
     dg = drop.to(dev) if drop is not None else None
-    y = AxonalRecdelHip.apply(leaves[0], leaves[1], bg, leaves[2], pg, dg, sigma, lif.tau,
-                              lif.v_threshold, lif.v_reset, p is not None, lif.detach_reset,
-                              0 if surr[0] == 'triangle' else 1, 1.0, False, 0, 2.0,
-                              lif.decay_input)
+    # hint: a known max d, so the forward may run before reading the window length
+    from delrec.kernels.recdel_base import apply_with_hint
+    y, _ = apply_with_hint(float(d.max()) if hint else None,
+                           leaves[0], leaves[1], bg, leaves[2], pg, dg, sigma, lif.tau,
+                           lif.v_threshold, lif.v_reset, p is not None, lif.detach_reset,
+                           0 if surr[0] == 'triangle' else 1, 1.0, False, 0, 2.0,
+                           lif.decay_input)
     (y * gy.to(dev)).sum().backward()
     torch.cuda.synchronize()
     return y.detach().cpu(), y_ref, u_ref, gref, leaves, bg, pg, lif
 
 
+# windows beyond the 256 lags of spike history the axonal kernels hold: the per-connection
+# synaptic scans with d[i, j] = d[j] (soft taps), incl. a learned spread, bias, soft reset
+LONG_CASES = [
+    (320, 2, 48, 300.0, 0.5, {}),
+    (300, 2, 40, 290.0, 0.7, {'sig_p': True}),
+    (300, 2, 40, 280.0, 0.0, {'bias': True, 'soft': True}),
+]
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize('case', CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}d{c[3]}s{c[4]}{"".join(c[5])}'
-                                            for c in CASES])
+@pytest.mark.parametrize('case', CASES + LONG_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}d{c[3]}s{c[4]}{"".join(c[5])}'
+                                                          for c in CASES + LONG_CASES])
 def test_axonal_fwd_bwd_matches_oracle(dev, case, monkeypatch):
+    _check_case(dev, case, monkeypatch)
+
+
+# the same with the largest delay already known (the deferred window read of the common regime)
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', [CASES[i] for i in (1, 3, 16, 17, 18)],
+                         ids=[f'T{c[0]}B{c[1]}N{c[2]}d{c[3]}' for c in [CASES[i] for i in (1, 3, 16, 17, 18)]])
+def test_axonal_deferred_window_read_matches_oracle(dev, case, monkeypatch):
+    _check_case(dev, case, monkeypatch, hint=True)
+
+
+def _check_case(dev, case, monkeypatch, hint=False):
     T, B, N, dmax, sigma, extra = case
-    print(f'case {case}', flush=True)
+    print(f'case {case} hint={hint}', flush=True)
     if extra.get('cj16'):
         monkeypatch.setenv('DELREC_AXONAL_CJ', '16')
-    y, y_ref, u_ref, gref, leaves, bg, pg, lif = _run(dev, T, B, N, dmax, sigma, extra)
+    y, y_ref, u_ref, gref, leaves, bg, pg, lif = _run(dev, T, B, N, dmax, sigma, extra, hint=hint)
     flip = first_flip(y, y_ref, u_ref, lif.v_threshold)
     assert flip is None, f'near-threshold flip at t={flip}; pick another seed'
     print(f'  spikes identical ({int(y.sum())} spikes of {y.numel()})')
@@ -200,27 +224,50 @@ def test_axonal_forward_posts_max_delay(dev, fused):
 
 
 @pytest.mark.gpu
-def test_window_beyond_256_lags_fails_loudly(dev):
-    """Delays whose taps reach past 256 lags: the forward without a window length cannot hold
-    them. Under gradients (the C++ Function) it writes NaN outputs and the backward raises;
-    without gradients the Python Function reads the window length and raises at once."""
+def test_window_beyond_256_lags_through_the_layer(dev):
+    """A layer whose delays reach 300 steps: the first call reads the window and takes the
+    synaptic scans (parity with the oracle), the hard-tap modes refuse such a window, and a
+    wrong max-delay hint (the window jumped past the register history between two calls)
+    still fails loudly: NaN outputs and an error in the backward, never silent spikes."""
     from delrec.delay_layers import axonal_recdel
     from delrec import _lib
     from configs.perf_MEM import Config
+    from oracle import scans
     cfg = Config()
     cfg.sigma_init = 0.5
     torch.manual_seed(0)
     layer = axonal_recdel(cfg, 64).to(dev)
     with torch.no_grad():
         layer.recurrent_delays[5] = 300.0
-    x = torch.randn(20, 2, 64, generator=gen(3)).to(dev)
-    print('no_grad forward', flush=True)
-    with torch.no_grad():
-        with pytest.raises(_lib.DelrecError) as err:
-            layer(x)
+    x = torch.randn(310, 2, 64, generator=gen(3)) * 1.2 + 0.4
+    print('forward + backward through the layer', flush=True)
+    xg = x.to(dev).requires_grad_(True)
+    y = layer(xg)
+    gy = torch.randn(310, 2, 64, generator=gen(4))
+    (y * gy.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    lif = lif_params(tau=float(layer.neuron_module.tau))
+    xr = x.clone().requires_grad_(True)
+    Wr = layer.recurrent_weights.detach().cpu().clone().requires_grad_(True)
+    dr = layer.recurrent_delays.detach().cpu().clone().requires_grad_(True)
+    y_ref, ext = scans.axonal_v2(xr, Wr, dr, lif, sigma=float(layer.sigma))
+    (y_ref * gy).sum().backward()
+    assert ext['L'] > 258
+    flip = first_flip(y.detach().cpu(), y_ref.detach(), ext['u'].detach(), lif.v_threshold)
+    assert flip is None, f'near-threshold flip at t={flip}'
+    scale = lambda r: ATOL * max(1.0, float(r.abs().max()))
+    assert_close(xg.grad, xr.grad, RTOL, scale(xr.grad), 'dx')
+    assert_close(layer.recurrent_weights.grad, Wr.grad, RTOL, scale(Wr.grad), 'dW')
+    assert_close(layer.recurrent_delays.grad, dr.grad, RTOL, scale(dr.grad), 'dd')
+    print('hard-tap mode with the long window', flush=True)
+    with pytest.raises(_lib.DelrecError) as err:
+        layer.multi_step_forward_triton(x.to(dev), approx=True)
     assert err.value.status == _lib.DELREC_ERR_WINDOW
-    print('forward + backward with gradients', flush=True)
-    xg = x.clone().requires_grad_(True)
+    print('stale max-delay hint', flush=True)
+    layer.zero_grad(set_to_none=True)
+    assert layer._dmax_hint == 300.0
+    layer._dmax_hint = 10.0
+    xg = x[:20].to(dev).requires_grad_(True)
     y = layer(xg)
     torch.cuda.synchronize()
     assert bool(torch.isnan(y).all()), 'the forward must not return spikes it could not compute'

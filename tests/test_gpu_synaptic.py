@@ -477,3 +477,33 @@ def test_hybrid_wrong_d_min_gives_nan(dev, env, monkeypatch):
         assert bool(dx.isnan().all())                # the whole backward refuses
     else:
         assert bool(u.isnan().any()) and bool(dx.isnan().any())
+
+
+# bases exactly 0 (where training clamps them): the source's first tap sits at lag 0 with
+# weight 0, which the offset-stacked backward reads as a zero-weight tap, not as a tap below
+# lag 1 (its safety net must not fire)
+@pytest.mark.gpu
+@pytest.mark.parametrize('bf16', [True, False], ids=['bf16', 'fp32'])
+def test_hybrid_zero_base_edge_tap(dev, bf16):
+    T, B, N, K = 20, 3, 64, 4
+    g = gen(8)
+    base = torch.rand(N, generator=g) * 6.0
+    base[::3] = 0.0
+    offsets = torch.randint(K + 1, (N, N), generator=g).float()
+    x = torch.randn(T, B, N, generator=g) * 1.2 + 0.3
+    W = torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)
+    if bf16:
+        W = W.bfloat16().float()
+    gy = torch.randn(T, B, N, generator=g)
+    lif = lif_params()
+    y_ref, u_ref, gref = oracle_synaptic(x, W, None, lif, 0.0, gy, base=base, offsets=offsets)
+    y, dx, layer = _hybrid_run(dev, T, B, N, W, base, offsets, bf16, 0.0, x, gy)
+    flip = first_flip(y, y_ref, u_ref, lif.v_threshold)
+    assert flip is None, f'near-threshold flip at t={flip}'
+    rtol = 2e-2 if bf16 else RTOL
+    scale = lambda r: ATOL * max(1.0, float(r.abs().max()))
+    assert bool(torch.isfinite(dx).all())
+    assert_close(dx, gref['x'], rtol, scale(gref['x']), 'dx')
+    assert_close(layer.recurrent_weights.grad.float(), gref['W'], rtol, scale(gref['W']), 'dW')
+    assert_close(layer.parametrizations.recurrent_delays.original.grad, gref['base'], rtol,
+                 scale(gref['base']), 'dbase')
