@@ -307,23 +307,36 @@ def cpu_baseline(layer, x, w, budget_s=60.0):
     step does not depend on T); the same at T' / 2 checks that the time per step does not
     depend on T' (the scaling assumed), reported as the ratio of the two per-step times."""
     from oracle import neuron as oneuron, scans
-    from oracle.delays import hybrid_delays
     cores = max(1, len(os.sched_getaffinity(0)))
+    threads = torch.get_num_threads()
     torch.set_num_threads(cores)
-    T, B, N = x.shape
-    lif = oneuron.LIFParams(tau=w['tau'])
+    try:
+        return _cpu_baseline(layer, x, w, budget_s, cores, oneuron, scans)
+    finally:
+        torch.set_num_threads(threads)
+
+
+def cpu_inputs(layer, x, w):
+    """Host copies of what the CPU baseline needs (the layer's weights and delays, its input
+    -- the first 32 steps of runs longer than 256 --, its full length): taken right after the
+    GPU measurement, so that the baseline can run after every GPU workload has been timed."""
+    from oracle.delays import hybrid_delays
     W = layer.recurrent_weights.detach().float().cpu()
-    if w['kind'] == 'axonal':
-        d = layer.recurrent_delays.detach().cpu()
-        fn = scans.axonal_v2
-    elif w['kind'] == 'hybrid':
+    if w['kind'] == 'hybrid':
         par = layer.parametrizations.recurrent_delays
         d = hybrid_delays(par.original.detach().cpu(), par[0].offsets.detach().float().cpu())
-        fn = scans.synaptic_v2
     else:
         d = layer.recurrent_delays.detach().cpu()
-        fn = scans.synaptic_v2
-    xc = x.detach().cpu()
+    T = x.shape[0]
+    return {'W': W, 'd': d, 'x': x[:T if T <= 256 else 32].detach().cpu(), 'T': T}
+
+
+def _cpu_baseline(layer, x, w, budget_s, cores, oneuron, scans):
+    inp = layer if isinstance(layer, dict) else cpu_inputs(layer, x, w)
+    W, d, xc, T = inp['W'], inp['d'], inp['x'], inp['T']
+    B, N = xc.shape[1], xc.shape[2]
+    lif = oneuron.LIFParams(tau=w['tau'])
+    fn = scans.axonal_v2 if w['kind'] == 'axonal' else scans.synaptic_v2
 
     def one(Tp):
         xs = xc[:Tp].clone().requires_grad_(True)
@@ -338,7 +351,7 @@ def cpu_baseline(layer, x, w, budget_s=60.0):
     # the median of 3 samples at T' and at T' / 2: T' = T where that fits the budget,
     # else the largest of 32, 16, 8 steps that does (one sample where none does)
     runs = 3
-    Tl = T
+    Tl = min(T, xc.shape[0])
     while Tl > 8 and per_step * Tl * 1.5 * runs > budget_s:
         Tl = min(Tl, 32) if Tl > 32 else Tl // 2
     if per_step * Tl * 1.5 * runs > budget_s:
@@ -529,10 +542,9 @@ def measure(name, steps, warmup, with_cpu):
     }
     if inter_ms is not None:
         line['inter_linear_ms'] = inter_ms
-    if with_cpu:
-        print(f'[bench] {name}: {ms:.2f} ms/step on the GPU; CPU baseline next', file=sys.stderr, flush=True)
-        line['cpu_baseline'] = cpu_baseline(m.layers[0], xs[0], w)
-    return line
+    print(f'[bench] {name}: {ms:.2f} ms/step on the GPU', file=sys.stderr, flush=True)
+    cpu_in = cpu_inputs(m.layers[0], xs[0], w) if with_cpu else None
+    return line, cpu_in
 
 
 def main():
@@ -564,7 +576,9 @@ def main():
         return
     from delrec import _lib
     _lib.load()
-    rec = measure(args.config, args.steps, args.warmup, not args.no_cpu)
+    # every GPU measurement first, then the CPU baselines (whose worker threads would
+    # otherwise compete with the host thread that feeds the GPU)
+    rec, cpu_in = measure(args.config, args.steps, args.warmup, not args.no_cpu)
     w = WORKLOADS[args.config]
     line = {
         'metric': 'neuron-timesteps/sec fwd+BPTT per recurrent layer; % HBM GB/s or MFMA peak',
@@ -590,19 +604,26 @@ def main():
     }
     if 'inter_linear_ms' in rec:
         line['inter_linear_ms'] = rec['inter_linear_ms']
-    if 'cpu_baseline' in rec:
-        line['cpu_baseline'] = rec['cpu_baseline']
-    # measured achievable peaks, and each dominant kernel's fraction of the measured one
-    peaks = measure_peaks()
-    line['peaks'] = peaks
-    with_measured(line['roofline'], peaks)
     extra = [c for c in args.extra.split(',') if c]
+    extra_cpu = {}
     if extra:
         line['extra'] = {}
         for c in extra:
             print(f'[bench] extra workload {c}', file=sys.stderr, flush=True)
-            line['extra'][c] = measure(c, args.steps, args.warmup, not args.no_cpu)
-            with_measured(line['extra'][c]['roofline'], peaks)
+            line['extra'][c], extra_cpu[c] = measure(c, args.steps, args.warmup, not args.no_cpu)
+    # measured achievable peaks, and each dominant kernel's fraction of the measured one
+    peaks = measure_peaks()
+    line['peaks'] = peaks
+    with_measured(line['roofline'], peaks)
+    for c in extra:
+        with_measured(line['extra'][c]['roofline'], peaks)
+    if cpu_in is not None:
+        print(f'[bench] CPU baseline {args.config}', file=sys.stderr, flush=True)
+        line['cpu_baseline'] = cpu_baseline(cpu_in, None, w)
+    for c in extra:
+        if extra_cpu.get(c) is not None:
+            print(f'[bench] CPU baseline {c}', file=sys.stderr, flush=True)
+            line['extra'][c]['cpu_baseline'] = cpu_baseline(extra_cpu[c], None, WORKLOADS[c])
     print(json.dumps(line), flush=True)
 
 
