@@ -229,7 +229,6 @@ __global__ void __launch_bounds__(256) hyb_bwd_farblk_kernel(HybBwd p) {
     constexpr int W = kHybBlockMax + KF - 1;
     __shared__ float sG[kHybBlockMax][kFarRows][65];
     __shared__ float sW[W][kFarRows][65];
-    __shared__ int slof[64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j0 = blockIdx.x * 64, b0 = blockIdx.y * kFarRows;
@@ -240,12 +239,28 @@ __global__ void __launch_bounds__(256) hyb_bwd_farblk_kernel(HybBwd p) {
     const size_t BN = (size_t)B * N;
     const Lif k = p.lif;
     const bool first = t0 == T - 1;
+    // the ring values phase 2 reads (its own lane mapping: row b0 + lane % 16, neurons
+    // 16 w + 4 (lane / 16) + q), issued first so that they arrive during phase 1
+    const int r2 = lane & (kFarRows - 1), b2 = b0 + r2;
+    int lof2[4];
+    float v2[4][W];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int jj = j0 + 16 * w + 4 * (lane >> 4) + q;
+        const int l = jj < N ? p.lof[jj] : 0;
+        lof2[q] = (jj < N && l >= P && b2 < B) ? l : -1;
+#pragma unroll
+        for (int x = 0; x < W; ++x) {
+            const int tau = tbase + l + x;
+            const bool rd = lof2[q] >= 0 && x < P + p.KF - 1 && tau < T && tau > t0 + P;
+            v2[q][x] = rd ? p.ring[((size_t)(tau % R) * N + jj) * B + b2] : 0.0f;
+        }
+    }
     // phase 1: lane = neuron j0 + lane, rows b0 + 4 w + rr
     const int j = j0 + lane;
     const bool inj = j < p.Nk;
     const int lof = j < N ? p.lof[j] : 0;
     const bool far = j < N && lof >= P;
-    if (w == 0) slof[lane] = far ? lof : -1;
     const int c = far ? p.colf[j] : 0;
     constexpr int RW = kFarRows / 4;                  // rows per wave
     float uu[RW][kHybBlockMax], gyv[RW][kHybBlockMax];
@@ -293,28 +308,20 @@ __global__ void __launch_bounds__(256) hyb_bwd_farblk_kernel(HybBwd p) {
     barrier_lds();   // (LDS only: no global value written here is read back in this launch)
     // phase 2: lane = row b0 + lane % 16; neurons 16 w + 4 (lane / 16) + q
     {
-        const int r = lane & (kFarRows - 1), b = b0 + r;
-        const bool bok = b < B;
+        const int r = r2, b = b2;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int jl = 16 * w + 4 * (lane >> 4) + q, jj = j0 + jl;
-            const int lj = slof[jl];
-            if (lj < 0 || !bok) continue;
+            const int lj = lof2[q];
+            if (lj < 0) continue;
 #pragma unroll
             for (int tt = 0; tt < kHybBlockMax; ++tt)
                 if (tt < P && t0 + 1 + tt < T)
                     p.ring[((size_t)((t0 + 1 + tt) % R) * N + jj) * B + b] = sG[tt][r][jl];
-            float v[W];
 #pragma unroll
             for (int x = 0; x < W; ++x) {
                 const int tau = tbase + lj + x;
-                const bool rd = x < P + p.KF - 1 && tau < T && tau > t0 + P;
-                v[x] = rd ? p.ring[((size_t)(tau % R) * N + jj) * B + b] : 0.0f;
-            }
-#pragma unroll
-            for (int x = 0; x < W; ++x) {
-                const int tau = tbase + lj + x;
-                sW[x][r][jl] = (tau <= t0 + P && tau < T) ? sG[max(tau - t0 - 1, 0)][r][jl] : v[x];
+                sW[x][r][jl] = (tau <= t0 + P && tau < T) ? sG[max(tau - t0 - 1, 0)][r][jl] : v2[q][x];
             }
         }
     }
@@ -358,19 +365,22 @@ __global__ void __launch_bounds__(256) hyb_bwd_farblk_kernel(HybBwd p) {
     }
 }
 
-// Step 4: RB = 2 batch rows per workgroup (one workgroup per CU at B = 512), the near sources
-// (compact index c, source perm[c]) on the threads. On entry, from global memory, all of it
-// independent of the chain: the packed near-to-near weights wnp[ci][c] into LDS, the block's
-// near product summed over its splits into LDS, and each (c, row) item's u, gy and older ring
-// values into registers. Per step t, latest first:
+// Step 4: RB = 2 batch rows per workgroup (one workgroup per CU at B = 512), 1024 threads (four
+// waves per SIMD to hide the LDS and VALU latencies of a short chain). An item is one near
+// source (compact index c, source perm[c]) and batch row: thread q owns item q for the LIF.
+// On entry, from global memory, all of it independent of the chain: each item's u, gy, older
+// ring values and state into registers, the block's near product summed over its splits and
+// the packed near-to-near weights wnp[ci][c] into LDS. Per step t, latest first:
 //  a G_j(t + 1) = that product row + sum over near receivers ci of w * gr_ci(t + 1 + e) from
 //    the LDS window of the block's near gr (slot s = step t0 - P + 1 + s; slots >= P, steps
-//    past the block, stay 0: the product already holds those) -- one thread per near source,
-//    its RB rows together; into the ring and an LDS copy of the block's G (tau <= t0 + 1);
+//    past the block, stay 0: the product already holds those) -- four threads per item, each
+//    a quarter of the receivers, summed across the four lanes; into the ring and an LDS copy
+//    of the block's G (tau <= t0 + 1);
 //  b the LIF backward of the items: gfut from that copy (tau <= t0 + 1) or the ring (written
 //    by earlier launches), gr into the history and the window.
 constexpr int kNearRows = 2;
-constexpr int kNearItems = (kHybNearMax * kNearRows + 255) / 256;   // (c, row) items per thread
+constexpr int kNearThreads = 1024;
+static_assert(kHybNearMax * kNearRows <= kNearThreads / 2, "at least two threads per item");
 
 namespace {
 
@@ -382,181 +392,168 @@ __host__ __device__ inline int near_ldw(int nslot) { return nslot | 1; }
 }  // namespace
 
 template <int KF>
-__global__ void __launch_bounds__(256) hyb_bwd_near_kernel(HybBwd p) {
-    constexpr int RB = kNearRows;
+__global__ void __launch_bounds__(kNearThreads) hyb_bwd_near_kernel(HybBwd p) {
+    constexpr int RB = kNearRows, NT = kNearThreads;
     extern __shared__ float sm[];
     const int Nn = p.Nn, P = p.P, D = p.D, T = p.T, N = p.N, B = p.B, R = p.R, t0 = p.t0;
     const int nslot = P + D;
     const int ldw = near_ldw(nslot);                  // per-receiver pitch of the window
-    const int Nn8 = (Nn + 7) & ~7;                    // receivers padded to the inner loop's groups
-    uint32_t* wl = reinterpret_cast<uint32_t*>(sm);   // [Nn8][Nn] packed weights (rows >= Nn: 0)
-    float* grw = sm + (size_t)Nn8 * Nn;               // [RB][Nn8][ldw]: gr of near receiver ci at slot s
-    float* gnp = grw + (size_t)RB * Nn8 * ldw;        // [P][RB][Nn]: the near product, summed
+    const int Nq = (Nn + 15) & ~15;                   // receivers padded: sp parts of groups of 4
+    uint32_t* wl = reinterpret_cast<uint32_t*>(sm);   // [Nq][Nn] packed weights (rows >= Nn: 0)
+    float* grw = sm + (size_t)Nq * Nn;                // [RB][Nq][ldw]: gr of near receiver ci at slot s
+    float* gnp = grw + (size_t)RB * Nq * ldw;         // [P][RB][Nn]: the near product, summed
     float* gq = gnp + (size_t)P * RB * Nn;            // [P][RB][Nn]: G(tau), slot tau - (t0 - P + 2)
     const int tid = threadIdx.x;
     const int b0 = blockIdx.x * RB;
     const int tb = max(t0 - P + 1, 0);
     const int ns = t0 - tb + 1;
     const int tbase = t0 - P + 1;                     // step of window slot 0
-    // start-up: every load that does not depend on the chain, in as few round trips as the
-    // registers allow -- the items' sources, the block product's partials of this
-    // workgroup's rows (16 splits per round), the packed weights (half per round); then the
-    // items' u, gy, older ring values and state
     const size_t BN = (size_t)B * N;
     const Lif k = p.lif;
     const bool first = t0 == T - 1;
-    int jv[kNearItems];
+    // start-up loads: the item's source, then its u, gy, older ring values and state; the
+    // block product's partials (16 splits per round) and the packed weights
+    const int ci_ = tid % Nn, ri_ = tid / Nn, bi_ = b0 + ri_;
+    const bool own = tid < Nn * RB && bi_ < B;
+    const int j = own ? p.perm[ci_] : 0;
+    const int lofj = own ? p.lof[j] : 0;
+    const size_t bj = (size_t)(own ? bi_ : 0) * N + j;
+    float hv[KF], uu[kHybBlockMax], gyv[kHybBlockMax], rg[kHybBlockMax][KF];
 #pragma unroll
-    for (int e = 0; e < kNearItems; ++e) {
-        const int q = tid + 256 * e, c = q % Nn, r = q / Nn;
-        jv[e] = (q < Nn * RB && b0 + r < B) ? p.perm[c] : -1;
+    for (int f = 0; f < KF; ++f) hv[f] = (own && f < p.KF) ? p.h[(size_t)f * N + j] : 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < kHybBlockMax; ++tt) {
+        const int t = t0 - tt;
+        const bool live = own && tt < ns;
+        const size_t o = (size_t)(live ? t : 0) * BN + bj;
+        uu[tt] = live ? p.u_in[o] : 0.0f;
+        gyv[tt] = live ? p.gy[o] : 0.0f;
+#pragma unroll
+        for (int f = 0; f < KF; ++f) {
+            const int tau = t + lofj + f;
+            const bool rd = live && f < p.KF && tau < T && tau > t0 + 1;
+            rg[tt][f] = rd ? p.ring[((size_t)(tau % R) * N + j) * B + bi_] : 0.0f;
+        }
     }
-    constexpr int GI = (kHybBlockMax * RB * kHybNearMax + 255) / 256;   // product items per thread
-    float gs[GI];
+    float lam = (own && !first) ? p.state[bj] : 0.0f;
+    float db = (own && !first && p.dbp) ? p.dbp[bj] : 0.0f;
+    const float mv = (own && p.drop) ? p.drop[bj] : 1.0f;
     {
+        constexpr int GI = (kHybBlockMax * RB * kHybNearMax + NT - 1) / NT;   // product items per thread
         const size_t ks_stride = (size_t)B * P * p.Nnp;
         const int ng = P * RB * Nn;
+        float gs[GI];
 #pragma unroll
         for (int e = 0; e < GI; ++e) gs[e] = 0.0f;
-        for (int k0 = 0; k0 < p.KSn; k0 += 16) {
-            float v[GI][16];
+        for (int k0 = 0; k0 < p.KSn; k0 += 8) {
+            float v[GI][8];
 #pragma unroll
             for (int e = 0; e < GI; ++e) {
-                const int q = tid + 256 * e, c = q % Nn, rr = q / Nn, r = rr % RB, row = rr / RB, b = b0 + r;
+                const int q = tid + NT * e, c = q % Nn, rr = q / Nn, r = rr % RB, row = rr / RB, b = b0 + r;
                 const bool ok = q < ng && b < B;
                 const float* src = p.npart + ((size_t)(ok ? b : 0) * P + (ok ? row : 0)) * p.Nnp + (ok ? c : 0);
 #pragma unroll
-                for (int x = 0; x < 16; ++x) v[e][x] = (ok && k0 + x < p.KSn) ? src[(size_t)(k0 + x) * ks_stride] : 0.0f;
+                for (int x = 0; x < 8; ++x) v[e][x] = (ok && k0 + x < p.KSn) ? src[(size_t)(k0 + x) * ks_stride] : 0.0f;
             }
 #pragma unroll
             for (int e = 0; e < GI; ++e)
 #pragma unroll
-                for (int x = 0; x < 16; ++x) gs[e] += v[e][x];
+                for (int x = 0; x < 8; ++x) gs[e] += v[e][x];
         }
 #pragma unroll
         for (int e = 0; e < GI; ++e) {
-            const int q = tid + 256 * e;
+            const int q = tid + NT * e;
             if (q < ng) gnp[q] = gs[e];
         }
     }
     {
-        constexpr int WH = (kHybNearMax * kHybNearMax + 511) / 512;      // weights per thread per round
+        constexpr int WH = (kHybNearMax * kHybNearMax + 2 * NT - 1) / (2 * NT);   // weights per thread and round
         const int nw = Nn * Nn;
-        for (int q = nw + tid; q < Nn8 * Nn; q += 256) wl[q] = 0u;
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
             uint32_t v[WH];
 #pragma unroll
             for (int e = 0; e < WH; ++e) {
-                const int q = (h2 * WH + e) * 256 + tid;
+                const int q = (h2 * WH + e) * NT + tid;
                 v[e] = q < nw ? p.wnp[q] : 0u;
             }
 #pragma unroll
             for (int e = 0; e < WH; ++e) {
-                const int q = (h2 * WH + e) * 256 + tid;
+                const int q = (h2 * WH + e) * NT + tid;
                 if (q < nw) wl[q] = v[e];
             }
         }
+        for (int q = nw + tid; q < Nq * Nn; q += NT) wl[q] = 0u;
     }
-    for (int q = tid; q < RB * Nn8 * ldw; q += 256) grw[q] = 0.0f;
-    int lofv[kNearItems];
-    float hv[kNearItems][KF], uu[kNearItems][kHybBlockMax], gyv[kNearItems][kHybBlockMax];
-    float rg[kNearItems][kHybBlockMax][KF], lam[kNearItems], db[kNearItems], mv[kNearItems];
-#pragma unroll
-    for (int e = 0; e < kNearItems; ++e) {
-        const int q = tid + 256 * e, r = q / Nn, b = b0 + r;
-        const bool ok = jv[e] >= 0;
-        const int j = ok ? jv[e] : 0;
-        lofv[e] = ok ? p.lof[j] : 0;
-        const size_t bj = (size_t)(ok ? b : 0) * N + j;
-#pragma unroll
-        for (int f = 0; f < KF; ++f) hv[e][f] = (ok && f < p.KF) ? p.h[(size_t)f * N + j] : 0.0f;
-#pragma unroll
-        for (int tt = 0; tt < kHybBlockMax; ++tt) {
-            const int t = t0 - tt;
-            const bool live = ok && tt < ns;
-            const size_t o = (size_t)(live ? t : 0) * BN + bj;
-            uu[e][tt] = live ? p.u_in[o] : 0.0f;
-            gyv[e][tt] = live ? p.gy[o] : 0.0f;
-#pragma unroll
-            for (int f = 0; f < KF; ++f) {
-                const int tau = t + lofv[e] + f;
-                const bool rd = live && f < p.KF && tau < T && tau > t0 + 1;
-                rg[e][tt][f] = rd ? p.ring[((size_t)(tau % R) * N + j) * B + b] : 0.0f;
-            }
-        }
-        lam[e] = (ok && !first) ? p.state[bj] : 0.0f;
-        db[e] = (ok && !first && p.dbp) ? p.dbp[bj] : 0.0f;
-        mv[e] = (ok && p.drop) ? p.drop[bj] : 1.0f;
-    }
+    for (int q = tid; q < RB * Nq * ldw; q += NT) grw[q] = 0.0f;
     barrier_lds();
+    // phase a mapping: sp = 4 (or 2 past 256 items) threads per item, item ia = tid / sp, part
+    // pa = tid % sp (receivers ci = sp m + pa)
+    const int sp = Nn * RB <= NT / 4 ? 4 : 2;
+    const int ia = tid / sp, pa = tid % sp;
+    const bool aown = ia < Nn * RB && b0 + ia / Nn < B;
+    const int ca = aown ? ia % Nn : 0, ra = aown ? ia / Nn : 0, ba = b0 + ra;   // idle threads: item 0's
+    const int ja = aown ? p.perm[ca] : 0;                                     // (in-bounds) reads
 #pragma unroll
     for (int tt = 0; tt < kHybBlockMax; ++tt) {
         if (tt >= ns) break;                          // (static indices into the item arrays)
         const int t = t0 - tt;
         const int row = t - tbase;                    // the product's row of tau = t + 1
-        // a: G(t + 1) of the items (one near source and batch row each); the receivers in
-        // groups of 8 (rows past Nn are zero weights), their LDS reads issued together. A
-        // valid offset e < D always lands in the window: slot row + 1 + e < P + D
-#pragma unroll
-        for (int e = 0; e < kNearItems; ++e) {
-            if (jv[e] < 0) continue;
-            const int q = tid + 256 * e, c = q % Nn, r = q / Nn, b = b0 + r;
+        // a: G(t + 1). A valid offset e < D always lands in the window: row + 1 + e < P + D
+        {
             float acc = 0.0f;
-            const uint32_t* wc = wl + c;
-            const float* gw = grw + (size_t)r * Nn8 * ldw + row + 1;   // slot row + 1 + e of receiver ci
-            for (int c0 = 0; c0 < Nn8; c0 += 8) {
-                uint32_t pw[8];
+            const uint32_t* wc = wl + (size_t)pa * Nn + (aown ? ca : 0);
+            const float* gw = grw + ((size_t)ra * Nq + pa) * ldw + row + 1;
+            const int nm = Nq / sp;                   // a multiple of 4
+            for (int m0 = 0; m0 < nm; m0 += 4) {
+                uint32_t pw[4];
 #pragma unroll
-                for (int x = 0; x < 8; ++x) pw[x] = wc[(size_t)(c0 + x) * Nn];
-                float gv[8];
+                for (int x = 0; x < 4; ++x) pw[x] = wc[(size_t)(sp * (m0 + x)) * Nn];
+                float gv[4];
 #pragma unroll
-                for (int x = 0; x < 8; ++x) gv[x] = gw[(size_t)(c0 + x) * ldw + (int)(pw[x] & 0xFu)];
+                for (int x = 0; x < 4; ++x) gv[x] = gw[(size_t)(sp * (m0 + x)) * ldw + (int)(pw[x] & 0xFu)];
 #pragma unroll
-                for (int x = 0; x < 8; ++x) acc = fmaf(__uint_as_float(pw[x] & ~0xFu), gv[x], acc);
+                for (int x = 0; x < 4; ++x) acc = fmaf(__uint_as_float(pw[x] & ~0xFu), gv[x], acc);
             }
-            const float sum = acc + gnp[((size_t)row * RB + r) * Nn + c];
-            gq[((size_t)row * RB + r) * Nn + c] = sum;
-            if (t + 1 < T) p.ring[((size_t)((t + 1) % R) * N + jv[e]) * B + b] = sum;
+            acc += __shfl_xor(acc, 1);
+            if (sp == 4) acc += __shfl_xor(acc, 2);
+            if (aown && pa == 0) {
+                const float sum = acc + gnp[((size_t)row * RB + ra) * Nn + ca];
+                gq[((size_t)row * RB + ra) * Nn + ca] = sum;
+                if (t + 1 < T) p.ring[((size_t)((t + 1) % R) * N + ja) * B + ba] = sum;
+            }
         }
         barrier_lds();
-        // b: the LIF backward of the items
-#pragma unroll
-        for (int e = 0; e < kNearItems; ++e) {
-            if (jv[e] < 0) continue;
-            const int q = tid + 256 * e, c = q % Nn, r = q / Nn, b = b0 + r, j = jv[e];
+        // b: the LIF backward of the thread's item
+        if (own) {
             float gf = 0.0f;
 #pragma unroll
             for (int f = 0; f < KF; ++f) {
-                const int tau = t + lofv[e] + f;
-                float gv = rg[e][tt][f];
-                if (tau <= t0 + 1) gv = tau < T ? gq[((size_t)(tau - tbase - 1) * RB + r) * Nn + c] : 0.0f;
-                gf = fmaf(hv[e][f], gv, gf);
+                const int tau = t + lofj + f;
+                float gv = rg[tt][f];
+                if (tau <= t0 + 1) gv = tau < T ? gq[((size_t)(tau - tbase - 1) * RB + ri_) * Nn + ci_] : 0.0f;
+                gf = fmaf(hv[f], gv, gf);
             }
-            const float y = lif_fire(k, uu[e][tt]);
-            const float du = lif_backward(k, gyv[e][tt] + gf, uu[e][tt], y, lam[e]);
-            lam[e] = k.decay * du;
+            const float y = lif_fire(k, uu[tt]);
+            const float du = lif_backward(k, gyv[tt] + gf, uu[tt], y, lam);
+            lam = k.decay * du;
             const float da = lif_dx(k, du);
-            const float gr = da * mv[e];
-            const size_t bj = (size_t)b * N + j, o = (size_t)t * BN + bj;
+            const float gr = da * mv;
+            const size_t o = (size_t)t * BN + bj;
             p.dx[o] = da;
             if (p.gr) p.gr[o] = gr;
-            db[e] += gr;
-            const size_t ho = (size_t)b * p.lda + (size_t)(p.PF + t) * p.Nk + j;
+            db += gr;
+            const size_t ho = (size_t)bi_ * p.lda + (size_t)(p.PF + t) * p.Nk + j;
             const uint32_t hi = hyb_bf16_rne(gr);
             p.hhi[ho] = (uint16_t)hi;
             p.hlo[ho] = (uint16_t)hyb_bf16_rne(gr - __uint_as_float(hi << 16));
-            grw[((size_t)r * Nn8 + c) * ldw + row] = gr;
+            grw[((size_t)ri_ * Nq + ci_) * ldw + row] = gr;
         }
         barrier_lds();
     }
-#pragma unroll
-    for (int e = 0; e < kNearItems; ++e) {
-        if (jv[e] < 0) continue;
-        const int q = tid + 256 * e, r = q / Nn, b = b0 + r;
-        const size_t bj = (size_t)b * N + jv[e];
-        p.state[bj] = lam[e];
-        if (p.dbp) p.dbp[bj] = db[e];
+    if (own) {
+        p.state[bj] = lam;
+        if (p.dbp) p.dbp[bj] = db;
     }
 }
 
@@ -889,8 +886,8 @@ void launch_hyb_bwd_farblk(const HybBwd& a, hipStream_t stream) {
 }
 
 size_t hyb_bwd_near_lds(int P, int D, int Nn) {
-    const size_t Nn8 = (size_t)(Nn + 7) & ~(size_t)7;
-    return (Nn8 * Nn + (size_t)kNearRows * Nn8 * near_ldw(P + D) + (size_t)2 * P * kNearRows * Nn) * sizeof(float);
+    const size_t Nq = (size_t)(Nn + 15) & ~(size_t)15;
+    return (Nq * Nn + (size_t)kNearRows * Nq * near_ldw(P + D) + (size_t)2 * P * kNearRows * Nn) * sizeof(float);
 }
 
 bool launch_hyb_bwd_near(const HybBwd& a, hipStream_t stream) {
@@ -900,7 +897,7 @@ bool launch_hyb_bwd_near(const HybBwd& a, hipStream_t stream) {
     const dim3 grid((a.B + kNearRows - 1) / kNearRows);
 #define DELREC_NEAR(KFV)                                                                         \
     ensure_lds((const void*)hyb_bwd_near_kernel<KFV>, lds);                                      \
-    hipLaunchKernelGGL(hyb_bwd_near_kernel<KFV>, grid, dim3(256), lds, stream, a);
+    hipLaunchKernelGGL(hyb_bwd_near_kernel<KFV>, grid, dim3(kNearThreads), lds, stream, a);
     if (a.KF <= 2) { DELREC_NEAR(2) } else if (a.KF <= 4) { DELREC_NEAR(4) } else { DELREC_NEAR(8) }
 #undef DELREC_NEAR
     return true;
