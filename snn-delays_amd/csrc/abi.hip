@@ -1253,9 +1253,26 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
             launch_hyb_pack(pk, false, s);
             launch_hyb_near_pack(pk, wnp, s);
         }
+        // the far product on the 4:2 sparse MFMA (bf16 W, blocks of 4 steps, 3 .. 6 offsets):
+        // its compressed W^T (values, then position words) takes the far planes' room, which
+        // holds it (5 Q / 4 <= D uint4 per 8 receivers and column); DELREC_FAR_SPARSE=0 keeps
+        // the dense product
+        const int fq = planes == 1 && P == 4 ? far_sparse_q(hq.D) : 0;
+        const size_t fwv = Nf > 0 && fq ? far_sparse_wv(hq.Nk, Nfp, fq) : 0;   // Nfp: 256 columns per tile
+        FarSparse fs{};
+        fs.a0 = ghi; fs.a1 = glo; fs.lda = hq.lda; fs.B = B; fs.rows = B * P; fs.Nk = hq.Nk; fs.Np = Nfp;
+        fs.KS = fwv ? far_sparse_splits(B * P, Nfp, hq.Nk, num_cus()) : 1;
+        fs.wv = Pf; fs.wi = reinterpret_cast<const uint32_t*>(Pf + fwv); fs.part = fpart;
+        const bool sparse = fwv > 0 && getenv_flag_off("DELREC_FAR_SPARSE") &&
+                            fwv + (fwv + 3) / 4 <= fplane && fwv * 16 < ((size_t)1 << 31) &&
+                            (size_t)fs.KS * B * P * Nfp <= hz.fpart &&
+                            far_sparse_lds(fq) <= (size_t)max_lds_bytes();
         if (Nf > 0) {
             pk.Np = Nfp; pk.c0 = Nn; pk.nc = Nf; pk.out = Pf;
-            launch_hyb_pack(pk, false, s);
+            if (sparse)
+                launch_far_sparse_pack(pk, fq, Pf, reinterpret_cast<uint32_t*>(Pf + fwv), s);
+            else
+                launch_hyb_pack(pk, false, s);
         }
         // gr before the first step (front pad) and past the last one (slices PF + T ..) are 0;
         // every column of the block's slices is written before a product reads them (the far
@@ -1272,8 +1289,8 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         gf.p0 = Pf; gf.p1 = planes > 1 ? Pf + fplane : nullptr; gf.Np = Nfp; gf.Kt = hq.Kt; gf.Nk = hq.Nk;
         // one-plane P: 256 x 256 tiles of 8 waves (128 x 256 tiles of 4 waves with DELREC_FAR256=0)
         const bool far256 = planes == 1 && getenv_flag_off("DELREC_FAR256");
-        gf.KS = Nf == 0 ? 1 : far256 ? lagstep_gemm256_splits(B * P, Nfp, hq.Kt, num_cus())
-                                     : lagstep_splits(B * P, Nfp, hq.Kt, num_cus(), fcol);
+        gf.KS = Nf == 0 ? 1 : sparse ? fs.KS : far256 ? lagstep_gemm256_splits(B * P, Nfp, hq.Kt, num_cus())
+                                                      : lagstep_splits(B * P, Nfp, hq.Kt, num_cus(), fcol);
         gf.part = fpart; gf.cm = 0;
         LagStepGemm gn = gf;   // block t0: near G(t0 - P + 2 + tt), the block's steps' t + 1
         gn.p0 = Pn; gn.p1 = planes > 1 ? Pn + nplane : nullptr; gn.Np = Nnp;
@@ -1283,8 +1300,10 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
             fprintf(stderr, "[delrec] hybrid offset-stacked backward: T=%d B=%d N=%d D=%d P=%d; near sources %d "
                     "(product KS=%d, %d row tiles, chain of %d-row workgroups); far sources %d (product KS=%d, "
                     "%s tiles, %d row tiles); far LIF grid %d x %d\n", T, B, N, hq.D, P, Nn, Nn > 0 ? gn.KS : 0,
-                    (B * P + 127) / 128, 2, Nf, Nf > 0 ? gf.KS : 0, far256 ? "256x256" : "128x256",
-                    (B * P + 255) / 256, (hq.Nk + 63) / 64, (B + 15) / 16);
+                    (B * P + 127) / 128, 2, Nf, Nf > 0 ? gf.KS : 0,
+                    sparse ? "sparse 128x256" : far256 ? "256x256" : "128x256",
+                    (B * P + (far256 && !sparse ? 255 : 127)) / (far256 && !sparse ? 256 : 128), (hq.Nk + 63) / 64,
+                    (B + 15) / 16);
         HybBwd l{};
         l.T = T; l.B = B; l.N = N; l.Nk = hq.Nk; l.KF = KF; l.R = hq.R; l.P = P; l.D = hq.D; l.PF = hq.PF;
         l.lda = hq.lda;
@@ -1299,7 +1318,10 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         for (int t0 = T - 1; t0 >= 0 && ok; t0 -= P) {
             if (Nf > 0) {
                 gf.aoff = (size_t)(hq.PF + t0 + 1) * hq.Nk;
-                if (far256)
+                fs.aoff = gf.aoff;
+                if (sparse)
+                    launch_far_sparse(fs, fq, s);
+                else if (far256)
                     launch_lagstep_gemm256(gf, s);
                 else
                     launch_lagstep_gemm(gf, 2, s, planes, fcol / 2);

@@ -1,0 +1,298 @@
+// The hybrid backward's per-block far product on the 4:2 sparse MFMA of gfx950
+// (v_smfmac_f32_16x16x64_bf16).
+//
+// For a block of P = 4 steps starting at t0 (reverse time), the far sources j need
+//   G_j(tau) = sum_i sum_e W^(e)_ij gr_i(tau + e),   tau = t0 + 1 + tt, tt < 4,
+// with W^(e) = W [off_ij - omin == e]: every connection has exactly one offset, so along the
+// contraction k = (receiver i, offset e) each row j of W^T holds one non-zero per receiver.
+// Grouping k in fours as (receivers 2p, 2p + 1) x (offsets 2q, 2q + 1) leaves at most two
+// non-zeros per group, which is the sparse MFMA's 4:2 format: W^T is the compressed operand
+// (rows j), the gr history the dense one (columns (b, tt)), and D offsets cost Q = ceil(D / 2)
+// sparse products of K = 64 per 32 receivers instead of D dense products of K = 32 -- 0.6 of
+// the MFMA issue at D = 5, and the history is read once per block slice instead of once per
+// (step, offset).
+//
+// Operand layouts (lane layout of the instruction: A lane l = row l % 16, compressed values
+// 2g, 2g + 1 belong to sparsity group 4 (l / 16) + g, their 2-bit positions in bits 4g .. 4g + 3
+// of the index word; B lane l = column l % 16, slot s = k 32 (s / 8) + 8 (l / 16) + s % 8;
+// C lane l = column l % 16, element e = row 4 (l / 16) + e):
+//  - group G of a 64-k product covers receiver pair pr(G) = 4 (G' / 2) + G' % 2 (+ 2 for
+//    G >= 8, G' = G mod 8) of the 32-receiver chunk at offsets 2q, 2q + 1, positions
+//    (2p, 2q), (2p + 1, 2q), (2p, 2q + 1), (2p + 1, 2q + 1); so lane group g of the dense
+//    operand holds pairs 4g .. 4g + 3 = receivers 8g .. 8g + 7 at slices tau + 2q and
+//    tau + 2q + 1: two 16-byte reads of the batch-major history, interleaved by 32-bit words;
+//  - the compressed W^T is stored per (chunk, q, 16-column block, lane): 8 bf16 (16 bytes) and
+//    a 32-bit index word (positions in the low 16 bits), so a wave loads a fragment as one
+//    1 KB and one 256-byte run.
+// Precision: bf16 W is exact; gr enters as its hi and lo bf16 planes (two products), fp32
+// accumulation -- the dense kernel's arithmetic, summed in another order.
+//
+// Workgroup: 4 waves (one per SIMD), a tile of 256 columns j x 128 rows (b, tt) (32 batch
+// rows); wave (wj, wc) owns 128 j x 64 rows: 8 x 4 blocks of 16 x 16, 128 accumulator
+// registers. Per 32-receiver chunk the tile's history -- 32 batch rows x (3 + 2Q) slices x
+// 64 bytes, both planes -- is staged through LDS (double-buffered, one register stage of
+// loads in flight); the compressed W fragments come straight from global memory (L2) into
+// registers, each q's fragments reloaded for the next chunk right after their last use.
+// k is split over KS workgroups; partials as the dense product's, row-major [KS][rows][Np].
+#include "kernels.h"
+
+namespace delrec {
+
+namespace {
+
+typedef float fs_floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 fs_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 fs_bf16x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t fs_u32x8 __attribute__((ext_vector_type(8)));
+
+__device__ uint32_t fs_buffer_load_u32(i32x4 rsrc, int voff, int soff, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i32");
+
+constexpr int kFarSparseRows = 32;    // batch rows per tile (x 4 steps = 128 product rows)
+
+// pair of the 32-receiver chunk held by sparsity group G of a 64-k product
+__host__ __device__ inline int fs_pair(int G) {
+    const int h = G >> 3, g = G & 7;
+    return 4 * (g >> 1) + (g & 1) + 2 * h;
+}
+
+}  // namespace
+
+// One thread per (chunk, q, column block, lane): the 8 compressed values and positions of
+// sparsity groups 4 (lane / 16) .. + 3 for column jb * 16 + lane % 16 (source perm[c0 + col];
+// columns past nc are 0). An offset outside [omin, omin + D) packs a NaN weight into the
+// q = 0 product, as the dense pack does, so that the results it enters are NaN.
+__global__ void __launch_bounds__(256) far_sparse_pack_kernel(HybPack p, int Q, uint4* __restrict__ wv,
+                                                              uint32_t* __restrict__ wi) {
+    const int NJB = p.Np / 16, nch = p.Nk / 32;
+    const size_t total = (size_t)nch * Q * NJB * 64;
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const int lane = (int)(id & 63);
+    const size_t r1 = id >> 6;
+    const int jb = (int)(r1 % NJB);
+    const size_t r2 = r1 / NJB;
+    const int q = (int)(r2 % Q), c = (int)(r2 / Q);
+    const int col = jb * 16 + (lane & 15);
+    const int j = col < p.nc ? p.perm[p.c0 + col] : -1;
+    const uint16_t* Wh = static_cast<const uint16_t*>(p.W);
+    uint32_t words[4];
+    uint32_t idx = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int G = 4 * (lane >> 4) + g;
+        const int i0 = c * 32 + 2 * fs_pair(G);
+        // receiver i0 sits at position 0 (offset 2q) or 2 (2q + 1), i0 + 1 at 1 or 3
+        int pos[2] = {0, 1};
+        uint32_t val[2] = {0u, 0u};
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int i = i0 + r;
+            if (j < 0 || i >= p.N) continue;
+            const size_t o = (size_t)i * p.N + j;
+            const int e = (int)p.off[o] - p.omin;
+            if (e < 0 || e >= p.D) {
+                if (q == 0) val[r] = 0x7FC0u;   // NaN
+            } else if (e == 2 * q || e == 2 * q + 1) {
+                val[r] = Wh[o];
+                pos[r] = r + 2 * (e - 2 * q);
+            }
+        }
+        // the two values of a group in ascending position
+        const bool sw = pos[0] > pos[1];
+        const uint32_t v0 = sw ? val[1] : val[0], v1 = sw ? val[0] : val[1];
+        const int p0 = sw ? pos[1] : pos[0], p1 = sw ? pos[0] : pos[1];
+        words[g] = v0 | (v1 << 16);
+        idx |= (uint32_t)(p0 | (p1 << 2)) << (4 * g);
+    }
+    wv[id] = make_uint4(words[0], words[1], words[2], words[3]);
+    wi[id] = idx;
+}
+
+template <int Q>
+__global__ void __launch_bounds__(256) far_sparse_kernel(FarSparse p) {
+    constexpr int S = 3 + 2 * Q;                          // staged slices per batch row
+    constexpr int RB = kFarSparseRows;
+    constexpr int BS = 16 * S;                            // words per batch row: [pair][slice]
+    constexpr int PL = RB * BS;                           // words per plane
+    constexpr int BUF = 2 * PL;                           // words per buffer (two planes)
+    constexpr int NS = S;                                 // staged uint4 per thread
+    static_assert(2 * RB * 4 == 256, "staging shape: one thread per (plane, batch row, quarter)");
+    extern __shared__ uint32_t lds[];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int wj = w & 1, wc = w >> 1;
+    const int lg = lane >> 4, lc = lane & 15;
+    const int NCT = (p.rows + 4 * RB - 1) / (4 * RB), NJT = p.Np / 256;
+    const int id = (int)blockIdx.x;
+    int ct, jt, ks;
+    if (NCT % 4 == 0 && NJT % 2 == 0) {
+        // XCD x (= id mod 8) serves a quarter of the row tiles x half of the column tiles
+        const int x = id & 7, slot = id >> 3, ncq = NCT / 4;
+        ks = slot % p.KS;
+        const int t = slot / p.KS;
+        ct = (x & 3) * ncq + t % ncq;
+        jt = (x >> 2) * (NJT / 2) + t / ncq;
+    } else {
+        ks = id % p.KS;
+        const int t = id / p.KS;
+        jt = t % NJT;
+        ct = t / NJT;
+    }
+    const int b0 = ct * RB, n0 = jt * 256;
+    const int nch = p.Nk / 32;
+    const int per = (nch + p.KS - 1) / p.KS;
+    const int c0 = ks * per, c1 = min(nch, c0 + per);
+    const int NJB = p.Np / 16;
+
+    const uint32_t hbytes = (uint32_t)((size_t)p.B * p.lda * 2);
+    const i32x4 rh0 = buffer_rsrc(p.a0, hbytes), rh1 = buffer_rsrc(p.a1, hbytes);
+    const size_t nfrag = (size_t)nch * Q * NJB * 64;
+    const i32x4 rwv = buffer_rsrc(p.wv, (uint32_t)(nfrag * 16)), rwi = buffer_rsrc(p.wi, (uint32_t)(nfrag * 4));
+    // staging: thread tid stages plane tid / 128 (wave-uniform), batch row (tid / 4) % 32 and
+    // 16-byte quarter tid % 4 of the chunk's 64 bytes, for every slice s < S (a uniform stride)
+    const bool hpl = __builtin_amdgcn_readfirstlane(w) >= 2;
+    const i32x4 rh = hpl ? rh1 : rh0;
+    const int sb = (tid >> 2) & 31, sq = tid & 3;
+    // batch rows past B land past the descriptor's end (zeros)
+    const uint32_t ho = (uint32_t)(((size_t)(b0 + sb) * p.lda + p.aoff + sq * 8) * 2);
+    const uint32_t hstep = (uint32_t)p.Nk * 2;
+    const int hl = (hpl ? PL : 0) + sb * BS + 4 * sq * S;   // word of (pair 4 sq, slice 0)
+    uint4 sreg[NS];
+    auto issue_stage = [&](int c) {
+#pragma unroll
+        for (int h = 0; h < NS; ++h)
+            sreg[h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rh, (int)(ho + (uint32_t)c * 64), h * hstep, 0));
+    };
+    // LDS: per plane and batch row, the chunk's 16 receiver pairs, each with its S slices in
+    // consecutive words, so that the two words of an operand group (one pair at slices
+    // tau + 2q, tau + 2q + 1) are adjacent
+    auto stash = [&](int buf) {
+        uint32_t* d = lds + buf * BUF + hl;
+#pragma unroll
+        for (int h = 0; h < NS; ++h) {
+            d[h] = sreg[h].x;
+            d[S + h] = sreg[h].y;
+            d[2 * S + h] = sreg[h].z;
+            d[3 * S + h] = sreg[h].w;
+        }
+    };
+    // compressed W fragments: wave's column blocks jb0 .. jb0 + 7
+    const int jb0 = (n0 + wj * 128) / 16;
+    uint4 av[Q][8];
+    uint32_t ai[Q][8];
+    auto load_w = [&](int c, int q) {
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {
+            const size_t f = (((size_t)c * Q + q) * NJB + jb0 + jb) * 64 + lane;
+            av[q][jb] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rwv, (int)(f * 16), 0, 0));
+            ai[q][jb] = fs_buffer_load_u32(rwi, (int)(f * 4), 0, 0);
+        }
+    };
+    fs_floatx4 acc[8][4];
+#pragma unroll
+    for (int jb = 0; jb < 8; ++jb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[jb][cb] = fs_floatx4{0.f, 0.f, 0.f, 0.f};
+    // dense-operand reads: column cb * 16 + lc of the wave's 64 rows is batch row
+    // wc * 16 + cb * 4 + lc / 4, step tt = lc % 4; pairs 4 lg .. + 3 at slices tt + 2q, + 1.
+    // Banks (word mod 64): tt adds 0 .. 3, lg 4 S lg, the batch row BS = 16 S (16 mod 64 for
+    // S = 9, 48 for S = 7): the 64 lanes of a read hit 64 distinct banks
+    const int bl = (wc * 16 + (lc >> 2)) * BS + 4 * lg * S + (lc & 3);
+
+    if (c0 < c1) {
+        issue_stage(c0);
+#pragma unroll
+        for (int q = 0; q < Q; ++q) load_w(c0, q);
+        stash(0);
+        barrier_lds();
+        if (c0 + 1 < c1) issue_stage(c0 + 1);
+    }
+    for (int c = c0; c < c1; ++c) {
+        const int buf = (c - c0) & 1;
+        const uint32_t* L = lds + buf * BUF;
+        const bool more = c + 1 < c1;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                // operand words: pair 4 lg + m at slice tt + 2q, then tt + 2q + 1
+                fs_bf16x16 bv[2];
+#pragma unroll
+                for (int pl = 0; pl < 2; ++pl) {
+                    const uint32_t* x = L + pl * PL + bl + cb * 4 * BS + 2 * q;
+                    bv[pl] = __builtin_bit_cast(fs_bf16x16, fs_u32x8{x[0], x[1], x[S], x[S + 1], x[2 * S], x[2 * S + 1],
+                                                                     x[3 * S], x[3 * S + 1]});
+                }
+#pragma unroll
+                for (int pl = 0; pl < 2; ++pl)
+#pragma unroll
+                    for (int jb = 0; jb < 8; ++jb)
+                        acc[jb][cb] = __builtin_amdgcn_smfmac_f32_16x16x64_bf16(
+                            __builtin_bit_cast(fs_bf16x8, av[q][jb]), bv[pl], acc[jb][cb], (int)ai[q][jb], 0, 0);
+            }
+            // this q's fragments are done for chunk c: the next chunk's (the last q's after
+            // the stage below, behind the history loads in the load queue)
+            if (more && q + 1 < Q) load_w(c + 1, q);
+        }
+        if (more) {
+            stash(buf ^ 1);
+            barrier_lds();
+            if (c + 2 < c1) issue_stage(c + 2);
+            load_w(c + 1, Q - 1);
+        }
+    }
+
+    float* out = p.part + (size_t)ks * p.rows * p.Np;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+        const int r = b0 * 4 + wc * 64 + cb * 16 + lc;
+        if (r >= p.rows) continue;
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {
+            const int j = n0 + wj * 128 + jb * 16 + 4 * lg;
+            *reinterpret_cast<fs_floatx4*>(out + (size_t)r * p.Np + j) = acc[jb][cb];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+
+int far_sparse_q(int D) { return D >= 3 && D <= 6 ? (D + 1) / 2 : 0; }
+
+size_t far_sparse_lds(int Q) {
+    return (size_t)2 * 2 * kFarSparseRows * 16 * (3 + 2 * Q) * sizeof(uint32_t);
+}
+
+size_t far_sparse_wv(int Nk, int Np, int Q) { return (size_t)(Nk / 32) * Q * (Np / 16) * 64; }
+
+int far_sparse_splits(int rows, int Np, int Nk, int cus) {
+    const int tiles = ((rows + 4 * kFarSparseRows - 1) / (4 * kFarSparseRows)) * (Np / 256);
+    const int nch = Nk / 32;
+    if (tiles < 1) return 1;
+    return std::max(1, std::min((cus + tiles - 1) / tiles, std::max(1, nch / 8)));
+}
+
+void launch_far_sparse_pack(const HybPack& a, int Q, uint4* wv, uint32_t* wi, hipStream_t stream) {
+    const size_t total = far_sparse_wv(a.Nk, a.Np, Q);
+    hipLaunchKernelGGL(far_sparse_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a, Q,
+                       wv, wi);
+}
+
+bool launch_far_sparse(const FarSparse& g, int Q, hipStream_t stream) {
+    const int tiles = ((g.rows + 4 * kFarSparseRows - 1) / (4 * kFarSparseRows)) * (g.Np / 256);
+    const dim3 grid((unsigned)(tiles * g.KS));
+    const size_t lds = far_sparse_lds(Q);
+    if (Q == 3) {
+        ensure_lds((const void*)far_sparse_kernel<3>, lds);
+        hipLaunchKernelGGL(far_sparse_kernel<3>, grid, dim3(256), lds, stream, g);
+        return true;
+    }
+    if (Q == 2) {
+        ensure_lds((const void*)far_sparse_kernel<2>, lds);
+        hipLaunchKernelGGL(far_sparse_kernel<2>, grid, dim3(256), lds, stream, g);
+        return true;
+    }
+    return false;
+}
+
+}  // namespace delrec

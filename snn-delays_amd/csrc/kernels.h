@@ -172,6 +172,17 @@ struct LagStepGemm {
     int cm;                      // column-major partials (a consumer that reads columns)
 };
 
+struct FarSparse {               // the hybrid backward's far product on the 4:2 sparse MFMA
+    const uint16_t* a0;          // gr history, hi / lo planes [b][slice][Nk]; slice 0 of the
+    const uint16_t* a1;          //   block's product at element aoff of each batch row
+    size_t lda, aoff;
+    int B, rows;                 // batch rows, product rows B * 4 (row b * 4 + step of the block)
+    int Nk, Np, KS;              // receivers (multiple of 32), far columns (multiple of 256), k splits
+    const uint4* wv;             // compressed W^T values [chunk][q][column block][lane]
+    const uint32_t* wi;          // their position words, same order
+    float* part;                 // [KS][rows][Np]
+};
+
 struct LagStepLif {
     int T, B, N, Nk, Np, KS, t, Lw;
     size_t lda;
@@ -341,6 +352,14 @@ void launch_hyb_pack(const HybPack& a, bool fwd, hipStream_t stream);
 void launch_hyb_taps(const HybTaps& a, hipStream_t stream);
 void launch_hyb_lif(const HybLif& l, int hw, hipStream_t stream);   // forward step
 
+// far product on the sparse MFMA: Q = ceil(D / 2) sparse products per 32 receivers (0: the
+// offset count is outside the supported 3 .. 6); blocks of 4 steps, bf16 W only
+int far_sparse_q(int D);
+size_t far_sparse_lds(int Q);
+size_t far_sparse_wv(int Nk, int Np, int Q);            // uint4 of values (and uint32 of positions)
+int far_sparse_splits(int rows, int Np, int Nk, int cus);
+void launch_far_sparse_pack(const HybPack& a, int Q, uint4* wv, uint32_t* wi, hipStream_t stream);
+bool launch_far_sparse(const FarSparse& g, int Q, hipStream_t stream);
 int lagstep_splits(int B, int Np, int Kt, int cus, int nc = 128);   // nc: workgroup columns
 int lagstep_block();
 size_t lagstep_gemm_lds(int pa, int pb = 2, int wn = 64);

@@ -19,7 +19,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG.parent / 'csrc'
 INCLUDE = PKG.parent.parent / 'include'
 OUT = PKG / 'libdelrec_hip.so'
-SOURCES = ('abi.hip', 'axonal.hip', 'gemm.hip', 'hybstep.hip', 'lagmm.hip', 'lagstep.hip', 'peaks.hip',
+SOURCES = ('abi.hip', 'axonal.hip', 'farsparse.hip', 'gemm.hip', 'hybstep.hip', 'lagmm.hip', 'lagstep.hip', 'peaks.hip',
            'readout.hip', 'spikelinear.hip', 'synaptic.hip')
 ARCH = os.environ.get('DELREC_OFFLOAD_ARCH', 'gfx950')
 
