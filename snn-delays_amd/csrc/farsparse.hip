@@ -49,6 +49,7 @@ __device__ uint32_t fs_buffer_load_u32(i32x4 rsrc, int voff, int soff, int aux)
     __asm("llvm.amdgcn.raw.buffer.load.i32");
 
 constexpr int kFarSparseRows = 32;    // batch rows per tile (x 4 steps = 128 product rows)
+constexpr int kFarSparsePairWords = 12;   // LDS words per receiver pair (slices + pad)
 
 // pair of the 32-receiver chunk held by sparsity group G of a 64-k product
 __host__ __device__ inline int fs_pair(int G) {
@@ -113,7 +114,9 @@ template <int Q>
 __global__ void __launch_bounds__(256) far_sparse_kernel(FarSparse p) {
     constexpr int S = 3 + 2 * Q;                          // staged slices per batch row
     constexpr int RB = kFarSparseRows;
-    constexpr int BS = 16 * S;                            // words per batch row: [pair][slice]
+    constexpr int PS = kFarSparsePairWords;               // words per pair: its S slices + pad
+    constexpr int BS = 16 * PS + 4;                       // words per batch row: [pair][slice]
+    static_assert(PS >= S && PS % 8 == 4 && BS % 64 == 4, "bank layout");
     constexpr int PL = RB * BS;                           // words per plane
     constexpr int BUF = 2 * PL;                           // words per buffer (two planes)
     constexpr int NS = S;                                 // staged uint4 per thread
@@ -148,46 +151,58 @@ __global__ void __launch_bounds__(256) far_sparse_kernel(FarSparse p) {
     const i32x4 rh0 = buffer_rsrc(p.a0, hbytes), rh1 = buffer_rsrc(p.a1, hbytes);
     const size_t nfrag = (size_t)nch * Q * NJB * 64;
     const i32x4 rwv = buffer_rsrc(p.wv, (uint32_t)(nfrag * 16)), rwi = buffer_rsrc(p.wi, (uint32_t)(nfrag * 4));
-    // staging: thread tid stages plane tid / 128 (wave-uniform), batch row (tid / 4) % 32 and
-    // 16-byte quarter tid % 4 of the chunk's 64 bytes, for every slice s < S (a uniform stride)
+    // staging: thread tid stages plane tid / 128 (wave-uniform), batch row b = (tid / 4) % 32
+    // and 16-byte quarter r = tid % 4 (pairs 4r .. 4r + 3) of the chunk's 64 bytes; load h
+    // takes slice (h + b) mod S, so that the four lanes of a row still read 64 contiguous bytes
+    // while the rows of one LDS store land in distinct banks
     const bool hpl = __builtin_amdgcn_readfirstlane(w) >= 2;
     const i32x4 rh = hpl ? rh1 : rh0;
     const int sb = (tid >> 2) & 31, sq = tid & 3;
     // batch rows past B land past the descriptor's end (zeros)
     const uint32_t ho = (uint32_t)(((size_t)(b0 + sb) * p.lda + p.aoff + sq * 8) * 2);
     const uint32_t hstep = (uint32_t)p.Nk * 2;
-    const int hl = (hpl ? PL : 0) + sb * BS + 4 * sq * S;   // word of (pair 4 sq, slice 0)
+    const int hl = (hpl ? PL : 0) + sb * BS + 4 * sq * PS;   // word of (pair 4 sq, slice 0)
     uint4 sreg[NS];
+    const int sr = sb % S;
+    auto slice_of = [&](int h) { return h + sr < S ? h + sr : h + sr - S; };
     auto issue_stage = [&](int c) {
 #pragma unroll
         for (int h = 0; h < NS; ++h)
-            sreg[h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rh, (int)(ho + (uint32_t)c * 64), h * hstep, 0));
+            sreg[h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(
+                rh, (int)(ho + (uint32_t)c * 64 + (uint32_t)slice_of(h) * hstep), 0, 0));
     };
-    // LDS: per plane and batch row, the chunk's 16 receiver pairs, each with its S slices in
-    // consecutive words, so that the two words of an operand group (one pair at slices
-    // tau + 2q, tau + 2q + 1) are adjacent
+    // LDS: per plane and batch row, the chunk's 16 receiver pairs at a pitch of PS words,
+    // each with its S slices in consecutive words, so that the two words of an operand group
+    // (one pair at slices tau + 2q, tau + 2q + 1) are adjacent
     auto stash = [&](int buf) {
         uint32_t* d = lds + buf * BUF + hl;
 #pragma unroll
         for (int h = 0; h < NS; ++h) {
-            d[h] = sreg[h].x;
-            d[S + h] = sreg[h].y;
-            d[2 * S + h] = sreg[h].z;
-            d[3 * S + h] = sreg[h].w;
+            const int sl = slice_of(h);
+            d[sl] = sreg[h].x;
+            d[PS + sl] = sreg[h].y;
+            d[2 * PS + sl] = sreg[h].z;
+            d[3 * PS + sl] = sreg[h].w;
         }
     };
-    // compressed W fragments: wave's column blocks jb0 .. jb0 + 7
+    // compressed W fragments of the wave's column blocks jb0 .. jb0 + 7 for q-step k (chunk
+    // c0 + k / Q, q = k mod Q), in register slot k mod 2: loaded right after step k - 2, one
+    // step ahead of their use
     const int jb0 = (n0 + wj * 128) / 16;
-    uint4 av[Q][8];
-    uint32_t ai[Q][8];
-    auto load_w = [&](int c, int q) {
+    uint4 av[2][8];
+    uint32_t ai[2][8];
+    auto load_w = [&](int k, int slot) {
+        const int c = c0 + k / Q, q = k % Q;
 #pragma unroll
         for (int jb = 0; jb < 8; ++jb) {
             const size_t f = (((size_t)c * Q + q) * NJB + jb0 + jb) * 64 + lane;
-            av[q][jb] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rwv, (int)(f * 16), 0, 0));
-            ai[q][jb] = fs_buffer_load_u32(rwi, (int)(f * 4), 0, 0);
+            av[slot][jb] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rwv, (int)(f * 16), 0, 0));
+            ai[slot][jb] = fs_buffer_load_u32(rwi, (int)(f * 4), 0, 0);
         }
     };
+    // the accumulators live in the AGPRs (the MFMA's AGPR form), which leaves the VGPRs to the
+    // operands in flight
+    asm volatile("; accumulators in AGPRs" ::"a"(0.0f));
     fs_floatx4 acc[8][4];
 #pragma unroll
     for (int jb = 0; jb < 8; ++jb)
@@ -195,52 +210,81 @@ __global__ void __launch_bounds__(256) far_sparse_kernel(FarSparse p) {
         for (int cb = 0; cb < 4; ++cb) acc[jb][cb] = fs_floatx4{0.f, 0.f, 0.f, 0.f};
     // dense-operand reads: column cb * 16 + lc of the wave's 64 rows is batch row
     // wc * 16 + cb * 4 + lc / 4, step tt = lc % 4; pairs 4 lg .. + 3 at slices tt + 2q, + 1.
-    // Banks (word mod 64): tt adds 0 .. 3, lg 4 S lg, the batch row BS = 16 S (16 mod 64 for
-    // S = 9, 48 for S = 7): the 64 lanes of a read hit 64 distinct banks
-    const int bl = (wc * 16 + (lc >> 2)) * BS + 4 * lg * S + (lc & 3);
-
-    if (c0 < c1) {
-        issue_stage(c0);
+    // Banks (word mod 64): tt adds 0 .. 3, the batch row 4 (BS = 4 mod 64) per row, lg 4 PS lg
+    // (16, 32 or 48 mod 64): the 64 lanes of a read hit 64 distinct banks, each half wave 32
+    // distinct banks mod 32
+    const int bl = (wc * 16 + (lc >> 2)) * BS + 4 * lg * PS + (lc & 3);
+    auto read_b = [&](const uint32_t* L, int cb, fs_bf16x16* bv) {
 #pragma unroll
-        for (int q = 0; q < Q; ++q) load_w(c0, q);
-        stash(0);
-        barrier_lds();
-        if (c0 + 1 < c1) issue_stage(c0 + 1);
-    }
-    for (int c = c0; c < c1; ++c) {
-        const int buf = (c - c0) & 1;
-        const uint32_t* L = lds + buf * BUF;
-        const bool more = c + 1 < c1;
+        for (int pl = 0; pl < 2; ++pl) {
+            const uint32_t* x = L + pl * PL + cb * 4 * BS;
+            bv[pl] = __builtin_bit_cast(fs_bf16x16, fs_u32x8{x[0], x[1], x[PS], x[PS + 1], x[2 * PS], x[2 * PS + 1],
+                                                             x[3 * PS], x[3 * PS + 1]});
+        }
+    };
+    const int ncl = c1 - c0, nstep = ncl * Q;
+    // One chunk = Q q-steps; q-step k (chunk k / Q) uses W slot k mod 2. In a step the 4
+    // column blocks run 16 products each while the next block's operands are read (ping-pong
+    // bA / bB; the next step's first block at the end). At a chunk's end: the next chunk's
+    // history (loaded during this chunk) into the other buffer, a barrier, and the loads of
+    // the chunk after it; then the compressed W of step k + 2 into the freed slot. Every load
+    // and barrier is unconditional (indices clamped to the last chunk / step), and the loop
+    // body is two chunks, so each slot and wait is static.
+    fs_bf16x16 bA[2], bB[2];
+    auto smfma = [&](int slot, int cb, const fs_bf16x16* bv) {
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+#pragma unroll
+            for (int jb = 0; jb < 8; ++jb)
+                acc[jb][cb] = __builtin_amdgcn_smfmac_f32_16x16x64_bf16(
+                    __builtin_bit_cast(fs_bf16x8, av[slot][jb]), bv[pl], acc[jb][cb], (int)ai[slot][jb], 0, 0);
+    };
+    auto chunk = [&](int cl, int s0) {
+        const uint32_t* L0 = lds + (cl & 1) * BUF + bl;
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-                // operand words: pair 4 lg + m at slice tt + 2q, then tt + 2q + 1
-                fs_bf16x16 bv[2];
-#pragma unroll
-                for (int pl = 0; pl < 2; ++pl) {
-                    const uint32_t* x = L + pl * PL + bl + cb * 4 * BS + 2 * q;
-                    bv[pl] = __builtin_bit_cast(fs_bf16x16, fs_u32x8{x[0], x[1], x[S], x[S + 1], x[2 * S], x[2 * S + 1],
-                                                                     x[3 * S], x[3 * S + 1]});
-                }
-#pragma unroll
-                for (int pl = 0; pl < 2; ++pl)
-#pragma unroll
-                    for (int jb = 0; jb < 8; ++jb)
-                        acc[jb][cb] = __builtin_amdgcn_smfmac_f32_16x16x64_bf16(
-                            __builtin_bit_cast(fs_bf16x8, av[q][jb]), bv[pl], acc[jb][cb], (int)ai[q][jb], 0, 0);
+            const int k = cl * Q + q, slot = (s0 + q) & 1;
+            const uint32_t* L = L0 + 2 * q;
+            read_b(L, 1, bB);
+            smfma(slot, 0, bA);
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+            read_b(L, 2, bA);
+            smfma(slot, 1, bB);
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+            read_b(L, 3, bB);
+            smfma(slot, 2, bA);
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+            if (q == Q - 1) {
+                stash((cl + 1) & 1);
+                barrier_lds();
+                issue_stage(c0 + min(cl + 2, ncl - 1));
+                read_b(lds + ((cl + 1) & 1) * BUF + bl, 0, bA);
+            } else {
+                read_b(L + 2, 0, bA);
             }
-            // this q's fragments are done for chunk c: the next chunk's (the last q's after
-            // the stage below, behind the history loads in the load queue)
-            if (more && q + 1 < Q) load_w(c + 1, q);
+            smfma(slot, 3, bB);
+            load_w(min(k + 2, nstep - 1), slot);
         }
-        if (more) {
-            stash(buf ^ 1);
-            barrier_lds();
-            if (c + 2 < c1) issue_stage(c + 2);
-            load_w(c + 1, Q - 1);
-        }
+    };
+
+    if (nstep > 0) {
+        issue_stage(c0);
+        load_w(0, 0);
+        load_w(min(1, nstep - 1), 1);
+        stash(0);
+        barrier_lds();
+        issue_stage(c0 + min(1, ncl - 1));
+        read_b(lds + bl, 0, bA);
     }
+    int cl = 0;
+    for (; cl + 1 < ncl; cl += 2) {
+        chunk(cl, 0);
+        chunk(cl + 1, Q & 1);
+    }
+    if (cl < ncl) chunk(cl, 0);
 
     float* out = p.part + (size_t)ks * p.rows * p.Np;
 #pragma unroll
@@ -260,7 +304,8 @@ __global__ void __launch_bounds__(256) far_sparse_kernel(FarSparse p) {
 int far_sparse_q(int D) { return D >= 3 && D <= 6 ? (D + 1) / 2 : 0; }
 
 size_t far_sparse_lds(int Q) {
-    return (size_t)2 * 2 * kFarSparseRows * 16 * (3 + 2 * Q) * sizeof(uint32_t);
+    (void)Q;   // the pair pitch holds up to 12 slices (Q <= 4)
+    return (size_t)2 * 2 * kFarSparseRows * (16 * kFarSparsePairWords + 4) * sizeof(uint32_t);
 }
 
 size_t far_sparse_wv(int Nk, int Np, int Q) { return (size_t)(Nk / 32) * Q * (Np / 16) * 64; }
