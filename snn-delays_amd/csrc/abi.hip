@@ -1241,32 +1241,48 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
             hipMemcpyAsync(colf, colf_h.data(), (size_t)N * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
             hipStreamSynchronize(s) != hipSuccess)
             return DELREC_ERR_LAUNCH;
-        const int Nnp = (Nn + 127) / 128 * 128, Nfp = (Nf + fcol - 1) / fcol * fcol;
+        // The far product on the 4:2 sparse MFMA where it can (bf16 W, blocks of 4 steps, 3 .. 6
+        // offsets; DELREC_FAR_SPARSE=0 keeps the dense one), the near one with
+        // DELREC_NEAR_SPARSE=1 (at C5's 95 near columns its one 256-column tile at 8 k-splits
+        // takes 36 us per block against 27 for the dense 128-column product): a compressed
+        // W^T (values, then position words) in place of the dense planes, 256 columns per
+        // tile. The plane room (Kt / 8) (Np + 384) holds either form of both parts: the
+        // compressed one takes 5 Q / 32 <= 20 D / 128 uint4 per receiver and column.
+        const int fq = planes == 1 && P == 4 ? far_sparse_q(hq.D) : 0;
+        const size_t proom = (size_t)planes * hz.planes;
+        const bool fits_lds = fq && far_sparse_lds(fq) <= (size_t)max_lds_bytes();
+        const size_t nwv = Nn > 0 && fits_lds ? far_sparse_wv(hq.Nk, 256, fq) : 0;
+        const int ksn = nwv ? far_sparse_splits(B * P, 256, hq.Nk, num_cus()) : 1;
+        const char* nse = getenv("DELREC_NEAR_SPARSE");
+        const bool nsparse = nwv > 0 && nse && strcmp(nse, "1") == 0 && nwv * 16 < ((size_t)1 << 31) &&
+                             (size_t)ksn * B * P * 256 <= hz.npart;
+        const int Nnp = nsparse ? 256 : (Nn + 127) / 128 * 128, Nfp = (Nf + fcol - 1) / fcol * fcol;
         const size_t nplane = (size_t)(hq.Kt / 8) * Nnp, fplane = (size_t)(hq.Kt / 8) * Nfp;
-        uint4* Pn = Pw;                              // near planes: hi (, lo)
-        uint4* Pf = Pw + (size_t)planes * nplane;    // far planes: hi (, lo)
+        const size_t nsize = nsparse ? nwv + (nwv + 3) / 4 : (size_t)planes * nplane;
+        uint4* Pn = Pw;              // near planes: hi (, lo), or the compressed near W^T
+        uint4* Pf = Pw + nsize;      // far planes: hi (, lo), or the compressed far W^T
         HybPack pk{};
         pk.N = N; pk.Nk = hq.Nk; pk.D = hq.D; pk.omin = a->off_min; pk.planes = planes;
         pk.W = a->W; pk.w_bf16 = a->w_bf16; pk.off = a->offsets; pk.perm = perm;
         if (Nn > 0) {
             pk.Np = Nnp; pk.c0 = 0; pk.nc = Nn; pk.out = Pn;
-            launch_hyb_pack(pk, false, s);
+            if (nsparse)
+                launch_far_sparse_pack(pk, fq, Pn, reinterpret_cast<uint32_t*>(Pn + nwv), s);
+            else
+                launch_hyb_pack(pk, false, s);
             launch_hyb_near_pack(pk, wnp, s);
         }
-        // the far product on the 4:2 sparse MFMA (bf16 W, blocks of 4 steps, 3 .. 6 offsets):
-        // its compressed W^T (values, then position words) takes the far planes' room, which
-        // holds it (5 Q / 4 <= D uint4 per 8 receivers and column); DELREC_FAR_SPARSE=0 keeps
-        // the dense product
-        const int fq = planes == 1 && P == 4 ? far_sparse_q(hq.D) : 0;
-        const size_t fwv = Nf > 0 && fq ? far_sparse_wv(hq.Nk, Nfp, fq) : 0;   // Nfp: 256 columns per tile
+        const size_t fwv = Nf > 0 && fits_lds ? far_sparse_wv(hq.Nk, Nfp, fq) : 0;   // Nfp: 256 columns per tile
         FarSparse fs{};
         fs.a0 = ghi; fs.a1 = glo; fs.lda = hq.lda; fs.B = B; fs.rows = B * P; fs.Nk = hq.Nk; fs.Np = Nfp;
         fs.KS = fwv ? far_sparse_splits(B * P, Nfp, hq.Nk, num_cus()) : 1;
         fs.wv = Pf; fs.wi = reinterpret_cast<const uint32_t*>(Pf + fwv); fs.part = fpart;
         const bool sparse = fwv > 0 && getenv_flag_off("DELREC_FAR_SPARSE") &&
-                            fwv + (fwv + 3) / 4 <= fplane && fwv * 16 < ((size_t)1 << 31) &&
-                            (size_t)fs.KS * B * P * Nfp <= hz.fpart &&
-                            far_sparse_lds(fq) <= (size_t)max_lds_bytes();
+                            nsize + fwv + (fwv + 3) / 4 <= proom && fwv * 16 < ((size_t)1 << 31) &&
+                            (size_t)fs.KS * B * P * Nfp <= hz.fpart;
+        if (!sparse && nsize + (size_t)planes * fplane > proom) return DELREC_ERR_WORKSPACE;
+        FarSparse fn = fs;   // the near product: 256 columns, its own splits and partials
+        fn.Np = 256; fn.KS = ksn; fn.wv = Pn; fn.wi = reinterpret_cast<const uint32_t*>(Pn + nwv); fn.part = npart;
         if (Nf > 0) {
             pk.Np = Nfp; pk.c0 = Nn; pk.nc = Nf; pk.out = Pf;
             if (sparse)
@@ -1294,13 +1310,13 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         gf.part = fpart; gf.cm = 0;
         LagStepGemm gn = gf;   // block t0: near G(t0 - P + 2 + tt), the block's steps' t + 1
         gn.p0 = Pn; gn.p1 = planes > 1 ? Pn + nplane : nullptr; gn.Np = Nnp;
-        gn.KS = Nn > 0 ? lagstep_splits(B * P, Nnp, hq.Kt, num_cus()) : 1;
+        gn.KS = Nn == 0 ? 1 : nsparse ? ksn : lagstep_splits(B * P, Nnp, hq.Kt, num_cus());
         gn.part = npart;
         if (getenv("DELREC_LOG_PLAN"))
             fprintf(stderr, "[delrec] hybrid offset-stacked backward: T=%d B=%d N=%d D=%d P=%d; near sources %d "
-                    "(product KS=%d, %d row tiles, chain of %d-row workgroups); far sources %d (product KS=%d, "
+                    "(product KS=%d%s, %d row tiles, chain of %d-row workgroups); far sources %d (product KS=%d, "
                     "%s tiles, %d row tiles); far LIF grid %d x %d\n", T, B, N, hq.D, P, Nn, Nn > 0 ? gn.KS : 0,
-                    (B * P + 127) / 128, 2, Nf, Nf > 0 ? gf.KS : 0,
+                    nsparse ? " sparse" : "", (B * P + 127) / 128, 2, Nf, Nf > 0 ? gf.KS : 0,
                     sparse ? "sparse 128x256" : far256 ? "256x256" : "128x256",
                     (B * P + (far256 && !sparse ? 255 : 127)) / (far256 && !sparse ? 256 : 128), (hq.Nk + 63) / 64,
                     (B + 15) / 16);
@@ -1330,7 +1346,11 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
             launch_hyb_bwd_farblk(l, s);
             if (Nn > 0) {
                 gn.aoff = (size_t)(hq.PF + t0 - P + 2) * hq.Nk;
-                launch_lagstep_gemm(gn, 2, s, planes);
+                fn.aoff = gn.aoff;
+                if (nsparse)
+                    launch_far_sparse(fn, fq, s);
+                else
+                    launch_lagstep_gemm(gn, 2, s, planes);
                 ok = launch_hyb_bwd_near(l, s);
             }
         }

@@ -1,12 +1,13 @@
-"""GPU parity of the hybrid backward's far product on the 4:2 sparse MFMA
-(``far_sparse_kernel``, csrc/farsparse.hip): the default in the offset-stacked scans for bf16
-W, blocks of 4 steps and 3 .. 6 offsets (one to three sparse products per 32 receivers).
+"""GPU parity of the hybrid backward's products on the 4:2 sparse MFMA (``far_sparse_kernel``,
+csrc/farsparse.hip): the default for the far sources in the offset-stacked scans with bf16
+W, blocks of 4 steps and 3 .. 6 offsets (one to three sparse products per 32 receivers), and
+for the near ones with DELREC_NEAR_SPARSE=1 (set in every test here).
 
 Against the float64 oracle (``test_gpu_synaptic.test_hybrid_fwd_bwd_matches_oracle``, offset-stacked scans
 forced): each offset count of the form, one and two 256-column tiles, row tiles past the
-batch's last row, a triangle of three taps, T not a multiple of the block. Against the dense
-far product (``DELREC_FAR_SPARSE=0``) on a batch of 128 rows, where the tiles take the
-XCD-grouped order: the same gradients up to the order of fp32 sums (both products are exact
+batch's last row, a triangle of three taps, T not a multiple of the block. On a batch of 128
+rows, where the tiles take the XCD-grouped order, against both dense products (``DELREC_FAR_SPARSE=0``,
+``DELREC_NEAR_SPARSE=0``): the same gradients up to the order of fp32 sums (both products are exact
 in their bf16 operands), and bit-identical results from two runs of the sparse form.
 """
 
@@ -30,12 +31,15 @@ SPARSE_CASES = [
 @pytest.mark.parametrize('case', SPARSE_CASES, ids=[f'T{c[0]}B{c[1]}N{c[2]}K{c[4]}s{c[6]}' for c in SPARSE_CASES])
 def test_far_sparse_matches_oracle(dev, case, monkeypatch, capfd):
     monkeypatch.setenv('DELREC_SYN_HYBSTEP', '1')
+    monkeypatch.setenv('DELREC_NEAR_SPARSE', '1')
     monkeypatch.setenv('DELREC_HYB_FWD', '0')
     monkeypatch.setenv('DELREC_LOG_PLAN', '1')
     hybrid_parity(dev, case)
     plan = capfd.readouterr().err
     print(plan, flush=True)
     assert 'sparse 128x256 tiles' in plan, plan
+    if 'near sources 0 ' not in plan:
+        assert ' sparse, ' in plan, plan   # the near product on the sparse MFMA as well
 
 
 def _grads(layer, x, gy):
@@ -61,12 +65,14 @@ def test_far_sparse_matches_dense_product(dev, monkeypatch, capfd):
     gy = torch.randn(T, B, N, generator=g).to(dev)
     layer = hybrid_layer(N, W, base, offsets, dev, bf16=True, sigma_init=0.0)
     monkeypatch.setenv('DELREC_SYN_HYBSTEP', '1')
+    monkeypatch.setenv('DELREC_NEAR_SPARSE', '1')
     monkeypatch.setenv('DELREC_LOG_PLAN', '1')
     sparse = _grads(layer, x, gy)
     again = _grads(layer, x, gy)
     plan = capfd.readouterr().err
     assert 'sparse 128x256 tiles, 4 row tiles' in plan, plan
     monkeypatch.setenv('DELREC_FAR_SPARSE', '0')
+    monkeypatch.delenv('DELREC_NEAR_SPARSE')
     dense = _grads(layer, x, gy)
     plan = capfd.readouterr().err
     assert 'far sources' in plan and 'sparse' not in plan, plan
@@ -77,5 +83,9 @@ def test_far_sparse_matches_dense_product(dev, monkeypatch, capfd):
         print(f'  {name}: max |sparse - dense| {err:.3e} (|dense| max {ref:.3e})', flush=True)
         if name == 'y':
             assert torch.equal(a, c), 'the forward differs'
+        elif name == 'dW':
+            # returned in bf16 (W's dtype): fp32 sums a few ulps apart may round to adjacent bf16
+            # values, one bf16 ulp (2^-7 relative at most) apart
+            torch.testing.assert_close(a, c, rtol=2.0 ** -7, atol=1e-5 * ref)
         else:
             torch.testing.assert_close(a, c, rtol=1e-4, atol=1e-5 * ref)
