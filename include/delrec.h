@@ -193,6 +193,13 @@ typedef struct {
     float d_min;                 /* hybrid: as in delrec_syn_fwd_args                    */
     int32_t off_min;
     int32_t off_count;
+    /* hybrid, optional (near_known != 0): how many sources j have a first lag
+       max(1, floor(1 + (base_j + off_min) - s_uniform) + 1) (fp32, in that order) below 4 and
+       below 2. The offset-stacked backward splits the sources by first lag; given these counts
+       (e.g. from the forward's own host read) it runs without a host synchronisation,
+       otherwise (near_known == 0, as a zeroed struct has it) it reads the first lags back from
+       the device once per call. Counts that do not match the device's make every output NaN. */
+    int32_t near_known, near_lt4, near_lt2;
 } delrec_syn_bwd_args;
 
 /* Plain multi-step LIF layer (no recurrence). */
@@ -341,7 +348,7 @@ int delrec_peak_mfma(int32_t kind, int32_t iters, float* sink, size_t sink_bytes
 const char* delrec_strerror(int status);
 /* "delrec-mi355x <DELREC_ABI_VERSION> (gfx950)": a binding checks it before use (the
  * argument structs change between versions). */
-#define DELREC_ABI_VERSION "0.4.0"
+#define DELREC_ABI_VERSION "0.5.0"
 const char* delrec_version(void);
 
 #ifdef __cplusplus

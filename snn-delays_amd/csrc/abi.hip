@@ -1214,33 +1214,31 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         HybTaps tp{};
         tp.N = N; tp.KF = KF; tp.omin = a->off_min; tp.s = a->s_uniform; tp.base = a->base; tp.lof = lof; tp.h = h;
         launch_hyb_taps(tp, s);
-        // the split needs the first lags on the host: one read-back per call
-        std::vector<int> lof_h(N), perm_h(N), colf_h(N);
-        if (hipMemcpyAsync(lof_h.data(), lof, (size_t)N * sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
-            hipStreamSynchronize(s) != hipSuccess)
-            return DELREC_ERR_LAUNCH;
-        // the longest block (at most kHybBlockMax steps) whose near sources the chain takes;
-        // P = 1 has none (every lof >= 1)
+        // the split by first lag: the near counts (lof < 4, lof < 2) come from the caller, who
+        // computed them with the forward's own host read; without them the first lags are
+        // read back here (one stream sync). The split itself runs on the device.
+        int n4 = a->near_lt4, n2 = a->near_lt2;
+        if (!a->near_known || n2 < 0 || n2 > n4 || n4 > N) {
+            std::vector<int> lof_h(N);
+            if (hipMemcpyAsync(lof_h.data(), lof, (size_t)N * sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess)
+                return DELREC_ERR_LAUNCH;
+            n4 = n2 = 0;
+            for (int j = 0; j < N; ++j) {
+                n4 += lof_h[j] < 4 ? 1 : 0;
+                n2 += lof_h[j] < 2 ? 1 : 0;
+            }
+        }
+        // the longest block (at most kHybBlockMax = 4 steps) whose near sources the chain
+        // takes; P = 1 has none (every lof >= 1)
+        static_assert(kHybBlockMax == 4, "near counts for blocks of 4 and 2 steps");
         int P = kHybBlockMax, Nn = 0;
         for (;; P /= 2) {
-            Nn = 0;
-            for (int j = 0; j < N; ++j) Nn += lof_h[j] < P ? 1 : 0;
+            Nn = P == 4 ? n4 : P == 2 ? n2 : 0;
             if (P == 1 || (Nn <= kHybNearMax && hyb_bwd_near_lds(P, hq.D, Nn) <= (size_t)max_lds_bytes())) break;
         }
         const int Nf = N - Nn;
-        for (int j = 0, cn = 0, cf = Nn; j < N; ++j) {
-            if (lof_h[j] < P) {
-                perm_h[cn++] = j;
-                colf_h[j] = -1;
-            } else {
-                colf_h[j] = cf - Nn;
-                perm_h[cf++] = j;
-            }
-        }
-        if (hipMemcpyAsync(perm, perm_h.data(), (size_t)N * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
-            hipMemcpyAsync(colf, colf_h.data(), (size_t)N * sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
-            hipStreamSynchronize(s) != hipSuccess)
-            return DELREC_ERR_LAUNCH;
+        launch_hyb_split(lof, N, P, Nn, perm, colf, h, KF, s);
         // The far product on the 4:2 sparse MFMA where it can (bf16 W, blocks of 4 steps, 3 .. 6
         // offsets; DELREC_FAR_SPARSE=0 keeps the dense one), the near one with
         // DELREC_NEAR_SPARSE=1 (at C5's 95 near columns its one 256-column tile at 8 k-splits

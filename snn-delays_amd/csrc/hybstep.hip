@@ -903,6 +903,69 @@ bool launch_hyb_bwd_near(const HybBwd& a, hipStream_t stream) {
     return true;
 }
 
+// The backward's split of the sources by first lag, on the device: perm = the near sources
+// (lof < P) in index order, then the far ones; colf[j] = j's far column (-1 for near ones).
+// One workgroup of 1024 threads walks the sources in chunks twice (the near count, then the
+// positions), so every store lands in [0, N) whatever the counts. The host chose the kernels'
+// shapes from its own near count Nn: where the two disagree (the first lags changed between
+// that count and this launch) the taps are overwritten with NaN, so that every output the
+// backward writes is NaN rather than silently wrong.
+__global__ void __launch_bounds__(1024) hyb_split_kernel(const int* __restrict__ lof, int N, int P, int Nn,
+                                                         int* __restrict__ perm, int* __restrict__ colf,
+                                                         float* __restrict__ h, int KF) {
+    __shared__ int wsum[16];
+    __shared__ int total;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    auto block_scan = [&](bool flag, int& before, int& all) {   // exclusive rank, chunk total
+        const uint64_t bal = __ballot(flag);
+        const int rank = __popcll(bal & ((1ull << lane) - 1ull));
+        __syncthreads();
+        if (lane == 0) wsum[w] = __popcll(bal);
+        __syncthreads();
+        int pre = 0, sum = 0;
+        for (int q = 0; q < 16; ++q) {
+            pre += q < w ? wsum[q] : 0;
+            sum += wsum[q];
+        }
+        before = pre + rank;
+        all = sum;
+    };
+    int nn = 0;
+    for (int j0 = 0; j0 < N; j0 += 1024) {
+        const int j = j0 + tid;
+        int before, all;
+        block_scan(j < N && lof[j] < P, before, all);
+        nn += all;
+    }
+    int near = 0;
+    for (int j0 = 0; j0 < N; j0 += 1024) {
+        const int j = j0 + tid;
+        const bool flag = j < N && lof[j] < P;
+        int before, all;
+        block_scan(flag, before, all);
+        if (j < N) {
+            const int pn = near + before;           // near sources before j
+            if (flag) {
+                perm[pn] = j;
+                colf[j] = -1;
+            } else {
+                perm[nn + (j - pn)] = j;
+                colf[j] = j - pn;
+            }
+        }
+        near += all;
+    }
+    if (tid == 0) total = nn;
+    __syncthreads();
+    if (total != Nn)
+        for (size_t q = tid; q < (size_t)KF * N; q += 1024) h[q] = __builtin_nanf("");
+}
+
+void launch_hyb_split(const int* lof, int N, int P, int Nn, int* perm, int* colf, float* h, int KF,
+                      hipStream_t stream) {
+    hipLaunchKernelGGL(hyb_split_kernel, dim3(1), dim3(1024), 0, stream, lof, N, P, Nn, perm, colf, h, KF);
+}
+
 void launch_hyb_near_pack(const HybPack& a, uint32_t* wnp, hipStream_t stream) {
     const size_t n = (size_t)a.nc * a.nc;
     if (n == 0) return;

@@ -280,6 +280,10 @@ constexpr int kHybNearMax = 160; // near sources the per-block near chain takes 
 void launch_hyb_bwd_farblk(const HybBwd& a, hipStream_t stream);
 bool launch_hyb_bwd_near(const HybBwd& a, hipStream_t stream);
 void launch_hyb_near_pack(const HybPack& a, uint32_t* wnp, hipStream_t stream);
+// perm / colf of the split by first lag (near: lof < P) on the device; taps h -> NaN when the
+// device's near count differs from Nn
+void launch_hyb_split(const int* lof, int N, int P, int Nn, int* perm, int* colf, float* h, int KF,
+                      hipStream_t stream);
 size_t hyb_bwd_near_lds(int P, int D, int Nn);
 
 struct HybScat {                 // the hybrid forward as a scatter on arrival (bf16 W)

@@ -88,7 +88,8 @@ class SynBwdArgs(ctypes.Structure):
                 ('s_uniform', c_f32), ('s_max', c_f32), ('drop', c_vp), ('lif', Lif),
                 ('dx', c_vp), ('dW', c_vp), ('dd', c_vp), ('ds', c_vp), ('db', c_vp),
                 ('workspace', c_vp), ('workspace_bytes', c_size),
-                ('d_min', c_f32), ('off_min', c_i32), ('off_count', c_i32)]
+                ('d_min', c_f32), ('off_min', c_i32), ('off_count', c_i32),
+                ('near_known', c_i32), ('near_lt4', c_i32), ('near_lt2', c_i32)]
 
 
 class SpikeLinearArgs(ctypes.Structure):
@@ -118,7 +119,7 @@ class LifBwdArgs(ctypes.Structure):
 
 
 # the DELREC_ABI_VERSION of include/delrec.h these ctypes structs mirror
-ABI_VERSION = '0.4.0'
+ABI_VERSION = '0.5.0'
 
 _lib = None
 

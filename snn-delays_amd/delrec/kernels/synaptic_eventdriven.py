@@ -44,7 +44,8 @@ def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop,
     device tensor holding every effective delay (for the window length); ``off_range`` =
     (smallest offset, offset count) of the hybrid's int8 offsets. Returns
     ``(y, u, bits, L, Wc, w_bf16, s_max, hyb)`` with ``hyb`` the hybrid's scan-form fields
-    (``hybrid_form``) for the backward."""
+    (``hybrid_form``) and its first-lag counts (below 4, below 2; -1 when not hybrid) for the
+    backward."""
     require_device(x)
     T, B, N = x.shape
     dev = x.device
@@ -63,12 +64,20 @@ def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop,
         # smallest possible delay, base_j + (smallest offset): they apply when that is
         # >= s - 1 for every source, i.e. min_j base_j + off_min in fp32 (a bound of the
         # smallest delay that also covers a source without a connection at off_min)
-        (d_max, d_min), s_max = read_scalars(d_all.max(), base.min() + float(off_range[0])), s_uniform
+        # The same read carries the backward's split of the sources by first lag: how many
+        # start below lag 4 and below lag 2, by the entry point's own fp32 formula
+        # max(1, floor(1 + (base_j + off_min) - s) + 1), so that the backward needs no read
+        lof = (torch.floor((1.0 + (base + float(off_range[0]))) - float(s_uniform)) + 1.0).clamp(min=1.0)
+        (d_max, d_min, n4, n2) = read_scalars(d_all.max(), base.min() + float(off_range[0]),
+                                              (lof < 4).sum().float(), (lof < 2).sum().float())
+        s_max = s_uniform
+        near = (int(n4), int(n2))
     else:
         (d_max,), s_max = read_scalars(d_all.max()), s_uniform
         d_min = d_max
     L = max(window_length_f64(d_max, s_max), 2)
     hyb = hybrid_form(d_min, s_uniform, off_range if d_eff is None and s_vec is None else None)
+    hyb = tuple(hyb) + (near if off_range is not None and s_vec is None and d_eff is None else (-1, -1))
     # the scan form follows the taps per connection: the entry point's smax (the largest
     # per-column half-width, or the uniform one)
     smax = float(s_max) if s_vec is not None else max(float(s_max), float(s_uniform))
@@ -85,8 +94,9 @@ def syn_forward(x, W, d_eff, base, offsets, s_vec, s_uniform, d_all, bias, drop,
 
 
 def syn_backward(gy, u, y, bits, Wc, w_bf16, d_eff, base, offsets, s_vec, s_uniform, s_max, drop, lif,
-                 L, need_W, need_d, need_s, need_b, hyb=(0.0, 0, 0, 0)):
-    """Launch ``delrec_syn_bwd`` (``hyb``: the forward's hybrid scan-form fields). Returns
+                 L, need_W, need_d, need_s, need_b, hyb=(0.0, 0, 0, 0, -1, -1)):
+    """Launch ``delrec_syn_bwd`` (``hyb``: the forward's hybrid scan-form fields and first-lag
+    counts). Returns
     ``(dx, dW, dd, ds, db)`` (``None`` where not requested)."""
     T, B, N = u.shape
     dev = u.device
@@ -105,7 +115,9 @@ def syn_backward(gy, u, y, bits, Wc, w_bf16, d_eff, base, offsets, s_vec, s_unif
         W=_lib.ptr(Wc), w_bf16=w_bf16, d=_lib.ptr(d_eff), base=_lib.ptr(base),
         offsets=_lib.ptr(offsets), s=_lib.ptr(s_vec), s_uniform=float(s_uniform), s_max=float(s_max),
         drop=_lib.ptr(drop), lif=lif, dx=_lib.ptr(dx), dW=_lib.ptr(dW), dd=_lib.ptr(dd), ds=_lib.ptr(ds), db=_lib.ptr(db),
-        workspace=_lib.ptr(ws), workspace_bytes=ws.numel(), d_min=hyb[0], off_min=hyb[1], off_count=hyb[2])
+        workspace=_lib.ptr(ws), workspace_bytes=ws.numel(), d_min=hyb[0], off_min=hyb[1], off_count=hyb[2],
+        near_known=int(len(hyb) > 5 and hyb[4] >= 0), near_lt4=max(hyb[4], 0) if len(hyb) > 5 else 0,
+        near_lt2=max(hyb[5], 0) if len(hyb) > 5 else 0)
     _lib.call('delrec_syn_bwd', args, _lib.stream_of(gy))
     return dx, dW, dd, ds, db
 
