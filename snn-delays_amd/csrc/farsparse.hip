@@ -153,8 +153,9 @@ __global__ void __launch_bounds__(256) far_sparse_kernel(FarSparse p) {
     const i32x4 rwv = buffer_rsrc(p.wv, (uint32_t)(nfrag * 16)), rwi = buffer_rsrc(p.wi, (uint32_t)(nfrag * 4));
     // staging: thread tid stages plane tid / 128 (wave-uniform), batch row b = (tid / 4) % 32
     // and 16-byte quarter r = tid % 4 (pairs 4r .. 4r + 3) of the chunk's 64 bytes; load h
-    // takes slice (h + b) mod S, so that the four lanes of a row still read 64 contiguous bytes
-    // while the rows of one LDS store land in distinct banks
+    // takes slice (h + 2b) mod S, so that the four lanes of a row still read 64 contiguous
+    // bytes while the rows of one LDS store spread over the banks (at most two lanes of a
+    // half wave per bank; the rotation by b alone left up to four)
     const bool hpl = __builtin_amdgcn_readfirstlane(w) >= 2;
     const i32x4 rh = hpl ? rh1 : rh0;
     const int sb = (tid >> 2) & 31, sq = tid & 3;
@@ -163,7 +164,7 @@ __global__ void __launch_bounds__(256) far_sparse_kernel(FarSparse p) {
     const uint32_t hstep = (uint32_t)p.Nk * 2;
     const int hl = (hpl ? PL : 0) + sb * BS + 4 * sq * PS;   // word of (pair 4 sq, slice 0)
     uint4 sreg[NS];
-    const int sr = sb % S;
+    const int sr = (2 * sb) % S;
     auto slice_of = [&](int h) { return h + sr < S ? h + sr : h + sr - S; };
     auto issue_stage = [&](int c) {
 #pragma unroll
