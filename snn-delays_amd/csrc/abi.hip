@@ -1281,6 +1281,16 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         if (!sparse && nsize + (size_t)planes * fplane > proom) return DELREC_ERR_WORKSPACE;
         FarSparse fn = fs;   // the near product: 256 columns, its own splits and partials
         fn.Np = 256; fn.KS = ksn; fn.wv = Pn; fn.wi = reinterpret_cast<const uint32_t*>(Pn + nwv); fn.part = npart;
+        // otherwise, for one W plane, blocks of 4 steps and D + 3 <= 8 slices, the dense near
+        // product with the history staged once per slice (DELREC_NEAR_BLOCK=0 keeps the plain
+        // strided GEMM)
+        NearBlock nb{};
+        nb.a0 = ghi; nb.a1 = glo; nb.lda = hq.lda; nb.B = B; nb.rows = B * P; nb.Nk = hq.Nk; nb.Np = Nnp;
+        nb.w = Pn; nb.part = npart;
+        nb.KS = near_block_splits(B * P, Nnp, hq.Nk, num_cus());
+        const bool nblock = Nn > 0 && !nsparse && planes == 1 && P == 4 && near_block_ok(hq.D) &&
+                            getenv_flag_off("DELREC_NEAR_BLOCK") && (size_t)nb.KS * B * P * Nnp <= hz.npart &&
+                            near_block_lds(hq.D) <= (size_t)max_lds_bytes();
         if (Nf > 0) {
             pk.Np = Nfp; pk.c0 = Nn; pk.nc = Nf; pk.out = Pf;
             if (sparse)
@@ -1308,13 +1318,13 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         gf.part = fpart; gf.cm = 0;
         LagStepGemm gn = gf;   // block t0: near G(t0 - P + 2 + tt), the block's steps' t + 1
         gn.p0 = Pn; gn.p1 = planes > 1 ? Pn + nplane : nullptr; gn.Np = Nnp;
-        gn.KS = Nn == 0 ? 1 : nsparse ? ksn : lagstep_splits(B * P, Nnp, hq.Kt, num_cus());
+        gn.KS = Nn == 0 ? 1 : nsparse ? ksn : nblock ? nb.KS : lagstep_splits(B * P, Nnp, hq.Kt, num_cus());
         gn.part = npart;
         if (getenv("DELREC_LOG_PLAN"))
             fprintf(stderr, "[delrec] hybrid offset-stacked backward: T=%d B=%d N=%d D=%d P=%d; near sources %d "
                     "(product KS=%d%s, %d row tiles, chain of %d-row workgroups); far sources %d (product KS=%d, "
                     "%s tiles, %d row tiles); far LIF grid %d x %d\n", T, B, N, hq.D, P, Nn, Nn > 0 ? gn.KS : 0,
-                    nsparse ? " sparse" : "", (B * P + 127) / 128, 2, Nf, Nf > 0 ? gf.KS : 0,
+                    nsparse ? " sparse" : nblock ? " block" : "", (B * P + 127) / 128, 2, Nf, Nf > 0 ? gf.KS : 0,
                     sparse ? "sparse 128x256" : far256 ? "256x256" : "128x256",
                     (B * P + (far256 && !sparse ? 255 : 127)) / (far256 && !sparse ? 256 : 128), (hq.Nk + 63) / 64,
                     (B + 15) / 16);
@@ -1345,8 +1355,11 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
             if (Nn > 0) {
                 gn.aoff = (size_t)(hq.PF + t0 - P + 2) * hq.Nk;
                 fn.aoff = gn.aoff;
+                nb.aoff = gn.aoff;
                 if (nsparse)
                     launch_far_sparse(fn, fq, s);
+                else if (nblock)
+                    launch_near_block(nb, hq.D, s);
                 else
                     launch_lagstep_gemm(gn, 2, s, planes);
                 ok = launch_hyb_bwd_near(l, s);

@@ -301,6 +301,159 @@ __global__ void __launch_bounds__(256) far_sparse_kernel(FarSparse p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// The near product of a block, dense: G_j(tau) of the near sources (columns j, dense bf16
+// W^(e) planes, k-blocked [(e Nk + i) / 8][Np]) for the block's rows (b, tt), tau = the block's
+// first row step + tt, from the history slices tau + e. The product reads every history slice
+// of a batch row once per 32-receiver chunk -- 32 batch rows x (D + 3) slices x 64 bytes x 2
+// planes, staged through LDS -- and builds the rows (b, tt) of all D offsets from it, where
+// a plain strided GEMM re-reads the window once per (step, offset): 4 (D) / (D + 3) of its
+// history traffic. Workgroup: 4 waves, 128 rows (32 batch rows x 4 steps) x 128 columns, a
+// wave 64 x 64 (4 x 4 blocks of v_mfma_f32_16x16x32_bf16, both gr planes); W and history
+// double-buffered in LDS from one register stage of loads. LDS: batch row pitch 132 words
+// and slice pitch 16 make the 16 lanes of a row block's 16-byte reads hit 16 distinct bank
+// groups; the history rows are loaded at slices rotated by the batch row (stores at most
+// two-way conflicted). k split over KS workgroups; partials row-major [KS][rows][Np].
+constexpr int kNearBlockRows = 32;      // batch rows per tile (x 4 steps)
+constexpr int kNearBlockSlices = 8;     // staged slices per batch row (D + 3 <= 8)
+constexpr int kNearBlockBP = 33;        // uint4 per staged batch row (8 slices x 4 + 1)
+
+template <int D>
+__global__ void __launch_bounds__(256) near_block_kernel(NearBlock p) {
+    constexpr int S = D + 3, SL = kNearBlockSlices, BP = kNearBlockBP, RB = kNearBlockRows;
+    static_assert(S <= SL, "slices per batch row");
+    constexpr int HPL = RB * BP;                  // uint4 per history plane
+    constexpr int HB = 2 * HPL;                   // W after the two history planes
+    constexpr int BUF = HB + D * 4 * 128;         // uint4 per buffer
+    constexpr int NH = (2 * RB * S * 4 + 255) / 256;   // history uint4 staged per thread
+    constexpr int NW = D * 4 * 128 / 256;              // W uint4 staged per thread
+    static_assert(D * 4 * 128 % 256 == 0, "W staging");
+    extern __shared__ uint4 nlds[];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int wi = w >> 1, wj = w & 1, lg = lane >> 4, lc = lane & 15;
+    const int NCT = (p.rows + 4 * RB - 1) / (4 * RB), NJT = p.Np / 128;
+    const int id = (int)blockIdx.x;
+    int ct, jt, ks;
+    if (p.KS % 8 == 0) {
+        // XCD x (= id mod 8) serves KS / 8 of the splits over every tile: their W slabs stay in
+        // its L2 while the row tiles stream past
+        const int x = id & 7, slot = id >> 3, kx = p.KS / 8;
+        ks = x * kx + slot % kx;
+        const int t = slot / kx;
+        jt = t % NJT;
+        ct = t / NJT;
+    } else {
+        ks = id % p.KS;
+        const int t = id / p.KS;
+        jt = t % NJT;
+        ct = t / NJT;
+    }
+    const int b0 = ct * RB, n0 = jt * 128;
+    const int nch = p.Nk / 32;
+    const int per = (nch + p.KS - 1) / p.KS;
+    const int c0 = ks * per, c1 = min(nch, c0 + per);
+
+    const uint32_t hbytes = (uint32_t)((size_t)p.B * p.lda * 2);
+    const i32x4 rh0 = buffer_rsrc(p.a0, hbytes), rh1 = buffer_rsrc(p.a1, hbytes);
+    const i32x4 rw = buffer_rsrc(p.w, (uint32_t)((size_t)(D * p.Nk / 8) * p.Np * 16));
+    // history staging: uint4 u = tid + 256 h: plane u / (RB S 4), batch row, slice (rotated
+    // by the batch row), 16-byte quarter; W staging: uint4 u = tid + 256 h: (offset e,
+    // k-block kb) = u / 128, column u % 128
+    uint32_t ho[NH];
+    int hl[NH];
+    bool hp[NH], hv[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        const int u = tid + 256 * h;
+        hv[h] = u < 2 * RB * S * 4;
+        const int uu = hv[h] ? u : 0;
+        const int pl = uu / (RB * S * 4), r = uu % (RB * S * 4);
+        const int b = r / (S * 4), q = (r / 4) % S, qd = r % 4;
+        const int sl = (q + b) % S;
+        ho[h] = (uint32_t)(((size_t)(b0 + b) * p.lda + p.aoff + (size_t)sl * p.Nk + qd * 8) * 2);
+        hl[h] = pl * HPL + b * BP + sl * 4 + qd;
+        hp[h] = pl != 0;
+    }
+    uint32_t wo[NW];
+#pragma unroll
+    for (int h = 0; h < NW; ++h) {
+        const int u = tid + 256 * h, ekb = u / 128, col = u % 128, e = ekb / 4, kb = ekb % 4;
+        wo[h] = (uint32_t)((((size_t)e * p.Nk / 8 + kb) * p.Np + n0 + col) * 16);
+    }
+    uint4 sh[NH], sw[NW];
+    auto issue = [&](int c) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+            sh[h] = hv[h] ? __builtin_bit_cast(uint4, raw_buffer_load_i32x4(hp[h] ? rh1 : rh0, (int)(ho[h] + (uint32_t)c * 64), 0, 0))
+                          : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int h = 0; h < NW; ++h)
+            sw[h] = __builtin_bit_cast(uint4, raw_buffer_load_i32x4(rw, (int)(wo[h] + (uint32_t)c * 4 * p.Np * 16), 0, 0));
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+            if (hv[h]) nlds[buf * BUF + hl[h]] = sh[h];
+#pragma unroll
+        for (int h = 0; h < NW; ++h) nlds[buf * BUF + HB + tid + 256 * h] = sw[h];
+    };
+    fs_floatx4 acc[4][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = fs_floatx4{0.f, 0.f, 0.f, 0.f};
+    // A fragment of row block mb: row r = wi 64 + mb 16 + lc = batch row r / 4, step r % 4,
+    // receivers 8 lg .. + 7 of the chunk at slice (r % 4) + e
+    int ar[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+        const int r = wi * 64 + mb * 16 + lc;
+        ar[mb] = (r >> 2) * BP + (r & 3) * 4 + lg;
+    }
+    const int bc = wj * 64 + lc;
+    if (c0 < c1) {
+        issue(c0);
+        stash(0);
+        barrier_lds();
+        if (c0 + 1 < c1) issue(c0 + 1);
+    }
+    for (int c = c0; c < c1; ++c) {
+        const uint4* L = nlds + ((c - c0) & 1) * BUF;
+#pragma unroll
+        for (int e = 0; e < D; ++e) {
+            fs_bf16x8 bf[4];
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) bf[nb] = __builtin_bit_cast(fs_bf16x8, L[HB + (e * 4 + lg) * 128 + bc + nb * 16]);
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl) {
+                fs_bf16x8 af[4];
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb) af[mb] = __builtin_bit_cast(fs_bf16x8, L[pl * HPL + ar[mb] + e * 4]);
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mb], bf[nb], acc[mb][nb], 0, 0, 0);
+            }
+        }
+        if (c + 1 < c1) {
+            stash(((c - c0) & 1) ^ 1);
+            barrier_lds();
+            if (c + 2 < c1) issue(c + 2);
+        }
+    }
+    float* out = p.part + (size_t)ks * p.rows * p.Np;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const int r = b0 * 4 + wi * 64 + mb * 16 + 4 * lg + e4;
+            if (r >= p.rows) continue;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) out[(size_t)r * p.Np + n0 + wj * 64 + nb * 16 + lc] = acc[mb][nb][e4];
+        }
+}
+
+// ---------------------------------------------------------------------------------------
 
 int far_sparse_q(int D) { return D >= 3 && D <= 6 ? (D + 1) / 2 : 0; }
 
@@ -316,6 +469,34 @@ int far_sparse_splits(int rows, int Np, int Nk, int cus) {
     const int nch = Nk / 32;
     if (tiles < 1) return 1;
     return std::max(1, std::min((cus + tiles - 1) / tiles, std::max(1, nch / 8)));
+}
+
+bool near_block_ok(int D) { return D >= 1 && D + 3 <= kNearBlockSlices; }
+
+size_t near_block_lds(int D) {
+    return (size_t)2 * (2 * kNearBlockRows * kNearBlockBP + D * 4 * 128) * sizeof(uint4);
+}
+
+int near_block_splits(int rows, int Np, int Nk, int cus) {
+    const int tiles = ((rows + 4 * kNearBlockRows - 1) / (4 * kNearBlockRows)) * (Np / 128);
+    const int nch = Nk / 32;
+    if (tiles < 1) return 1;
+    return std::max(1, std::min((cus + tiles - 1) / tiles, std::max(1, nch / 4)));
+}
+
+bool launch_near_block(const NearBlock& g, int D, hipStream_t stream) {
+    const int tiles = ((g.rows + 4 * kNearBlockRows - 1) / (4 * kNearBlockRows)) * (g.Np / 128);
+    const dim3 grid((unsigned)(tiles * g.KS));
+    const size_t lds = near_block_lds(D);
+#define DELREC_NEAR_BLOCK(DV)                                                                   \
+    if (D == DV) {                                                                              \
+        ensure_lds((const void*)near_block_kernel<DV>, lds);                                    \
+        hipLaunchKernelGGL(near_block_kernel<DV>, grid, dim3(256), lds, stream, g);             \
+        return true;                                                                            \
+    }
+    DELREC_NEAR_BLOCK(1) DELREC_NEAR_BLOCK(2) DELREC_NEAR_BLOCK(3) DELREC_NEAR_BLOCK(4) DELREC_NEAR_BLOCK(5)
+#undef DELREC_NEAR_BLOCK
+    return false;
 }
 
 void launch_far_sparse_pack(const HybPack& a, int Q, uint4* wv, uint32_t* wi, hipStream_t stream) {

@@ -983,8 +983,13 @@ HybBwdSizes hyb_bwd_sizes(const HybStepDims& q, int B, int cus, int fcol) {
     for (int P = 1; P <= kHybBlockMax; P *= 2) {
         for (int c = 128; c <= std::min(q.Np, kHybNearMax); c += 128)
             z.npart = std::max(z.npart, (size_t)lagstep_splits(B * P, c, q.Kt, cus) * B * P * c);
-        // (the near product on the sparse MFMA: one 256-column tile, blocks of 4 steps)
-        if (P == 4) z.npart = std::max(z.npart, (size_t)far_sparse_splits(B * P, 256, q.Nk, cus) * B * P * 256);
+        // (the near product on the sparse MFMA: one 256-column tile; the near-block product:
+        // 128-column tiles; both for blocks of 4 steps)
+        if (P == 4) {
+            z.npart = std::max(z.npart, (size_t)far_sparse_splits(B * P, 256, q.Nk, cus) * B * P * 256);
+            for (int c = 128; c <= std::min(q.Np, kHybNearMax); c += 128)
+                z.npart = std::max(z.npart, (size_t)near_block_splits(B * P, c, q.Nk, cus) * B * P * c);
+        }
         // (256-column far parts may run either far kernel: the larger split count sizes them)
         for (int c = fcol; c <= (q.Np + fcol - 1) / fcol * fcol; c += fcol) {
             int ks = lagstep_splits(B * P, c, q.Kt, cus, fcol);

@@ -183,6 +183,16 @@ struct FarSparse {               // the hybrid backward's far product on the 4:2
     float* part;                 // [KS][rows][Np]
 };
 
+struct NearBlock {               // the hybrid backward's near product of a block (dense, bf16 W)
+    const uint16_t* a0;          // gr history, hi / lo planes [b][slice][Nk]; the block's first
+    const uint16_t* a1;          //   row step's slice at element aoff of each batch row
+    size_t lda, aoff;
+    int B, rows;                 // batch rows, product rows B * 4 (row b * 4 + step of the block)
+    int Nk, Np, KS;              // receivers (multiple of 32), near columns (multiple of 128), k splits
+    const uint4* w;              // W^(e) planes, k-blocked [(e Nk + i) / 8][Np], e < D
+    float* part;                 // [KS][rows][Np]
+};
+
 struct LagStepLif {
     int T, B, N, Nk, Np, KS, t, Lw;
     size_t lda;
@@ -364,6 +374,12 @@ size_t far_sparse_wv(int Nk, int Np, int Q);            // uint4 of values (and 
 int far_sparse_splits(int rows, int Np, int Nk, int cus);
 void launch_far_sparse_pack(const HybPack& a, int Q, uint4* wv, uint32_t* wi, hipStream_t stream);
 bool launch_far_sparse(const FarSparse& g, int Q, hipStream_t stream);
+// near product of a block, dense with the history staged once per slice: D offsets with
+// D + 3 <= 8, blocks of 4 steps, one W plane
+bool near_block_ok(int D);
+size_t near_block_lds(int D);
+int near_block_splits(int rows, int Np, int Nk, int cus);
+bool launch_near_block(const NearBlock& g, int D, hipStream_t stream);
 int lagstep_splits(int B, int Np, int Kt, int cus, int nc = 128);   // nc: workgroup columns
 int lagstep_block();
 size_t lagstep_gemm_lds(int pa, int pb = 2, int wn = 64);

@@ -1,7 +1,7 @@
 """C5 (two stacked hybrid layers, N = 2048, bf16 W) at the benchmark's own batch of 512 rows,
 so that every kernel runs the tiling the benchmark times: the far product's 16 row tiles of
 128 (on the sparse MFMA, its XCD-grouped form) at its 2 k-splits, the far LIF's 32 tiles of 16
-rows, the near product's 4 tiles of 128, the near chain's 256 workgroups of 2 rows, the lag
+rows, the near product's 16 row tiles of 128 at 16 k-splits, the near chain's 256 workgroups of 2 rows, the lag
 correlation's 16 chunks of 32 rows (a batch of 32 runs one far row tile instead).
 
 Batch rows are independent through the whole recurrence, and a row whose upstream
@@ -83,6 +83,7 @@ def test_c5_at_benchmark_tiling_both_layers(dev, monkeypatch, capfd):
         plan = capfd.readouterr().err
         print(plan, flush=True)
         assert 'far sources' in plan and 'product KS=2, sparse 128x256 tiles, 16 row tiles' in plan, plan
+        assert 'near sources' in plan and '(product KS=16 block, 16 row tiles' in plan, plan
         y_prev = y
         y_rows = y[:, rows].cpu()
         print(f'  firing rate {float(y.mean()):.4f} (rows: {float(y_rows.mean()):.4f})', flush=True)

@@ -6,8 +6,9 @@ for the near ones with DELREC_NEAR_SPARSE=1 (set in every test here).
 Against the float64 oracle (``test_gpu_synaptic.test_hybrid_fwd_bwd_matches_oracle``, offset-stacked scans
 forced): each offset count of the form, one and two 256-column tiles, row tiles past the
 batch's last row, a triangle of three taps, T not a multiple of the block. On a batch of 128
-rows, where the tiles take the XCD-grouped order, against both dense products (``DELREC_FAR_SPARSE=0``,
-``DELREC_NEAR_SPARSE=0``): the same gradients up to the order of fp32 sums (both products are exact
+rows, where the tiles take the XCD-grouped order, against the dense far product with the
+near-block product (``DELREC_FAR_SPARSE=0``) and against both products as plain strided GEMMs
+(``DELREC_NEAR_BLOCK=0`` too): the same gradients up to the order of fp32 sums (both products are exact
 in their bf16 operands), and bit-identical results from two runs of the sparse form.
 """
 
@@ -73,19 +74,24 @@ def test_far_sparse_matches_dense_product(dev, monkeypatch, capfd):
     assert 'sparse 128x256 tiles, 4 row tiles' in plan, plan
     monkeypatch.setenv('DELREC_FAR_SPARSE', '0')
     monkeypatch.delenv('DELREC_NEAR_SPARSE')
-    dense = _grads(layer, x, gy)
+    block = _grads(layer, x, gy)          # dense far product, near-block product
     plan = capfd.readouterr().err
-    assert 'far sources' in plan and 'sparse' not in plan, plan
-    for name, a, b, c in zip(('y', 'dx', 'dW', 'dbase'), sparse, again, dense):
+    assert 'far sources' in plan and 'sparse' not in plan and ' block, ' in plan, plan
+    monkeypatch.setenv('DELREC_NEAR_BLOCK', '0')
+    dense = _grads(layer, x, gy)          # both products as plain strided GEMMs
+    plan = capfd.readouterr().err
+    assert 'far sources' in plan and 'sparse' not in plan and ' block, ' not in plan, plan
+    for name, a, b, c, d in zip(('y', 'dx', 'dW', 'dbase'), sparse, again, block, dense):
         assert torch.equal(a, b), f'{name} differs between two runs of the sparse product'
-        err = float((a - c).abs().max())
-        ref = float(c.abs().max())
-        print(f'  {name}: max |sparse - dense| {err:.3e} (|dense| max {ref:.3e})', flush=True)
-        if name == 'y':
-            assert torch.equal(a, c), 'the forward differs'
-        elif name == 'dW':
-            # returned in bf16 (W's dtype): fp32 sums a few ulps apart may round to adjacent bf16
-            # values, one bf16 ulp (2^-7 relative at most) apart
-            torch.testing.assert_close(a, c, rtol=2.0 ** -7, atol=1e-5 * ref)
-        else:
-            torch.testing.assert_close(a, c, rtol=1e-4, atol=1e-5 * ref)
+        ref = float(d.abs().max())
+        for other, label in ((a, 'sparse'), (c, 'near-block')):
+            err = float((other - d).abs().max())
+            print(f'  {name}: max |{label} - dense| {err:.3e} (|dense| max {ref:.3e})', flush=True)
+            if name == 'y':
+                assert torch.equal(other, d), 'the forward differs'
+            elif name == 'dW':
+                # returned in bf16 (W's dtype): fp32 sums a few ulps apart may round to adjacent
+                # bf16 values, one bf16 ulp (2^-7 relative at most) apart
+                torch.testing.assert_close(other, d, rtol=2.0 ** -7, atol=1e-5 * ref)
+            else:
+                torch.testing.assert_close(other, d, rtol=1e-4, atol=1e-5 * ref)
