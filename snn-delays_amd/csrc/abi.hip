@@ -676,7 +676,9 @@ int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_
             c.take<uint4>(spike_linear_ws(N, L) / sizeof(uint4));
             break;
         case DELREC_WS_SPIKE_LINEAR_DW:
-            c.take<float>(spike_linear_dw_ws(T, B, N, L, num_cus()) / sizeof(float));
+            c.take<uint4>(spike_linear_dw_planes(T, B, L));
+            c.take<float>((spike_linear_dw_ws(T, B, N, L, num_cus()) -
+                           spike_linear_dw_planes(T, B, L) * sizeof(uint4)) / sizeof(float));
             break;
         case DELREC_WS_READOUT_CE:
             c.take<float>((size_t)B);
@@ -1080,8 +1082,10 @@ int delrec_spike_linear_dw(const delrec_spike_linear_dw_args* a, void* stream) {
     p.T = a->T; p.B = a->B; p.K = a->K; p.M = a->M;
     p.bits = a->bits; p.g = a->g; p.dW = a->dW;
     spike_linear_dw_dims(p, num_cus());
+    Carver cv(a->workspace, a->workspace_bytes);
+    p.gp = cv.take<uint4>(spike_linear_dw_planes(p.T, p.B, p.M));
+    if (!p.gp) return DELREC_ERR_WORKSPACE;
     if (p.KS > 1) {
-        Carver cv(a->workspace, a->workspace_bytes);
         p.part = cv.take<float>((size_t)p.KS * p.M * p.K);
         if (!p.part) return DELREC_ERR_WORKSPACE;
     }

@@ -330,6 +330,7 @@ struct SpikeLinearDw {           // dW[m][k] = sum_{t,b} g[t][b][m] y[t][b][k]
     const float* g;              // (T, B, M)
     float* dW;                   // (M, K)
     float* part;                 // [KS][M][K] when KS > 1
+    uint4* gp;                   // g's bf16 planes [3][B][ceil(T/32)][4][M] (8 steps per uint4)
 };
 struct ReadoutCe {               // time reduction (+ leaky integrator) + cross-entropy, fused
     int T, B, C;
@@ -345,6 +346,7 @@ struct ReadoutCe {               // time reduction (+ leaky integrator) + cross-
 };
 void launch_readout_ce(const ReadoutCe& p, hipStream_t stream);
 void spike_linear_dw_dims(SpikeLinearDw& p, int cus);
+size_t spike_linear_dw_planes(int T, int B, int M);   // uint4 of g's planes in the workspace
 size_t spike_linear_dw_ws(int T, int B, int K, int M, int cus);
 void launch_spike_linear_dw(const SpikeLinearDw& p, hipStream_t stream);
 

@@ -187,89 +187,111 @@ __global__ void __launch_bounds__(256) spike_linear_kernel(SpikeLinear p, const 
         }
 }
 
+// g (T, B, M) fp32 into bf16 hi + mid + lo planes [plane][b][32-step word][8-step block][m]
+// (8 steps of one output per uint4; steps past T are 0), once per call, so the K / 128 input
+// tiles of the weight gradient stage the planes as they are instead of each splitting g
+// again. One thread per (b, word, block, m).
+__global__ void __launch_bounds__(256) spike_linear_gsplit_kernel(SpikeLinearDw p) {
+    const int TW = (p.T + 31) >> 5;
+    const size_t total = (size_t)p.B * TW * 4 * p.M;
+    const size_t gstep = (size_t)p.B * p.M;
+    for (size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x; id < total; id += (size_t)gridDim.x * blockDim.x) {
+        const int m = (int)(id % p.M);
+        const size_t r = id / p.M;
+        const int h = (int)(r & 3), wd = (int)((r >> 2) % TW), b = (int)(r / (4 * (size_t)TW));
+        const int t0 = wd * 32 + 8 * h;
+        uint32_t pl[kSpikeLinearPlanes][4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            uint32_t v2[kSpikeLinearPlanes][2];
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+                const int t = t0 + e + f;
+                float v = t < p.T ? p.g[(size_t)t * gstep + (size_t)b * p.M + m] : 0.0f;
+#pragma unroll
+                for (int q = 0; q < kSpikeLinearPlanes; ++q) {
+                    v2[q][f] = sl_bf16_rne(v);
+                    v -= __uint_as_float(v2[q][f] << 16);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < kSpikeLinearPlanes; ++q) pl[q][e / 2] = v2[q][0] | (v2[q][1] << 16);
+        }
+        const size_t plane = (size_t)p.B * TW * 4 * p.M;
+#pragma unroll
+        for (int q = 0; q < kSpikeLinearPlanes; ++q) p.gp[q * plane + id] = make_uint4(pl[q][0], pl[q][1], pl[q][2], pl[q][3]);
+    }
+}
+
 // The weight gradient of that Linear, dW[m][k] = sum_{t,b} g[t][b][m] * y[t][b][k], as the
 // same binary-activation GEMM with the spikes on the other side: D = g^T (M x TB) . Y (TB x K).
 // The contraction runs over stages of 32 steps of one batch row -- exactly one spike word per
 // neuron -- so each lane expands its B fragment (8 steps of one neuron) from one word; g^T is
-// split into bf16 hi + mid + lo planes (about 2^-25 relative, fp32 accumulation) as it is staged.
-// Tile: 128 outputs m x 128 inputs k per workgroup, 4 waves of 64 x 64; stages of a split in
-// (batch row, word) order; loads of stage s + 1 in flight while stage s multiplies. With at
-// least one tile per CU there is no split: each workgroup writes its dW tile directly, and
-// the 16 input tiles of one output tile sit on one XCD (they stream the same g columns).
+// split into bf16 hi + mid + lo planes (about 2^-25 relative, fp32 accumulation) before it.
+// Tile: 128 outputs m x 256 inputs k per workgroup, 4 waves of 64 x 128; stages of a split in
+// (batch row, word) order; loads of stage s + 1 in flight while stage s multiplies. The
+// stages are split so that about two workgroups run per CU (one stage in flight each hides
+// too little load latency: 23 ms at C5's 2048 x 2048 x 524288 with one, 12.5 ms with two);
+// the input tiles of one output tile and split sit on one XCD, where they stream the same g
+// columns from its L2. A 128 x 128 tile at two per CU takes 15 ms there.
 __global__ void __launch_bounds__(256) spike_linear_dw_kernel(SpikeLinearDw p) {
     constexpr int PL = kSpikeLinearPlanes;
     __shared__ uint4 sa[2][PL][4 * 128];     // [buffer][plane][r-block * 128 + m]: 8 steps of g^T
-    __shared__ uint32_t sb[2][128];          // [buffer][k]: the stage's spike words
+    __shared__ uint32_t sb[2][256];          // [buffer][k]: the stage's spike words
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int wi = w >> 1, wj = w & 1, g = lane >> 4, lc = lane & 15;
-    const int MT = p.Mp / 128, KT = p.Kp / 128, TW = (p.T + 31) >> 5;
+    const int MT = p.Mp / 128, KT = p.Kp / 256, TW = (p.T + 31) >> 5;
     const int id = (int)blockIdx.x;
     int mt, kt, ks;
-    if (p.KS == 1 && MT % 8 == 0) {
-        const int xcd = id & 7, slot = id >> 3;        // the input tiles of an output tile on one XCD
-        kt = slot % KT;
-        mt = xcd + 8 * (slot / KT);
-        ks = 0;
+    if (MT % 8 == 0) {
+        // the input tiles of an output tile (and of one split) on one XCD: they stream the
+        // same g columns, so all but the first read them from that XCD's L2
+        const int xcd = id & 7, slot = id >> 3, rest = slot / KT;
+        kt = slot - rest * KT;
+        mt = xcd + 8 * (rest % (MT / 8));
+        ks = rest / (MT / 8);
     } else {
         ks = id % p.KS;
         const int tile = id / p.KS;
         mt = tile / KT;
         kt = tile - mt * KT;
     }
-    const int m0 = mt * 128, k0 = kt * 128;
+    const int m0 = mt * 128, k0 = kt * 256;
     const int nst = p.B * TW;
     const int per = (nst + p.KS - 1) / p.KS;
     const int s0 = ks * per, s1 = min(nst, s0 + per);
-    // staging: g^T -- thread (m = m0 + (tid & 127), steps 16 (tid >> 7) .. + 15 of the word);
-    // spikes -- thread tid < 128 loads the word of input k0 + tid
-    const int sm = tid & 127, sr = (tid >> 7) * 16;
-    const bool mok = m0 + sm < p.M;
-    const size_t gstep = (size_t)p.B * p.M;            // floats between consecutive steps
-    float rg[16];
+    // staging: g^T from its three bf16 planes (split once by spike_linear_gsplit_kernel) --
+    // uint4 u = tid + 256 x: plane u / 512, 8-step block (u / 128) % 4, output m = m0 + u % 128;
+    // spikes -- thread tid loads the word of input k0 + tid
+    uint4 rg[6];
     uint32_t rb = 0;
     auto issue = [&](int s) {
         const int b = s / TW, wd = s - b * TW;
-        const int tbase = wd * 32 + sr;
-        const float* src = p.g + ((size_t)tbase * p.B + b) * p.M + m0 + sm;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) rg[e] = (s < s1 && mok && tbase + e < p.T) ? src[(size_t)e * gstep] : 0.0f;
-        rb = (s < s1 && tid < 128 && k0 + tid < p.K) ? p.bits[((size_t)b * TW + wd) * p.K + k0 + tid] : 0u;
+        for (int x = 0; x < 6; ++x) {
+            const int u = tid + 256 * x, q = u >> 9, h = (u >> 7) & 3, m = m0 + (u & 127);
+            rg[x] = (s < s1 && m < p.M) ? p.gp[((((size_t)q * p.B + b) * TW + wd) * 4 + h) * p.M + m] : make_uint4(0u, 0u, 0u, 0u);
+        }
+        rb = (s < s1 && k0 + tid < p.K) ? p.bits[((size_t)b * TW + wd) * p.K + k0 + tid] : 0u;
     };
     auto stash = [&](int buf) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {       // two 8-step blocks per thread
-            uint32_t pl[PL][4];
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                uint32_t v2[PL][2];
-#pragma unroll
-                for (int f = 0; f < 2; ++f) {
-                    float r = rg[8 * h + e + f];
-#pragma unroll
-                    for (int q = 0; q < PL; ++q) {
-                        v2[q][f] = sl_bf16_rne(r);
-                        r -= __uint_as_float(v2[q][f] << 16);
-                    }
-                }
-#pragma unroll
-                for (int q = 0; q < PL; ++q) pl[q][e / 2] = v2[q][0] | (v2[q][1] << 16);
-            }
-            const int rblk = (sr >> 3) + h;
-#pragma unroll
-            for (int q = 0; q < PL; ++q) sa[buf][q][rblk * 128 + sm] = uint4{pl[q][0], pl[q][1], pl[q][2], pl[q][3]};
+        for (int x = 0; x < 6; ++x) {
+            const int u = tid + 256 * x;
+            sa[buf][u >> 9][((u >> 7) & 3) * 128 + (u & 127)] = rg[x];
         }
-        if (tid < 128) sb[buf][tid] = rb;
+        sb[buf][tid] = rb;
     };
-    sl_floatx4 acc[4][4];
+    sl_floatx4 acc[4][8];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = sl_floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int nb = 0; nb < 8; ++nb) acc[mb][nb] = sl_floatx4{0.f, 0.f, 0.f, 0.f};
     auto compute = [&](int buf) {
-        sl_bf16x8 fb[4];
+        sl_bf16x8 fb[8];
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {      // input k = k0 + wj 64 + nb 16 + lc, steps 8 g .. 8 g + 7
-            const uint32_t wd = sb[buf][wj * 64 + nb * 16 + lc] >> (8 * g);
+        for (int nb = 0; nb < 8; ++nb) {      // input k = k0 + wj 128 + nb 16 + lc, steps 8 g .. 8 g + 7
+            const uint32_t wd = sb[buf][wj * 128 + nb * 16 + lc] >> (8 * g);
             uint32_t pk[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -282,7 +304,7 @@ __global__ void __launch_bounds__(256) spike_linear_dw_kernel(SpikeLinearDw p) {
             for (int mb = 0; mb < 4; ++mb) {
                 const sl_bf16x8 fa = __builtin_bit_cast(sl_bf16x8, sa[buf][q][g * 128 + wi * 64 + mb * 16 + lc]);
 #pragma unroll
-                for (int nb = 0; nb < 4; ++nb)
+                for (int nb = 0; nb < 8; ++nb)
                     acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb[nb], acc[mb][nb], 0, 0, 0);
             }
     };
@@ -296,7 +318,7 @@ __global__ void __launch_bounds__(256) spike_linear_dw_kernel(SpikeLinearDw p) {
         stash(buf ^ 1);
         barrier_lds();
     }
-    // rows m = m0 + wi 64 + mb 16 + 4 g + e, columns k = k0 + wj 64 + nb 16 + lc
+    // rows m = m0 + wi 64 + mb 16 + 4 g + e, columns k = k0 + wj 128 + nb 16 + lc
     float* out = p.KS == 1 ? p.dW : p.part + (size_t)ks * p.M * p.K;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
@@ -305,8 +327,8 @@ __global__ void __launch_bounds__(256) spike_linear_dw_kernel(SpikeLinearDw p) {
             const int m = m0 + wi * 64 + mb * 16 + 4 * g + e;
             if (m >= p.M) continue;
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb) {
-                const int k = k0 + wj * 64 + nb * 16 + lc;
+            for (int nb = 0; nb < 8; ++nb) {
+                const int k = k0 + wj * 128 + nb * 16 + lc;
                 if (k < p.K) out[(size_t)m * p.K + k] = acc[mb][nb][e];
             }
         }
@@ -324,21 +346,29 @@ __global__ void __launch_bounds__(256) spike_linear_dw_sum_kernel(SpikeLinearDw 
 
 void spike_linear_dw_dims(SpikeLinearDw& p, int cus) {
     p.Mp = (p.M + 127) / 128 * 128;
-    p.Kp = (p.K + 127) / 128 * 128;
-    const int tiles = (p.Mp / 128) * (p.Kp / 128);
+    p.Kp = (p.K + 255) / 256 * 256;
+    const int tiles = (p.Mp / 128) * (p.Kp / 256);
     const int nst = p.B * ((p.T + 31) >> 5);
-    p.KS = std::max(1, std::min((cus + tiles - 1) / tiles, std::max(1, nst / 16)));   // >= 16 stages a split
+    p.KS = std::max(1, std::min((2 * cus + tiles - 1) / tiles, std::max(1, nst / 16)));   // >= 16 stages a split
 }
 
 size_t spike_linear_dw_ws(int T, int B, int K, int M, int cus) {
     SpikeLinearDw p{};
     p.T = T; p.B = B; p.K = K; p.M = M;
     spike_linear_dw_dims(p, cus);
-    return p.KS > 1 ? (size_t)p.KS * M * K * sizeof(float) : 0;
+    const size_t planes = (size_t)kSpikeLinearPlanes * B * ((T + 31) / 32) * 4 * M * sizeof(uint4);
+    return planes + 256 + (p.KS > 1 ? (size_t)p.KS * M * K * sizeof(float) : 0);
+}
+
+size_t spike_linear_dw_planes(int T, int B, int M) {
+    return (size_t)kSpikeLinearPlanes * B * ((T + 31) / 32) * 4 * M;
 }
 
 void launch_spike_linear_dw(const SpikeLinearDw& p, hipStream_t stream) {
-    const unsigned grid = (unsigned)((p.Mp / 128) * (p.Kp / 128) * p.KS);
+    const size_t items = (size_t)p.B * ((p.T + 31) / 32) * 4 * p.M;
+    hipLaunchKernelGGL(spike_linear_gsplit_kernel, dim3((unsigned)std::min<size_t>((items + 255) / 256, 65536)),
+                       dim3(256), 0, stream, p);
+    const unsigned grid = (unsigned)((p.Mp / 128) * (p.Kp / 256) * p.KS);
     hipLaunchKernelGGL(spike_linear_dw_kernel, dim3(grid), dim3(256), 0, stream, p);
     if (p.KS > 1) hipLaunchKernelGGL(spike_linear_dw_sum_kernel, dim3(1024), dim3(256), 0, stream, p);
 }

@@ -89,11 +89,14 @@ def test_recurrent_layer_output_feeds_the_spike_gemm(dev):
 
 
 @pytest.mark.gpu
-def test_spike_linear_weight_gradient_at_the_c5_width(dev):
-    """dW = g^T y on the bits at the inter-layer width of C5 (K = M = 2048, 512 batch rows,
-    the tile count that takes the unsplit XCD-grouped form), against float64."""
+@pytest.mark.parametrize('shape', [(40, 512, 2048, 2048), (33, 8, 4100, 4096)], ids=['c5_width', 'unsplit'])
+def test_spike_linear_weight_gradient_at_the_c5_width(dev, shape):
+    """dW = g^T y on the bits at the inter-layer width of C5 (K = M = 2048, 512 batch rows:
+    128 tiles of 128 x 256, split four ways over the steps, the tiles of one output tile and
+    split grouped on one XCD), and at a width whose 512 tiles run unsplit with K off the tile
+    multiple, against float64."""
     from delrec.spike_linear import spike_linear_dw
-    T, B, K, M = 40, 512, 2048, 2048
+    T, B, K, M = shape
     g = gen(12)
     y = (torch.rand(T, B, K, generator=g) < 0.03).float()
     gout = torch.randn(T, B, M, generator=g)
