@@ -240,7 +240,8 @@ typedef struct {
  * g[t][b][m] * y[t][b][k] (the reference computes it as the torch.nn.Linear backward,
  * g^T x on the fp32 spikes). g is applied as bf16 hi + mid + lo (about 2^-25 relative per
  * term, fp32 accumulation). Workspace: delrec_query_workspace(DELREC_WS_SPIKE_LINEAR_DW, T,
- * B, K, M, 0) (0 bytes when the output tiles alone fill the GPU). */
+ * B, K, M, 0): g's three bf16 planes (6 bytes per element of g, steps padded to 32) and, when
+ * the output tiles alone do not fill the GPU twice over, the splits' partial dW. */
 typedef struct {
     int32_t T, B, K, M;
     const uint32_t* bits;        /* (B, ceil(T/32), K) spike words                        */
