@@ -2,6 +2,7 @@
 surrogate ids, window length, dropout-mask normalisation."""
 
 import math
+import time
 
 import numpy as np
 import torch
@@ -29,9 +30,16 @@ def lif_struct(neuron, surrogate_function, gamma=None):
 _PINNED = {}
 
 
+# read_scalars polls its event without pause this long, then sleeps between polls (a long
+# forward scan would otherwise hold a host core for its whole duration)
+_SPIN_S, _NAP_S = 2e-4, 5e-5
+
+
 def read_scalars(*vals):
     """Copy a few 0-dim device tensors to the host through a pinned buffer and wait for them
-    by polling an event: the one device-to-host read of a forward, with a short wake-up."""
+    by polling an event: the one device-to-host read of a forward. Short waits (the small
+    configurations' scans take 0.1 ms) are spun for the earliest wake-up; past 0.2 ms the
+    thread sleeps 50 us between polls, which adds at most one nap to a long wait."""
     dev = vals[0].device
     buf = _PINNED.get(dev)
     if buf is None:
@@ -42,8 +50,10 @@ def read_scalars(*vals):
     stacked = vals[0].reshape(1) if n == 1 else torch.stack([v.reshape(()) for v in vals])
     host[:n].copy_(stacked.to(torch.float32), non_blocking=True)
     ev.record()
+    t0 = time.perf_counter()
     while not ev.query():
-        pass
+        if time.perf_counter() - t0 > _SPIN_S:
+            time.sleep(_NAP_S)
     return host[:n].tolist()
 
 

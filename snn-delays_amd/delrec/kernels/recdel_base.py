@@ -17,7 +17,8 @@ Modes (reference ``recdel_base.py:361-383``):
 Windows of more than 256 lags (the spike history the axonal kernels hold in registers) take
 the per-connection scans of the synaptic layer with every connection of source j at the
 source's delay, ``d[i, j] = d[j]``: the same triangle taps and the same sums, the delay
-gradient ``dd[j] = sum_i dd[i, j]`` (soft taps; the hard-tap modes raise for such windows).
+gradient ``dd[j] = sum_i dd[i, j]``; the hard-tap modes there run the soft scan at the tap's
+own delay with a half-width of 1 (``_long_window_forward``).
 """
 
 import ctypes
@@ -29,7 +30,7 @@ import torch
 from .. import _lib
 from ..spike_linear import attach_bits
 from ._common import (bits_shape, drop_bn, read_scalars, require_device, round_half_even_f32, weights,
-                      window_length_f32)
+                      window_length_f32, window_length_f64)
 from .delays import build_lag, build_lag_interp
 
 
@@ -137,11 +138,10 @@ class AxonalRecdelHip(torch.autograd.Function):
             (d_max,), s_max = read_scalars(dc.max()), 1.0 + sigma
         _APPLY_STATE.last_dmax = float(d_max)
         if window_length_f32(d_max, s_max) - 1 > REGISTER_LAGS:
-            if approx or ste_mode:
-                raise _lib.DelrecError('delrec_axonal_fwd', _lib.DELREC_ERR_WINDOW,
-                                       f'the hard-tap modes (approx, STE) take windows of at most '
-                                       f'{REGISTER_LAGS} lags; max d = {d_max:g}')
-            return _long_window_forward(ctx, x, W, d, dc, s_vec, sigma, bc, m, lif, p_spread)
+            hard = 'approx' if approx and not ste_mode else ('round' if ste_mode == 1 else
+                                                             'interp' if ste_mode else None)
+            return _long_window_forward(ctx, x, W, d, dc, s_vec, sigma, bc, m, lif, p_spread, hard,
+                                        d_max, s_max)
         lag = frac = None
         if ste_mode:
             L = window_length_f32(d_max, s_max)
@@ -214,29 +214,64 @@ class AxonalRecdelHip(torch.autograd.Function):
         return (dx, dW, db, dd, dp) + (None,) * 13
 
 
-def _long_window_forward(ctx, x, W, d, dc, s_vec, sigma, bc, m, lif, p_spread):
+def _long_window_forward(ctx, x, W, d, dc, s_vec, sigma, bc, m, lif, p_spread, hard, d_max, s_max):
     """The axonal layer through the synaptic scans with d[i, j] = d[j] (windows beyond the
-    register history)."""
+    register history).
+
+    The hard-tap forwards are the soft scan with a half-width of 1 at a delay of the tap's
+    own: weight max(0, 1 - |l - (1 + d')|) is 1 at lag l = 1 + d' for an integer d' = lag - 1
+    (``approx``, ``ste_round``: the rounded tap), and 1 - frac, frac at lags floor(1 + d) and
+    the next for d' = max(d, 0) (``ste_interp``: ``frac = 1 + d - lag`` is exact in fp32, so
+    the weights are the reference's own; d < 0 clamps to the one tap at lag 1). The STE
+    backward is the soft one at the layer's own delays and spread, except for dW, which pairs
+    the gradient of rec with the hard trace the forward used; ``approx`` back-propagates
+    through its one tap and takes the straight-through delay gradient
+    ``dd[j] = sum_{t,b} gz[t,b,j] (y[t-lag_j-1, b, j] - y[t-lag_j, b, j])`` with
+    ``gz = (dx m) W`` the gradient of the delayed trace."""
     from .synaptic_eventdriven import syn_forward
     N = x.shape[-1]
-    d_syn = dc.unsqueeze(0).expand(N, N).contiguous()
-    y, u, bits, L, Wc, w_bf16, s_max, _ = syn_forward(x, W, d_syn, None, None, s_vec, 1.0 + sigma, dc, bc, m, lif)
-    ctx.save_for_backward(u, y, bits, Wc, d_syn, s_vec, m, p_spread)
-    ctx.meta = ('long', L, w_bf16, sigma, s_max, W.dtype, s_vec is not None)
+    expand = lambda v: v.unsqueeze(0).expand(N, N).contiguous()
+    d_syn = expand(dc)
+    if hard is None:
+        d_fwd, s_fwd, s_uni = dc, s_vec, 1.0 + sigma
+    else:
+        if hard == 'interp':
+            d_fwd = dc.clamp(min=0.0)
+        else:
+            L_h = round_half_even_f32(d_max) + 2 if hard == 'approx' else window_length_f32(d_max, s_max)
+            d_fwd = (build_lag(dc, L_h) - 1).to(torch.float32)
+        s_fwd, s_uni = None, 1.0
+    y, u, bits, L, Wc, w_bf16, s_fmax, _ = syn_forward(x, W, d_syn if hard is None else expand(d_fwd), None, None,
+                                                       s_fwd, s_uni, d_fwd, bc, m, lif)
+    if hard is None or hard == 'approx':
+        d_bwd, s_bwd, L_bwd, s_bmax = (d_syn, s_vec, L, s_fmax) if hard is None else (expand(d_fwd), None, L, 1.0)
+    else:
+        d_bwd, s_bwd, s_bmax = d_syn, s_vec, float(s_max)
+        L_bwd = max(window_length_f64(d_max, s_max), 2)
+    ctx.save_for_backward(u, y, bits, Wc, d_bwd, s_bwd, m, p_spread, None if hard is None else d_fwd)
+    ctx.meta = ('long', L_bwd, w_bf16, sigma, s_bmax, W.dtype, s_vec is not None, hard)
     ctx.lif = lif
     return attach_bits(y, bits)
 
 
 def _long_window_backward(ctx, gy):
     from .synaptic_eventdriven import syn_backward
-    u, y, bits, Wc, d_syn, s_vec, m, p_spread = ctx.saved_tensors
-    _, L, w_bf16, sigma, s_max, w_dtype, use_sig_p = ctx.meta
-    need_p = use_sig_p and ctx.needs_input_grad[4]
-    dx, dW, dd, ds, db = syn_backward(gy, u, y, bits, Wc, w_bf16, d_syn, None, None, s_vec, 1.0 + sigma, s_max, m,
-                                      ctx.lif, L, ctx.needs_input_grad[1], ctx.needs_input_grad[3], need_p,
-                                      ctx.needs_input_grad[2])
+    u, y, bits, Wc, d_syn, s_vec, m, p_spread, d_tap = ctx.saved_tensors
+    _, L, w_bf16, sigma, s_max, w_dtype, use_sig_p, hard = ctx.meta
+    approx = hard == 'approx'
+    need_d = ctx.needs_input_grad[3]
+    need_p = use_sig_p and ctx.needs_input_grad[4] and not approx
+    s_uni = 1.0 if approx else 1.0 + sigma
+    ste = hard is not None and not approx
+    dx, dW, dd, ds, db = syn_backward(gy, u, y, bits, Wc, w_bf16, d_syn, None, None, None if approx else s_vec,
+                                      s_uni, s_max, m, ctx.lif, L, ctx.needs_input_grad[1] and not ste,
+                                      need_d and not approx, need_p, ctx.needs_input_grad[2])
     if dd is not None:
         dd = dd.sum(0)          # every connection of source j carries d[j]
+    if approx and need_d:
+        dd = _straight_through_dd(dx, m, Wc, y, d_tap)
+    if ste and ctx.needs_input_grad[1]:
+        dW = _hard_trace_dw(dx, m, y, d_tap)
     dp = None
     if need_p:
         with torch.enable_grad():
@@ -246,6 +281,43 @@ def _long_window_backward(ctx, gy):
     if dW is not None and w_dtype != torch.float32:
         dW = dW.to(w_dtype)
     return (dx, dW, db, dd, dp) + (None,) * 13
+
+
+def _delayed(y, lag):
+    """y[t - lag_j, b, j] (0 before the first step) for a per-source lag (N,) >= 0."""
+    T, B, N = y.shape
+    pad = int(lag.max())
+    yp = torch.cat([torch.zeros(pad, B, N, device=y.device, dtype=y.dtype), y])
+    idx = (torch.arange(T, device=y.device).view(T, 1) + pad - lag.view(1, N)).view(T, 1, N).expand(T, B, N)
+    return yp.gather(0, idx)
+
+
+def _straight_through_dd(dx, m, Wc, y, d_tap):
+    """``approx``'s delay gradient for the long-window route (see ``_long_window_forward``):
+    the gradient of the delayed trace z_j (rec_i = sum_j W_ij z_j enters the LIF input times
+    the dropout mask, as x does) against the difference of the spikes one lag past the tap
+    and at it."""
+    T, B, N = y.shape
+    g = dx if m is None else dx * m
+    gz = (g.reshape(T * B, N) @ Wc.float()).view(T, B, N)
+    lag = d_tap.to(torch.long) + 1
+    return (gz * (_delayed(y, lag + 1) - _delayed(y, lag))).sum((0, 1))
+
+
+def _hard_trace_dw(dx, m, y, d_tap):
+    """The STE modes' weight gradient for the long-window route: dW[i, j] = sum_{t,b}
+    gr[t,b,i] z[t,b,j] with gr = dx m the gradient of rec and z the forward's hard trace
+    (the value the straight-through trace carries), z_j = (1 - frac) y[t - lag_j] +
+    frac y[t - lag_j - 1] for the tap's delay d' = lag - 1 + frac (frac = 0: the rounded
+    tap)."""
+    T, B, N = y.shape
+    g = dx if m is None else dx * m
+    pos = 1.0 + d_tap
+    lag = torch.floor(pos)
+    frac = pos - lag
+    lag = lag.to(torch.long)
+    z = (1.0 - frac) * _delayed(y, lag) + frac * _delayed(y, lag + 1)
+    return g.reshape(T * B, N).t() @ z.reshape(T * B, N)
 
 
 # The reference's name for this Function (``delrec.triton_kernels.AxonalRecdelTriton``).

@@ -168,6 +168,58 @@ def test_hard_lag_builders():
     torch.testing.assert_close(frac, torch.tensor([0.0, 0.4, 0.6, 0.5, 0.7]))
 
 
+def test_long_window_approx_delay_gradient_matches_the_oracle():
+    """The long-window route's straight-through delay gradient of ``approx`` (host tensor
+    algebra over the backward's dx and the spikes), fed the oracle's own dx and spikes, equals
+    the oracle's autograd dd -- with dropout, and a negative delay clamped to lag 1."""
+    from helpers import gen, lif_params
+    from oracle import scans
+    from delrec.kernels.delays import build_lag
+    from delrec.kernels.recdel_base import _straight_through_dd
+    T, B, N = 60, 2, 24
+    g = gen(1)
+    x = torch.randn(T, B, N, generator=g) * 1.1 + 0.35
+    W = torch.randn(N, N, generator=g) * (4 / N ** 0.5)
+    d = torch.rand(N, generator=g) * 40
+    d[3] = -0.7
+    drop = (torch.rand(B, N, generator=g) > 0.2).float() / 0.8
+    xr, Wr, dr = (t.clone().requires_grad_(True) for t in (x, W, d))
+    y, _ = scans.axonal_v2(xr, Wr, dr, lif_params(), sigma=0.0, taps='approx', drop=drop)
+    (y * torch.randn(T, B, N, generator=g)).sum().backward()
+    lag = build_lag(d, int(torch.round(d).max()) + 2)
+    dd = _straight_through_dd(xr.grad, drop, W, y.detach(), (lag - 1).float())
+    assert float(dr.grad.abs().max()) > 1.0
+    torch.testing.assert_close(dd, dr.grad, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize('taps', ['ste_round', 'ste_interp'])
+def test_long_window_ste_weight_gradient_matches_the_oracle(taps):
+    """The long-window route's STE weight gradient (the gradient of rec against the forward's
+    hard trace, host tensor algebra), fed the oracle's own dx and spikes, equals the oracle's
+    autograd dW -- with dropout and a spread, whose soft taps the trace must not use."""
+    from helpers import gen, lif_params
+    from oracle import scans
+    from delrec.kernels.delays import build_lag
+    from delrec.kernels.recdel_base import _hard_trace_dw
+    from delrec.kernels._common import window_length_f32
+    T, B, N = 60, 2, 24
+    g = gen(2)
+    x = torch.randn(T, B, N, generator=g) * 1.1 + 0.35
+    W = torch.randn(N, N, generator=g) * (4 / N ** 0.5)
+    d = torch.rand(N, generator=g) * 40
+    d[5] = -0.4
+    drop = (torch.rand(B, N, generator=g) > 0.2).float() / 0.8
+    xr, Wr, dr = (t.clone().requires_grad_(True) for t in (x, W, d))
+    y, _ = scans.axonal_v2(xr, Wr, dr, lif_params(), sigma=0.7, taps=taps, drop=drop)
+    (y * torch.randn(T, B, N, generator=g)).sum().backward()
+    if taps == 'ste_round':
+        d_tap = (build_lag(d, window_length_f32(float(d.max()), 1.7)) - 1).float()
+    else:
+        d_tap = d.clamp(min=0.0)
+    dW = _hard_trace_dw(xr.grad, drop, y.detach(), d_tap)
+    torch.testing.assert_close(dW, Wr.grad, rtol=1e-5, atol=1e-5)
+
+
 def test_sigma_schedule_clamp_and_round():
     from delrec import networks
     from delrec.delay_layers import axonal_recdel

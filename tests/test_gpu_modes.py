@@ -44,6 +44,12 @@ MODES = [
     ('triton_ste', True, 'ste_round', 24, 3, 48, 9.0, 0.5),
     ('triton_ste', False, 'ste_interp', 24, 3, 48, 9.0, 0.5),
     ('triton_ste', False, 'ste_interp', 20, 2, 64, 12.0, 1.0),
+    # windows beyond the 256 lags of the axonal kernels' spike history: the synaptic scans
+    # at the tap's own delay (forward) and the soft or straight-through backward
+    ('triton_approx', True, 'approx', 300, 2, 40, 290.0, 0.0),
+    ('triton_approx', True, 'approx', 300, 2, 40, 290.0, 0.6),
+    ('triton_ste', True, 'ste_round', 300, 2, 40, 290.0, 0.5),
+    ('triton_ste', False, 'ste_interp', 310, 2, 40, 300.0, 0.7),
 ]
 
 
@@ -63,6 +69,8 @@ def test_hard_tap_modes_match_oracle(dev, case):
     y_ref, ext = scans.axonal_v2(xr, Wr, dr, lif, sigma=sigma, taps=taps)
     (y_ref * gy).sum().backward()
 
+    if T > 256:
+        assert float(d.max()) > 256.0, 'the case must take the long-window route'
     xg = x.to(dev).requires_grad_(True)
     y = layer(xg)
     (y * gy.to(dev)).sum().backward()
