@@ -31,15 +31,17 @@ _PINNED = {}
 
 
 # read_scalars polls its event without pause this long, then sleeps between polls (a long
-# forward scan would otherwise hold a host core for its whole duration)
-_SPIN_S, _NAP_S = 2e-4, 5e-5
+# wait would otherwise hold a host core for its whole duration)
+_SPIN_S, _NAP_S = 5e-3, 5e-5
 
 
 def read_scalars(*vals):
     """Copy a few 0-dim device tensors to the host through a pinned buffer and wait for them
-    by polling an event: the one device-to-host read of a forward. Short waits (the small
-    configurations' scans take 0.1 ms) are spun for the earliest wake-up; past 0.2 ms the
-    thread sleeps 50 us between polls, which adds at most one nap to a long wait."""
+    by polling an event: the one device-to-host read of a forward, which waits for the GPU
+    work queued before it (a previous backward: 0.1 to 5 ms at the small and mid-size shapes,
+    100 ms at the largest). Waits up to 5 ms are spun for the earliest wake-up; past that the
+    thread sleeps 50 us between polls, which adds at most one nap (about 0.1 ms with the
+    kernel's timer slack) to a wait of 5 ms or more."""
     dev = vals[0].device
     buf = _PINNED.get(dev)
     if buf is None:
