@@ -1378,7 +1378,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
             launch_lag_bf16(g, need_gr ? gr : a->dx, a->bits, s);
             LagGemm f{};
             f.N = N; f.KS = q.KS; f.W = a->W; f.w_bf16 = a->w_bf16; f.s = a->s; f.s_uniform = a->s_uniform;
-            f.pw = g.pw; f.pd = g.pd; f.ps = g.ps;
+            f.pw = g.pw; f.pd = g.pd; f.ps = g.ps; f.perm = lag_bf16_perm(g); f.cls = lag_bf16_cls(g);
             launch_lag_finish(f, a->dW, a->dd, a->ds, s);
         }
         return finish_launch();
@@ -1441,7 +1441,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
             launch_lag_bf16(g, a->drop ? gr : a->dx, a->bits, s);
             LagGemm f{};
             f.N = N; f.KS = q.KS; f.W = a->W; f.w_bf16 = a->w_bf16; f.s = a->s; f.s_uniform = a->s_uniform;
-            f.pw = g.pw; f.pd = g.pd; f.ps = g.ps;
+            f.pw = g.pw; f.pd = g.pd; f.ps = g.ps; f.perm = lag_bf16_perm(g); f.cls = lag_bf16_cls(g);
             launch_lag_finish(f, a->dW, a->dd, a->ds, s);
         }
         return finish_launch();
@@ -1482,7 +1482,7 @@ int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream) {
         launch_lag_bf16(g, a->drop ? gr : a->dx, a->bits, s);
         LagGemm f{};
         f.N = N; f.KS = q.KS; f.W = a->W; f.w_bf16 = a->w_bf16; f.s = a->s; f.s_uniform = a->s_uniform;
-        f.pw = g.pw; f.pd = g.pd; f.ps = g.ps;
+        f.pw = g.pw; f.pd = g.pd; f.ps = g.ps; f.perm = lag_bf16_perm(g); f.cls = lag_bf16_cls(g);
         launch_lag_finish(f, a->dW, a->dd, a->ds, s);
     }
     return finish_launch();

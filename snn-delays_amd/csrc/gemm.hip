@@ -15,28 +15,44 @@ __global__ void lag_finish_kernel(LagGemm p, float* dW, float* dd) {
     const size_t NN = (size_t)p.N * p.N;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= NN) return;
+    // the partials' column position -> the column (the event-driven correlation's order);
+    // there, silent columns' sums are 0 and the sparse tiles' columns hold one partial per
+    // 64-row chunk (the even ones)
+    const int jp = (int)(idx % p.N);
+    int k0 = 0, kd = 1;
+    if (p.cls) {
+        if (jp < p.cls[0]) k0 = p.KS;
+        else if (jp < (p.cls[0] + p.cls[1]) / 64 * 64) kd = 2;
+    }
     float aw = 0.0f, ad = 0.0f;
 #pragma unroll 8
-    for (int k = 0; k < p.KS; ++k) {
+    for (int k = k0; k < p.KS; k += kd) {
         aw += p.pw[(size_t)k * NN + idx];
         if (p.pd) ad += p.pd[(size_t)k * NN + idx];
     }
-    if (dW) dW[idx] = aw;
+    const int j = p.perm ? p.perm[jp] : jp;
+    const size_t out = idx - jp + j;
+    if (dW) dW[out] = aw;
     if (dd) {
-        const int j = (int)(idx % p.N);
         const float s = p.s ? p.s[j] : p.s_uniform;
-        dd[idx] = load_w(p.W, p.w_bf16, idx) * (ad / (s * s));
+        dd[out] = load_w(p.W, p.w_bf16, out) * (ad / (s * s));
     }
 }
 
 __global__ void lag_ds_kernel(LagGemm p, float* ds) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= p.N) return;
+    const int jp = blockIdx.x * blockDim.x + threadIdx.x;
+    if (jp >= p.N) return;
+    const int j = p.perm ? p.perm[jp] : jp;
     const size_t NN = (size_t)p.N * p.N;
+    int k0 = 0, kd = 1;   // as lag_finish_kernel
+    if (p.cls) {
+        if (jp < p.cls[0]) k0 = p.KS;
+        else if (jp < (p.cls[0] + p.cls[1]) / 64 * 64) kd = 2;
+    }
     float acc = 0.0f;
     for (int i = 0; i < p.N; ++i) {
         float c = 0.0f;
-        for (int k = 0; k < p.KS; ++k) c += p.ps[(size_t)k * NN + (size_t)i * p.N + j];
+        for (int k = k0; k < p.KS; k += kd) c += p.ps[(size_t)k * NN + (size_t)i * p.N + jp];
         acc += load_w(p.W, p.w_bf16, (size_t)i * p.N + j) * c;
     }
     ds[j] = acc;

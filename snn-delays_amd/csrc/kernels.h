@@ -117,6 +117,8 @@ struct LagGemm {
     float* pw;                  // [KS][N][N] partial sum_l h * C_l
     float* pd;                  // [KS][N][N] partial sum_l sign * C_l, or NULL
     float* ps;                  // [KS][N][N] partial sum_l dh/ds * C_l, or NULL
+    const int* perm;            // column order of the partials (event-driven form), or NULL
+    const int* cls;             // and its class sizes (silent, sparse, dense), or NULL
 };
 
 // bf16-MFMA lag-correlation GEMM (lagmm.hip): operands packed in the k-blocked layout,
@@ -142,6 +144,11 @@ struct LagBf16 {
     float* pd;                   // [KS][N][N] partial sum_l sign * C_l
     float* ps;                   // [KS][N][N] partial sum_l dh/ds * C_l, or NULL
     int planes;                  // gr planes multiplied: 3 (hi, mid, lo), or 2 (hi, mid) for bf16 W
+    // the event-driven form (set by launch_lag_bf16): the sparse tiles' spike code words
+    // [t][Bp / 64][4][Np] and the column order perm (class sizes cls[0..2]); NULL otherwise
+    const uint32_t* ycode;
+    const int* perm;
+    const int* cls;
 };
 
 // lag-stacked per-step GEMM scans (lagstep.hip)
@@ -473,6 +480,11 @@ size_t syn_bwd_hyb_g_lds(int N, int L, int D, int* gs);
 void launch_lag_cols(const LagBf16& a, hipStream_t stream);
 // packs gr / spikes, then the lag GEMM into a.pw / a.pd / a.ps
 void launch_lag_bf16(const LagBf16& a, const float* gr, const uint32_t* bits, hipStream_t stream);
+// whether launch_lag_bf16 takes the event-driven form (spike columns by class), and the
+// column order and class sizes of the partial sums it leaves there (else NULL)
+bool lag_bf16_sparse(const LagBf16& a);
+const int* lag_bf16_perm(const LagBf16& a);
+const int* lag_bf16_cls(const LagBf16& a);
 // dW = sum_k pw; dd = W/s^2 * sum_k pd; ds[j] = sum_i W[i,j] * sum_k ps[i,j]
 void launch_lag_finish(const LagGemm& a, float* dW, float* dd, float* ds, hipStream_t stream);
 
