@@ -823,11 +823,16 @@ void launch_lag_cols(const LagBf16& a, hipStream_t stream) {
 }
 
 bool lag_bf16_sparse(const LagBf16& a) {
+    // DELREC_LAG_SPARSE=0 turns the form off, =1 takes it whatever the grid
     const char* e = std::getenv("DELREC_LAG_SPARSE");
-    const bool off = e && e[0] == '0';
-    // bf16 W (two gr planes; the third plane's buffer holds the event-driven form's arrays)
-    // and whole 64-row chunks
-    return !off && a.planes == 2 && a.Bp % 64 == 0;
+    const bool off = e && e[0] == '0', force = e && e[0] == '1';
+    // bf16 W (two gr planes; the third plane's buffer holds the event-driven form's arrays),
+    // whole 64-row chunks, and a dense grid of at least 4096 workgroups (16 per CU): below
+    // that the correlation takes one workgroup's walk over the steps whatever its share of the
+    // work, and two launches (sparse and dense tiles) take two walks (C3, 512 workgroups:
+    // 0.39 ms dense, 0.60 ms split)
+    const size_t wgs = (size_t)(a.Np / kWT) * (a.Np / kWT) * (a.Bp / 32);
+    return !off && a.planes == 2 && a.Bp % 64 == 0 && (force || wgs >= 4096);
 }
 
 namespace {

@@ -1,5 +1,6 @@
 """GPU parity of the event-driven lag correlation (``lag_win_sp_kernel``, csrc/lagmm.hip): the
-weight- and delay-gradient correlation for bf16 W when the batch fills 64-row chunks. Spike
+weight- and delay-gradient correlation for bf16 W when the batch fills 64-row chunks and the
+dense grid has at least 4096 workgroups (forced here with DELREC_LAG_SPARSE=1). Spike
 columns are ordered by class on the device -- silent (no products), sparse (at most two spikes
 in any group of four batch rows: the exact compressed operand of the 4:2 sparse MFMA), dense
 (the dense MFMA on 0/1 spikes) -- and put back by lag_finish.
@@ -67,6 +68,7 @@ def test_sparse_lag_correlation_matches_dense(dev, case, monkeypatch, capfd):
     layer = hybrid_layer(N, W, base, offsets, dev, bf16=True, sigma_init=sigma)
     xd, gyd = x.to(dev), gy.to(dev)
     monkeypatch.setenv('DELREC_LOG_PLAN', '1')
+    monkeypatch.setenv('DELREC_LAG_SPARSE', '1')   # these grids are below the form's own threshold
     y, dx, dW, dbase = _grads(layer, xd, gyd)
     plan = capfd.readouterr().err
     assert 'lag correlation: event-driven spikes' in plan, plan
