@@ -618,6 +618,27 @@ void delrec::ensure_lds(const void* fn, size_t bytes) {
     done.emplace_back(fn, bytes);
 }
 
+namespace delrec {
+namespace {
+
+// The input neurons in activity order (the kernels then skip the silent ones), unless
+// DELREC_SPIKE_ORDER=0 (natural order, the spike words read as given)
+template <class P>
+void spike_linear_order(P& p, void* room, hipStream_t s) {
+    const char* e = getenv("DELREC_SPIKE_ORDER");
+    p.ldb = p.K;
+    if (e && e[0] == '0') return;
+    const SpikeOrder o = spike_order_carve(room, p.T, p.B, p.K);
+    launch_spike_order(p.bits, p.T, p.B, p.K, o, s);
+    p.bits = o.bits;
+    p.ldb = spike_order_kp(p.K);
+    p.perm = o.perm;
+    p.cls = o.cls;
+}
+
+}  // namespace
+}  // namespace delrec
+
 extern "C" {
 
 int delrec_peak_mfma(int32_t kind, int32_t iters, float* sink, size_t sink_bytes, double* flops, void* stream) {
@@ -674,8 +695,10 @@ int delrec_query_workspace(int32_t kind, int32_t T, int32_t B, int32_t N, int32_
             break;
         case DELREC_WS_SPIKE_LINEAR:
             c.take<uint4>(spike_linear_ws(N, L) / sizeof(uint4));
+            c.take<uint4>(spike_order_ws(T, B, N) / sizeof(uint4));
             break;
         case DELREC_WS_SPIKE_LINEAR_DW:
+            c.take<uint4>(spike_order_ws(T, B, N) / sizeof(uint4));
             c.take<uint4>(spike_linear_dw_planes(T, B, L));
             c.take<float>((spike_linear_dw_ws(T, B, N, L, num_cus()) -
                            spike_linear_dw_planes(T, B, L) * sizeof(uint4)) / sizeof(float));
@@ -1064,14 +1087,19 @@ int delrec_spike_linear_fwd(const delrec_spike_linear_args* a, void* stream) {
     p.T = a->T; p.B = a->B; p.K = a->K; p.M = a->M;
     p.bits = a->bits; p.W = a->W; p.bias = a->bias; p.out = a->out;
     spike_linear_dims(p);
-    // 32-bit byte offsets: the spike words, the packed planes and one output row block
+    // 32-bit byte offsets: the spike words (in the activity order's pitch), the packed planes
+    // and one output row block
     const int TW = (p.T + 31) / 32;
-    if ((size_t)p.B * TW * p.K * 4 >= ((size_t)1 << 31) || spike_linear_ws(p.K, p.M) >= ((size_t)1 << 31))
+    if ((size_t)p.B * TW * spike_order_kp(p.K) * 4 >= ((size_t)1 << 31) ||
+        spike_linear_ws(p.K, p.M) >= ((size_t)1 << 31))
         return DELREC_ERR_UNSUPPORTED;
     Carver cv(a->workspace, a->workspace_bytes);
     uint4* wp = cv.take<uint4>(spike_linear_ws(p.K, p.M) / sizeof(uint4));
-    if (!wp) return DELREC_ERR_WORKSPACE;
-    launch_spike_linear(p, wp, static_cast<hipStream_t>(stream));
+    uint4* ob = cv.take<uint4>(spike_order_ws(p.T, p.B, p.K) / sizeof(uint4));
+    if (!wp || !ob) return DELREC_ERR_WORKSPACE;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    spike_linear_order(p, ob, s);
+    launch_spike_linear(p, wp, s);
     return finish_launch();
 }
 
@@ -1083,13 +1111,16 @@ int delrec_spike_linear_dw(const delrec_spike_linear_dw_args* a, void* stream) {
     p.bits = a->bits; p.g = a->g; p.dW = a->dW;
     spike_linear_dw_dims(p, num_cus());
     Carver cv(a->workspace, a->workspace_bytes);
+    uint4* ob = cv.take<uint4>(spike_order_ws(p.T, p.B, p.K) / sizeof(uint4));
     p.gp = cv.take<uint4>(spike_linear_dw_planes(p.T, p.B, p.M));
-    if (!p.gp) return DELREC_ERR_WORKSPACE;
+    if (!ob || !p.gp) return DELREC_ERR_WORKSPACE;
     if (p.KS > 1) {
         p.part = cv.take<float>((size_t)p.KS * p.M * p.K);
         if (!p.part) return DELREC_ERR_WORKSPACE;
     }
-    launch_spike_linear_dw(p, static_cast<hipStream_t>(stream));
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    spike_linear_order(p, ob, s);
+    launch_spike_linear_dw(p, s);
     return finish_launch();
 }
 

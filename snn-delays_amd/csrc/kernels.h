@@ -321,9 +321,28 @@ struct HybScat {                 // the hybrid forward as a scatter on arrival (
 bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t lds, hipStream_t stream);
 
 // Linear layer on spike inputs (spikelinear.hip): out[t][b][m] = bias[m] + sum_k y W[m][k]
+// The input neurons of a spike Linear in activity order (silent ones first, then those that
+// spike, stably; positions K .. KP-1 padding, perm -1): cnt [2][KP] counts, the order, the
+// class sizes (cls[0] = silent neurons), and the spike words regathered in that order
+// (B, ceil(T/32), KP). KP = K rounded up to 256.
+struct SpikeOrder {
+    int* cnt;
+    int* perm;
+    int* cls;
+    uint32_t* bits;
+};
+int spike_order_kp(int K);
+size_t spike_order_ws(int T, int B, int K);
+SpikeOrder spike_order_carve(void* base, int T, int B, int K);
+void launch_spike_order(const uint32_t* bits, int T, int B, int K, const SpikeOrder& o, hipStream_t stream);
+void launch_col_order(const int* cnt, int N, int Np, int* perm, int* cls, hipStream_t stream);
+
 struct SpikeLinear {
     int T, B, K, M, Kp, Mp;      // Kp = K rounded up to 32, Mp = M rounded up to 128
-    const uint32_t* bits;        // (B, ceil(T/32), K) spike words
+    const uint32_t* bits;        // (B, ceil(T/32), ldb) spike words
+    int ldb;                     // their row pitch (K, or the order's KP)
+    const int* perm;             // input neuron of each position (activity order), or NULL
+    const int* cls;              // the order's class sizes (stages below cls[0] / 32 are skipped)
     const float* W;              // (M, K) fp32
     const float* bias;           // (M) or NULL
     float* out;                  // (T, B, M) fp32
@@ -333,7 +352,10 @@ size_t spike_linear_ws(int K, int M);   // bytes of the packed W^T planes
 void launch_spike_linear(const SpikeLinear& p, uint4* wp, hipStream_t stream);
 struct SpikeLinearDw {           // dW[m][k] = sum_{t,b} g[t][b][m] y[t][b][k]
     int T, B, K, M, Kp, Mp, KS;  // Kp, Mp rounded up to 128; KS splits of the (b, word) stages
-    const uint32_t* bits;        // (B, ceil(T/32), K)
+    const uint32_t* bits;        // (B, ceil(T/32), ldb)
+    int ldb;                     // their row pitch (K, or the order's KP)
+    const int* perm;             // input neuron of each column position, or NULL
+    const int* cls;              // the order's class sizes (tiles of silent neurons: zeros)
     const float* g;              // (T, B, M)
     float* dW;                   // (M, K)
     float* part;                 // [KS][M][K] when KS > 1

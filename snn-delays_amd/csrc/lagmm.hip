@@ -863,6 +863,10 @@ LagSpRoom lag_sp_room(const LagBf16& a) {
 
 }  // namespace
 
+void launch_col_order(const int* cnt, int N, int Np, int* perm, int* cls, hipStream_t stream) {
+    hipLaunchKernelGGL(lag_perm_kernel, dim3(1), dim3(1024), 0, stream, cnt, N, Np, perm, cls);
+}
+
 const int* lag_bf16_perm(const LagBf16& a) { return lag_bf16_sparse(a) ? lag_sp_room(a).perm : nullptr; }
 const int* lag_bf16_cls(const LagBf16& a) { return lag_bf16_sparse(a) ? lag_sp_room(a).cls : nullptr; }
 

@@ -31,8 +31,9 @@ constexpr int kSpikeLinearPlanes = 3;
 
 }  // namespace
 
-// W^T planes, k-blocked: element (k, m) = W[m][k] at ((k / 8) * Mp + m) * 8 + k % 8, hi, mid
-// and lo planes in turn; columns m >= M and rows k >= K are 0.
+// W^T planes, k-blocked: element (k, m) = W[m][k'] at ((k / 8) * Mp + m) * 8 + k % 8, hi, mid
+// and lo planes in turn, k' = perm[k] (k without an order); columns m >= M and rows without a
+// neuron are 0.
 __global__ void __launch_bounds__(256) spike_linear_pack_kernel(SpikeLinear p, uint4* out) {
     const size_t total = (size_t)(p.Kp / 8) * p.Mp;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -44,8 +45,9 @@ __global__ void __launch_bounds__(256) spike_linear_pack_kernel(SpikeLinear p, u
         uint32_t v2[kSpikeLinearPlanes][2];
 #pragma unroll
         for (int f = 0; f < 2; ++f) {
-            const int k = kb * 8 + e + f;
-            float r = (m < p.M && k < p.K) ? p.W[(size_t)m * p.K + k] : 0.0f;
+            const int kp = kb * 8 + e + f;
+            const int k = p.perm ? p.perm[kp] : kp;
+            float r = (m < p.M && k >= 0 && k < p.K) ? p.W[(size_t)m * p.K + k] : 0.0f;
 #pragma unroll
             for (int q = 0; q < kSpikeLinearPlanes; ++q) {   // each plane the remainder's bf16
                 v2[q][f] = sl_bf16_rne(r);
@@ -61,9 +63,10 @@ __global__ void __launch_bounds__(256) spike_linear_pack_kernel(SpikeLinear p, u
 }
 
 // Tile: 128 steps t0 .. t0 + 127 of batch row b x 128 columns n0 .. n0 + 127; 4 waves of
-// 64 x 64 (4 x 4 MFMA blocks, three W planes). Stage s covers neurons 32 s .. 32 s + 31. Loads
-// of stage s + 2 are issued while stage s multiplies; stage s + 1 goes to LDS after it; one
-// barrier per stage.
+// 64 x 64 (4 x 4 MFMA blocks, three W planes). Stage s covers neuron positions 32 s .. 32 s +
+// 31; with an activity order the stages wholly below the first spiking neuron are skipped
+// (their spike words are all 0). Loads of stage s + 2 are issued while stage s multiplies;
+// stage s + 1 goes to LDS after it; one barrier per stage.
 __global__ void __launch_bounds__(256) spike_linear_kernel(SpikeLinear p, const uint4* wp) {
     constexpr int PL = kSpikeLinearPlanes;
     __shared__ uint4 sw[2][PL][512];     // [buffer][plane][k-block * 128 + column]
@@ -75,9 +78,10 @@ __global__ void __launch_bounds__(256) spike_linear_kernel(SpikeLinear p, const 
     const int nt = id % NT, rest = id / NT, tt = rest % TT, b = rest / TT;
     const int t0 = tt * 128, n0 = nt * 128;
     const int nst = p.Kp / 32;
+    const int s0 = p.cls ? min(p.cls[0] / 32, nst) : 0;
     const size_t plane = (size_t)(p.Kp / 8) * p.Mp;
     const i32x4 rw = buffer_rsrc(wp, (uint32_t)(PL * plane * 16));
-    const i32x4 rb = buffer_rsrc(p.bits, (uint32_t)((size_t)p.B * TW * p.K * 4));
+    const i32x4 rb = buffer_rsrc(p.bits, (uint32_t)((size_t)p.B * TW * p.ldb * 4));
     // staging: W uint4 c = tid + 256 h (k-block c >> 7, column c & 127) of both planes; the
     // spike word of (32-step block tid >> 5, neuron tid & 31) for threads below 128
     uint32_t ow[2];
@@ -89,7 +93,7 @@ __global__ void __launch_bounds__(256) spike_linear_kernel(SpikeLinear p, const 
     const uint32_t wstep = (uint32_t)(4 * p.Mp * 16);
     const int tb = tid >> 5, kk = tid & 31;
     const bool aload = tid < 128 && (t0 >> 5) + tb < TW;
-    const uint32_t oa0 = aload ? (uint32_t)((((size_t)b * TW + (t0 >> 5) + tb) * p.K + kk) * 4) : 0x7ffffff0u;
+    const uint32_t oa0 = aload ? (uint32_t)((((size_t)b * TW + (t0 >> 5) + tb) * p.ldb + kk) * 4) : 0x7ffffff0u;
     uint4 rwv[2][PL][2];   // [register set][plane][h]
     uint32_t rav[2];
     auto issue = [&](int set, int s) {
@@ -148,11 +152,11 @@ __global__ void __launch_bounds__(256) spike_linear_kernel(SpikeLinear p, const 
                     acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[mb], fb[q][nb], acc[mb][nb], 0, 0, 0);
     };
 
-    issue(0, 0);
-    issue(1, 1);
+    issue(0, s0);
+    issue(1, s0 + 1);
     stash(0, 0);
     barrier_lds();
-    for (int s = 0; s < nst; s += 2) {
+    for (int s = s0; s < nst; s += 2) {
         // stage s in LDS buffer 0, stage s + 1 in register set 1
         issue(0, s + 2);
         compute(0);
@@ -272,7 +276,7 @@ __global__ void __launch_bounds__(256) spike_linear_dw_kernel(SpikeLinearDw p) {
             const int u = tid + 256 * x, q = u >> 9, h = (u >> 7) & 3, m = m0 + (u & 127);
             rg[x] = (s < s1 && m < p.M) ? p.gp[((((size_t)q * p.B + b) * TW + wd) * 4 + h) * p.M + m] : make_uint4(0u, 0u, 0u, 0u);
         }
-        rb = (s < s1 && k0 + tid < p.K) ? p.bits[((size_t)b * TW + wd) * p.K + k0 + tid] : 0u;
+        rb = (s < s1 && k0 + tid < p.ldb) ? p.bits[((size_t)b * TW + wd) * p.ldb + k0 + tid] : 0u;
     };
     auto stash = [&](int buf) {
 #pragma unroll
@@ -308,17 +312,20 @@ __global__ void __launch_bounds__(256) spike_linear_dw_kernel(SpikeLinearDw p) {
                     acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb[nb], acc[mb][nb], 0, 0, 0);
             }
     };
+    // a tile of silent input neurons (activity order) has dW = 0: no stages
+    const int se = (p.cls && k0 + 256 <= p.cls[0]) ? s0 : s1;
     issue(s0);
     stash(0);
     barrier_lds();
-    for (int s = s0; s < s1; ++s) {
+    for (int s = s0; s < se; ++s) {
         const int buf = (s - s0) & 1;
         issue(s + 1);                 // past s1: zeros (no load)
         compute(buf);
         stash(buf ^ 1);
         barrier_lds();
     }
-    // rows m = m0 + wi 64 + mb 16 + 4 g + e, columns k = k0 + wj 128 + nb 16 + lc
+    // rows m = m0 + wi 64 + mb 16 + 4 g + e, column positions k0 + wj 128 + nb 16 + lc (the
+    // input neurons perm[.] with an order)
     float* out = p.KS == 1 ? p.dW : p.part + (size_t)ks * p.M * p.K;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
@@ -328,8 +335,9 @@ __global__ void __launch_bounds__(256) spike_linear_dw_kernel(SpikeLinearDw p) {
             if (m >= p.M) continue;
 #pragma unroll
             for (int nb = 0; nb < 8; ++nb) {
-                const int k = k0 + wj * 128 + nb * 16 + lc;
-                if (k < p.K) out[(size_t)m * p.K + k] = acc[mb][nb][e];
+                const int kp = k0 + wj * 128 + nb * 16 + lc;
+                const int k = p.perm ? p.perm[kp] : kp;
+                if (k >= 0 && k < p.K) out[(size_t)m * p.K + k] = acc[mb][nb][e];
             }
         }
 }
@@ -384,6 +392,68 @@ size_t spike_linear_ws(int K, int M) {
     p.M = M;
     spike_linear_dims(p);
     return (size_t)kSpikeLinearPlanes * (p.Kp / 8) * p.Mp * sizeof(uint4);
+}
+
+// ---------------------------------------------------------------------------------------
+// Input neurons in activity order: cnt[k] = 1 where neuron k spikes anywhere (cnt[KP ..] stay
+// 0: no second class), the column order of the event-driven lag correlation (silent first,
+// stably), and the spike words regathered in that order.
+__global__ void spike_active_kernel(const uint32_t* __restrict__ bits, size_t rows, int K, int* __restrict__ cnt) {
+    const size_t n = rows * K;
+    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < n; q += (size_t)gridDim.x * blockDim.x)
+        if (bits[q]) cnt[q % K] = 1;   // every writer stores the same value
+}
+
+__global__ void spike_zero_kernel(int* __restrict__ p, int n) {
+    for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < n; q += gridDim.x * blockDim.x) p[q] = 0;
+}
+
+__global__ void spike_gather_kernel(const uint32_t* __restrict__ bits, size_t rows, int K, int KP,
+                                    const int* __restrict__ perm, uint32_t* __restrict__ out) {
+    const size_t n = rows * KP;
+    for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < n; q += (size_t)gridDim.x * blockDim.x) {
+        const int kp = (int)(q % KP);
+        const int k = perm[kp];
+        out[q] = k >= 0 ? bits[(q / KP) * K + k] : 0u;
+    }
+}
+
+int spike_order_kp(int K) { return (K + 255) / 256 * 256; }
+
+namespace {
+size_t sl_up(size_t v) { return (v + 255) / 256 * 256; }
+}
+
+size_t spike_order_ws(int T, int B, int K) {
+    const size_t KP = spike_order_kp(K), rows = (size_t)B * ((T + 31) / 32);
+    return sl_up(2 * KP * sizeof(int)) + sl_up(KP * sizeof(int)) + 256 + sl_up(rows * KP * sizeof(uint32_t));
+}
+
+SpikeOrder spike_order_carve(void* base, int T, int B, int K) {
+    const size_t KP = spike_order_kp(K);
+    char* c = static_cast<char*>(base);
+    SpikeOrder o;
+    o.cnt = reinterpret_cast<int*>(c);
+    c += sl_up(2 * KP * sizeof(int));
+    o.perm = reinterpret_cast<int*>(c);
+    c += sl_up(KP * sizeof(int));
+    o.cls = reinterpret_cast<int*>(c);
+    c += 256;
+    o.bits = reinterpret_cast<uint32_t*>(c);
+    (void)T;
+    (void)B;
+    return o;
+}
+
+void launch_spike_order(const uint32_t* bits, int T, int B, int K, const SpikeOrder& o, hipStream_t stream) {
+    const int KP = spike_order_kp(K);
+    const size_t rows = (size_t)B * ((T + 31) / 32);
+    hipLaunchKernelGGL(spike_zero_kernel, dim3((2 * KP + 255) / 256), dim3(256), 0, stream, o.cnt, 2 * KP);
+    const unsigned blocks = (unsigned)std::min<size_t>((rows * K + 255) / 256, 65535u * 4);
+    hipLaunchKernelGGL(spike_active_kernel, dim3(blocks), dim3(256), 0, stream, bits, rows, K, o.cnt);
+    launch_col_order(o.cnt, K, KP, o.perm, o.cls, stream);
+    const unsigned gblocks = (unsigned)std::min<size_t>((rows * KP + 255) / 256, 65535u * 4);
+    hipLaunchKernelGGL(spike_gather_kernel, dim3(gblocks), dim3(256), 0, stream, bits, rows, K, KP, o.perm, o.bits);
 }
 
 void launch_spike_linear(const SpikeLinear& p, uint4* wp, hipStream_t stream) {

@@ -4,7 +4,9 @@
 The spikes are exact; W (forward) and g (weight gradient) enter as bf16 hi + mid + lo (about
 2^-25 relative), so the tolerance is fp32's: rtol 1e-5, atol 1e-6 relative to the output's
 magnitude. Shapes cover T, K and M off their tile multiples (128 steps, 32
-neurons, 128 outputs), with and without bias, and the bits attached by a recurrent layer.
+neurons, 128 outputs), with and without bias, inputs mostly or wholly silent (the kernels take
+the input neurons in activity order and skip the silent ones), and the bits attached by a
+recurrent layer.
 """
 
 import numpy as np
@@ -27,22 +29,25 @@ def pack_bits(y):
 
 
 CASES = [
-    # T, B, K, M, bias, firing rate
-    (64, 3, 64, 128, False, 0.05),
-    (70, 5, 300, 130, True, 0.1),
-    (200, 2, 33, 7, True, 0.5),
-    (129, 4, 2048, 256, False, 0.03),
+    # T, B, K, M, bias, firing rate, silent input fraction
+    (64, 3, 64, 128, False, 0.05, 0.0),
+    (70, 5, 300, 130, True, 0.1, 0.0),
+    (200, 2, 33, 7, True, 0.5, 0.0),
+    (129, 4, 2048, 256, False, 0.03, 0.0),
+    (96, 4, 700, 200, True, 0.08, 0.7),     # most inputs silent: the stages below them skipped
+    (40, 2, 300, 64, False, 0.1, 1.0),      # every input silent: out = bias, dW = 0
 ]
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('case', CASES, ids=[f'T{c[0]}B{c[1]}K{c[2]}M{c[3]}{"b" if c[4] else ""}' for c in CASES])
+@pytest.mark.parametrize('case', CASES, ids=[f'T{c[0]}B{c[1]}K{c[2]}M{c[3]}{"b" if c[4] else ""}q{c[6]}' for c in CASES])
 def test_spike_linear_matches_linear(dev, case):
     from delrec.spike_linear import SpikeLinear, attach_bits
-    T, B, K, M, bias, rate = case
+    T, B, K, M, bias, rate, quiet = case
     print(f'case {case}', flush=True)
     g = gen(11)
     y = (torch.rand(T, B, K, generator=g) < rate).float()
+    y[:, :, torch.randperm(K, generator=g)[:int(quiet * K)]] = 0.0
     lin = SpikeLinear(K, M, bias=bias)
     with torch.no_grad():
         lin.weight.copy_(torch.randn(M, K, generator=g) / K ** 0.5)
