@@ -431,16 +431,18 @@ __global__ void __launch_bounds__(256) lag_win_kernel(LagBf16 p) {
 //  sparse  never more than two spikes in a group: the spikes are the exact compressed operand
 //          of the 4:2 sparse MFMA (v_smfmac_f32_16x16x64_bf16: values bf16 1.0, or 0 where a
 //          group has fewer), half the dense issue;
-//  dense   some group with three or four spikes: the dense MFMA on 0/1 bf16 spikes.
+//  dense   some group with three or four spikes: the dense kernel above (lag_win_kernel) on
+//          the spike operand packed in the same column order.
 // The columns are reordered by class (stable) so that 64-column tiles hold one class where
 // they can (a tile takes the heaviest class among its columns); the partial sums stay in that
-// order and lag_finish puts each column back. Output C^T: rows j (spike columns), columns i.
+// order and lag_finish puts each column back. The sparse kernel's output is C^T: rows j
+// (spike columns), columns i.
 //
-// Operand lanes: the sparse A lane l is row l % 16, values 2gg, 2gg + 1 in group 4 (l / 16) + gg
+// Sparse operand lanes: the A lane l is row l % 16, values 2gg, 2gg + 1 in group 4 (l / 16) + gg
 // with their 2-bit positions in bits 4gg .. 4gg + 3 of the index, so lane group g = l / 16
-// covers batch rows 16g .. 16g + 15; a dense A lane covers rows 8g .. 8g + 7 (and 32 + 8g ..
-// in the second K = 32 half); a B lane supplies rows 8g .. 8g + 7 and 32 + 8g .. + 7 of its
-// column (slots 0-7, 8-15), the two halves of one 32-byte run of the paired gr layout.
+// covers batch rows 16g .. 16g + 15 of the 64-row chunk; a B lane supplies rows 8g .. 8g + 7
+// and 32 + 8g .. + 7 of its receiver (slots 0-7, 8-15): the k-blocks g and g + 4 of the chunk
+// in the dense kernel's gr planes.
 
 // 16 spike bits (bit q = batch row 16g + q) -> one sparse A lane as a code word: bits 0-15 the
 // value positions, 16-23 two value bits per group (value 2gg at bit 16 + 2gg, 2gg + 1 at
