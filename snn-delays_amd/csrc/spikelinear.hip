@@ -357,7 +357,10 @@ void spike_linear_dw_dims(SpikeLinearDw& p, int cus) {
     p.Kp = (p.K + 255) / 256 * 256;
     const int tiles = (p.Mp / 128) * (p.Kp / 256);
     const int nst = p.B * ((p.T + 31) >> 5);
-    p.KS = std::max(1, std::min((2 * cus + tiles - 1) / tiles, std::max(1, nst / 16)));   // >= 16 stages a split
+    // about four workgroups per CU when every tile works (two fit a CU at a time), so that the
+    // tiles of spiking inputs alone -- those of silent inputs end at once -- still keep about
+    // two per CU at C5's first layer (30 % spiking); >= 16 stages a split
+    p.KS = std::max(1, std::min((4 * cus + tiles - 1) / tiles, std::max(1, nst / 16)));
 }
 
 size_t spike_linear_dw_ws(int T, int B, int K, int M, int cus) {
