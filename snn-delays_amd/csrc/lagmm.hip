@@ -616,14 +616,14 @@ __device__ uint32_t lw_buffer_load_u32(i32x4 rsrc, int voff, int soff, int aux)
 // one 64-row chunk bc; waves of JB column blocks (16) x IB receiver blocks (16), JB x IB = 4
 // (JB = 4: each wave 16 receivers x all 64 columns). Step n reads the gr slice q0 + n (both
 // planes; per lane and block the k-blocks g and g + 4 of the chunk: K = 64) and multiplies it
-// with the code words of slices n - r, r < RL, held expanded in a window of KWY = RL + 2 slots
-// (loaded two steps ahead); gr rotates through two slots. The chunk's sums go to the partial
-// of its first 32 rows (the partials are per 32-row chunk, as the dense kernel's; lag_finish
-// reads the even ones for these columns).
-template <int RL, int JB, int IB, bool DS>
+// with the code words of slices n - r, r < RL, held expanded in a window of KWY = RL + P
+// slots (loaded P steps ahead); gr rotates through KWA slots (KWA - 1 steps ahead). The
+// chunk's sums go to the partial of its first 32 rows (the partials are per 32-row chunk, as
+// the dense kernel's; lag_finish reads the even ones for these columns).
+template <int RL, int JB, int IB, bool DS, int KWA = 2, int P = 2>
 __device__ __forceinline__ void lag_win_sp_body(const LagBf16& p, int i0, int j0, int bc, int rt,
                                                 float (*tw)[65], float (*td)[65], float (*ts)[65]) {
-    constexpr int KWA = 2, P = 2, KWY = RL + P;
+    constexpr int KWY = RL + P;
     static_assert(JB * IB == 4 && KWY % KWA == 0 && KWY % P == 0, "wave shape / window slots");
     const int N = p.N, Np = p.Np, T = p.T, NC = p.Bp / 64;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -680,13 +680,15 @@ __device__ __forceinline__ void lag_win_sp_body(const LagBf16& p, int i0, int j0
                 for (int jb = 0; jb < JB; ++jb)
                     raw[sl][jb] = lw_buffer_load_u32(rcd, (int)(vc + (uint32_t)jb * 64 + (uint32_t)sl * cslice), 0, 0);
 #pragma unroll
-            for (int ib = 0; ib < IB; ++ib) {
-                bh[0][ib] = load_b(rhi, va + (uint32_t)ib * 256 + (uint32_t)q0 * gslice);
-                bm[0][ib] = load_b(rmd, va + (uint32_t)ib * 256 + (uint32_t)q0 * gslice);
-            }
+            for (int sl = 0; sl < KWA - 1; ++sl)
+#pragma unroll
+                for (int ib = 0; ib < IB; ++ib) {
+                    bh[sl][ib] = load_b(rhi, va + (uint32_t)ib * 256 + (uint32_t)(q0 + sl) * gslice);
+                    bm[sl][ib] = load_b(rmd, va + (uint32_t)ib * 256 + (uint32_t)(q0 + sl) * gslice);
+                }
             const int nsteps = T - q0;
             uint32_t oy = vc + (uint32_t)P * cslice;                 // code slice n + P
-            uint32_t oa = va + (uint32_t)(q0 + KWA - 1) * gslice;    // gr slice q0 + n + 1
+            uint32_t oa = va + (uint32_t)(q0 + KWA - 1) * gslice;    // gr slice q0 + n + KWA - 1
             for (int n0 = 0; n0 < nsteps; n0 += KWY) {
 #pragma unroll
                 for (int u = 0; u < KWY; ++u) {
@@ -702,8 +704,8 @@ __device__ __forceinline__ void lag_win_sp_body(const LagBf16& p, int i0, int j0
                         raw[u % P][jb] = lw_buffer_load_u32(rcd, (int)(oy + (uint32_t)jb * 64), 0, 0);
 #pragma unroll
                     for (int ib = 0; ib < IB; ++ib) {
-                        bh[(u + 1) % KWA][ib] = load_b(rhi, oa + (uint32_t)ib * 256);
-                        bm[(u + 1) % KWA][ib] = load_b(rmd, oa + (uint32_t)ib * 256);
+                        bh[(u + KWA - 1) % KWA][ib] = load_b(rhi, oa + (uint32_t)ib * 256);
+                        bm[(u + KWA - 1) % KWA][ib] = load_b(rmd, oa + (uint32_t)ib * 256);
                     }
                     oy += cslice;
                     oa += gslice;
@@ -805,8 +807,10 @@ __global__ void __launch_bounds__(256) lag_win_sp_kernel(LagBf16 p) {
     if (RL == 6 && rt > 6 && rt <= 10) return;
     if (RL == 8 && (rt <= 6 || rt > 8)) return;
     if (RL == 10 && (rt <= 8 || rt > 10)) return;
+    // 6-lag passes: 2 x 2 waves with gr two steps ahead (three slots); 4 x 1 waves with one
+    // step ahead, a fifth of the L1 traffic for the B operand, measured 5 % slower (C5)
     if constexpr (RL == 6)
-        lag_win_sp_body<RL, 4, 1, DS>(p, i0, j0, bc, rt, tw, td, ts);
+        lag_win_sp_body<RL, 2, 2, DS, 3, 3>(p, i0, j0, bc, rt, tw, td, ts);
     else
         lag_win_sp_body<RL, 2, 2, DS>(p, i0, j0, bc, rt, tw, td, ts);
 }
