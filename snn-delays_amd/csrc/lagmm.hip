@@ -416,8 +416,9 @@ __global__ void __launch_bounds__(256) lag_win_kernel(LagBf16 p) {
     if (RL == 10 && (rt <= 8 || rt > 10)) return;
     if (RL == 12 && rt <= 10) return;
     // gr-slice registers: 3 slots (2 slices ahead) beside a 12-slot spike window (6-, 8- and
-    // 10-lag passes), 4 slots (3 ahead) beside the 16-slot one (12-lag passes)
-    lag_win_body<RL, RL <= 10 ? 12 : 16, RL <= 10 ? 3 : 4, DS, NP>(p, i0, j0, bc, rt);
+    // 10-lag passes) or a 15-slot one (12-lag passes; a 16-slot window with 4 gr slots left
+    // more spilled registers in the step loop: 11.5 against 8.9 ms at T250 B256 N1024 sigma 4)
+    lag_win_body<RL, RL <= 10 ? 12 : 15, 3, DS, NP>(p, i0, j0, bc, rt);
 }
 
 // ---------------------------------------------------------------------------------------
