@@ -334,6 +334,7 @@ bool syn_hybstep(int T, int B, int N, int L, bool hybrid, int off_count, int tap
 struct ArriveShape {
     bool ok;
     int npt, block, kf, R, RP, hw;
+    int pitch;   // packed words per source row: npt * block, one per lane column
     int sh;   // the packed offset field's shift: log2 of a slot's bytes where R slots are 2^16 bytes, else 0
     size_t lds;
 };
@@ -344,6 +345,7 @@ ArriveShape syn_arrive(int N, int L, bool hybrid, bool bf16, int off_count, int 
     if (N > 2048) return a;
     a.npt = N <= 1024 ? 1 : 2;
     a.block = a.npt == 1 ? (N + 63) / 64 * 64 : 1024;
+    a.pitch = a.npt * a.block;
     a.kf = taps <= 2 ? 2 : 4;
     a.R = 1;   // D + KF - 1 slots, rounded up to a power of two (the kernel wraps by a mask)
     while (a.R < off_count + a.kf - 1) a.R *= 2;
@@ -392,7 +394,7 @@ template <class C>
 void syn_fwd_ws(C& c, int T, int B, int N, int L, bool hybrid, bool bf16, int taps, int offc, bool lags_ok) {
     const ArriveShape ar = syn_arrive(N, L, hybrid, bf16, offc, taps, lags_ok);
     if (ar.ok) {
-        c.template take<uint32_t>((size_t)N * N);   // packed W^T | offsets^T
+        c.template take<uint32_t>((size_t)N * ar.pitch);   // packed W^T | offsets^T
         c.template take<int>((size_t)N);            // first lag per source
         c.template take<float>((size_t)ar.kf * N);  // tap weights per source
         return;
@@ -986,12 +988,12 @@ int syn_fwd_hybstep(const delrec_syn_fwd_args* a, int KF, hipStream_t s) {
 int syn_fwd_arrive(const delrec_syn_fwd_args* a, const ArriveShape& ar, hipStream_t s) {
     const int N = a->N;
     Carver cv(a->workspace, a->workspace_bytes);
-    uint32_t* wpk = cv.take<uint32_t>((size_t)N * N);
+    uint32_t* wpk = cv.take<uint32_t>((size_t)N * ar.pitch);
     int* lof = cv.take<int>((size_t)N);
     float* h = cv.take<float>((size_t)ar.kf * N);
     if (!wpk || !lof || !h) return DELREC_ERR_WORKSPACE;
     launch_pack_hybrid(static_cast<const uint16_t*>(a->W), a->offsets, N, wpk, s, a->off_min, ar.sh,
-                       a->off_count);
+                       a->off_count, ar.pitch);
     HybTaps tp{};   // kf rows: a run shorter than kf gets taps of weight 0 past its triangle
     tp.N = N; tp.KF = ar.kf; tp.omin = a->off_min; tp.s = a->s_uniform; tp.base = a->base; tp.lof = lof; tp.h = h;
     launch_hyb_taps(tp, s);

@@ -593,8 +593,11 @@ __global__ void __launch_bounds__(256) hyb_near_pack_kernel(HybPack p, uint32_t*
 // bf16(W) << 16 | (offset - smallest offset) in the low half word (one 4-byte load), the
 // slot, and KF read-modify-writes w * h_j(lof_j + f) of the run. Where the R slots are
 // exactly 2^16 bytes (C3: 16 x 4 KB, C5: 8 x 8 KB) the low half holds the offset times the
-// slot bytes, so a 16-bit add of (t mod R) * slot bytes wraps the slot by itself and one add
-// places the receiver: two VALU instead of three (offset byte-add, mask, scale-add).
+// slot bytes plus the receiver's column bytes, so a 16-bit add of (t mod R) * slot bytes
+// wraps the slot by itself and is the run's LDS address: one VALU instead of three (offset
+// byte-add, mask, scale-add) -- ten VALU per arrival and wave at two receivers per lane.
+// The packed rows have one word per lane column (NPT * block), so every lane reads a word of
+// its own column, weight 0 past N.
 //
 // Per step: every wave walks the arrival list of step t (flattened from per-wave segments,
 // sources in a fixed order) over its own receivers, 64 arrivals at a time: lane a of the
@@ -607,6 +610,7 @@ __global__ void __launch_bounds__(256) hyb_near_pack_kernel(HybPack p, uint32_t*
 // source's spike into its history word and appends the sources arriving at t + 1 to its
 // wave's segment of the other list buffer; one LDS barrier per step.
 constexpr int kArriveWaves = 16;   // list segments per buffer (a 1024-lane block)
+typedef __attribute__((address_space(3))) char lds_char;
 
 template <int NPT, int KF, int HW, int CH, bool WS>
 __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
@@ -623,6 +627,19 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
     const size_t BN = (size_t)B * N;
     const Lif k = p.lif;
 
+    if constexpr (WS) {
+        // the packed offset fields are absolute LDS byte addresses: the ring must start at LDS
+        // address 0 (no static LDS in this kernel, so the dynamic array does); otherwise every
+        // output of the row is NaN
+        if ((uint32_t)(size_t)(lds_char*)ring != 0u) {
+            for (size_t q = tid; q < (size_t)T * N; q += BS) {
+                const size_t t = q / N, i = q - t * N;
+                p.u[t * BN + (size_t)b * N + i] = __builtin_nanf("");
+                p.y[t * BN + (size_t)b * N + i] = __builtin_nanf("");
+            }
+            return;
+        }
+    }
     for (int q = tid; q < RP * NR; q += BS) ring[q] = 0.0f;
     if (tid < 2 * kArriveWaves) cnt[tid] = 0;    // nothing arrives at step 0; absent waves stay 0
 
@@ -644,12 +661,13 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
         for (int w = 0; w < HW; ++w) hist[c][w] = 0ull;
         word[c] = 0u;
     }
-    // one descriptor for the packed connections; source o's words start o * N in, a lane
-    // past N reads beyond the matrix (0: weight 0, no contribution)
-    const i32x4 rw = buffer_rsrc(p.wpk, (uint32_t)((size_t)N * N * 4u));
+    // one descriptor for the packed connections; source o's words start o * NPT * BS in, one
+    // per lane column (the columns past N hold weight 0 in their own ring column)
+    const int pitch = NPT * BS;
+    const i32x4 rw = buffer_rsrc(p.wpk, (uint32_t)((size_t)N * pitch * 4u));
     int wio[NPT];
 #pragma unroll
-    for (int c = 0; c < NPT; ++c) wio[c] = act[c] ? idx[c] * 4 : 0x40000000;
+    for (int c = 0; c < NPT; ++c) wio[c] = idx[c] * 4;
     __syncthreads();
 
     int tm = 0;   // t mod R
@@ -661,6 +679,7 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
 
         // ---- scatter of the sources arriving at t
         const int bsel = t & 1;
+        const uint32_t tmsh = (uint32_t)tm << SH;   // this step's slot bytes (WS)
         int cw[kArriveWaves];
         {
             const int4* c4 = reinterpret_cast<const int4*>(cnt + bsel * kArriveWaves);
@@ -703,7 +722,7 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
                     const int o = __builtin_amdgcn_readlane(src, (f + e) & 63);
 #pragma unroll
                     for (int c = 0; c < NPT; ++c)
-                        wb[e][c] = __float_as_uint(raw_buffer_load_f32(rw, wio[c], o * N * 4, 0));
+                        wb[e][c] = __float_as_uint(raw_buffer_load_f32(rw, wio[c], o * pitch * 4, 0));
                 }
             };
             // two word buffers in turn: chunk f0's words in one while the next chunk's load
@@ -728,14 +747,19 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
                         // the offset byte holds offset - smallest offset, in [0, D) for the
                         // offsets the caller describes; R is a power of two, so the slot wraps
                         // by a mask (one byte-add and one AND), and a byte outside that range
-                        // still lands in the ring. A lane past N reads the word 0: weight 0
-                        // into its own column
+                        // still lands in the ring. A column past N holds weight 0 (its own
+                        // ring column)
                         wf[c] = __uint_as_float(wv & 0xFFFF0000u);
                         if constexpr (WS) {
-                            // the field is the offset's slot bytes and R slots are 2^16 bytes:
-                            // a 16-bit add wraps the slot, one add places the receiver
-                            const uint32_t ab = (uint16_t)((uint16_t)wv + (uint16_t)(tm << SH));
-                            run[c] = reinterpret_cast<float*>(reinterpret_cast<char*>(ring + idx[c]) + ab);
+                            // the field is the offset's slot bytes plus the receiver's column
+                            // bytes and R slots are 2^16 bytes: one 16-bit add of the step's
+                            // slot bytes wraps the slot and is the byte address in the ring
+                            // (one SDWA add whose 16-bit result is zero-extended: the
+                            // compiler's form is an add and a mask)
+                            uint32_t ab;
+                            asm("v_add_u32_sdwa %0, %1, %2 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+                                : "=v"(ab) : "v"(wv), "v"(tmsh));
+                            run[c] = (float*)(lds_char*)(size_t)ab;
                         } else {
                             const int sl = (tm + (int)(wv & 0xFFu)) & (R - 1);
                             run[c] = ring + sl * NR + idx[c];
@@ -808,9 +832,9 @@ __global__ void __launch_bounds__(1024, NPT) hyb_fwd_arrive_kernel(HybScat p) {
     }
 }
 
-// wpk[o * N + i] = bf16 bits of W[i, o] << 16 | uint8(offset[i, o] - smallest offset) << a.sh
-// (launch_pack_hybrid with the smallest offset and a.sh: the slot bytes' log2 where R slots
-// of them are 2^16 bytes, else 0)
+// wpk[o * npt * block + i] = bf16 bits of W[i, o] << 16 | the offset field (launch_pack_hybrid
+// with the smallest offset, a.sh: the slot bytes' log2 where R slots of them are 2^16 bytes,
+// else 0, and the pitch npt * block)
 bool launch_hyb_fwd_arrive(const HybScat& a, int npt, int hw, int block, size_t lds, hipStream_t stream) {
 #define DELREC_ARRIVE_WS(NPTV, KFV, HWV, WSV)                                                     \
     if (npt == NPTV && a.KF <= KFV && hw == HWV && (a.sh > 0) == WSV) {                          \

@@ -481,8 +481,10 @@ void launch_syn_fwd(const SynFwd& a, int block, size_t lds, hipStream_t stream);
 // `blocks` workgroups; returns the flops one launch issues. sink: blocks * 512 floats.
 int peak_mfma_blocks(int cus);
 double launch_peak_mfma(int kind, int iters, float* sink, int blocks, hipStream_t stream);
+// wpk[o * pitch + i]: bf16 W[i, o] << 16 | the offset's low field (see pack_hybrid_kernel);
+// pitch >= N (0: N), columns N .. pitch-1 weight 0
 void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream,
-                        int omin = 0, int sh = 0, int D = 0);
+                        int omin = 0, int sh = 0, int D = 0, int pitch = 0);
 // event-driven forward, ring in LDS, one receiver per lane, kf >= ceil(2 s_max) taps
 bool launch_syn_fwd_scatter(const SynFwd& a, int kf, int block, size_t lds, hipStream_t stream);
 bool launch_syn_bwd(const SynBwd& a, int block, size_t lds, hipStream_t stream);

@@ -381,39 +381,45 @@ __global__ void __launch_bounds__(1024) syn_fwd_scatter(SynFwd p) {
     }
 }
 
-// wpk[o*N + i] = W[i*N + o] << 16 | uint8(off[i*N + o] - omin) << sh (the low 16 bits)
-// through 32 x 32 LDS tiles. With D > 0 the offsets must lie in [omin, omin + D) (the ring
-// the arrival forward sizes from the caller's range): a connection outside it would land in
-// another slot, so it is packed as a NaN weight at offset 0 instead (its receiver's outputs
-// become NaN as soon as its source fires).
+// wpk[o * pitch + i] = W[i*N + o] << 16 | a low half from off[i*N + o] - omin, through 32 x 32
+// LDS tiles. The low half: with sh = 0, offset - omin in the low byte; with sh > 0 (the
+// arrival forward, whose R ring slots are exactly 2^16 bytes of 2^sh each), (offset - omin) <<
+// sh plus the receiver's column bytes i * 4 (< 2^sh), so that a 16-bit add of the step's slot
+// bytes gives the connection's LDS byte address in the ring (at LDS address 0) directly. With
+// D > 0 the offsets must lie in [omin, omin + D) (the ring the arrival forward sizes from the
+// caller's range): a connection outside it would land in another slot, so it is packed as a
+// NaN weight at offset 0 instead (its receiver's outputs become NaN as soon as its source
+// fires). The columns past N (up to pitch) weight 0, in their own ring column.
 __global__ void __launch_bounds__(256) pack_hybrid_kernel(const uint16_t* __restrict__ W,
-                                                          const int8_t* __restrict__ off, int N, int omin,
-                                                          int sh, int D, uint32_t* __restrict__ wpk) {
+                                                         const int8_t* __restrict__ off, int N, int omin,
+                                                         int sh, int D, int pitch, uint32_t* __restrict__ wpk) {
     __shared__ uint32_t tile[32][33];
     const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
     for (int r = threadIdx.y; r < 32; r += 8) {
         const int i = by + r, o = bx + threadIdx.x;
-        uint32_t v = 0;
+        const uint32_t col = sh > 0 ? (uint32_t)i * 4u : 0u;
+        uint32_t v = col;
         if (i < N && o < N) {
             const int e = (int)off[(size_t)i * N + o] - omin;
             if (D > 0 && (e < 0 || e >= D))
-                v = 0x7FC00000u;
+                v = 0x7FC00000u | col;
             else
-                v = ((uint32_t)W[(size_t)i * N + o] << 16) | (((uint32_t)(uint8_t)e << sh) & 0xFFFFu);
+                v = ((uint32_t)W[(size_t)i * N + o] << 16) | ((((uint32_t)(uint8_t)e << sh) + col) & 0xFFFFu);
         }
         tile[r][threadIdx.x] = v;
     }
     __syncthreads();
     for (int r = threadIdx.y; r < 32; r += 8) {
         const int o = bx + r, i = by + threadIdx.x;
-        if (i < N && o < N) wpk[(size_t)o * N + i] = tile[threadIdx.x][r];
+        if (i < pitch && o < N) wpk[(size_t)o * pitch + i] = tile[threadIdx.x][r];
     }
 }
 
 void launch_pack_hybrid(const uint16_t* W, const int8_t* off, int N, uint32_t* wpk, hipStream_t stream, int omin,
-                        int sh, int D) {
-    const dim3 grid((N + 31) / 32, (N + 31) / 32), block(32, 8);
-    hipLaunchKernelGGL(pack_hybrid_kernel, grid, block, 0, stream, W, off, N, omin, sh, D, wpk);
+                        int sh, int D, int pitch) {
+    if (pitch < N) pitch = N;
+    const dim3 grid((N + 31) / 32, (pitch + 31) / 32), block(32, 8);
+    hipLaunchKernelGGL(pack_hybrid_kernel, grid, block, 0, stream, W, off, N, omin, sh, D, pitch, wpk);
 }
 
 // Forward in gather form, for rings too large for LDS: lane i owns receiver i and sums
