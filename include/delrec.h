@@ -297,12 +297,20 @@ int delrec_axonal_bwd(const delrec_axonal_bwd_args* a, void* stream);
  * GPU (other streams, other threads) race and must not be issued. Allocates nothing. */
 int delrec_axonal_bwd_noalloc(const delrec_axonal_bwd_args* a, void* stream);
 int delrec_syn_fwd(const delrec_syn_fwd_args* a, void* stream);
-/* The hybrid's offset-stacked backward (off_count > 0, rings beyond LDS) reads each source's
- * first lag back to the host once per call to split the sources: that call synchronises the
- * stream before it launches its scan. Every other path is fully asynchronous. */
+/* The hybrid's offset-stacked backward (off_count > 0, rings beyond LDS) splits the sources
+ * by first lag: without the caller's counts (near_known == 0) it reads the first lags back
+ * to the host once per call, which synchronises the stream before it launches its scan.
+ * Every other path is fully asynchronous. */
 int delrec_syn_bwd(const delrec_syn_bwd_args* a, void* stream);
 int delrec_spike_linear_fwd(const delrec_spike_linear_args* a, void* stream);
 int delrec_spike_linear_dw(const delrec_spike_linear_dw_args* a, void* stream);
+/* The same Linear's input gradient dy = g W (the reference: the torch.nn.Linear backward, an
+ * fp32 GEMM) as one bf16 GEMM with fp32 accumulation and output: this splits the rows of g
+ * (rows x M fp32, rows = T B) into out (rows x 3M bf16) = [hi | lo | hi], hi = bf16(x), lo =
+ * bf16(x - hi), for the caller to multiply by W stacked [W_hi; W_hi; W_lo] (3M x K), which
+ * sums g_hi W_hi + g_lo W_hi + g_hi W_lo (about 2^-16 relative per product). No counterpart
+ * in the reference. */
+int delrec_spike_linear_dx_split(const float* g, int64_t rows, int32_t M, void* out, void* stream);
 int delrec_readout_ce(const delrec_readout_ce_args* a, void* stream);
 int delrec_lif_fwd(const delrec_lif_fwd_args* a, void* stream);
 int delrec_lif_bwd(const delrec_lif_bwd_args* a, void* stream);

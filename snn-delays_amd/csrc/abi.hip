@@ -1126,6 +1126,12 @@ int delrec_spike_linear_dw(const delrec_spike_linear_dw_args* a, void* stream) {
     return finish_launch();
 }
 
+int delrec_spike_linear_dx_split(const float* g, int64_t rows, int32_t M, void* out, void* stream) {
+    if (!g || !out || rows <= 0 || M <= 0) return DELREC_ERR_ARG;
+    launch_spike_linear_dx_split(g, (size_t)rows, M, static_cast<uint16_t*>(out), static_cast<hipStream_t>(stream));
+    return finish_launch();
+}
+
 int delrec_readout_ce(const delrec_readout_ce_args* a, void* stream) {
     if (!a || a->T <= 0 || a->B <= 0 || a->C <= 0) return DELREC_ERR_ARG;
     if (!a->logits || !a->labels || !a->dlogits || !a->loss) return DELREC_ERR_ARG;

@@ -335,6 +335,8 @@ int spike_order_kp(int K);
 size_t spike_order_ws(int T, int B, int K);
 SpikeOrder spike_order_carve(void* base, int T, int B, int K);
 void launch_spike_order(const uint32_t* bits, int T, int B, int K, const SpikeOrder& o, hipStream_t stream);
+// rows x M fp32 -> rows x 3M bf16 [hi | lo | hi] (the input gradient's split operand)
+void launch_spike_linear_dx_split(const float* g, size_t rows, int M, uint16_t* out, hipStream_t stream);
 void launch_col_order(const int* cnt, int N, int Np, int* perm, int* cls, hipStream_t stream);
 
 struct SpikeLinear {

@@ -195,6 +195,52 @@ __global__ void __launch_bounds__(256) spike_linear_kernel(SpikeLinear p, const 
 // (8 steps of one output per uint4; steps past T are 0), once per call, so the K / 128 input
 // tiles of the weight gradient stage the planes as they are instead of each splitting g
 // again. One thread per (b, word, block, m).
+// The input gradient dy = g W as one bf16 GEMM: each row of g (M fp32) becomes 3M bf16,
+// [hi | lo | hi] with hi = bf16(x) and lo = bf16(x - hi), so that against W stacked as
+// [W_hi; W_hi; W_lo] (3M x K) the product sums g_hi W_hi + g_lo W_hi + g_hi W_lo (about 2^-16
+// relative per product, the missing g_lo W_lo included). One thread per 4 consecutive
+// elements of a row (16-byte loads and 8-byte stores when M is a multiple of 4).
+__global__ void __launch_bounds__(256) spike_linear_dx_split_kernel(const float* __restrict__ g, size_t rows, int M,
+                                                                    uint16_t* __restrict__ out) {
+    const int M4 = (M + 3) / 4;
+    const size_t total = rows * (size_t)M4;
+    const bool vec = (M & 3) == 0;
+    for (size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x; id < total; id += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = id / M4;
+        const int m = (int)(id - r * M4) * 4;
+        const float* src = g + r * M + m;
+        uint16_t* dst = out + r * 3 * (size_t)M + m;
+        if (vec) {
+            const float4 v = *reinterpret_cast<const float4*>(src);
+            const float x[4] = {v.x, v.y, v.z, v.w};
+            uint32_t h[4], l[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h[e] = sl_bf16_rne(x[e]);
+                l[e] = sl_bf16_rne(x[e] - __uint_as_float(h[e] << 16));
+            }
+            const uint2 hv = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            *reinterpret_cast<uint2*>(dst) = hv;
+            *reinterpret_cast<uint2*>(dst + M) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+            *reinterpret_cast<uint2*>(dst + 2 * (size_t)M) = hv;
+        } else {
+            for (int e = 0; e < 4 && m + e < M; ++e) {
+                const float x = src[e];
+                const uint32_t h = sl_bf16_rne(x), l = sl_bf16_rne(x - __uint_as_float(h << 16));
+                dst[e] = (uint16_t)h;
+                dst[M + e] = (uint16_t)l;
+                dst[2 * (size_t)M + e] = (uint16_t)h;
+            }
+        }
+    }
+}
+
+void launch_spike_linear_dx_split(const float* g, size_t rows, int M, uint16_t* out, hipStream_t stream) {
+    const size_t total = rows * (size_t)((M + 3) / 4);
+    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, (size_t)65535 * 8);
+    hipLaunchKernelGGL(spike_linear_dx_split_kernel, dim3(blocks), dim3(256), 0, stream, g, rows, M, out);
+}
+
 __global__ void __launch_bounds__(256) spike_linear_gsplit_kernel(SpikeLinearDw p) {
     const int TW = (p.T + 31) >> 5;
     const size_t total = (size_t)p.B * TW * 4 * p.M;

@@ -36,7 +36,7 @@ EXPORTS = ('delrec_axonal_fwd', 'delrec_axonal_bwd', 'delrec_axonal_bwd_noalloc'
            'delrec_lif_fwd', 'delrec_lif_bwd', 'delrec_delay_grad', 'delrec_query_workspace',
            'delrec_strerror', 'delrec_version', 'delrec_scan_timing', 'delrec_scan_timing_read',
            'delrec_max_post', 'delrec_max_take', 'delrec_peak_mfma', 'delrec_spike_linear_dw',
-           'delrec_readout_ce')
+           'delrec_spike_linear_dx_split', 'delrec_readout_ce')
 
 
 class DelrecError(RuntimeError):
@@ -155,6 +155,8 @@ def load():
     lib.delrec_max_take.argtypes = [ctypes.c_uint32, ctypes.POINTER(c_f32), c_i32]
     lib.delrec_peak_mfma.restype = c_i32
     lib.delrec_peak_mfma.argtypes = [c_i32, c_i32, c_vp, c_size, ctypes.POINTER(ctypes.c_double), c_vp]
+    lib.delrec_spike_linear_dx_split.restype = c_i32
+    lib.delrec_spike_linear_dx_split.argtypes = [c_vp, ctypes.c_int64, c_i32, c_vp, c_vp]
     got = lib.delrec_version().decode()
     if got.split()[1:2] != [ABI_VERSION]:
         raise ImportError(f'{LIB_PATH} reports "{got}"; this binding lays out the argument structs of '
@@ -327,6 +329,12 @@ class PostedMax:
 def delay_grad(C, W, d, sigma, N, Lm, out, stream):
     _check('delrec_delay_grad', load().delrec_delay_grad(ptr(C), ptr(W), ptr(d), float(sigma), N,
                                                          Lm, ptr(out), stream))
+
+
+def spike_linear_dx_split(g2, out, stream):
+    """``out`` (rows, 3M) bf16 = [hi | lo | hi] of ``g2`` (rows, M) fp32."""
+    rows, M = g2.shape
+    _check('delrec_spike_linear_dx_split', load().delrec_spike_linear_dx_split(ptr(g2), rows, M, ptr(out), stream))
 
 
 def version():

@@ -6,7 +6,13 @@ next Linear). Its input is the layer's spike train, so its forward and its weigh
 are binary-activation GEMMs; the recurrent layers' autograd Functions attach their spike
 bits to their output (``attach_bits``), and ``SpikeLinear`` reads those bits instead of the
 fp32 spikes: the forward ``out = y W^T + b`` and the weight gradient ``dW = g^T y`` both run on
-the bits. The input gradient ``dy = g W`` is a plain GEMM (torch), and ``db = sum g``.
+the bits. The input gradient ``dy = g W`` is a plain GEMM: for GEMMs of at least 2^40 flops
+(C5's inter-layer Linear: 4.4 * 10^12) one bf16 GEMM with fp32 output (torch's
+``mm(..., out_dtype=float32)``) over g split into ``[hi | lo | hi]`` by
+``delrec_spike_linear_dx_split`` and W stacked ``[W_hi; W_hi; W_lo]`` (about 2^-16 relative
+per product, within the gradients' rtol 1e-4), where the device's torch offers that GEMM;
+otherwise torch's fp32 GEMM, the reference's own (``DELREC_LINEAR_DX_SPLIT=1`` / ``=0``
+takes the split GEMM at any size / never); ``db = sum g``.
 
 The bits are used only while they still describe the tensor: ``attach_bits`` records the
 tensor's version counter, and an input that was modified in place since (or any other input
@@ -14,6 +20,8 @@ without bits -- an input projection of analog data, a batch-normalised train, a 
 or sizes past the kernels' 32-bit addressing) takes ``torch.nn.functional.linear``, the
 reference's own operation.
 """
+
+import os
 
 import torch
 
@@ -72,12 +80,48 @@ class SpikeLinearFn(torch.autograd.Function):
         g2 = g.reshape(-1, M)
         dx = dW = db = None
         if ctx.needs_input_grad[0]:
-            dx = (g2 @ weight.to(torch.float32)).reshape(T, B, K).to(ctx.x_dtype)
+            dx = input_grad(g2, weight.to(torch.float32)).reshape(T, B, K).to(ctx.x_dtype)
         if ctx.needs_input_grad[1]:
             dW = spike_linear_dw(g, bits, K).to(weight.dtype)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             db = g2.sum(0)
         return dx, dW, db, None
+
+
+_MM_OUT_DTYPE = {}
+
+
+def _mm_out_dtype(device):
+    """Whether torch runs a bf16 x bf16 GEMM with fp32 output on ``device`` (checked once)."""
+    ok = _MM_OUT_DTYPE.get(device)
+    if ok is None:
+        try:
+            a = torch.ones(16, 16, device=device, dtype=torch.bfloat16)
+            ok = torch.mm(a, a, out_dtype=torch.float32).dtype == torch.float32
+        except (RuntimeError, TypeError, NotImplementedError):
+            ok = False
+        _MM_OUT_DTYPE[device] = ok
+    return ok
+
+
+_SPLIT_FLOPS = 1 << 40
+
+
+def input_grad(g2, W):
+    """``dy = g2 W`` (rows, K) for g2 (rows, M) and W (M, K) fp32: at 2^40 flops or more one
+    bf16 GEMM with fp32 accumulation and output over ``[g_hi | g_lo | g_hi]`` and
+    ``[W_hi; W_hi; W_lo]``, else -- or where the device's torch has no fp32-output bf16 GEMM --
+    the fp32 GEMM the reference's ``torch.nn.Linear`` backward runs."""
+    rows, M = g2.shape
+    mode = os.environ.get('DELREC_LINEAR_DX_SPLIT')
+    big = 2 * rows * M * W.shape[1] >= _SPLIT_FLOPS
+    if mode == '0' or (mode != '1' and not big) or not (g2.is_cuda and _mm_out_dtype(g2.device)):
+        return g2 @ W
+    gs = torch.empty(rows, 3 * M, device=g2.device, dtype=torch.bfloat16)
+    _lib.spike_linear_dx_split(g2, gs, _lib.stream_of(g2))
+    w_hi = W.to(torch.bfloat16)
+    w_lo = (W - w_hi.to(torch.float32)).to(torch.bfloat16)
+    return torch.mm(gs, torch.cat([w_hi, w_hi, w_lo], 0), out_dtype=torch.float32)
 
 
 def spike_linear_dw(g, bits, K):

@@ -63,7 +63,7 @@ def test_spike_linear_matches_linear(dev, case):
     torch.cuda.synchronize()
     scale = float(ref.abs().max())
     torch.testing.assert_close(out.detach().cpu().double(), ref, rtol=1e-5, atol=1e-6 * max(scale, 1.0))
-    # the backward (dW on the spike bits, dx a plain GEMM): against float64 autograd
+    # the backward (dW on the spike bits, dx torch's GEMM at these sizes): against float64 autograd
     xr = y.double().requires_grad_(True)
     wr = lin.weight.detach().cpu().double().requires_grad_(True)
     torch.nn.functional.linear(xr, wr).backward(gout.double())
@@ -132,3 +132,54 @@ def test_spike_linear_ignores_bits_of_a_modified_tensor(dev):
     assert 'SpikeLinear' not in type(out.grad_fn).__name__
     torch.testing.assert_close(out.detach().cpu(), torch.nn.functional.linear(2.0 * y, lin.weight.detach().cpu(),
                                                                            lin.bias.detach().cpu()))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('M', [256, 130, 7])
+def test_input_gradient_split_is_exact_bf16_rounding(dev, M):
+    """``delrec_spike_linear_dx_split``: each row of g becomes [hi | lo | hi] with hi the bf16
+    round-to-nearest-even of x and lo that of x - hi -- torch's own bf16 conversion, bit for
+    bit (M a multiple of 4 takes the vector stores, 130 and 7 the element tail)."""
+    from delrec import _lib
+    rows = 1000
+    print(f'rows={rows} M={M}', flush=True)
+    g = (torch.randn(rows, M, generator=gen(5)) * torch.logspace(-30, 30, M, base=2.0)).to(dev)
+    g[0, 0] = 0.0
+    out = torch.empty(rows, 3 * M, device=dev, dtype=torch.bfloat16)
+    _lib.spike_linear_dx_split(g, out, _lib.stream_of(g))
+    torch.cuda.synchronize()
+    hi = g.to(torch.bfloat16)
+    lo = (g - hi.to(torch.float32)).to(torch.bfloat16)
+    assert torch.equal(out[:, :M].view(torch.int16), hi.view(torch.int16))
+    assert torch.equal(out[:, M:2 * M].view(torch.int16), lo.view(torch.int16))
+    assert torch.equal(out[:, 2 * M:].view(torch.int16), hi.view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_input_gradient_takes_the_bf16_split_gemm(dev, monkeypatch):
+    """The Linear's input gradient as the split bf16 GEMM (torch's fp32-output bf16 mm is
+    present on this device; forced here, the GEMM being below the size that takes it by
+    itself) matches float64 at C5's width on 4 x 64 spike rows."""
+    from delrec import _lib, spike_linear
+    assert spike_linear._mm_out_dtype(dev), 'no fp32-output bf16 GEMM: the split path would not run'
+    monkeypatch.setenv('DELREC_LINEAR_DX_SPLIT', '1')   # this GEMM is below the size the split takes
+    calls = []
+    real = _lib.spike_linear_dx_split
+    monkeypatch.setattr(_lib, 'spike_linear_dx_split', lambda *a: (calls.append(1), real(*a))[1])
+    T, B, K, M = 64, 4, 2048, 2048
+    g = gen(17)
+    y = (torch.rand(T, B, K, generator=g) < 0.05).float()
+    lin = spike_linear.SpikeLinear(K, M, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(M, K, generator=g) / K ** 0.5)
+    lin = lin.to(dev)
+    xg = spike_linear.attach_bits(y.to(dev).requires_grad_(True), pack_bits(y).to(dev))
+    gout = torch.randn(T, B, M, generator=g)
+    lin(xg).backward(gout.to(dev))
+    torch.cuda.synchronize()
+    assert calls, 'the input gradient did not take the split GEMM'
+    ref = gout.double().reshape(-1, M) @ lin.weight.detach().cpu().double()
+    got = xg.grad.cpu().double().reshape(-1, K)
+    err = float((got - ref).abs().max())
+    print(f'  max |dx - float64| {err:.3e} (|dx| max {float(ref.abs().max()):.3e})', flush=True)
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-5 * float(ref.abs().max()))
