@@ -209,9 +209,9 @@ def layer_inputs(m):
 def inter_linear_ms(m, ys, reps=5):
     """The Linear between stacked layers on the first layer's spikes, forward and forward +
     backward: the binary-activation GEMMs on its spike bits (forward, and dW = g^T y; dx = g W
-    is a plain GEMM) against torch's fp32 GEMMs on the fp32 spikes (same weights), average ms
-    per call, and the largest differences between the two paths' outputs and weight
-    gradients."""
+    the split bf16 GEMM) against torch's fp32 GEMMs on the fp32 spikes (same weights), average
+    ms per call, and the largest differences between the two paths' outputs, weight gradients
+    and input gradients (with the largest input gradient, for scale)."""
     from delrec.spike_linear import attach_bits, spike_bits
     lin, y = m.inter[0], ys[0]
     bits = spike_bits(y)
@@ -241,12 +241,14 @@ def inter_linear_ms(m, ys, reps=5):
             lin.weight.grad = None
             xi = make()
             lin(xi).backward(gout)
-            return lin.weight.grad
+            return lin.weight.grad, xi.grad
 
-        out[name + '_fwd_bwd'], dw = timed(fwd_bwd)
-        res[name] = (o, dw.clone())
+        out[name + '_fwd_bwd'], (dw, dx) = timed(fwd_bwd)
+        res[name] = (o, dw.clone(), dx)
     out['max_abs_diff'] = float((res['spike_bits_gemm'][0] - res['torch_fp32'][0]).abs().max())
     out['max_abs_diff_dW'] = float((res['spike_bits_gemm'][1] - res['torch_fp32'][1]).abs().max())
+    out['max_abs_diff_dx'] = float((res['spike_bits_gemm'][2] - res['torch_fp32'][2]).abs().max())
+    out['max_abs_dx'] = float(res['torch_fp32'][2].abs().max())
     lin.weight.grad = None
     return out
 
