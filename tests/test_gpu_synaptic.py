@@ -479,6 +479,41 @@ def test_hybrid_wrong_d_min_gives_nan(dev, env, monkeypatch):
         assert bool(u.isnan().any()) and bool(dx.isnan().any())
 
 
+# the same layer handed to the C ABI with an offset range one short of the offsets' own (a
+# caller's out-of-contract off_count): the forward packs each connection at the largest
+# offset as a NaN weight in its receiver's own ring column, so those receivers' membranes
+# turn NaN once the source fires -- never a silently dropped or misplaced connection
+@pytest.mark.gpu
+def test_hybrid_arrival_offsets_past_the_stated_range_give_nan(dev, monkeypatch):
+    from delrec.kernels import synaptic_eventdriven as se
+    monkeypatch.setenv('DELREC_HYB_FWD', '1')
+    real = se.hybrid_form
+    monkeypatch.setattr(se, 'hybrid_form', lambda d_min, s, rng: real(d_min, s, None if rng is None else (rng[0], rng[1] - 1)))
+    T, B, N, K = 20, 3, 96, 4
+    print(f'T={T} B={B} N={N}, offsets 0..{K}, stated {K} offsets', flush=True)
+    g = gen(8)
+    x = torch.randn(T, B, N, generator=g) * 1.5 + 0.5
+    W = (torch.randn(N, N, generator=g) * (1.5 / N ** 0.5)).bfloat16().float()
+    base = 1.0 + torch.rand(N, generator=g) * 6.0
+    offsets = torch.randint(K + 1, (N, N), generator=g).float()
+    seen = {}
+    fwd = se.syn_forward
+
+    def keep(*a, **k):
+        out = fwd(*a, **k)
+        seen['u'] = out[1].detach()
+        return out
+
+    import delrec.kernels.synaptic_hybrid as sh
+    monkeypatch.setattr(sh, 'syn_forward', keep)
+    gy = torch.randn(T, B, N, generator=g)
+    _hybrid_run(dev, T, B, N, W, base, offsets, True, 0.0, x, gy)
+    u = seen['u'].cpu()
+    print(f'  NaN membranes {int(u.isnan().sum())} of {u.numel()}', flush=True)
+    assert bool(u.isnan().any())
+    assert not bool(u[0].isnan().any()), 'no input has arrived at step 0: its membranes are finite'
+
+
 # bases exactly 0 (where training clamps them): the source's first tap sits at lag 0 with
 # weight 0, which the offset-stacked backward reads as a zero-weight tap, not as a tap below
 # lag 1 (its safety net must not fire)
