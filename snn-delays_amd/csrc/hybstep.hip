@@ -588,8 +588,10 @@ __global__ void __launch_bounds__(256) hyb_near_pack_kernel(HybPack p, uint32_t*
 // s = (t + e) mod R with no wrap; the mirror slot R + m is read and cleared with slot m.
 // The ring is slot-major, ring[slot][receiver] with a pitch of NR = NPT * 1024 receivers, so
 // the lanes of a wave always hit 64 distinct banks whatever slot each connection selects, and
-// the taps of a run are immediate offsets of one address. (C5: 9 slots of 2048 receivers,
-// 74 KB, so two rows' workgroups share a CU.) Per connection: the packed word
+// the taps of a run are immediate offsets of one address. (C5: 9 slots of 2048 receivers and
+// the lists, 82 KB, so one row's workgroup per CU: a ring without the mirror slot, 74 KB at
+// 64 VGPRs, ran two per CU at the same speed -- the LDS traffic sets the pace, not the
+// occupancy.) Per connection: the packed word
 // bf16(W) << 16 | (offset - smallest offset) in the low half word (one 4-byte load), the
 // slot, and KF read-modify-writes w * h_j(lof_j + f) of the run. Where the R slots are
 // exactly 2^16 bytes (C3: 16 x 4 KB, C5: 8 x 8 KB) the low half holds the offset times the
