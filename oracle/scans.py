@@ -191,9 +191,9 @@ def synaptic_v1(x, W, d, lif, sigma=0.0, bias=None, drop=None, p_spread=None,
                       lambda y: torch.einsum('bo,io,iol->bil', y, W, mask))
 
 
-def vanilla(x, W, lif, drop=None):
+def vanilla(x, W, lif, drop=None, forced=None):
     """Delay-free recurrent LIF: ``rec[t] = y[t-1] W`` (note the product order of the
-    reference, ``delay_layers_pytorch.py:34``)."""
+    reference, ``delay_layers_pytorch.py:34``). ``forced``: as in ``axonal_v2``."""
     T, B, N = x.shape
     m = _drop(drop, B, N, x)
     v = lif_initial_v(lif, x[0])
@@ -201,19 +201,19 @@ def vanilla(x, W, lif, drop=None):
     prev = torch.zeros(B, N, dtype=x.dtype, device=x.device)
     for t in range(T):
         rec = torch.matmul(prev * m, W)
-        y, h, v = lif_step(lif, x[t] + rec, v)
+        y, h, v = lif_step(lif, x[t] + rec, v, None if forced is None else forced[t])
         prev = y
         ys.append(y)
         us.append(h)
     return torch.stack(ys), {'u': torch.stack(us)}
 
 
-def lif_layer(x, lif):
-    """A plain multi-step LIF layer (no recurrence)."""
+def lif_layer(x, lif, forced=None):
+    """A plain multi-step LIF layer (no recurrence). ``forced``: as in ``axonal_v2``."""
     v = lif_initial_v(lif, x[0])
     ys, us = [], []
     for t in range(x.shape[0]):
-        y, h, v = lif_step(lif, x[t], v)
+        y, h, v = lif_step(lif, x[t], v, None if forced is None else forced[t])
         ys.append(y)
         us.append(h)
     return torch.stack(ys), {'u': torch.stack(us)}

@@ -3,6 +3,7 @@
 import torch
 
 from oracle import neuron as oneuron, scans
+from oracle.delays import axonal_mask, dmask_dd, syn_mask
 
 
 def gen(seed):
@@ -48,9 +49,16 @@ def lif_params(tau=2.0, v_th=1.0, v_reset=0.0, decay_input=False, detach_reset=F
                              detach_reset=detach_reset, surrogate=surrogate)
 
 
+def _cast(t, dtype):
+    return t if t is None or dtype is None else t.detach().cpu().to(dtype)
+
+
 def oracle_axonal(x, W, d, lif, sigma, gy, bias=None, p=None, use_sig_p=False, drop=None,
-                  round_delays=False):
-    """Oracle forward + BPTT. Returns (y, u, grads dict)."""
+                  round_delays=False, dtype=None, forced=None):
+    """Oracle forward + BPTT. Returns (y, u, grads dict). ``dtype``: every tensor cast to it
+    first (float64: the reference the device gradients are held to); ``forced``: the spike
+    train the neurons are teacher-forced with (``oracle.neuron.lif_step``)."""
+    x, W, d, gy, bias, p, drop, forced = (_cast(t, dtype) for t in (x, W, d, gy, bias, p, drop, forced))
     leaves = {'x': x.clone().requires_grad_(True), 'W': W.clone().requires_grad_(True),
               'd': d.clone().requires_grad_(True)}
     if bias is not None:
@@ -59,19 +67,27 @@ def oracle_axonal(x, W, d, lif, sigma, gy, bias=None, p=None, use_sig_p=False, d
         leaves['p'] = p.clone().requires_grad_(True)
     y, ext = scans.axonal_v2(leaves['x'], leaves['W'], leaves['d'], lif, sigma=sigma,
                              bias=leaves.get('bias'), drop=drop, p_spread=leaves.get('p'),
-                             use_sig_p=use_sig_p, round_delays=round_delays)
+                             use_sig_p=use_sig_p, round_delays=round_delays, forced=forced)
     (y * gy).sum().backward()
     return y.detach(), ext['u'].detach(), {k: v.grad for k, v in leaves.items()}
 
 
 def oracle_synaptic(x, W, d, lif, sigma, gy, bias=None, p=None, use_sig_p=False, drop=None,
-                    base=None, offsets=None, round_delays=False):
+                    base=None, offsets=None, round_delays=False, dtype=None, forced=None):
     """Oracle synaptic forward + BPTT. With ``base``/``offsets`` the delay is the hybrid
-    parametrisation and the gradient is reported for ``base``."""
+    parametrisation and the gradient is reported for ``base``. ``dtype`` / ``forced``: as in
+    ``oracle_axonal``; a hybrid delay is the parametrisation's fp32 sum ``base + offsets``
+    in every dtype (exact in float64), its gradient flowing to ``base``."""
+    d32 = None if base is None else base.detach().cpu().float() + 0.0 + 1.0 * offsets.detach().cpu().float()
+    x, W, d, gy, bias, p, drop, base, forced = (_cast(t, dtype)
+                                                for t in (x, W, d, gy, bias, p, drop, base, forced))
     leaves = {'x': x.clone().requires_grad_(True), 'W': W.clone().requires_grad_(True)}
     if base is not None:
         leaves['base'] = base.clone().requires_grad_(True)
-        dd = leaves['base'] + 0.0 + 1.0 * offsets
+        if dtype is None or dtype == torch.float32:
+            dd = leaves['base'] + 0.0 + 1.0 * offsets
+        else:
+            dd = leaves['base'] + (d32.to(dtype) - leaves['base'].detach())
     else:
         leaves['d'] = d.clone().requires_grad_(True)
         dd = leaves['d']
@@ -81,7 +97,7 @@ def oracle_synaptic(x, W, d, lif, sigma, gy, bias=None, p=None, use_sig_p=False,
         leaves['p'] = p.clone().requires_grad_(True)
     y, ext = scans.synaptic_v2(leaves['x'], leaves['W'], dd, lif, sigma=sigma, bias=leaves.get('bias'),
                                drop=drop, p_spread=leaves.get('p'), use_sig_p=use_sig_p,
-                               round_delays=round_delays)
+                               round_delays=round_delays, forced=forced)
     (y * gy).sum().backward()
     return y.detach(), ext['u'].detach(), {k: v.grad for k, v in leaves.items()}
 
@@ -116,7 +132,14 @@ class OracleModel(torch.nn.Module):
 #         future-gradient product and again in the lag correlation behind dW;
 #   EPS = 2^-20 for fp32 W: three bf16 planes (2^-24) plus gr's own deviation from float64
 #         after an fp32 BPTT chain (about 1e-6 relative).
+#   EPS = 2^-15 for the lag- and offset-stacked per-step product scans with fp32 W (taken where
+#         the rings do not fit LDS): as for bf16 W, gr enters their future-gradient products and
+#         the correlation behind dW as hi + lo bf16 planes, hi*hi + hi*lo + lo*hi (about 2^-16
+#         per term each time), and W.h as two planes (2^-17).
+# The same budget bounds a delay gradient's element, dd[i, j] = W[i, j] sum_l dh/dd C_l[i, j]
+# (dbase[j]: the sum over the column's receivers i), from its own terms.
 GRAD_KAPPA = 4.0
+STACKED_EPS = 2.0 ** -15
 
 
 def grad_eps(w_bf16):
@@ -190,3 +213,59 @@ def check_elementwise(name, got, ref64, rtol, atol, ref32=None, term_sq=None, ep
         at = tuple(int(i) for i in torch.unravel_index(torch.tensor(worst), ref.shape))
         raise AssertionError(f'{name}: {still} of {err.numel()} elements differ; at {at}: got '
                              f'{float(got.reshape(-1)[worst]):.6e} ref {float(ref.reshape(-1)[worst]):.6e}')
+
+
+def grads64(run, leaves, gy, forced):
+    """The oracle's gradients in float64 on the fp32 leaves' values, teacher-forced with the
+    device's spike train ``forced``: ``run(l, forced)`` is the oracle forward on the leaves
+    ``l`` (name -> float64 tensor) returning y. Returns name -> gradient."""
+    l64 = {k: v.detach().cpu().double().requires_grad_(True) for k, v in leaves.items()}
+    y = run(l64, forced.detach().cpu().double())
+    (y * gy.detach().cpu().double()).sum().backward()
+    return {k: v.grad for k, v in l64.items()}
+
+
+def check_grads(got, g64, g32, rtol, atol=1e-5, budget=None, eps=None):
+    """Each device gradient in ``got`` (name -> tensor) against the float64 oracle's
+    (``g64``) at the fixed, unscaled ``rtol`` / ``atol``. An element that misses them gets the
+    floor of ``check_elementwise``: the fp32 oracle's (``g32``) own distance from float64 at
+    that element and, for a name in ``budget`` (name -> ``term_sq`` callable), the rounding
+    budget of that element's own terms at ``eps`` per term."""
+    budget = budget or {}
+    for k, v in got.items():
+        check_elementwise('d' + k, v, g64[k], rtol, atol, ref32=lambda k=k: g32[k],
+                          term_sq=budget.get(k), eps=eps)
+
+
+def syn_budget(gr, y, d, sigma, W=None, drop=None, hybrid=False):
+    """``term_sq`` callables of a synaptic / hybrid run with one uniform spread: 'W' always and,
+    with ``W`` given, the delay gradient -- 'd' per connection, or 'base' (``hybrid``) per
+    source. ``gr``: the float64 oracle's dx; ``y``: the spike train; ``d``: the (N, N) delays;
+    ``drop``: the (B, N) dropout multiplier the recurrent input is scaled by."""
+    gr = gr.detach().cpu().double()
+    if drop is not None:
+        gr = gr * drop.detach().cpu().double()[None]
+    y = y.detach().cpu()
+    d = d.detach().cpu().float()
+    h, L = syn_mask(d, sigma)
+    out = {'W': lambda idx: dw_term_sq_synaptic(gr, y, h, idx)}
+    if W is not None:
+        dh = dmask_dd(d.double(), sigma, L)
+        g2, yy, T = gr ** 2, y.double(), y.shape[0]
+        qd = torch.zeros(d.shape, dtype=torch.float64)
+        for l in range(1, min(L, T)):
+            qd += dh[:, :, l] ** 2 * torch.einsum('tbi,tbj->ij', g2[l:], yy[:T - l])
+        qd *= W.detach().cpu().double() ** 2
+        if hybrid:
+            qb = qd.sum(0)
+            out['base'] = lambda idx: qb[idx[0]]
+        else:
+            out['d'] = lambda idx: qd[idx]
+    return out
+
+
+def axonal_budget(gr, y, d, sigma):
+    """``term_sq`` of an axonal dW (no dropout, one spread); ``d`` the (N,) delays."""
+    h, _ = axonal_mask(d.detach().cpu().float(), sigma)
+    y = y.detach().cpu()
+    return {'W': lambda idx: dw_term_sq_axonal(gr, y, h, idx)}

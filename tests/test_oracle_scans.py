@@ -382,7 +382,7 @@ def test_plain_lif_layer_is_the_recurrent_scan_without_weights():
     torch.testing.assert_close(e0['u'], e1['u'], rtol=0, atol=0)
 
 
-@pytest.mark.parametrize('kind', ['axonal', 'synaptic', 'hybrid'])
+@pytest.mark.parametrize('kind', ['axonal', 'synaptic', 'hybrid', 'vanilla', 'lif'])
 @pytest.mark.parametrize('soft', [False, True])
 def test_teacher_forcing_with_own_spikes_reproduces_the_free_run(kind, soft):
     """Every GPU parity test at a workload shape runs the oracle forced with the kernel's
@@ -407,6 +407,12 @@ def test_teacher_forcing_with_own_spikes_reproduces_the_free_run(kind, soft):
               'd': d.clone().requires_grad_(True)}
         if kind == 'axonal':
             y, ext = scans.axonal_v2(lv['x'], lv['W'], lv['d'], lif, sigma=0.6, forced=forced)
+        elif kind == 'vanilla':
+            y, ext = scans.vanilla(lv['x'], lv['W'], lif, forced=forced)
+            y = y + 0.0 * lv['d'].sum()
+        elif kind == 'lif':
+            y, ext = scans.lif_layer(lv['x'], lif, forced=forced)
+            y = y + 0.0 * (lv['W'].sum() + lv['d'].sum())
         elif kind == 'synaptic':
             y, ext = scans.synaptic_v2(lv['x'], lv['W'], lv['d'], lif, sigma=0.6, forced=forced)
         else:
