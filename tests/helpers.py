@@ -269,3 +269,15 @@ def axonal_budget(gr, y, d, sigma):
     h, _ = axonal_mask(d.detach().cpu().float(), sigma)
     y = y.detach().cpu()
     return {'W': lambda idx: dw_term_sq_axonal(gr, y, h, idx)}
+
+
+def gemm_term_sq(A, B):
+    """``term_sq`` of a product C = A @ B: Q[i, j] = sum_k (A[i, k] B[k, j])^2 for the pairs
+    ``idx``, in chunks of 256 pairs."""
+    A2, B2 = A.detach().cpu().double() ** 2, B.detach().cpu().double() ** 2
+
+    def q(idx):
+        ii, jj = idx
+        return torch.cat([(A2[ii[s:s + 256]] * B2[:, jj[s:s + 256]].t()).sum(1)
+                          for s in range(0, ii.numel(), 256)])
+    return q

@@ -2,8 +2,10 @@
 ``delrec_spike_linear_dw`` through ``delrec.spike_linear.SpikeLinear``) against
 ``torch.nn.functional.linear`` and its autograd in float64 on the same spikes and weights.
 The spikes are exact; W (forward) and g (weight gradient) enter as bf16 hi + mid + lo (about
-2^-25 relative), so the tolerance is fp32's: rtol 1e-5, atol 1e-6 relative to the output's
-magnitude. Shapes cover T, K and M off their tile multiples (128 steps, 32
+2^-25 relative), so the tolerance is fp32's: rtol 1e-5, atol 1e-6, unscaled (gradients rtol
+1e-4, atol 1e-5), where an element whose terms cancel gets the fp32 accumulation budget of its
+own terms, 4 * 2^-20 * sqrt(sum of its squared terms) (``helpers.check_elementwise``; 2^-16
+per term for the split bf16 input gradient). Shapes cover T, K and M off their tile multiples (128 steps, 32
 neurons, 128 outputs), with and without bias, inputs mostly or wholly silent (the kernels take
 the input neurons in activity order and skip the silent ones), and the bits attached by a
 recurrent layer.
@@ -13,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import gen
+from helpers import check_elementwise, gemm_term_sq, gen, grad_eps
 
 
 def pack_bits(y):
@@ -61,14 +63,19 @@ def test_spike_linear_matches_linear(dev, case):
     gout = torch.randn(T, B, M, generator=g)
     out.backward(gout.to(dev))
     torch.cuda.synchronize()
-    scale = float(ref.abs().max())
-    torch.testing.assert_close(out.detach().cpu().double(), ref, rtol=1e-5, atol=1e-6 * max(scale, 1.0))
+    # unscaled tolerances; an element whose terms cancel gets the fp32 accumulation budget of
+    # its own terms (4 * 2^-20 * sqrt(sum of its squared terms), helpers.check_elementwise)
+    y2, w64, g2 = y.reshape(-1, K), lin.weight.detach().cpu().double(), gout.reshape(-1, M)
+    check_elementwise('out', out.detach().reshape(-1, M), ref.reshape(-1, M), 1e-5, 1e-6,
+                      term_sq=gemm_term_sq(y2, w64.t()), eps=grad_eps(False))
     # the backward (dW on the spike bits, dx torch's GEMM at these sizes): against float64 autograd
     xr = y.double().requires_grad_(True)
     wr = lin.weight.detach().cpu().double().requires_grad_(True)
     torch.nn.functional.linear(xr, wr).backward(gout.double())
-    torch.testing.assert_close(xg.grad.cpu().double(), xr.grad, rtol=1e-4, atol=1e-5 * float(xr.grad.abs().max()))
-    torch.testing.assert_close(lin.weight.grad.cpu().double(), wr.grad, rtol=1e-4, atol=1e-5 * float(wr.grad.abs().max()))
+    check_elementwise('dx', xg.grad.reshape(-1, K), xr.grad.reshape(-1, K), 1e-4, 1e-5,
+                      term_sq=gemm_term_sq(g2, w64), eps=grad_eps(False))
+    check_elementwise('dW', lin.weight.grad, wr.grad, 1e-4, 1e-5, term_sq=gemm_term_sq(g2.t(), y2),
+                      eps=grad_eps(False))
 
 
 @pytest.mark.gpu
@@ -90,7 +97,9 @@ def test_recurrent_layer_output_feeds_the_spike_gemm(dev):
         ref = torch.nn.functional.linear(y.double(), lin.weight.double(), lin.bias.double())
     torch.cuda.synchronize()
     assert float(y.mean()) > 0
-    torch.testing.assert_close(out.double(), ref, rtol=1e-5, atol=1e-6 * max(float(ref.abs().max()), 1.0))
+    N = w['N']
+    check_elementwise('out', out.reshape(-1, 96), ref.reshape(-1, 96), 1e-5, 1e-6,
+                      term_sq=gemm_term_sq(y.reshape(-1, N), lin.weight.detach().t()), eps=grad_eps(False))
 
 
 @pytest.mark.gpu
@@ -110,9 +119,10 @@ def test_spike_linear_weight_gradient_at_the_c5_width(dev, shape):
     ref = gout.reshape(-1, M).double().t() @ y.reshape(-1, K).double()
     err = (dW.cpu().double() - ref).abs()
     print(f'  dW max abs err {float(err.max()):.3e}, |ref|max {float(ref.abs().max()):.3e}', flush=True)
-    # fp32 accumulation of about 600 O(1) terms per entry: the fp32 bound, relative to the
-    # largest entry as in the tests above
-    torch.testing.assert_close(dW.cpu().double(), ref, rtol=1e-5, atol=1e-5 * float(ref.abs().max()))
+    # fp32 accumulation of about 600 O(1) terms per entry: rtol 1e-5, atol 1e-5 unscaled; an
+    # entry whose terms cancel gets the fp32 accumulation budget of its own terms
+    check_elementwise('dW', dW, ref, 1e-5, 1e-5, term_sq=gemm_term_sq(gout.reshape(-1, M).t(), y.reshape(-1, K)),
+                      eps=grad_eps(False))
 
 
 @pytest.mark.gpu
@@ -182,4 +192,6 @@ def test_input_gradient_takes_the_bf16_split_gemm(dev, monkeypatch):
     got = xg.grad.cpu().double().reshape(-1, K)
     err = float((got - ref).abs().max())
     print(f'  max |dx - float64| {err:.3e} (|dx| max {float(ref.abs().max()):.3e})', flush=True)
-    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-5 * float(ref.abs().max()))
+    # three bf16 products of the split operands: about 2^-16 per term
+    check_elementwise('dx', got, ref, 1e-4, 1e-5, term_sq=gemm_term_sq(gout.reshape(-1, M), lin.weight.detach()),
+                      eps=2.0 ** -16)
