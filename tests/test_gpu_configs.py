@@ -4,7 +4,8 @@ the product modules the benchmark times, against the CPU oracle.
 C1 and C2 run whole. C3, C4 and C5 keep the workload's N, delays, half-width and W dtype
 (so the dispatcher picks the kernels the benchmark times) and shorten the run: T long
 enough for the longest delays to arrive; C4 keeps B = 256 (its GEMM splits follow B), C5
-takes 32 batch rows (its kernels are per row or tile the batch).
+takes 32 batch rows (its kernels are per row or tile the batch). Each shape runs its step
+twice, and the second must reproduce the first bit for bit (spikes, membrane, every gradient).
 
 The oracle runs teacher-forced with the kernel's spike train (``oracle.neuron.lif_step``):
 it then follows the kernel's trajectory exactly, so every spike of every step can be
@@ -83,6 +84,25 @@ def test_workload_shape_matches_oracle(dev, case, monkeypatch):
     y_hip = y.detach().cpu()
     assert bool(((y_hip == 0) | (y_hip == 1)).all()), 'spikes are not 0/1'
     print(f'  firing rate {float(y_hip.mean()):.4f}', flush=True)
+
+    # the same step once more: spikes, membrane and every gradient bit-identical (the kernels
+    # add their partial sums in a fixed order; no atomics on the values)
+    first = {n: q.grad.detach().clone() for n, q in layer.named_parameters() if q.grad is not None}
+    first['x'], u1 = xg.grad.detach().clone(), seen.get('u')
+    u1 = None if u1 is None else u1.clone()
+    xg2 = x.detach().clone().requires_grad_(True)
+    layer.zero_grad(set_to_none=True)
+    y2 = layer(xg2)
+    (y2 * gy.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    again = {n: q.grad for n, q in layer.named_parameters() if q.grad is not None}
+    again['x'] = xg2.grad
+    assert torch.equal(y2.detach().cpu(), y_hip), 'spikes differ between two identical steps'
+    assert u1 is None or torch.equal(seen['u'], u1), 'membranes differ between two identical steps'
+    assert sorted(again) == sorted(first)
+    for n in first:
+        assert torch.equal(again[n], first[n]), f'{n} gradient differs between two identical steps'
+    print(f'  a second identical step: bit-identical ({", ".join(sorted(first))})', flush=True)
     if w['kind'] == 'axonal':
         # the C++ Function keeps its membrane to itself: the same scan through the Python
         # Function, whose saved tensors start with it
