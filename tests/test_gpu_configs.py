@@ -86,7 +86,7 @@ def test_workload_shape_matches_oracle(dev, case, monkeypatch):
     print(f'  firing rate {float(y_hip.mean()):.4f}', flush=True)
 
     # the same step once more: spikes, membrane and every gradient bit-identical (the kernels
-    # add their partial sums in a fixed order; no atomics on the values)
+    # add their partial sums in a fixed order; no floating-point atomics)
     first = {n: q.grad.detach().clone() for n, q in layer.named_parameters() if q.grad is not None}
     first['x'], u1 = xg.grad.detach().clone(), seen.get('u')
     u1 = None if u1 is None else u1.clone()
